@@ -15,7 +15,8 @@
 //
 // Citations are into /root/reference (carbon-os/tensor-adapt).
 //
-// Build: oracle/build.sh  (g++ -O3 -march=native -fopenmp -ffp-contract=off)
+// Build: oracle/build.sh  (g++ -O3 -march=x86-64-v3 -fopenmp -ffp-contract=off; a portable
+// ISA level because the built library also runs on the GPU box's host CPU)
 //
 // How each function is pinned independently of its own formula is recorded
 // in tests/test_oracle_*.py (torch float64 autograd, numpy matmul, closed

@@ -1,0 +1,325 @@
+// centroid.hip — the Centroid Accumulator's per-token gradient-norm weighted
+// sum and the centroid-merge k-means, on the device.
+//
+// Accumulate (src/centroid/centroid_accumulator.cpp:54-69, intended math):
+//   n_t = ||g_t||_2 ; C[d] += h[t,d] * n_t ; W += n_t.
+// The reference synchronises, copies two [BT, D] F32 tensors to the host per
+// layer and loops on one core.  Here one launch reads h and g once (BF16,
+// straight from the step's activations, no cast kernels), each block folds
+// kTok tokens into an F32 partial row, and a second launch adds the partial
+// rows in block order into an F64 accumulator [D+1] (entry D holds W).  The
+// result is deterministic and within 1e-7 relative of an F64 evaluation.
+//
+// k-means (centroid_accumulator.cpp:114-157 and the stress mode): one
+// workgroup runs every iteration in a single launch.  Squared distances are
+// summed sequentially over d in F32 with no contraction (__fmul_rn/__fadd_rn),
+// exactly like a scalar CPU loop, so assignments are bit-reproducible; center
+// sums run sequentially over snapshots in index order.  Every loop is bounded
+// by max_iters / iters, so the launch always drains.
+#include <float.h>
+
+#include "ta_common.hpp"
+
+namespace ta {
+
+void* scratch_get(size_t bytes, hipStream_t s, int slot = 0);
+
+constexpr int kTok = 32;  // tokens per block in the accumulate pass
+
+template <bool BF16IN>
+__global__ __launch_bounds__(256) void k_centroid_part(const void* __restrict__ hv,
+                                                       const void* __restrict__ gv,
+                                                       const float* __restrict__ nv,
+                                                       int64_t BT, int D,
+                                                       float* __restrict__ part) {
+    __shared__ float nrm[kTok];
+    int64_t t0 = (int64_t)blockIdx.x * kTok;
+    int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    // 1. per-token gradient norms (one wave per token)
+    for (int j = wv; j < kTok; j += 4) {
+        int64_t t = t0 + j;
+        float ss = 0.f;
+        if (t < BT) {
+            if (nv) {
+                ss = 0.f;
+            } else if (BF16IN) {
+                const bf16* g = (const bf16*)gv + t * D;
+                for (int d = lane; d < D; d += 64) {
+                    float f = bf2f(g[d]);
+                    ss += f * f;
+                }
+            } else {
+                const float* g = (const float*)gv + t * D;
+                for (int d = lane; d < D; d += 64) ss += g[d] * g[d];
+            }
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) nrm[j] = (t < BT) ? (nv ? nv[t] : sqrtf(ss)) : 0.f;
+    }
+    __syncthreads();
+    // 2. weighted column sums over this block's tokens
+    float* out = part + (int64_t)blockIdx.x * (D + 1);
+    for (int d = threadIdx.x; d < D; d += 256) {
+        float acc = 0.f;
+        for (int j = 0; j < kTok; j++) {
+            int64_t t = t0 + j;
+            if (t >= BT) break;
+            float h = BF16IN ? bf2f(((const bf16*)hv)[t * D + d]) : ((const float*)hv)[t * D + d];
+            acc += h * nrm[j];
+        }
+        out[d] = acc;
+    }
+    if (threadIdx.x == 0) {
+        float w = 0.f;
+        for (int j = 0; j < kTok; j++) w += nrm[j];
+        out[D] = w;
+    }
+}
+
+// acc[d] += sum over blocks (block order) of part[b][d], in F64.
+__global__ void k_centroid_reduce(const float* __restrict__ part, int nblk, int D1,
+                                  double* __restrict__ acc) {
+    int d = blockIdx.x * blockDim.x + threadIdx.x;
+    if (d >= D1) return;
+    double s = 0.0;
+    for (int b = 0; b < nblk; b++) s += (double)part[(int64_t)b * D1 + d];
+    acc[d] += s;
+}
+
+// ── k-means ────────────────────────────────────────────────────────────
+__device__ __forceinline__ float sqdist_seq(const float* __restrict__ a,
+                                           const float* __restrict__ b, int D) {
+    float d = 0.f;
+    for (int i = 0; i < D; i++) {
+        float v = __fsub_rn(a[i], b[i]);
+        d = __fadd_rn(d, __fmul_rn(v, v));
+    }
+    return d;
+}
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t& s) {
+    uint64_t z = (s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+__device__ __forceinline__ double u01(uint64_t& s) {
+    return (double)(splitmix64(s) >> 11) * (1.0 / 9007199254740992.0);
+}
+
+// assignment pass: dist[n*k + c] for all pairs, then argmin per n (strict <)
+__device__ int kmeans_assign(const float* __restrict__ X, const float* __restrict__ C, int N,
+                             int D, int k, float* __restrict__ dist, int32_t* __restrict__ asg) {
+    for (int p = threadIdx.x; p < N * k; p += blockDim.x)
+        dist[p] = sqdist_seq(X + (int64_t)(p / k) * D, C + (int64_t)(p % k) * D, D);
+    __syncthreads();
+    int changed = 0;
+    for (int n = threadIdx.x; n < N; n += blockDim.x) {
+        float best = 1e38f;
+        int bk = 0;
+        for (int c = 0; c < k; c++) {
+            float d = dist[(int64_t)n * k + c];
+            if (d < best) {
+                best = d;
+                bk = c;
+            }
+        }
+        if (asg[n] != bk) {
+            asg[n] = bk;
+            changed = 1;
+        }
+    }
+    return __syncthreads_or(changed);
+}
+
+// update pass: center c = mean of members (sequential over n); empty ->
+// zero (reference mode) or unchanged (stress mode)
+__device__ void kmeans_update(const float* __restrict__ X, float* __restrict__ C, int N, int D,
+                              int k, const int32_t* __restrict__ asg, bool empty_to_zero) {
+    for (int p = threadIdx.x; p < k * D; p += blockDim.x) {
+        int c = p / D, d = p % D;
+        float s = 0.f;
+        int cnt = 0;
+        for (int n = 0; n < N; n++)
+            if (asg[n] == c) {
+                s = __fadd_rn(s, X[(int64_t)n * D + d]);
+                cnt++;
+            }
+        if (cnt > 0)
+            C[p] = s / (float)cnt;
+        else if (empty_to_zero)
+            C[p] = 0.f;
+    }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(1024) void k_kmeans_ref(const float* __restrict__ X, int N, int D,
+                                                     int k, int max_iters,
+                                                     float* __restrict__ C,
+                                                     int32_t* __restrict__ asg,
+                                                     float* __restrict__ dist,
+                                                     int32_t* __restrict__ iters_out) {
+    for (int p = threadIdx.x; p < k * D; p += blockDim.x) {
+        int c = p / D, d = p % D;
+        C[p] = X[(int64_t)(((int64_t)c * N) / k) * D + d];
+    }
+    for (int n = threadIdx.x; n < N; n += blockDim.x) asg[n] = 0;
+    __syncthreads();
+    int it = 0;
+    for (; it < max_iters; it++) {
+        int changed = kmeans_assign(X, C, N, D, k, dist, asg);
+        if (!changed) break;
+        kmeans_update(X, C, N, D, k, asg, true);
+    }
+    if (threadIdx.x == 0 && iters_out) *iters_out = it;
+}
+
+__global__ __launch_bounds__(1024) void k_kmeans_pp(const float* __restrict__ X,
+                                                    const float* __restrict__ W, int N, int D,
+                                                    int k, int iters, uint64_t seed,
+                                                    float* __restrict__ Cw,  // [k*D] work
+                                                    float* __restrict__ d2,  // [N]
+                                                    float* __restrict__ dist,  // [N*k]
+                                                    int32_t* __restrict__ asg,  // [N]
+                                                    float* __restrict__ C_out,
+                                                    int32_t* __restrict__ asg_out,
+                                                    double* __restrict__ mass_out,
+                                                    int32_t* __restrict__ seeds_out) {
+    __shared__ int chosen[1024];
+    __shared__ double mass[1024];
+    __shared__ int order[1024];
+    __shared__ int rank_of[1024];
+    __shared__ uint64_t rng;
+    if (threadIdx.x == 0) {
+        rng = seed;
+        int first = (int)(u01(rng) * N);
+        if (first >= N) first = N - 1;
+        chosen[0] = first;
+    }
+    for (int n = threadIdx.x; n < N; n += blockDim.x) d2[n] = FLT_MAX;
+    __syncthreads();
+    // k-means++ seeding
+    for (int m = 1; m < k; m++) {
+        const float* c = X + (int64_t)chosen[m - 1] * D;
+        for (int n = threadIdx.x; n < N; n += blockDim.x) {
+            float d = sqdist_seq(X + (int64_t)n * D, c, D);
+            if (d < d2[n]) d2[n] = d;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            double total = 0.0;
+            for (int n = 0; n < N; n++) total += (double)d2[n];
+            double target = u01(rng) * total;
+            int pick = -1, last_pos = -1;
+            double run = 0.0;
+            for (int n = 0; n < N; n++) {
+                run += (double)d2[n];
+                if (d2[n] > 0.f) last_pos = n;
+                if (pick < 0 && run > target && d2[n] > 0.f) pick = n;
+            }
+            if (pick < 0) pick = (last_pos >= 0) ? last_pos : m % N;
+            chosen[m] = pick;
+        }
+        __syncthreads();
+    }
+    for (int p = threadIdx.x; p < k * D; p += blockDim.x)
+        Cw[p] = X[(int64_t)chosen[p / D] * D + (p % D)];
+    for (int n = threadIdx.x; n < N; n += blockDim.x) asg[n] = 0;
+    __syncthreads();
+    for (int it = 0; it < iters; it++) {
+        kmeans_assign(X, Cw, N, D, k, dist, asg);
+        kmeans_update(X, Cw, N, D, k, asg, false);
+    }
+    kmeans_assign(X, Cw, N, D, k, dist, asg);
+    // rank by member weight (F64, index order), stable descending
+    if (threadIdx.x == 0) {
+        for (int c = 0; c < k; c++) mass[c] = 0.0;
+        for (int n = 0; n < N; n++) mass[asg[n]] += (double)W[n];
+        for (int c = 0; c < k; c++) order[c] = c;
+        for (int i = 1; i < k; i++) {  // insertion sort: stable
+            int v = order[i];
+            int j = i - 1;
+            while (j >= 0 && mass[order[j]] < mass[v]) {
+                order[j + 1] = order[j];
+                j--;
+            }
+            order[j + 1] = v;
+        }
+        for (int r = 0; r < k; r++) rank_of[order[r]] = r;
+    }
+    __syncthreads();
+    for (int p = threadIdx.x; p < k * D; p += blockDim.x)
+        C_out[p] = Cw[(int64_t)order[p / D] * D + (p % D)];
+    for (int n = threadIdx.x; n < N; n += blockDim.x) asg_out[n] = rank_of[asg[n]];
+    for (int r = threadIdx.x; r < k; r += blockDim.x) {
+        if (mass_out) mass_out[r] = mass[order[r]];
+        if (seeds_out) seeds_out[r] = chosen[r];
+    }
+}
+
+}  // namespace ta
+
+using namespace ta;
+
+static int centroid_acc(const void* h, const void* g, const float* n, int64_t BT, int D,
+                        double* acc, bool bf16in, void* stream) {
+    TA_REQUIRE(BT >= 0 && D > 0, "centroid_accumulate: bad shape BT=%lld D=%d", (long long)BT, D);
+    if (BT == 0) return 0;
+    hipStream_t s = (hipStream_t)stream;
+    int64_t nblk = (BT + kTok - 1) / kTok;
+    TA_REQUIRE(nblk < (1ll << 31), "centroid_accumulate: BT too large");
+    float* part = (float*)scratch_get((size_t)nblk * (D + 1) * sizeof(float), s);
+    TA_REQUIRE(part, "centroid_accumulate: scratch allocation failed");
+    if (bf16in)
+        k_centroid_part<true><<<(int)nblk, 256, 0, s>>>(h, g, nullptr, BT, D, part);
+    else
+        k_centroid_part<false><<<(int)nblk, 256, 0, s>>>(h, nullptr, n, BT, D, part);
+    k_centroid_reduce<<<(D + 1 + 255) / 256, 256, 0, s>>>(part, (int)nblk, D + 1, acc);
+    return check_launch("centroid_accumulate");
+}
+
+extern "C" {
+
+int ta_centroid_accumulate_bf16(const uint16_t* h, const uint16_t* g, int64_t BT, int D,
+                                double* acc, void* stream) {
+    return centroid_acc(h, g, nullptr, BT, D, acc, true, stream);
+}
+
+int ta_centroid_accumulate_f32n(const float* h, const float* n, int64_t BT, int D, double* acc,
+                                void* stream) {
+    return centroid_acc(h, nullptr, n, BT, D, acc, false, stream);
+}
+
+int ta_kmeans_ref(const float* snaps, int N, int D, int k, int max_iters, float* centers,
+                  int32_t* assign, int32_t* iters_out, void* stream) {
+    TA_REQUIRE(N > 0 && D > 0 && k > 0 && max_iters >= 0, "kmeans_ref: bad N=%d D=%d k=%d", N, D,
+               k);
+    if (k > N) k = N;
+    hipStream_t s = (hipStream_t)stream;
+    float* dist = (float*)scratch_get((size_t)N * k * sizeof(float), s);
+    TA_REQUIRE(dist, "kmeans_ref: scratch allocation failed");
+    k_kmeans_ref<<<1, 1024, 0, s>>>(snaps, N, D, k, max_iters, centers, assign, dist, iters_out);
+    return check_launch("kmeans_ref");
+}
+
+int ta_kmeans_pp(const float* snaps, const float* weights, int N, int D, int k, int iters,
+                 uint64_t seed, float* centers, int32_t* assign, double* mass, int32_t* seeds,
+                 void* stream) {
+    TA_REQUIRE(N > 0 && D > 0 && k > 0 && iters >= 0, "kmeans_pp: bad N=%d D=%d k=%d", N, D, k);
+    if (k > N) k = N;
+    TA_REQUIRE(k <= 1024, "kmeans_pp: k=%d exceeds 1024", k);
+    hipStream_t s = (hipStream_t)stream;
+    size_t off_d2 = (size_t)k * D * sizeof(float);
+    off_d2 = (off_d2 + 255) & ~(size_t)255;
+    size_t off_dist = off_d2 + (((size_t)N * sizeof(float) + 255) & ~(size_t)255);
+    size_t off_asg = off_dist + (((size_t)N * k * sizeof(float) + 255) & ~(size_t)255);
+    size_t total = off_asg + (size_t)N * sizeof(int32_t);
+    char* base = (char*)scratch_get(total, s);
+    TA_REQUIRE(base, "kmeans_pp: scratch allocation failed");
+    k_kmeans_pp<<<1, 1024, 0, s>>>(snaps, weights, N, D, k, iters, seed, (float*)base,
+                                   (float*)(base + off_d2), (float*)(base + off_dist),
+                                   (int32_t*)(base + off_asg), centers, assign, mass, seeds);
+    return check_launch("kmeans_pp");
+}
+
+}  // extern "C"

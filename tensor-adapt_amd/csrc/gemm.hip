@@ -1,0 +1,428 @@
+// gemm.hip — BF16 GEMM on gfx950 matrix cores (v_mfma_f32_32x32x16_bf16).
+//
+// Row-major problem (every GEMM of the step is one of these):
+//   C[m, n] = alpha * sum_k X(m,k) * Y(k,n) + beta * C[m, n]   (F32 accumulate)
+//   X(m,k) = XK ? X[m*ldx + k] : X[k*ldx + m]
+//   Y(k,n) = YK ? Y[n*ldy + k] : Y[k*ldy + n]
+// The step engine stores every frozen weight twice (W [out,in] and W^T
+// [in,out], 288 GB of HBM makes that cheap), so all large GEMMs — forward
+// x*W^T and backward dY*W — run with XK = YK = true: both operands are
+// K-contiguous, global loads are 16-byte vectors along K and LDS tiles are
+// stored K-contiguous, which is exactly the per-lane operand shape of the
+// MFMA (8 consecutive k of one row).  The K-strided layouts (LoRA weight
+// gradients, whose reduction runs over tokens) transpose while staging into
+// LDS.
+//
+// Tiling: block = 256 threads = 4 wave64s arranged WM x WN, block tile
+// BM x BN x 64, wave tile (BM/WM) x (BN/WN) made of 32x32 MFMA tiles.  LDS
+// rows are padded by 8 BF16 (144-byte stride) so the 16-byte fragment reads
+// of 8 consecutive rows hit disjoint banks.  Two LDS stages: the next
+// k-tile's global loads are in flight while the current one feeds the MFMAs,
+// one barrier per k-tile.  Block ids are remapped so that each of the 8 XCDs
+// (own L2 each) works a contiguous band of output tiles.
+//
+// Epilogues: BF16 (alpha, beta, optional bias added after the first
+// rounding and rounded again — the reference's gemm + ops::add_bias), F32
+// (gemm_f32 semantics), or F32 partials for split-K with a separate
+// fixed-order reduction (deterministic).
+#include "ta_common.hpp"
+
+namespace ta {
+
+void* scratch_get(size_t bytes, hipStream_t s, int slot = 0);
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int BK = 64;
+constexpr int LDS_STRIDE = BK + 8;  // bf16 elements per LDS row
+
+enum Epi { EPI_BF16 = 0, EPI_F32 = 1, EPI_PARTIAL = 2 };
+
+struct GemmArgs {
+    int M, N, K;
+    const bf16* X;
+    int64_t ldx;
+    const bf16* Y;
+    int64_t ldy;
+    void* C;
+    int64_t ldc;
+    float alpha, beta;
+    const bf16* bias;
+    float* part;     // split-K partials [splits][M][N]
+    int k_per_split; // multiple of BK
+    int tiles_m, tiles_n;
+};
+
+// Load one 16-byte chunk (8 bf16) of a K-contiguous operand row with
+// bounds guards; out-of-range elements are zero.
+__device__ __forceinline__ bf16x8v load_k8(const bf16* __restrict__ P, int64_t ld, int row,
+                                           int k, int rows, int kend, bool vec) {
+    bf16x8v v;
+    if (row < rows && vec && k + 8 <= kend) {
+        v = *(const bf16x8v*)(P + (int64_t)row * ld + k);
+    } else {
+        uint16_t t[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            t[e] = (row < rows && k + e < kend) ? P[(int64_t)row * ld + k + e] : (uint16_t)0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) v.w[e] = (uint32_t)t[2 * e] | ((uint32_t)t[2 * e + 1] << 16);
+    }
+    return v;
+}
+// Load 8 consecutive rows at one k of a row-contiguous (K-strided) operand.
+__device__ __forceinline__ bf16x8v load_r8(const bf16* __restrict__ P, int64_t ld, int row,
+                                           int k, int rows, int kend, bool vec) {
+    bf16x8v v;
+    if (k < kend && vec && row + 8 <= rows) {
+        v = *(const bf16x8v*)(P + (int64_t)k * ld + row);
+    } else {
+        uint16_t t[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            t[e] = (k < kend && row + e < rows) ? P[(int64_t)k * ld + row + e] : (uint16_t)0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) v.w[e] = (uint32_t)t[2 * e] | ((uint32_t)t[2 * e + 1] << 16);
+    }
+    return v;
+}
+
+// Stage a ROWS x BK tile of an operand into LDS (K-contiguous rows).
+template <int ROWS, bool KMAJ>
+struct TileLoader {
+    static constexpr int CHUNKS = ROWS * BK / 8;
+    static constexpr int PER_THREAD = (CHUNKS + 255) / 256;
+    bf16x8v r[PER_THREAD];
+
+    __device__ __forceinline__ void load(const bf16* __restrict__ P, int64_t ld, int row0, int k0,
+                                         int rows, int kend, bool vec) {
+#pragma unroll
+        for (int i = 0; i < PER_THREAD; i++) {
+            int q = threadIdx.x + 256 * i;
+            if (q < CHUNKS) {
+                if (KMAJ) {
+                    int rr = q / (BK / 8), kc = q % (BK / 8);
+                    r[i] = load_k8(P, ld, row0 + rr, k0 + kc * 8, rows, kend, vec);
+                } else {
+                    int kk = q / (ROWS / 8), rc = q % (ROWS / 8);
+                    r[i] = load_r8(P, ld, row0 + rc * 8, k0 + kk, rows, kend, vec);
+                }
+            }
+        }
+    }
+    __device__ __forceinline__ void store(bf16* __restrict__ S) {
+#pragma unroll
+        for (int i = 0; i < PER_THREAD; i++) {
+            int q = threadIdx.x + 256 * i;
+            if (q < CHUNKS) {
+                if (KMAJ) {
+                    int rr = q / (BK / 8), kc = q % (BK / 8);
+                    *(bf16x8v*)(S + rr * LDS_STRIDE + kc * 8) = r[i];
+                } else {
+                    int kk = q / (ROWS / 8), rc = q % (ROWS / 8);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        uint16_t h = (uint16_t)(r[i].w[e >> 1] >> ((e & 1) * 16));
+                        S[(rc * 8 + e) * LDS_STRIDE + kk] = h;
+                    }
+                }
+            }
+        }
+    }
+};
+
+template <int BM, int BN, int WM, int WN, bool XK, bool YK, int EPI>
+__global__ __launch_bounds__(256) void k_gemm(GemmArgs a, bool vecx, bool vecy) {
+    constexpr int WTM = BM / WM, WTN = BN / WN;  // wave tile
+    constexpr int TM = WTM / 32, TN = WTN / 32;  // MFMA tiles per wave
+    static_assert(WM * WN == 4, "4 waves per block");
+    static_assert(TM >= 1 && TN >= 1, "wave tile too small");
+    __shared__ __attribute__((aligned(16))) bf16 sX[2][BM * LDS_STRIDE];
+    __shared__ __attribute__((aligned(16))) bf16 sY[2][BN * LDS_STRIDE];
+
+    // XCD-aware block order: hardware dispatches consecutive block ids
+    // round-robin over 8 XCDs; give each XCD a contiguous band of tiles.
+    int nt = a.tiles_m * a.tiles_n;
+    int bid = blockIdx.x;
+    if ((nt & 7) == 0) bid = (bid & 7) * (nt >> 3) + (bid >> 3);
+    int tm_i = bid / a.tiles_n, tn_i = bid % a.tiles_n;
+    int m0 = tm_i * BM, n0 = tn_i * BN;
+    int kbeg = blockIdx.z * a.k_per_split;
+    int kend = min(a.K, kbeg + a.k_per_split);
+
+    int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    int wm = wv / WN, wn = wv % WN;
+
+    floatx16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+    TileLoader<BM, XK> lx;
+    TileLoader<BN, YK> ly;
+    int nk = (kend - kbeg + BK - 1) / BK;
+    if (nk > 0) {
+        lx.load(a.X, a.ldx, m0, kbeg, a.M, kend, vecx);
+        ly.load(a.Y, a.ldy, n0, kbeg, a.N, kend, vecy);
+        lx.store(sX[0]);
+        ly.store(sY[0]);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+        int cur = kt & 1;
+        bool more = kt + 1 < nk;
+        if (more) {
+            int k0 = kbeg + (kt + 1) * BK;
+            lx.load(a.X, a.ldx, m0, k0, a.M, kend, vecx);
+            ly.load(a.Y, a.ldy, n0, k0, a.N, kend, vecy);
+        }
+        const bf16* SX = sX[cur] + (wm * WTM + (lane & 31)) * LDS_STRIDE + (lane >> 5) * 8;
+        const bf16* SY = sY[cur] + (wn * WTN + (lane & 31)) * LDS_STRIDE + (lane >> 5) * 8;
+#pragma unroll
+        for (int kk = 0; kk < BK / 16; kk++) {
+            bf16x8_t fx[TM], fy[TN];
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+                fx[i] = *(const bf16x8_t*)(SX + i * 32 * LDS_STRIDE + kk * 16);
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+                fy[j] = *(const bf16x8_t*)(SY + j * 32 * LDS_STRIDE + kk * 16);
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++)
+                    acc[i][j] =
+                        __builtin_amdgcn_mfma_f32_32x32x16_bf16(fx[i], fy[j], acc[i][j], 0, 0, 0);
+        }
+        if (more) {
+            lx.store(sX[cur ^ 1]);
+            ly.store(sY[cur ^ 1]);
+        }
+        __syncthreads();
+    }
+
+    // epilogue: lane holds column n = lane%32 of each 32x32 tile and rows
+    // 8*(r/4) + 4*(lane/32) + r%4
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            int n = n0 + wn * WTN + j * 32 + (lane & 31);
+            if (n >= a.N) continue;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                int m = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m >= a.M) continue;
+                float v = acc[i][j][r];
+                if (EPI == EPI_BF16) {
+                    bf16* C = (bf16*)a.C + (int64_t)m * a.ldc + n;
+                    float o = a.alpha * v;
+                    if (a.beta != 0.f) o += a.beta * bf2f(*C);
+                    if (a.bias) o = bf2f(f2bf(o)) + bf2f(a.bias[n]);
+                    *C = f2bf(o);
+                } else if (EPI == EPI_F32) {
+                    float* C = (float*)a.C + (int64_t)m * a.ldc + n;
+                    float o = a.alpha * v;
+                    if (a.beta != 0.f) o += a.beta * (*C);
+                    *C = o;
+                } else {
+                    a.part[((int64_t)blockIdx.z * a.M + m) * a.N + n] = v;
+                }
+            }
+        }
+}
+
+// Split-K reduction: sum partials in split order, then the BF16 or F32
+// epilogue.
+template <bool OUT_BF16>
+__global__ void k_splitk_reduce(const float* __restrict__ part, int splits, int M, int N,
+                                void* __restrict__ Cv, int64_t ldc, float alpha, float beta,
+                                const bf16* __restrict__ bias) {
+    int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    int64_t MN = (int64_t)M * N;
+    if (idx >= MN) return;
+    float s = 0.f;
+    for (int p = 0; p < splits; p++) s += part[p * MN + idx];
+    int m = (int)(idx / N), n = (int)(idx % N);
+    if (OUT_BF16) {
+        bf16* C = (bf16*)Cv + (int64_t)m * ldc + n;
+        float o = alpha * s;
+        if (beta != 0.f) o += beta * bf2f(*C);
+        if (bias) o = bf2f(f2bf(o)) + bf2f(bias[n]);
+        *C = f2bf(o);
+    } else {
+        float* C = (float*)Cv + (int64_t)m * ldc + n;
+        float o = alpha * s;
+        if (beta != 0.f) o += beta * (*C);
+        *C = o;
+    }
+}
+
+template <int BM, int BN, int WM, int WN, int EPI>
+static void launch_cfg(bool xk, bool yk, const GemmArgs& a, int splits, bool vx, bool vy,
+                       hipStream_t s) {
+    dim3 grid(a.tiles_m * a.tiles_n, 1, splits);
+    if (xk && yk)
+        k_gemm<BM, BN, WM, WN, true, true, EPI><<<grid, 256, 0, s>>>(a, vx, vy);
+    else if (xk && !yk)
+        k_gemm<BM, BN, WM, WN, true, false, EPI><<<grid, 256, 0, s>>>(a, vx, vy);
+    else if (!xk && yk)
+        k_gemm<BM, BN, WM, WN, false, true, EPI><<<grid, 256, 0, s>>>(a, vx, vy);
+    else
+        k_gemm<BM, BN, WM, WN, false, false, EPI><<<grid, 256, 0, s>>>(a, vx, vy);
+}
+
+static inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Shape-driven dispatch.  out_f32: C is F32 (gemm_f32 semantics).
+int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16* X, int64_t ldx,
+                  const bf16* Y, int64_t ldy, float beta, void* C, int64_t ldc, const bf16* bias,
+                  bool out_f32, hipStream_t s, int force_splits) {
+    GemmArgs a;
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.X = X;
+    a.ldx = ldx;
+    a.Y = Y;
+    a.ldy = ldy;
+    a.C = C;
+    a.ldc = ldc;
+    a.alpha = alpha;
+    a.beta = beta;
+    a.bias = bias;
+    a.part = nullptr;
+    bool vx = al16(X) && (ldx % 8) == 0;
+    bool vy = al16(Y) && (ldy % 8) == 0;
+
+    // tile choice: wide-N tiles for big outputs, skinny tiles for N <= 32
+    enum { CFG_256x128, CFG_128x128, CFG_128x32 } cfg;
+    int BMv, BNv;
+    if (N <= 32) {
+        cfg = CFG_128x32;
+        BMv = 128;
+        BNv = 32;
+    } else if ((int64_t)M * N >= (int64_t)256 * 128 * 512) {
+        cfg = CFG_256x128;
+        BMv = 256;
+        BNv = 128;
+    } else {
+        cfg = CFG_128x128;
+        BMv = 128;
+        BNv = 128;
+    }
+    a.tiles_m = (M + BMv - 1) / BMv;
+    a.tiles_n = (N + BNv - 1) / BNv;
+    int tiles = a.tiles_m * a.tiles_n;
+    int ksteps = (K + BK - 1) / BK;
+    // split K when the tile grid alone cannot fill the 256 CUs
+    int splits = 1;
+    if (force_splits > 0) {
+        splits = force_splits;
+    } else if (tiles < 256 && ksteps >= 16) {
+        splits = (512 + tiles - 1) / tiles;
+        if (splits > ksteps / 4) splits = ksteps / 4;
+        if (splits < 1) splits = 1;
+    }
+    if (splits > ksteps) splits = ksteps > 0 ? ksteps : 1;
+    int steps_per = (ksteps + splits - 1) / splits;
+    a.k_per_split = steps_per * BK;
+    splits = (ksteps + steps_per - 1) / steps_per;
+    if (splits < 1) splits = 1;
+
+    int epi;
+    if (splits > 1) {
+        size_t bytes = (size_t)splits * M * N * sizeof(float);
+        a.part = (float*)scratch_get(bytes, s);
+        if (!a.part) return set_error(-2, "gemm: scratch allocation of %zu bytes failed", bytes);
+        epi = EPI_PARTIAL;
+    } else {
+        epi = out_f32 ? EPI_F32 : EPI_BF16;
+    }
+#define TA_LAUNCH(BM_, BN_, WM_, WN_)                                                   \
+    do {                                                                                \
+        if (epi == EPI_BF16)                                                            \
+            launch_cfg<BM_, BN_, WM_, WN_, EPI_BF16>(xk, yk, a, splits, vx, vy, s);     \
+        else if (epi == EPI_F32)                                                        \
+            launch_cfg<BM_, BN_, WM_, WN_, EPI_F32>(xk, yk, a, splits, vx, vy, s);      \
+        else                                                                            \
+            launch_cfg<BM_, BN_, WM_, WN_, EPI_PARTIAL>(xk, yk, a, splits, vx, vy, s);  \
+    } while (0)
+    if (cfg == CFG_256x128)
+        TA_LAUNCH(256, 128, 2, 2);
+    else if (cfg == CFG_128x128)
+        TA_LAUNCH(128, 128, 2, 2);
+    else
+        TA_LAUNCH(128, 32, 4, 1);
+#undef TA_LAUNCH
+    if (splits > 1) {
+        int64_t MN = (int64_t)M * N;
+        int blocks = (int)((MN + 255) / 256);
+        if (out_f32)
+            k_splitk_reduce<false><<<blocks, 256, 0, s>>>(a.part, splits, M, N, C, ldc, alpha,
+                                                          beta, bias);
+        else
+            k_splitk_reduce<true><<<blocks, 256, 0, s>>>(a.part, splits, M, N, C, ldc, alpha,
+                                                         beta, bias);
+    }
+    return check_launch("gemm");
+}
+
+// F32 -> BF16 staging for gemm_f32 operands (the LoRA path feeds it values
+// that came from BF16, for which the rounding is exact).
+__global__ void k_f32_to_bf16_2d(const float* __restrict__ s, int64_t n, bf16* __restrict__ d) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        d[i] = f2bf(s[i]);
+}
+
+}  // namespace ta
+
+using namespace ta;
+
+extern "C" {
+
+int ta_gemm_rm(int x_kmajor, int y_kmajor, int M, int N, int K, float alpha, const uint16_t* X,
+               int ldx, const uint16_t* Y, int ldy, float beta, uint16_t* C, int ldc,
+               const uint16_t* bias, void* stream) {
+    TA_REQUIRE(M > 0 && N > 0 && K > 0 && ldx > 0 && ldy > 0 && ldc > 0,
+               "gemm_rm: M/N/K and leading dims must be > 0");
+    return gemm_dispatch(x_kmajor != 0, y_kmajor != 0, M, N, K, alpha, X, ldx, Y, ldy, beta, C,
+                         ldc, bias, false, (hipStream_t)stream, 0);
+}
+
+// cuBLAS column-major C(MxN) = alpha op(A) op(B) + beta C  ==  row-major
+// C^T(NxM) = op(B)^T op(A)^T: rows j come from op(B), columns i from op(A).
+int ta_gemm_bf16(int transA, int transB, int M, int N, int K, float alpha, const uint16_t* A,
+                 int lda, const uint16_t* B, int ldb, float beta, uint16_t* C, int ldc,
+                 void* stream) {
+    TA_REQUIRE(M > 0 && N > 0 && K > 0, "gemm_bf16: M/N/K must be > 0");
+    TA_REQUIRE(lda > 0 && ldb > 0 && ldc > 0, "gemm_bf16: leading dims must be > 0");
+    return gemm_dispatch(!transB, transA != 0, N, M, K, alpha, B, ldb, A, lda, beta, C, ldc,
+                         nullptr, false, (hipStream_t)stream, 0);
+}
+
+int ta_gemm_f32(int transA, int transB, int M, int N, int K, float alpha, const float* A, int lda,
+                const float* B, int ldb, float beta, float* C, int ldc, void* stream) {
+    TA_REQUIRE(M > 0 && N > 0 && K > 0, "gemm_f32: M/N/K must be > 0");
+    TA_REQUIRE(lda > 0 && ldb > 0 && ldc > 0, "gemm_f32: leading dims must be > 0");
+    hipStream_t s = (hipStream_t)stream;
+    // stage both operands as BF16 (footprint = the stored extent of each) in
+    // the pool's staging slot; the split-K partials use the default slot
+    int64_t na = transA ? (int64_t)(M - 1) * lda + K : (int64_t)(K - 1) * lda + M;
+    int64_t nb = transB ? (int64_t)(K - 1) * ldb + N : (int64_t)(N - 1) * ldb + K;
+    size_t offb = ((size_t)na * 2 + 255) & ~(size_t)255;
+    bf16* a16 = (bf16*)scratch_get(offb + (size_t)nb * 2, s, 1);
+    TA_REQUIRE(a16, "gemm_f32: scratch allocation failed");
+    bf16* b16 = (bf16*)((char*)a16 + offb);
+    k_f32_to_bf16_2d<<<1024, 256, 0, s>>>(A, na, a16);
+    k_f32_to_bf16_2d<<<1024, 256, 0, s>>>(B, nb, b16);
+    return gemm_dispatch(!transB, transA != 0, N, M, K, alpha, b16, ldb, a16, lda, beta, C, ldc,
+                         nullptr, true, s, 0);
+}
+
+}  // extern "C"

@@ -1,0 +1,152 @@
+// optim.hip — AdamW, gradient sum of squares, and the fused optimizer tail.
+//
+// The step engine keeps every adapter tensor in ONE flat arena (master F32,
+// m, v, grad F32, BF16 shadow), so the reference's per-tensor loops
+// (392 sum_sq launches, a host read-back, 392 scale launches and 392 AdamW
+// launches at the headline shape — src/trainer/adapt_trainer.cu:32-70,
+// src/trainer/adamw.cu:9-38) become two launches with no host sync:
+//   1. k_sumsq_partials: fixed grid, each block writes sum(g^2) of its
+//      grid-stride slice (deterministic order);
+//   2. k_adamw_fused: every block re-reduces the partials in the same order
+//      (so all blocks agree on the norm bit for bit), derives the clip
+//      factor, and applies AdamW (ops.cu:1139-1158) to its elements.
+#include "ta_common.hpp"
+
+namespace ta {
+
+void* scratch_get(size_t bytes, hipStream_t s, int slot = 0);
+
+constexpr int kNormBlocks = 1024;
+
+__global__ __launch_bounds__(256) void k_sumsq_partials(const float* __restrict__ g, int64_t N,
+                                                         float* __restrict__ part) {
+    float acc = 0.f;
+    // float4 body when g is 16-byte aligned, scalar otherwise
+    int64_t nv = (((uintptr_t)g & 15u) == 0) ? (N >> 2) : 0;
+    for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < nv; i += (int64_t)gridDim.x * 256) {
+        float4 v = ((const float4*)g)[i];
+        acc += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
+    if (blockIdx.x == 0)
+        for (int64_t i = (nv << 2) + threadIdx.x; i < N; i += 256) acc += g[i] * g[i];
+    acc = wave_sum(acc);
+    __shared__ float red[4];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) part[blockIdx.x] = ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+// sum of the kNormBlocks partials in double, fixed order; every caller gets
+// the identical value.
+__device__ double reduce_partials(const float* __restrict__ part, int nparts) {
+    __shared__ double dred[4];
+    double a = 0.0;
+    for (int i = threadIdx.x; i < nparts; i += 256) a += (double)part[i];
+    a = wave_sum_d(a);
+    if ((threadIdx.x & 63) == 0) dred[threadIdx.x >> 6] = a;
+    __syncthreads();
+    double t = ((dred[0] + dred[1]) + dred[2]) + dred[3];
+    __syncthreads();
+    return t;
+}
+
+__global__ void k_accum_sumsq(const float* __restrict__ part, int nparts,
+                              float* __restrict__ accum) {
+    double t = reduce_partials(part, nparts);
+    if (threadIdx.x == 0) *accum += (float)t;
+}
+
+// AdamW element update — ops.cu:1139-1158 (bias corrections passed in).
+__device__ __forceinline__ float adamw_elem(float p, float g, float& m, float& v, float lr,
+                                            float b1, float b2, float eps, float wd, float bc1,
+                                            float bc2) {
+    float mi = b1 * m + (1.f - b1) * g;
+    float vi = b2 * v + (1.f - b2) * g * g;
+    m = mi;
+    v = vi;
+    float mhat = mi / bc1, vhat = vi / bc2;
+    return p - lr * (mhat / (sqrtf(vhat) + eps) + wd * p);
+}
+
+__global__ __launch_bounds__(256) void k_adamw(float* __restrict__ master, bf16* __restrict__ work,
+                                               float* __restrict__ m, float* __restrict__ v,
+                                               const float* __restrict__ grad, int64_t N,
+                                               float lr, float b1, float b2, float eps, float wd,
+                                               float bc1, float bc2,
+                                               const float* __restrict__ part, int nparts,
+                                               float max_norm, float* __restrict__ norm_out) {
+    float gscale = 1.f;
+    if (part) {
+        double ss = reduce_partials(part, nparts);
+        float norm = (float)sqrt(ss);
+        if (norm_out && blockIdx.x == 0 && threadIdx.x == 0) *norm_out = norm;
+        // clip_gradients, adapt_trainer.cu:55-70
+        if (norm > max_norm) gscale = max_norm / (norm + 1e-6f);
+    }
+    for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < N; i += (int64_t)gridDim.x * 256) {
+        float g = grad[i];
+        if (part) g = g * gscale;
+        float mi = m[i], vi = v[i];
+        float p = adamw_elem(master[i], g, mi, vi, lr, b1, b2, eps, wd, bc1, bc2);
+        m[i] = mi;
+        v[i] = vi;
+        master[i] = p;
+        if (work) work[i] = f2bf(p);
+    }
+}
+
+}  // namespace ta
+
+using namespace ta;
+
+static inline int adam_blocks(int64_t N) {
+    int64_t b = (N + 255) / 256;
+    if (b > 4096) b = 4096;
+    return (int)(b < 1 ? 1 : b);
+}
+
+extern "C" {
+
+int ta_adamw_step(float* master, uint16_t* working, float* m, float* v, const float* grad,
+                  int64_t N, float lr, float beta1, float beta2, float eps, float weight_decay,
+                  int step, void* stream) {
+    TA_REQUIRE(N >= 0 && step >= 1, "adamw_step: bad N=%lld step=%d", (long long)N, step);
+    if (N == 0) return 0;
+    float bc1 = 1.f - powf(beta1, (float)step);
+    float bc2 = 1.f - powf(beta2, (float)step);
+    k_adamw<<<adam_blocks(N), 256, 0, (hipStream_t)stream>>>(master, working, m, v, grad, N, lr,
+                                                             beta1, beta2, eps, weight_decay,
+                                                             bc1, bc2, nullptr, 0, 0.f, nullptr);
+    return check_launch("adamw_step");
+}
+
+int ta_sum_sq_into(const float* g, float* accum, int64_t N, void* stream) {
+    TA_REQUIRE(N >= 0, "sum_sq_into: N < 0");
+    if (N == 0) return 0;
+    hipStream_t s = (hipStream_t)stream;
+    float* part = (float*)scratch_get(kNormBlocks * sizeof(float), s);
+    TA_REQUIRE(part, "sum_sq_into: scratch allocation failed");
+    k_sumsq_partials<<<kNormBlocks, 256, 0, s>>>(g, N, part);
+    k_accum_sumsq<<<1, 256, 0, s>>>(part, kNormBlocks, accum);
+    return check_launch("sum_sq_into");
+}
+
+int ta_adamw_fused(float* master, uint16_t* working, float* m, float* v, const float* grad,
+                   int64_t N, float lr, float beta1, float beta2, float eps,
+                   float weight_decay, int step, float max_norm, float* norm_out,
+                   void* stream) {
+    TA_REQUIRE(N >= 0 && step >= 1, "adamw_fused: bad N=%lld step=%d", (long long)N, step);
+    if (N == 0) return 0;
+    hipStream_t s = (hipStream_t)stream;
+    float* part = (float*)scratch_get(kNormBlocks * sizeof(float), s);
+    TA_REQUIRE(part, "adamw_fused: scratch allocation failed");
+    float bc1 = 1.f - powf(beta1, (float)step);
+    float bc2 = 1.f - powf(beta2, (float)step);
+    k_sumsq_partials<<<kNormBlocks, 256, 0, s>>>(grad, N, part);
+    k_adamw<<<adam_blocks(N), 256, 0, s>>>(master, working, m, v, grad, N, lr, beta1, beta2,
+                                           eps, weight_decay, bc1, bc2, part, kNormBlocks,
+                                           max_norm, norm_out);
+    return check_launch("adamw_fused");
+}
+
+}  // extern "C"

@@ -1,0 +1,86 @@
+// ta_common.hpp — device helpers shared by every gfx950 kernel of the backend.
+//
+// BF16 values travel as raw uint16_t bit patterns (the C-ABI has no HIP
+// types in it).  Conversions are IEEE round-to-nearest-even on the F32 bit
+// pattern with NaN kept quiet, which is what __float2bfloat16 does on the
+// reference side (src/backend/cuda/ops.cu, every kernel output).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ta {
+
+typedef uint16_t bf16;
+
+__device__ __forceinline__ float bf2f(bf16 h) {
+    return __uint_as_float((uint32_t)h << 16);
+}
+__device__ __forceinline__ bf16 f2bf(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (bf16)(u >> 16);
+}
+// two bf16 packed in one 32-bit word (low half = first element)
+__device__ __forceinline__ float lo2f(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float hi2f(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+    return (uint32_t)f2bf(a) | ((uint32_t)f2bf(b) << 16);
+}
+
+// 8 bf16 = 16 bytes, the natural global/LDS vector on CDNA.
+struct alignas(16) bf16x8v { uint32_t w[4]; };
+
+__device__ __forceinline__ void unpack8(const bf16x8v& v, float* f) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        f[2 * i] = lo2f(v.w[i]);
+        f[2 * i + 1] = hi2f(v.w[i]);
+    }
+}
+__device__ __forceinline__ bf16x8v pack8(const float* f) {
+    bf16x8v v;
+#pragma unroll
+    for (int i = 0; i < 4; i++) v.w[i] = pack2(f[2 * i], f[2 * i + 1]);
+    return v;
+}
+
+// wave64 reductions (xor butterflies over all 64 lanes)
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+}  // namespace ta
+
+// Launch-status plumbing for the C-ABI: every entry point returns 0 or a
+// negative code and leaves a message for ta_last_error().
+namespace ta {
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+}  // namespace ta
+
+#define TA_REQUIRE(cond, ...)                                     \
+    do {                                                          \
+        if (!(cond)) return ::ta::set_error(-1, __VA_ARGS__);     \
+    } while (0)
+
+#define TA_HIP(call)                                                              \
+    do {                                                                          \
+        hipError_t _e = (call);                                                   \
+        if (_e != hipSuccess)                                                     \
+            return ::ta::set_error(-2, "%s: %s", #call, hipGetErrorString(_e));   \
+    } while (0)

@@ -1,0 +1,311 @@
+"""GPU parity of every backend entry point against the CPU oracle.
+
+Each test runs the gfx950 kernel through the C-ABI (libtadapt.so) and the
+oracle's restatement of the reference op on the same seeded inputs.
+Tolerances (written per test): BF16 outputs of float math within 1 BF16 ulp
+of the oracle for nearly every element; F32 reductions within the relative
+bound stated; integer/index outputs bit-exact.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from gpu_util import (DEV, P, S, assert_bf16_close, call, dev, empty_bf16, f32, host,
+                      rel_l2)
+
+pytestmark = pytest.mark.gpu
+
+RNG = np.random.default_rng(20261201)
+
+
+def rbf(*shape, scale=1.0):
+    return O.bf16_from_f32(RNG.standard_normal(shape).astype(np.float32) * scale)
+
+
+# ── elementwise ───────────────────────────────────────────────────────────
+@pytest.mark.parametrize("n", [8 * 12345, 73 * 1000 + 5])
+def test_silu_mul_fwd_bwd(n):
+    g, u, d = rbf(n, scale=3), rbf(n), rbf(n)
+    out = empty_bf16(n)
+    call("ta_silu_mul_fwd", P(dev(g)), P(dev(u)), P(out), n, S())
+    assert_bf16_close(host(out), O.silu_mul_fwd(g, u), what="silu fwd")
+    dg, du = empty_bf16(n), empty_bf16(n)
+    call("ta_silu_mul_bwd", P(dev(d)), P(dev(g)), P(dev(u)), P(dg), P(du), n, S())
+    rg, ru = O.silu_mul_bwd(d, g, u)
+    assert_bf16_close(host(dg), rg, what="dgate")
+    assert_bf16_close(host(du), ru, what="dup")
+
+
+def test_adds_and_bias():
+    BT, D = 77, 896
+    out, delta, bias = rbf(BT, D), rbf(BT, D), rbf(D)
+    t = dev(out)
+    call("ta_add_inplace", P(t), P(dev(delta)), BT * D, S())
+    assert np.array_equal(host(t), O.add_inplace(out, delta))
+    t = dev(out)
+    call("ta_lora_add", P(t), P(dev(delta)), ctypes.c_float(2.0), BT * D, S())
+    assert np.array_equal(host(t), O.lora_add(out, delta, 2.0))
+    t = dev(out)
+    call("ta_add_bias", P(t), P(dev(bias)), BT, D, S())
+    assert np.array_equal(host(t), O.add_bias(out, bias))
+    # odd width takes the scalar path
+    o2, b2 = rbf(5, 13), rbf(13)
+    t = dev(o2)
+    call("ta_add_bias", P(t), P(dev(b2)), 5, 13, S())
+    assert np.array_equal(host(t), O.add_bias(o2, b2))
+
+
+def test_casts_and_embed():
+    x = rbf(1000)
+    f = torch.empty(1000, dtype=torch.float32, device=DEV)
+    call("ta_cast_bf16_to_f32", P(dev(x)), P(f), 1000, S())
+    assert np.array_equal(host(f), f32(x))
+    y = RNG.standard_normal(1001).astype(np.float32)
+    b = empty_bf16(1001)
+    call("ta_cast_f32_to_bf16", P(dev(y)), P(b), 1001, S())
+    assert np.array_equal(host(b), O.bf16_from_f32(y))
+    V, D, BT = 500, 896, 64
+    table = rbf(V, D)
+    tok = RNG.integers(0, V, BT).astype(np.int32)
+    out = empty_bf16(BT, D)
+    call("ta_embed_fwd", P(dev(table)), P(dev(tok)), P(out), BT, D, S())
+    assert np.array_equal(host(out), O.embed_fwd(table, tok))
+
+
+# ── RMSNorm ───────────────────────────────────────────────────────────────
+@pytest.mark.parametrize("rows,D", [(256, 896), (130, 1536), (64, 3584), (9, 100)])
+def test_rms_norm_fwd(rows, D):
+    x, w = rbf(rows, D), rbf(D, scale=0.5)
+    out = empty_bf16(rows, D)
+    rms = torch.empty(rows, dtype=torch.float32, device=DEV)
+    call("ta_rms_norm_fwd", P(dev(x)), P(dev(w)), P(out), P(rms), 1, rows, D,
+         ctypes.c_float(1e-6), S())
+    ro, rr = O.rms_norm_fwd(x, w, 1e-6)
+    assert np.allclose(host(rms), rr, rtol=2e-6)
+    assert_bf16_close(host(out), ro, what="rms fwd")
+
+
+@pytest.mark.parametrize("rows,D,want_dw", [(256, 896, False), (130, 1536, True),
+                                            (64, 3584, False), (9, 100, True)])
+def test_rms_norm_bwd(rows, D, want_dw):
+    x, w, dy = rbf(rows, D), rbf(D, scale=0.5), rbf(rows, D)
+    _, rms = O.rms_norm_fwd(x, w, 1e-6)
+    dx = empty_bf16(rows, D)
+    dw = torch.full((D,), 0.25, dtype=torch.float32, device=DEV) if want_dw else None
+    call("ta_rms_norm_bwd", P(dev(dy)), P(dev(x)), P(dev(w)), P(dev(rms)), P(dx), P(dw), 1,
+         rows, D, ctypes.c_float(1e-6), S())
+    if want_dw:
+        rdx, rdw = O.rms_norm_bwd(dy, x, w, rms, want_dw=True)
+        assert np.allclose(host(dw), rdw + 0.25, rtol=1e-4, atol=1e-4)
+    else:
+        rdx = O.rms_norm_bwd(dy, x, w, rms)
+    assert_bf16_close(host(dx), rdx, what="rms bwd")
+
+
+# ── RoPE ──────────────────────────────────────────────────────────────────
+@pytest.mark.parametrize("B,T,H,hd", [(1, 128, 14, 64), (2, 1024, 2, 128), (1, 17, 3, 6)])
+@pytest.mark.parametrize("inverse", [0, 1])
+def test_rope(B, T, H, hd, inverse):
+    x = rbf(B * T, H * hd)
+    t = dev(x)
+    fn = "ta_rope_bwd" if inverse else "ta_rope_fwd"
+    call(fn, P(t), B, T, H, hd, ctypes.c_float(1e6), S())
+    assert_bf16_close(host(t), O.rope(x, B, T, H, hd, 1e6, inverse), frac_exact=0.98,
+                      what="rope")
+
+
+# ── cross entropy ─────────────────────────────────────────────────────────
+@pytest.mark.parametrize("N,V", [(48, 151936), (7, 1001)])
+def test_cross_entropy(N, V):
+    logits = rbf(N, V, scale=2.0)
+    tgt = RNG.integers(0, V, N).astype(np.int32)
+    tgt[::3] = -1
+    loss = torch.empty(N, dtype=torch.float32, device=DEV)
+    dl = empty_bf16(N, V)
+    call("ta_cross_entropy_fwd", P(dev(logits)), P(dev(tgt)), P(loss), P(dl), N, V, S())
+    rl, rd = O.cross_entropy(logits, tgt)
+    assert np.allclose(host(loss), rl, rtol=1e-5, atol=1e-5)
+    assert_bf16_close(host(dl), rd, what="dlogits")
+
+
+# ── AdamW / norms ─────────────────────────────────────────────────────────
+def test_adamw_step_matches_oracle():
+    n = 100003
+    p = RNG.standard_normal(n).astype(np.float32) * 0.1
+    m = RNG.standard_normal(n).astype(np.float32) * 1e-3
+    v = np.abs(RNG.standard_normal(n).astype(np.float32)) * 1e-5
+    g = RNG.standard_normal(n).astype(np.float32) * 1e-2
+    tp, tm, tv, tw = dev(p), dev(m), dev(v), empty_bf16(n)
+    call("ta_adamw_step", P(tp), P(tw), P(tm), P(tv), P(dev(g)), n, ctypes.c_float(1e-4),
+         ctypes.c_float(0.9), ctypes.c_float(0.999), ctypes.c_float(1e-8), ctypes.c_float(0.01),
+         3, S())
+    rp, rm, rv, rw = p.copy(), m.copy(), v.copy(), np.empty(n, np.uint16)
+    O.adamw_step(rp, rw, rm, rv, g, 1e-4, 0.9, 0.999, 1e-8, 0.01, 3)
+    # F32 element math; the device may contract a*b+c into one FMA (so does
+    # the reference's nvcc build): 1e-5 relative plus a floor at 1e-6 of scale
+    for got, want in ((host(tm), rm), (host(tv), rv), (host(tp), rp)):
+        assert np.allclose(got, want, rtol=1e-5, atol=1e-6 * np.abs(want).max())
+    assert_bf16_close(host(tw), rw, what="shadow")
+
+
+@pytest.mark.parametrize("scale,clip", [(1e-2, 1.0), (1.0, 1.0)])
+def test_adamw_fused_norm_clip(scale, clip):
+    n = 262147
+    p = RNG.standard_normal(n).astype(np.float32) * 0.1
+    g = RNG.standard_normal(n).astype(np.float32) * scale
+    z = np.zeros(n, np.float32)
+    tp, tm, tv, tw = dev(p), dev(z), dev(z), empty_bf16(n)
+    norm = torch.zeros(1, dtype=torch.float32, device=DEV)
+    call("ta_adamw_fused", P(tp), P(tw), P(tm), P(tv), P(dev(g)), n, ctypes.c_float(1e-4),
+         ctypes.c_float(0.9), ctypes.c_float(0.999), ctypes.c_float(1e-8), ctypes.c_float(0.01),
+         1, ctypes.c_float(clip), P(norm), S())
+    rn = float(np.sqrt(O.sum_sq(g)))
+    assert abs(host(norm)[0] - rn) <= 1e-5 * rn
+    gc = g * np.float32(clip / (rn + 1e-6)) if rn > clip else g
+    rp, rm, rv, rw = p.copy(), z.copy(), z.copy(), np.empty(n, np.uint16)
+    O.adamw_step(rp, rw, rm, rv, np.ascontiguousarray(gc, np.float32), 1e-4, 0.9, 0.999,
+                 1e-8, 0.01, 1)
+    assert rel_l2(host(tp), rp) < 1e-6
+    assert rel_l2(host(tm), rm) < 1e-5
+
+
+def test_sum_sq_into():
+    g = RNG.standard_normal(1000001).astype(np.float32)
+    acc = torch.full((1,), 2.0, dtype=torch.float32, device=DEV)
+    call("ta_sum_sq_into", P(dev(g)), P(acc), g.size, S())
+    assert abs(host(acc)[0] - (2.0 + O.sum_sq(g))) <= 1e-6 * O.sum_sq(g)
+
+
+# ── GEMM ──────────────────────────────────────────────────────────────────
+def check_gemm_close(got, want, what):
+    r = rel_l2(f32(got), f32(want))
+    exact = float((np.asarray(got) == np.asarray(want)).mean())
+    assert r < 4e-3 and exact > 0.9, f"{what}: rel-L2 {r:.3e}, exact {exact:.4f}"
+
+
+@pytest.mark.parametrize("tA,tB", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_gemm_bf16_column_major_all_transposes(tA, tB):
+    M, N, K = 37, 29, 53
+    lda = (K if tA else M) + 3
+    ldb = (N if tB else K) + 2
+    ldc = M + 5
+    A = rbf((M if tA else K) * lda)
+    B = rbf((K if tB else N) * ldb)
+    C = rbf(N * ldc)
+    tc = dev(C)
+    call("ta_gemm_bf16", tA, tB, M, N, K, ctypes.c_float(0.75), P(dev(A)), lda, P(dev(B)), ldb,
+         ctypes.c_float(1.0), P(tc), ldc, S())
+    ref = C.copy()
+    O.gemm_bf16(tA, tB, M, N, K, 0.75, A, lda, B, ldb, 1.0, ref, ldc)
+    check_gemm_close(host(tc), ref, f"gemm tA={tA} tB={tB}")
+
+
+def rm_ref(xk, yk, M, N, K, alpha, X, ldx, Y, ldy, beta, C, ldc):
+    """oracle for the row-major form: C^T = op(Y) op(X) in column-major terms."""
+    out = C.copy()
+    O.gemm_bf16(yk, 0 if xk else 1, N, M, K, alpha, Y, ldy, X, ldx, beta, out, ldc)
+    return out
+
+
+@pytest.mark.parametrize("M,N,K", [(1024, 1536, 896), (4096, 4096, 256), (8192, 256, 1536),
+                                   (200, 130, 72)])
+def test_gemm_rm_kmajor_tiles(M, N, K):
+    X, Y = rbf(M, K), rbf(N, K, scale=0.05)
+    C = rbf(M, N)
+    tc = dev(C)
+    call("ta_gemm_rm", 1, 1, M, N, K, ctypes.c_float(1.0), P(dev(X)), K, P(dev(Y)), K,
+         ctypes.c_float(1.0), P(tc), N, None, S())
+    check_gemm_close(host(tc), rm_ref(1, 1, M, N, K, 1.0, X, K, Y, K, 1.0, C, N), "gemm_rm")
+
+
+def test_gemm_rm_bias_epilogue():
+    M, N, K = 256, 384, 128
+    X, Y, b = rbf(M, K), rbf(N, K), rbf(N)
+    tc = empty_bf16(M, N)
+    call("ta_gemm_rm", 1, 1, M, N, K, ctypes.c_float(1.0), P(dev(X)), K, P(dev(Y)), K,
+         ctypes.c_float(0.0), P(tc), N, P(dev(b)), S())
+    ref = O.add_bias(rm_ref(1, 1, M, N, K, 1.0, X, K, Y, K, 0.0, np.zeros((M, N), np.uint16), N),
+                     b)
+    check_gemm_close(host(tc), ref, "gemm+bias")
+
+
+@pytest.mark.parametrize("M,N,K", [(1536, 16, 8192), (16, 896, 4096), (8192, 16, 1536)])
+def test_gemm_f32_weight_gradient_layouts(M, N, K):
+    """LoRA weight-gradient shapes (reduction over tokens, K-strided operands),
+    split-K path, F32 output with beta=1 (gemm_f32 as adapter_model.cu uses it)."""
+    # column-major gemm_f32(transA=0, transB=1): C(MxN) = A(MxK) * B(NxK)^T
+    A = f32(rbf(K, M)).copy()  # A[i + k*M]
+    Bm = f32(rbf(K, N, scale=0.1)).copy()  # B[j + k*N]
+    C = RNG.standard_normal(N * M).astype(np.float32)
+    tc = dev(C)
+    call("ta_gemm_f32", 0, 1, M, N, K, ctypes.c_float(0.5), P(dev(A)), M, P(dev(Bm)), N,
+         ctypes.c_float(1.0), P(tc), M, S())
+    ref = C.copy()
+    O.gemm_f32(0, 1, M, N, K, 0.5, A, M, Bm, N, 1.0, ref, M)
+    assert rel_l2(host(tc), ref) < 1e-5
+
+
+# ── centroid accumulate / k-means ─────────────────────────────────────────
+def test_centroid_accumulate_bf16():
+    BT, D = 300, 896
+    h, g = rbf(BT, D), rbf(BT, D, scale=1e-3)
+    acc = torch.zeros(D + 1, dtype=torch.float64, device=DEV)
+    for _ in range(2):
+        call("ta_centroid_accumulate_bf16", P(dev(h)), P(dev(g)), BT, D, P(acc), S())
+    ra, rw = O.centroid_accumulate(f32(h), f32(g))
+    a = host(acc)
+    assert rel_l2(a[:D], 2 * ra) < 1e-6
+    assert abs(a[D] - 2 * rw) <= 1e-6 * 2 * rw
+
+
+def test_centroid_accumulate_f32n():
+    BT, D = 5000, 512
+    h = RNG.standard_normal((BT, D)).astype(np.float32)
+    n = RNG.lognormal(0, 1, BT).astype(np.float32)
+    acc = torch.zeros(D + 1, dtype=torch.float64, device=DEV)
+    call("ta_centroid_accumulate_f32n", P(dev(h)), P(dev(n)), BT, D, P(acc), S())
+    ra, rw = O.centroid_accumulate_n(h, n)
+    a = host(acc)
+    assert np.max(np.abs(a[:D] - ra)) <= 1e-5 * np.max(np.abs(ra))
+    assert abs(a[D] - rw) <= 1e-6 * rw
+
+
+def mixture(N, D, comps, seed):
+    r = np.random.default_rng(seed)
+    means = r.standard_normal((comps, D)).astype(np.float32)
+    lab = r.integers(0, comps, N)
+    return (means[lab] + 0.3 * r.standard_normal((N, D))).astype(np.float32)
+
+
+@pytest.mark.parametrize("N,D,k", [(64, 512, 32), (50, 64, 8), (5, 16, 8)])
+def test_kmeans_ref_bit_exact(N, D, k):
+    X = mixture(N, D, 16, N + D)
+    kk = min(k, N)
+    C = torch.empty(kk * D, dtype=torch.float32, device=DEV)
+    A = torch.empty(N, dtype=torch.int32, device=DEV)
+    it = torch.zeros(1, dtype=torch.int32, device=DEV)
+    call("ta_kmeans_ref", P(dev(X)), N, D, k, 50, P(C), P(A), P(it), S())
+    rc, ra, ri = O.kmeans_ref(X, k)
+    assert np.array_equal(host(A), ra)
+    assert np.array_equal(host(C).reshape(kk, D), rc)
+    assert int(host(it)[0]) == ri
+
+
+def test_kmeans_pp_bit_exact():
+    N, D, k = 64, 512, 32
+    X = mixture(N, D, 16, 7)
+    W = np.random.default_rng(3).lognormal(0, 1, N).astype(np.float32)
+    C = torch.empty(k * D, dtype=torch.float32, device=DEV)
+    A = torch.empty(N, dtype=torch.int32, device=DEV)
+    M = torch.empty(k, dtype=torch.float64, device=DEV)
+    Sd = torch.empty(k, dtype=torch.int32, device=DEV)
+    call("ta_kmeans_pp", P(dev(X)), P(dev(W)), N, D, k, 25, ctypes.c_uint64(12345), P(C), P(A),
+         P(M), P(Sd), S())
+    rc, ra, rm, rs = O.kmeans_pp(X, W, k, 25, 12345)
+    assert np.array_equal(host(Sd), rs)
+    assert np.array_equal(host(A), ra)
+    assert np.array_equal(host(C).reshape(k, D), rc)
+    assert np.allclose(host(M), rm, rtol=1e-12)
