@@ -1,12 +1,520 @@
-// attention.hip — placeholder until the causal GQA attention kernels land.
+// attention.hip — causal GQA attention with saved probabilities on gfx950
+// (v_mfma_f32_16x16x32_bf16), replacing sdpa_fwd_batched / sdpa_bwd_batched
+// (src/backend/cuda/ops.cu:578-681, 707-870).
+//
+// Layouts are the reference's: Q/dO/dQ [B*T, Hq*hd], K/V/dK/dV
+// [B*T, Hkv*hd] BF16, probabilities P [B*Hq, T, T] F32 (zeros above the
+// diagonal); kv head = hq / (Hq/Hkv).  Nothing is packed, expanded or cast:
+// kernels read the strided heads in place (the reference launches 6 layout
+// kernels and allocates ~1.3 GB of temporaries per call at the headline
+// shape).
+//
+// Tiles are 64 queries x 64 keys.  A block is 4 waves; in the forward and
+// the dQ kernel wave w owns query rows 16w..16w+15 of the block's tile, so
+// softmax row statistics reduce over 16 lanes with xor shuffles.  The MFMA
+// C layout (lane: column l%16, rows 4*(l/16)+r) is converted to the A
+// operand layout (row l%16, 8 consecutive k) through a per-wave LDS tile.
+//
+// Forward (per b, hq, query tile; heaviest tiles launch first):
+//   pass 1: online row max / sum of exp over key tiles 0..diag;
+//   pass 2: recompute S, P = exp(S - max) / sum (the reference's softmax,
+//   ops.cu:352-396), store P (F32), O += P*V with P rounded to BF16.
+// Backward:
+//   k_attn_bwd_dq (per b, hq, query tile): pass 1 accumulates the row dot
+//   D = sum_k P*dP (dP = dO V^T recomputed on MFMA); pass 2 forms
+//   dS = P (dP - D) (ops.cu:405-435) and dQ = scale * dS K.  D is stored.
+//   k_attn_bwd_dkv (per b, kv head, key tile): loops over the query heads
+//   of the GQA group and the query tiles at or below the diagonal and
+//   accumulates dV = P^T dO and dK = scale * dS^T Q for the kv head in
+//   registers — the group sum of ops.cu:539-555 without atomics, so dK/dV
+//   are deterministic.
+#include <float.h>
+
 #include "ta_common.hpp"
+
+namespace ta {
+
+void* scratch_get(size_t bytes, hipStream_t s, int slot = 0);
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int TQ = 64, TK = 64;
+constexpr int LDT = TK + 8;  // stride of [hd][key] and [row][key] LDS tiles
+
+__device__ __forceinline__ floatx4 mfma16(bf16x8_t a, bf16x8_t b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ floatx4 zero4() {
+    floatx4 z;
+    z[0] = z[1] = z[2] = z[3] = 0.f;
+    return z;
+}
+__device__ __forceinline__ bf16x8_t ld_frag(const bf16* p) { return *(const bf16x8_t*)p; }
+
+// 16 bytes of a head row from global memory (row < T guarded, zero beyond).
+__device__ __forceinline__ bf16x8_t ld_head8(const bf16* base, int64_t row_stride, int row,
+                                             int T, int col) {
+    if (row < T) return *(const bf16x8_t*)(base + (int64_t)row * row_stride + col);
+    bf16x8_t z;
+#pragma unroll
+    for (int e = 0; e < 8; e++) z[e] = (__bf16)0.f;
+    return z;
+}
+
+// Stage rows [r0, r0+64) of one head ([row][HD], global row stride rs) into
+// LDS as [row][HD + 8] (K-contiguous for MFMA operands over hd).
+template <int HD>
+__device__ __forceinline__ void stage_rows(bf16* __restrict__ s, const bf16* __restrict__ g,
+                                           int64_t rs, int r0, int T) {
+    constexpr int CH = 64 * HD / 8;
+    for (int q = threadIdx.x; q < CH; q += 256) {
+        int r = q / (HD / 8), c = (q % (HD / 8)) * 8;
+        bf16x8v v;
+        if (r0 + r < T)
+            v = *(const bf16x8v*)(g + (int64_t)(r0 + r) * rs + c);
+        else
+            v.w[0] = v.w[1] = v.w[2] = v.w[3] = 0u;
+        *(bf16x8v*)(s + r * (HD + 8) + c) = v;
+    }
+}
+// Same rows staged transposed: LDS [HD][64 + 8] (row index contiguous).
+template <int HD>
+__device__ __forceinline__ void stage_rows_t(bf16* __restrict__ s, const bf16* __restrict__ g,
+                                             int64_t rs, int r0, int T) {
+    constexpr int CH = 64 * HD / 8;
+    for (int q = threadIdx.x; q < CH; q += 256) {
+        int r = q % 64, c = (q / 64) * 8;  // consecutive threads: consecutive rows
+        bf16x8v v;
+        if (r0 + r < T)
+            v = *(const bf16x8v*)(g + (int64_t)(r0 + r) * rs + c);
+        else
+            v.w[0] = v.w[1] = v.w[2] = v.w[3] = 0u;
+#pragma unroll
+        for (int e = 0; e < 8; e++) s[(c + e) * LDT + r] = (bf16)(v.w[e >> 1] >> ((e & 1) * 16));
+    }
+}
+
+// S (or dP) for one wave: 16 rows x 64 keys = 4 MFMA tiles, A fragments in
+// registers (af[HD/32]), B rows from an LDS [key][HD+8] tile.
+template <int HD>
+__device__ __forceinline__ void wave_qk(floatx4 (&S)[4], const bf16x8_t (&af)[HD / 32],
+                                        const bf16* __restrict__ sB, int lane) {
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        S[t] = zero4();
+        const bf16* rowp = sB + (16 * t + (lane & 15)) * (HD + 8) + 8 * (lane >> 4);
+#pragma unroll
+        for (int ks = 0; ks < HD / 32; ks++) S[t] = mfma16(af[ks], ld_frag(rowp + 32 * ks), S[t]);
+    }
+}
+
+// acc[16 x HD] += A[16 x 64] * B[64 x HD]; A from this wave's LDS tile
+// sA [16][LDT] (row-major, k contiguous), B^T from LDS [HD][LDT].
+template <int HD>
+__device__ __forceinline__ void wave_pv(floatx4 (&acc)[HD / 16], const bf16* __restrict__ sA,
+                                        const bf16* __restrict__ sBt, int lane) {
+#pragma unroll
+    for (int kc = 0; kc < 2; kc++) {
+        bf16x8_t a = ld_frag(sA + (lane & 15) * LDT + 32 * kc + 8 * (lane >> 4));
+#pragma unroll
+        for (int j = 0; j < HD / 16; j++) {
+            bf16x8_t b = ld_frag(sBt + (16 * j + (lane & 15)) * LDT + 32 * kc + 8 * (lane >> 4));
+            acc[j] = mfma16(a, b, acc[j]);
+        }
+    }
+}
+
+__device__ __forceinline__ float red16_max(float v) {
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ float red16_sum(float v) {
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// ── forward ───────────────────────────────────────────────────────────────
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
+                                                  const bf16* __restrict__ K,
+                                                  const bf16* __restrict__ V,
+                                                  bf16* __restrict__ O, float* __restrict__ P,
+                                                  int T, int Hq, int Hkv, float scale,
+                                                  int zero_fill) {
+    __shared__ __attribute__((aligned(16))) bf16 sK[TK * (HD + 8)];
+    __shared__ __attribute__((aligned(16))) bf16 sVt[HD * LDT];
+    __shared__ __attribute__((aligned(16))) bf16 sP[4][16 * LDT];
+    int nqt = (T + TQ - 1) / TQ;
+    int qt = nqt - 1 - (int)(blockIdx.x % nqt);  // heavy (long) rows first
+    int bh = (int)(blockIdx.x / nqt);
+    int b = bh / Hq, hq = bh % Hq, hkv = hq / (Hq / Hkv);
+    int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int64_t qs = (int64_t)Hq * HD, ks_ = (int64_t)Hkv * HD;
+    const bf16* Qh = Q + (int64_t)b * T * qs + hq * HD;
+    const bf16* Kh = K + (int64_t)b * T * ks_ + hkv * HD;
+    const bf16* Vh = V + (int64_t)b * T * ks_ + hkv * HD;
+    float* Ph = P + (int64_t)bh * T * T;
+    int q0 = qt * TQ;
+    int rowA = q0 + 16 * w + (lane & 15);  // A-operand row of this lane
+    bf16x8_t qf[HD / 32];
+#pragma unroll
+    for (int ks = 0; ks < HD / 32; ks++) qf[ks] = ld_head8(Qh, qs, rowA, T, 32 * ks + 8 * (lane >> 4));
+    int rbase = q0 + 16 * w + 4 * (lane >> 4);  // C-layout rows rbase + r
+
+    // pass 1: online max / sum
+    float m[4], l[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        m[r] = -FLT_MAX;
+        l[r] = 0.f;
+    }
+    for (int kt = 0; kt <= qt; kt++) {
+        stage_rows<HD>(sK, Kh, ks_, kt * TK, T);
+        __syncthreads();
+        floatx4 S[4];
+        wave_qk<HD>(S, qf, sK, lane);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            int row = rbase + r;
+            float tmax = -FLT_MAX;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                int key = kt * TK + 16 * t + (lane & 15);
+                float s = S[t][r] * scale;
+                S[t][r] = s;
+                if (key <= row && key < T) tmax = fmaxf(tmax, s);
+            }
+            tmax = red16_max(tmax);
+            float mn = fmaxf(m[r], tmax);
+            float add = 0.f;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                int key = kt * TK + 16 * t + (lane & 15);
+                if (key <= row && key < T) add += exp2f((S[t][r] - mn) * kLog2e);
+            }
+            l[r] = (m[r] == -FLT_MAX ? 0.f : l[r] * exp2f((m[r] - mn) * kLog2e)) + add;
+            m[r] = mn;
+        }
+        __syncthreads();
+    }
+    float inv[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) inv[r] = 1.f / red16_sum(l[r]);
+
+    // pass 2: P, O
+    floatx4 acc[HD / 16];
+#pragma unroll
+    for (int j = 0; j < HD / 16; j++) acc[j] = zero4();
+    for (int kt = 0; kt <= qt; kt++) {
+        stage_rows<HD>(sK, Kh, ks_, kt * TK, T);
+        stage_rows_t<HD>(sVt, Vh, ks_, kt * TK, T);
+        __syncthreads();
+        floatx4 S[4];
+        wave_qk<HD>(S, qf, sK, lane);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            int kl = 16 * t + (lane & 15);
+            int key = kt * TK + kl;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                int row = rbase + r;
+                float p = 0.f;
+                if (key <= row && key < T) p = exp2f((S[t][r] * scale - m[r]) * kLog2e) * inv[r];
+                if (row < T && key < T) Ph[(int64_t)row * T + key] = p;
+                sP[w][(4 * (lane >> 4) + r) * LDT + kl] = f2bf(p);
+            }
+        }
+        __syncthreads();
+        wave_pv<HD>(acc, sP[w], sVt, lane);
+        __syncthreads();
+    }
+    // zeros above the diagonal (ops.cu:352-396 leaves exact zeros there)
+    if (zero_fill) {
+        int k0 = (qt + 1) * TK;
+        int width = T - k0;
+        if (width > 0) {
+            for (int i = threadIdx.x; i < TQ * width; i += 256) {
+                int r = i / width, c = i % width;
+                if (q0 + r < T) Ph[(int64_t)(q0 + r) * T + k0 + c] = 0.f;
+            }
+        }
+    }
+    // O (bf16) — lane holds column 16j + l%16 of rows rbase + r
+    bf16* Oh = O + (int64_t)b * T * qs + hq * HD;
+#pragma unroll
+    for (int j = 0; j < HD / 16; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            int row = rbase + r;
+            if (row < T) Oh[(int64_t)row * qs + 16 * j + (lane & 15)] = f2bf(acc[j][r]);
+        }
+}
+
+// ── backward: dQ (and the row dots D) ─────────────────────────────────────
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO,
+                                                     const bf16* __restrict__ K,
+                                                     const bf16* __restrict__ V,
+                                                     const float* __restrict__ P,
+                                                     bf16* __restrict__ dQ,
+                                                     float* __restrict__ Dout, int T, int Hq,
+                                                     int Hkv, float scale) {
+    __shared__ __attribute__((aligned(16))) bf16 sV[TK * (HD + 8)];
+    __shared__ __attribute__((aligned(16))) bf16 sKt[HD * LDT];
+    __shared__ __attribute__((aligned(16))) bf16 sS[4][16 * LDT];
+    int nqt = (T + TQ - 1) / TQ;
+    int qt = nqt - 1 - (int)(blockIdx.x % nqt);
+    int bh = (int)(blockIdx.x / nqt);
+    int b = bh / Hq, hq = bh % Hq, hkv = hq / (Hq / Hkv);
+    int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int64_t qs = (int64_t)Hq * HD, ks_ = (int64_t)Hkv * HD;
+    const bf16* dOh = dO + (int64_t)b * T * qs + hq * HD;
+    const bf16* Kh = K + (int64_t)b * T * ks_ + hkv * HD;
+    const bf16* Vh = V + (int64_t)b * T * ks_ + hkv * HD;
+    const float* Ph = P + (int64_t)bh * T * T;
+    int q0 = qt * TQ;
+    int rowA = q0 + 16 * w + (lane & 15);
+    bf16x8_t of[HD / 32];
+#pragma unroll
+    for (int ks = 0; ks < HD / 32; ks++)
+        of[ks] = ld_head8(dOh, qs, rowA, T, 32 * ks + 8 * (lane >> 4));
+    int rbase = q0 + 16 * w + 4 * (lane >> 4);
+
+    // pass 1: D = sum_k P * dP
+    float dsum[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int kt = 0; kt <= qt; kt++) {
+        stage_rows<HD>(sV, Vh, ks_, kt * TK, T);
+        __syncthreads();
+        floatx4 dP[4];
+        wave_qk<HD>(dP, of, sV, lane);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            int key = kt * TK + 16 * t + (lane & 15);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                int row = rbase + r;
+                if (key <= row && key < T && row < T)
+                    dsum[r] += Ph[(int64_t)row * T + key] * dP[t][r];
+            }
+        }
+        __syncthreads();
+    }
+    float D[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        D[r] = red16_sum(dsum[r]);
+        int row = rbase + r;
+        if ((lane & 15) == 0 && row < T) Dout[(int64_t)bh * T + row] = D[r];
+    }
+
+    // pass 2: dS, dQ
+    floatx4 acc[HD / 16];
+#pragma unroll
+    for (int j = 0; j < HD / 16; j++) acc[j] = zero4();
+    for (int kt = 0; kt <= qt; kt++) {
+        stage_rows<HD>(sV, Vh, ks_, kt * TK, T);
+        stage_rows_t<HD>(sKt, Kh, ks_, kt * TK, T);
+        __syncthreads();
+        floatx4 dP[4];
+        wave_qk<HD>(dP, of, sV, lane);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            int kl = 16 * t + (lane & 15);
+            int key = kt * TK + kl;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                int row = rbase + r;
+                float ds = 0.f;
+                if (key <= row && key < T && row < T) {
+                    float p = Ph[(int64_t)row * T + key];
+                    ds = p * (dP[t][r] - D[r]);
+                }
+                sS[w][(4 * (lane >> 4) + r) * LDT + kl] = f2bf(ds);
+            }
+        }
+        __syncthreads();
+        wave_pv<HD>(acc, sS[w], sKt, lane);
+        __syncthreads();
+    }
+    bf16* dQh = dQ + (int64_t)b * T * qs + hq * HD;
+#pragma unroll
+    for (int j = 0; j < HD / 16; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            int row = rbase + r;
+            if (row < T) dQh[(int64_t)row * qs + 16 * j + (lane & 15)] = f2bf(scale * acc[j][r]);
+        }
+}
+
+// ── backward: dK, dV for one kv head and key tile ─────────────────────────
+// Wave w owns keys 16w..16w+15 of the tile; for every query head of the
+// group and query tile qt >= kt:  dP^T = V dO^T (keys x queries),
+// dS^T = P^T (dP^T - D), dV += P^T dO, dK += dS^T Q.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_bwd_dkv(const bf16* __restrict__ dO,
+                                                      const bf16* __restrict__ Q,
+                                                      const bf16* __restrict__ K,
+                                                      const bf16* __restrict__ V,
+                                                      const float* __restrict__ P,
+                                                      const float* __restrict__ Dq,
+                                                      bf16* __restrict__ dK,
+                                                      bf16* __restrict__ dV, int T, int Hq,
+                                                      int Hkv, float scale) {
+    __shared__ __attribute__((aligned(16))) bf16 sO[TQ * (HD + 8)];  // dO [q][hd]
+    __shared__ __attribute__((aligned(16))) bf16 sOt[HD * LDT];      // dO^T [hd][q]
+    __shared__ __attribute__((aligned(16))) bf16 sQt[HD * LDT];      // Q^T [hd][q]
+    __shared__ __attribute__((aligned(16))) bf16 sA[4][16 * LDT];    // per-wave P^T / dS^T
+    __shared__ float sD[TQ];
+    int nkt = (T + TK - 1) / TK;
+    int kt = (int)(blockIdx.x % nkt);  // low kt = most query tiles: they start first
+    int bkv = (int)(blockIdx.x / nkt);
+    int b = bkv / Hkv, hkv = bkv % Hkv;
+    int grp = Hq / Hkv;
+    int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int64_t qs = (int64_t)Hq * HD, ks_ = (int64_t)Hkv * HD;
+    const bf16* Kh = K + (int64_t)b * T * ks_ + hkv * HD;
+    const bf16* Vh = V + (int64_t)b * T * ks_ + hkv * HD;
+    int k0 = kt * TK;
+    int keyA = k0 + 16 * w + (lane & 15);  // A-operand row (key) of this lane
+    bf16x8_t vf[HD / 32];
+#pragma unroll
+    for (int s = 0; s < HD / 32; s++) vf[s] = ld_head8(Vh, ks_, keyA, T, 32 * s + 8 * (lane >> 4));
+    int kbase = k0 + 16 * w + 4 * (lane >> 4);  // C-layout key rows kbase + r
+
+    floatx4 accK[HD / 16], accV[HD / 16];
+#pragma unroll
+    for (int j = 0; j < HD / 16; j++) {
+        accK[j] = zero4();
+        accV[j] = zero4();
+    }
+    int nqt = (T + TQ - 1) / TQ;
+    for (int g = 0; g < grp; g++) {
+        int hq = hkv * grp + g;
+        int bh = b * Hq + hq;
+        const bf16* dOh = dO + (int64_t)b * T * qs + hq * HD;
+        const bf16* Qh = Q + (int64_t)b * T * qs + hq * HD;
+        const float* Ph = P + (int64_t)bh * T * T;
+        for (int qt = kt; qt < nqt; qt++) {
+            int q0 = qt * TQ;
+            stage_rows<HD>(sO, dOh, qs, q0, T);
+            stage_rows_t<HD>(sOt, dOh, qs, q0, T);
+            stage_rows_t<HD>(sQt, Qh, qs, q0, T);
+            if (threadIdx.x < TQ)
+                sD[threadIdx.x] = (q0 + threadIdx.x < T) ? Dq[(int64_t)bh * T + q0 + threadIdx.x] : 0.f;
+            __syncthreads();
+            floatx4 dPt[4];
+            wave_qk<HD>(dPt, vf, sO, lane);  // rows = keys, cols = queries
+            // P^T tile for this wave: P[q][key], lane keys kbase..kbase+3
+            float pv[4][4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                int ql = 16 * t + (lane & 15);
+                int q = q0 + ql;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    int key = kbase + r;
+                    pv[t][r] = (q < T && key < T && key <= q) ? Ph[(int64_t)q * T + key] : 0.f;
+                }
+            }
+            // dV += P^T dO
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    sA[w][(4 * (lane >> 4) + r) * LDT + 16 * t + (lane & 15)] = f2bf(pv[t][r]);
+            __syncthreads();
+            wave_pv<HD>(accV, sA[w], sOt, lane);
+            __syncthreads();
+            // dK += dS^T Q
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                int ql = 16 * t + (lane & 15);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    float ds = pv[t][r] * (dPt[t][r] - sD[ql]);
+                    sA[w][(4 * (lane >> 4) + r) * LDT + ql] = f2bf(ds);
+                }
+            }
+            __syncthreads();
+            wave_pv<HD>(accK, sA[w], sQt, lane);
+            __syncthreads();
+        }
+    }
+    bf16* dKh = dK + (int64_t)b * T * ks_ + hkv * HD;
+    bf16* dVh = dV + (int64_t)b * T * ks_ + hkv * HD;
+#pragma unroll
+    for (int j = 0; j < HD / 16; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            int key = kbase + r;
+            if (key < T) {
+                dKh[(int64_t)key * ks_ + 16 * j + (lane & 15)] = f2bf(scale * accK[j][r]);
+                dVh[(int64_t)key * ks_ + 16 * j + (lane & 15)] = f2bf(accV[j][r]);
+            }
+        }
+}
+
+static inline bool a16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* P, int B, int T,
+             int Hq, int Hkv, int hd, bool zero_fill, hipStream_t s) {
+    TA_REQUIRE(B > 0 && T > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0,
+               "sdpa_fwd: bad shape B=%d T=%d Hq=%d Hkv=%d", B, T, Hq, Hkv);
+    TA_REQUIRE(hd == 64 || hd == 128, "sdpa_fwd: head_dim %d not supported (64 or 128)", hd);
+    TA_REQUIRE(a16(Q) && a16(K) && a16(V) && a16(O), "sdpa_fwd: tensors must be 16-byte aligned");
+    int nqt = (T + TQ - 1) / TQ;
+    int64_t blocks = (int64_t)B * Hq * nqt;
+    float scale = 1.f / sqrtf((float)hd);
+    if (hd == 64)
+        k_attn_fwd<64><<<(int)blocks, 256, 0, s>>>(Q, K, V, O, P, T, Hq, Hkv, scale, zero_fill);
+    else
+        k_attn_fwd<128><<<(int)blocks, 256, 0, s>>>(Q, K, V, O, P, T, Hq, Hkv, scale, zero_fill);
+    return check_launch("sdpa_fwd");
+}
+
+int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const float* P,
+             bf16* dQ, bf16* dK, bf16* dV, int B, int T, int Hq, int Hkv, int hd, float* Dbuf,
+             hipStream_t s) {
+    TA_REQUIRE(B > 0 && T > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0,
+               "sdpa_bwd: bad shape B=%d T=%d Hq=%d Hkv=%d", B, T, Hq, Hkv);
+    TA_REQUIRE(hd == 64 || hd == 128, "sdpa_bwd: head_dim %d not supported (64 or 128)", hd);
+    TA_REQUIRE(a16(dO) && a16(Q) && a16(K) && a16(V) && a16(dQ) && a16(dK) && a16(dV),
+               "sdpa_bwd: tensors must be 16-byte aligned");
+    if (!Dbuf) {
+        Dbuf = (float*)scratch_get((size_t)B * Hq * T * sizeof(float), s);
+        TA_REQUIRE(Dbuf, "sdpa_bwd: scratch allocation failed");
+    }
+    int nqt = (T + TQ - 1) / TQ;
+    float scale = 1.f / sqrtf((float)hd);
+    int64_t b1 = (int64_t)B * Hq * nqt, b2 = (int64_t)B * Hkv * nqt;
+    if (hd == 64) {
+        k_attn_bwd_dq<64><<<(int)b1, 256, 0, s>>>(dO, K, V, P, dQ, Dbuf, T, Hq, Hkv, scale);
+        k_attn_bwd_dkv<64><<<(int)b2, 256, 0, s>>>(dO, Q, K, V, P, Dbuf, dK, dV, T, Hq, Hkv, scale);
+    } else {
+        k_attn_bwd_dq<128><<<(int)b1, 256, 0, s>>>(dO, K, V, P, dQ, Dbuf, T, Hq, Hkv, scale);
+        k_attn_bwd_dkv<128><<<(int)b2, 256, 0, s>>>(dO, Q, K, V, P, Dbuf, dK, dV, T, Hq, Hkv,
+                                                    scale);
+    }
+    return check_launch("sdpa_bwd");
+}
+
+}  // namespace ta
+
 extern "C" {
-int ta_sdpa_fwd(const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, float*, int, int,
-                int, int, int, void*) {
-    return ta::set_error(-9, "sdpa_fwd: not built yet");
+
+int ta_sdpa_fwd(const uint16_t* Q, const uint16_t* K, const uint16_t* V, uint16_t* out,
+                float* attn_w, int B, int T, int Hq, int Hkv, int head_dim, void* stream) {
+    return ta::attn_fwd(Q, K, V, out, attn_w, B, T, Hq, Hkv, head_dim, true, (hipStream_t)stream);
 }
-int ta_sdpa_bwd(const uint16_t*, const uint16_t*, const uint16_t*, const uint16_t*, const float*,
-                uint16_t*, uint16_t*, uint16_t*, int, int, int, int, int, void*) {
-    return ta::set_error(-9, "sdpa_bwd: not built yet");
+
+int ta_sdpa_bwd(const uint16_t* dout, const uint16_t* Q, const uint16_t* K, const uint16_t* V,
+                const float* attn_w, uint16_t* dQ, uint16_t* dK, uint16_t* dV, int B, int T,
+                int Hq, int Hkv, int head_dim, void* stream) {
+    return ta::attn_bwd(dout, Q, K, V, attn_w, dQ, dK, dV, B, T, Hq, Hkv, head_dim, nullptr,
+                        (hipStream_t)stream);
 }
-}
+
+}  // extern "C"

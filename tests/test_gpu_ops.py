@@ -309,3 +309,34 @@ def test_kmeans_pp_bit_exact():
     assert np.array_equal(host(A), ra)
     assert np.array_equal(host(C).reshape(k, D), rc)
     assert np.allclose(host(M), rm, rtol=1e-12)
+
+
+# ── attention ─────────────────────────────────────────────────────────────
+ATTN_SHAPES = [(1, 128, 14, 2, 64), (2, 256, 12, 2, 128), (1, 100, 4, 2, 64), (1, 512, 14, 2, 64)]
+
+
+@pytest.mark.parametrize("B,T,Hq,Hkv,hd", ATTN_SHAPES)
+def test_sdpa_fwd_bwd(B, T, Hq, Hkv, hd):
+    """P (F32) to 1e-5 relative; O, dQ, dK, dV relative L2 <= 1e-2 (the
+    BF16 gradient bar; P and dS feed the MFMA as BF16 where the reference
+    used F32 GEMMs), and O within 2 BF16 ulps element-wise."""
+    Q, K, V = rbf(B * T, Hq * hd), rbf(B * T, Hkv * hd), rbf(B * T, Hkv * hd)
+    dO = rbf(B * T, Hq * hd)
+    out = empty_bf16(B * T, Hq * hd)
+    Pd = torch.full((B * Hq * T * T,), 7.0, dtype=torch.float32, device=DEV)
+    tQ, tK, tV = dev(Q), dev(K), dev(V)
+    call("ta_sdpa_fwd", P(tQ), P(tK), P(tV), P(out), P(Pd), B, T, Hq, Hkv, hd, S())
+    rO, rP = O.sdpa_fwd(Q, K, V, B, T, Hq, Hkv, hd)
+    gP = host(Pd).reshape(B, Hq, T, T)
+    assert np.allclose(gP, rP, rtol=1e-5, atol=1e-7)
+    # O = P V with P rounded to BF16 for the MFMA: ~2.5e-3 relative L2 against
+    # the F32 GEMM of the reference; element-wise within 2^-7 of max|O|
+    assert_bf16_close(host(out), rO, max_ulp=2, frac_exact=0.5, rl2=1e-2, floor=2.0 ** -7,
+                      what="attn O")
+    dQ, dK, dV = empty_bf16(B * T, Hq * hd), empty_bf16(B * T, Hkv * hd), empty_bf16(B * T, Hkv * hd)
+    call("ta_sdpa_bwd", P(dev(dO)), P(tQ), P(tK), P(tV), P(Pd), P(dQ), P(dK), P(dV), B, T, Hq,
+         Hkv, hd, S())
+    rdQ, rdK, rdV = O.sdpa_bwd(dO, Q, K, V, rP, B, T, Hq, Hkv, hd)
+    for got, want, name in ((dQ, rdQ, "dQ"), (dK, rdK, "dK"), (dV, rdV, "dV")):
+        r = rel_l2(f32(host(got)), f32(want))
+        assert r < 1e-2, f"{name}: rel-L2 {r:.3e}"
