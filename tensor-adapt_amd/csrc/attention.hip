@@ -18,7 +18,10 @@
 // Forward (per b, hq, query tile; heaviest tiles launch first):
 //   pass 1: online row max / sum of exp over key tiles 0..diag;
 //   pass 2: recompute S, P = exp(S - max) / sum (the reference's softmax,
-//   ops.cu:352-396), store P (F32), O += P*V with P rounded to BF16.
+//   ops.cu:352-396), store P (F32), O += P*V.
+// Every product whose left operand is an F32 quantity (P, dS) runs as two
+// MFMAs on its BF16 hi/lo split, keeping ~16 mantissa bits: the reference
+// computes these GEMMs in F32 (ops.cu:628-855).
 // Backward:
 //   k_attn_bwd_dq (per b, hq, query tile): pass 1 accumulates the row dot
 //   D = sum_k P*dP (dP = dO V^T recomputed on MFMA); pass 2 forms
@@ -109,20 +112,33 @@ __device__ __forceinline__ void wave_qk(floatx4 (&S)[4], const bf16x8_t (&af)[HD
     }
 }
 
-// acc[16 x HD] += A[16 x 64] * B[64 x HD]; A from this wave's LDS tile
-// sA [16][LDT] (row-major, k contiguous), B^T from LDS [HD][LDT].
+// acc[16 x HD] += A[16 x 64] * B[64 x HD]; A (an F32 quantity: P or dS)
+// arrives as two BF16 tiles, hi = bf16(a) and lo = bf16(a - hi), in this
+// wave's LDS slots sA[0], sA[1] ([16][LDT], k contiguous), so the product
+// keeps ~16 mantissa bits of A like the reference's F32 GEMMs; B^T comes
+// from LDS [HD][LDT] (exact BF16 values).
 template <int HD>
-__device__ __forceinline__ void wave_pv(floatx4 (&acc)[HD / 16], const bf16* __restrict__ sA,
+__device__ __forceinline__ void wave_pv(floatx4 (&acc)[HD / 16], const bf16* __restrict__ sAhi,
+                                        const bf16* __restrict__ sAlo,
                                         const bf16* __restrict__ sBt, int lane) {
 #pragma unroll
     for (int kc = 0; kc < 2; kc++) {
-        bf16x8_t a = ld_frag(sA + (lane & 15) * LDT + 32 * kc + 8 * (lane >> 4));
+        bf16x8_t ah = ld_frag(sAhi + (lane & 15) * LDT + 32 * kc + 8 * (lane >> 4));
+        bf16x8_t al = ld_frag(sAlo + (lane & 15) * LDT + 32 * kc + 8 * (lane >> 4));
 #pragma unroll
         for (int j = 0; j < HD / 16; j++) {
             bf16x8_t b = ld_frag(sBt + (16 * j + (lane & 15)) * LDT + 32 * kc + 8 * (lane >> 4));
-            acc[j] = mfma16(a, b, acc[j]);
+            acc[j] = mfma16(al, b, acc[j]);
+            acc[j] = mfma16(ah, b, acc[j]);
         }
     }
+}
+
+// store an F32 value as its hi/lo BF16 pair into two LDS tiles
+__device__ __forceinline__ void put_split(bf16* hi, bf16* lo, int idx, float v) {
+    bf16 h = f2bf(v);
+    hi[idx] = h;
+    lo[idx] = f2bf(v - bf2f(h));
 }
 
 __device__ __forceinline__ float red16_max(float v) {
@@ -146,7 +162,7 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
                                                   int zero_fill) {
     __shared__ __attribute__((aligned(16))) bf16 sK[TK * (HD + 8)];
     __shared__ __attribute__((aligned(16))) bf16 sVt[HD * LDT];
-    __shared__ __attribute__((aligned(16))) bf16 sP[4][16 * LDT];
+    __shared__ __attribute__((aligned(16))) bf16 sP[4][2][16 * LDT];
     int nqt = (T + TQ - 1) / TQ;
     int qt = nqt - 1 - (int)(blockIdx.x % nqt);  // heavy (long) rows first
     int bh = (int)(blockIdx.x / nqt);
@@ -224,11 +240,11 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
                 float p = 0.f;
                 if (key <= row && key < T) p = exp2f((S[t][r] * scale - m[r]) * kLog2e) * inv[r];
                 if (row < T && key < T) Ph[(int64_t)row * T + key] = p;
-                sP[w][(4 * (lane >> 4) + r) * LDT + kl] = f2bf(p);
+                put_split(sP[w][0], sP[w][1], (4 * (lane >> 4) + r) * LDT + kl, p);
             }
         }
         __syncthreads();
-        wave_pv<HD>(acc, sP[w], sVt, lane);
+        wave_pv<HD>(acc, sP[w][0], sP[w][1], sVt, lane);
         __syncthreads();
     }
     // zeros above the diagonal (ops.cu:352-396 leaves exact zeros there)
@@ -264,7 +280,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO
                                                      int Hkv, float scale) {
     __shared__ __attribute__((aligned(16))) bf16 sV[TK * (HD + 8)];
     __shared__ __attribute__((aligned(16))) bf16 sKt[HD * LDT];
-    __shared__ __attribute__((aligned(16))) bf16 sS[4][16 * LDT];
+    __shared__ __attribute__((aligned(16))) bf16 sS[4][2][16 * LDT];
     int nqt = (T + TQ - 1) / TQ;
     int qt = nqt - 1 - (int)(blockIdx.x % nqt);
     int bh = (int)(blockIdx.x / nqt);
@@ -332,11 +348,11 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO
                     float p = Ph[(int64_t)row * T + key];
                     ds = p * (dP[t][r] - D[r]);
                 }
-                sS[w][(4 * (lane >> 4) + r) * LDT + kl] = f2bf(ds);
+                put_split(sS[w][0], sS[w][1], (4 * (lane >> 4) + r) * LDT + kl, ds);
             }
         }
         __syncthreads();
-        wave_pv<HD>(acc, sS[w], sKt, lane);
+        wave_pv<HD>(acc, sS[w][0], sS[w][1], sKt, lane);
         __syncthreads();
     }
     bf16* dQh = dQ + (int64_t)b * T * qs + hq * HD;
@@ -366,7 +382,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dkv(const bf16* __restrict__ d
     __shared__ __attribute__((aligned(16))) bf16 sO[TQ * (HD + 8)];  // dO [q][hd]
     __shared__ __attribute__((aligned(16))) bf16 sOt[HD * LDT];      // dO^T [hd][q]
     __shared__ __attribute__((aligned(16))) bf16 sQt[HD * LDT];      // Q^T [hd][q]
-    __shared__ __attribute__((aligned(16))) bf16 sA[4][16 * LDT];    // per-wave P^T / dS^T
+    __shared__ __attribute__((aligned(16))) bf16 sA[4][2][16 * LDT];  // per-wave P^T / dS^T hi,lo
     __shared__ float sD[TQ];
     int nkt = (T + TK - 1) / TK;
     int kt = (int)(blockIdx.x % nkt);  // low kt = most query tiles: they start first
@@ -424,9 +440,10 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dkv(const bf16* __restrict__ d
             for (int t = 0; t < 4; t++)
 #pragma unroll
                 for (int r = 0; r < 4; r++)
-                    sA[w][(4 * (lane >> 4) + r) * LDT + 16 * t + (lane & 15)] = f2bf(pv[t][r]);
+                    put_split(sA[w][0], sA[w][1], (4 * (lane >> 4) + r) * LDT + 16 * t + (lane & 15),
+                              pv[t][r]);
             __syncthreads();
-            wave_pv<HD>(accV, sA[w], sOt, lane);
+            wave_pv<HD>(accV, sA[w][0], sA[w][1], sOt, lane);
             __syncthreads();
             // dK += dS^T Q
 #pragma unroll
@@ -435,11 +452,11 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dkv(const bf16* __restrict__ d
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     float ds = pv[t][r] * (dPt[t][r] - sD[ql]);
-                    sA[w][(4 * (lane >> 4) + r) * LDT + ql] = f2bf(ds);
+                    put_split(sA[w][0], sA[w][1], (4 * (lane >> 4) + r) * LDT + ql, ds);
                 }
             }
             __syncthreads();
-            wave_pv<HD>(accK, sA[w], sQt, lane);
+            wave_pv<HD>(accK, sA[w][0], sA[w][1], sQt, lane);
             __syncthreads();
         }
     }

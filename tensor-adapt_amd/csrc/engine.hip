@@ -1,0 +1,716 @@
+// engine.hip — the MI355X step engine behind include/ta_engine.h.
+//
+// One object owns everything a LoRA step touches, allocated once:
+//   * the frozen base: every projection W [out,in] AND its transpose
+//     W^T [in,out] (also E^T for the tied LM head), so both the forward
+//     x*W^T and the input gradient dY*W are K-contiguous MFMA GEMMs;
+//   * one flat adapter arena (F32 master, m, v, grad; BF16 shadow) so the
+//     whole optimizer tail is two launches (optim.hip);
+//   * the per-layer activation cache of Qwen2Base::forward
+//     (src/base/arch/qwen2.hpp:17-35) and the backward scratch.
+// A step replays qwen2.cu:47-308 / adapter_model.cu:96-220 /
+// adapt_trainer.cu:130-277 op for op (same rounding points) on one stream
+// with no allocation, no device-to-device copy of the residual stream and a
+// single host synchronisation at the end (the reference synchronises for
+// every attention call, every centroid layer and the grad norm).
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <chrono>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "ta_backend.h"
+#include "ta_common.hpp"
+#include "ta_engine.h"
+
+namespace ta {
+
+int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16* X, int64_t ldx,
+                  const bf16* Y, int64_t ldy, float beta, void* C, int64_t ldc, const bf16* bias,
+                  bool out_f32, hipStream_t s, int force_splits);
+int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* P, int B, int T, int Hq,
+             int Hkv, int hd, bool zero_fill, hipStream_t s);
+int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const float* P,
+             bf16* dQ, bf16* dK, bf16* dV, int B, int T, int Hq, int Hkv, int hd, float* Dbuf,
+             hipStream_t s);
+int transpose_bf16(const bf16* in, bf16* out, int64_t rows, int64_t cols, hipStream_t s);
+int fill_normal_bf16(bf16* out, int64_t n, uint64_t seed, uint64_t sid, float std, hipStream_t s);
+int fill_bf16(bf16* out, int64_t n, float v, hipStream_t s);
+int kaiming_init(float* a32, bf16* a16, int64_t n, int in_dim, hipStream_t s);
+int add2_bf16(bf16* out, const bf16* a, const bf16* b, int64_t n, hipStream_t s);
+
+#define CK(x)                    \
+    do {                         \
+        int _rc = (x);           \
+        if (_rc != 0) return _rc; \
+    } while (0)
+
+enum { PQ = 0, PK, PV, PO, PG, PU, PD, NPAIR };
+static const char* kProj[NPAIR] = {"self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj",
+                                   "self_attn.o_proj", "mlp.gate_proj",    "mlp.up_proj",
+                                   "mlp.down_proj"};
+
+struct Pair {
+    bool on = false;
+    int in = 0, out = 0;
+    int64_t offA = 0, offB = 0;  // element offsets in the adapter arena
+    bf16* h = nullptr;           // cached x*A^T [BT, r] from the forward
+};
+
+struct Layer {
+    bf16 *in_norm = nullptr, *post_norm = nullptr, *bias[3] = {nullptr, nullptr, nullptr};
+    bf16* W[NPAIR] = {};
+    bf16* Wt[NPAIR] = {};
+    Pair pr[NPAIR];
+    // forward cache
+    bf16 *res_in, *xn, *Q, *K, *V, *ao, *res_mid, *xn2, *gate, *up, *act;
+    float *in_rms, *post_rms, *attn_w;
+};
+
+struct Engine {
+    ta_model_config mc;
+    ta_adapt_config ac;
+    int B, T, BT, H, qd, kvd, I, V, r;
+    float scale;  // alpha / r
+    hipStream_t s = nullptr;
+    bool own_stream = false;
+    std::vector<void*> allocs;
+    std::map<std::string, std::pair<void*, std::pair<int64_t, int>>> named;
+
+    bf16 *embed = nullptr, *embedT = nullptr, *lm = nullptr, *lmT = nullptr, *final_norm = nullptr;
+    std::vector<Layer> L;
+
+    int64_t nparam = 0;
+    float *master = nullptr, *mom = nullptr, *vel = nullptr, *grad = nullptr;
+    bf16* shadow = nullptr;
+
+    bf16 *x_final, *xfn, *logits, *g_res, *dres, *tmpH, *dact, *dgate, *dup, *dxn2, *dao, *dQ, *dK,
+        *dV, *dxn, *delta, *dh;
+    float *final_rms, *loss_tok, *norm_dev, *Dbuf;
+    double* cacc;
+    int32_t *tok_dev, *tgt_dev;
+    int32_t *tok_host, *tgt_host;  // pinned
+    float *loss_host, *norm_host;  // pinned
+    hipEvent_t ev[4];
+    int64_t step_count = 0;
+    float phase[3] = {0, 0, 0};
+};
+
+static int dmalloc(Engine* e, void** p, size_t bytes, const char* what) {
+    if (bytes == 0) bytes = 256;
+    hipError_t err = hipMalloc(p, bytes);
+    if (err != hipSuccess)
+        return set_error(-2, "engine: hipMalloc(%zu) for %s failed: %s", bytes, what,
+                         hipGetErrorString(err));
+    e->allocs.push_back(*p);
+    return 0;
+}
+template <typename T>
+static int alloc(Engine* e, T** p, int64_t n, const char* name, int is_f32 = -1) {
+    CK(dmalloc(e, (void**)p, (size_t)n * sizeof(T), name));
+    if (is_f32 >= 0) e->named[name] = {(void*)*p, {n, is_f32}};
+    return 0;
+}
+
+static int engine_alloc(Engine* e) {
+    const int BT = e->BT, H = e->H, qd = e->qd, kvd = e->kvd, I = e->I, V = e->V, r = e->r;
+    const ta_model_config& c = e->mc;
+    CK(alloc(e, &e->embed, (int64_t)V * H, "embed"));
+    CK(alloc(e, &e->final_norm, H, "final_norm"));
+    if (c.tie) {
+        CK(alloc(e, &e->embedT, (int64_t)H * V, "embedT"));
+        e->lm = e->embed;
+        e->lmT = e->embedT;
+    } else {
+        CK(alloc(e, &e->lm, (int64_t)V * H, "lm_head"));
+        CK(alloc(e, &e->lmT, (int64_t)H * V, "lm_headT"));
+    }
+    int outs[NPAIR] = {qd, kvd, kvd, H, I, I, H};
+    int ins[NPAIR] = {H, H, H, qd, H, H, I};
+    e->L.resize(c.layers);
+    // adapter arena layout: layer-major, targets in q,k,v,o,gate,up,down
+    // order, A then B, each padded to 64 elements (256-byte aligned F32)
+    int64_t off = 0;
+    for (int l = 0; l < c.layers; l++)
+        for (int p = 0; p < NPAIR; p++) {
+            Pair& pr = e->L[l].pr[p];
+            pr.on = (e->ac.inject_mask >> p) & 1;
+            pr.in = ins[p];
+            pr.out = outs[p];
+            if (!pr.on) continue;
+            pr.offA = off;
+            off += ((int64_t)r * pr.in + 63) / 64 * 64;
+            pr.offB = off;
+            off += ((int64_t)pr.out * r + 63) / 64 * 64;
+        }
+    e->nparam = off;
+    CK(alloc(e, &e->master, off, "adapter.master", 1));
+    CK(alloc(e, &e->mom, off, "adapter.m", 1));
+    CK(alloc(e, &e->vel, off, "adapter.v", 1));
+    CK(alloc(e, &e->grad, off, "adapter.grad", 1));
+    CK(alloc(e, &e->shadow, off, "adapter.shadow", 0));
+    for (int l = 0; l < c.layers; l++) {
+        Layer& ly = e->L[l];
+        std::string p = "l" + std::to_string(l) + ".";
+        CK(alloc(e, &ly.in_norm, H, "w"));
+        CK(alloc(e, &ly.post_norm, H, "w"));
+        CK(alloc(e, &ly.bias[0], qd, "w"));
+        CK(alloc(e, &ly.bias[1], kvd, "w"));
+        CK(alloc(e, &ly.bias[2], kvd, "w"));
+        for (int q = 0; q < NPAIR; q++) {
+            CK(alloc(e, &ly.W[q], (int64_t)outs[q] * ins[q], "w"));
+            CK(alloc(e, &ly.Wt[q], (int64_t)outs[q] * ins[q], "wt"));
+            if (ly.pr[q].on) CK(alloc(e, &ly.pr[q].h, (int64_t)BT * r, "lora.h"));
+        }
+        CK(alloc(e, &ly.res_in, (int64_t)BT * H, (p + "res_in").c_str(), 0));
+        CK(alloc(e, &ly.in_rms, BT, (p + "in_rms").c_str(), 1));
+        CK(alloc(e, &ly.xn, (int64_t)BT * H, (p + "x_normed").c_str(), 0));
+        CK(alloc(e, &ly.Q, (int64_t)BT * qd, (p + "Q").c_str(), 0));
+        CK(alloc(e, &ly.K, (int64_t)BT * kvd, (p + "K").c_str(), 0));
+        CK(alloc(e, &ly.V, (int64_t)BT * kvd, (p + "V").c_str(), 0));
+        CK(alloc(e, &ly.ao, (int64_t)BT * qd, (p + "attn_out").c_str(), 0));
+        CK(alloc(e, &ly.attn_w, (int64_t)e->B * c.n_q * e->T * e->T, (p + "attn_w").c_str(), 1));
+        CK(alloc(e, &ly.res_mid, (int64_t)BT * H, (p + "res_mid").c_str(), 0));
+        CK(alloc(e, &ly.post_rms, BT, (p + "post_rms").c_str(), 1));
+        CK(alloc(e, &ly.xn2, (int64_t)BT * H, (p + "x_normed2").c_str(), 0));
+        CK(alloc(e, &ly.gate, (int64_t)BT * I, (p + "gate").c_str(), 0));
+        CK(alloc(e, &ly.up, (int64_t)BT * I, (p + "up").c_str(), 0));
+        CK(alloc(e, &ly.act, (int64_t)BT * I, (p + "act").c_str(), 0));
+    }
+    int maxout = std::max(std::max(qd, H), I);
+    CK(alloc(e, &e->x_final, (int64_t)BT * H, "x_final", 0));
+    CK(alloc(e, &e->final_rms, BT, "final_rms", 1));
+    CK(alloc(e, &e->xfn, (int64_t)BT * H, "xfn", 0));
+    CK(alloc(e, &e->logits, (int64_t)BT * V, "logits", 0));
+    CK(alloc(e, &e->loss_tok, BT, "loss_tok", 1));
+    CK(alloc(e, &e->g_res, (int64_t)BT * H, "grad", 0));
+    CK(alloc(e, &e->dres, (int64_t)BT * H, "dres", 0));
+    CK(alloc(e, &e->tmpH, (int64_t)BT * H, "tmpH", 0));
+    CK(alloc(e, &e->dact, (int64_t)BT * I, "dact", 0));
+    CK(alloc(e, &e->dgate, (int64_t)BT * I, "dgate", 0));
+    CK(alloc(e, &e->dup, (int64_t)BT * I, "dup", 0));
+    CK(alloc(e, &e->dxn2, (int64_t)BT * H, "dx_normed2", 0));
+    CK(alloc(e, &e->dao, (int64_t)BT * qd, "dattn_out", 0));
+    CK(alloc(e, &e->dQ, (int64_t)BT * qd, "dQ", 0));
+    CK(alloc(e, &e->dK, (int64_t)BT * kvd, "dK", 0));
+    CK(alloc(e, &e->dV, (int64_t)BT * kvd, "dV", 0));
+    CK(alloc(e, &e->dxn, (int64_t)BT * H, "dx_normed", 0));
+    CK(alloc(e, &e->delta, (int64_t)BT * maxout, "delta", 0));
+    CK(alloc(e, &e->dh, (int64_t)BT * r, "dh", 0));
+    CK(alloc(e, &e->Dbuf, (int64_t)e->B * c.n_q * e->T, "Dbuf", 1));
+    CK(alloc(e, &e->norm_dev, 64, "norm", 1));
+    CK(alloc(e, &e->cacc, H + 1, "centroid"));
+    CK(alloc(e, &e->tok_dev, BT, "tok"));
+    CK(alloc(e, &e->tgt_dev, BT, "tgt"));
+    TA_HIP(hipHostMalloc((void**)&e->tok_host, BT * sizeof(int32_t)));
+    TA_HIP(hipHostMalloc((void**)&e->tgt_host, BT * sizeof(int32_t)));
+    TA_HIP(hipHostMalloc((void**)&e->loss_host, BT * sizeof(float)));
+    TA_HIP(hipHostMalloc((void**)&e->norm_host, 64));
+    for (int i = 0; i < 4; i++) TA_HIP(hipEventCreate(&e->ev[i]));
+    return 0;
+}
+
+// Adapter state at creation (AdapterModel::create, adapter_model.cu:41-90):
+// A from the fixed-seed hash, B = 0, moments 0.
+static int adapter_init(Engine* e) {
+    TA_HIP(hipMemsetAsync(e->master, 0, e->nparam * 4, e->s));
+    TA_HIP(hipMemsetAsync(e->mom, 0, e->nparam * 4, e->s));
+    TA_HIP(hipMemsetAsync(e->vel, 0, e->nparam * 4, e->s));
+    TA_HIP(hipMemsetAsync(e->grad, 0, e->nparam * 4, e->s));
+    TA_HIP(hipMemsetAsync(e->shadow, 0, e->nparam * 2, e->s));
+    for (auto& ly : e->L)
+        for (auto& p : ly.pr)
+            if (p.on)
+                CK(kaiming_init(e->master + p.offA, e->shadow + p.offA, (int64_t)e->r * p.in, p.in,
+                                e->s));
+    TA_HIP(hipMemsetAsync(e->cacc, 0, (e->H + 1) * sizeof(double), e->s));
+    return 0;
+}
+
+// ── one LoRA pair (adapter_model.cu:96-129 forward, 131-220 backward) ────
+static int lora_fwd(Engine* e, Pair& p, const bf16* x, bf16* y) {
+    const bf16* A = e->shadow + p.offA;
+    const bf16* Bm = e->shadow + p.offB;
+    // h = bf16(x A^T) [BT, r]; delta = bf16(h B^T) [BT, out]; y = bf16(y + s*delta)
+    CK(gemm_dispatch(true, true, e->BT, e->r, p.in, 1.f, x, p.in, A, p.in, 0.f, p.h, e->r, nullptr,
+                     false, e->s, 0));
+    CK(gemm_dispatch(true, true, e->BT, p.out, e->r, 1.f, p.h, e->r, Bm, e->r, 0.f, e->delta, p.out,
+                     nullptr, false, e->s, 0));
+    return ta_lora_add(y, e->delta, e->scale, (int64_t)e->BT * p.out, e->s);
+}
+
+static int lora_bwd(Engine* e, Pair& p, const bf16* x, const bf16* go, bf16* gx) {
+    const bf16* A = e->shadow + p.offA;
+    const bf16* Bm = e->shadow + p.offB;
+    float* gA = e->grad + p.offA;
+    float* gB = e->grad + p.offB;
+    const int BT = e->BT, r = e->r;
+    // h is the forward's x*A^T (the reference recomputes the same product)
+    // gB += s * go^T h       [out, r]
+    CK(gemm_dispatch(false, false, p.out, r, BT, e->scale, go, p.out, p.h, r, 1.f, gB, r, nullptr,
+                     true, e->s, 0));
+    // dh = bf16(go B)        [BT, r]
+    CK(gemm_dispatch(true, false, BT, r, p.out, 1.f, go, p.out, Bm, r, 0.f, e->dh, r, nullptr,
+                     false, e->s, 0));
+    // gA += s * dh^T x       [r, in]
+    CK(gemm_dispatch(false, false, r, p.in, BT, e->scale, e->dh, r, x, p.in, 1.f, gA, p.in, nullptr,
+                     true, e->s, 0));
+    // gx = bf16(gx + s * dh A)
+    return gemm_dispatch(true, false, BT, p.in, r, e->scale, e->dh, r, A, p.in, 1.f, gx, p.in,
+                         nullptr, false, e->s, 0);
+}
+
+// proj_fwd (qwen2.cu:21-30) with the bias add fused: y = bf16(bf16(x W^T) + b)
+static int proj_fwd(Engine* e, const bf16* W, const bf16* x, bf16* y, int in, int out,
+                    const bf16* bias) {
+    return gemm_dispatch(true, true, e->BT, out, in, 1.f, x, in, W, in, 0.f, y, out, bias, false,
+                         e->s, 0);
+}
+// proj_bwd_x (qwen2.cu:32-41): dx = bf16(dy W + beta dx), W^T resident
+static int proj_bwd_x(Engine* e, const bf16* Wt, const bf16* dy, bf16* dx, int out, int in,
+                      float beta) {
+    return gemm_dispatch(true, true, e->BT, in, out, 1.f, dy, out, Wt, out, beta, dx, in, nullptr,
+                         false, e->s, 0);
+}
+
+static void mask_targets(const int32_t* in, int32_t* tgt, int B, int T) {
+    // adapt_trainer.cu:145-182 (151644 <|im_start|>, 77091 "assistant", 151645 <|im_end|>)
+    for (int b = 0; b < B; ++b) {
+        bool in_asst = false;
+        int off = b * T;
+        for (int t = 0; t < T; ++t) {
+            int idx = off + t, tok = in[idx];
+            if (tok == 151644) in_asst = (t + 1 < T && in[off + t + 1] == 77091);
+            bool mask = !in_asst;
+            if (tok == 151644 || tok == 77091) mask = true;
+            if (tok == 151645) {
+                in_asst = false;
+                mask = false;
+            }
+            if (mask) tgt[idx] = -1;
+        }
+    }
+}
+
+// CosineSchedule::lr_at — include/tensor/trainer/cosine_schedule.hpp:18-29
+static float cosine_lr(float base, int64_t warmup, int64_t total, float floor_frac, int64_t step) {
+    if (step < warmup) return base * (float)(step + 1) / (float)warmup;
+    float progress = (float)(step - warmup) / (float)(total - warmup);
+    progress = std::min(progress, 1.f);
+    float cos_val = 0.5f * (1.f + std::cos((float)M_PI * progress));
+    float floor = base * floor_frac;
+    return floor + (base - floor) * cos_val;
+}
+
+static int forward(Engine* e) {
+    const ta_model_config& c = e->mc;
+    const int BT = e->BT, H = e->H, qd = e->qd, kvd = e->kvd, I = e->I;
+    hipStream_t s = e->s;
+    CK(ta_embed_fwd(e->embed, e->tok_dev, e->L[0].res_in, BT, H, s));
+    for (int l = 0; l < c.layers; l++) {
+        Layer& ly = e->L[l];
+        bf16* res_out = (l + 1 < c.layers) ? e->L[l + 1].res_in : e->x_final;
+        CK(ta_rms_norm_fwd(ly.res_in, ly.in_norm, ly.xn, ly.in_rms, 1, BT, H, c.rms_eps, s));
+        CK(proj_fwd(e, ly.W[PQ], ly.xn, ly.Q, H, qd, ly.bias[0]));
+        CK(proj_fwd(e, ly.W[PK], ly.xn, ly.K, H, kvd, ly.bias[1]));
+        CK(proj_fwd(e, ly.W[PV], ly.xn, ly.V, H, kvd, ly.bias[2]));
+        if (ly.pr[PQ].on) CK(lora_fwd(e, ly.pr[PQ], ly.xn, ly.Q));
+        if (ly.pr[PK].on) CK(lora_fwd(e, ly.pr[PK], ly.xn, ly.K));
+        if (ly.pr[PV].on) CK(lora_fwd(e, ly.pr[PV], ly.xn, ly.V));
+        CK(ta_rope_fwd(ly.Q, e->B, e->T, c.n_q, c.head_dim, c.rope_theta, s));
+        CK(ta_rope_fwd(ly.K, e->B, e->T, c.n_kv, c.head_dim, c.rope_theta, s));
+        // the upper triangle of attn_w is never read by the backward: skip its fill
+        CK(attn_fwd(ly.Q, ly.K, ly.V, ly.ao, ly.attn_w, e->B, e->T, c.n_q, c.n_kv, c.head_dim, false,
+                    s));
+        CK(proj_fwd(e, ly.W[PO], ly.ao, e->tmpH, qd, H, nullptr));
+        if (ly.pr[PO].on) CK(lora_fwd(e, ly.pr[PO], ly.ao, e->tmpH));
+        CK(add2_bf16(ly.res_mid, ly.res_in, e->tmpH, (int64_t)BT * H, s));
+        CK(ta_rms_norm_fwd(ly.res_mid, ly.post_norm, ly.xn2, ly.post_rms, 1, BT, H, c.rms_eps, s));
+        CK(proj_fwd(e, ly.W[PG], ly.xn2, ly.gate, H, I, nullptr));
+        CK(proj_fwd(e, ly.W[PU], ly.xn2, ly.up, H, I, nullptr));
+        if (ly.pr[PG].on) CK(lora_fwd(e, ly.pr[PG], ly.xn2, ly.gate));
+        if (ly.pr[PU].on) CK(lora_fwd(e, ly.pr[PU], ly.xn2, ly.up));
+        CK(ta_silu_mul_fwd(ly.gate, ly.up, ly.act, (int64_t)BT * I, s));
+        CK(proj_fwd(e, ly.W[PD], ly.act, e->tmpH, I, H, nullptr));
+        if (ly.pr[PD].on) CK(lora_fwd(e, ly.pr[PD], ly.act, e->tmpH));
+        CK(add2_bf16(res_out, ly.res_mid, e->tmpH, (int64_t)BT * H, s));
+    }
+    CK(ta_rms_norm_fwd(e->x_final, e->final_norm, e->xfn, e->final_rms, 1, BT, H, c.rms_eps, s));
+    // LM head (qwen2.cu:163-175), tied to the embedding when c.tie
+    CK(gemm_dispatch(true, true, BT, e->V, H, 1.f, e->xfn, H, e->lm, H, 0.f, e->logits, e->V,
+                     nullptr, false, s, 0));
+    // loss (adapt_trainer.cu:201-205): dlogits overwrite the logits in place
+    return ta_cross_entropy_fwd(e->logits, e->tgt_dev, e->loss_tok, e->logits, BT, e->V, s);
+}
+
+static int backward(Engine* e) {
+    const ta_model_config& c = e->mc;
+    const int BT = e->BT, H = e->H, qd = e->qd, kvd = e->kvd, I = e->I;
+    hipStream_t s = e->s;
+    // dres = dlogits * W_lm (qwen2.cu:205); grad = rms_norm_bwd(final)
+    CK(gemm_dispatch(true, true, BT, H, e->V, 1.f, e->logits, e->V, e->lmT, e->V, 0.f, e->dres, H,
+                     nullptr, false, s, 0));
+    CK(ta_rms_norm_bwd(e->dres, e->x_final, e->final_norm, e->final_rms, e->g_res, nullptr, 1, BT,
+                       H, c.rms_eps, s));
+    for (int l = c.layers - 1; l >= 0; l--) {
+        Layer& ly = e->L[l];
+        // FFN (qwen2.cu:222-246)
+        CK(proj_bwd_x(e, ly.Wt[PD], e->g_res, e->dact, H, I, 0.f));
+        if (ly.pr[PD].on) CK(lora_bwd(e, ly.pr[PD], ly.act, e->g_res, e->dact));
+        CK(ta_silu_mul_bwd(e->dact, ly.gate, ly.up, e->dgate, e->dup, (int64_t)BT * I, s));
+        CK(proj_bwd_x(e, ly.Wt[PG], e->dgate, e->dxn2, I, H, 0.f));
+        CK(proj_bwd_x(e, ly.Wt[PU], e->dup, e->dxn2, I, H, 1.f));
+        if (ly.pr[PG].on) CK(lora_bwd(e, ly.pr[PG], ly.xn2, e->dgate, e->dxn2));
+        if (ly.pr[PU].on) CK(lora_bwd(e, ly.pr[PU], ly.xn2, e->dup, e->dxn2));
+        CK(ta_rms_norm_bwd(e->dxn2, ly.res_mid, ly.post_norm, ly.post_rms, e->tmpH, nullptr, 1, BT,
+                           H, c.rms_eps, s));
+        CK(ta_add_inplace(e->g_res, e->tmpH, (int64_t)BT * H, s));
+        // attention (qwen2.cu:250-304)
+        CK(proj_bwd_x(e, ly.Wt[PO], e->g_res, e->dao, H, qd, 0.f));
+        if (ly.pr[PO].on) CK(lora_bwd(e, ly.pr[PO], ly.ao, e->g_res, e->dao));
+        CK(attn_bwd(e->dao, ly.Q, ly.K, ly.V, ly.attn_w, e->dQ, e->dK, e->dV, e->B, e->T, c.n_q,
+                    c.n_kv, c.head_dim, e->Dbuf, s));
+        CK(ta_rope_bwd(e->dQ, e->B, e->T, c.n_q, c.head_dim, c.rope_theta, s));
+        CK(ta_rope_bwd(e->dK, e->B, e->T, c.n_kv, c.head_dim, c.rope_theta, s));
+        CK(proj_bwd_x(e, ly.Wt[PQ], e->dQ, e->dxn, qd, H, 0.f));
+        CK(proj_bwd_x(e, ly.Wt[PK], e->dK, e->dxn, kvd, H, 1.f));
+        CK(proj_bwd_x(e, ly.Wt[PV], e->dV, e->dxn, kvd, H, 1.f));
+        if (ly.pr[PQ].on) CK(lora_bwd(e, ly.pr[PQ], ly.xn, e->dQ, e->dxn));
+        if (ly.pr[PK].on) CK(lora_bwd(e, ly.pr[PK], ly.xn, e->dK, e->dxn));
+        if (ly.pr[PV].on) CK(lora_bwd(e, ly.pr[PV], ly.xn, e->dV, e->dxn));
+        // centroid side channel (adapt_trainer.cu:210-232): h = x_normed,
+        // g = dx_attn_in of this layer
+        CK(ta_centroid_accumulate_bf16(ly.xn, e->dxn, BT, H, e->cacc, s));
+        CK(ta_rms_norm_bwd(e->dxn, ly.res_in, ly.in_norm, ly.in_rms, e->tmpH, nullptr, 1, BT, H,
+                           c.rms_eps, s));
+        CK(ta_add_inplace(e->g_res, e->tmpH, (int64_t)BT * H, s));
+    }
+    return 0;
+}
+
+static int engine_step(Engine* e, const int32_t* inputs, const int32_t* targets, float lr_override,
+                       ta_step_metrics* m) {
+    auto t0 = std::chrono::steady_clock::now();
+    const int BT = e->BT;
+    memcpy(e->tok_host, inputs, BT * sizeof(int32_t));
+    memcpy(e->tgt_host, targets, BT * sizeof(int32_t));
+    mask_targets(e->tok_host, e->tgt_host, e->B, e->T);
+    TA_HIP(hipMemcpyAsync(e->tok_dev, e->tok_host, BT * 4, hipMemcpyHostToDevice, e->s));
+    TA_HIP(hipMemcpyAsync(e->tgt_dev, e->tgt_host, BT * 4, hipMemcpyHostToDevice, e->s));
+    // zero_grad (adapter_model.cu:222-229)
+    TA_HIP(hipMemsetAsync(e->grad, 0, e->nparam * sizeof(float), e->s));
+    TA_HIP(hipEventRecord(e->ev[0], e->s));
+    CK(forward(e));
+    TA_HIP(hipEventRecord(e->ev[1], e->s));
+    CK(backward(e));
+    TA_HIP(hipEventRecord(e->ev[2], e->s));
+    // tail: loss read-back, grad norm + clip + AdamW on the device
+    TA_HIP(hipMemcpyAsync(e->loss_host, e->loss_tok, BT * 4, hipMemcpyDeviceToHost, e->s));
+    float lr = (lr_override > 0.f)
+                   ? lr_override
+                   : cosine_lr(e->ac.lr, e->ac.warmup, e->ac.total_steps, 0.1f, e->step_count);
+    int t = (int)e->step_count + 1;
+    CK(ta_adamw_fused(e->master, e->shadow, e->mom, e->vel, e->grad, e->nparam, lr, e->ac.b1,
+                      e->ac.b2, e->ac.eps, e->ac.wd, t, e->ac.grad_clip, e->norm_dev, e->s));
+    TA_HIP(hipMemcpyAsync(e->norm_host, e->norm_dev, 4, hipMemcpyDeviceToHost, e->s));
+    TA_HIP(hipEventRecord(e->ev[3], e->s));
+    TA_HIP(hipStreamSynchronize(e->s));
+    for (int i = 0; i < 3; i++) TA_HIP(hipEventElapsedTime(&e->phase[i], e->ev[i], e->ev[i + 1]));
+    // adapt_trainer.cu:237-246: mean over tokens whose loss > 1e-9
+    float mean = 0.f;
+    int valid = 0;
+    for (int i = 0; i < BT; i++)
+        if (e->loss_host[i] > 1e-9f) {
+            mean += e->loss_host[i];
+            valid++;
+        }
+    if (valid > 0) mean /= (float)valid;
+    float norm = e->norm_host[0];
+    e->step_count++;
+    if (m) {
+        m->loss = mean;
+        m->lr = lr;
+        m->gnorm_raw = norm;
+        m->gnorm = std::min(norm, e->ac.grad_clip);
+        m->valid_tokens = valid;
+        m->step = (int)e->step_count;
+        m->step_ms =
+            std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
+    }
+    return 0;
+}
+
+static bf16** weight_slot(Engine* e, const std::string& name, int64_t* n, int* layer, int* proj) {
+    const int H = e->H;
+    *layer = -1;
+    *proj = -1;
+    if (name == "model.embed_tokens.weight") {
+        *n = (int64_t)e->V * H;
+        return &e->embed;
+    }
+    if (name == "model.norm.weight") {
+        *n = H;
+        return &e->final_norm;
+    }
+    if (name == "lm_head.weight") {
+        *n = (int64_t)e->V * H;
+        return e->mc.tie ? nullptr : &e->lm;
+    }
+    const std::string pre = "model.layers.";
+    if (name.compare(0, pre.size(), pre) != 0) return nullptr;
+    size_t dot = name.find('.', pre.size());
+    if (dot == std::string::npos) return nullptr;
+    int l = atoi(name.substr(pre.size(), dot - pre.size()).c_str());
+    if (l < 0 || l >= (int)e->L.size()) return nullptr;
+    std::string k = name.substr(dot + 1);
+    Layer& ly = e->L[l];
+    *layer = l;
+    if (k == "input_layernorm.weight") {
+        *n = H;
+        return &ly.in_norm;
+    }
+    if (k == "post_attention_layernorm.weight") {
+        *n = H;
+        return &ly.post_norm;
+    }
+    for (int b = 0; b < 3; b++)
+        if (k == std::string(kProj[b]) + ".bias") {
+            *n = b == 0 ? e->qd : e->kvd;
+            return &ly.bias[b];
+        }
+    for (int p = 0; p < NPAIR; p++)
+        if (k == std::string(kProj[p]) + ".weight") {
+            *n = (int64_t)ly.pr[p].in * ly.pr[p].out;
+            *proj = p;
+            return &ly.W[p];
+        }
+    return nullptr;
+}
+
+// after a projection (or the LM head / embedding) changes: refresh W^T
+static int refresh_transpose(Engine* e, const std::string& name, int layer, int proj) {
+    if (proj >= 0) {
+        Pair& p = e->L[layer].pr[proj];
+        return transpose_bf16(e->L[layer].W[proj], e->L[layer].Wt[proj], p.out, p.in, e->s);
+    }
+    if (name == "model.embed_tokens.weight" && e->mc.tie)
+        return transpose_bf16(e->embed, e->embedT, e->V, e->H, e->s);
+    if (name == "lm_head.weight") return transpose_bf16(e->lm, e->lmT, e->V, e->H, e->s);
+    return 0;
+}
+
+}  // namespace ta
+
+using namespace ta;
+
+extern "C" {
+
+void* ta_engine_create(const ta_model_config* mc, const ta_adapt_config* ac, int B, int T,
+                       void* stream) {
+    if (!mc || !ac || B <= 0 || T <= 0) {
+        set_error(-1, "engine_create: bad arguments");
+        return nullptr;
+    }
+    if (mc->n_kv <= 0 || mc->n_q % mc->n_kv != 0 || mc->hidden <= 0 || mc->layers <= 0 ||
+        (mc->head_dim != 64 && mc->head_dim != 128) || ac->rank <= 0 || mc->vocab <= 0) {
+        set_error(-1, "engine_create: unsupported shape (head_dim 64/128, n_q %% n_kv == 0)");
+        return nullptr;
+    }
+    Engine* e = new Engine();
+    e->mc = *mc;
+    e->ac = *ac;
+    e->B = B;
+    e->T = T;
+    e->BT = B * T;
+    e->H = mc->hidden;
+    e->qd = mc->n_q * mc->head_dim;
+    e->kvd = mc->n_kv * mc->head_dim;
+    e->I = mc->inter;
+    e->V = mc->vocab;
+    e->r = ac->rank;
+    e->scale = ac->alpha / (float)ac->rank;  // adapter_model.cu:139
+    if (stream) {
+        e->s = (hipStream_t)stream;
+    } else {
+        if (hipStreamCreate(&e->s) != hipSuccess) {
+            set_error(-2, "engine_create: hipStreamCreate failed");
+            delete e;
+            return nullptr;
+        }
+        e->own_stream = true;
+    }
+    if (engine_alloc(e) != 0 || adapter_init(e) != 0) {
+        std::string msg = ta_last_error();
+        ta_engine_destroy(e);
+        set_error(-2, "%s", msg.c_str());
+        return nullptr;
+    }
+    return e;
+}
+
+int ta_engine_destroy(void* ep) {
+    Engine* e = (Engine*)ep;
+    if (!e) return 0;
+    if (e->s) (void)hipStreamSynchronize(e->s);
+    for (void* p : e->allocs) (void)hipFree(p);
+    for (void* p : {(void*)e->tok_host, (void*)e->tgt_host, (void*)e->loss_host,
+                    (void*)e->norm_host})
+        if (p) (void)hipHostFree(p);
+    for (auto& ev : e->ev)
+        if (ev) (void)hipEventDestroy(ev);
+    if (e->own_stream) (void)hipStreamDestroy(e->s);
+    delete e;
+    return 0;
+}
+
+int ta_engine_set_weight(void* ep, const char* name, const uint16_t* host, int64_t n) {
+    Engine* e = (Engine*)ep;
+    TA_REQUIRE(e && name && host, "engine_set_weight: null argument");
+    int64_t want = 0;
+    int layer, proj;
+    bf16** slot = weight_slot(e, name, &want, &layer, &proj);
+    TA_REQUIRE(slot, "engine_set_weight: unknown tensor '%s'", name);
+    TA_REQUIRE(n == want, "engine_set_weight: '%s' has %lld elements, expected %lld", name,
+               (long long)n, (long long)want);
+    TA_HIP(hipMemcpyAsync(*slot, host, n * 2, hipMemcpyHostToDevice, e->s));
+    CK(refresh_transpose(e, name, layer, proj));
+    TA_HIP(hipStreamSynchronize(e->s));
+    return 0;
+}
+
+int ta_engine_init_random(void* ep, uint64_t seed, float std) {
+    Engine* e = (Engine*)ep;
+    TA_REQUIRE(e, "engine_init_random: null engine");
+    uint64_t sid = 0;
+    CK(fill_normal_bf16(e->embed, (int64_t)e->V * e->H, seed, sid++, std, e->s));
+    CK(refresh_transpose(e, "model.embed_tokens.weight", -1, -1));
+    if (!e->mc.tie) {
+        CK(fill_normal_bf16(e->lm, (int64_t)e->V * e->H, seed, sid++, std, e->s));
+        CK(refresh_transpose(e, "lm_head.weight", -1, -1));
+    }
+    CK(fill_bf16(e->final_norm, e->H, 1.f, e->s));
+    for (int l = 0; l < (int)e->L.size(); l++) {
+        Layer& ly = e->L[l];
+        CK(fill_bf16(ly.in_norm, e->H, 1.f, e->s));
+        CK(fill_bf16(ly.post_norm, e->H, 1.f, e->s));
+        CK(fill_bf16(ly.bias[0], e->qd, 0.f, e->s));
+        CK(fill_bf16(ly.bias[1], e->kvd, 0.f, e->s));
+        CK(fill_bf16(ly.bias[2], e->kvd, 0.f, e->s));
+        for (int p = 0; p < NPAIR; p++) {
+            CK(fill_normal_bf16(ly.W[p], (int64_t)ly.pr[p].in * ly.pr[p].out, seed,
+                                1000 + l * 16 + p, std, e->s));
+            CK(refresh_transpose(e, "", l, p));
+        }
+    }
+    TA_HIP(hipStreamSynchronize(e->s));
+    return 0;
+}
+
+int ta_engine_step(void* ep, const int32_t* inputs, const int32_t* targets, float lr_override,
+                   ta_step_metrics* m) {
+    Engine* e = (Engine*)ep;
+    TA_REQUIRE(e && inputs && targets, "engine_step: null argument");
+    for (int i = 0; i < e->BT; i++)
+        TA_REQUIRE(inputs[i] >= 0 && inputs[i] < e->V, "engine_step: token id %d out of range",
+                   inputs[i]);
+    return engine_step(e, inputs, targets, lr_override, m);
+}
+
+// Locate one adapter tensor: device pointer, element count and element size.
+static int adapter_slot(Engine* e, int layer, int target, int which, void** ptr, int64_t* cnt,
+                        size_t* es) {
+    TA_REQUIRE(layer >= 0 && layer < (int)e->L.size() && target >= 0 && target < NPAIR,
+               "engine adapter: bad layer/target");
+    Pair& p = e->L[layer].pr[target];
+    TA_REQUIRE(p.on, "engine adapter: target %d not injected", target);
+    bool isA = (which == 0 || which == 2 || which == 3 || which == 6 || which == 8);
+    *cnt = isA ? (int64_t)e->r * p.in : (int64_t)p.out * e->r;
+    int64_t off = isA ? p.offA : p.offB;
+    *es = 4;
+    switch (which) {
+        case 0: case 1: *ptr = e->master + off; break;
+        case 2: case 4: *ptr = e->mom + off; break;
+        case 3: case 5: *ptr = e->vel + off; break;
+        case 6: case 7: *ptr = e->grad + off; break;
+        case 8: case 9: *ptr = e->shadow + off; *es = 2; break;
+        default: return set_error(-1, "engine adapter: bad which=%d", which);
+    }
+    return 0;
+}
+
+int ta_engine_write_adapter(void* ep, int layer, int target, int which, const void* host,
+                            int64_t n) {
+    Engine* e = (Engine*)ep;
+    TA_REQUIRE(e && host, "engine_write_adapter: null argument");
+    void* dst;
+    int64_t cnt;
+    size_t es;
+    CK(adapter_slot(e, layer, target, which, &dst, &cnt, &es));
+    TA_REQUIRE(n == cnt, "engine_write_adapter: n=%lld, tensor has %lld", (long long)n,
+               (long long)cnt);
+    TA_HIP(hipMemcpyAsync(dst, host, cnt * es, hipMemcpyHostToDevice, e->s));
+    TA_HIP(hipStreamSynchronize(e->s));
+    return 0;
+}
+
+int ta_engine_read_adapter(void* ep, int layer, int target, int which, void* host, int64_t n) {
+    Engine* e = (Engine*)ep;
+    TA_REQUIRE(e && host, "engine_read_adapter: null argument");
+    void* src;
+    int64_t cnt;
+    size_t es;
+    CK(adapter_slot(e, layer, target, which, &src, &cnt, &es));
+    TA_REQUIRE(n == cnt, "engine_read_adapter: n=%lld, tensor has %lld", (long long)n,
+               (long long)cnt);
+    TA_HIP(hipMemcpyAsync(host, src, cnt * es, hipMemcpyDeviceToHost, e->s));
+    TA_HIP(hipStreamSynchronize(e->s));
+    return 0;
+}
+
+int ta_engine_centroid(void* ep, double* host) {
+    Engine* e = (Engine*)ep;
+    TA_REQUIRE(e && host, "engine_centroid: null argument");
+    TA_HIP(hipMemcpyAsync(host, e->cacc, (e->H + 1) * sizeof(double), hipMemcpyDeviceToHost, e->s));
+    TA_HIP(hipStreamSynchronize(e->s));
+    return 0;
+}
+
+void* ta_engine_buffer(void* ep, const char* name, int64_t* n, int* is_f32) {
+    Engine* e = (Engine*)ep;
+    if (!e || !name) return nullptr;
+    auto it = e->named.find(name);
+    if (it == e->named.end()) {
+        set_error(-1, "engine_buffer: no buffer '%s'", name);
+        return nullptr;
+    }
+    if (n) *n = it->second.second.first;
+    if (is_f32) *is_f32 = it->second.second.second;
+    return it->second.first;
+}
+
+int ta_engine_read_buffer(void* ep, const char* name, void* host, int64_t n) {
+    Engine* e = (Engine*)ep;
+    TA_REQUIRE(e && name && host, "engine_read_buffer: null argument");
+    auto it = e->named.find(name);
+    TA_REQUIRE(it != e->named.end(), "engine_read_buffer: no buffer '%s'", name);
+    TA_REQUIRE(n >= 0 && n <= it->second.second.first, "engine_read_buffer: n=%lld too large",
+               (long long)n);
+    size_t es = it->second.second.second ? 4 : 2;
+    TA_HIP(hipStreamSynchronize(e->s));
+    TA_HIP(hipMemcpy(host, it->second.first, n * es, hipMemcpyDeviceToHost));
+    return 0;
+}
+
+int ta_engine_phase_ms(void* ep, float* f, float* b, float* t) {
+    Engine* e = (Engine*)ep;
+    TA_REQUIRE(e, "engine_phase_ms: null engine");
+    if (f) *f = e->phase[0];
+    if (b) *b = e->phase[1];
+    if (t) *t = e->phase[2];
+    return 0;
+}
+
+}  // extern "C"

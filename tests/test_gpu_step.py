@@ -1,0 +1,213 @@
+"""Full LoRA training step on the GPU engine vs the CPU oracle.
+
+Same seeded BF16 base, same tokens, same adapter init on both sides; the
+engine runs its gfx950 kernels through include/ta_engine.h.  Bars (from the
+north star): loss within 1e-3 relative; per-tensor gradients and updated
+adapters relative L2 <= 1e-2; token masking and step counters exact.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+import tadapt
+
+pytestmark = pytest.mark.gpu
+
+C1_MODEL = dict(vocab=151936, hidden=896, layers=1, n_q=14, n_kv=2, head_dim=64, inter=4864,
+                rms_eps=1e-6, rope_theta=1e6, tie=1)
+C1_ADAPT = dict(rank=8, alpha=16.0, inject_mask=0b0000101, lr=1e-4, grad_clip=1.0, warmup=0,
+                total_steps=1, b1=0.9, b2=0.999, eps=1e-8, wd=0.01)
+SMALL_MODEL = dict(vocab=2048, hidden=256, layers=2, n_q=4, n_kv=2, head_dim=64, inter=512,
+                   rms_eps=1e-6, rope_theta=1e6, tie=1)
+SMALL_ADAPT = dict(rank=16, alpha=32.0, inject_mask=0b1111111, lr=1e-3, grad_clip=1.0, warmup=1,
+                   total_steps=4, b1=0.9, b2=0.999, eps=1e-8, wd=0.01)
+
+
+def base_tensors(mc, seed):
+    """HF-named synthetic Qwen2 base: N(0, 0.02) weights, unit norms, zero biases."""
+    rng = np.random.default_rng(seed)
+    H, I, V = mc["hidden"], mc["inter"], mc["vocab"]
+    qd, kvd = mc["n_q"] * mc["head_dim"], mc["n_kv"] * mc["head_dim"]
+
+    def w(*shape):
+        return O.bf16_from_f32((rng.standard_normal(shape) * 0.02).astype(np.float32))
+
+    one = lambda n: O.bf16_from_f32(np.ones(n, np.float32))
+    zero = lambda n: np.zeros(n, np.uint16)
+    t = {"model.embed_tokens.weight": w(V, H), "model.norm.weight": one(H)}
+    for l in range(mc["layers"]):
+        p = f"model.layers.{l}."
+        t[p + "input_layernorm.weight"] = one(H)
+        t[p + "post_attention_layernorm.weight"] = one(H)
+        t[p + "self_attn.q_proj.weight"] = w(qd, H)
+        t[p + "self_attn.q_proj.bias"] = zero(qd)
+        t[p + "self_attn.k_proj.weight"] = w(kvd, H)
+        t[p + "self_attn.k_proj.bias"] = zero(kvd)
+        t[p + "self_attn.v_proj.weight"] = w(kvd, H)
+        t[p + "self_attn.v_proj.bias"] = zero(kvd)
+        t[p + "self_attn.o_proj.weight"] = w(H, qd)
+        t[p + "mlp.gate_proj.weight"] = w(I, H)
+        t[p + "mlp.up_proj.weight"] = w(I, H)
+        t[p + "mlp.down_proj.weight"] = w(H, I)
+    return t
+
+
+def make_pair(mc, ac, B, T, seed):
+    tensors = base_tensors(mc, seed)
+    orc = O.OracleModel(mc, ac)
+    eng = tadapt.Engine(mc, ac, B, T)
+    for name, arr in tensors.items():
+        orc.set_weight(name, arr)
+        eng.set_weight(name, arr)
+    return orc, eng
+
+
+def chat_tokens(V, B, T, rng):
+    """uniform ids with a few assistant spans (<|im_start|> assistant ... <|im_end|>)
+    so that some targets survive the trainer's masking."""
+    toks = rng.integers(0, min(V, 150000), B * T).astype(np.int32)
+    if V > 151645:
+        for b in range(B):
+            s = b * T + 5
+            toks[s], toks[s + 1] = 151644, 77091
+            toks[s + 12] = 151645
+    return toks
+
+
+def rel(a, b):
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    nb = np.linalg.norm(b)
+    return float(np.linalg.norm(a - b) / nb) if nb > 0 else float(np.linalg.norm(a))
+
+
+def pairs(mc, ac):
+    for l in range(mc["layers"]):
+        for ti, t in enumerate(tadapt.TARGETS):
+            if (ac["inject_mask"] >> ti) & 1:
+                yield l, t
+
+
+def compare(orc, eng, mc, ac, what, bar=1e-2):
+    bad = []
+    for l, t in pairs(mc, ac):
+        for which in what:
+            r = rel(eng.adapter(l, t, which), orc.adapter(l, t, which))
+            if r > bar:
+                bad.append(f"l{l}.{t}.{which}: rel-L2 {r:.3e}")
+    assert not bad, "; ".join(bad)
+
+
+def check_band(orc, eng, mc, ac, before=None):
+    """Updated adapters vs the oracle where the update is determined.
+
+    An AdamW update m_hat/(sqrt(v_hat)+eps) is a sign function of the
+    gradient wherever the moments held nothing before (B at step 1, A at the
+    first step with B != 0), so an element whose gradient lies inside the
+    GPU-vs-oracle gradient error band can legitimately move the other way.
+    Checked per tensor: over the elements where |g_oracle| exceeds 4x the
+    RMS gradient difference, the update (updated - before; before = 0 for B
+    at step 1) has relative L2 <= 1e-2 against the oracle's; as a sanity
+    bound on the gradient error, fewer
+    than 25% of elements are excluded (measured on MI355X: ~1% at c1, 3-10%
+    on the 2-layer config whose gradients differ from the oracle by up to
+    1e-2: one-ulp BF16 rounding differences propagate through the
+    layers)."""
+    for l, t in pairs(mc, ac):
+        for w in ("A", "B"):
+            go, gg = orc.adapter(l, t, "g" + w), eng.adapter(l, t, "g" + w)
+            if not np.any(go):
+                continue
+            band = 4.0 * float(np.sqrt(np.mean((gg.astype(np.float64) - go) ** 2)))
+            sure = np.abs(go) > band
+            b0 = before[(l, t, w)] if before else np.zeros_like(go)
+            uo = (orc.adapter(l, t, w).astype(np.float64) - b0)[sure]
+            ug = (eng.adapter(l, t, w).astype(np.float64) - b0)[sure]
+            assert rel(ug, uo) <= 1e-2, (l, t, w, rel(ug, uo))
+            assert (~sure).mean() < 0.25, (l, t, w, float((~sure).mean()))
+
+
+def check_adamw_of_own_grads(eng, mc, ac, state, lr, t, gnorm_raw):
+    """The engine's update is exactly AdamW (clip, bias correction, weight
+    decay; ops.cu:1139-1158, adapt_trainer.cu:55-70) of its own gradients
+    from the given starting state."""
+    scale = np.float32(ac["grad_clip"] / (gnorm_raw + 1e-6)) if gnorm_raw > ac["grad_clip"] else None
+    for l, tg in pairs(mc, ac):
+        for w in ("A", "B"):
+            g = eng.adapter(l, tg, "g" + w)
+            if scale is not None:
+                g = (g * scale).astype(np.float32)
+            p = state[(l, tg, w)].copy()
+            m = state[(l, tg, "m" + w)].copy()
+            v = state[(l, tg, "v" + w)].copy()
+            sh = np.empty(p.size, np.uint16)
+            O.adamw_step(p, sh, m, v, np.ascontiguousarray(g, np.float32), lr, ac["b1"], ac["b2"],
+                         ac["eps"], ac["wd"], t)
+            got = eng.adapter(l, tg, w)
+            tol = 1e-5 * np.abs(p) + 1e-6 * np.abs(p).max() + 1e-12
+            assert np.all(np.abs(got - p) <= tol), (l, tg, w)
+            mg = eng.adapter(l, tg, "m" + w)
+            assert np.all(np.abs(mg - m) <= 1e-5 * np.abs(m) + 1e-6 * np.abs(m).max() + 1e-30)
+
+
+def sync_state(orc, eng, mc, ac):
+    """Give the engine the oracle's adapter state (masters, shadows, moments)."""
+    for l, t in pairs(mc, ac):
+        for which in ("A", "B", "mA", "vA", "mB", "vB", "A16", "B16"):
+            eng.write_adapter(l, t, which, orc.adapter(l, t, which))
+
+
+def snapshot(orc, mc, ac):
+    return {(l, t, w): orc.adapter(l, t, w).copy() for l, t in pairs(mc, ac)
+            for w in ("A", "B", "mA", "vA", "mB", "vB")}
+
+
+def test_c1_single_step_matches_oracle():
+    mc, ac, B, T = C1_MODEL, C1_ADAPT, 1, 128
+    orc, eng = make_pair(mc, ac, B, T, seed=11)
+    state = snapshot(orc, mc, ac)
+    rng = np.random.default_rng(5)
+    toks = chat_tokens(mc["vocab"], B, T + 1, rng)[:B * T + 1]
+    inp, tgt = toks[:-1].copy(), toks[1:].copy()
+    so = orc.step(inp, tgt, B, T, lr_override=1e-4)
+    sg = eng.step(inp, tgt, lr_override=1e-4)
+    assert sg["valid_tokens"] == so["valid_tokens"] > 0
+    assert sg["step"] == so["step"] == 1
+    assert abs(sg["loss"] - so["loss"]) <= 1e-3 * abs(so["loss"])
+    # the random base gives near-uniform logits: loss ~ ln V (docs/lora_training.md:11)
+    assert abs(so["loss"] - np.log(mc["vocab"])) < 0.5
+    assert abs(sg["gnorm_raw"] - so["gnorm_raw"]) <= 1e-2 * so["gnorm_raw"]
+    assert so["gnorm_raw"] < ac["grad_clip"]  # no clipping: raw grads are comparable
+    compare(orc, eng, mc, ac, ("gB", "mB", "vB", "A", "A16"))
+    # A grads are exactly zero at step 1 (B = 0)
+    assert not np.any(eng.adapter(0, "q", "gA"))
+    check_adamw_of_own_grads(eng, mc, ac, state, sg["lr"], 1, sg["gnorm_raw"])
+    check_band(orc, eng, mc, ac)
+
+
+def test_small_all_targets_multistep_matches_oracle():
+    """Three steps over all seven targets, cosine schedule with warmup.  Before
+    each step the engine receives the oracle's adapter state, so every step
+    is compared from the same starting point (steps 2-3 have B != 0: the full
+    LoRA backward runs)."""
+    mc, ac, B, T = SMALL_MODEL, SMALL_ADAPT, 2, 64
+    orc, eng = make_pair(mc, ac, B, T, seed=23)
+    rng = np.random.default_rng(9)
+    for step in range(3):
+        sync_state(orc, eng, mc, ac)
+        state = snapshot(orc, mc, ac)
+        toks = rng.integers(0, mc["vocab"], B * T + 1).astype(np.int32)
+        inp, tgt = toks[:-1].copy(), toks[1:].copy()
+        so = orc.step(inp, tgt, B, T)
+        sg = eng.step(inp, tgt)
+        assert sg["step"] == so["step"] == step + 1
+        assert abs(sg["lr"] - so["lr"]) <= 1e-7 * so["lr"]
+        assert abs(sg["loss"] - so["loss"]) <= 1e-3 * abs(so["loss"]), (step, sg, so)
+        assert abs(sg["gnorm_raw"] - so["gnorm_raw"]) <= 1e-2 * so["gnorm_raw"], (step, sg, so)
+        if so["gnorm_raw"] <= ac["grad_clip"]:
+            compare(orc, eng, mc, ac, ("gB",) if step == 0 else ("gA", "gB"))
+        check_adamw_of_own_grads(eng, mc, ac, state, sg["lr"], step + 1, sg["gnorm_raw"])
+        check_band(orc, eng, mc, ac, before={k: v for k, v in state.items() if k[2] in "AB"})
+    ca, cw = eng.centroid()
+    oa, ow = orc.centroid()
+    assert rel(ca, oa) < 1e-2 and abs(cw - ow) <= 1e-2 * ow
