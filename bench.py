@@ -1,0 +1,205 @@
+#!/usr/bin/env python3
+"""Headline benchmark: LoRA training throughput of the MI355X step engine.
+
+Workload ("c3"): Qwen2-1.5B shape — 28 layers,
+hidden 1536, 12 Q / 2 KV heads, head_dim 128, SwiGLU 8960, vocab 151936,
+tied embedding — BF16 frozen base ~N(0, 0.02) generated on the device from a
+seed, LoRA r=16 alpha=32 on all seven projections, batch 8 x seq 1024 of
+uniform random token ids (next-token targets as Dataset::next_batch makes
+them), AdamW.  A step is one full training step (forward, cross entropy,
+backward, centroid accumulation, grad norm/clip, AdamW) with the batch
+already resident in HBM.
+
+Prints one JSON line.  Besides tokens/s it carries:
+  roofline     — the kernel class with the largest share of step time,
+                 timed with HIP events on the engine's stream during the
+                 timed steps: algorithmic flops (or bytes) / measured time,
+                 against MI355X peak (2.5 PFLOP/s dense BF16, 8 TB/s HBM).
+  cpu_baseline — the CPU restatement of the reference step (oracle/, a
+                 port: the reference has no CPU path) on this host's cores,
+                 on a bounded sample, extrapolated to the c3 model.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "tensor-adapt_amd"))
+
+C3_MODEL = dict(vocab=151936, hidden=1536, layers=28, n_q=12, n_kv=2, head_dim=128, inter=8960,
+                rms_eps=1e-6, rope_theta=1e6, tie=1)
+C3_ADAPT = dict(rank=16, alpha=32.0, inject_mask=0b1111111, lr=1e-4, grad_clip=1.0, warmup=5,
+                total_steps=50, b1=0.9, b2=0.999, eps=1e-8, wd=0.0)
+C3_B, C3_T = 8, 1024
+
+CAT_NAMES = ["gemm_fwd", "gemm_dx", "lm_head", "lora", "attn_fwd", "attn_bwd", "norm",
+             "elementwise", "cross_entropy", "adamw_tail", "centroid"]
+MFMA_CATS = {0, 1, 2, 3, 4, 5}
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+
+def token_batches(n, B, T, V, seed):
+    """n batches of Dataset::next_batch windows (src/data/dataset.cpp:56-71)
+    over a uniform random uint32 token stream: input[b,t] = tok[pos+t],
+    target = the next token, pos += T per row."""
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    stream = rng.integers(0, V, n * B * T + 1, dtype=np.int64).astype(np.int32)
+    out = []
+    pos = 0
+    for _ in range(n):
+        inp = np.empty(B * T, np.int32)
+        tgt = np.empty(B * T, np.int32)
+        for b in range(B):
+            inp[b * T:(b + 1) * T] = stream[pos:pos + T]
+            tgt[b * T:(b + 1) * T] = stream[pos + 1:pos + T + 1]
+            pos += T
+        out.append((inp, tgt))
+    return out
+
+
+def cpu_baseline(model, adapt):
+    """Oracle (CPU restatement of the reference step) on this host, bounded
+    sample: (A) one c3 transformer layer, forward+backward+AdamW, B=1 x
+    T=1024, with a 2048-entry vocabulary so the LM head is negligible;
+    (B) the c3 LM head + cross entropy + final norm alone (0 layers, full
+    151936 vocabulary) on 256 tokens.  Per-token cost of the c3 model =
+    28 * A/1024 + B/256 (the head is linear in tokens, a layer is linear in
+    B at fixed T=1024)."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import numpy as np
+    import oracle as O
+    rng = np.random.default_rng(7)
+
+    def run(mc, B, T):
+        m = O.OracleModel(mc, adapt)
+        H, I, V = mc["hidden"], mc["inter"], mc["vocab"]
+        qd, kvd = mc["n_q"] * mc["head_dim"], mc["n_kv"] * mc["head_dim"]
+        w = lambda *s: O.bf16_from_f32((rng.standard_normal(s, np.float32) * 0.02))
+        ones = O.bf16_from_f32(np.ones(H, np.float32))
+        m.set_weight("model.embed_tokens.weight", w(V, H))
+        m.set_weight("model.norm.weight", ones)
+        for l in range(mc["layers"]):
+            p = f"model.layers.{l}."
+            for n, a in (("input_layernorm.weight", ones), ("post_attention_layernorm.weight", ones),
+                         ("self_attn.q_proj.weight", w(qd, H)), ("self_attn.k_proj.weight", w(kvd, H)),
+                         ("self_attn.v_proj.weight", w(kvd, H)), ("self_attn.o_proj.weight", w(H, qd)),
+                         ("self_attn.q_proj.bias", np.zeros(qd, np.uint16)),
+                         ("self_attn.k_proj.bias", np.zeros(kvd, np.uint16)),
+                         ("self_attn.v_proj.bias", np.zeros(kvd, np.uint16)),
+                         ("mlp.gate_proj.weight", w(I, H)), ("mlp.up_proj.weight", w(I, H)),
+                         ("mlp.down_proj.weight", w(H, I))):
+                m.set_weight(p + n, a)
+        toks = rng.integers(0, V, B * T + 1).astype(np.int32)
+        t0 = time.perf_counter()
+        m.step(toks[:-1], toks[1:], B, T)
+        return time.perf_counter() - t0
+
+    layer_mc = dict(model, layers=1, vocab=2048)
+    head_mc = dict(model, layers=0)
+    t_layer = run(layer_mc, 1, 1024)
+    t_head = run(head_mc, 1, 256)
+    per_tok = model["layers"] * t_layer / 1024.0 + t_head / 256.0
+    cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    return {"value": round(1.0 / per_tok, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": ("oracle step on one c3 layer (B=1, T=1024, %.1f s) and the c3 LM head + "
+                       "CE on 256 tokens (%.1f s), extrapolated to 28 layers" % (t_layer, t_head))}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--categories", action="store_true",
+                    help="print the per-kernel-class time split to stderr")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build runs on one GPU (one process, one MI355X); "
+              f"--gpus {args.gpus} is not supported", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import tadapt
+
+    model, adapt, B, T = C3_MODEL, C3_ADAPT, C3_B, C3_T
+    eng = tadapt.Engine(model, adapt, B, T)
+    eng.init_random(seed=20261201, std=0.02)
+    batches = token_batches(args.warmup + args.steps + len(CAT_NAMES), B, T, model["vocab"], 1)
+    dev = [(torch.from_numpy(i).cuda(), torch.from_numpy(t).cuda()) for i, t in batches]
+    it = iter(dev)
+
+    for _ in range(args.warmup):
+        eng.step_resident(*next(it))
+    # survey: one step per kernel class with that class timed, to find the
+    # class that dominates the step (not part of the timed region)
+    split = {}
+    for c in range(len(CAT_NAMES)):
+        eng.profile(c)
+        eng.step_resident(*next(it))
+        split[c] = eng.profile_read()
+    eng.profile(-1)
+    dom = max(split, key=lambda c: split[c]["ms"])
+    if args.categories:
+        for c, v in split.items():
+            print(f"  {CAT_NAMES[c]:14s} {v['ms']:8.2f} ms  {v['launches']:5d} launches", file=sys.stderr)
+
+    # timed region: the dominant class is event-timed on the engine's stream
+    eng.profile(dom)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    last = None
+    for _ in range(args.steps):
+        last = eng.step_resident(*next(it))
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    prof = eng.profile_read()
+    eng.profile(-1)
+
+    tokens = B * T * args.steps
+    value = tokens / dt
+    if dom in MFMA_CATS:
+        achieved = prof["flops"] / (prof["ms"] * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4)}
+    else:
+        achieved = prof["bytes"] / (prof["ms"] * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4)}
+    roof["traffic"] = None
+    roof["kernel"] = CAT_NAMES[dom]
+    roof["share_of_step"] = round(prof["ms"] / (dt * 1e3), 4)
+    roof["launches"] = prof["launches"]
+
+    out = {
+        "metric": "train tokens/s Qwen2-1.5B LoRA r=16 seq1024; bwd MFMA util %, HBM GB/s",
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / args.steps, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (uniform random token ids; random-init N(0,0.02) BF16 base)",
+        "config": {"workload": "c3: Qwen2-1.5B shape, LoRA r=16 alpha=32 on q,k,v,o,gate,up,down, "
+                               "batch 8 x seq 1024, AdamW, centroid accumulator on",
+                   "global_batch": B, "seq_len": T, "layers": model["layers"],
+                   "hidden": model["hidden"], "parallelism": "single GPU"},
+        "roofline": roof,
+        "loss": round(last["loss"], 4),
+    }
+    del eng
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(model, adapt)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

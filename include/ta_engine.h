@@ -74,6 +74,35 @@ int ta_engine_init_random(void* engine, uint64_t seed, float std);
 int ta_engine_step(void* engine, const int32_t* inputs, const int32_t* targets,
                    float lr_override, ta_step_metrics* metrics);
 
+/* Same step with the batch already resident in device memory (int32 [B*T]
+ * each; the assistant-span masking runs on the device).  No host-to-device
+ * transfer happens inside the step. */
+int ta_engine_step_resident(void* engine, const int32_t* d_inputs, const int32_t* d_targets,
+                            float lr_override, ta_step_metrics* metrics);
+
+/* Kernel-class timing during real steps.  category (TA_CAT_*) selects which
+ * launches are bracketed with HIP events on the engine's stream (-1: none);
+ * each step then adds their summed duration, launch count and algorithmic
+ * work (flops for MFMA GEMMs and attention, HBM bytes for streaming
+ * kernels) to the totals, which ta_engine_profile_read returns and clears. */
+enum {
+    TA_CAT_GEMM_FWD = 0, /* frozen-base projections, forward: x W^T        */
+    TA_CAT_GEMM_DX = 1,  /* frozen-base input gradients: dY W              */
+    TA_CAT_LMHEAD = 2,   /* LM head forward + backward GEMMs              */
+    TA_CAT_LORA = 3,     /* every LoRA GEMM (fwd h, delta; bwd gB, dh, gA, dx) */
+    TA_CAT_ATTN_FWD = 4,
+    TA_CAT_ATTN_BWD = 5,
+    TA_CAT_NORM = 6,     /* RMSNorm forward + backward                    */
+    TA_CAT_ELEMWISE = 7, /* SiLU fwd/bwd, RoPE, residual/LoRA adds        */
+    TA_CAT_CE = 8,
+    TA_CAT_TAIL = 9,     /* grad norm + clip + AdamW                      */
+    TA_CAT_CENTROID = 10,
+    TA_NCAT = 11
+};
+int ta_engine_profile(void* engine, int category);
+int ta_engine_profile_read(void* engine, double* total_ms, int64_t* launches, double* flops,
+                           double* bytes);
+
 /* Copy adapter state to host memory.  target: 0..6 = q,k,v,o,gate,up,down;
  * which: 0 A master, 1 B master, 2 mA, 3 vA, 4 mB, 5 vB, 6 gA, 7 gB (F32),
  * 8 A shadow, 9 B shadow (BF16).  n must equal the tensor's element count. */

@@ -41,6 +41,8 @@ int fill_normal_bf16(bf16* out, int64_t n, uint64_t seed, uint64_t sid, float st
 int fill_bf16(bf16* out, int64_t n, float v, hipStream_t s);
 int kaiming_init(float* a32, bf16* a16, int64_t n, int in_dim, hipStream_t s);
 int add2_bf16(bf16* out, const bf16* a, const bf16* b, int64_t n, hipStream_t s);
+int mask_targets_dev(const int32_t* in, const int32_t* tgt_in, int32_t* tgt, int B, int T,
+                     hipStream_t s);
 
 #define CK(x)                    \
     do {                         \
@@ -97,7 +99,55 @@ struct Engine {
     hipEvent_t ev[4];
     int64_t step_count = 0;
     float phase[3] = {0, 0, 0};
+    const int32_t* tok_cur = nullptr;  // token ids the forward embeds
+
+    // kernel-class timing (ta_engine_profile)
+    int prof_cat = -1;
+    std::vector<hipEvent_t> pev;
+    std::vector<std::pair<double, double>> pwork;  // (flops, bytes) per timed launch
+    double p_ms = 0, p_flops = 0, p_bytes = 0;
+    int64_t p_n = 0;
 };
+
+// Bracket one launch of category `cat` with events when that category is
+// being timed.  Work figures are the algorithmic flops / HBM bytes of the
+// launch, computed from its shape.
+static void prof_begin(Engine* e, int cat) {
+    if (cat != e->prof_cat) return;
+    size_t i = e->pwork.size();
+    while (e->pev.size() < 2 * (i + 1)) {
+        hipEvent_t ev;
+        if (hipEventCreate(&ev) != hipSuccess) return;
+        e->pev.push_back(ev);
+    }
+    (void)hipEventRecord(e->pev[2 * i], e->s);
+}
+static void prof_end(Engine* e, int cat, double flops, double bytes) {
+    if (cat != e->prof_cat) return;
+    size_t i = e->pwork.size();
+    if (e->pev.size() < 2 * (i + 1)) return;
+    (void)hipEventRecord(e->pev[2 * i + 1], e->s);
+    e->pwork.push_back({flops, bytes});
+}
+static int prof_collect(Engine* e) {
+    for (size_t i = 0; i < e->pwork.size(); i++) {
+        float ms = 0.f;
+        TA_HIP(hipEventElapsedTime(&ms, e->pev[2 * i], e->pev[2 * i + 1]));
+        e->p_ms += ms;
+        e->p_n++;
+        e->p_flops += e->pwork[i].first;
+        e->p_bytes += e->pwork[i].second;
+    }
+    e->pwork.clear();
+    return 0;
+}
+#define TIMED(cat, flops, bytes, call)             \
+    do {                                           \
+        prof_begin(e, cat);                        \
+        int _rc2 = (call);                         \
+        prof_end(e, cat, (double)(flops), (double)(bytes)); \
+        if (_rc2 != 0) return _rc2;                \
+    } while (0)
 
 static int dmalloc(Engine* e, void** p, size_t bytes, const char* what) {
     if (bytes == 0) bytes = 256;
@@ -231,15 +281,27 @@ static int adapter_init(Engine* e) {
 }
 
 // ── one LoRA pair (adapter_model.cu:96-129 forward, 131-220 backward) ────
+// algorithmic work of an M x N x K GEMM: flops, and bytes of one read of
+// each operand plus the output (read too when accumulating)
+static inline double gflops(double M, double N, double K) { return 2.0 * M * N * K; }
+static inline double gbytes(double M, double N, double K, double in_b, double out_b, bool acc) {
+    return (M * K + K * N) * in_b + M * N * out_b * (acc ? 2.0 : 1.0);
+}
+
 static int lora_fwd(Engine* e, Pair& p, const bf16* x, bf16* y) {
     const bf16* A = e->shadow + p.offA;
     const bf16* Bm = e->shadow + p.offB;
+    const double BT = e->BT, r = e->r;
     // h = bf16(x A^T) [BT, r]; delta = bf16(h B^T) [BT, out]; y = bf16(y + s*delta)
-    CK(gemm_dispatch(true, true, e->BT, e->r, p.in, 1.f, x, p.in, A, p.in, 0.f, p.h, e->r, nullptr,
-                     false, e->s, 0));
-    CK(gemm_dispatch(true, true, e->BT, p.out, e->r, 1.f, p.h, e->r, Bm, e->r, 0.f, e->delta, p.out,
-                     nullptr, false, e->s, 0));
-    return ta_lora_add(y, e->delta, e->scale, (int64_t)e->BT * p.out, e->s);
+    TIMED(TA_CAT_LORA, gflops(BT, r, p.in), gbytes(BT, r, p.in, 2, 2, false),
+          gemm_dispatch(true, true, e->BT, e->r, p.in, 1.f, x, p.in, A, p.in, 0.f, p.h, e->r,
+                        nullptr, false, e->s, 0));
+    TIMED(TA_CAT_LORA, gflops(BT, p.out, r), gbytes(BT, p.out, r, 2, 2, false),
+          gemm_dispatch(true, true, e->BT, p.out, e->r, 1.f, p.h, e->r, Bm, e->r, 0.f, e->delta,
+                        p.out, nullptr, false, e->s, 0));
+    TIMED(TA_CAT_ELEMWISE, 0, BT * p.out * 6,
+          ta_lora_add(y, e->delta, e->scale, (int64_t)e->BT * p.out, e->s));
+    return 0;
 }
 
 static int lora_bwd(Engine* e, Pair& p, const bf16* x, const bf16* go, bf16* gx) {
@@ -250,30 +312,39 @@ static int lora_bwd(Engine* e, Pair& p, const bf16* x, const bf16* go, bf16* gx)
     const int BT = e->BT, r = e->r;
     // h is the forward's x*A^T (the reference recomputes the same product)
     // gB += s * go^T h       [out, r]
-    CK(gemm_dispatch(false, false, p.out, r, BT, e->scale, go, p.out, p.h, r, 1.f, gB, r, nullptr,
-                     true, e->s, 0));
+    TIMED(TA_CAT_LORA, gflops(p.out, r, BT), gbytes(p.out, r, BT, 2, 4, true),
+          gemm_dispatch(false, false, p.out, r, BT, e->scale, go, p.out, p.h, r, 1.f, gB, r,
+                        nullptr, true, e->s, 0));
     // dh = bf16(go B)        [BT, r]
-    CK(gemm_dispatch(true, false, BT, r, p.out, 1.f, go, p.out, Bm, r, 0.f, e->dh, r, nullptr,
-                     false, e->s, 0));
+    TIMED(TA_CAT_LORA, gflops(BT, r, p.out), gbytes(BT, r, p.out, 2, 2, false),
+          gemm_dispatch(true, false, BT, r, p.out, 1.f, go, p.out, Bm, r, 0.f, e->dh, r, nullptr,
+                        false, e->s, 0));
     // gA += s * dh^T x       [r, in]
-    CK(gemm_dispatch(false, false, r, p.in, BT, e->scale, e->dh, r, x, p.in, 1.f, gA, p.in, nullptr,
-                     true, e->s, 0));
+    TIMED(TA_CAT_LORA, gflops(r, p.in, BT), gbytes(r, p.in, BT, 2, 4, true),
+          gemm_dispatch(false, false, r, p.in, BT, e->scale, e->dh, r, x, p.in, 1.f, gA, p.in,
+                        nullptr, true, e->s, 0));
     // gx = bf16(gx + s * dh A)
-    return gemm_dispatch(true, false, BT, p.in, r, e->scale, e->dh, r, A, p.in, 1.f, gx, p.in,
-                         nullptr, false, e->s, 0);
+    TIMED(TA_CAT_LORA, gflops(BT, p.in, r), gbytes(BT, p.in, r, 2, 2, true),
+          gemm_dispatch(true, false, BT, p.in, r, e->scale, e->dh, r, A, p.in, 1.f, gx, p.in,
+                        nullptr, false, e->s, 0));
+    return 0;
 }
 
 // proj_fwd (qwen2.cu:21-30) with the bias add fused: y = bf16(bf16(x W^T) + b)
 static int proj_fwd(Engine* e, const bf16* W, const bf16* x, bf16* y, int in, int out,
                     const bf16* bias) {
-    return gemm_dispatch(true, true, e->BT, out, in, 1.f, x, in, W, in, 0.f, y, out, bias, false,
-                         e->s, 0);
+    TIMED(TA_CAT_GEMM_FWD, gflops(e->BT, out, in), gbytes(e->BT, out, in, 2, 2, false),
+          gemm_dispatch(true, true, e->BT, out, in, 1.f, x, in, W, in, 0.f, y, out, bias, false,
+                        e->s, 0));
+    return 0;
 }
 // proj_bwd_x (qwen2.cu:32-41): dx = bf16(dy W + beta dx), W^T resident
 static int proj_bwd_x(Engine* e, const bf16* Wt, const bf16* dy, bf16* dx, int out, int in,
                       float beta) {
-    return gemm_dispatch(true, true, e->BT, in, out, 1.f, dy, out, Wt, out, beta, dx, in, nullptr,
-                         false, e->s, 0);
+    TIMED(TA_CAT_GEMM_DX, gflops(e->BT, in, out), gbytes(e->BT, in, out, 2, 2, beta != 0.f),
+          gemm_dispatch(true, true, e->BT, in, out, 1.f, dy, out, Wt, out, beta, dx, in, nullptr,
+                        false, e->s, 0));
+    return 0;
 }
 
 static void mask_targets(const int32_t* in, int32_t* tgt, int B, int T) {
@@ -308,73 +379,100 @@ static float cosine_lr(float base, int64_t warmup, int64_t total, float floor_fr
 static int forward(Engine* e) {
     const ta_model_config& c = e->mc;
     const int BT = e->BT, H = e->H, qd = e->qd, kvd = e->kvd, I = e->I;
+    const double dBT = BT, tri = (double)e->B * c.n_q * e->T * (e->T + 1) / 2.0;
     hipStream_t s = e->s;
-    CK(ta_embed_fwd(e->embed, e->tok_dev, e->L[0].res_in, BT, H, s));
+    TIMED(TA_CAT_ELEMWISE, 0, dBT * H * 4, ta_embed_fwd(e->embed, e->tok_cur, e->L[0].res_in, BT, H, s));
+    const double nrm_b = dBT * H * 4 + H * 2 + dBT * 4;
     for (int l = 0; l < c.layers; l++) {
         Layer& ly = e->L[l];
         bf16* res_out = (l + 1 < c.layers) ? e->L[l + 1].res_in : e->x_final;
-        CK(ta_rms_norm_fwd(ly.res_in, ly.in_norm, ly.xn, ly.in_rms, 1, BT, H, c.rms_eps, s));
+        TIMED(TA_CAT_NORM, 0, nrm_b,
+              ta_rms_norm_fwd(ly.res_in, ly.in_norm, ly.xn, ly.in_rms, 1, BT, H, c.rms_eps, s));
         CK(proj_fwd(e, ly.W[PQ], ly.xn, ly.Q, H, qd, ly.bias[0]));
         CK(proj_fwd(e, ly.W[PK], ly.xn, ly.K, H, kvd, ly.bias[1]));
         CK(proj_fwd(e, ly.W[PV], ly.xn, ly.V, H, kvd, ly.bias[2]));
         if (ly.pr[PQ].on) CK(lora_fwd(e, ly.pr[PQ], ly.xn, ly.Q));
         if (ly.pr[PK].on) CK(lora_fwd(e, ly.pr[PK], ly.xn, ly.K));
         if (ly.pr[PV].on) CK(lora_fwd(e, ly.pr[PV], ly.xn, ly.V));
-        CK(ta_rope_fwd(ly.Q, e->B, e->T, c.n_q, c.head_dim, c.rope_theta, s));
-        CK(ta_rope_fwd(ly.K, e->B, e->T, c.n_kv, c.head_dim, c.rope_theta, s));
+        TIMED(TA_CAT_ELEMWISE, 0, dBT * qd * 4,
+              ta_rope_fwd(ly.Q, e->B, e->T, c.n_q, c.head_dim, c.rope_theta, s));
+        TIMED(TA_CAT_ELEMWISE, 0, dBT * kvd * 4,
+              ta_rope_fwd(ly.K, e->B, e->T, c.n_kv, c.head_dim, c.rope_theta, s));
         // the upper triangle of attn_w is never read by the backward: skip its fill
-        CK(attn_fwd(ly.Q, ly.K, ly.V, ly.ao, ly.attn_w, e->B, e->T, c.n_q, c.n_kv, c.head_dim, false,
-                    s));
+        TIMED(TA_CAT_ATTN_FWD, 4.0 * tri * c.head_dim,
+              tri * 4 + dBT * (2.0 * qd + 2.0 * kvd) * 2,
+              attn_fwd(ly.Q, ly.K, ly.V, ly.ao, ly.attn_w, e->B, e->T, c.n_q, c.n_kv, c.head_dim,
+                       false, s));
         CK(proj_fwd(e, ly.W[PO], ly.ao, e->tmpH, qd, H, nullptr));
         if (ly.pr[PO].on) CK(lora_fwd(e, ly.pr[PO], ly.ao, e->tmpH));
-        CK(add2_bf16(ly.res_mid, ly.res_in, e->tmpH, (int64_t)BT * H, s));
-        CK(ta_rms_norm_fwd(ly.res_mid, ly.post_norm, ly.xn2, ly.post_rms, 1, BT, H, c.rms_eps, s));
+        TIMED(TA_CAT_ELEMWISE, 0, dBT * H * 6,
+              add2_bf16(ly.res_mid, ly.res_in, e->tmpH, (int64_t)BT * H, s));
+        TIMED(TA_CAT_NORM, 0, nrm_b,
+              ta_rms_norm_fwd(ly.res_mid, ly.post_norm, ly.xn2, ly.post_rms, 1, BT, H, c.rms_eps,
+                              s));
         CK(proj_fwd(e, ly.W[PG], ly.xn2, ly.gate, H, I, nullptr));
         CK(proj_fwd(e, ly.W[PU], ly.xn2, ly.up, H, I, nullptr));
         if (ly.pr[PG].on) CK(lora_fwd(e, ly.pr[PG], ly.xn2, ly.gate));
         if (ly.pr[PU].on) CK(lora_fwd(e, ly.pr[PU], ly.xn2, ly.up));
-        CK(ta_silu_mul_fwd(ly.gate, ly.up, ly.act, (int64_t)BT * I, s));
+        TIMED(TA_CAT_ELEMWISE, 0, dBT * I * 6,
+              ta_silu_mul_fwd(ly.gate, ly.up, ly.act, (int64_t)BT * I, s));
         CK(proj_fwd(e, ly.W[PD], ly.act, e->tmpH, I, H, nullptr));
         if (ly.pr[PD].on) CK(lora_fwd(e, ly.pr[PD], ly.act, e->tmpH));
-        CK(add2_bf16(res_out, ly.res_mid, e->tmpH, (int64_t)BT * H, s));
+        TIMED(TA_CAT_ELEMWISE, 0, dBT * H * 6,
+              add2_bf16(res_out, ly.res_mid, e->tmpH, (int64_t)BT * H, s));
     }
-    CK(ta_rms_norm_fwd(e->x_final, e->final_norm, e->xfn, e->final_rms, 1, BT, H, c.rms_eps, s));
+    TIMED(TA_CAT_NORM, 0, nrm_b,
+          ta_rms_norm_fwd(e->x_final, e->final_norm, e->xfn, e->final_rms, 1, BT, H, c.rms_eps, s));
     // LM head (qwen2.cu:163-175), tied to the embedding when c.tie
-    CK(gemm_dispatch(true, true, BT, e->V, H, 1.f, e->xfn, H, e->lm, H, 0.f, e->logits, e->V,
-                     nullptr, false, s, 0));
+    TIMED(TA_CAT_LMHEAD, gflops(BT, e->V, H), gbytes(BT, e->V, H, 2, 2, false),
+          gemm_dispatch(true, true, BT, e->V, H, 1.f, e->xfn, H, e->lm, H, 0.f, e->logits, e->V,
+                        nullptr, false, s, 0));
     // loss (adapt_trainer.cu:201-205): dlogits overwrite the logits in place
-    return ta_cross_entropy_fwd(e->logits, e->tgt_dev, e->loss_tok, e->logits, BT, e->V, s);
+    TIMED(TA_CAT_CE, 0, dBT * e->V * 6,
+          ta_cross_entropy_fwd(e->logits, e->tgt_dev, e->loss_tok, e->logits, BT, e->V, s));
+    return 0;
 }
 
 static int backward(Engine* e) {
     const ta_model_config& c = e->mc;
     const int BT = e->BT, H = e->H, qd = e->qd, kvd = e->kvd, I = e->I;
+    const double dBT = BT, tri = (double)e->B * c.n_q * e->T * (e->T + 1) / 2.0;
     hipStream_t s = e->s;
+    const double nrm_b = dBT * H * 6 + H * 2 + dBT * 4;
     // dres = dlogits * W_lm (qwen2.cu:205); grad = rms_norm_bwd(final)
-    CK(gemm_dispatch(true, true, BT, H, e->V, 1.f, e->logits, e->V, e->lmT, e->V, 0.f, e->dres, H,
-                     nullptr, false, s, 0));
-    CK(ta_rms_norm_bwd(e->dres, e->x_final, e->final_norm, e->final_rms, e->g_res, nullptr, 1, BT,
-                       H, c.rms_eps, s));
+    TIMED(TA_CAT_LMHEAD, gflops(BT, H, e->V), gbytes(BT, H, e->V, 2, 2, false),
+          gemm_dispatch(true, true, BT, H, e->V, 1.f, e->logits, e->V, e->lmT, e->V, 0.f, e->dres,
+                        H, nullptr, false, s, 0));
+    TIMED(TA_CAT_NORM, 0, nrm_b,
+          ta_rms_norm_bwd(e->dres, e->x_final, e->final_norm, e->final_rms, e->g_res, nullptr, 1,
+                          BT, H, c.rms_eps, s));
     for (int l = c.layers - 1; l >= 0; l--) {
         Layer& ly = e->L[l];
         // FFN (qwen2.cu:222-246)
         CK(proj_bwd_x(e, ly.Wt[PD], e->g_res, e->dact, H, I, 0.f));
         if (ly.pr[PD].on) CK(lora_bwd(e, ly.pr[PD], ly.act, e->g_res, e->dact));
-        CK(ta_silu_mul_bwd(e->dact, ly.gate, ly.up, e->dgate, e->dup, (int64_t)BT * I, s));
+        TIMED(TA_CAT_ELEMWISE, 0, dBT * I * 10,
+              ta_silu_mul_bwd(e->dact, ly.gate, ly.up, e->dgate, e->dup, (int64_t)BT * I, s));
         CK(proj_bwd_x(e, ly.Wt[PG], e->dgate, e->dxn2, I, H, 0.f));
         CK(proj_bwd_x(e, ly.Wt[PU], e->dup, e->dxn2, I, H, 1.f));
         if (ly.pr[PG].on) CK(lora_bwd(e, ly.pr[PG], ly.xn2, e->dgate, e->dxn2));
         if (ly.pr[PU].on) CK(lora_bwd(e, ly.pr[PU], ly.xn2, e->dup, e->dxn2));
-        CK(ta_rms_norm_bwd(e->dxn2, ly.res_mid, ly.post_norm, ly.post_rms, e->tmpH, nullptr, 1, BT,
-                           H, c.rms_eps, s));
-        CK(ta_add_inplace(e->g_res, e->tmpH, (int64_t)BT * H, s));
+        TIMED(TA_CAT_NORM, 0, nrm_b,
+              ta_rms_norm_bwd(e->dxn2, ly.res_mid, ly.post_norm, ly.post_rms, e->tmpH, nullptr, 1,
+                              BT, H, c.rms_eps, s));
+        TIMED(TA_CAT_ELEMWISE, 0, dBT * H * 6,
+              ta_add_inplace(e->g_res, e->tmpH, (int64_t)BT * H, s));
         // attention (qwen2.cu:250-304)
         CK(proj_bwd_x(e, ly.Wt[PO], e->g_res, e->dao, H, qd, 0.f));
         if (ly.pr[PO].on) CK(lora_bwd(e, ly.pr[PO], ly.ao, e->g_res, e->dao));
-        CK(attn_bwd(e->dao, ly.Q, ly.K, ly.V, ly.attn_w, e->dQ, e->dK, e->dV, e->B, e->T, c.n_q,
-                    c.n_kv, c.head_dim, e->Dbuf, s));
-        CK(ta_rope_bwd(e->dQ, e->B, e->T, c.n_q, c.head_dim, c.rope_theta, s));
-        CK(ta_rope_bwd(e->dK, e->B, e->T, c.n_kv, c.head_dim, c.rope_theta, s));
+        TIMED(TA_CAT_ATTN_BWD, 8.0 * tri * c.head_dim,
+              tri * 4 + dBT * (2.0 * qd + 2.0 * kvd) * 2 + dBT * (qd + 2.0 * kvd) * 2,
+              attn_bwd(e->dao, ly.Q, ly.K, ly.V, ly.attn_w, e->dQ, e->dK, e->dV, e->B, e->T, c.n_q,
+                       c.n_kv, c.head_dim, e->Dbuf, s));
+        TIMED(TA_CAT_ELEMWISE, 0, dBT * qd * 4,
+              ta_rope_bwd(e->dQ, e->B, e->T, c.n_q, c.head_dim, c.rope_theta, s));
+        TIMED(TA_CAT_ELEMWISE, 0, dBT * kvd * 4,
+              ta_rope_bwd(e->dK, e->B, e->T, c.n_kv, c.head_dim, c.rope_theta, s));
         CK(proj_bwd_x(e, ly.Wt[PQ], e->dQ, e->dxn, qd, H, 0.f));
         CK(proj_bwd_x(e, ly.Wt[PK], e->dK, e->dxn, kvd, H, 1.f));
         CK(proj_bwd_x(e, ly.Wt[PV], e->dV, e->dxn, kvd, H, 1.f));
@@ -383,23 +481,21 @@ static int backward(Engine* e) {
         if (ly.pr[PV].on) CK(lora_bwd(e, ly.pr[PV], ly.xn, e->dV, e->dxn));
         // centroid side channel (adapt_trainer.cu:210-232): h = x_normed,
         // g = dx_attn_in of this layer
-        CK(ta_centroid_accumulate_bf16(ly.xn, e->dxn, BT, H, e->cacc, s));
-        CK(ta_rms_norm_bwd(e->dxn, ly.res_in, ly.in_norm, ly.in_rms, e->tmpH, nullptr, 1, BT, H,
-                           c.rms_eps, s));
-        CK(ta_add_inplace(e->g_res, e->tmpH, (int64_t)BT * H, s));
+        TIMED(TA_CAT_CENTROID, 0, dBT * H * 4,
+              ta_centroid_accumulate_bf16(ly.xn, e->dxn, BT, H, e->cacc, s));
+        TIMED(TA_CAT_NORM, 0, nrm_b,
+              ta_rms_norm_bwd(e->dxn, ly.res_in, ly.in_norm, ly.in_rms, e->tmpH, nullptr, 1, BT, H,
+                              c.rms_eps, s));
+        TIMED(TA_CAT_ELEMWISE, 0, dBT * H * 6,
+              ta_add_inplace(e->g_res, e->tmpH, (int64_t)BT * H, s));
     }
     return 0;
 }
 
-static int engine_step(Engine* e, const int32_t* inputs, const int32_t* targets, float lr_override,
-                       ta_step_metrics* m) {
-    auto t0 = std::chrono::steady_clock::now();
+// The step body; the batch is already in e->tok_cur / e->tgt_dev (masked).
+static int engine_step_body(Engine* e, float lr_override, ta_step_metrics* m,
+                            std::chrono::steady_clock::time_point t0) {
     const int BT = e->BT;
-    memcpy(e->tok_host, inputs, BT * sizeof(int32_t));
-    memcpy(e->tgt_host, targets, BT * sizeof(int32_t));
-    mask_targets(e->tok_host, e->tgt_host, e->B, e->T);
-    TA_HIP(hipMemcpyAsync(e->tok_dev, e->tok_host, BT * 4, hipMemcpyHostToDevice, e->s));
-    TA_HIP(hipMemcpyAsync(e->tgt_dev, e->tgt_host, BT * 4, hipMemcpyHostToDevice, e->s));
     // zero_grad (adapter_model.cu:222-229)
     TA_HIP(hipMemsetAsync(e->grad, 0, e->nparam * sizeof(float), e->s));
     TA_HIP(hipEventRecord(e->ev[0], e->s));
@@ -413,12 +509,14 @@ static int engine_step(Engine* e, const int32_t* inputs, const int32_t* targets,
                    ? lr_override
                    : cosine_lr(e->ac.lr, e->ac.warmup, e->ac.total_steps, 0.1f, e->step_count);
     int t = (int)e->step_count + 1;
-    CK(ta_adamw_fused(e->master, e->shadow, e->mom, e->vel, e->grad, e->nparam, lr, e->ac.b1,
-                      e->ac.b2, e->ac.eps, e->ac.wd, t, e->ac.grad_clip, e->norm_dev, e->s));
+    TIMED(TA_CAT_TAIL, 0, (double)e->nparam * 34,
+          ta_adamw_fused(e->master, e->shadow, e->mom, e->vel, e->grad, e->nparam, lr, e->ac.b1,
+                         e->ac.b2, e->ac.eps, e->ac.wd, t, e->ac.grad_clip, e->norm_dev, e->s));
     TA_HIP(hipMemcpyAsync(e->norm_host, e->norm_dev, 4, hipMemcpyDeviceToHost, e->s));
     TA_HIP(hipEventRecord(e->ev[3], e->s));
     TA_HIP(hipStreamSynchronize(e->s));
     for (int i = 0; i < 3; i++) TA_HIP(hipEventElapsedTime(&e->phase[i], e->ev[i], e->ev[i + 1]));
+    CK(prof_collect(e));
     // adapt_trainer.cu:237-246: mean over tokens whose loss > 1e-9
     float mean = 0.f;
     int valid = 0;
@@ -441,6 +539,19 @@ static int engine_step(Engine* e, const int32_t* inputs, const int32_t* targets,
             std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     }
     return 0;
+}
+
+static int engine_step(Engine* e, const int32_t* inputs, const int32_t* targets, float lr_override,
+                       ta_step_metrics* m) {
+    auto t0 = std::chrono::steady_clock::now();
+    const int BT = e->BT;
+    memcpy(e->tok_host, inputs, BT * sizeof(int32_t));
+    memcpy(e->tgt_host, targets, BT * sizeof(int32_t));
+    mask_targets(e->tok_host, e->tgt_host, e->B, e->T);
+    TA_HIP(hipMemcpyAsync(e->tok_dev, e->tok_host, BT * 4, hipMemcpyHostToDevice, e->s));
+    TA_HIP(hipMemcpyAsync(e->tgt_dev, e->tgt_host, BT * 4, hipMemcpyHostToDevice, e->s));
+    e->tok_cur = e->tok_dev;
+    return engine_step_body(e, lr_override, m, t0);
 }
 
 static bf16** weight_slot(Engine* e, const std::string& name, int64_t* n, int* layer, int* proj) {
@@ -561,6 +672,7 @@ int ta_engine_destroy(void* ep) {
         if (p) (void)hipHostFree(p);
     for (auto& ev : e->ev)
         if (ev) (void)hipEventDestroy(ev);
+    for (auto& ev : e->pev) (void)hipEventDestroy(ev);
     if (e->own_stream) (void)hipStreamDestroy(e->s);
     delete e;
     return 0;
@@ -653,6 +765,38 @@ int ta_engine_write_adapter(void* ep, int layer, int target, int which, const vo
                (long long)cnt);
     TA_HIP(hipMemcpyAsync(dst, host, cnt * es, hipMemcpyHostToDevice, e->s));
     TA_HIP(hipStreamSynchronize(e->s));
+    return 0;
+}
+
+int ta_engine_step_resident(void* ep, const int32_t* d_inputs, const int32_t* d_targets,
+                            float lr_override, ta_step_metrics* m) {
+    Engine* e = (Engine*)ep;
+    TA_REQUIRE(e && d_inputs && d_targets, "engine_step_resident: null argument");
+    auto t0 = std::chrono::steady_clock::now();
+    CK(mask_targets_dev(d_inputs, d_targets, e->tgt_dev, e->B, e->T, e->s));
+    e->tok_cur = d_inputs;
+    return engine_step_body(e, lr_override, m, t0);
+}
+
+int ta_engine_profile(void* ep, int category) {
+    Engine* e = (Engine*)ep;
+    TA_REQUIRE(e, "engine_profile: null engine");
+    TA_REQUIRE(category >= -1 && category < TA_NCAT, "engine_profile: bad category %d", category);
+    e->prof_cat = category;
+    e->p_ms = e->p_flops = e->p_bytes = 0;
+    e->p_n = 0;
+    return 0;
+}
+
+int ta_engine_profile_read(void* ep, double* ms, int64_t* n, double* flops, double* bytes) {
+    Engine* e = (Engine*)ep;
+    TA_REQUIRE(e, "engine_profile_read: null engine");
+    if (ms) *ms = e->p_ms;
+    if (n) *n = e->p_n;
+    if (flops) *flops = e->p_flops;
+    if (bytes) *bytes = e->p_bytes;
+    e->p_ms = e->p_flops = e->p_bytes = 0;
+    e->p_n = 0;
     return 0;
 }
 

@@ -126,4 +126,32 @@ int add2_bf16(bf16* out, const bf16* a, const bf16* b, int64_t n, hipStream_t s)
     return check_launch("add2");
 }
 
+// Assistant-span masking of src/trainer/adapt_trainer.cu:145-182 on device
+// tokens: one thread per batch row walks its T tokens in order (the state
+// machine is sequential along t); targets outside assistant spans become -1.
+__global__ void k_mask_targets(const int32_t* __restrict__ in, const int32_t* __restrict__ tgt_in,
+                               int32_t* __restrict__ tgt, int B, int T) {
+    int b = blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= B) return;
+    bool in_asst = false;
+    int64_t off = (int64_t)b * T;
+    for (int t = 0; t < T; ++t) {
+        int64_t idx = off + t;
+        int tok = in[idx];
+        if (tok == 151644) in_asst = (t + 1 < T && in[off + t + 1] == 77091);
+        bool mask = !in_asst;
+        if (tok == 151644 || tok == 77091) mask = true;
+        if (tok == 151645) {
+            in_asst = false;
+            mask = false;
+        }
+        tgt[idx] = mask ? -1 : tgt_in[idx];
+    }
+}
+int mask_targets_dev(const int32_t* in, const int32_t* tgt_in, int32_t* tgt, int B, int T,
+                     hipStream_t s) {
+    k_mask_targets<<<(B + 63) / 64, 64, 0, s>>>(in, tgt_in, tgt, B, T);
+    return check_launch("mask_targets");
+}
+
 }  // namespace ta

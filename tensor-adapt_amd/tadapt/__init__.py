@@ -175,6 +175,23 @@ class Engine:
              ctypes.byref(m))
         return {k: getattr(m, k) for k, _ in StepMetrics._fields_}
 
+    def step_resident(self, d_inputs, d_targets, lr_override=0.0):
+        """Step on device-resident int32 token tensors (torch, [B*T] each)."""
+        m = StepMetrics()
+        call("ta_engine_step_resident", self.h, ptr(d_inputs), ptr(d_targets), lr_override,
+             ctypes.byref(m))
+        return {k: getattr(m, k) for k, _ in StepMetrics._fields_}
+
+    def profile(self, category):
+        call("ta_engine_profile", self.h, category)
+
+    def profile_read(self):
+        ms, n = ctypes.c_double(), ctypes.c_int64()
+        fl, by = ctypes.c_double(), ctypes.c_double()
+        call("ta_engine_profile_read", self.h, ctypes.byref(ms), ctypes.byref(n),
+             ctypes.byref(fl), ctypes.byref(by))
+        return {"ms": ms.value, "launches": n.value, "flops": fl.value, "bytes": by.value}
+
     def write_adapter(self, layer, target, which, arr):
         import numpy as np
         t = TARGETS.index(target) if isinstance(target, str) else target
