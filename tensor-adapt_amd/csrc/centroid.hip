@@ -24,8 +24,10 @@ namespace ta {
 
 void* scratch_get(size_t bytes, hipStream_t s, int slot = 0);
 
-constexpr int kTok = 32;  // tokens per block in the accumulate pass
+constexpr int kTok = 64;  // tokens per block in the accumulate pass
 
+// Per-block partial row: part[blk][d] = sum_{t in block} h[t][d] * n_t,
+// part[blk][D] = sum n_t.  Rows move as 16-byte vectors when D % 8 == 0.
 template <bool BF16IN>
 __global__ __launch_bounds__(256) void k_centroid_part(const void* __restrict__ hv,
                                                        const void* __restrict__ gv,
@@ -35,13 +37,20 @@ __global__ __launch_bounds__(256) void k_centroid_part(const void* __restrict__ 
     __shared__ float nrm[kTok];
     int64_t t0 = (int64_t)blockIdx.x * kTok;
     int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const bool v8 = BF16IN && (D & 7) == 0;
     // 1. per-token gradient norms (one wave per token)
     for (int j = wv; j < kTok; j += 4) {
         int64_t t = t0 + j;
         float ss = 0.f;
-        if (t < BT) {
-            if (nv) {
-                ss = 0.f;
+        if (t < BT && !nv) {
+            if (v8) {
+                const bf16x8v* g = (const bf16x8v*)((const bf16*)gv + t * D);
+                for (int c = lane; c < (D >> 3); c += 64) {
+                    float f[8];
+                    unpack8(g[c], f);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) ss += f[e] * f[e];
+                }
             } else if (BF16IN) {
                 const bf16* g = (const bf16*)gv + t * D;
                 for (int d = lane; d < D; d += 64) {
@@ -59,15 +68,31 @@ __global__ __launch_bounds__(256) void k_centroid_part(const void* __restrict__ 
     __syncthreads();
     // 2. weighted column sums over this block's tokens
     float* out = part + (int64_t)blockIdx.x * (D + 1);
-    for (int d = threadIdx.x; d < D; d += 256) {
-        float acc = 0.f;
-        for (int j = 0; j < kTok; j++) {
-            int64_t t = t0 + j;
-            if (t >= BT) break;
-            float h = BF16IN ? bf2f(((const bf16*)hv)[t * D + d]) : ((const float*)hv)[t * D + d];
-            acc += h * nrm[j];
+    if (v8) {
+        for (int c = threadIdx.x; c < (D >> 3); c += 256) {
+            float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            for (int j = 0; j < kTok; j++) {
+                int64_t t = t0 + j;
+                if (t >= BT) break;
+                float f[8];
+                unpack8(((const bf16x8v*)((const bf16*)hv + t * D))[c], f);
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc[e] += f[e] * nrm[j];
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) out[c * 8 + e] = acc[e];
         }
-        out[d] = acc;
+    } else {
+        for (int d = threadIdx.x; d < D; d += 256) {
+            float acc = 0.f;
+            for (int j = 0; j < kTok; j++) {
+                int64_t t = t0 + j;
+                if (t >= BT) break;
+                float h = BF16IN ? bf2f(((const bf16*)hv)[t * D + d]) : ((const float*)hv)[t * D + d];
+                acc += h * nrm[j];
+            }
+            out[d] = acc;
+        }
     }
     if (threadIdx.x == 0) {
         float w = 0.f;
@@ -82,6 +107,7 @@ __global__ void k_centroid_reduce(const float* __restrict__ part, int nblk, int 
     int d = blockIdx.x * blockDim.x + threadIdx.x;
     if (d >= D1) return;
     double s = 0.0;
+#pragma unroll 8
     for (int b = 0; b < nblk; b++) s += (double)part[(int64_t)b * D1 + d];
     acc[d] += s;
 }

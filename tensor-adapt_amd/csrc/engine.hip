@@ -18,6 +18,7 @@
 #include <string.h>
 
 #include <chrono>
+#include <initializer_list>
 #include <map>
 #include <string>
 #include <vector>
@@ -43,6 +44,14 @@ int kaiming_init(float* a32, bf16* a16, int64_t n, int in_dim, hipStream_t s);
 int add2_bf16(bf16* out, const bf16* a, const bf16* b, int64_t n, hipStream_t s);
 int mask_targets_dev(const int32_t* in, const int32_t* tgt_in, int32_t* tgt, int B, int T,
                      hipStream_t s);
+int lora_skinny_nt(const bf16* X, int64_t ldx, int M, int K, int r, const bf16* const* Y,
+                   bf16* const* C, int64_t ldc, int n, hipStream_t s);
+int lora_rank_update(bool delta, bf16* Y, int64_t ldy, int M, int N, int r, float scale,
+                     const bf16* const* U, const int64_t* ldu, const bf16* const* V, int n,
+                     hipStream_t s);
+int lora_wgrad(const bf16* L, int64_t ldl, int NL, const bf16* Sm, int64_t lds, int NS, int T,
+               int r, float scale, bool trans, float* const* G, hipStream_t s);
+int transpose_batch(const bf16* src, bf16* dst, const void* descs, int nd, hipStream_t s);
 
 #define CK(x)                    \
     do {                         \
@@ -88,9 +97,12 @@ struct Engine {
     int64_t nparam = 0;
     float *master = nullptr, *mom = nullptr, *vel = nullptr, *grad = nullptr;
     bf16* shadow = nullptr;
+    bf16* shadowT = nullptr;       // B^T of every B shadow (same offsets), per step
+    void* tdesc = nullptr;         // device descriptors of those transposes
+    int ntdesc = 0;
 
     bf16 *x_final, *xfn, *logits, *g_res, *dres, *tmpH, *dact, *dgate, *dup, *dxn2, *dao, *dQ, *dK,
-        *dV, *dxn, *delta, *dh;
+        *dV, *dxn, *delta, *dh, *dh_cat;
     float *final_rms, *loss_tok, *norm_dev, *Dbuf;
     double* cacc;
     int32_t *tok_dev, *tgt_dev;
@@ -202,6 +214,21 @@ static int engine_alloc(Engine* e) {
     CK(alloc(e, &e->vel, off, "adapter.v", 1));
     CK(alloc(e, &e->grad, off, "adapter.grad", 1));
     CK(alloc(e, &e->shadow, off, "adapter.shadow", 0));
+    CK(alloc(e, &e->shadowT, off, "adapter.shadowT", 0));
+    {
+        struct TD {
+            int64_t src, dst;
+            int rows, cols;
+        };
+        std::vector<TD> td;
+        for (auto& ly : e->L)
+            for (auto& pr : ly.pr)
+                if (pr.on) td.push_back({pr.offB, pr.offB, pr.out, e->r});
+        e->ntdesc = (int)td.size();
+        CK(dmalloc(e, &e->tdesc, td.size() * sizeof(TD) + 16, "tdesc"));
+        if (!td.empty())
+            TA_HIP(hipMemcpy(e->tdesc, td.data(), td.size() * sizeof(TD), hipMemcpyHostToDevice));
+    }
     for (int l = 0; l < c.layers; l++) {
         Layer& ly = e->L[l];
         std::string p = "l" + std::to_string(l) + ".";
@@ -250,6 +277,7 @@ static int engine_alloc(Engine* e) {
     CK(alloc(e, &e->dxn, (int64_t)BT * H, "dx_normed", 0));
     CK(alloc(e, &e->delta, (int64_t)BT * maxout, "delta", 0));
     CK(alloc(e, &e->dh, (int64_t)BT * r, "dh", 0));
+    CK(alloc(e, &e->dh_cat, (int64_t)BT * r * 3, "dh_cat", 0));
     CK(alloc(e, &e->Dbuf, (int64_t)e->B * c.n_q * e->T, "Dbuf", 1));
     CK(alloc(e, &e->norm_dev, 64, "norm", 1));
     CK(alloc(e, &e->cacc, H + 1, "centroid"));
@@ -288,45 +316,83 @@ static inline double gbytes(double M, double N, double K, double in_b, double ou
     return (M * K + K * N) * in_b + M * N * out_b * (acc ? 2.0 : 1.0);
 }
 
-static int lora_fwd(Engine* e, Pair& p, const bf16* x, bf16* y) {
-    const bf16* A = e->shadow + p.offA;
-    const bf16* Bm = e->shadow + p.offB;
+// LoRA forward for the on-pairs of one input-sharing group (q,k,v on
+// x_normed; gate,up on x_normed2; o; down), adapter_model.cu:96-129:
+//   h_p = bf16(x A_p^T)                (one pass over x for the group)
+//   y_p = bf16(y_p + s * bf16(h_p B_p^T))
+static int lora_group_fwd(Engine* e, Layer& ly, std::initializer_list<int> group, const bf16* x,
+                          int in, bf16* const* ys) {
+    const bf16* Ay[3];
+    bf16* hs[3];
+    int n = 0;
+    for (int p : group)
+        if (ly.pr[p].on) {
+            Ay[n] = e->shadow + ly.pr[p].offA;
+            hs[n++] = ly.pr[p].h;
+        }
+    if (!n) return 0;
     const double BT = e->BT, r = e->r;
-    // h = bf16(x A^T) [BT, r]; delta = bf16(h B^T) [BT, out]; y = bf16(y + s*delta)
-    TIMED(TA_CAT_LORA, gflops(BT, r, p.in), gbytes(BT, r, p.in, 2, 2, false),
-          gemm_dispatch(true, true, e->BT, e->r, p.in, 1.f, x, p.in, A, p.in, 0.f, p.h, e->r,
-                        nullptr, false, e->s, 0));
-    TIMED(TA_CAT_LORA, gflops(BT, p.out, r), gbytes(BT, p.out, r, 2, 2, false),
-          gemm_dispatch(true, true, e->BT, p.out, e->r, 1.f, p.h, e->r, Bm, e->r, 0.f, e->delta,
-                        p.out, nullptr, false, e->s, 0));
-    TIMED(TA_CAT_ELEMWISE, 0, BT * p.out * 6,
-          ta_lora_add(y, e->delta, e->scale, (int64_t)e->BT * p.out, e->s));
+    TIMED(TA_CAT_LORA, gflops(BT, n * r, in), BT * in * 2 + BT * n * r * 2,
+          lora_skinny_nt(x, in, e->BT, in, e->r, Ay, hs, e->r, n, e->s));
+    int i = 0;
+    for (int p : group) {
+        Pair& pr = ly.pr[p];
+        bf16* y = ys[i++];
+        if (!pr.on) continue;
+        const bf16* U[1] = {pr.h};
+        const int64_t ldu[1] = {e->r};
+        const bf16* V[1] = {e->shadow + pr.offB};
+        TIMED(TA_CAT_LORA, gflops(BT, pr.out, r), BT * pr.out * 4 + BT * r * 2,
+              lora_rank_update(true, y, pr.out, e->BT, pr.out, e->r, e->scale, U, ldu, V, 1, e->s));
+    }
     return 0;
 }
 
-static int lora_bwd(Engine* e, Pair& p, const bf16* x, const bf16* go, bf16* gx) {
-    const bf16* A = e->shadow + p.offA;
-    const bf16* Bm = e->shadow + p.offB;
-    float* gA = e->grad + p.offA;
-    float* gB = e->grad + p.offB;
+// LoRA backward for one group, adapter_model.cu:131-220, pairs in order:
+//   dh_p = bf16(go_p B_p)            (B^T shadow, one pass over go_p)
+//   gB_p += s * go_p^T h_p           (h_p cached by the forward)
+//   gA_p += s * dh_p^T x             (all pairs of the group in one pass over x)
+//   gx = bf16(s * dh_p A_p + gx)     (pairs applied in order, gx read once)
+static int lora_group_bwd(Engine* e, Layer& ly, std::initializer_list<int> group, const bf16* x,
+                          int in, const bf16* const* gos, bf16* gx) {
+    int on[3], n = 0, i = 0;
+    const bf16* go_on[3];
+    for (int p : group) {
+        if (ly.pr[p].on) {
+            on[n] = p;
+            go_on[n++] = gos[i];
+        }
+        i++;
+    }
+    if (!n) return 0;
     const int BT = e->BT, r = e->r;
-    // h is the forward's x*A^T (the reference recomputes the same product)
-    // gB += s * go^T h       [out, r]
-    TIMED(TA_CAT_LORA, gflops(p.out, r, BT), gbytes(p.out, r, BT, 2, 4, true),
-          gemm_dispatch(false, false, p.out, r, BT, e->scale, go, p.out, p.h, r, 1.f, gB, r,
-                        nullptr, true, e->s, 0));
-    // dh = bf16(go B)        [BT, r]
-    TIMED(TA_CAT_LORA, gflops(BT, r, p.out), gbytes(BT, r, p.out, 2, 2, false),
-          gemm_dispatch(true, false, BT, r, p.out, 1.f, go, p.out, Bm, r, 0.f, e->dh, r, nullptr,
-                        false, e->s, 0));
-    // gA += s * dh^T x       [r, in]
-    TIMED(TA_CAT_LORA, gflops(r, p.in, BT), gbytes(r, p.in, BT, 2, 4, true),
-          gemm_dispatch(false, false, r, p.in, BT, e->scale, e->dh, r, x, p.in, 1.f, gA, p.in,
-                        nullptr, true, e->s, 0));
-    // gx = bf16(gx + s * dh A)
-    TIMED(TA_CAT_LORA, gflops(BT, p.in, r), gbytes(BT, p.in, r, 2, 2, true),
-          gemm_dispatch(true, false, BT, p.in, r, e->scale, e->dh, r, A, p.in, 1.f, gx, p.in,
-                        nullptr, false, e->s, 0));
+    const double dBT = BT;
+    const int64_t ldh = (int64_t)n * r;
+    for (int q = 0; q < n; q++) {
+        Pair& pr = ly.pr[on[q]];
+        const bf16* Yt[1] = {e->shadowT + pr.offB};
+        bf16* C[1] = {e->dh_cat + q * r};
+        TIMED(TA_CAT_LORA, gflops(dBT, r, pr.out), dBT * pr.out * 2 + dBT * r * 2,
+              lora_skinny_nt(go_on[q], pr.out, BT, pr.out, r, Yt, C, ldh, 1, e->s));
+        float* G[3] = {e->grad + pr.offB, nullptr, nullptr};
+        TIMED(TA_CAT_LORA, gflops(pr.out, r, dBT), dBT * (pr.out + r) * 2 + pr.out * r * 8.0,
+              lora_wgrad(go_on[q], pr.out, pr.out, pr.h, r, r, BT, r, e->scale, false, G, e->s));
+    }
+    float* GA[3] = {nullptr, nullptr, nullptr};
+    const bf16* U[3];
+    int64_t ldu[3];
+    const bf16* V[3];
+    for (int q = 0; q < n; q++) {
+        Pair& pr = ly.pr[on[q]];
+        GA[q] = e->grad + pr.offA;
+        U[q] = e->dh_cat + q * r;
+        ldu[q] = ldh;
+        V[q] = e->shadow + pr.offA;
+    }
+    TIMED(TA_CAT_LORA, gflops(ldh, in, dBT), dBT * (in + ldh) * 2 + ldh * in * 8.0,
+          lora_wgrad(x, in, in, e->dh_cat, ldh, (int)ldh, BT, r, e->scale, true, GA, e->s));
+    TIMED(TA_CAT_LORA, gflops(dBT, in, ldh), dBT * in * 4 + dBT * ldh * 2,
+          lora_rank_update(false, gx, in, BT, in, r, e->scale, U, ldu, V, n, e->s));
     return 0;
 }
 
@@ -391,9 +457,10 @@ static int forward(Engine* e) {
         CK(proj_fwd(e, ly.W[PQ], ly.xn, ly.Q, H, qd, ly.bias[0]));
         CK(proj_fwd(e, ly.W[PK], ly.xn, ly.K, H, kvd, ly.bias[1]));
         CK(proj_fwd(e, ly.W[PV], ly.xn, ly.V, H, kvd, ly.bias[2]));
-        if (ly.pr[PQ].on) CK(lora_fwd(e, ly.pr[PQ], ly.xn, ly.Q));
-        if (ly.pr[PK].on) CK(lora_fwd(e, ly.pr[PK], ly.xn, ly.K));
-        if (ly.pr[PV].on) CK(lora_fwd(e, ly.pr[PV], ly.xn, ly.V));
+        {
+            bf16* ys[3] = {ly.Q, ly.K, ly.V};
+            CK(lora_group_fwd(e, ly, {PQ, PK, PV}, ly.xn, H, ys));
+        }
         TIMED(TA_CAT_ELEMWISE, 0, dBT * qd * 4,
               ta_rope_fwd(ly.Q, e->B, e->T, c.n_q, c.head_dim, c.rope_theta, s));
         TIMED(TA_CAT_ELEMWISE, 0, dBT * kvd * 4,
@@ -404,7 +471,10 @@ static int forward(Engine* e) {
               attn_fwd(ly.Q, ly.K, ly.V, ly.ao, ly.attn_w, e->B, e->T, c.n_q, c.n_kv, c.head_dim,
                        false, s));
         CK(proj_fwd(e, ly.W[PO], ly.ao, e->tmpH, qd, H, nullptr));
-        if (ly.pr[PO].on) CK(lora_fwd(e, ly.pr[PO], ly.ao, e->tmpH));
+        {
+            bf16* ys[1] = {e->tmpH};
+            CK(lora_group_fwd(e, ly, {PO}, ly.ao, qd, ys));
+        }
         TIMED(TA_CAT_ELEMWISE, 0, dBT * H * 6,
               add2_bf16(ly.res_mid, ly.res_in, e->tmpH, (int64_t)BT * H, s));
         TIMED(TA_CAT_NORM, 0, nrm_b,
@@ -412,12 +482,17 @@ static int forward(Engine* e) {
                               s));
         CK(proj_fwd(e, ly.W[PG], ly.xn2, ly.gate, H, I, nullptr));
         CK(proj_fwd(e, ly.W[PU], ly.xn2, ly.up, H, I, nullptr));
-        if (ly.pr[PG].on) CK(lora_fwd(e, ly.pr[PG], ly.xn2, ly.gate));
-        if (ly.pr[PU].on) CK(lora_fwd(e, ly.pr[PU], ly.xn2, ly.up));
+        {
+            bf16* ys[2] = {ly.gate, ly.up};
+            CK(lora_group_fwd(e, ly, {PG, PU}, ly.xn2, H, ys));
+        }
         TIMED(TA_CAT_ELEMWISE, 0, dBT * I * 6,
               ta_silu_mul_fwd(ly.gate, ly.up, ly.act, (int64_t)BT * I, s));
         CK(proj_fwd(e, ly.W[PD], ly.act, e->tmpH, I, H, nullptr));
-        if (ly.pr[PD].on) CK(lora_fwd(e, ly.pr[PD], ly.act, e->tmpH));
+        {
+            bf16* ys[1] = {e->tmpH};
+            CK(lora_group_fwd(e, ly, {PD}, ly.act, I, ys));
+        }
         TIMED(TA_CAT_ELEMWISE, 0, dBT * H * 6,
               add2_bf16(res_out, ly.res_mid, e->tmpH, (int64_t)BT * H, s));
     }
@@ -450,13 +525,18 @@ static int backward(Engine* e) {
         Layer& ly = e->L[l];
         // FFN (qwen2.cu:222-246)
         CK(proj_bwd_x(e, ly.Wt[PD], e->g_res, e->dact, H, I, 0.f));
-        if (ly.pr[PD].on) CK(lora_bwd(e, ly.pr[PD], ly.act, e->g_res, e->dact));
+        {
+            const bf16* gos[1] = {e->g_res};
+            CK(lora_group_bwd(e, ly, {PD}, ly.act, I, gos, e->dact));
+        }
         TIMED(TA_CAT_ELEMWISE, 0, dBT * I * 10,
               ta_silu_mul_bwd(e->dact, ly.gate, ly.up, e->dgate, e->dup, (int64_t)BT * I, s));
         CK(proj_bwd_x(e, ly.Wt[PG], e->dgate, e->dxn2, I, H, 0.f));
         CK(proj_bwd_x(e, ly.Wt[PU], e->dup, e->dxn2, I, H, 1.f));
-        if (ly.pr[PG].on) CK(lora_bwd(e, ly.pr[PG], ly.xn2, e->dgate, e->dxn2));
-        if (ly.pr[PU].on) CK(lora_bwd(e, ly.pr[PU], ly.xn2, e->dup, e->dxn2));
+        {
+            const bf16* gos[2] = {e->dgate, e->dup};
+            CK(lora_group_bwd(e, ly, {PG, PU}, ly.xn2, H, gos, e->dxn2));
+        }
         TIMED(TA_CAT_NORM, 0, nrm_b,
               ta_rms_norm_bwd(e->dxn2, ly.res_mid, ly.post_norm, ly.post_rms, e->tmpH, nullptr, 1,
                               BT, H, c.rms_eps, s));
@@ -464,7 +544,10 @@ static int backward(Engine* e) {
               ta_add_inplace(e->g_res, e->tmpH, (int64_t)BT * H, s));
         // attention (qwen2.cu:250-304)
         CK(proj_bwd_x(e, ly.Wt[PO], e->g_res, e->dao, H, qd, 0.f));
-        if (ly.pr[PO].on) CK(lora_bwd(e, ly.pr[PO], ly.ao, e->g_res, e->dao));
+        {
+            const bf16* gos[1] = {e->g_res};
+            CK(lora_group_bwd(e, ly, {PO}, ly.ao, qd, gos, e->dao));
+        }
         TIMED(TA_CAT_ATTN_BWD, 8.0 * tri * c.head_dim,
               tri * 4 + dBT * (2.0 * qd + 2.0 * kvd) * 2 + dBT * (qd + 2.0 * kvd) * 2,
               attn_bwd(e->dao, ly.Q, ly.K, ly.V, ly.attn_w, e->dQ, e->dK, e->dV, e->B, e->T, c.n_q,
@@ -476,9 +559,10 @@ static int backward(Engine* e) {
         CK(proj_bwd_x(e, ly.Wt[PQ], e->dQ, e->dxn, qd, H, 0.f));
         CK(proj_bwd_x(e, ly.Wt[PK], e->dK, e->dxn, kvd, H, 1.f));
         CK(proj_bwd_x(e, ly.Wt[PV], e->dV, e->dxn, kvd, H, 1.f));
-        if (ly.pr[PQ].on) CK(lora_bwd(e, ly.pr[PQ], ly.xn, e->dQ, e->dxn));
-        if (ly.pr[PK].on) CK(lora_bwd(e, ly.pr[PK], ly.xn, e->dK, e->dxn));
-        if (ly.pr[PV].on) CK(lora_bwd(e, ly.pr[PV], ly.xn, e->dV, e->dxn));
+        {
+            const bf16* gos[3] = {e->dQ, e->dK, e->dV};
+            CK(lora_group_bwd(e, ly, {PQ, PK, PV}, ly.xn, H, gos, e->dxn));
+        }
         // centroid side channel (adapt_trainer.cu:210-232): h = x_normed,
         // g = dx_attn_in of this layer
         TIMED(TA_CAT_CENTROID, 0, dBT * H * 4,
@@ -498,6 +582,8 @@ static int engine_step_body(Engine* e, float lr_override, ta_step_metrics* m,
     const int BT = e->BT;
     // zero_grad (adapter_model.cu:222-229)
     TA_HIP(hipMemsetAsync(e->grad, 0, e->nparam * sizeof(float), e->s));
+    // B^T shadows for dh = go B (the shadows changed in the last AdamW)
+    CK(transpose_batch(e->shadow, e->shadowT, e->tdesc, e->ntdesc, e->s));
     TA_HIP(hipEventRecord(e->ev[0], e->s));
     CK(forward(e));
     TA_HIP(hipEventRecord(e->ev[1], e->s));

@@ -1,0 +1,406 @@
+// lora.hip — the LoRA products of apply_lora_fwd / apply_lora_bwd
+// (src/adapter/adapter_model.cu:96-220) as purpose-built gfx950 kernels.
+//
+// At rank r = 8..64 every LoRA product is skinny: one side is r wide, the
+// other is tokens (B*T) or a hidden/intermediate width.  They are HBM-bound
+// (about r flops per byte), so the design goal is one pass over each large
+// operand, not MFMA tile efficiency:
+//
+//   k_skinny_nt   C_p = bf16(X Y_p^T) for up to 3 pairs sharing X -
+//                 h = x A^T for q,k,v (or gate,up) in ONE pass over x, and
+//                 dh = go B (with the B^T shadow) — 16 tokens per block, the
+//                 4 waves split K and reduce through LDS in a fixed order.
+//   k_rank_update Y = Y (+) s * U_p V_p for up to 3 pairs applied in order
+//                 on one [64 x 64] tile held in LDS:  the forward delta add
+//                 y = bf16(y + s*bf16(h B^T)) (adapter_model.cu:108-127) and
+//                 the input-gradient update gx = bf16(s*dh A + gx)
+//                 (adapter_model.cu:210-219), so y / gx are read and written
+//                 once per group instead of once per pair and GEMM.
+//   k_wgrad       partial G = sum over a token range of P^T Q (gB = go^T h,
+//                 gA = dh^T x), split over token ranges for parallelism;
+//                 k_wgrad_reduce adds s * (sum of partials, fixed order) into
+//                 the F32 gradients (the reference's gemm_f32 with beta = 1).
+//
+// All MFMAs are v_mfma_f32_16x16x32_bf16; rank dimensions are zero-padded to
+// multiples of 32 (r = 8, 16) or looped (r = 64).
+#include "ta_common.hpp"
+
+namespace ta {
+
+void* scratch_get(size_t bytes, hipStream_t s, int slot = 0);
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ floatx4 mf16(bf16x8_t a, bf16x8_t b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ bf16x8_t zfrag() {
+    bf16x8_t z;
+#pragma unroll
+    for (int e = 0; e < 8; e++) z[e] = (__bf16)0.f;
+    return z;
+}
+// 8 consecutive k of a K-contiguous row, zero beyond kend
+__device__ __forceinline__ bf16x8_t ld8(const bf16* __restrict__ row, int k, int kend) {
+    if (k + 8 <= kend) return *(const bf16x8_t*)(row + k);
+    bf16x8_t v = zfrag();
+    for (int e = 0; e < 8; e++)
+        if (k + e < kend) v[e] = __builtin_bit_cast(__bf16, row[k + e]);
+    return v;
+}
+
+struct Pairs3 {
+    const bf16* y[3];  // k_skinny_nt: Y_p [r x K]; k_rank_update: V_p
+    bf16* c[3];        // k_skinny_nt outputs C_p [M x r] (ldc = r)
+    const bf16* u[3];  // k_rank_update: U_p [M x r]
+    int64_t ldu[3];
+    int n;             // pairs
+    int64_t ldc;       // k_skinny_nt: row stride of every C_p
+};
+
+// ── C_p = bf16(X Y_p^T) ───────────────────────────────────────────────────
+// grid: ceil(M/16) blocks x 256 threads.  Column c of the concatenated
+// output belongs to pair c / r, rank index c % r.
+template <int NT>  // 16-column tiles covering n*r columns
+__global__ __launch_bounds__(256) void k_skinny_nt(const bf16* __restrict__ X, int64_t ldx, int M,
+                                                   int K, int r, Pairs3 p) {
+    __shared__ floatx4 red[3][NT][64];
+    int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int m0 = blockIdx.x * 16;
+    int row = m0 + (lane & 15);
+    int ncat = p.n * r;
+    floatx4 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const bf16* xr = X + (int64_t)(row < M ? row : 0) * ldx;
+    const bf16* yr[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+        int c = 16 * t + (lane & 15);
+        yr[t] = (c < ncat) ? p.y[c / r] + (int64_t)(c % r) * K : nullptr;
+    }
+    int nks = (K + 31) / 32;
+    for (int ks = w; ks < nks; ks += 4) {
+        int k = 32 * ks + 8 * (lane >> 4);
+        bf16x8_t a = (row < M) ? ld8(xr, k, K) : zfrag();
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            bf16x8_t b = yr[t] ? ld8(yr[t], k, K) : zfrag();
+            acc[t] = mf16(a, b, acc[t]);
+        }
+    }
+    if (w > 0)
+#pragma unroll
+        for (int t = 0; t < NT; t++) red[w - 1][t][lane] = acc[t];
+    __syncthreads();
+    if (w == 0) {
+#pragma unroll
+        for (int t = 0; t < NT; t++) {
+            floatx4 v = acc[t];
+            for (int q = 0; q < 3; q++) {
+                floatx4 o = red[q][t][lane];
+                v[0] += o[0];
+                v[1] += o[1];
+                v[2] += o[2];
+                v[3] += o[3];
+            }
+            int c = 16 * t + (lane & 15);
+            if (c >= ncat) continue;
+            bf16* out = p.c[c / r] + (c % r);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                int m = m0 + 4 * (lane >> 4) + i;
+                if (m < M) out[(int64_t)m * p.ldc] = f2bf(v[i]);
+            }
+        }
+    }
+}
+
+// ── Y (+)= s * U_p V_p, pairs applied in order, one 64 x 64 tile of Y ─────
+// DELTA: V_p is [N x r] (B of the pair): Y = bf16(Y + s * bf16(U V^T)).
+// GEMM : V_p is [r x N] (A of the pair): Y = bf16(s * (U V) + Y).
+constexpr int RU_LD = 64 + 8;
+template <bool DELTA, int RK>  // RK: rank rounded up to a multiple of 32
+__global__ __launch_bounds__(256) void k_rank_update(bf16* __restrict__ Y, int64_t ldy, int M, int N,
+                                                     int r, float s, Pairs3 p) {
+    __shared__ __attribute__((aligned(16))) bf16 sY[64 * RU_LD];
+    __shared__ __attribute__((aligned(16))) bf16 sV[64 * (RK + 8)];  // [n][k]
+    int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    bool vec = ((ldy & 7) == 0) && (((uintptr_t)Y & 15) == 0);
+    // stage the Y tile (coalesced 16-byte rows)
+    for (int q = threadIdx.x; q < 64 * 8; q += 256) {
+        int rr = q >> 3, cc = (q & 7) * 8;
+        int m = m0 + rr, n = n0 + cc;
+        bf16x8v v;
+        if (m < M && vec && n + 8 <= N) {
+            v = *(const bf16x8v*)(Y + (int64_t)m * ldy + n);
+        } else {
+            uint16_t tt[8];
+            for (int e = 0; e < 8; e++)
+                tt[e] = (m < M && n + e < N) ? Y[(int64_t)m * ldy + n + e] : (uint16_t)0;
+            for (int e = 0; e < 4; e++) v.w[e] = tt[2 * e] | ((uint32_t)tt[2 * e + 1] << 16);
+        }
+        *(bf16x8v*)(sY + rr * RU_LD + cc) = v;
+    }
+    for (int pi = 0; pi < p.n; pi++) {
+        // stage V_p as [n][k] (k = rank index), zero-padded to RK
+        __syncthreads();
+        for (int q = threadIdx.x; q < 64 * RK; q += 256) {
+            // DELTA reads B[n][k] (k contiguous), GEMM reads A[k][n] (n contiguous)
+            int nn = DELTA ? q / RK : q % 64, kk = DELTA ? q % RK : q / 64;
+            int n = n0 + nn;
+            uint16_t v = 0;
+            if (n < N && kk < r) v = DELTA ? p.y[pi][(int64_t)n * r + kk] : p.y[pi][(int64_t)kk * N + n];
+            sV[nn * (RK + 8) + kk] = v;
+        }
+        __syncthreads();
+        floatx4 acc[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+        int row = m0 + 16 * w + (lane & 15);
+        const bf16* ur = p.u[pi] + (int64_t)(row < M ? row : 0) * p.ldu[pi];
+#pragma unroll
+        for (int kc = 0; kc < RK / 32; kc++) {
+            int k = 32 * kc + 8 * (lane >> 4);
+            bf16x8_t a = (row < M) ? ld8(ur, k, r) : zfrag();
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                bf16x8_t b = *(const bf16x8_t*)(sV + (16 * t + (lane & 15)) * (RK + 8) + k);
+                acc[t] = mf16(a, b, acc[t]);
+            }
+        }
+        // each lane owns column 16t + l%16, rows 4(l/16)+i of this wave's strip
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                int idx = (16 * w + 4 * (lane >> 4) + i) * RU_LD + 16 * t + (lane & 15);
+                float y = bf2f(sY[idx]);
+                float o = DELTA ? y + s * bf2f(f2bf(acc[t][i])) : s * acc[t][i] + y;
+                sY[idx] = f2bf(o);
+            }
+    }
+    __syncthreads();
+    for (int q = threadIdx.x; q < 64 * 8; q += 256) {
+        int rr = q >> 3, cc = (q & 7) * 8;
+        int m = m0 + rr, n = n0 + cc;
+        if (m >= M) continue;
+        bf16x8v v = *(const bf16x8v*)(sY + rr * RU_LD + cc);
+        if (vec && n + 8 <= N) {
+            *(bf16x8v*)(Y + (int64_t)m * ldy + n) = v;
+        } else {
+            for (int e = 0; e < 8; e++)
+                if (n + e < N) Y[(int64_t)m * ldy + n + e] = (uint16_t)(v.w[e >> 1] >> ((e & 1) * 16));
+        }
+    }
+}
+
+// ── weight gradients: partial[z][l][s] = sum_{t in range z} L[t][l] * Sm[t][s]
+// L: [T x NL] (ldl), Sm: [T x NS] (lds), NS <= 192.  Block: 64 columns of L
+// (4 waves x 16), one token range; token tiles of 64 staged transposed.
+constexpr int WG_TK = 64;
+template <int NST>  // 16-column tiles of the small side
+__global__ __launch_bounds__(256) void k_wgrad(const bf16* __restrict__ L, int64_t ldl, int NL,
+                                               const bf16* __restrict__ Sm, int64_t lds, int NS,
+                                               int T, int tokens_per_split,
+                                               float* __restrict__ part) {
+    __shared__ __attribute__((aligned(16))) bf16 sL[64 * (WG_TK + 8)];         // [l][t]
+    __shared__ __attribute__((aligned(16))) bf16 sS[NST * 16 * (WG_TK + 8)];   // [s][t]
+    int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int l0 = blockIdx.x * 64;
+    int t_beg = blockIdx.y * tokens_per_split;
+    int t_end = min(T, t_beg + tokens_per_split);
+    floatx4 acc[NST];
+#pragma unroll
+    for (int t = 0; t < NST; t++) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    bool vecl = ((ldl & 7) == 0) && (((uintptr_t)L & 15) == 0);
+    for (int tb = t_beg; tb < t_end; tb += WG_TK) {
+        __syncthreads();
+        // L tile [TK tokens x 64 cols] -> sL[col][token]
+        for (int q = threadIdx.x; q < WG_TK * 8; q += 256) {
+            int tt = q >> 3, cc = (q & 7) * 8;
+            int tok = tb + tt, l = l0 + cc;
+            bf16x8v v;
+            if (tok < t_end && vecl && l + 8 <= NL) {
+                v = *(const bf16x8v*)(L + (int64_t)tok * ldl + l);
+            } else {
+                uint16_t x[8];
+                for (int e = 0; e < 8; e++)
+                    x[e] = (tok < t_end && l + e < NL) ? L[(int64_t)tok * ldl + l + e] : (uint16_t)0;
+                for (int e = 0; e < 4; e++) v.w[e] = x[2 * e] | ((uint32_t)x[2 * e + 1] << 16);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                sL[(cc + e) * (WG_TK + 8) + tt] = (uint16_t)(v.w[e >> 1] >> ((e & 1) * 16));
+        }
+        // small tile [TK tokens x NST*16] -> sS[s][token]
+        for (int q = threadIdx.x; q < WG_TK * NST * 16; q += 256) {
+            int tt = q / (NST * 16), ss = q % (NST * 16);
+            int tok = tb + tt;
+            sS[ss * (WG_TK + 8) + tt] =
+                (tok < t_end && ss < NS) ? Sm[(int64_t)tok * lds + ss] : (uint16_t)0;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kc = 0; kc < WG_TK / 32; kc++) {
+            bf16x8_t a =
+                *(const bf16x8_t*)(sL + (16 * w + (lane & 15)) * (WG_TK + 8) + 32 * kc + 8 * (lane >> 4));
+#pragma unroll
+            for (int t = 0; t < NST; t++) {
+                bf16x8_t b = *(const bf16x8_t*)(sS + (16 * t + (lane & 15)) * (WG_TK + 8) + 32 * kc +
+                                                8 * (lane >> 4));
+                acc[t] = mf16(a, b, acc[t]);
+            }
+        }
+    }
+    // C layout: column s = 16t + l%16, rows l = 16w + 4(l/16) + i
+    float* out = part + (int64_t)blockIdx.y * NL * NS;
+#pragma unroll
+    for (int t = 0; t < NST; t++) {
+        int sidx = 16 * t + (lane & 15);
+        if (sidx >= NS) continue;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            int l = l0 + 16 * w + 4 * (lane >> 4) + i;
+            if (l < NL) out[(int64_t)l * NS + sidx] = acc[t][i];
+        }
+    }
+}
+
+// G += scale * sum_z partial[z] (z in order).  TRANS=false: G_p[l][s] for
+// one pair (gB: [out x r], NS = r).  TRANS=true: column s belongs to pair
+// s / r, G_p[s % r][l] (gA: [r x in]).
+template <bool TRANS>
+__global__ void k_wgrad_reduce(const float* __restrict__ part, int splits, int NL, int NS, int r,
+                               float scale, float* g0, float* g1, float* g2) {
+    int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    int64_t n = (int64_t)NL * NS;
+    if (idx >= n) return;
+    float v = 0.f;
+    for (int z = 0; z < splits; z++) v += part[(int64_t)z * n + idx];
+    int l = (int)(idx / NS), s = (int)(idx % NS);
+    if (!TRANS) {
+        g0[(int64_t)l * NS + s] += scale * v;
+    } else {
+        int pp = s / r, j = s % r;
+        float* g = pp == 0 ? g0 : (pp == 1 ? g1 : g2);
+        g[(int64_t)j * NL + l] += scale * v;
+    }
+}
+
+// Batched transpose of the BF16 B shadows into B^T (one launch per step).
+struct TDesc {
+    int64_t src, dst;
+    int rows, cols;
+};
+__global__ void k_transpose_batch(const bf16* __restrict__ src, bf16* __restrict__ dst,
+                                  const TDesc* __restrict__ d, int nd) {
+    const TDesc t = d[blockIdx.y];
+    int64_t n = (int64_t)t.rows * t.cols;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        int rr = (int)(i / t.cols), cc = (int)(i % t.cols);
+        dst[t.dst + (int64_t)cc * t.rows + rr] = src[t.src + i];
+    }
+}
+
+// ── host launchers ────────────────────────────────────────────────────────
+int lora_skinny_nt(const bf16* X, int64_t ldx, int M, int K, int r, const bf16* const* Y,
+                   bf16* const* C, int64_t ldc, int n, hipStream_t s) {
+    TA_REQUIRE(n >= 1 && n <= 3 && r >= 1 && M > 0 && K > 0, "lora_skinny_nt: bad arguments");
+    TA_REQUIRE(((uintptr_t)X & 15) == 0 && (ldx & 7) == 0 && (K & 7) == 0,
+               "lora_skinny_nt: X rows must be 16-byte aligned and K a multiple of 8");
+    Pairs3 p{};
+    p.n = n;
+    p.ldc = ldc;
+    for (int i = 0; i < n; i++) {
+        p.y[i] = Y[i];
+        p.c[i] = C[i];
+        TA_REQUIRE(((uintptr_t)Y[i] & 15) == 0, "lora_skinny_nt: Y must be 16-byte aligned");
+    }
+    int nt = (n * r + 15) / 16;
+    dim3 grid((M + 15) / 16);
+    switch (nt) {
+        case 1: k_skinny_nt<1><<<grid, 256, 0, s>>>(X, ldx, M, K, r, p); break;
+        case 2: k_skinny_nt<2><<<grid, 256, 0, s>>>(X, ldx, M, K, r, p); break;
+        case 3: k_skinny_nt<3><<<grid, 256, 0, s>>>(X, ldx, M, K, r, p); break;
+        case 4: k_skinny_nt<4><<<grid, 256, 0, s>>>(X, ldx, M, K, r, p); break;
+        case 6: k_skinny_nt<6><<<grid, 256, 0, s>>>(X, ldx, M, K, r, p); break;
+        case 8: k_skinny_nt<8><<<grid, 256, 0, s>>>(X, ldx, M, K, r, p); break;
+        case 12: k_skinny_nt<12><<<grid, 256, 0, s>>>(X, ldx, M, K, r, p); break;
+        default: return set_error(-1, "lora_skinny_nt: %d pairs x rank %d unsupported", n, r);
+    }
+    return check_launch("lora_skinny_nt");
+}
+
+int lora_rank_update(bool delta, bf16* Y, int64_t ldy, int M, int N, int r, float scale,
+                     const bf16* const* U, const int64_t* ldu, const bf16* const* V, int n,
+                     hipStream_t s) {
+    TA_REQUIRE(n >= 1 && n <= 3 && r >= 1 && r <= 64, "lora_rank_update: bad arguments");
+    Pairs3 p{};
+    p.n = n;
+    for (int i = 0; i < n; i++) {
+        p.u[i] = U[i];
+        p.ldu[i] = ldu[i];
+        p.y[i] = V[i];
+        TA_REQUIRE(((uintptr_t)U[i] & 15) == 0 && (ldu[i] & 7) == 0,
+                   "lora_rank_update: U rows must be 16-byte aligned");
+    }
+    dim3 grid((N + 63) / 64, (M + 63) / 64);
+    int rk = (r + 31) / 32 * 32;
+#define RU(D, R) k_rank_update<D, R><<<grid, 256, 0, s>>>(Y, ldy, M, N, r, scale, p)
+    if (delta) {
+        if (rk == 32) RU(true, 32); else RU(true, 64);
+    } else {
+        if (rk == 32) RU(false, 32); else RU(false, 64);
+    }
+#undef RU
+    return check_launch("lora_rank_update");
+}
+
+// G (F32) += scale * L^T Sm over T tokens.  trans=false: one pair, G [NL x NS];
+// trans=true: NS = n*r columns, pair p's G_p is [r x NL].
+int lora_wgrad(const bf16* L, int64_t ldl, int NL, const bf16* Sm, int64_t lds, int NS, int T,
+               int r, float scale, bool trans, float* const* G, hipStream_t s) {
+    TA_REQUIRE(NL > 0 && NS > 0 && NS <= 192 && T > 0, "lora_wgrad: bad arguments");
+    int ltiles = (NL + 63) / 64;
+    int tiles_t = (T + WG_TK - 1) / WG_TK;
+    int splits = (768 + ltiles - 1) / ltiles;
+    if (splits > tiles_t) splits = tiles_t;
+    if (splits < 1) splits = 1;
+    int per = (tiles_t + splits - 1) / splits * WG_TK;
+    splits = (T + per - 1) / per;
+    float* part = (float*)scratch_get((size_t)splits * NL * NS * sizeof(float), s);
+    TA_REQUIRE(part, "lora_wgrad: scratch allocation failed");
+    dim3 grid(ltiles, splits);
+    int nst = (NS + 15) / 16;
+    switch (nst) {
+        case 1: k_wgrad<1><<<grid, 256, 0, s>>>(L, ldl, NL, Sm, lds, NS, T, per, part); break;
+        case 2: k_wgrad<2><<<grid, 256, 0, s>>>(L, ldl, NL, Sm, lds, NS, T, per, part); break;
+        case 3: k_wgrad<3><<<grid, 256, 0, s>>>(L, ldl, NL, Sm, lds, NS, T, per, part); break;
+        case 4: k_wgrad<4><<<grid, 256, 0, s>>>(L, ldl, NL, Sm, lds, NS, T, per, part); break;
+        case 8: k_wgrad<8><<<grid, 256, 0, s>>>(L, ldl, NL, Sm, lds, NS, T, per, part); break;
+        case 12: k_wgrad<12><<<grid, 256, 0, s>>>(L, ldl, NL, Sm, lds, NS, T, per, part); break;
+        default: return set_error(-1, "lora_wgrad: %d small columns unsupported", NS);
+    }
+    int64_t n = (int64_t)NL * NS;
+    int blocks = (int)((n + 255) / 256);
+    if (trans)
+        k_wgrad_reduce<true><<<blocks, 256, 0, s>>>(part, splits, NL, NS, r, scale, G[0],
+                                                    G[1] ? G[1] : G[0], G[2] ? G[2] : G[0]);
+    else
+        k_wgrad_reduce<false><<<blocks, 256, 0, s>>>(part, splits, NL, NS, r, scale, G[0], G[0],
+                                                     G[0]);
+    return check_launch("lora_wgrad");
+}
+
+int transpose_batch(const bf16* src, bf16* dst, const void* descs, int nd, hipStream_t s) {
+    if (nd <= 0) return 0;
+    dim3 grid(64, nd);
+    k_transpose_batch<<<grid, 256, 0, s>>>(src, dst, (const TDesc*)descs, nd);
+    return check_launch("transpose_batch");
+}
+
+}  // namespace ta
