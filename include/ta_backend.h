@@ -145,6 +145,11 @@ int ta_gemm_rm(int x_kmajor, int y_kmajor, int M, int N, int K, float alpha,
                const uint16_t* X, int ldx, const uint16_t* Y, int ldy, float beta,
                uint16_t* C, int ldc, const uint16_t* bias, void* stream);
 
+/* Tile/pipeline variant of the large K-contiguous GEMM kernel (0 = the
+ * default; 1..3 alternatives kept for tuning sweeps).  No reference
+ * counterpart. */
+int ta_gemm_variant(int variant);
+
 /* ── centroid accumulator ───────────────────────────────────────────
  * replaces CentroidAccumulator::accumulate  src/centroid/centroid_accumulator.cpp:23-70
  * (intended math, see defect D1 there): for each token t,

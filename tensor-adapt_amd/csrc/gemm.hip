@@ -236,6 +236,207 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a, bool vecx, bool vecy) 
         }
 }
 
+// ── Large K-contiguous GEMMs (every frozen-base projection, the LM head) ──
+// Block tile 256 x BN with NW = WMW x WNW waves (NW*64 threads), wave tile
+// (256/WMW) x (BN/WNW) of 32x32 MFMA tiles.  With 8 waves two share each
+// SIMD, which hides LDS and global latency without deep software
+// pipelining.  Two LDS stages and two register staging sets: the global
+// loads of tile k+2 are issued before the MFMAs of tile k and stored after
+// the MFMAs of tile k+1, so each load has two iterations of matrix work to
+// arrive.  Staging is branch-free: K is a multiple of 64 and rows are
+// 16-byte aligned (the dispatcher checks), and rows past the end are
+// clamped to the last row — their products land only in output rows and
+// columns that are never stored.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+template <int ROWS, int NTH>
+struct FastLoader {
+    static constexpr int PT = ROWS * BK / 8 / NTH;
+    static_assert(PT * NTH * 8 == ROWS * BK, "tile must split evenly over the threads");
+    u32x4 r[PT];  // a native vector type: stays in registers
+    __device__ __forceinline__ void load(const bf16* __restrict__ P, int64_t ld, int row0, int k0,
+                                         int rows) {
+#pragma unroll
+        for (int i = 0; i < PT; i++) {
+            int q = threadIdx.x + NTH * i;
+            int row = min(row0 + (q >> 3), rows - 1);
+            r[i] = *(const u32x4*)(P + (int64_t)row * ld + k0 + (q & 7) * 8);
+        }
+    }
+    __device__ __forceinline__ void store(bf16* __restrict__ S) {
+#pragma unroll
+        for (int i = 0; i < PT; i++) {
+            int q = threadIdx.x + NTH * i;
+            *(u32x4*)(S + (q >> 3) * LDS_STRIDE + (q & 7) * 8) = r[i];
+        }
+    }
+};
+
+// One BK slice of MFMAs for a wave (kept out of line of the loop body but
+// always inlined, so the accumulators stay in registers).
+template <int TM, int TN, int WTM, int WTN>
+__device__ __attribute__((always_inline)) inline void big_mma(floatx16 (&acc)[TM][TN],
+                                                              const bf16* SXb, const bf16* SYb,
+                                                              int wm, int wn, int lane) {
+    const bf16* SX = SXb + (wm * WTM + (lane & 31)) * LDS_STRIDE + (lane >> 5) * 8;
+    const bf16* SY = SYb + (wn * WTN + (lane & 31)) * LDS_STRIDE + (lane >> 5) * 8;
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; kk++) {
+        bf16x8_t fx[TM], fy[TN];
+#pragma unroll
+        for (int i = 0; i < TM; i++) fx[i] = *(const bf16x8_t*)(SX + i * 32 * LDS_STRIDE + kk * 16);
+#pragma unroll
+        for (int j = 0; j < TN; j++) fy[j] = *(const bf16x8_t*)(SY + j * 32 * LDS_STRIDE + kk * 16);
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+                acc[i][j] =
+                    __builtin_amdgcn_mfma_f32_32x32x16_bf16(fx[i], fy[j], acc[i][j], 0, 0, 0);
+    }
+}
+
+template <int BN, int WMW, int WNW, int EPI, int PIPE>
+__global__ __launch_bounds__(WMW * WNW * 64) void k_gemm_big(GemmArgs a) {
+    constexpr int BM = 256, NTH = WMW * WNW * 64;
+    constexpr int WTM = BM / WMW, WTN = BN / WNW;
+    constexpr int TM = WTM / 32, TN = WTN / 32;
+    static_assert(TM * 32 == WTM && TN * 32 == WTN, "wave tile must be 32-aligned");
+    __shared__ __attribute__((aligned(16))) bf16 sX[2][BM * LDS_STRIDE];
+    __shared__ __attribute__((aligned(16))) bf16 sY[2][BN * LDS_STRIDE];
+
+    int nt = a.tiles_m * a.tiles_n;
+    int bid = blockIdx.x;
+    if ((nt & 7) == 0) bid = (bid & 7) * (nt >> 3) + (bid >> 3);
+    int tm_i = bid / a.tiles_n, tn_i = bid % a.tiles_n;
+    int m0 = tm_i * BM, n0 = tn_i * BN;
+    int kbeg = blockIdx.z * a.k_per_split;
+    int kend = min(a.K, kbeg + a.k_per_split);
+    int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    int wm = wv / WNW, wn = wv % WNW;
+
+    floatx16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+    FastLoader<BM, NTH> lx0;
+    FastLoader<BN, NTH> ly0;
+    FastLoader<BM, PIPE == 2 ? NTH : BM * BK / 8> lx1;  // unused when PIPE == 1
+    FastLoader<BN, PIPE == 2 ? NTH : BN * BK / 8> ly1;
+    const int nk = (kend - kbeg) / BK;
+
+#define compute(SXb, SYb) big_mma<TM, TN, WTM, WTN>(acc, SXb, SYb, wm, wn, lane)
+    if constexpr (PIPE == 1) {
+        // one staging set: tile k+1 is loaded while tile k feeds the MFMAs
+        if (nk > 0) {
+            lx0.load(a.X, a.ldx, m0, kbeg, a.M);
+            ly0.load(a.Y, a.ldy, n0, kbeg, a.N);
+            lx0.store(sX[0]);
+            ly0.store(sY[0]);
+        }
+        __syncthreads();
+        for (int kt = 0; kt < nk; kt++) {
+            const int cur = kt & 1;
+            const bool more = kt + 1 < nk;
+            if (more) {
+                lx0.load(a.X, a.ldx, m0, kbeg + (kt + 1) * BK, a.M);
+                ly0.load(a.Y, a.ldy, n0, kbeg + (kt + 1) * BK, a.N);
+            }
+            compute(sX[cur], sY[cur]);
+            if (more) {
+                lx0.store(sX[cur ^ 1]);
+                ly0.store(sY[cur ^ 1]);
+            }
+            __syncthreads();
+        }
+    } else {
+        if (nk > 0) {
+            lx0.load(a.X, a.ldx, m0, kbeg, a.M);
+            ly0.load(a.Y, a.ldy, n0, kbeg, a.N);
+            lx0.store(sX[0]);
+            ly0.store(sY[0]);
+            if (nk > 1) {
+                lx1.load(a.X, a.ldx, m0, kbeg + BK, a.M);
+                ly1.load(a.Y, a.ldy, n0, kbeg + BK, a.N);
+            }
+        }
+        __syncthreads();
+        // two k-tiles per trip so the staging set of each tile is static
+        for (int kt = 0; kt < nk; kt += 2) {
+            // even tile kt: data in LDS stage 0; tile kt+1 sits in set 1
+            if (kt + 2 < nk) {
+                lx0.load(a.X, a.ldx, m0, kbeg + (kt + 2) * BK, a.M);
+                ly0.load(a.Y, a.ldy, n0, kbeg + (kt + 2) * BK, a.N);
+            }
+            compute(sX[0], sY[0]);
+            if (kt + 1 < nk) {
+                lx1.store(sX[1]);
+                ly1.store(sY[1]);
+            }
+            __syncthreads();
+            if (kt + 1 >= nk) break;
+            // odd tile kt+1: LDS stage 1; tile kt+2 sits in set 0
+            if (kt + 3 < nk) {
+                lx1.load(a.X, a.ldx, m0, kbeg + (kt + 3) * BK, a.M);
+                ly1.load(a.Y, a.ldy, n0, kbeg + (kt + 3) * BK, a.N);
+            }
+            compute(sX[1], sY[1]);
+            if (kt + 2 < nk) {
+                lx0.store(sX[0]);
+                ly0.store(sY[0]);
+            }
+            __syncthreads();
+        }
+    }
+
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            int n = n0 + wn * WTN + j * 32 + (lane & 31);
+            if (n >= a.N) continue;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                int m = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                if (m >= a.M) continue;
+                float v = acc[i][j][r];
+                if (EPI == EPI_BF16) {
+                    bf16* C = (bf16*)a.C + (int64_t)m * a.ldc + n;
+                    float o = a.alpha * v;
+                    if (a.beta != 0.f) o += a.beta * bf2f(*C);
+                    if (a.bias) o = bf2f(f2bf(o)) + bf2f(a.bias[n]);
+                    *C = f2bf(o);
+                } else {
+                    a.part[((int64_t)blockIdx.z * a.M + m) * a.N + n] = v;
+                }
+            }
+        }
+}
+
+#undef compute
+
+// Tile/pipeline variants of k_gemm_big; variant 0 is the default.
+static int g_big_variant = 0;
+static int big_bn(int variant) {
+    return (variant == 1 || variant == 3) ? 128 : ((variant == 4 || variant == 5) ? 256 : 192);
+}
+
+template <int EPI>
+static void launch_big(int variant, dim3 grid, const GemmArgs& a, hipStream_t s) {
+    switch (variant) {
+        case 1: k_gemm_big<128, 2, 2, EPI, 1><<<grid, 256, 0, s>>>(a); break;
+        case 2: k_gemm_big<192, 2, 2, EPI, 1><<<grid, 256, 0, s>>>(a); break;
+        case 3: k_gemm_big<128, 4, 2, EPI, 2><<<grid, 512, 0, s>>>(a); break;
+        case 4: k_gemm_big<256, 4, 2, EPI, 1><<<grid, 512, 0, s>>>(a); break;
+        case 5: k_gemm_big<256, 2, 4, EPI, 1><<<grid, 512, 0, s>>>(a); break;
+        default: k_gemm_big<192, 4, 2, EPI, 1><<<grid, 512, 0, s>>>(a); break;
+    }
+}
+
 // Split-K reduction: sum partials in split order, then the BF16 or F32
 // epilogue.
 template <bool OUT_BF16>
@@ -298,6 +499,41 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
     a.part = nullptr;
     bool vx = al16(X) && (ldx % 8) == 0;
     bool vy = al16(Y) && (ldy % 8) == 0;
+
+    // large K-contiguous BF16 GEMMs: 256 x 192 tiles, 8 waves
+    if (xk && yk && !out_f32 && M >= 1024 && N >= 1024 && (K % BK) == 0 && vx && vy) {
+        // default: 256 x 192 tiles up to N = 3072 (N = 1536 gives one block per
+        // CU at M = 8192), 256 x 256 for wider outputs
+        int variant = g_big_variant;
+        if (variant == 0 && N > 3072) variant = 4;
+        const int BNb = big_bn(variant);
+        a.tiles_m = (M + 255) / 256;
+        a.tiles_n = (N + BNb - 1) / BNb;
+        int tiles = a.tiles_m * a.tiles_n;
+        int ksteps = (K + BK - 1) / BK;
+        int splits = 1;
+        if (force_splits > 0)
+            splits = force_splits;
+        else if (tiles < 192 && ksteps >= 32)
+            splits = std::min((256 + tiles - 1) / tiles, ksteps / 16);
+        if (splits < 1) splits = 1;
+        int steps_per = (ksteps + splits - 1) / splits;
+        a.k_per_split = steps_per * BK;
+        splits = (ksteps + steps_per - 1) / steps_per;
+        dim3 grid(tiles, 1, splits);
+        if (splits > 1) {
+            size_t bytes = (size_t)splits * M * N * sizeof(float);
+            a.part = (float*)scratch_get(bytes, s);
+            if (!a.part) return set_error(-2, "gemm: scratch allocation of %zu bytes failed", bytes);
+            launch_big<EPI_PARTIAL>(variant, grid, a, s);
+            int64_t MN = (int64_t)M * N;
+            k_splitk_reduce<true><<<(int)((MN + 255) / 256), 256, 0, s>>>(a.part, splits, M, N, C,
+                                                                          ldc, alpha, beta, bias);
+        } else {
+            launch_big<EPI_BF16>(variant, grid, a, s);
+        }
+        return check_launch("gemm");
+    }
 
     // tile choice: wide-N tiles for big outputs, skinny tiles for N <= 32
     enum { CFG_256x128, CFG_128x128, CFG_128x32 } cfg;
@@ -385,6 +621,12 @@ __global__ void k_f32_to_bf16_2d(const float* __restrict__ s, int64_t n, bf16* _
 using namespace ta;
 
 extern "C" {
+
+int ta_gemm_variant(int v) {
+    TA_REQUIRE(v >= 0 && v <= 5, "gemm_variant: %d out of range", v);
+    g_big_variant = v;
+    return 0;
+}
 
 int ta_gemm_rm(int x_kmajor, int y_kmajor, int M, int N, int K, float alpha, const uint16_t* X,
                int ldx, const uint16_t* Y, int ldy, float beta, uint16_t* C, int ldc,
