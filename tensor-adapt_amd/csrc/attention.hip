@@ -33,6 +33,8 @@
 //   are deterministic.
 #include <float.h>
 
+#include <algorithm>
+
 #include "ta_common.hpp"
 
 namespace ta {
@@ -82,19 +84,36 @@ __device__ __forceinline__ void stage_rows(bf16* __restrict__ s, const bf16* __r
     }
 }
 // Same rows staged transposed: LDS [HD][64 + 8] (row index contiguous).
+// Each thread loads 4 consecutive rows x 8 columns and writes one 8-byte
+// word (4 rows) per column, so the transpose costs 2 LDS writes per 16-byte
+// chunk instead of 8.
 template <int HD>
 __device__ __forceinline__ void stage_rows_t(bf16* __restrict__ s, const bf16* __restrict__ g,
                                              int64_t rs, int r0, int T) {
-    constexpr int CH = 64 * HD / 8;
+    constexpr int CH = 16 * (HD / 8);  // 16 row groups x HD/8 column chunks
     for (int q = threadIdx.x; q < CH; q += 256) {
-        int r = q % 64, c = (q / 64) * 8;  // consecutive threads: consecutive rows
-        bf16x8v v;
-        if (r0 + r < T)
-            v = *(const bf16x8v*)(g + (int64_t)(r0 + r) * rs + c);
-        else
-            v.w[0] = v.w[1] = v.w[2] = v.w[3] = 0u;
+        int rg = q & 15, c = (q >> 4) * 8;
+        uint32_t w[4][4];
 #pragma unroll
-        for (int e = 0; e < 8; e++) s[(c + e) * LDT + r] = (bf16)(v.w[e >> 1] >> ((e & 1) * 16));
+        for (int i = 0; i < 4; i++) {
+            int row = r0 + 4 * rg + i;
+            bf16x8v v;
+            if (row < T)
+                v = *(const bf16x8v*)(g + (int64_t)row * rs + c);
+            else
+                v.w[0] = v.w[1] = v.w[2] = v.w[3] = 0u;
+#pragma unroll
+            for (int j = 0; j < 4; j++) w[i][j] = v.w[j];
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            int j = e >> 1, sh = (e & 1) * 16;
+            uint64_t word = (uint64_t)((w[0][j] >> sh) & 0xffffu) |
+                            ((uint64_t)((w[1][j] >> sh) & 0xffffu) << 16) |
+                            ((uint64_t)((w[2][j] >> sh) & 0xffffu) << 32) |
+                            ((uint64_t)((w[3][j] >> sh) & 0xffffu) << 48);
+            *(uint64_t*)(s + (c + e) * LDT + 4 * rg) = word;
+        }
     }
 }
 
@@ -164,8 +183,9 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
     __shared__ __attribute__((aligned(16))) bf16 sVt[HD * LDT];
     __shared__ __attribute__((aligned(16))) bf16 sP[4][2][16 * LDT];
     int nqt = (T + TQ - 1) / TQ;
-    int qt = nqt - 1 - (int)(blockIdx.x % nqt);  // heavy (long) rows first
-    int bh = (int)(blockIdx.x / nqt);
+    int nbh = gridDim.x / nqt;
+    int qt = nqt - 1 - (int)(blockIdx.x / nbh);  // longest rows launch first
+    int bh = (int)(blockIdx.x % nbh);
     int b = bh / Hq, hq = bh % Hq, hkv = hq / (Hq / Hkv);
     int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     int64_t qs = (int64_t)Hq * HD, ks_ = (int64_t)Hkv * HD;
@@ -282,8 +302,9 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO
     __shared__ __attribute__((aligned(16))) bf16 sKt[HD * LDT];
     __shared__ __attribute__((aligned(16))) bf16 sS[4][2][16 * LDT];
     int nqt = (T + TQ - 1) / TQ;
-    int qt = nqt - 1 - (int)(blockIdx.x % nqt);
-    int bh = (int)(blockIdx.x / nqt);
+    int nbh = gridDim.x / nqt;
+    int qt = nqt - 1 - (int)(blockIdx.x / nbh);  // longest rows launch first
+    int bh = (int)(blockIdx.x % nbh);
     int b = bh / Hq, hq = bh % Hq, hkv = hq / (Hq / Hkv);
     int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     int64_t qs = (int64_t)Hq * HD, ks_ = (int64_t)Hkv * HD;
@@ -365,34 +386,38 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO
         }
 }
 
-// ── backward: dK, dV for one kv head and key tile ─────────────────────────
-// Wave w owns keys 16w..16w+15 of the tile; for every query head of the
-// group and query tile qt >= kt:  dP^T = V dO^T (keys x queries),
-// dS^T = P^T (dP^T - D), dV += P^T dO, dK += dS^T Q.
+// ── backward: dK, dV contributions of one query head, one key tile ─────────
+// Wave w owns keys 16w..16w+15 of the tile; for each query tile qt >= kt:
+// dP^T = V dO^T (keys x queries), dS^T = P^T (dP^T - D), dV_h += P^T dO,
+// dK_h += dS^T Q.  The head's F32 contributions go to part[bh] ([T][hd] for
+// dK then dV); k_attn_dkv_reduce sums the GQA group in head order — the
+// group sum of ops.cu:539-555 without atomics, so dK/dV are deterministic.
+// One block per (head, key tile) keeps the work per block within 16x of the
+// longest instead of (group size) x that.
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_bwd_dkv(const bf16* __restrict__ dO,
                                                       const bf16* __restrict__ Q,
-                                                      const bf16* __restrict__ K,
                                                       const bf16* __restrict__ V,
                                                       const float* __restrict__ P,
                                                       const float* __restrict__ Dq,
-                                                      bf16* __restrict__ dK,
-                                                      bf16* __restrict__ dV, int T, int Hq,
-                                                      int Hkv, float scale) {
-    __shared__ __attribute__((aligned(16))) bf16 sO[TQ * (HD + 8)];  // dO [q][hd]
-    __shared__ __attribute__((aligned(16))) bf16 sOt[HD * LDT];      // dO^T [hd][q]
-    __shared__ __attribute__((aligned(16))) bf16 sQt[HD * LDT];      // Q^T [hd][q]
-    __shared__ __attribute__((aligned(16))) bf16 sA[4][2][16 * LDT];  // per-wave P^T / dS^T hi,lo
+                                                      float* __restrict__ part, int T, int Hq,
+                                                      int Hkv) {
+    __shared__ __attribute__((aligned(16))) bf16 sO[TQ * (HD + 8)];     // dO [q][hd]
+    __shared__ __attribute__((aligned(16))) bf16 sOt[HD * LDT];         // dO^T [hd][q]
+    __shared__ __attribute__((aligned(16))) bf16 sQt[HD * LDT];         // Q^T [hd][q]
+    __shared__ __attribute__((aligned(16))) bf16 sA[4][2][16 * LDT];    // per-wave P^T / dS^T hi,lo
     __shared__ float sD[TQ];
     int nkt = (T + TK - 1) / TK;
-    int kt = (int)(blockIdx.x % nkt);  // low kt = most query tiles: they start first
-    int bkv = (int)(blockIdx.x / nkt);
-    int b = bkv / Hkv, hkv = bkv % Hkv;
-    int grp = Hq / Hkv;
+    int nbh = gridDim.x / nkt;
+    int kt = (int)(blockIdx.x / nbh);  // low kt = most query tiles: they launch first
+    int bh = (int)(blockIdx.x % nbh);
+    int b = bh / Hq, hq = bh % Hq, hkv = hq / (Hq / Hkv);
     int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     int64_t qs = (int64_t)Hq * HD, ks_ = (int64_t)Hkv * HD;
-    const bf16* Kh = K + (int64_t)b * T * ks_ + hkv * HD;
     const bf16* Vh = V + (int64_t)b * T * ks_ + hkv * HD;
+    const bf16* dOh = dO + (int64_t)b * T * qs + hq * HD;
+    const bf16* Qh = Q + (int64_t)b * T * qs + hq * HD;
+    const float* Ph = P + (int64_t)bh * T * T;
     int k0 = kt * TK;
     int keyA = k0 + 16 * w + (lane & 15);  // A-operand row (key) of this lane
     bf16x8_t vf[HD / 32];
@@ -407,71 +432,98 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dkv(const bf16* __restrict__ d
         accV[j] = zero4();
     }
     int nqt = (T + TQ - 1) / TQ;
-    for (int g = 0; g < grp; g++) {
-        int hq = hkv * grp + g;
-        int bh = b * Hq + hq;
-        const bf16* dOh = dO + (int64_t)b * T * qs + hq * HD;
-        const bf16* Qh = Q + (int64_t)b * T * qs + hq * HD;
-        const float* Ph = P + (int64_t)bh * T * T;
-        for (int qt = kt; qt < nqt; qt++) {
-            int q0 = qt * TQ;
-            stage_rows<HD>(sO, dOh, qs, q0, T);
-            stage_rows_t<HD>(sOt, dOh, qs, q0, T);
-            stage_rows_t<HD>(sQt, Qh, qs, q0, T);
-            if (threadIdx.x < TQ)
-                sD[threadIdx.x] = (q0 + threadIdx.x < T) ? Dq[(int64_t)bh * T + q0 + threadIdx.x] : 0.f;
-            __syncthreads();
-            floatx4 dPt[4];
-            wave_qk<HD>(dPt, vf, sO, lane);  // rows = keys, cols = queries
-            // P^T tile for this wave: P[q][key], lane keys kbase..kbase+3
-            float pv[4][4];
+    for (int qt = kt; qt < nqt; qt++) {
+        int q0 = qt * TQ;
+        stage_rows<HD>(sO, dOh, qs, q0, T);
+        stage_rows_t<HD>(sOt, dOh, qs, q0, T);
+        stage_rows_t<HD>(sQt, Qh, qs, q0, T);
+        if (threadIdx.x < TQ)
+            sD[threadIdx.x] = (q0 + threadIdx.x < T) ? Dq[(int64_t)bh * T + q0 + threadIdx.x] : 0.f;
+        __syncthreads();
+        floatx4 dPt[4];
+        wave_qk<HD>(dPt, vf, sO, lane);  // rows = keys, cols = queries
+        // P^T tile for this wave: P[q][key], lane keys kbase..kbase+3
+        float pv[4][4];
 #pragma unroll
-            for (int t = 0; t < 4; t++) {
-                int ql = 16 * t + (lane & 15);
-                int q = q0 + ql;
+        for (int t = 0; t < 4; t++) {
+            int q = q0 + 16 * t + (lane & 15);
+            const float* prow = Ph + (int64_t)q * T;
+            if ((T & 3) == 0 && q < T && kbase + 3 < T && kbase + 3 <= q) {  // 16-byte aligned
+                float4 v4 = *(const float4*)(prow + kbase);
+                pv[t][0] = v4.x;
+                pv[t][1] = v4.y;
+                pv[t][2] = v4.z;
+                pv[t][3] = v4.w;
+            } else {
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     int key = kbase + r;
-                    pv[t][r] = (q < T && key < T && key <= q) ? Ph[(int64_t)q * T + key] : 0.f;
+                    pv[t][r] = (q < T && key < T && key <= q) ? prow[key] : 0.f;
                 }
             }
-            // dV += P^T dO
-#pragma unroll
-            for (int t = 0; t < 4; t++)
-#pragma unroll
-                for (int r = 0; r < 4; r++)
-                    put_split(sA[w][0], sA[w][1], (4 * (lane >> 4) + r) * LDT + 16 * t + (lane & 15),
-                              pv[t][r]);
-            __syncthreads();
-            wave_pv<HD>(accV, sA[w][0], sA[w][1], sOt, lane);
-            __syncthreads();
-            // dK += dS^T Q
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                int ql = 16 * t + (lane & 15);
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    float ds = pv[t][r] * (dPt[t][r] - sD[ql]);
-                    put_split(sA[w][0], sA[w][1], (4 * (lane >> 4) + r) * LDT + ql, ds);
-                }
-            }
-            __syncthreads();
-            wave_pv<HD>(accK, sA[w][0], sA[w][1], sQt, lane);
-            __syncthreads();
         }
+        // dV += P^T dO
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                put_split(sA[w][0], sA[w][1], (4 * (lane >> 4) + r) * LDT + 16 * t + (lane & 15),
+                          pv[t][r]);
+        __syncthreads();
+        wave_pv<HD>(accV, sA[w][0], sA[w][1], sOt, lane);
+        __syncthreads();
+        // dK += dS^T Q
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            int ql = 16 * t + (lane & 15);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                float ds = pv[t][r] * (dPt[t][r] - sD[ql]);
+                put_split(sA[w][0], sA[w][1], (4 * (lane >> 4) + r) * LDT + ql, ds);
+            }
+        }
+        __syncthreads();
+        wave_pv<HD>(accK, sA[w][0], sA[w][1], sQt, lane);
+        __syncthreads();
     }
-    bf16* dKh = dK + (int64_t)b * T * ks_ + hkv * HD;
-    bf16* dVh = dV + (int64_t)b * T * ks_ + hkv * HD;
+    float* pK = part + (int64_t)bh * T * HD;
+    float* pV = part + ((int64_t)gridDim.x / nkt + bh) * T * HD;
 #pragma unroll
     for (int j = 0; j < HD / 16; j++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             int key = kbase + r;
             if (key < T) {
-                dKh[(int64_t)key * ks_ + 16 * j + (lane & 15)] = f2bf(scale * accK[j][r]);
-                dVh[(int64_t)key * ks_ + 16 * j + (lane & 15)] = f2bf(accV[j][r]);
+                pK[(int64_t)key * HD + 16 * j + (lane & 15)] = accK[j][r];
+                pV[(int64_t)key * HD + 16 * j + (lane & 15)] = accV[j][r];
             }
         }
+}
+
+// dK[b,t,hkv,:] = bf16(scale * sum_g part_K[b, hkv*grp+g, t, :]) and dV
+// likewise without the scale; heads summed in order.
+__global__ void k_attn_dkv_reduce(const float* __restrict__ part, bf16* __restrict__ dK,
+                                  bf16* __restrict__ dV, int B, int T, int Hq, int Hkv, int HD,
+                                  float scale) {
+    int64_t n = (int64_t)B * T * Hkv * HD;
+    int64_t nbh = (int64_t)B * Hq;
+    int grp = Hq / Hkv;
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        int d = (int)(i % HD);
+        int64_t r = i / HD;
+        int hkv = (int)(r % Hkv);
+        int64_t bt = r / Hkv;
+        int t = (int)(bt % T), b = (int)(bt / T);
+        float sk = 0.f, sv = 0.f;
+        for (int g = 0; g < grp; g++) {
+            int64_t bh = (int64_t)b * Hq + hkv * grp + g;
+            sk += part[(bh * T + t) * HD + d];
+            sv += part[((nbh + bh) * T + t) * HD + d];
+        }
+        dK[i] = f2bf(scale * sk);
+        dV[i] = f2bf(sv);
+    }
 }
 
 static inline bool a16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -492,9 +544,11 @@ int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* P, int
     return check_launch("sdpa_fwd");
 }
 
+// Dbuf: [B*Hq*T] F32 row dots; part: [2*B*Hq*T*hd] F32 per-head dK/dV
+// contributions (both drawn from the scratch pool when NULL).
 int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const float* P,
              bf16* dQ, bf16* dK, bf16* dV, int B, int T, int Hq, int Hkv, int hd, float* Dbuf,
-             hipStream_t s) {
+             float* part, hipStream_t s) {
     TA_REQUIRE(B > 0 && T > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0,
                "sdpa_bwd: bad shape B=%d T=%d Hq=%d Hkv=%d", B, T, Hq, Hkv);
     TA_REQUIRE(hd == 64 || hd == 128, "sdpa_bwd: head_dim %d not supported (64 or 128)", hd);
@@ -504,17 +558,23 @@ int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const 
         Dbuf = (float*)scratch_get((size_t)B * Hq * T * sizeof(float), s);
         TA_REQUIRE(Dbuf, "sdpa_bwd: scratch allocation failed");
     }
+    if (!part) {
+        part = (float*)scratch_get((size_t)2 * B * Hq * T * hd * sizeof(float), s, 2);
+        TA_REQUIRE(part, "sdpa_bwd: scratch allocation failed");
+    }
     int nqt = (T + TQ - 1) / TQ;
     float scale = 1.f / sqrtf((float)hd);
-    int64_t b1 = (int64_t)B * Hq * nqt, b2 = (int64_t)B * Hkv * nqt;
+    int64_t b1 = (int64_t)B * Hq * nqt;
     if (hd == 64) {
         k_attn_bwd_dq<64><<<(int)b1, 256, 0, s>>>(dO, K, V, P, dQ, Dbuf, T, Hq, Hkv, scale);
-        k_attn_bwd_dkv<64><<<(int)b2, 256, 0, s>>>(dO, Q, K, V, P, Dbuf, dK, dV, T, Hq, Hkv, scale);
+        k_attn_bwd_dkv<64><<<(int)b1, 256, 0, s>>>(dO, Q, V, P, Dbuf, part, T, Hq, Hkv);
     } else {
         k_attn_bwd_dq<128><<<(int)b1, 256, 0, s>>>(dO, K, V, P, dQ, Dbuf, T, Hq, Hkv, scale);
-        k_attn_bwd_dkv<128><<<(int)b2, 256, 0, s>>>(dO, Q, K, V, P, Dbuf, dK, dV, T, Hq, Hkv,
-                                                    scale);
+        k_attn_bwd_dkv<128><<<(int)b1, 256, 0, s>>>(dO, Q, V, P, Dbuf, part, T, Hq, Hkv);
     }
+    int64_t n = (int64_t)B * T * Hkv * hd;
+    int rb = (int)std::min<int64_t>((n + 255) / 256, 4096);
+    k_attn_dkv_reduce<<<rb, 256, 0, s>>>(part, dK, dV, B, T, Hq, Hkv, hd, scale);
     return check_launch("sdpa_bwd");
 }
 
@@ -531,7 +591,7 @@ int ta_sdpa_bwd(const uint16_t* dout, const uint16_t* Q, const uint16_t* K, cons
                 const float* attn_w, uint16_t* dQ, uint16_t* dK, uint16_t* dV, int B, int T,
                 int Hq, int Hkv, int head_dim, void* stream) {
     return ta::attn_bwd(dout, Q, K, V, attn_w, dQ, dK, dV, B, T, Hq, Hkv, head_dim, nullptr,
-                        (hipStream_t)stream);
+                        nullptr, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -36,7 +36,7 @@ int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* P, int
              int Hkv, int hd, bool zero_fill, hipStream_t s);
 int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const float* P,
              bf16* dQ, bf16* dK, bf16* dV, int B, int T, int Hq, int Hkv, int hd, float* Dbuf,
-             hipStream_t s);
+             float* part, hipStream_t s);
 int transpose_bf16(const bf16* in, bf16* out, int64_t rows, int64_t cols, hipStream_t s);
 int fill_normal_bf16(bf16* out, int64_t n, uint64_t seed, uint64_t sid, float std, hipStream_t s);
 int fill_bf16(bf16* out, int64_t n, float v, hipStream_t s);
@@ -103,7 +103,7 @@ struct Engine {
 
     bf16 *x_final, *xfn, *logits, *g_res, *dres, *tmpH, *dact, *dgate, *dup, *dxn2, *dao, *dQ, *dK,
         *dV, *dxn, *delta, *dh, *dh_cat;
-    float *final_rms, *loss_tok, *norm_dev, *Dbuf;
+    float *final_rms, *loss_tok, *norm_dev, *Dbuf, *dkv_part;
     double* cacc;
     int32_t *tok_dev, *tgt_dev;
     int32_t *tok_host, *tgt_host;  // pinned
@@ -279,6 +279,7 @@ static int engine_alloc(Engine* e) {
     CK(alloc(e, &e->dh, (int64_t)BT * r, "dh", 0));
     CK(alloc(e, &e->dh_cat, (int64_t)BT * r * 3, "dh_cat", 0));
     CK(alloc(e, &e->Dbuf, (int64_t)e->B * c.n_q * e->T, "Dbuf", 1));
+    CK(alloc(e, &e->dkv_part, (int64_t)2 * e->B * c.n_q * e->T * c.head_dim, "dkv_part", 1));
     CK(alloc(e, &e->norm_dev, 64, "norm", 1));
     CK(alloc(e, &e->cacc, H + 1, "centroid"));
     CK(alloc(e, &e->tok_dev, BT, "tok"));
@@ -551,7 +552,7 @@ static int backward(Engine* e) {
         TIMED(TA_CAT_ATTN_BWD, 8.0 * tri * c.head_dim,
               tri * 4 + dBT * (2.0 * qd + 2.0 * kvd) * 2 + dBT * (qd + 2.0 * kvd) * 2,
               attn_bwd(e->dao, ly.Q, ly.K, ly.V, ly.attn_w, e->dQ, e->dK, e->dV, e->B, e->T, c.n_q,
-                       c.n_kv, c.head_dim, e->Dbuf, s));
+                       c.n_kv, c.head_dim, e->Dbuf, e->dkv_part, s));
         TIMED(TA_CAT_ELEMWISE, 0, dBT * qd * 4,
               ta_rope_bwd(e->dQ, e->B, e->T, c.n_q, c.head_dim, c.rope_theta, s));
         TIMED(TA_CAT_ELEMWISE, 0, dBT * kvd * 4,
