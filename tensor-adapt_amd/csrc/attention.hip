@@ -35,11 +35,9 @@
 
 #include <algorithm>
 
-#include "ta_common.hpp"
+#include "ta_internal.hpp"
 
 namespace ta {
-
-void* scratch_get(size_t bytes, hipStream_t s, int slot = 0);
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));

@@ -18,11 +18,9 @@
 // by max_iters / iters, so the launch always drains.
 #include <float.h>
 
-#include "ta_common.hpp"
+#include "ta_internal.hpp"
 
 namespace ta {
-
-void* scratch_get(size_t bytes, hipStream_t s, int slot = 0);
 
 constexpr int kTok = 64;  // tokens per block in the accumulate pass
 

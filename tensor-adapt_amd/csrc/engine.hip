@@ -24,34 +24,10 @@
 #include <vector>
 
 #include "ta_backend.h"
-#include "ta_common.hpp"
 #include "ta_engine.h"
+#include "ta_internal.hpp"
 
 namespace ta {
-
-int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16* X, int64_t ldx,
-                  const bf16* Y, int64_t ldy, float beta, void* C, int64_t ldc, const bf16* bias,
-                  bool out_f32, hipStream_t s, int force_splits);
-int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* P, int B, int T, int Hq,
-             int Hkv, int hd, bool zero_fill, hipStream_t s);
-int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const float* P,
-             bf16* dQ, bf16* dK, bf16* dV, int B, int T, int Hq, int Hkv, int hd, float* Dbuf,
-             float* part, hipStream_t s);
-int transpose_bf16(const bf16* in, bf16* out, int64_t rows, int64_t cols, hipStream_t s);
-int fill_normal_bf16(bf16* out, int64_t n, uint64_t seed, uint64_t sid, float std, hipStream_t s);
-int fill_bf16(bf16* out, int64_t n, float v, hipStream_t s);
-int kaiming_init(float* a32, bf16* a16, int64_t n, int in_dim, hipStream_t s);
-int add2_bf16(bf16* out, const bf16* a, const bf16* b, int64_t n, hipStream_t s);
-int mask_targets_dev(const int32_t* in, const int32_t* tgt_in, int32_t* tgt, int B, int T,
-                     hipStream_t s);
-int lora_skinny_nt(const bf16* X, int64_t ldx, int M, int K, int r, const bf16* const* Y,
-                   bf16* const* C, int64_t ldc, int n, hipStream_t s);
-int lora_rank_update(bool delta, bf16* Y, int64_t ldy, int M, int N, int r, float scale,
-                     const bf16* const* U, const int64_t* ldu, const bf16* const* V, int n,
-                     hipStream_t s);
-int lora_wgrad(const bf16* L, int64_t ldl, int NL, const bf16* Sm, int64_t lds, int NS, int T,
-               int r, float scale, bool trans, float* const* G, hipStream_t s);
-int transpose_batch(const bf16* src, bf16* dst, const void* descs, int nd, hipStream_t s);
 
 #define CK(x)                    \
     do {                         \
@@ -97,7 +73,7 @@ struct Engine {
     int64_t nparam = 0;
     float *master = nullptr, *mom = nullptr, *vel = nullptr, *grad = nullptr;
     bf16* shadow = nullptr;
-    bf16* shadowT = nullptr;       // B^T of every B shadow (same offsets), per step
+    bf16* shadowT = nullptr;       // A^T and B^T of every shadow (same offsets), per step
     void* tdesc = nullptr;         // device descriptors of those transposes
     int ntdesc = 0;
 
@@ -223,7 +199,10 @@ static int engine_alloc(Engine* e) {
         std::vector<TD> td;
         for (auto& ly : e->L)
             for (auto& pr : ly.pr)
-                if (pr.on) td.push_back({pr.offB, pr.offB, pr.out, e->r});
+                if (pr.on) {
+                    td.push_back({pr.offB, pr.offB, pr.out, e->r});  // B [out,r] -> B^T
+                    td.push_back({pr.offA, pr.offA, e->r, pr.in});   // A [r,in] -> A^T
+                }
         e->ntdesc = (int)td.size();
         CK(dmalloc(e, &e->tdesc, td.size() * sizeof(TD) + 16, "tdesc"));
         if (!td.empty())
@@ -317,12 +296,13 @@ static inline double gbytes(double M, double N, double K, double in_b, double ou
     return (M * K + K * N) * in_b + M * N * out_b * (acc ? 2.0 : 1.0);
 }
 
-// LoRA forward for the on-pairs of one input-sharing group (q,k,v on
-// x_normed; gate,up on x_normed2; o; down), adapter_model.cu:96-129:
-//   h_p = bf16(x A_p^T)                (one pass over x for the group)
-//   y_p = bf16(y_p + s * bf16(h_p B_p^T))
-static int lora_group_fwd(Engine* e, Layer& ly, std::initializer_list<int> group, const bf16* x,
-                          int in, bf16* const* ys) {
+// LoRA forward, first half, for the on-pairs of one input-sharing group (q,k,v
+// on x_normed; gate,up on x_normed2; o; down): h_p = bf16(x A_p^T) in one
+// pass over x (adapter_model.cu:104-114).  The second half,
+// y_p = bf16(y_p + s * bf16(h_p B_p^T)) (adapter_model.cu:116-127), runs in
+// the epilogue of y_p's projection GEMM (fwd_epi).
+static int lora_group_h(Engine* e, Layer& ly, std::initializer_list<int> group, const bf16* x,
+                        int in) {
     const bf16* Ay[3];
     bf16* hs[3];
     int n = 0;
@@ -335,27 +315,31 @@ static int lora_group_fwd(Engine* e, Layer& ly, std::initializer_list<int> group
     const double BT = e->BT, r = e->r;
     TIMED(TA_CAT_LORA, gflops(BT, n * r, in), BT * in * 2 + BT * n * r * 2,
           lora_skinny_nt(x, in, e->BT, in, e->r, Ay, hs, e->r, n, e->s));
-    int i = 0;
-    for (int p : group) {
-        Pair& pr = ly.pr[p];
-        bf16* y = ys[i++];
-        if (!pr.on) continue;
-        const bf16* U[1] = {pr.h};
-        const int64_t ldu[1] = {e->r};
-        const bf16* V[1] = {e->shadow + pr.offB};
-        TIMED(TA_CAT_LORA, gflops(BT, pr.out, r), BT * pr.out * 4 + BT * r * 2,
-              lora_rank_update(true, y, pr.out, e->BT, pr.out, e->r, e->scale, U, ldu, V, 1, e->s));
-    }
     return 0;
+}
+
+static LoraEpi fwd_epi(Engine* e, const Pair& pr) {
+    LoraEpi ep{};
+    if (!pr.on) return ep;
+    ep.n = 1;
+    ep.r = e->r;
+    ep.delta = true;
+    ep.s = e->scale;
+    ep.u[0] = pr.h;
+    ep.ldu[0] = e->r;
+    ep.v_nk[0] = ep.v_alt[0] = e->shadow + pr.offB;
+    return ep;
 }
 
 // LoRA backward for one group, adapter_model.cu:131-220, pairs in order:
 //   dh_p = bf16(go_p B_p)            (B^T shadow, one pass over go_p)
 //   gB_p += s * go_p^T h_p           (h_p cached by the forward)
 //   gA_p += s * dh_p^T x             (all pairs of the group in one pass over x)
-//   gx = bf16(s * dh_p A_p + gx)     (pairs applied in order, gx read once)
+// and returns the terms gx = bf16(s * dh_p A_p + gx) (pairs in order) for
+// the epilogue of the last input-gradient GEMM of the group.
 static int lora_group_bwd(Engine* e, Layer& ly, std::initializer_list<int> group, const bf16* x,
-                          int in, const bf16* const* gos, bf16* gx) {
+                          int in, const bf16* const* gos, LoraEpi* ep) {
+    *ep = LoraEpi{};
     int on[3], n = 0, i = 0;
     const bf16* go_on[3];
     for (int p : group) {
@@ -380,37 +364,39 @@ static int lora_group_bwd(Engine* e, Layer& ly, std::initializer_list<int> group
               lora_wgrad(go_on[q], pr.out, pr.out, pr.h, r, r, BT, r, e->scale, false, G, e->s));
     }
     float* GA[3] = {nullptr, nullptr, nullptr};
-    const bf16* U[3];
-    int64_t ldu[3];
-    const bf16* V[3];
+    ep->n = n;
+    ep->r = r;
+    ep->delta = false;
+    ep->s = e->scale;
     for (int q = 0; q < n; q++) {
         Pair& pr = ly.pr[on[q]];
         GA[q] = e->grad + pr.offA;
-        U[q] = e->dh_cat + q * r;
-        ldu[q] = ldh;
-        V[q] = e->shadow + pr.offA;
+        ep->u[q] = e->dh_cat + q * r;
+        ep->ldu[q] = ldh;
+        ep->v_nk[q] = e->shadowT + pr.offA;
+        ep->v_alt[q] = e->shadow + pr.offA;
     }
     TIMED(TA_CAT_LORA, gflops(ldh, in, dBT), dBT * (in + ldh) * 2 + ldh * in * 8.0,
           lora_wgrad(x, in, in, e->dh_cat, ldh, (int)ldh, BT, r, e->scale, true, GA, e->s));
-    TIMED(TA_CAT_LORA, gflops(dBT, in, ldh), dBT * in * 4 + dBT * ldh * 2,
-          lora_rank_update(false, gx, in, BT, in, r, e->scale, U, ldu, V, n, e->s));
     return 0;
 }
 
 // proj_fwd (qwen2.cu:21-30) with the bias add fused: y = bf16(bf16(x W^T) + b)
+// (with the pair's LoRA delta, when given, in the same epilogue)
 static int proj_fwd(Engine* e, const bf16* W, const bf16* x, bf16* y, int in, int out,
-                    const bf16* bias) {
+                    const bf16* bias, const LoraEpi* lora = nullptr) {
     TIMED(TA_CAT_GEMM_FWD, gflops(e->BT, out, in), gbytes(e->BT, out, in, 2, 2, false),
           gemm_dispatch(true, true, e->BT, out, in, 1.f, x, in, W, in, 0.f, y, out, bias, false,
-                        e->s, 0));
+                        e->s, 0, lora && lora->n ? lora : nullptr));
     return 0;
 }
 // proj_bwd_x (qwen2.cu:32-41): dx = bf16(dy W + beta dx), W^T resident
+// (with the group's LoRA dx terms, when given, in the same epilogue)
 static int proj_bwd_x(Engine* e, const bf16* Wt, const bf16* dy, bf16* dx, int out, int in,
-                      float beta) {
+                      float beta, const LoraEpi* lora = nullptr) {
     TIMED(TA_CAT_GEMM_DX, gflops(e->BT, in, out), gbytes(e->BT, in, out, 2, 2, beta != 0.f),
           gemm_dispatch(true, true, e->BT, in, out, 1.f, dy, out, Wt, out, beta, dx, in, nullptr,
-                        false, e->s, 0));
+                        false, e->s, 0, lora && lora->n ? lora : nullptr));
     return 0;
 }
 
@@ -455,12 +441,12 @@ static int forward(Engine* e) {
         bf16* res_out = (l + 1 < c.layers) ? e->L[l + 1].res_in : e->x_final;
         TIMED(TA_CAT_NORM, 0, nrm_b,
               ta_rms_norm_fwd(ly.res_in, ly.in_norm, ly.xn, ly.in_rms, 1, BT, H, c.rms_eps, s));
-        CK(proj_fwd(e, ly.W[PQ], ly.xn, ly.Q, H, qd, ly.bias[0]));
-        CK(proj_fwd(e, ly.W[PK], ly.xn, ly.K, H, kvd, ly.bias[1]));
-        CK(proj_fwd(e, ly.W[PV], ly.xn, ly.V, H, kvd, ly.bias[2]));
+        CK(lora_group_h(e, ly, {PQ, PK, PV}, ly.xn, H));
         {
-            bf16* ys[3] = {ly.Q, ly.K, ly.V};
-            CK(lora_group_fwd(e, ly, {PQ, PK, PV}, ly.xn, H, ys));
+            LoraEpi eq = fwd_epi(e, ly.pr[PQ]), ek = fwd_epi(e, ly.pr[PK]), ev = fwd_epi(e, ly.pr[PV]);
+            CK(proj_fwd(e, ly.W[PQ], ly.xn, ly.Q, H, qd, ly.bias[0], &eq));
+            CK(proj_fwd(e, ly.W[PK], ly.xn, ly.K, H, kvd, ly.bias[1], &ek));
+            CK(proj_fwd(e, ly.W[PV], ly.xn, ly.V, H, kvd, ly.bias[2], &ev));
         }
         TIMED(TA_CAT_ELEMWISE, 0, dBT * qd * 4,
               ta_rope_fwd(ly.Q, e->B, e->T, c.n_q, c.head_dim, c.rope_theta, s));
@@ -471,28 +457,28 @@ static int forward(Engine* e) {
               tri * 4 + dBT * (2.0 * qd + 2.0 * kvd) * 2,
               attn_fwd(ly.Q, ly.K, ly.V, ly.ao, ly.attn_w, e->B, e->T, c.n_q, c.n_kv, c.head_dim,
                        false, s));
-        CK(proj_fwd(e, ly.W[PO], ly.ao, e->tmpH, qd, H, nullptr));
+        CK(lora_group_h(e, ly, {PO}, ly.ao, qd));
         {
-            bf16* ys[1] = {e->tmpH};
-            CK(lora_group_fwd(e, ly, {PO}, ly.ao, qd, ys));
+            LoraEpi eo = fwd_epi(e, ly.pr[PO]);
+            CK(proj_fwd(e, ly.W[PO], ly.ao, e->tmpH, qd, H, nullptr, &eo));
         }
         TIMED(TA_CAT_ELEMWISE, 0, dBT * H * 6,
               add2_bf16(ly.res_mid, ly.res_in, e->tmpH, (int64_t)BT * H, s));
         TIMED(TA_CAT_NORM, 0, nrm_b,
               ta_rms_norm_fwd(ly.res_mid, ly.post_norm, ly.xn2, ly.post_rms, 1, BT, H, c.rms_eps,
                               s));
-        CK(proj_fwd(e, ly.W[PG], ly.xn2, ly.gate, H, I, nullptr));
-        CK(proj_fwd(e, ly.W[PU], ly.xn2, ly.up, H, I, nullptr));
+        CK(lora_group_h(e, ly, {PG, PU}, ly.xn2, H));
         {
-            bf16* ys[2] = {ly.gate, ly.up};
-            CK(lora_group_fwd(e, ly, {PG, PU}, ly.xn2, H, ys));
+            LoraEpi eg = fwd_epi(e, ly.pr[PG]), eu = fwd_epi(e, ly.pr[PU]);
+            CK(proj_fwd(e, ly.W[PG], ly.xn2, ly.gate, H, I, nullptr, &eg));
+            CK(proj_fwd(e, ly.W[PU], ly.xn2, ly.up, H, I, nullptr, &eu));
         }
         TIMED(TA_CAT_ELEMWISE, 0, dBT * I * 6,
               ta_silu_mul_fwd(ly.gate, ly.up, ly.act, (int64_t)BT * I, s));
-        CK(proj_fwd(e, ly.W[PD], ly.act, e->tmpH, I, H, nullptr));
+        CK(lora_group_h(e, ly, {PD}, ly.act, I));
         {
-            bf16* ys[1] = {e->tmpH};
-            CK(lora_group_fwd(e, ly, {PD}, ly.act, I, ys));
+            LoraEpi ed = fwd_epi(e, ly.pr[PD]);
+            CK(proj_fwd(e, ly.W[PD], ly.act, e->tmpH, I, H, nullptr, &ed));
         }
         TIMED(TA_CAT_ELEMWISE, 0, dBT * H * 6,
               add2_bf16(res_out, ly.res_mid, e->tmpH, (int64_t)BT * H, s));
@@ -502,7 +488,7 @@ static int forward(Engine* e) {
     // LM head (qwen2.cu:163-175), tied to the embedding when c.tie
     TIMED(TA_CAT_LMHEAD, gflops(BT, e->V, H), gbytes(BT, e->V, H, 2, 2, false),
           gemm_dispatch(true, true, BT, e->V, H, 1.f, e->xfn, H, e->lm, H, 0.f, e->logits, e->V,
-                        nullptr, false, s, 0));
+                        nullptr, false, s, 0, nullptr));
     // loss (adapt_trainer.cu:201-205): dlogits overwrite the logits in place
     TIMED(TA_CAT_CE, 0, dBT * e->V * 6,
           ta_cross_entropy_fwd(e->logits, e->tgt_dev, e->loss_tok, e->logits, BT, e->V, s));
@@ -518,25 +504,27 @@ static int backward(Engine* e) {
     // dres = dlogits * W_lm (qwen2.cu:205); grad = rms_norm_bwd(final)
     TIMED(TA_CAT_LMHEAD, gflops(BT, H, e->V), gbytes(BT, H, e->V, 2, 2, false),
           gemm_dispatch(true, true, BT, H, e->V, 1.f, e->logits, e->V, e->lmT, e->V, 0.f, e->dres,
-                        H, nullptr, false, s, 0));
+                        H, nullptr, false, s, 0, nullptr));
     TIMED(TA_CAT_NORM, 0, nrm_b,
           ta_rms_norm_bwd(e->dres, e->x_final, e->final_norm, e->final_rms, e->g_res, nullptr, 1,
                           BT, H, c.rms_eps, s));
     for (int l = c.layers - 1; l >= 0; l--) {
         Layer& ly = e->L[l];
         // FFN (qwen2.cu:222-246)
-        CK(proj_bwd_x(e, ly.Wt[PD], e->g_res, e->dact, H, I, 0.f));
         {
             const bf16* gos[1] = {e->g_res};
-            CK(lora_group_bwd(e, ly, {PD}, ly.act, I, gos, e->dact));
+            LoraEpi ep;
+            CK(lora_group_bwd(e, ly, {PD}, ly.act, I, gos, &ep));
+            CK(proj_bwd_x(e, ly.Wt[PD], e->g_res, e->dact, H, I, 0.f, &ep));
         }
         TIMED(TA_CAT_ELEMWISE, 0, dBT * I * 10,
               ta_silu_mul_bwd(e->dact, ly.gate, ly.up, e->dgate, e->dup, (int64_t)BT * I, s));
-        CK(proj_bwd_x(e, ly.Wt[PG], e->dgate, e->dxn2, I, H, 0.f));
-        CK(proj_bwd_x(e, ly.Wt[PU], e->dup, e->dxn2, I, H, 1.f));
         {
             const bf16* gos[2] = {e->dgate, e->dup};
-            CK(lora_group_bwd(e, ly, {PG, PU}, ly.xn2, H, gos, e->dxn2));
+            LoraEpi ep;
+            CK(lora_group_bwd(e, ly, {PG, PU}, ly.xn2, H, gos, &ep));
+            CK(proj_bwd_x(e, ly.Wt[PG], e->dgate, e->dxn2, I, H, 0.f));
+            CK(proj_bwd_x(e, ly.Wt[PU], e->dup, e->dxn2, I, H, 1.f, &ep));
         }
         TIMED(TA_CAT_NORM, 0, nrm_b,
               ta_rms_norm_bwd(e->dxn2, ly.res_mid, ly.post_norm, ly.post_rms, e->tmpH, nullptr, 1,
@@ -544,10 +532,11 @@ static int backward(Engine* e) {
         TIMED(TA_CAT_ELEMWISE, 0, dBT * H * 6,
               ta_add_inplace(e->g_res, e->tmpH, (int64_t)BT * H, s));
         // attention (qwen2.cu:250-304)
-        CK(proj_bwd_x(e, ly.Wt[PO], e->g_res, e->dao, H, qd, 0.f));
         {
             const bf16* gos[1] = {e->g_res};
-            CK(lora_group_bwd(e, ly, {PO}, ly.ao, qd, gos, e->dao));
+            LoraEpi ep;
+            CK(lora_group_bwd(e, ly, {PO}, ly.ao, qd, gos, &ep));
+            CK(proj_bwd_x(e, ly.Wt[PO], e->g_res, e->dao, H, qd, 0.f, &ep));
         }
         TIMED(TA_CAT_ATTN_BWD, 8.0 * tri * c.head_dim,
               tri * 4 + dBT * (2.0 * qd + 2.0 * kvd) * 2 + dBT * (qd + 2.0 * kvd) * 2,
@@ -557,12 +546,13 @@ static int backward(Engine* e) {
               ta_rope_bwd(e->dQ, e->B, e->T, c.n_q, c.head_dim, c.rope_theta, s));
         TIMED(TA_CAT_ELEMWISE, 0, dBT * kvd * 4,
               ta_rope_bwd(e->dK, e->B, e->T, c.n_kv, c.head_dim, c.rope_theta, s));
-        CK(proj_bwd_x(e, ly.Wt[PQ], e->dQ, e->dxn, qd, H, 0.f));
-        CK(proj_bwd_x(e, ly.Wt[PK], e->dK, e->dxn, kvd, H, 1.f));
-        CK(proj_bwd_x(e, ly.Wt[PV], e->dV, e->dxn, kvd, H, 1.f));
         {
             const bf16* gos[3] = {e->dQ, e->dK, e->dV};
-            CK(lora_group_bwd(e, ly, {PQ, PK, PV}, ly.xn, H, gos, e->dxn));
+            LoraEpi ep;
+            CK(lora_group_bwd(e, ly, {PQ, PK, PV}, ly.xn, H, gos, &ep));
+            CK(proj_bwd_x(e, ly.Wt[PQ], e->dQ, e->dxn, qd, H, 0.f));
+            CK(proj_bwd_x(e, ly.Wt[PK], e->dK, e->dxn, kvd, H, 1.f));
+            CK(proj_bwd_x(e, ly.Wt[PV], e->dV, e->dxn, kvd, H, 1.f, &ep));
         }
         // centroid side channel (adapt_trainer.cu:210-232): h = x_normed,
         // g = dx_attn_in of this layer

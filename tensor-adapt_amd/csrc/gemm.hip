@@ -25,11 +25,9 @@
 // rounding and rounded again — the reference's gemm + ops::add_bias), F32
 // (gemm_f32 semantics), or F32 partials for split-K with a separate
 // fixed-order reduction (deterministic).
-#include "ta_common.hpp"
+#include "ta_internal.hpp"
 
 namespace ta {
-
-void* scratch_get(size_t bytes, hipStream_t s, int slot = 0);
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
@@ -52,6 +50,15 @@ struct GemmArgs {
     float* part;     // split-K partials [splits][M][N]
     int k_per_split; // multiple of BK
     int tiles_m, tiles_n;
+    // LoRA epilogue (k_gemm_big only): after the base rounding, for each
+    // pair p in order, with D_p = U_p V_p^T (U_p [M x r], V_p [N x r]):
+    //   delta: C = bf16(C + s * bf16(D_p))    (apply_lora_fwd)
+    //   else : C = bf16(s * D_p + C)          (apply_lora_bwd's dx GEMM)
+    int lora_n, lora_r, lora_delta;
+    float lora_s;
+    const bf16* lora_u[3];
+    int64_t lora_ldu[3];
+    const bf16* lora_v[3];
 };
 
 // Load one 16-byte chunk (8 bf16) of a K-contiguous operand row with
@@ -393,28 +400,84 @@ __global__ __launch_bounds__(WMW * WNW * 64) void k_gemm_big(GemmArgs a) {
         }
     }
 
+    if constexpr (EPI == EPI_PARTIAL) {
 #pragma unroll
-    for (int i = 0; i < TM; i++)
+        for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < TN; j++) {
-            int n = n0 + wn * WTN + j * 32 + (lane & 31);
-            if (n >= a.N) continue;
+            for (int j = 0; j < TN; j++) {
+                int n = n0 + wn * WTN + j * 32 + (lane & 31);
+                if (n >= a.N) continue;
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                int m = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                if (m >= a.M) continue;
-                float v = acc[i][j][r];
-                if (EPI == EPI_BF16) {
-                    bf16* C = (bf16*)a.C + (int64_t)m * a.ldc + n;
-                    float o = a.alpha * v;
-                    if (a.beta != 0.f) o += a.beta * bf2f(*C);
-                    if (a.bias) o = bf2f(f2bf(o)) + bf2f(a.bias[n]);
-                    *C = f2bf(o);
-                } else {
-                    a.part[((int64_t)blockIdx.z * a.M + m) * a.N + n] = v;
+                for (int r = 0; r < 16; r++) {
+                    int m = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    if (m < a.M) a.part[((int64_t)blockIdx.z * a.M + m) * a.N + n] = acc[i][j][r];
                 }
             }
+    } else {
+        // three small unrolled passes keep acc in registers: (1) base
+        // epilogue in place, (2) LoRA terms pair by pair, (3) store
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                int n = n0 + wn * WTN + j * 32 + (lane & 31);
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    int m = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    float o = a.alpha * acc[i][j][r];
+                    if (a.beta != 0.f && m < a.M && n < a.N)
+                        o += a.beta * bf2f(((const bf16*)a.C)[(int64_t)m * a.ldc + n]);
+                    if (a.bias && n < a.N) o = bf2f(f2bf(o)) + bf2f(a.bias[n]);
+                    acc[i][j][r] = bf2f(f2bf(o));
+                }
+            }
+        // LoRA terms: D = U V^T on the same 32x32 MFMA layout as acc; static
+        // pair indices (a runtime index into the by-value argument struct
+        // would move it to scratch)
+#pragma unroll
+        for (int p = 0; p < 3; p++) {
+            if (p >= a.lora_n) break;
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    int arow = min(m0 + wm * WTM + i * 32 + (lane & 31), a.M - 1);
+                    int bcol = min(n0 + wn * WTN + j * 32 + (lane & 31), a.N - 1);
+                    floatx16 d;
+#pragma unroll
+                    for (int r = 0; r < 16; r++) d[r] = 0.f;
+                    for (int k = 0; k < a.lora_r; k += 16) {
+                        int kk = k + 8 * (lane >> 5);
+                        bf16x8_t fa, fb;
+                        if (kk < a.lora_r) {
+                            fa = *(const bf16x8_t*)(a.lora_u[p] + (int64_t)arow * a.lora_ldu[p] + kk);
+                            fb = *(const bf16x8_t*)(a.lora_v[p] + (int64_t)bcol * a.lora_r + kk);
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 8; e++) fa[e] = fb[e] = (__bf16)0.f;
+                        }
+                        d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, fb, d, 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int r = 0; r < 16; r++)
+                        acc[i][j][r] = a.lora_delta
+                                           ? bf2f(f2bf(acc[i][j][r] + a.lora_s * bf2f(f2bf(d[r]))))
+                                           : bf2f(f2bf(a.lora_s * d[r] + acc[i][j][r]));
+                }
         }
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                int n = n0 + wn * WTN + j * 32 + (lane & 31);
+                if (n >= a.N) continue;
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    int m = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    if (m < a.M) ((bf16*)a.C)[(int64_t)m * a.ldc + n] = f2bf(acc[i][j][r]);
+                }
+            }
+    }
 }
 
 #undef compute
@@ -479,10 +542,13 @@ static void launch_cfg(bool xk, bool yk, const GemmArgs& a, int splits, bool vx,
 
 static inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-// Shape-driven dispatch.  out_f32: C is F32 (gemm_f32 semantics).
+// Shape-driven dispatch.  out_f32: C is F32 (gemm_f32 semantics).  lora
+// (may be NULL): rank-r terms applied to C after the base epilogue, fused
+// into the large-GEMM kernel's epilogue when that kernel runs unsplit and
+// applied by k_rank_update right after the GEMM otherwise.
 int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16* X, int64_t ldx,
                   const bf16* Y, int64_t ldy, float beta, void* C, int64_t ldc, const bf16* bias,
-                  bool out_f32, hipStream_t s, int force_splits) {
+                  bool out_f32, hipStream_t s, int force_splits, const LoraEpi* lora) {
     GemmArgs a;
     a.M = M;
     a.N = N;
@@ -497,6 +563,24 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
     a.beta = beta;
     a.bias = bias;
     a.part = nullptr;
+    a.lora_n = 0;
+    a.lora_r = 0;
+    a.lora_delta = 0;
+    a.lora_s = 0.f;
+    for (int p = 0; p < 3; p++) {
+        a.lora_u[p] = a.lora_v[p] = nullptr;
+        a.lora_ldu[p] = 0;
+    }
+    if (lora && lora->n > 0) {
+        if (out_f32 || lora->n > 3 || (lora->r & 7) != 0)
+            return set_error(-1, "gemm: unsupported LoRA epilogue (n=%d r=%d)", lora->n, lora->r);
+    }
+    // runs the LoRA terms as a separate pass when the kernel did not fuse them
+    auto lora_after = [&]() -> int {
+        if (!lora || lora->n == 0) return 0;
+        return lora_rank_update(lora->delta, (bf16*)C, ldc, M, N, lora->r, lora->s, lora->u,
+                                lora->ldu, lora->v_alt, lora->n, s);
+    };
     bool vx = al16(X) && (ldx % 8) == 0;
     bool vy = al16(Y) && (ldy % 8) == 0;
 
@@ -529,7 +613,20 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
             int64_t MN = (int64_t)M * N;
             k_splitk_reduce<true><<<(int)((MN + 255) / 256), 256, 0, s>>>(a.part, splits, M, N, C,
                                                                           ldc, alpha, beta, bias);
+            int rc = check_launch("gemm");
+            return rc ? rc : lora_after();
         } else {
+            if (lora && lora->n > 0) {
+                a.lora_n = lora->n;
+                a.lora_r = lora->r;
+                a.lora_delta = lora->delta ? 1 : 0;
+                a.lora_s = lora->s;
+                for (int p = 0; p < lora->n; p++) {
+                    a.lora_u[p] = lora->u[p];
+                    a.lora_ldu[p] = lora->ldu[p];
+                    a.lora_v[p] = lora->v_nk[p];
+                }
+            }
             launch_big<EPI_BF16>(variant, grid, a, s);
         }
         return check_launch("gemm");
@@ -605,7 +702,8 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
             k_splitk_reduce<true><<<blocks, 256, 0, s>>>(a.part, splits, M, N, C, ldc, alpha,
                                                          beta, bias);
     }
-    return check_launch("gemm");
+    int rc = check_launch("gemm");
+    return rc ? rc : lora_after();
 }
 
 // F32 -> BF16 staging for gemm_f32 operands (the LoRA path feeds it values
@@ -634,7 +732,7 @@ int ta_gemm_rm(int x_kmajor, int y_kmajor, int M, int N, int K, float alpha, con
     TA_REQUIRE(M > 0 && N > 0 && K > 0 && ldx > 0 && ldy > 0 && ldc > 0,
                "gemm_rm: M/N/K and leading dims must be > 0");
     return gemm_dispatch(x_kmajor != 0, y_kmajor != 0, M, N, K, alpha, X, ldx, Y, ldy, beta, C,
-                         ldc, bias, false, (hipStream_t)stream, 0);
+                         ldc, bias, false, (hipStream_t)stream, 0, nullptr);
 }
 
 // cuBLAS column-major C(MxN) = alpha op(A) op(B) + beta C  ==  row-major
@@ -645,7 +743,7 @@ int ta_gemm_bf16(int transA, int transB, int M, int N, int K, float alpha, const
     TA_REQUIRE(M > 0 && N > 0 && K > 0, "gemm_bf16: M/N/K must be > 0");
     TA_REQUIRE(lda > 0 && ldb > 0 && ldc > 0, "gemm_bf16: leading dims must be > 0");
     return gemm_dispatch(!transB, transA != 0, N, M, K, alpha, B, ldb, A, lda, beta, C, ldc,
-                         nullptr, false, (hipStream_t)stream, 0);
+                         nullptr, false, (hipStream_t)stream, 0, nullptr);
 }
 
 int ta_gemm_f32(int transA, int transB, int M, int N, int K, float alpha, const float* A, int lda,
@@ -664,7 +762,7 @@ int ta_gemm_f32(int transA, int transB, int M, int N, int K, float alpha, const 
     k_f32_to_bf16_2d<<<1024, 256, 0, s>>>(A, na, a16);
     k_f32_to_bf16_2d<<<1024, 256, 0, s>>>(B, nb, b16);
     return gemm_dispatch(!transB, transA != 0, N, M, K, alpha, b16, ldb, a16, lda, beta, C, ldc,
-                         nullptr, true, s, 0);
+                         nullptr, true, s, 0, nullptr);
 }
 
 }  // extern "C"

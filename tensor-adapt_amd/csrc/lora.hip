@@ -23,11 +23,9 @@
 //
 // All MFMAs are v_mfma_f32_16x16x32_bf16; rank dimensions are zero-padded to
 // multiples of 32 (r = 8, 16) or looped (r = 64).
-#include "ta_common.hpp"
+#include "ta_internal.hpp"
 
 namespace ta {
-
-void* scratch_get(size_t bytes, hipStream_t s, int slot = 0);
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));

@@ -9,11 +9,9 @@
 // RoPE: one thread per (token, 4 consecutive pairs) computes the 4 angles
 // once and rotates that slice of every head of the token, so sincos work is
 // amortised over H heads and the data moves as 16-byte vectors.
-#include "ta_common.hpp"
+#include "ta_internal.hpp"
 
 namespace ta {
-
-void* scratch_get(size_t bytes, hipStream_t s, int slot = 0);
 
 constexpr int kMaxChunks = 8;  // 8 chunks x 8 elems x 64 lanes = D <= 4096 in registers
 

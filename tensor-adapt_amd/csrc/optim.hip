@@ -10,11 +10,9 @@
 //   2. k_adamw_fused: every block re-reduces the partials in the same order
 //      (so all blocks agree on the norm bit for bit), derives the clip
 //      factor, and applies AdamW (ops.cu:1139-1158) to its elements.
-#include "ta_common.hpp"
+#include "ta_internal.hpp"
 
 namespace ta {
-
-void* scratch_get(size_t bytes, hipStream_t s, int slot = 0);
 
 constexpr int kNormBlocks = 1024;
 

@@ -1,0 +1,50 @@
+// ta_internal.hpp — launchers shared between the backend's translation units
+// (not part of the C-ABI).
+#pragma once
+#include "ta_common.hpp"
+
+namespace ta {
+
+void* scratch_get(size_t bytes, hipStream_t s, int slot = 0);
+
+// LoRA terms for gemm_dispatch.  After the base epilogue, for each pair p
+// in order, with D_p = U_p V_p^T (U_p [M x r], V_p [N x r]):
+//   delta: C = bf16(C + s * bf16(D_p))   (apply_lora_fwd's add)
+//   else : C = bf16(s * D_p + C)         (apply_lora_bwd's dx GEMM, beta 1)
+// v_nk: V_p as [N x r] rows (B for the delta, A^T for the dx update);
+// v_alt: the same operand in k_rank_update's layout (B [N x r] / A [r x N]).
+struct LoraEpi {
+    int n, r;
+    bool delta;
+    float s;
+    const bf16* u[3];
+    int64_t ldu[3];
+    const bf16* v_nk[3];
+    const bf16* v_alt[3];
+};
+
+int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16* X, int64_t ldx,
+                  const bf16* Y, int64_t ldy, float beta, void* C, int64_t ldc, const bf16* bias,
+                  bool out_f32, hipStream_t s, int force_splits, const LoraEpi* lora);
+int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* P, int B, int T, int Hq,
+             int Hkv, int hd, bool zero_fill, hipStream_t s);
+int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const float* P,
+             bf16* dQ, bf16* dK, bf16* dV, int B, int T, int Hq, int Hkv, int hd, float* Dbuf,
+             float* part, hipStream_t s);
+int transpose_bf16(const bf16* in, bf16* out, int64_t rows, int64_t cols, hipStream_t s);
+int fill_normal_bf16(bf16* out, int64_t n, uint64_t seed, uint64_t sid, float std, hipStream_t s);
+int fill_bf16(bf16* out, int64_t n, float v, hipStream_t s);
+int kaiming_init(float* a32, bf16* a16, int64_t n, int in_dim, hipStream_t s);
+int add2_bf16(bf16* out, const bf16* a, const bf16* b, int64_t n, hipStream_t s);
+int mask_targets_dev(const int32_t* in, const int32_t* tgt_in, int32_t* tgt, int B, int T,
+                     hipStream_t s);
+int lora_skinny_nt(const bf16* X, int64_t ldx, int M, int K, int r, const bf16* const* Y,
+                   bf16* const* C, int64_t ldc, int n, hipStream_t s);
+int lora_rank_update(bool delta, bf16* Y, int64_t ldy, int M, int N, int r, float scale,
+                     const bf16* const* U, const int64_t* ldu, const bf16* const* V, int n,
+                     hipStream_t s);
+int lora_wgrad(const bf16* L, int64_t ldl, int NL, const bf16* Sm, int64_t lds, int NS, int T,
+               int r, float scale, bool trans, float* const* G, hipStream_t s);
+int transpose_batch(const bf16* src, bf16* dst, const void* descs, int nd, hipStream_t s);
+
+}  // namespace ta
