@@ -11,10 +11,12 @@ backward, centroid accumulation, grad norm/clip, AdamW) with the batch
 already resident in HBM.
 
 Prints one JSON line.  Besides tokens/s it carries:
-  roofline     — the kernel class with the largest share of step time,
-                 timed with HIP events on the engine's stream during the
-                 timed steps: algorithmic flops (or bytes) / measured time,
-                 against MI355X peak (2.5 PFLOP/s dense BF16, 8 TB/s HBM).
+  roofline     — the instrumented kernel with the largest share of step
+                 time, every launch of it timed with HIP events on its launch
+                 stream during the timed steps: algorithmic flops (or bytes)
+                 per launch / average launch time, against MI355X peak
+                 (2.5 PFLOP/s dense BF16, 8 TB/s HBM); the bound is the
+                 resource whose peak gives the longer time for that work.
   cpu_baseline — the CPU restatement of the reference step (oracle/, a
                  port: the reference has no CPU path) on this host's cores,
                  on a bounded sample, extrapolated to the c3 model.
@@ -36,7 +38,6 @@ C3_B, C3_T = 8, 1024
 
 CAT_NAMES = ["gemm_fwd", "gemm_dx", "lm_head", "lora", "attn_fwd", "attn_bwd", "norm",
              "elementwise", "cross_entropy", "adamw_tail", "centroid"]
-MFMA_CATS = {0, 1, 2, 3, 4, 5}
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 
@@ -59,6 +60,23 @@ def token_batches(n, B, T, V, seed):
             pos += T
         out.append((inp, tgt))
     return out
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` measured with rocprofv3 --pmc
+    (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy's counters), as recorded
+    in the traffic table under profiles/; None when no row names it."""
+    path = os.path.join(ROOT, "profiles", "c3_traffic.md")
+    if not kernel or not os.path.exists(path):
+        return None
+    for line in open(path):
+        cells = [c.strip().strip("`") for c in line.split("|")]
+        if len(cells) > 3 and cells[1] == kernel:
+            try:
+                return int(float(cells[-2]))
+            except ValueError:
+                return None
+    return None
 
 
 def cpu_baseline(model, adapt):
@@ -117,6 +135,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--categories", action="store_true",
                     help="print the per-kernel-class time split to stderr")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="run one plain device copy of MIB MiB first (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU (one process, one MI355X); "
@@ -129,27 +149,44 @@ def main():
     model, adapt, B, T = C3_MODEL, C3_ADAPT, C3_B, C3_T
     eng = tadapt.Engine(model, adapt, B, T)
     eng.init_random(seed=20261201, std=0.02)
-    batches = token_batches(args.warmup + args.steps + len(CAT_NAMES), B, T, model["vocab"], 1)
+    nb = args.warmup + args.steps + len(CAT_NAMES) + len(tadapt.KPROF_KERNELS)
+    batches = token_batches(nb, B, T, model["vocab"], 1)
     dev = [(torch.from_numpy(i).cuda(), torch.from_numpy(t).cuda()) for i, t in batches]
     it = iter(dev)
 
+    if args.copy_calibration:
+        # a plain device copy of known size, for scaling the HBM byte
+        # counters of a --pmc run (FETCH_SIZE / WRITE_SIZE of this kernel
+        # against exactly copy_calibration MiB read and written)
+        n = args.copy_calibration << 19
+        src = torch.ones(n, dtype=torch.bfloat16, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     for _ in range(args.warmup):
         eng.step_resident(*next(it))
-    # survey: one step per kernel class with that class timed, to find the
-    # class that dominates the step (not part of the timed region)
-    split = {}
-    for c in range(len(CAT_NAMES)):
-        eng.profile(c)
-        eng.step_resident(*next(it))
-        split[c] = eng.profile_read()
-    eng.profile(-1)
-    dom = max(split, key=lambda c: split[c]["ms"])
     if args.categories:
-        for c, v in split.items():
+        # one step per kernel class with that class timed (not timed region)
+        for c in range(len(CAT_NAMES)):
+            eng.profile(c)
+            eng.step_resident(*next(it))
+            v = eng.profile_read()
             print(f"  {CAT_NAMES[c]:14s} {v['ms']:8.2f} ms  {v['launches']:5d} launches", file=sys.stderr)
+        eng.profile(-1)
+    # survey: one step per instrumented kernel, to find the kernel with the
+    # largest share of the step (not part of the timed region)
+    split = {}
+    for k in range(len(tadapt.KPROF_KERNELS)):
+        tadapt.kprof_select(k)
+        eng.step_resident(*next(it))
+        split[k] = tadapt.kprof_read()
+    tadapt.kprof_select(-1)
+    dom = max(split, key=lambda k: split[k]["ms"])
 
-    # timed region: the dominant class is event-timed on the engine's stream
-    eng.profile(dom)
+    # timed region; the dominant kernel is event-timed on its launch stream
+    tadapt.kprof_select(dom)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     last = None
@@ -157,23 +194,31 @@ def main():
         last = eng.step_resident(*next(it))
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    prof = eng.profile_read()
-    eng.profile(-1)
+    prof = tadapt.kprof_read()
+    tadapt.kprof_select(-1)
 
     tokens = B * T * args.steps
     value = tokens / dt
-    if dom in MFMA_CATS:
-        achieved = prof["flops"] / (prof["ms"] * 1e-3) / 1e12
+    sec = prof["ms"] * 1e-3
+    t_mfma = prof["flops"] / (PEAK_BF16_TFLOPS * 1e12)
+    t_hbm = prof["bytes"] / (PEAK_HBM_GBS * 1e9)
+    if t_mfma >= t_hbm:
+        achieved = prof["flops"] / sec / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4)}
     else:
-        achieved = prof["bytes"] / (prof["ms"] * 1e-3) / 1e9
+        achieved = prof["bytes"] / sec / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                 "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4)}
-    roof["traffic"] = None
-    roof["kernel"] = CAT_NAMES[dom]
-    roof["share_of_step"] = round(prof["ms"] / (dt * 1e3), 4)
+    name = tadapt.kprof_name(dom)
+    roof["traffic"] = measured_traffic(name)
+    roof["kernel"] = name
     roof["launches"] = prof["launches"]
+    roof["avg_launch_us"] = round(prof["ms"] * 1e3 / max(prof["launches"], 1), 1)
+    roof["algorithmic_per_launch"] = {
+        "flops": round(prof["flops"] / max(prof["launches"], 1)),
+        "bytes": round(prof["bytes"] / max(prof["launches"], 1))}
+    roof["share_of_step"] = round(sec / dt, 4)
 
     out = {
         "metric": "train tokens/s Qwen2-1.5B LoRA r=16 seq1024; bwd MFMA util %, HBM GB/s",

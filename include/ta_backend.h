@@ -180,6 +180,18 @@ int ta_kmeans_pp(const float* snaps, const float* weights, int N, int D, int k, 
                  uint64_t seed, float* centers, int32_t* assign, double* mass,
                  int32_t* seeds, void* stream);
 
+/* ── kernel-level timing (measurement; no reference counterpart) ─────
+ * ta_kprof_select(kid) starts timing every launch of one kernel (ids: 0 the
+ * large K-contiguous GEMM, 1 its wide-N tile shape, 2 attention forward,
+ * 3 attention backward dQ pass, 4 attention backward dK/dV pass; -1 stops)
+ * with events recorded on the launch's own stream.  ta_kprof_read waits for
+ * the recorded launches and returns their summed time, count, algorithmic
+ * flops and HBM bytes, then clears them; ta_kprof_name gives the timed
+ * kernel's symbol as a profiler prints it ("" before its first launch). */
+int ta_kprof_select(int kid);
+int ta_kprof_read(double* ms, int64_t* launches, double* flops, double* bytes);
+const char* ta_kprof_name(int kid);
+
 #ifdef __cplusplus
 }
 #endif

@@ -535,10 +535,20 @@ int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* P, int
     int nqt = (T + TQ - 1) / TQ;
     int64_t blocks = (int64_t)B * Hq * nqt;
     float scale = 1.f / sqrtf((float)hd);
+    const bool timed = kprof_begin(KP_ATTN_FWD, s);
     if (hd == 64)
         k_attn_fwd<64><<<(int)blocks, 256, 0, s>>>(Q, K, V, O, P, T, Hq, Hkv, scale, zero_fill);
     else
         k_attn_fwd<128><<<(int)blocks, 256, 0, s>>>(Q, K, V, O, P, T, Hq, Hkv, scale, zero_fill);
+    if (timed) {
+        // causal S = QK^T and O = PV; Q, K, V read, O written, P written
+        // (causal half, or all of it when the upper triangle is zero-filled)
+        double tri = (double)B * Hq * T * (T + 1) / 2.0, bt = (double)B * T;
+        double pbytes = zero_fill ? 4.0 * B * Hq * (double)T * T : 4.0 * tri;
+        kprof_end(KP_ATTN_FWD, s, 4.0 * hd * tri,
+                  2.0 * bt * hd * (2.0 * Hq + 2.0 * Hkv) + pbytes,
+                  hd == 64 ? "void ta::k_attn_fwd<64>" : "void ta::k_attn_fwd<128>");
+    }
     return check_launch("sdpa_fwd");
 }
 
@@ -563,13 +573,29 @@ int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const 
     int nqt = (T + TQ - 1) / TQ;
     float scale = 1.f / sqrtf((float)hd);
     int64_t b1 = (int64_t)B * Hq * nqt;
-    if (hd == 64) {
+    // algorithmic work (causal half): dq pass dP = dO V^T, dQ = dS K; dkv
+    // pass dP again, dV = P^T dO, dK = dS^T Q.  Bytes: BF16 operands and P
+    // read once, outputs written once (dq: dQ + row dots; dkv: F32 partials)
+    const double tri = (double)B * Hq * T * (T + 1) / 2.0, bt = (double)B * T;
+    bool timed = kprof_begin(KP_ATTN_BWD_DQ, s);
+    if (hd == 64)
         k_attn_bwd_dq<64><<<(int)b1, 256, 0, s>>>(dO, K, V, P, dQ, Dbuf, T, Hq, Hkv, scale);
-        k_attn_bwd_dkv<64><<<(int)b1, 256, 0, s>>>(dO, Q, V, P, Dbuf, part, T, Hq, Hkv);
-    } else {
+    else
         k_attn_bwd_dq<128><<<(int)b1, 256, 0, s>>>(dO, K, V, P, dQ, Dbuf, T, Hq, Hkv, scale);
+    if (timed)
+        kprof_end(KP_ATTN_BWD_DQ, s, 4.0 * hd * tri,
+                  4.0 * tri + 2.0 * bt * hd * (2.0 * Hq + 2.0 * Hkv) + 4.0 * bt * Hq,
+                  hd == 64 ? "void ta::k_attn_bwd_dq<64>" : "void ta::k_attn_bwd_dq<128>");
+    timed = kprof_begin(KP_ATTN_BWD_DKV, s);
+    if (hd == 64)
+        k_attn_bwd_dkv<64><<<(int)b1, 256, 0, s>>>(dO, Q, V, P, Dbuf, part, T, Hq, Hkv);
+    else
         k_attn_bwd_dkv<128><<<(int)b1, 256, 0, s>>>(dO, Q, V, P, Dbuf, part, T, Hq, Hkv);
-    }
+    if (timed)
+        kprof_end(KP_ATTN_BWD_DKV, s, 6.0 * hd * tri,
+                  4.0 * tri + 2.0 * bt * hd * (2.0 * Hq + Hkv) + 4.0 * bt * Hq +
+                      8.0 * bt * Hq * hd,
+                  hd == 64 ? "void ta::k_attn_bwd_dkv<64>" : "void ta::k_attn_bwd_dkv<128>");
     int64_t n = (int64_t)B * T * Hkv * hd;
     int rb = (int)std::min<int64_t>((n + 255) / 256, 4096);
     k_attn_dkv_reduce<<<rb, 256, 0, s>>>(part, dK, dV, B, T, Hq, Hkv, hd, scale);

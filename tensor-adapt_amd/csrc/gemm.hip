@@ -488,6 +488,19 @@ static int big_bn(int variant) {
     return (variant == 1 || variant == 3) ? 128 : ((variant == 4 || variant == 5) ? 256 : 192);
 }
 
+// symbol of the unsplit BF16-output instance of each variant, as printed
+// by the profiler
+static const char* big_name(int variant) {
+    switch (variant) {
+        case 1: return "void ta::k_gemm_big<128, 2, 2, 0, 1>(ta::GemmArgs)";
+        case 2: return "void ta::k_gemm_big<192, 2, 2, 0, 1>(ta::GemmArgs)";
+        case 3: return "void ta::k_gemm_big<128, 4, 2, 0, 2>(ta::GemmArgs)";
+        case 4: return "void ta::k_gemm_big<256, 4, 2, 0, 1>(ta::GemmArgs)";
+        case 5: return "void ta::k_gemm_big<256, 2, 4, 0, 1>(ta::GemmArgs)";
+        default: return "void ta::k_gemm_big<192, 4, 2, 0, 1>(ta::GemmArgs)";
+    }
+}
+
 template <int EPI>
 static void launch_big(int variant, dim3 grid, const GemmArgs& a, hipStream_t s) {
     switch (variant) {
@@ -627,7 +640,19 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
                     a.lora_v[p] = lora->v_nk[p];
                 }
             }
+            // measurement hook: algorithmic work of the launch (MNK product,
+            // rank-r epilogue products; operands read once, C written once and
+            // read once more when beta != 0)
+            const int kid = BNb == 256 ? KP_GEMM_BIG_WIDE : KP_GEMM_BIG;
+            const bool timed = kprof_begin(kid, s);
             launch_big<EPI_BF16>(variant, grid, a, s);
+            if (timed) {
+                double mn = (double)M * N;
+                double fl = 2.0 * mn * K + 2.0 * mn * a.lora_r * a.lora_n;
+                double by = 2.0 * ((double)M * K + (double)N * K + mn * (beta != 0.f ? 2 : 1)) +
+                            2.0 * a.lora_n * (double)(M + N) * a.lora_r;
+                kprof_end(kid, s, fl, by, big_name(variant));
+            }
         }
         return check_launch("gemm");
     }

@@ -7,6 +7,20 @@ namespace ta {
 
 void* scratch_get(size_t bytes, hipStream_t s, int slot = 0);
 
+// Kernel ids of the kernel-level timer (ta_kprof_select).
+enum KernelId {
+    KP_GEMM_BIG = 0,       // large K-contiguous GEMM, N <= 3072 tile shape
+    KP_GEMM_BIG_WIDE = 1,  // large K-contiguous GEMM, N > 3072 tile shape
+    KP_ATTN_FWD = 2,
+    KP_ATTN_BWD_DQ = 3,
+    KP_ATTN_BWD_DKV = 4,
+    KP_COUNT = 5
+};
+// Bracket one launch of kernel `kid` on stream s when that kernel is being
+// timed; name is the kernel's symbol as a profiler prints it.
+bool kprof_begin(int kid, hipStream_t s);
+void kprof_end(int kid, hipStream_t s, double flops, double bytes, const char* name);
+
 // LoRA terms for gemm_dispatch.  After the base epilogue, for each pair p
 // in order, with D_p = U_p V_p^T (U_p [M x r], V_p [N x r]):
 //   delta: C = bf16(C + s * bf16(D_p))   (apply_lora_fwd's add)

@@ -112,6 +112,26 @@ def stream():
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
 
 
+# ── kernel-level timer (ta_kprof_*) ─────────────────────────────────────
+KPROF_KERNELS = ["gemm_big", "gemm_big_wide", "attn_fwd", "attn_bwd_dq", "attn_bwd_dkv"]
+
+
+def kprof_select(kid):
+    """Time every launch of kernel `kid` (index into KPROF_KERNELS, -1 off)."""
+    call("ta_kprof_select", kid)
+
+
+def kprof_read():
+    ms, n = ctypes.c_double(), ctypes.c_int64()
+    fl, by = ctypes.c_double(), ctypes.c_double()
+    call("ta_kprof_read", ctypes.byref(ms), ctypes.byref(n), ctypes.byref(fl), ctypes.byref(by))
+    return {"ms": ms.value, "launches": n.value, "flops": fl.value, "bytes": by.value}
+
+
+def kprof_name(kid):
+    return lib().ta_kprof_name(kid).decode()
+
+
 # ── step engine (include/ta_engine.h) ─────────────────────────────────────
 class ModelConfig(ctypes.Structure):
     _fields_ = [("vocab", ctypes.c_int), ("hidden", ctypes.c_int), ("layers", ctypes.c_int),

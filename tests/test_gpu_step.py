@@ -10,6 +10,7 @@ import pytest
 
 import oracle as O
 import tadapt
+from step_util import chat_tokens, make_pair, pairs, rel
 
 pytestmark = pytest.mark.gpu
 
@@ -21,71 +22,6 @@ SMALL_MODEL = dict(vocab=2048, hidden=256, layers=2, n_q=4, n_kv=2, head_dim=64,
                    rms_eps=1e-6, rope_theta=1e6, tie=1)
 SMALL_ADAPT = dict(rank=16, alpha=32.0, inject_mask=0b1111111, lr=1e-3, grad_clip=1.0, warmup=1,
                    total_steps=4, b1=0.9, b2=0.999, eps=1e-8, wd=0.01)
-
-
-def base_tensors(mc, seed):
-    """HF-named synthetic Qwen2 base: N(0, 0.02) weights, unit norms, zero biases."""
-    rng = np.random.default_rng(seed)
-    H, I, V = mc["hidden"], mc["inter"], mc["vocab"]
-    qd, kvd = mc["n_q"] * mc["head_dim"], mc["n_kv"] * mc["head_dim"]
-
-    def w(*shape):
-        return O.bf16_from_f32((rng.standard_normal(shape) * 0.02).astype(np.float32))
-
-    one = lambda n: O.bf16_from_f32(np.ones(n, np.float32))
-    zero = lambda n: np.zeros(n, np.uint16)
-    t = {"model.embed_tokens.weight": w(V, H), "model.norm.weight": one(H)}
-    for l in range(mc["layers"]):
-        p = f"model.layers.{l}."
-        t[p + "input_layernorm.weight"] = one(H)
-        t[p + "post_attention_layernorm.weight"] = one(H)
-        t[p + "self_attn.q_proj.weight"] = w(qd, H)
-        t[p + "self_attn.q_proj.bias"] = zero(qd)
-        t[p + "self_attn.k_proj.weight"] = w(kvd, H)
-        t[p + "self_attn.k_proj.bias"] = zero(kvd)
-        t[p + "self_attn.v_proj.weight"] = w(kvd, H)
-        t[p + "self_attn.v_proj.bias"] = zero(kvd)
-        t[p + "self_attn.o_proj.weight"] = w(H, qd)
-        t[p + "mlp.gate_proj.weight"] = w(I, H)
-        t[p + "mlp.up_proj.weight"] = w(I, H)
-        t[p + "mlp.down_proj.weight"] = w(H, I)
-    return t
-
-
-def make_pair(mc, ac, B, T, seed):
-    tensors = base_tensors(mc, seed)
-    orc = O.OracleModel(mc, ac)
-    eng = tadapt.Engine(mc, ac, B, T)
-    for name, arr in tensors.items():
-        orc.set_weight(name, arr)
-        eng.set_weight(name, arr)
-    return orc, eng
-
-
-def chat_tokens(V, B, T, rng):
-    """uniform ids with a few assistant spans (<|im_start|> assistant ... <|im_end|>)
-    so that some targets survive the trainer's masking."""
-    toks = rng.integers(0, min(V, 150000), B * T).astype(np.int32)
-    if V > 151645:
-        for b in range(B):
-            s = b * T + 5
-            toks[s], toks[s + 1] = 151644, 77091
-            toks[s + 12] = 151645
-    return toks
-
-
-def rel(a, b):
-    a = np.asarray(a, np.float64).ravel()
-    b = np.asarray(b, np.float64).ravel()
-    nb = np.linalg.norm(b)
-    return float(np.linalg.norm(a - b) / nb) if nb > 0 else float(np.linalg.norm(a))
-
-
-def pairs(mc, ac):
-    for l in range(mc["layers"]):
-        for ti, t in enumerate(tadapt.TARGETS):
-            if (ac["inject_mask"] >> ti) & 1:
-                yield l, t
 
 
 def compare(orc, eng, mc, ac, what, bar=1e-2):
