@@ -159,6 +159,10 @@ int ta_gemm_variant(int variant);
  * F64 vector of D+1 entries, accumulated in a fixed order. */
 int ta_centroid_accumulate_bf16(const uint16_t* h, const uint16_t* g, int64_t BT, int D,
                                 double* acc, void* stream);
+/* Same with F32 h and g (the dtype the reference trainer hands over,
+ * adapt_trainer.cu:215-231). */
+int ta_centroid_accumulate_f32(const float* h, const float* g, int64_t BT, int D, double* acc,
+                               void* stream);
 /* Same with F32 h and given per-token norms n (the stress configuration). */
 int ta_centroid_accumulate_f32n(const float* h, const float* n, int64_t BT, int D,
                                 double* acc, void* stream);
@@ -179,6 +183,18 @@ int ta_kmeans_ref(const float* snaps, int N, int D, int k, int max_iters, float*
 int ta_kmeans_pp(const float* snaps, const float* weights, int N, int D, int k, int iters,
                  uint64_t seed, float* centers, int32_t* assign, double* mass,
                  int32_t* seeds, void* stream);
+
+/* ── device memory (the host API's Tensor storage) ───────────────────
+ * Caching allocator replacing the reference's one cudaMalloc/cudaFree per
+ * Tensor (src/backend/cuda/tensor.cu:18-27,115-122).  Blocks are rounded to
+ * a size class and recycled per device; ta_mem_free returns a block to the
+ * cache (no hipFree), so it must only be called once the work using the
+ * block has been enqueued on the stream that later users of the cache are
+ * ordered on.  ta_mem_trim synchronises the device and releases the cache. */
+int ta_mem_alloc(void** ptr, int64_t bytes, int device);
+int ta_mem_free(void* ptr, int device);
+int ta_mem_stats(int device, int64_t* in_use, int64_t* cached);
+int ta_mem_trim(int device);
 
 /* ── kernel-level timing (measurement; no reference counterpart) ─────
  * ta_kprof_select(kid) starts timing every launch of one kernel (ids: 0 the

@@ -128,6 +128,11 @@ int ta_engine_read_buffer(void* engine, const char* name, void* host_dst, int64_
  * with events on the engine's stream. */
 int ta_engine_phase_ms(void* engine, float* fwd_ms, float* bwd_ms, float* tail_ms);
 
+/* The step's learning rate: CosineSchedule::lr_at
+ * (include/tensor/trainer/cosine_schedule.hpp:18-29) for the 0-based step,
+ * as the engine applies it (adapt_trainer.cu:252).  Host only. */
+float ta_cosine_lr(float base_lr, int64_t warmup, int64_t total, float floor_frac, int64_t step);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,9 +1,11 @@
 """Builds the gfx950 backend library in-tree: tensor-adapt_amd/libtadapt.so.
 
 Every .hip under csrc/ is compiled with hipcc for gfx950 only (no other
-targets, no CUDA path) in parallel, then linked into one shared library whose
-exported symbols are the C-ABI of include/ta_backend.h (and the step engine's
-ta_engine_* entry points).  Object files go to csrc/_build/ (git-ignored).
+targets, no CUDA path) and every .cpp (host-only C++: the C++ host API over
+the C-ABI) with the host compiler, in parallel, then linked into one shared
+library whose exported symbols are the C-ABI of include/ta_backend.h and
+include/ta_engine.h plus the C++ API of include/tensor/.  Object files go to
+csrc/_build/ (git-ignored).
 """
 import concurrent.futures as cf
 import os
@@ -24,13 +26,23 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-Wall",
          "-I" + CSRC, "-I" + INCLUDE]
 
 
+CXX = os.environ.get("CXX", "g++")
+CXXFLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-D__HIP_PLATFORM_AMD__",
+            "-I/opt/rocm/include", "-I" + CSRC, "-I" + INCLUDE]
+
+
 def sources():
-    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC)
+                  if f.endswith(".hip") or f.endswith(".cpp"))
 
 
 def _compile(src):
-    obj = os.path.join(BUILD, os.path.basename(src)[:-4] + ".o")
-    cmd = [HIPCC] + FLAGS + ["-c", src, "-o", obj]
+    base, ext = os.path.splitext(os.path.basename(src))
+    obj = os.path.join(BUILD, base + (".o" if ext == ".hip" else ".cpp.o"))
+    if ext == ".hip":
+        cmd = [HIPCC] + FLAGS + ["-c", src, "-o", obj]
+    else:
+        cmd = [CXX] + CXXFLAGS + ["-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     # the host pass warns that it does not know the packed-fp32 feature: harmless
     err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)

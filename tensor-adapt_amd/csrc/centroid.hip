@@ -297,7 +297,7 @@ static int centroid_acc(const void* h, const void* g, const float* n, int64_t BT
     if (bf16in)
         k_centroid_part<true><<<(int)nblk, 256, 0, s>>>(h, g, nullptr, BT, D, part);
     else
-        k_centroid_part<false><<<(int)nblk, 256, 0, s>>>(h, nullptr, n, BT, D, part);
+        k_centroid_part<false><<<(int)nblk, 256, 0, s>>>(h, g, n, BT, D, part);
     k_centroid_reduce<<<(D + 1 + 255) / 256, 256, 0, s>>>(part, (int)nblk, D + 1, acc);
     return check_launch("centroid_accumulate");
 }
@@ -307,6 +307,12 @@ extern "C" {
 int ta_centroid_accumulate_bf16(const uint16_t* h, const uint16_t* g, int64_t BT, int D,
                                 double* acc, void* stream) {
     return centroid_acc(h, g, nullptr, BT, D, acc, true, stream);
+}
+
+int ta_centroid_accumulate_f32(const float* h, const float* g, int64_t BT, int D, double* acc,
+                               void* stream) {
+    TA_REQUIRE(h && g && acc, "centroid_accumulate_f32: null argument");
+    return centroid_acc(h, g, nullptr, BT, D, acc, false, stream);
 }
 
 int ta_centroid_accumulate_f32n(const float* h, const float* n, int64_t BT, int D, double* acc,

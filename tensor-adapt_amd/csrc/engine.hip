@@ -26,6 +26,7 @@
 #include "ta_backend.h"
 #include "ta_engine.h"
 #include "ta_internal.hpp"
+#include <tensor/trainer/cosine_schedule.hpp>
 
 namespace ta {
 
@@ -419,14 +420,10 @@ static void mask_targets(const int32_t* in, int32_t* tgt, int B, int T) {
     }
 }
 
-// CosineSchedule::lr_at — include/tensor/trainer/cosine_schedule.hpp:18-29
+// CosineSchedule::lr_at (include/tensor/trainer/cosine_schedule.hpp:18-29)
 static float cosine_lr(float base, int64_t warmup, int64_t total, float floor_frac, int64_t step) {
-    if (step < warmup) return base * (float)(step + 1) / (float)warmup;
-    float progress = (float)(step - warmup) / (float)(total - warmup);
-    progress = std::min(progress, 1.f);
-    float cos_val = 0.5f * (1.f + std::cos((float)M_PI * progress));
-    float floor = base * floor_frac;
-    return floor + (base - floor) * cos_val;
+    tensor::trainer::CosineSchedule cs{base, (size_t)warmup, (size_t)total, floor_frac};
+    return cs.lr_at((size_t)step);
 }
 
 static int forward(Engine* e) {
@@ -935,3 +932,8 @@ int ta_engine_phase_ms(void* ep, float* f, float* b, float* t) {
 }
 
 }  // extern "C"
+
+extern "C" float ta_cosine_lr(float base_lr, int64_t warmup, int64_t total, float floor_frac,
+                              int64_t step) {
+    return cosine_lr(base_lr, warmup, total, floor_frac, step);
+}

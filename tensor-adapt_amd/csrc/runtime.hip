@@ -10,8 +10,10 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <map>
 #include <mutex>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 #include "ta_internal.hpp"
@@ -69,6 +71,29 @@ void* scratch_get(size_t bytes, hipStream_t s, int slot) {
     }
     sc.bytes = want;
     return sc.ptr;
+}
+
+// Caching allocator behind the host API's Tensor (ta_mem_alloc/free).
+// Sizes round up to a power of two below 2 MiB and to a multiple of 2 MiB
+// above; a freed block goes back to its device's bin and is handed out again
+// without hipFree/hipMalloc.  Reuse is ordered by the device's one stream:
+// the caller frees a block only after the work that reads it is enqueued on
+// that stream (what the Tensor destructor does).
+struct MemPool {
+    std::map<size_t, std::vector<void*>> bins;  // size class -> free blocks
+    std::unordered_map<void*, size_t> live;     // block -> size class
+    size_t cached = 0, in_use = 0;
+};
+static std::mutex g_mem_mu;
+static MemPool g_mem[64];
+
+static size_t mem_class(size_t bytes) {
+    const size_t two_mib = (size_t)2 << 20;
+    if (bytes <= 256) return 256;
+    if (bytes >= two_mib) return (bytes + two_mib - 1) / two_mib * two_mib;
+    size_t c = 512;
+    while (c < bytes) c <<= 1;
+    return c;
 }
 
 // Kernel-level timing (measurement only).  When kernel id `sel` is
@@ -141,6 +166,79 @@ int ta_kprof_read(double* ms, int64_t* launches, double* flops, double* bytes) {
     if (flops) *flops = tf;
     if (bytes) *bytes = tb;
     ta::g_kp.used = 0;
+    return 0;
+}
+
+int ta_mem_alloc(void** ptr, int64_t bytes, int device) {
+    TA_REQUIRE(ptr && bytes >= 0 && device >= 0 && device < 64, "mem_alloc: bad argument");
+    *ptr = nullptr;
+    if (bytes == 0) return 0;
+    TA_HIP(hipSetDevice(device));
+    size_t c = ta::mem_class((size_t)bytes);
+    std::lock_guard<std::mutex> lk(ta::g_mem_mu);
+    ta::MemPool& mp = ta::g_mem[device];
+    auto it = mp.bins.find(c);
+    if (it != mp.bins.end() && !it->second.empty()) {
+        *ptr = it->second.back();
+        it->second.pop_back();
+        mp.cached -= c;
+    } else {
+        hipError_t e = hipMalloc(ptr, c);
+        if (e != hipSuccess) {
+            // give the cached blocks back and try once more
+            (void)hipDeviceSynchronize();
+            for (auto& kv : mp.bins)
+                for (void* q : kv.second) (void)hipFree(q);
+            mp.bins.clear();
+            mp.cached = 0;
+            (void)hipGetLastError();
+            e = hipMalloc(ptr, c);
+        }
+        if (e != hipSuccess) {
+            *ptr = nullptr;
+            return ta::set_error(-2, "mem_alloc: %lld bytes on device %d: %s", (long long)bytes,
+                                 device, hipGetErrorString(e));
+        }
+    }
+    mp.live[*ptr] = c;
+    mp.in_use += c;
+    return 0;
+}
+
+int ta_mem_free(void* ptr, int device) {
+    if (!ptr) return 0;
+    TA_REQUIRE(device >= 0 && device < 64, "mem_free: bad device %d", device);
+    std::lock_guard<std::mutex> lk(ta::g_mem_mu);
+    ta::MemPool& mp = ta::g_mem[device];
+    auto it = mp.live.find(ptr);
+    TA_REQUIRE(it != mp.live.end(), "mem_free: %p was not allocated by ta_mem_alloc on device %d",
+               ptr, device);
+    size_t c = it->second;
+    mp.live.erase(it);
+    mp.in_use -= c;
+    mp.bins[c].push_back(ptr);
+    mp.cached += c;
+    return 0;
+}
+
+int ta_mem_stats(int device, int64_t* in_use, int64_t* cached) {
+    TA_REQUIRE(device >= 0 && device < 64, "mem_stats: bad device %d", device);
+    std::lock_guard<std::mutex> lk(ta::g_mem_mu);
+    if (in_use) *in_use = (int64_t)ta::g_mem[device].in_use;
+    if (cached) *cached = (int64_t)ta::g_mem[device].cached;
+    return 0;
+}
+
+int ta_mem_trim(int device) {
+    TA_REQUIRE(device >= 0 && device < 64, "mem_trim: bad device %d", device);
+    TA_HIP(hipSetDevice(device));
+    TA_HIP(hipDeviceSynchronize());
+    std::lock_guard<std::mutex> lk(ta::g_mem_mu);
+    ta::MemPool& mp = ta::g_mem[device];
+    for (auto& kv : mp.bins)
+        for (void* q : kv.second) (void)hipFree(q);
+    mp.bins.clear();
+    mp.cached = 0;
     return 0;
 }
 

@@ -1,0 +1,372 @@
+// Tests of the C++ host API (include/tensor/**) as a caller of the
+// reference's interface would use it: Device, Tensor, GEMM, ops::, the
+// Centroid Accumulator (snapshot / merge file formats) and Dataset.
+//
+//   test_host_api cpu <dir>   no device use; writes <dir>/batches.bin and
+//                             <dir>/lr.bin for the Python side to compare
+//                             with the reference's compiled host code
+//   test_host_api gpu <dir>   device paths on hip:0
+// Exit status 0 when every check passed; each failure prints one line.
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <filesystem>
+#include <fstream>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "ta_backend.h"
+#include <tensor/backend/cuda/device.hpp>
+#include <tensor/backend/cuda/ops.hpp>
+#include <tensor/backend/cuda/tensor.hpp>
+#include <tensor/centroid/centroid_accumulator.hpp>
+#include <tensor/centroid/centroid_merge.hpp>
+#include <tensor/core/tensor_view.hpp>
+#include <tensor/data/dataset.hpp>
+#include <tensor/trainer/cosine_schedule.hpp>
+
+namespace fs = std::filesystem;
+using namespace tensor;
+using backend::cuda::CudaError;
+using backend::cuda::Device;
+using backend::cuda::GemmParams;
+using backend::cuda::Tensor;
+using core::DType;
+using core::Shape;
+using core::TensorView;
+namespace ops = backend::cuda::ops;
+
+static int g_fail = 0;
+#define CHECK(cond)                                                            \
+    do {                                                                       \
+        if (!(cond)) {                                                         \
+            std::printf("FAIL %s:%d: %s\n", __FILE__, __LINE__, #cond);        \
+            g_fail++;                                                          \
+        }                                                                      \
+    } while (0)
+
+template <typename E>
+static bool throws(const std::function<void()>& f, const char* prefix = nullptr) {
+    try {
+        f();
+    } catch (const E& e) {
+        return !prefix || std::strncmp(e.what(), prefix, std::strlen(prefix)) == 0;
+    } catch (...) {
+        return false;
+    }
+    return false;
+}
+
+static uint16_t f2bf(float f) {  // round to nearest even
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+static float bf2f(uint16_t b) {
+    uint32_t u = (uint32_t)b << 16;
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+static uint32_t lcg(uint32_t& s) { return s = s * 1664525u + 1013904223u; }
+static float urand(uint32_t& s) { return (float)(lcg(s) >> 8) / 16777216.f * 2.f - 1.f; }
+
+template <typename T>
+static void write_file(const fs::path& p, const std::vector<T>& v) {
+    std::ofstream f(p, std::ios::binary);
+    f.write(reinterpret_cast<const char*>(v.data()), (std::streamsize)(v.size() * sizeof(T)));
+}
+static std::vector<char> read_file(const fs::path& p) {
+    std::ifstream f(p, std::ios::binary);
+    return std::vector<char>(std::istreambuf_iterator<char>(f), {});
+}
+
+static void cpu_tests(const fs::path& dir) {
+    // core types
+    CHECK(core::dtype_size(DType::BF16) == 2 && core::dtype_size(DType::F64) == 8);
+    CHECK(core::to_string(DType::F8_E4M3) == "F8_E4M3");
+    CHECK((Shape{}.numel() == 1 && Shape{3, 4, 5}.numel() == 60 && Shape{3, 0}.numel() == 0));
+    std::vector<float> host(6, 1.f);
+    TensorView tv{host.data(), DType::F32, Shape{2, 3}};
+    CHECK(tv.nbytes() == 24 && tv.as<float>().size() == 6);
+    CHECK(throws<std::invalid_argument>([&] { (void)tv.as<uint16_t>(); }));
+
+    // device spec errors (reference message prefix)
+    CHECK(throws<CudaError>([] { (void)Device::open("gpu:0"); },
+                            "CudaError: invalid device spec"));
+    CHECK(throws<CudaError>([] { (void)Device::open("cuda:x"); },
+                            "CudaError: invalid device index"));
+    CHECK(throws<std::runtime_error>([] { (void)Device::open("hip:-1"); }));
+
+    // Dataset: two files concatenated in name order, wrap-around windows
+    fs::create_directories(dir / "data");
+    std::vector<uint32_t> a(37), b(29);
+    uint32_t s = 7;
+    for (auto& t : a) t = lcg(s) % 151936u;
+    for (auto& t : b) t = lcg(s) % 151936u;
+    write_file(dir / "data" / "b.bin", b);
+    write_file(dir / "data" / "a.bin", a);
+    write_file(dir / "data" / "skip.txt", a);
+    auto ds = data::Dataset::load((dir / "data").string());
+    CHECK(ds.total_tokens() == 66);
+    std::vector<int32_t> out;
+    const int B = 3, T = 10, NB = 5;  // 150 tokens: wraps twice
+    for (int i = 0; i < NB; i++) {
+        auto [in, tg] = ds.next_batch(B, T);
+        CHECK(in.size() == (size_t)B * T && tg.size() == (size_t)B * T);
+        out.insert(out.end(), in.begin(), in.end());
+        out.insert(out.end(), tg.begin(), tg.end());
+    }
+    CHECK(ds.tokens_consumed() == (size_t)NB * B * T);
+    write_file(dir / "batches.bin", out);
+    CHECK(throws<data::DataError>([&] { (void)data::Dataset::load((dir / "missing").string()); },
+                                  "DataError: path not found"));
+    fs::create_directories(dir / "empty");
+    CHECK(throws<data::DataError>([&] { (void)data::Dataset::load((dir / "empty").string()); },
+                                  "DataError: no .bin files"));
+    CHECK(throws<std::runtime_error>(
+        [&] { backend::cuda::Tensor t; (void)t.to_host_f32(); }) == false);  // empty F32: fine
+
+    // learning-rate schedule over a grid, for comparison with the reference
+    std::vector<float> lr;
+    for (int warm : {0, 1, 5, 100})
+        for (int total : {1, 50, 1000})
+            for (int step = 0; step < 60; step++) {
+                if (total <= warm) continue;
+                trainer::CosineSchedule cs{3e-4f, (size_t)warm, (size_t)total};
+                lr.push_back(cs.lr_at((size_t)step));
+            }
+    write_file(dir / "lr.bin", lr);
+
+    // merging an empty directory is an error, as in the reference
+    fs::create_directories(dir / "no_snapshots");
+    CHECK(throws<std::runtime_error>(
+        [&] { centroid::CentroidMerge::run((dir / "no_snapshots").string(), "x", 4); },
+        "No .centroid files"));
+}
+
+static void gpu_tests(const fs::path& dir) {
+    Device dev = Device::open("hip:0");
+    CHECK(dev.supports_bf16_gemm() && dev.sm_major() >= 9);
+    CHECK(dev.arch().rfind("gfx950", 0) == 0);
+    { Device d2 = Device::open("cuda:0"); CHECK(d2.id() == 0); }
+
+    // Tensor round trips and dtype checks
+    std::vector<uint16_t> hb(1000);
+    uint32_t s = 3;
+    for (auto& v : hb) v = f2bf(urand(s));
+    Tensor tb = Tensor::from_host(TensorView{hb.data(), DType::BF16, Shape{10, 100}}, dev);
+    CHECK(tb.to_host_bf16() == hb);
+    CHECK(throws<std::runtime_error>([&] { (void)tb.to_host_f32(); }));
+    Tensor tz = Tensor::zeros_f32(Shape{257}, dev);
+    auto z = tz.to_host_f32();
+    CHECK(z.size() == 257 && std::all_of(z.begin(), z.end(), [](float x) { return x == 0.f; }));
+    std::vector<int32_t> hi = {5, -1, 151645, 0};
+    Tensor ti = Tensor::from_host(TensorView{hi.data(), DType::I32, Shape{4}}, dev);
+    auto u = ti.to_host_u32();
+    CHECK(u.size() == 4 && u[0] == 5 && u[1] == 0xffffffffu && u[2] == 151645u);
+    Tensor moved = std::move(tb);
+    CHECK(tb.empty() && !moved.empty() && moved.numel() == 1000);
+
+    // GEMM: column-major semantics vs a double brute force (one BF16 rounding)
+    {
+        const int M = 37, N = 45, K = 96;
+        std::vector<uint16_t> A(M * K), Bm(K * N), C(M * N);
+        for (auto& v : A) v = f2bf(urand(s));
+        for (auto& v : Bm) v = f2bf(urand(s));
+        for (auto& v : C) v = f2bf(urand(s));
+        for (int ta = 0; ta < 2; ta++)
+            for (int tb2 = 0; tb2 < 2; tb2++) {
+                int lda = ta ? K : M, ldb = tb2 ? N : K;
+                Tensor dA = Tensor::from_host(TensorView{A.data(), DType::BF16, Shape{A.size()}}, dev);
+                Tensor dB = Tensor::from_host(TensorView{Bm.data(), DType::BF16, Shape{Bm.size()}}, dev);
+                Tensor dC = Tensor::from_host(TensorView{C.data(), DType::BF16, Shape{C.size()}}, dev);
+                GemmParams p{(bool)ta, (bool)tb2, M, N, K, 0.5f, 1.0f};
+                backend::cuda::gemm_bf16(dev, p, dA.bf16(), lda, dB.bf16(), ldb, dC.bf16(), M);
+                auto got = dC.to_host_bf16();
+                int bad = 0;
+                for (int i = 0; i < M; i++)
+                    for (int j = 0; j < N; j++) {
+                        double acc = 0;
+                        for (int k = 0; k < K; k++) {
+                            float a = bf2f(ta ? A[k + i * lda] : A[i + k * lda]);
+                            float b = bf2f(tb2 ? Bm[j + k * ldb] : Bm[k + j * ldb]);
+                            acc += (double)a * b;
+                        }
+                        double want = 0.5 * acc + bf2f(C[i + j * M]);
+                        double g = bf2f(got[i + j * M]);
+                        if (std::fabs(g - want) > std::fabs(want) * (1.0 / 128) + 1e-6) bad++;
+                    }
+                CHECK(bad == 0);
+            }
+        Tensor dA = Tensor::empty_bf16(Shape{4}, dev);
+        CHECK(throws<CudaError>([&] {
+            backend::cuda::gemm_bf16(dev, GemmParams{false, false, 0, 1, 1}, dA.bf16(), 1,
+                                     dA.bf16(), 1, dA.bf16(), 1);
+        }, "CudaError: gemm_bf16: M/N/K must be > 0"));
+        CHECK(throws<CudaError>([&] {
+            backend::cuda::gemm_bf16(dev, GemmParams{false, false, 1, 1, 1}, dA.bf16(), 0,
+                                     dA.bf16(), 1, dA.bf16(), 1);
+        }, "CudaError: gemm_bf16: leading dims must be > 0"));
+    }
+
+    // ops: RMSNorm of a constant row is w*c/sqrt(c^2+eps); rms_out = inverse RMS
+    {
+        const int D = 1536, rows = 4;
+        std::vector<uint16_t> x(rows * D), w(D, f2bf(1.f));
+        for (int r = 0; r < rows; r++)
+            for (int d = 0; d < D; d++) x[r * D + d] = f2bf(0.25f * (r + 1));
+        Tensor dx = Tensor::from_host(TensorView{x.data(), DType::BF16, Shape{(size_t)rows, (size_t)D}}, dev);
+        Tensor dw = Tensor::from_host(TensorView{w.data(), DType::BF16, Shape{(size_t)D}}, dev);
+        Tensor out = Tensor::empty_bf16(Shape{(size_t)rows, (size_t)D}, dev);
+        Tensor rms = Tensor::empty_f32(Shape{(size_t)rows}, dev);
+        ops::rms_norm_fwd(dx.bf16(), dw.bf16(), out.bf16(), rms.f32(), 1, rows, D, 1e-6f,
+                          dev.stream());
+        auto o = out.to_host_bf16();
+        auto r = rms.to_host_f32();
+        for (int i = 0; i < rows; i++) {
+            double c = 0.25 * (i + 1);
+            CHECK(std::fabs(r[i] - 1.0 / std::sqrt(c * c + 1e-6)) < 1e-5 / c);
+            CHECK(std::fabs(bf2f(o[i * D + 7]) - c / std::sqrt(c * c + 1e-6)) < 4e-3);
+        }
+        CHECK(throws<CudaError>([&] {
+            ops::rms_norm_fwd(dx.bf16(), dw.bf16(), out.bf16(), rms.f32(), 1, rows, -1, 1e-6f,
+                              dev.stream());
+        }));
+    }
+
+    // ops: cross entropy of zero logits is ln V with gradient (1/V - onehot)/N
+    {
+        const int N = 3, V = 151936;
+        Tensor lg = Tensor::zeros(Shape{(size_t)N, (size_t)V}, DType::BF16, dev);
+        std::vector<int32_t> tg = {5, -1, V - 1};
+        Tensor dt = Tensor::from_host(TensorView{tg.data(), DType::I32, Shape{3}}, dev);
+        Tensor loss = Tensor::empty_f32(Shape{(size_t)N}, dev);
+        ops::cross_entropy_fwd(lg.bf16(), dt.i32(), loss.f32(), lg.bf16(), N, V, dev.stream());
+        auto l = loss.to_host_f32();
+        for (int i = 0; i < N; i++) CHECK(std::fabs(l[i] - std::log((double)V)) < 1e-4);
+        auto g = lg.to_host_bf16();
+        CHECK(std::fabs(bf2f(g[5]) - (1.0 / V - 1.0) / N) < 2e-3);
+        CHECK(bf2f(g[(size_t)V + 9]) == bf2f(f2bf((float)(1.0 / V / N))));
+    }
+
+    // Centroid Accumulator: equal gradient norms -> centroid = mean of h;
+    // snapshot and merged files in the reference's byte layout
+    {
+        const int D = 64, BT = 200;
+        fs::path sdir = dir / "snapshots";
+        fs::remove_all(sdir);
+        centroid::CentroidAccumulator acc(D, sdir.string());
+        std::vector<uint16_t> h(BT * D), g(BT * D, 0);
+        std::vector<double> mean(D, 0.0);
+        for (int t = 0; t < BT; t++) {
+            for (int d = 0; d < D; d++) {
+                h[t * D + d] = f2bf(urand(s));
+                mean[d] += bf2f(h[t * D + d]) / BT;
+            }
+            g[t * D + (t % D)] = f2bf((t & 1) ? -2.f : 2.f);  // ||g_t|| = 2
+        }
+        Tensor th = Tensor::from_host(TensorView{h.data(), DType::BF16, Shape{(size_t)BT, (size_t)D}}, dev);
+        Tensor tg = Tensor::from_host(TensorView{g.data(), DType::BF16, Shape{(size_t)BT, (size_t)D}}, dev);
+        acc.write_snapshot(0);  // W == 0: no file
+        CHECK(!fs::exists(sdir / "step-0.centroid"));
+        acc.accumulate(th, tg, dev);
+        Tensor wrong = Tensor::empty_bf16(Shape{(size_t)BT, 32}, dev);
+        acc.accumulate(wrong, wrong, dev);  // other D: ignored
+        acc.write_snapshot(10);
+        auto bytes = read_file(sdir / "step-10.centroid");
+        CHECK(bytes.size() == 4 + 4 * D + 4);
+        int32_t d0;
+        std::memcpy(&d0, bytes.data(), 4);
+        CHECK(d0 == D);
+        std::vector<float> c(D);
+        std::memcpy(c.data(), bytes.data() + 4, 4 * D);
+        float w;
+        std::memcpy(&w, bytes.data() + 4 + 4 * D, 4);
+        CHECK(w == 400.f);
+        double err = 0;
+        for (int d = 0; d < D; d++) err = std::max(err, std::fabs(c[d] - mean[d]));
+        CHECK(err < 1e-6);
+        // F32 inputs take the same path as the BF16 ones
+        std::vector<float> hf(BT * D), gf(BT * D);
+        for (int i = 0; i < BT * D; i++) {
+            hf[i] = bf2f(h[i]);
+            gf[i] = bf2f(g[i]);
+        }
+        Tensor thf = Tensor::from_host(TensorView{hf.data(), DType::F32, Shape{(size_t)BT, (size_t)D}}, dev);
+        Tensor tgf = Tensor::from_host(TensorView{gf.data(), DType::F32, Shape{(size_t)BT, (size_t)D}}, dev);
+        acc.accumulate(thf, tgf, dev);
+        auto sums = acc.sums();
+        CHECK(sums[D] == 800.0);
+        for (int d = 0; d < D; d++) CHECK(std::fabs(sums[d] / 800.0 - mean[d]) < 1e-6);
+        acc.write_snapshot(20);
+        // merge: k = 1 keeps the first snapshot (the first assignment pass
+        // changes nothing, so the loop stops before any update)
+        acc.merge_and_write(1, (dir / "merged1.centroid").string());
+        auto m = read_file(dir / "merged1.centroid");
+        CHECK(m.size() == 8 + 4 * D);
+        int32_t hk[2];
+        std::memcpy(hk, m.data(), 8);
+        CHECK(hk[0] == 1 && hk[1] == D);
+        CHECK(std::memcmp(m.data() + 8, bytes.data() + 4, 4 * D) == 0);
+        // standalone merge over the directory, k clamped to the snapshot count
+        for (int i = 0; i < 4; i++) {
+            std::vector<float> v(D, (i < 2 ? 1.f : 100.f) + 0.01f * i);
+            std::ofstream f(sdir / ("step-" + std::to_string(100 + i) + ".centroid"),
+                            std::ios::binary);
+            int32_t dd = D;
+            float ww = 1.f;
+            f.write((const char*)&dd, 4);
+            f.write((const char*)v.data(), 4 * D);
+            f.write((const char*)&ww, 4);
+        }
+        centroid::CentroidMerge::run(sdir.string(), (dir / "merged.centroid").string(), 9);
+        auto mm = read_file(dir / "merged.centroid");
+        std::memcpy(hk, mm.data(), 8);
+        CHECK(hk[0] == 6 && hk[1] == D && mm.size() == 8 + 4 * 6 * D);
+    }
+
+    // memory: every block is back in the cache once the tensors are gone
+    {
+        int64_t in_use = -1, cached = -1;
+        {
+            Tensor t1 = Tensor::empty_f32(Shape{1 << 20}, dev);
+            ta_mem_stats(0, &in_use, &cached);
+            CHECK(in_use >= (4 << 20));
+        }
+        int64_t in2 = -1, cached2 = -1;
+        ta_mem_stats(0, &in2, &cached2);
+        CHECK(in2 < in_use && cached2 >= (4 << 20));
+        void* p = nullptr;
+        CHECK(ta_mem_free(&p, 0) != 0);  // not ours: rejected
+    }
+    dev.sync();
+}
+
+int main(int argc, char** argv) {
+    if (argc < 3) {
+        std::printf("usage: %s cpu|gpu <dir>\n", argv[0]);
+        return 2;
+    }
+    fs::path dir = argv[2];
+    fs::create_directories(dir);
+    std::string mode = argv[1];
+    try {
+        if (mode == "cpu")
+            cpu_tests(dir);
+        else if (mode == "gpu")
+            gpu_tests(dir);
+        else
+            return 2;
+    } catch (const std::exception& e) {
+        std::printf("FAIL uncaught exception: %s\n", e.what());
+        g_fail++;
+    }
+    std::printf("%s: %s (%d failures)\n", argv[0], g_fail ? "FAILED" : "OK", g_fail);
+    return g_fail ? 1 : 0;
+}

@@ -1,0 +1,107 @@
+"""The C++ host API (include/tensor/**) through its test program
+tests/cpp/test_host_api, and the pieces of it that the reference's own host
+code pins bit for bit: Dataset batches (src/data/dataset.cpp:56-71) and the
+cosine schedule (include/tensor/trainer/cosine_schedule.hpp:18-29), both
+compiled from the reference sources into oracle/_ref/ by oracle/build_ref.sh
+when the reference tree is present.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle as O
+import tadapt
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+BIN = os.path.join(ROOT, "tests", "cpp", "_build", "test_host_api")
+REF = os.path.join(ROOT, "oracle", "_ref", "libref_host.so")
+
+
+def _binary():
+    if not os.path.exists(BIN):
+        subprocess.check_call([os.path.join(ROOT, "tests", "cpp", "build.sh")])
+    return BIN
+
+
+def _ref():
+    if not os.path.exists(REF):
+        pytest.skip("oracle/_ref not built (the reference tree is absent)")
+    L = ctypes.CDLL(REF)
+    L.ref_cosine_lr.restype = ctypes.c_float
+    L.ref_cosine_lr.argtypes = [ctypes.c_float, ctypes.c_int64, ctypes.c_int64, ctypes.c_float,
+                                ctypes.c_int64]
+    L.ref_dataset_batches.restype = ctypes.c_int64
+    L.ref_dataset_batches.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                      ctypes.c_void_p, ctypes.c_void_p]
+    return L
+
+
+def _lr_grid():
+    for warm in (0, 1, 5, 100):
+        for total in (1, 50, 1000):
+            for step in range(60):
+                if total <= warm:
+                    continue
+                yield warm, total, step
+
+
+@pytest.fixture(scope="module")
+def cpu_run(tmp_path_factory):
+    d = tmp_path_factory.mktemp("host_api")
+    r = subprocess.run([_binary(), "cpu", str(d)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stdout + r.stderr
+    return d
+
+
+def test_host_api_cpu_checks(cpu_run):
+    assert (cpu_run / "batches.bin").exists()
+
+
+def test_dataset_batches_match_reference_and_oracle(cpu_run):
+    got = np.fromfile(cpu_run / "batches.bin", np.int32)
+    B, T, NB = 3, 10, 5
+    data = cpu_run / "data"
+    toks = np.concatenate([np.fromfile(data / "a.bin", np.uint32),
+                           np.fromfile(data / "b.bin", np.uint32)])
+    pos, want = 0, []
+    for _ in range(NB):
+        i, t, pos = O.next_batch(toks, pos, B, T)
+        want += [i, t]
+    np.testing.assert_array_equal(got, np.concatenate(want))
+    L = _ref()
+    inp = np.empty(NB * B * T, np.int32)
+    tgt = np.empty(NB * B * T, np.int32)
+    n = L.ref_dataset_batches(str(data).encode(), B, T, NB, inp.ctypes.data, tgt.ctypes.data)
+    assert n == toks.size
+    ref = np.concatenate([np.concatenate([inp[k * B * T:(k + 1) * B * T],
+                                          tgt[k * B * T:(k + 1) * B * T]]) for k in range(NB)])
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_cosine_schedule_bit_exact_vs_reference(cpu_run):
+    """The C++ header, the engine's exported schedule and the oracle all
+    equal the reference's compiled lr_at bit for bit."""
+    got = np.fromfile(cpu_run / "lr.bin", np.float32)
+    L = _ref()
+    lib = tadapt.lib()
+    ref, eng, orc = [], [], []
+    for warm, total, step in _lr_grid():
+        ref.append(L.ref_cosine_lr(3e-4, warm, total, 0.1, step))
+        eng.append(lib.ta_cosine_lr(3e-4, warm, total, 0.1, step))
+        orc.append(O.cosine_lr(3e-4, warm, total, 0.1, step))
+    ref = np.array(ref, np.float32)
+    assert got.size == ref.size
+    np.testing.assert_array_equal(got.view(np.uint32), ref.view(np.uint32))
+    np.testing.assert_array_equal(np.array(eng, np.float32).view(np.uint32), ref.view(np.uint32))
+    np.testing.assert_array_equal(np.array(orc, np.float32).view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.gpu
+def test_host_api_gpu(tmp_path):
+    print("case: test_host_api gpu", flush=True)
+    r = subprocess.run([_binary(), "gpu", str(tmp_path)], capture_output=True, text=True,
+                       timeout=110)
+    assert r.returncode == 0, r.stdout + r.stderr[-2000:]
