@@ -184,6 +184,14 @@ def main():
         split[k] = tadapt.kprof_read()
     tadapt.kprof_select(-1)
     dom = max(split, key=lambda k: split[k]["ms"])
+    if args.categories:
+        for k, v in split.items():
+            if not v["launches"]:
+                continue
+            sec = v["ms"] * 1e-3
+            print(f"  kernel {tadapt.KPROF_KERNELS[k]:14s} {v['ms']:7.2f} ms/step {v['launches']:4d} "
+                  f"launches  {v['flops'] / sec / 1e12:7.1f} TFLOP/s  {v['bytes'] / sec / 1e9:7.1f} GB/s "
+                  f"(algorithmic)  {tadapt.kprof_name(k)}", file=sys.stderr)
 
     # timed region; the dominant kernel is event-timed on its launch stream
     tadapt.kprof_select(dom)

@@ -263,7 +263,7 @@ static int engine_alloc(Engine* e) {
     CK(alloc(e, &e->norm_dev, 64, "norm", 1));
     CK(alloc(e, &e->cacc, H + 1, "centroid"));
     CK(alloc(e, &e->tok_dev, BT, "tok"));
-    CK(alloc(e, &e->tgt_dev, BT, "tgt"));
+    CK(alloc(e, &e->tgt_dev, BT, "targets", 1));  // int32, 4-byte elements
     TA_HIP(hipHostMalloc((void**)&e->tok_host, BT * sizeof(int32_t)));
     TA_HIP(hipHostMalloc((void**)&e->tgt_host, BT * sizeof(int32_t)));
     TA_HIP(hipHostMalloc((void**)&e->loss_host, BT * sizeof(float)));

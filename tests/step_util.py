@@ -4,7 +4,6 @@ names, the engine/oracle pair built from it, and the comparison metric."""
 import numpy as np
 
 import oracle as O
-import tadapt
 
 
 def base_tensors(mc, seed):
@@ -39,6 +38,7 @@ def base_tensors(mc, seed):
 def make_pair(mc, ac, B, T, seed):
     tensors = base_tensors(mc, seed)
     orc = O.OracleModel(mc, ac)
+    import tadapt
     eng = tadapt.Engine(mc, ac, B, T)
     for name, arr in tensors.items():
         orc.set_weight(name, arr)
@@ -67,6 +67,6 @@ def rel(a, b):
 
 def pairs(mc, ac):
     for l in range(mc["layers"]):
-        for ti, t in enumerate(tadapt.TARGETS):
+        for ti, t in enumerate(O.TARGETS):
             if (ac["inject_mask"] >> ti) & 1:
                 yield l, t
