@@ -485,7 +485,9 @@ __global__ __launch_bounds__(WMW * WNW * 64) void k_gemm_big(GemmArgs a) {
 // Tile/pipeline variants of k_gemm_big; variant 0 is the default.
 static int g_big_variant = 0;
 static int big_bn(int variant) {
-    return (variant == 1 || variant == 3) ? 128 : ((variant == 4 || variant == 5) ? 256 : 192);
+    return (variant == 1 || variant == 3) ? 128
+           : (variant == 4 || variant == 5 || variant == 6) ? 256
+                                                                            : 192;
 }
 
 // symbol of the unsplit BF16-output instance of each variant, as printed
@@ -497,6 +499,7 @@ static const char* big_name(int variant) {
         case 3: return "void ta::k_gemm_big<128, 4, 2, 0, 2>(ta::GemmArgs)";
         case 4: return "void ta::k_gemm_big<256, 4, 2, 0, 1>(ta::GemmArgs)";
         case 5: return "void ta::k_gemm_big<256, 2, 4, 0, 1>(ta::GemmArgs)";
+        case 6: return "void ta::k_gemm_big<256, 2, 2, 0, 1>(ta::GemmArgs)";
         default: return "void ta::k_gemm_big<192, 4, 2, 0, 1>(ta::GemmArgs)";
     }
 }
@@ -509,6 +512,7 @@ static void launch_big(int variant, dim3 grid, const GemmArgs& a, hipStream_t s)
         case 3: k_gemm_big<128, 4, 2, EPI, 2><<<grid, 512, 0, s>>>(a); break;
         case 4: k_gemm_big<256, 4, 2, EPI, 1><<<grid, 512, 0, s>>>(a); break;
         case 5: k_gemm_big<256, 2, 4, EPI, 1><<<grid, 512, 0, s>>>(a); break;
+        case 6: k_gemm_big<256, 2, 2, EPI, 1><<<grid, 256, 0, s>>>(a); break;
         default: k_gemm_big<192, 4, 2, EPI, 1><<<grid, 512, 0, s>>>(a); break;
     }
 }
@@ -522,8 +526,7 @@ __global__ void k_splitk_reduce(const float* __restrict__ part, int splits, int 
     int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     int64_t MN = (int64_t)M * N;
     if (idx >= MN) return;
-    float s = 0.f;
-    for (int p = 0; p < splits; p++) s += part[p * MN + idx];
+    float s = sum_splits(part, splits, MN, idx);
     int m = (int)(idx / N), n = (int)(idx % N);
     if (OUT_BF16) {
         bf16* C = (bf16*)Cv + (int64_t)m * ldc + n;
@@ -746,7 +749,7 @@ using namespace ta;
 extern "C" {
 
 int ta_gemm_variant(int v) {
-    TA_REQUIRE(v >= 0 && v <= 5, "gemm_variant: %d out of range", v);
+    TA_REQUIRE(v >= 0 && v <= 6, "gemm_variant: %d out of range", v);
     g_big_variant = v;
     return 0;
 }

@@ -58,60 +58,97 @@ struct Pairs3 {
 };
 
 // ── C_p = bf16(X Y_p^T) ───────────────────────────────────────────────────
-// grid: ceil(M/16) blocks x 256 threads.  Column c of the concatenated
-// output belongs to pair c / r, rank index c % r.
-template <int NT>  // 16-column tiles covering n*r columns
-__global__ __launch_bounds__(256) void k_skinny_nt(const bf16* __restrict__ X, int64_t ldx, int M,
-                                                   int K, int r, Pairs3 p) {
-    __shared__ floatx4 red[3][NT][64];
+// grid: ceil(M/32) blocks x 512 threads (8 waves).  Each wave covers all 32
+// rows of the block (2 groups of 16) for the 32-wide K chunks it takes round
+// robin, so one fragment of Y_p serves 32 rows; it issues the loads of U
+// chunks before their MFMAs (U 16-byte loads per lane and operand in
+// flight).  The waves' partial sums are added in wave order through LDS.
+// Column c of the concatenated output belongs to pair c / r, rank c % r.
+constexpr int SK_W = 8, SK_RG = 2;  // waves, 16-row groups per block
+template <int NT, int U>  // NT: 16-column tiles covering n*r columns
+__global__ __launch_bounds__(SK_W * 64) void k_skinny_nt(const bf16* __restrict__ X, int64_t ldx,
+                                                         int M, int K, int r, Pairs3 p) {
+    __shared__ floatx4 red[SK_W / 2][SK_RG][NT][64];
     int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    int m0 = blockIdx.x * 16;
-    int row = m0 + (lane & 15);
+    int m0 = blockIdx.x * 16 * SK_RG;
     int ncat = p.n * r;
-    floatx4 acc[NT];
+    floatx4 acc[SK_RG][NT];
 #pragma unroll
-    for (int t = 0; t < NT; t++) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-    const bf16* xr = X + (int64_t)(row < M ? row : 0) * ldx;
+    for (int g = 0; g < SK_RG; g++)
+#pragma unroll
+        for (int t = 0; t < NT; t++) acc[g][t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const bf16* xr[SK_RG];
+    bool rin[SK_RG];
+#pragma unroll
+    for (int g = 0; g < SK_RG; g++) {
+        int row = m0 + 16 * g + (lane & 15);
+        rin[g] = row < M;
+        xr[g] = X + (int64_t)(rin[g] ? row : 0) * ldx;
+    }
     const bf16* yr[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         int c = 16 * t + (lane & 15);
         yr[t] = (c < ncat) ? p.y[c / r] + (int64_t)(c % r) * K : nullptr;
     }
-    int nks = (K + 31) / 32;
-    for (int ks = w; ks < nks; ks += 4) {
-        int k = 32 * ks + 8 * (lane >> 4);
-        bf16x8_t a = (row < M) ? ld8(xr, k, K) : zfrag();
+    const int nks = (K + 31) / 32;
+    const int ko = 8 * (lane >> 4);
+    for (int ks0 = w; ks0 < nks; ks0 += SK_W * U) {
+        bf16x8_t a[U][SK_RG], b[U][NT];
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-            bf16x8_t b = yr[t] ? ld8(yr[t], k, K) : zfrag();
-            acc[t] = mf16(a, b, acc[t]);
+        for (int u = 0; u < U; u++) {
+            int ks = ks0 + SK_W * u;
+            int k = 32 * ks + ko;
+            bool in = ks < nks;
+#pragma unroll
+            for (int g = 0; g < SK_RG; g++) a[u][g] = (in && rin[g]) ? ld8(xr[g], k, K) : zfrag();
+#pragma unroll
+            for (int t = 0; t < NT; t++) b[u][t] = (in && yr[t]) ? ld8(yr[t], k, K) : zfrag();
         }
-    }
-    if (w > 0)
 #pragma unroll
-        for (int t = 0; t < NT; t++) red[w - 1][t][lane] = acc[t];
-    __syncthreads();
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int g = 0; g < SK_RG; g++)
+#pragma unroll
+                for (int t = 0; t < NT; t++) acc[g][t] = mf16(a[u][g], b[u][t], acc[g][t]);
+    }
+    // fixed-order tree over the waves: w += w + h for h = 4, 2, 1
+#pragma unroll
+    for (int h = SK_W / 2; h >= 1; h >>= 1) {
+        if (w >= h && w < 2 * h)
+#pragma unroll
+            for (int g = 0; g < SK_RG; g++)
+#pragma unroll
+                for (int t = 0; t < NT; t++) red[w - h][g][t][lane] = acc[g][t];
+        __syncthreads();
+        if (w < h)
+#pragma unroll
+            for (int g = 0; g < SK_RG; g++)
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    floatx4 o = red[w][g][t][lane];
+                    acc[g][t][0] += o[0];
+                    acc[g][t][1] += o[1];
+                    acc[g][t][2] += o[2];
+                    acc[g][t][3] += o[3];
+                }
+        __syncthreads();
+    }
     if (w == 0) {
 #pragma unroll
-        for (int t = 0; t < NT; t++) {
-            floatx4 v = acc[t];
-            for (int q = 0; q < 3; q++) {
-                floatx4 o = red[q][t][lane];
-                v[0] += o[0];
-                v[1] += o[1];
-                v[2] += o[2];
-                v[3] += o[3];
-            }
-            int c = 16 * t + (lane & 15);
-            if (c >= ncat) continue;
-            bf16* out = p.c[c / r] + (c % r);
+        for (int g = 0; g < SK_RG; g++)
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                int m = m0 + 4 * (lane >> 4) + i;
-                if (m < M) out[(int64_t)m * p.ldc] = f2bf(v[i]);
+            for (int t = 0; t < NT; t++) {
+                floatx4 v = acc[g][t];
+                int c = 16 * t + (lane & 15);
+                if (c >= ncat) continue;
+                bf16* out = p.c[c / r] + (c % r);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    int m = m0 + 16 * g + 4 * (lane >> 4) + i;
+                    if (m < M) out[(int64_t)m * p.ldc] = f2bf(v[i]);
+                }
             }
-        }
     }
 }
 
@@ -199,13 +236,37 @@ __global__ __launch_bounds__(256) void k_rank_update(bf16* __restrict__ Y, int64
 // L: [T x NL] (ldl), Sm: [T x NS] (lds), NS <= 192.  Block: 64 columns of L
 // (4 waves x 16), one token range; token tiles of 64 staged transposed.
 constexpr int WG_TK = 64;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 8 consecutive BF16 of row `tok`, columns [c, c+8) (zero outside the
+// matrix), as a 16-byte vector
+__device__ __forceinline__ u32x4 ld8z(const bf16* __restrict__ P, int64_t ld, int tok, int t_end,
+                                      int c, int ncols, bool vec) {
+    if (tok < t_end && vec && c + 8 <= ncols) return *(const u32x4*)(P + (int64_t)tok * ld + c);
+    uint16_t x[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++)
+        x[e] = (tok < t_end && c + e < ncols) ? P[(int64_t)tok * ld + c + e] : (uint16_t)0;
+    u32x4 v;
+#pragma unroll
+    for (int e = 0; e < 4; e++) v[e] = x[2 * e] | ((uint32_t)x[2 * e + 1] << 16);
+    return v;
+}
+// scatter the 8 values of v to S[(c + e) * (WG_TK + 8) + tt] (transposed)
+__device__ __forceinline__ void st8t(bf16* S, int c, int tt, u32x4 v) {
+#pragma unroll
+    for (int e = 0; e < 8; e++) S[(c + e) * (WG_TK + 8) + tt] = (uint16_t)(v[e >> 1] >> ((e & 1) * 16));
+}
+
 template <int NST>  // 16-column tiles of the small side
 __global__ __launch_bounds__(256) void k_wgrad(const bf16* __restrict__ L, int64_t ldl, int NL,
                                                const bf16* __restrict__ Sm, int64_t lds, int NS,
                                                int T, int tokens_per_split,
                                                float* __restrict__ part) {
-    __shared__ __attribute__((aligned(16))) bf16 sL[64 * (WG_TK + 8)];         // [l][t]
-    __shared__ __attribute__((aligned(16))) bf16 sS[NST * 16 * (WG_TK + 8)];   // [s][t]
+    __shared__ __attribute__((aligned(16))) bf16 sL[64 * (WG_TK + 8)];        // [l][t]
+    __shared__ __attribute__((aligned(16))) bf16 sS[NST * 16 * (WG_TK + 8)];  // [s][t]
+    constexpr int SCH = NST * 2 * WG_TK;       // 16-byte chunks of the small tile
+    constexpr int SPT = (SCH + 255) / 256;     // ... per thread
     int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     int l0 = blockIdx.x * 64;
     int t_beg = blockIdx.y * tokens_per_split;
@@ -213,34 +274,38 @@ __global__ __launch_bounds__(256) void k_wgrad(const bf16* __restrict__ L, int64
     floatx4 acc[NST];
 #pragma unroll
     for (int t = 0; t < NST; t++) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-    bool vecl = ((ldl & 7) == 0) && (((uintptr_t)L & 15) == 0);
+    const bool vecl = ((ldl & 7) == 0) && (((uintptr_t)L & 15) == 0);
+    const bool vecs = ((lds & 7) == 0) && (((uintptr_t)Sm & 15) == 0);
+    // staging registers: the next token tile is loaded while this one computes
+    u32x4 rl[2], rs[SPT];
+#define WG_LOAD(tb)                                                                         \
+    do {                                                                                    \
+        _Pragma("unroll") for (int i = 0; i < 2; i++) {                                     \
+            int q = threadIdx.x + 256 * i;                                                  \
+            rl[i] = ld8z(L, ldl, (tb) + (q >> 3), t_end, l0 + (q & 7) * 8, NL, vecl);       \
+        }                                                                                   \
+        _Pragma("unroll") for (int i = 0; i < SPT; i++) {                                   \
+            int q = threadIdx.x + 256 * i;                                                  \
+            if (q < SCH)                                                                    \
+                rs[i] = ld8z(Sm, lds, (tb) + q / (NST * 2), t_end, (q % (NST * 2)) * 8, NS, \
+                             vecs);                                                         \
+        }                                                                                   \
+    } while (0)
+    if (t_beg < t_end) WG_LOAD(t_beg);
     for (int tb = t_beg; tb < t_end; tb += WG_TK) {
-        __syncthreads();
-        // L tile [TK tokens x 64 cols] -> sL[col][token]
-        for (int q = threadIdx.x; q < WG_TK * 8; q += 256) {
-            int tt = q >> 3, cc = (q & 7) * 8;
-            int tok = tb + tt, l = l0 + cc;
-            bf16x8v v;
-            if (tok < t_end && vecl && l + 8 <= NL) {
-                v = *(const bf16x8v*)(L + (int64_t)tok * ldl + l);
-            } else {
-                uint16_t x[8];
-                for (int e = 0; e < 8; e++)
-                    x[e] = (tok < t_end && l + e < NL) ? L[(int64_t)tok * ldl + l + e] : (uint16_t)0;
-                for (int e = 0; e < 4; e++) v.w[e] = x[2 * e] | ((uint32_t)x[2 * e + 1] << 16);
-            }
+        __syncthreads();  // the previous tile's MFMAs are done with LDS
 #pragma unroll
-            for (int e = 0; e < 8; e++)
-                sL[(cc + e) * (WG_TK + 8) + tt] = (uint16_t)(v.w[e >> 1] >> ((e & 1) * 16));
+        for (int i = 0; i < 2; i++) {
+            int q = threadIdx.x + 256 * i;
+            st8t(sL, (q & 7) * 8, q >> 3, rl[i]);
         }
-        // small tile [TK tokens x NST*16] -> sS[s][token]
-        for (int q = threadIdx.x; q < WG_TK * NST * 16; q += 256) {
-            int tt = q / (NST * 16), ss = q % (NST * 16);
-            int tok = tb + tt;
-            sS[ss * (WG_TK + 8) + tt] =
-                (tok < t_end && ss < NS) ? Sm[(int64_t)tok * lds + ss] : (uint16_t)0;
+#pragma unroll
+        for (int i = 0; i < SPT; i++) {
+            int q = threadIdx.x + 256 * i;
+            if (q < SCH) st8t(sS, (q % (NST * 2)) * 8, q / (NST * 2), rs[i]);
         }
         __syncthreads();
+        if (tb + WG_TK < t_end) WG_LOAD(tb + WG_TK);
 #pragma unroll
         for (int kc = 0; kc < WG_TK / 32; kc++) {
             bf16x8_t a =
@@ -253,6 +318,7 @@ __global__ __launch_bounds__(256) void k_wgrad(const bf16* __restrict__ L, int64
             }
         }
     }
+#undef WG_LOAD
     // C layout: column s = 16t + l%16, rows l = 16w + 4(l/16) + i
     float* out = part + (int64_t)blockIdx.y * NL * NS;
 #pragma unroll
@@ -276,8 +342,7 @@ __global__ void k_wgrad_reduce(const float* __restrict__ part, int splits, int N
     int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     int64_t n = (int64_t)NL * NS;
     if (idx >= n) return;
-    float v = 0.f;
-    for (int z = 0; z < splits; z++) v += part[(int64_t)z * n + idx];
+    float v = sum_splits(part, splits, n, idx);
     int l = (int)(idx / NS), s = (int)(idx % NS);
     if (!TRANS) {
         g0[(int64_t)l * NS + s] += scale * v;
@@ -319,17 +384,22 @@ int lora_skinny_nt(const bf16* X, int64_t ldx, int M, int K, int r, const bf16* 
         TA_REQUIRE(((uintptr_t)Y[i] & 15) == 0, "lora_skinny_nt: Y must be 16-byte aligned");
     }
     int nt = (n * r + 15) / 16;
-    dim3 grid((M + 15) / 16);
+    dim3 grid((M + 16 * SK_RG - 1) / (16 * SK_RG));
+    const bool timed = kprof_begin(KP_LORA_SKINNY, s);
     switch (nt) {
-        case 1: k_skinny_nt<1><<<grid, 256, 0, s>>>(X, ldx, M, K, r, p); break;
-        case 2: k_skinny_nt<2><<<grid, 256, 0, s>>>(X, ldx, M, K, r, p); break;
-        case 3: k_skinny_nt<3><<<grid, 256, 0, s>>>(X, ldx, M, K, r, p); break;
-        case 4: k_skinny_nt<4><<<grid, 256, 0, s>>>(X, ldx, M, K, r, p); break;
-        case 6: k_skinny_nt<6><<<grid, 256, 0, s>>>(X, ldx, M, K, r, p); break;
-        case 8: k_skinny_nt<8><<<grid, 256, 0, s>>>(X, ldx, M, K, r, p); break;
-        case 12: k_skinny_nt<12><<<grid, 256, 0, s>>>(X, ldx, M, K, r, p); break;
+        case 1: k_skinny_nt<1, 4><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
+        case 2: k_skinny_nt<2, 4><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
+        case 3: k_skinny_nt<3, 3><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
+        case 4: k_skinny_nt<4, 2><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
+        case 6: k_skinny_nt<6, 2><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
+        case 8: k_skinny_nt<8, 1><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
+        case 12: k_skinny_nt<12, 1><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
         default: return set_error(-1, "lora_skinny_nt: %d pairs x rank %d unsupported", n, r);
     }
+    if (timed)  // X and the Y_p read once, C_p written once
+        kprof_end(KP_LORA_SKINNY, s, 2.0 * M * K * n * r,
+                  2.0 * ((double)M * K + (double)n * r * K + (double)M * n * r),
+                  "ta::k_skinny_nt (all instances)");
     return check_launch("lora_skinny_nt");
 }
 
@@ -374,6 +444,7 @@ int lora_wgrad(const bf16* L, int64_t ldl, int NL, const bf16* Sm, int64_t lds, 
     TA_REQUIRE(part, "lora_wgrad: scratch allocation failed");
     dim3 grid(ltiles, splits);
     int nst = (NS + 15) / 16;
+    const bool timed = kprof_begin(KP_LORA_WGRAD, s);
     switch (nst) {
         case 1: k_wgrad<1><<<grid, 256, 0, s>>>(L, ldl, NL, Sm, lds, NS, T, per, part); break;
         case 2: k_wgrad<2><<<grid, 256, 0, s>>>(L, ldl, NL, Sm, lds, NS, T, per, part); break;
@@ -391,6 +462,10 @@ int lora_wgrad(const bf16* L, int64_t ldl, int NL, const bf16* Sm, int64_t lds, 
     else
         k_wgrad_reduce<false><<<blocks, 256, 0, s>>>(part, splits, NL, NS, r, scale, G[0], G[0],
                                                      G[0]);
+    if (timed)  // L and Sm read once; G read and written once (F32)
+        kprof_end(KP_LORA_WGRAD, s, 2.0 * T * NL * NS,
+                  2.0 * ((double)T * NL + (double)T * NS) + 8.0 * NL * NS,
+                  "ta::k_wgrad + ta::k_wgrad_reduce (all instances)");
     return check_launch("lora_wgrad");
 }
 

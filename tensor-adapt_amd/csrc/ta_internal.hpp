@@ -14,12 +14,31 @@ enum KernelId {
     KP_ATTN_FWD = 2,
     KP_ATTN_BWD_DQ = 3,
     KP_ATTN_BWD_DKV = 4,
-    KP_COUNT = 5
+    KP_LORA_SKINNY = 5,  // h = x A^T / dh = go B
+    KP_LORA_WGRAD = 6,   // gB = go^T h / gA = dh^T x partials
+    KP_COUNT = 7
 };
 // Bracket one launch of kernel `kid` on stream s when that kernel is being
 // timed; name is the kernel's symbol as a profiler prints it.
 bool kprof_begin(int kid, hipStream_t s);
 void kprof_end(int kid, hipStream_t s, double flops, double bytes, const char* name);
+
+// sum_{z < splits} part[z * stride + idx], added in z order (deterministic);
+// the loads of 8 splits are issued together so their latencies overlap.
+__device__ __forceinline__ float sum_splits(const float* __restrict__ part, int splits,
+                                            int64_t stride, int64_t idx) {
+    float s = 0.f;
+    int z = 0;
+    for (; z + 8 <= splits; z += 8) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = part[(int64_t)(z + i) * stride + idx];
+#pragma unroll
+        for (int i = 0; i < 8; i++) s += v[i];
+    }
+    for (; z < splits; z++) s += part[(int64_t)z * stride + idx];
+    return s;
+}
 
 // LoRA terms for gemm_dispatch.  After the base epilogue, for each pair p
 // in order, with D_p = U_p V_p^T (U_p [M x r], V_p [N x r]):

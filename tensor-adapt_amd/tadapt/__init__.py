@@ -113,7 +113,8 @@ def stream():
 
 
 # ── kernel-level timer (ta_kprof_*) ─────────────────────────────────────
-KPROF_KERNELS = ["gemm_big", "gemm_big_wide", "attn_fwd", "attn_bwd_dq", "attn_bwd_dkv"]
+KPROF_KERNELS = ["gemm_big", "gemm_big_wide", "attn_fwd", "attn_bwd_dq", "attn_bwd_dkv",
+                 "lora_skinny", "lora_wgrad"]
 
 
 def kprof_select(kid):
