@@ -14,23 +14,26 @@
 // softmax row statistics reduce over 16 lanes with xor shuffles.  The MFMA
 // C layout (lane: column l%16, rows 4*(l/16)+r) is converted to the A
 // operand layout (row l%16, 8 consecutive k) through a per-wave LDS tile.
+// Every loop over tiles loads the next tile's operands into registers while
+// the current tile computes, so global latency overlaps the MFMAs.
 //
 // Forward (per b, hq, query tile; heaviest tiles launch first):
 //   pass 1: online row max / sum of exp over key tiles 0..diag;
 //   pass 2: recompute S, P = exp(S - max) / sum (the reference's softmax,
-//   ops.cu:352-396), store P (F32), O += P*V.
+//   ops.cu:352-396), store P (F32), O += P*V; O is stored in BF16 and, for
+//   the backward's row dots, in F32.
 // Every product whose left operand is an F32 quantity (P, dS) runs as two
 // MFMAs on its BF16 hi/lo split, keeping ~16 mantissa bits: the reference
 // computes these GEMMs in F32 (ops.cu:628-855).
 // Backward:
-//   k_attn_bwd_dq (per b, hq, query tile): pass 1 accumulates the row dot
-//   D = sum_k P*dP (dP = dO V^T recomputed on MFMA); pass 2 forms
-//   dS = P (dP - D) (ops.cu:405-435) and dQ = scale * dS K.  D is stored.
-//   k_attn_bwd_dkv (per b, kv head, key tile): loops over the query heads
-//   of the GQA group and the query tiles at or below the diagonal and
-//   accumulates dV = P^T dO and dK = scale * dS^T Q for the kv head in
-//   registers — the group sum of ops.cu:539-555 without atomics, so dK/dV
-//   are deterministic.
+//   row dots D = sum_k P dP (ops.cu:405-435) = dO . O with the F32 O of the
+//   forward (k_attn_rowdot_o), or from P and dP = dO V^T when no F32 O is
+//   at hand (k_attn_rowdot_p, the C-ABI's sdpa_bwd);
+//   k_attn_bwd_dq (per b, hq, query tile): dS = P (dP - D), dQ = scale dS K;
+//   k_attn_bwd_dkv (per b, hq, key tile): dV_h = P^T dO and
+//   dK_h = scale dS^T Q for the query head as F32 partials, then
+//   k_attn_dkv_reduce sums the heads of each GQA group in head order — the
+//   group sum of ops.cu:539-555 without atomics, so dK/dV are deterministic.
 #include <float.h>
 
 #include <algorithm>
@@ -65,55 +68,78 @@ __device__ __forceinline__ bf16x8_t ld_head8(const bf16* base, int64_t row_strid
     return z;
 }
 
-// Stage rows [r0, r0+64) of one head ([row][HD], global row stride rs) into
-// LDS as [row][HD + 8] (K-contiguous for MFMA operands over hd).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Rows [r0, r0+64) of one head ([row][HD] in global memory, row stride rs),
+// held in registers between load() and store() so that the next tile's
+// global loads overlap the current tile's MFMAs.  store() writes LDS
+// [row][HD + 8] (K-contiguous rows for MFMA operands over hd).
 template <int HD>
-__device__ __forceinline__ void stage_rows(bf16* __restrict__ s, const bf16* __restrict__ g,
-                                           int64_t rs, int r0, int T) {
-    constexpr int CH = 64 * HD / 8;
-    for (int q = threadIdx.x; q < CH; q += 256) {
-        int r = q / (HD / 8), c = (q % (HD / 8)) * 8;
-        bf16x8v v;
-        if (r0 + r < T)
-            v = *(const bf16x8v*)(g + (int64_t)(r0 + r) * rs + c);
-        else
-            v.w[0] = v.w[1] = v.w[2] = v.w[3] = 0u;
-        *(bf16x8v*)(s + r * (HD + 8) + c) = v;
+struct Rows64 {
+    static constexpr int CPR = HD / 8;         // 16-byte chunks per row
+    static constexpr int NR = 64 * CPR / 256;  // chunks per thread
+    u32x4 v[NR];
+    __device__ __forceinline__ void load(const bf16* __restrict__ g, int64_t rs, int r0, int T) {
+#pragma unroll
+        for (int i = 0; i < NR; i++) {
+            int q = threadIdx.x + 256 * i;
+            int r = q / CPR, c = (q % CPR) * 8;
+            v[i] = (r0 + r < T) ? *(const u32x4*)(g + (int64_t)(r0 + r) * rs + c)
+                                : u32x4{0u, 0u, 0u, 0u};
+        }
     }
-}
-// Same rows staged transposed: LDS [HD][64 + 8] (row index contiguous).
-// Each thread loads 4 consecutive rows x 8 columns and writes one 8-byte
-// word (4 rows) per column, so the transpose costs 2 LDS writes per 16-byte
-// chunk instead of 8.
+    __device__ __forceinline__ void store(bf16* __restrict__ s) const {
+#pragma unroll
+        for (int i = 0; i < NR; i++) {
+            int q = threadIdx.x + 256 * i;
+            *(u32x4*)(s + (q / CPR) * (HD + 8) + (q % CPR) * 8) = v[i];
+        }
+    }
+};
+
+// The same 64 rows loaded as 4 consecutive rows x 8 columns per thread, so
+// they can be written transposed to LDS [HD][64 + 8] (row index contiguous)
+// with one 8-byte word per column (store_t), and/or as rows (store_rows).
 template <int HD>
-__device__ __forceinline__ void stage_rows_t(bf16* __restrict__ s, const bf16* __restrict__ g,
-                                             int64_t rs, int r0, int T) {
-    constexpr int CH = 16 * (HD / 8);  // 16 row groups x HD/8 column chunks
-    for (int q = threadIdx.x; q < CH; q += 256) {
+struct Rows64T {
+    static constexpr int NG = 16 * (HD / 8);  // 4-row x 8-column groups
+    u32x4 v[4];
+    __device__ __forceinline__ void load(const bf16* __restrict__ g, int64_t rs, int r0, int T) {
+        int q = threadIdx.x;
+        if (q >= NG) return;
         int rg = q & 15, c = (q >> 4) * 8;
-        uint32_t w[4][4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             int row = r0 + 4 * rg + i;
-            bf16x8v v;
-            if (row < T)
-                v = *(const bf16x8v*)(g + (int64_t)row * rs + c);
-            else
-                v.w[0] = v.w[1] = v.w[2] = v.w[3] = 0u;
-#pragma unroll
-            for (int j = 0; j < 4; j++) w[i][j] = v.w[j];
+            v[i] = (row < T) ? *(const u32x4*)(g + (int64_t)row * rs + c) : u32x4{0u, 0u, 0u, 0u};
         }
+    }
+    __device__ __forceinline__ void store_t(bf16* __restrict__ s) const {
+        int q = threadIdx.x;
+        if (q >= NG) return;
+        int rg = q & 15, c = (q >> 4) * 8;
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             int j = e >> 1, sh = (e & 1) * 16;
-            uint64_t word = (uint64_t)((w[0][j] >> sh) & 0xffffu) |
-                            ((uint64_t)((w[1][j] >> sh) & 0xffffu) << 16) |
-                            ((uint64_t)((w[2][j] >> sh) & 0xffffu) << 32) |
-                            ((uint64_t)((w[3][j] >> sh) & 0xffffu) << 48);
+            uint64_t word = (uint64_t)((v[0][j] >> sh) & 0xffffu) |
+                            ((uint64_t)((v[1][j] >> sh) & 0xffffu) << 16) |
+                            ((uint64_t)((v[2][j] >> sh) & 0xffffu) << 32) |
+                            ((uint64_t)((v[3][j] >> sh) & 0xffffu) << 48);
             *(uint64_t*)(s + (c + e) * LDT + 4 * rg) = word;
         }
     }
-}
+    __device__ __forceinline__ void store_rows(bf16* __restrict__ s) const {
+        int q = threadIdx.x;
+        if (q >= NG) return;
+        int rg = q & 15, c = (q >> 4) * 8;
+#pragma unroll
+        for (int i = 0; i < 4; i++) *(u32x4*)(s + (4 * rg + i) * (HD + 8) + c) = v[i];
+    }
+};
+
+// Orders this wave's LDS writes before its later LDS reads (a wave's LDS
+// operations complete in order; this keeps the compiler from moving them).
+__device__ __forceinline__ void wave_sync() { __builtin_amdgcn_wave_barrier(); }
 
 // S (or dP) for one wave: 16 rows x 64 keys = 4 MFMA tiles, A fragments in
 // registers (af[HD/32]), B rows from an LDS [key][HD+8] tile.
@@ -174,9 +200,9 @@ template <int HD>
 __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
                                                   const bf16* __restrict__ K,
                                                   const bf16* __restrict__ V,
-                                                  bf16* __restrict__ O, float* __restrict__ P,
-                                                  int T, int Hq, int Hkv, float scale,
-                                                  int zero_fill) {
+                                                  bf16* __restrict__ O, float* __restrict__ O32,
+                                                  float* __restrict__ P, int T, int Hq, int Hkv,
+                                                  float scale, int zero_fill) {
     __shared__ __attribute__((aligned(16))) bf16 sK[TK * (HD + 8)];
     __shared__ __attribute__((aligned(16))) bf16 sVt[HD * LDT];
     __shared__ __attribute__((aligned(16))) bf16 sP[4][2][16 * LDT];
@@ -197,6 +223,8 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
 #pragma unroll
     for (int ks = 0; ks < HD / 32; ks++) qf[ks] = ld_head8(Qh, qs, rowA, T, 32 * ks + 8 * (lane >> 4));
     int rbase = q0 + 16 * w + 4 * (lane >> 4);  // C-layout rows rbase + r
+    Rows64<HD> lk;
+    Rows64T<HD> lv;
 
     // pass 1: online max / sum
     float m[4], l[4];
@@ -205,9 +233,12 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
         m[r] = -FLT_MAX;
         l[r] = 0.f;
     }
+    lk.load(Kh, ks_, 0, T);
     for (int kt = 0; kt <= qt; kt++) {
-        stage_rows<HD>(sK, Kh, ks_, kt * TK, T);
+        __syncthreads();  // every wave is done with the previous tile
+        lk.store(sK);
         __syncthreads();
+        if (kt < qt) lk.load(Kh, ks_, (kt + 1) * TK, T);
         floatx4 S[4];
         wave_qk<HD>(S, qf, sK, lane);
 #pragma unroll
@@ -217,9 +248,9 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
 #pragma unroll
             for (int t = 0; t < 4; t++) {
                 int key = kt * TK + 16 * t + (lane & 15);
-                float s = S[t][r] * scale;
-                S[t][r] = s;
-                if (key <= row && key < T) tmax = fmaxf(tmax, s);
+                float sc = S[t][r] * scale;
+                S[t][r] = sc;
+                if (key <= row && key < T) tmax = fmaxf(tmax, sc);
             }
             tmax = red16_max(tmax);
             float mn = fmaxf(m[r], tmax);
@@ -232,7 +263,6 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
             l[r] = (m[r] == -FLT_MAX ? 0.f : l[r] * exp2f((m[r] - mn) * kLog2e)) + add;
             m[r] = mn;
         }
-        __syncthreads();
     }
     float inv[4];
 #pragma unroll
@@ -242,10 +272,17 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
     floatx4 acc[HD / 16];
 #pragma unroll
     for (int j = 0; j < HD / 16; j++) acc[j] = zero4();
+    lk.load(Kh, ks_, 0, T);
+    lv.load(Vh, ks_, 0, T);
     for (int kt = 0; kt <= qt; kt++) {
-        stage_rows<HD>(sK, Kh, ks_, kt * TK, T);
-        stage_rows_t<HD>(sVt, Vh, ks_, kt * TK, T);
         __syncthreads();
+        lk.store(sK);
+        lv.store_t(sVt);
+        __syncthreads();
+        if (kt < qt) {
+            lk.load(Kh, ks_, (kt + 1) * TK, T);
+            lv.load(Vh, ks_, (kt + 1) * TK, T);
+        }
         floatx4 S[4];
         wave_qk<HD>(S, qf, sK, lane);
 #pragma unroll
@@ -261,9 +298,8 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
                 put_split(sP[w][0], sP[w][1], (4 * (lane >> 4) + r) * LDT + kl, p);
             }
         }
-        __syncthreads();
+        wave_sync();  // sP[w] is this wave's own tile
         wave_pv<HD>(acc, sP[w][0], sP[w][1], sVt, lane);
-        __syncthreads();
     }
     // zeros above the diagonal (ops.cu:352-396 leaves exact zeros there)
     if (zero_fill) {
@@ -276,26 +312,138 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
             }
         }
     }
-    // O (bf16) — lane holds column 16j + l%16 of rows rbase + r
+    // O (bf16, and F32 when O32 is given) — lane holds column 16j + l%16 of
+    // rows rbase + r
     bf16* Oh = O + (int64_t)b * T * qs + hq * HD;
+    float* O32h = O32 ? O32 + (int64_t)b * T * qs + hq * HD : nullptr;
 #pragma unroll
     for (int j = 0; j < HD / 16; j++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             int row = rbase + r;
-            if (row < T) Oh[(int64_t)row * qs + 16 * j + (lane & 15)] = f2bf(acc[j][r]);
+            if (row < T) {
+                Oh[(int64_t)row * qs + 16 * j + (lane & 15)] = f2bf(acc[j][r]);
+                if (O32h) O32h[(int64_t)row * qs + 16 * j + (lane & 15)] = acc[j][r];
+            }
         }
 }
 
-// ── backward: dQ (and the row dots D) ─────────────────────────────────────
+// ── backward: the row dots D = sum_k P * dP ──────────────────────────────
+// From the forward's F32 output: D[bh, t] = dO[t, h, :] . O[t, h, :], since
+// sum_k P dP = sum_k P (dO V_k) = dO (sum_k P V_k).  HD/8 lanes per row.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_rowdot_o(const bf16* __restrict__ dO,
+                                                       const float* __restrict__ O32,
+                                                       float* __restrict__ D, int B, int T,
+                                                       int Hq) {
+    constexpr int LPR = HD / 8;  // lanes per (token, head)
+    int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    int64_t pr = gid / LPR;  // (b, t, h) in dO's row-major order
+    int sub = (int)(gid % LPR);
+    int64_t npr = (int64_t)B * T * Hq;
+    float s = 0.f;
+    if (pr < npr) {
+        const bf16* o = dO + pr * HD + sub * 8;
+        const float* f = O32 + pr * HD + sub * 8;
+        bf16x8v a = *(const bf16x8v*)o;
+        float4 f0 = *(const float4*)f, f1 = *(const float4*)(f + 4);
+        float x[8];
+        unpack8(a, x);
+        s = x[0] * f0.x + x[1] * f0.y + x[2] * f0.z + x[3] * f0.w + x[4] * f1.x + x[5] * f1.y +
+            x[6] * f1.z + x[7] * f1.w;
+    }
+#pragma unroll
+    for (int o = 1; o < LPR; o <<= 1) s += __shfl_xor(s, o, 64);
+    if (sub == 0 && pr < npr) {
+        int h = (int)(pr % Hq);
+        int64_t bt = pr / Hq;
+        int t = (int)(bt % T), b = (int)(bt / T);
+        D[((int64_t)b * Hq + h) * T + t] = s;
+    }
+}
+
+// Without the F32 output (the C-ABI's sdpa_bwd): D = sum_k P * dP with
+// dP = dO V^T recomputed on MFMA, per (b, hq, query tile).
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_rowdot_p(const bf16* __restrict__ dO,
+                                                       const bf16* __restrict__ V,
+                                                       const float* __restrict__ P,
+                                                       float* __restrict__ Dout, int T, int Hq,
+                                                       int Hkv) {
+    __shared__ __attribute__((aligned(16))) bf16 sV[TK * (HD + 8)];
+    int nqt = (T + TQ - 1) / TQ;
+    int nbh = gridDim.x / nqt;
+    int qt = nqt - 1 - (int)(blockIdx.x / nbh);
+    int bh = (int)(blockIdx.x % nbh);
+    int b = bh / Hq, hq = bh % Hq, hkv = hq / (Hq / Hkv);
+    int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int64_t qs = (int64_t)Hq * HD, ks_ = (int64_t)Hkv * HD;
+    const bf16* dOh = dO + (int64_t)b * T * qs + hq * HD;
+    const bf16* Vh = V + (int64_t)b * T * ks_ + hkv * HD;
+    const float* Ph = P + (int64_t)bh * T * T;
+    int q0 = qt * TQ;
+    int rowA = q0 + 16 * w + (lane & 15);
+    bf16x8_t of[HD / 32];
+#pragma unroll
+    for (int ks = 0; ks < HD / 32; ks++)
+        of[ks] = ld_head8(dOh, qs, rowA, T, 32 * ks + 8 * (lane >> 4));
+    int rbase = q0 + 16 * w + 4 * (lane >> 4);
+    float dsum[4] = {0.f, 0.f, 0.f, 0.f};
+    Rows64<HD> lv;
+    lv.load(Vh, ks_, 0, T);
+    for (int kt = 0; kt <= qt; kt++) {
+        __syncthreads();
+        lv.store(sV);
+        __syncthreads();
+        if (kt < qt) lv.load(Vh, ks_, (kt + 1) * TK, T);
+        floatx4 dP[4];
+        wave_qk<HD>(dP, of, sV, lane);
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            int key = kt * TK + 16 * t + (lane & 15);
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                int row = rbase + r;
+                if (key <= row && key < T && row < T)
+                    dsum[r] += Ph[(int64_t)row * T + key] * dP[t][r];
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        float d = red16_sum(dsum[r]);
+        int row = rbase + r;
+        if ((lane & 15) == 0 && row < T) Dout[(int64_t)bh * T + row] = d;
+    }
+}
+
+// P values a lane needs for one key tile in the C layout of a 16 x 64 wave
+// tile: p[t][r] = P[row0 + r][key0 + 16t + l%16] for keys <= row (0 above).
+__device__ __forceinline__ void load_p_rows(float (&p)[4][4], const float* __restrict__ Ph, int T,
+                                            int row0, int key0, int lane) {
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        int key = key0 + 16 * t + (lane & 15);
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            int row = row0 + r;
+            p[t][r] = (key <= row && key < T && row < T) ? Ph[(int64_t)row * T + key] : 0.f;
+        }
+    }
+}
+
+// ── backward: dQ ──────────────────────────────────────────────────────────
+// Per (b, hq, query tile), one pass over the key tiles at or below the
+// diagonal: dP = dO V^T, dS = P (dP - D) (ops.cu:405-435), dQ = scale dS K.
+// The next tile's V, K and P are loaded while the current one computes.
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO,
                                                      const bf16* __restrict__ K,
                                                      const bf16* __restrict__ V,
                                                      const float* __restrict__ P,
-                                                     bf16* __restrict__ dQ,
-                                                     float* __restrict__ Dout, int T, int Hq,
-                                                     int Hkv, float scale) {
+                                                     const float* __restrict__ Dq,
+                                                     bf16* __restrict__ dQ, int T, int Hq, int Hkv,
+                                                     float scale) {
     __shared__ __attribute__((aligned(16))) bf16 sV[TK * (HD + 8)];
     __shared__ __attribute__((aligned(16))) bf16 sKt[HD * LDT];
     __shared__ __attribute__((aligned(16))) bf16 sS[4][2][16 * LDT];
@@ -317,62 +465,46 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO
     for (int ks = 0; ks < HD / 32; ks++)
         of[ks] = ld_head8(dOh, qs, rowA, T, 32 * ks + 8 * (lane >> 4));
     int rbase = q0 + 16 * w + 4 * (lane >> 4);
-
-    // pass 1: D = sum_k P * dP
-    float dsum[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int kt = 0; kt <= qt; kt++) {
-        stage_rows<HD>(sV, Vh, ks_, kt * TK, T);
-        __syncthreads();
-        floatx4 dP[4];
-        wave_qk<HD>(dP, of, sV, lane);
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            int key = kt * TK + 16 * t + (lane & 15);
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                int row = rbase + r;
-                if (key <= row && key < T && row < T)
-                    dsum[r] += Ph[(int64_t)row * T + key] * dP[t][r];
-            }
-        }
-        __syncthreads();
-    }
     float D[4];
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        D[r] = red16_sum(dsum[r]);
-        int row = rbase + r;
-        if ((lane & 15) == 0 && row < T) Dout[(int64_t)bh * T + row] = D[r];
-    }
+    for (int r = 0; r < 4; r++) D[r] = (rbase + r < T) ? Dq[(int64_t)bh * T + rbase + r] : 0.f;
 
-    // pass 2: dS, dQ
     floatx4 acc[HD / 16];
 #pragma unroll
     for (int j = 0; j < HD / 16; j++) acc[j] = zero4();
+    Rows64<HD> lv;
+    Rows64T<HD> lkt;
+    float pn[4][4];
+    lv.load(Vh, ks_, 0, T);
+    lkt.load(Kh, ks_, 0, T);
+    load_p_rows(pn, Ph, T, rbase, 0, lane);
     for (int kt = 0; kt <= qt; kt++) {
-        stage_rows<HD>(sV, Vh, ks_, kt * TK, T);
-        stage_rows_t<HD>(sKt, Kh, ks_, kt * TK, T);
         __syncthreads();
+        lv.store(sV);
+        lkt.store_t(sKt);
+        float pc[4][4];
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) pc[t][r] = pn[t][r];
+        __syncthreads();
+        if (kt < qt) {
+            lv.load(Vh, ks_, (kt + 1) * TK, T);
+            lkt.load(Kh, ks_, (kt + 1) * TK, T);
+            load_p_rows(pn, Ph, T, rbase, (kt + 1) * TK, lane);
+        }
         floatx4 dP[4];
         wave_qk<HD>(dP, of, sV, lane);
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             int kl = 16 * t + (lane & 15);
-            int key = kt * TK + kl;
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                int row = rbase + r;
-                float ds = 0.f;
-                if (key <= row && key < T && row < T) {
-                    float p = Ph[(int64_t)row * T + key];
-                    ds = p * (dP[t][r] - D[r]);
-                }
-                put_split(sS[w][0], sS[w][1], (4 * (lane >> 4) + r) * LDT + kl, ds);
-            }
+            for (int r = 0; r < 4; r++)
+                put_split(sS[w][0], sS[w][1], (4 * (lane >> 4) + r) * LDT + kl,
+                          pc[t][r] * (dP[t][r] - D[r]));
         }
-        __syncthreads();
+        wave_sync();
         wave_pv<HD>(acc, sS[w][0], sS[w][1], sKt, lane);
-        __syncthreads();
     }
     bf16* dQh = dQ + (int64_t)b * T * qs + hq * HD;
 #pragma unroll
@@ -384,14 +516,37 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO
         }
 }
 
+// P^T values for the dK/dV kernel: p[t][r] = P[q0 + 16t + l%16][kbase + r]
+// for keys <= query (0 above the diagonal).
+__device__ __forceinline__ void load_p_cols(float (&p)[4][4], const float* __restrict__ Ph, int T,
+                                            int q0, int kbase, int lane) {
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        int q = q0 + 16 * t + (lane & 15);
+        const float* prow = Ph + (int64_t)q * T;
+        if ((T & 3) == 0 && q < T && kbase + 3 < T && kbase + 3 <= q) {  // 16-byte aligned
+            float4 v4 = *(const float4*)(prow + kbase);
+            p[t][0] = v4.x;
+            p[t][1] = v4.y;
+            p[t][2] = v4.z;
+            p[t][3] = v4.w;
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                int key = kbase + r;
+                p[t][r] = (q < T && key < T && key <= q) ? prow[key] : 0.f;
+            }
+        }
+    }
+}
+
 // ── backward: dK, dV contributions of one query head, one key tile ─────────
 // Wave w owns keys 16w..16w+15 of the tile; for each query tile qt >= kt:
 // dP^T = V dO^T (keys x queries), dS^T = P^T (dP^T - D), dV_h += P^T dO,
 // dK_h += dS^T Q.  The head's F32 contributions go to part[bh] ([T][hd] for
 // dK then dV); k_attn_dkv_reduce sums the GQA group in head order — the
 // group sum of ops.cu:539-555 without atomics, so dK/dV are deterministic.
-// One block per (head, key tile) keeps the work per block within 16x of the
-// longest instead of (group size) x that.
+// The next query tile's dO, Q, D and P are loaded while this one computes.
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_bwd_dkv(const bf16* __restrict__ dO,
                                                       const bf16* __restrict__ Q,
@@ -416,6 +571,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dkv(const bf16* __restrict__ d
     const bf16* dOh = dO + (int64_t)b * T * qs + hq * HD;
     const bf16* Qh = Q + (int64_t)b * T * qs + hq * HD;
     const float* Ph = P + (int64_t)bh * T * T;
+    const float* Dh = Dq + (int64_t)bh * T;
     int k0 = kt * TK;
     int keyA = k0 + 16 * w + (lane & 15);  // A-operand row (key) of this lane
     bf16x8_t vf[HD / 32];
@@ -430,36 +586,34 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dkv(const bf16* __restrict__ d
         accV[j] = zero4();
     }
     int nqt = (T + TQ - 1) / TQ;
+    Rows64T<HD> ldo, lq;
+    float pn[4][4];
+    float dn = 0.f;
+    ldo.load(dOh, qs, kt * TQ, T);
+    lq.load(Qh, qs, kt * TQ, T);
+    load_p_cols(pn, Ph, T, kt * TQ, kbase, lane);
+    if (threadIdx.x < TQ) dn = (kt * TQ + threadIdx.x < T) ? Dh[kt * TQ + threadIdx.x] : 0.f;
     for (int qt = kt; qt < nqt; qt++) {
-        int q0 = qt * TQ;
-        stage_rows<HD>(sO, dOh, qs, q0, T);
-        stage_rows_t<HD>(sOt, dOh, qs, q0, T);
-        stage_rows_t<HD>(sQt, Qh, qs, q0, T);
-        if (threadIdx.x < TQ)
-            sD[threadIdx.x] = (q0 + threadIdx.x < T) ? Dq[(int64_t)bh * T + q0 + threadIdx.x] : 0.f;
         __syncthreads();
-        floatx4 dPt[4];
-        wave_qk<HD>(dPt, vf, sO, lane);  // rows = keys, cols = queries
-        // P^T tile for this wave: P[q][key], lane keys kbase..kbase+3
+        ldo.store_rows(sO);
+        ldo.store_t(sOt);
+        lq.store_t(sQt);
+        if (threadIdx.x < TQ) sD[threadIdx.x] = dn;
         float pv[4][4];
 #pragma unroll
-        for (int t = 0; t < 4; t++) {
-            int q = q0 + 16 * t + (lane & 15);
-            const float* prow = Ph + (int64_t)q * T;
-            if ((T & 3) == 0 && q < T && kbase + 3 < T && kbase + 3 <= q) {  // 16-byte aligned
-                float4 v4 = *(const float4*)(prow + kbase);
-                pv[t][0] = v4.x;
-                pv[t][1] = v4.y;
-                pv[t][2] = v4.z;
-                pv[t][3] = v4.w;
-            } else {
+        for (int t = 0; t < 4; t++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    int key = kbase + r;
-                    pv[t][r] = (q < T && key < T && key <= q) ? prow[key] : 0.f;
-                }
-            }
+            for (int r = 0; r < 4; r++) pv[t][r] = pn[t][r];
+        __syncthreads();
+        if (qt + 1 < nqt) {
+            int qn = (qt + 1) * TQ;
+            ldo.load(dOh, qs, qn, T);
+            lq.load(Qh, qs, qn, T);
+            load_p_cols(pn, Ph, T, qn, kbase, lane);
+            if (threadIdx.x < TQ) dn = (qn + threadIdx.x < T) ? Dh[qn + threadIdx.x] : 0.f;
         }
+        floatx4 dPt[4];
+        wave_qk<HD>(dPt, vf, sO, lane);  // rows = keys, cols = queries
         // dV += P^T dO
 #pragma unroll
         for (int t = 0; t < 4; t++)
@@ -467,22 +621,20 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dkv(const bf16* __restrict__ d
             for (int r = 0; r < 4; r++)
                 put_split(sA[w][0], sA[w][1], (4 * (lane >> 4) + r) * LDT + 16 * t + (lane & 15),
                           pv[t][r]);
-        __syncthreads();
+        wave_sync();
         wave_pv<HD>(accV, sA[w][0], sA[w][1], sOt, lane);
-        __syncthreads();
+        wave_sync();
         // dK += dS^T Q
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             int ql = 16 * t + (lane & 15);
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                float ds = pv[t][r] * (dPt[t][r] - sD[ql]);
-                put_split(sA[w][0], sA[w][1], (4 * (lane >> 4) + r) * LDT + ql, ds);
-            }
+            for (int r = 0; r < 4; r++)
+                put_split(sA[w][0], sA[w][1], (4 * (lane >> 4) + r) * LDT + ql,
+                          pv[t][r] * (dPt[t][r] - sD[ql]));
         }
-        __syncthreads();
+        wave_sync();
         wave_pv<HD>(accK, sA[w][0], sA[w][1], sQt, lane);
-        __syncthreads();
     }
     float* pK = part + (int64_t)bh * T * HD;
     float* pV = part + ((int64_t)gridDim.x / nkt + bh) * T * HD;
@@ -526,8 +678,8 @@ __global__ void k_attn_dkv_reduce(const float* __restrict__ part, bf16* __restri
 
 static inline bool a16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* P, int B, int T,
-             int Hq, int Hkv, int hd, bool zero_fill, hipStream_t s) {
+int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* O32, float* P, int B,
+             int T, int Hq, int Hkv, int hd, bool zero_fill, hipStream_t s) {
     TA_REQUIRE(B > 0 && T > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0,
                "sdpa_fwd: bad shape B=%d T=%d Hq=%d Hkv=%d", B, T, Hq, Hkv);
     TA_REQUIRE(hd == 64 || hd == 128, "sdpa_fwd: head_dim %d not supported (64 or 128)", hd);
@@ -537,31 +689,37 @@ int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* P, int
     float scale = 1.f / sqrtf((float)hd);
     const bool timed = kprof_begin(KP_ATTN_FWD, s);
     if (hd == 64)
-        k_attn_fwd<64><<<(int)blocks, 256, 0, s>>>(Q, K, V, O, P, T, Hq, Hkv, scale, zero_fill);
+        k_attn_fwd<64><<<(int)blocks, 256, 0, s>>>(Q, K, V, O, O32, P, T, Hq, Hkv, scale,
+                                                   zero_fill);
     else
-        k_attn_fwd<128><<<(int)blocks, 256, 0, s>>>(Q, K, V, O, P, T, Hq, Hkv, scale, zero_fill);
+        k_attn_fwd<128><<<(int)blocks, 256, 0, s>>>(Q, K, V, O, O32, P, T, Hq, Hkv, scale,
+                                                    zero_fill);
     if (timed) {
-        // causal S = QK^T and O = PV; Q, K, V read, O written, P written
-        // (causal half, or all of it when the upper triangle is zero-filled)
+        // causal S = QK^T and O = PV; Q, K, V read, O written (and O32),
+        // P written (causal half, or all of it when the upper triangle is
+        // zero-filled)
         double tri = (double)B * Hq * T * (T + 1) / 2.0, bt = (double)B * T;
         double pbytes = zero_fill ? 4.0 * B * Hq * (double)T * T : 4.0 * tri;
         kprof_end(KP_ATTN_FWD, s, 4.0 * hd * tri,
-                  2.0 * bt * hd * (2.0 * Hq + 2.0 * Hkv) + pbytes,
+                  2.0 * bt * hd * (2.0 * Hq + 2.0 * Hkv) + (O32 ? 4.0 * bt * Hq * hd : 0.0) +
+                      pbytes,
                   hd == 64 ? "void ta::k_attn_fwd<64>" : "void ta::k_attn_fwd<128>");
     }
     return check_launch("sdpa_fwd");
 }
 
 // Dbuf: [B*Hq*T] F32 row dots; part: [2*B*Hq*T*hd] F32 per-head dK/dV
-// contributions (both drawn from the scratch pool when NULL).
+// contributions (both drawn from the scratch pool when NULL).  O32: the
+// forward's F32 output [B*T, Hq*hd] (NULL: the row dots are formed from P).
 int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const float* P,
-             bf16* dQ, bf16* dK, bf16* dV, int B, int T, int Hq, int Hkv, int hd, float* Dbuf,
-             float* part, hipStream_t s) {
+             const float* O32, bf16* dQ, bf16* dK, bf16* dV, int B, int T, int Hq, int Hkv, int hd,
+             float* Dbuf, float* part, hipStream_t s) {
     TA_REQUIRE(B > 0 && T > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0,
                "sdpa_bwd: bad shape B=%d T=%d Hq=%d Hkv=%d", B, T, Hq, Hkv);
     TA_REQUIRE(hd == 64 || hd == 128, "sdpa_bwd: head_dim %d not supported (64 or 128)", hd);
     TA_REQUIRE(a16(dO) && a16(Q) && a16(K) && a16(V) && a16(dQ) && a16(dK) && a16(dV),
                "sdpa_bwd: tensors must be 16-byte aligned");
+    TA_REQUIRE(!O32 || a16(O32), "sdpa_bwd: O32 must be 16-byte aligned");
     if (!Dbuf) {
         Dbuf = (float*)scratch_get((size_t)B * Hq * T * sizeof(float), s);
         TA_REQUIRE(Dbuf, "sdpa_bwd: scratch allocation failed");
@@ -573,15 +731,29 @@ int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const 
     int nqt = (T + TQ - 1) / TQ;
     float scale = 1.f / sqrtf((float)hd);
     int64_t b1 = (int64_t)B * Hq * nqt;
+    // row dots D
+    if (O32) {
+        int64_t thr = (int64_t)B * T * Hq * (hd / 8);
+        int blocks = (int)((thr + 255) / 256);
+        if (hd == 64)
+            k_attn_rowdot_o<64><<<blocks, 256, 0, s>>>(dO, O32, Dbuf, B, T, Hq);
+        else
+            k_attn_rowdot_o<128><<<blocks, 256, 0, s>>>(dO, O32, Dbuf, B, T, Hq);
+    } else {
+        if (hd == 64)
+            k_attn_rowdot_p<64><<<(int)b1, 256, 0, s>>>(dO, V, P, Dbuf, T, Hq, Hkv);
+        else
+            k_attn_rowdot_p<128><<<(int)b1, 256, 0, s>>>(dO, V, P, Dbuf, T, Hq, Hkv);
+    }
     // algorithmic work (causal half): dq pass dP = dO V^T, dQ = dS K; dkv
-    // pass dP again, dV = P^T dO, dK = dS^T Q.  Bytes: BF16 operands and P
-    // read once, outputs written once (dq: dQ + row dots; dkv: F32 partials)
+    // pass dP again, dV = P^T dO, dK = dS^T Q.  Bytes: BF16 operands, P and
+    // the row dots read once, outputs written once (dkv: F32 partials)
     const double tri = (double)B * Hq * T * (T + 1) / 2.0, bt = (double)B * T;
     bool timed = kprof_begin(KP_ATTN_BWD_DQ, s);
     if (hd == 64)
-        k_attn_bwd_dq<64><<<(int)b1, 256, 0, s>>>(dO, K, V, P, dQ, Dbuf, T, Hq, Hkv, scale);
+        k_attn_bwd_dq<64><<<(int)b1, 256, 0, s>>>(dO, K, V, P, Dbuf, dQ, T, Hq, Hkv, scale);
     else
-        k_attn_bwd_dq<128><<<(int)b1, 256, 0, s>>>(dO, K, V, P, dQ, Dbuf, T, Hq, Hkv, scale);
+        k_attn_bwd_dq<128><<<(int)b1, 256, 0, s>>>(dO, K, V, P, Dbuf, dQ, T, Hq, Hkv, scale);
     if (timed)
         kprof_end(KP_ATTN_BWD_DQ, s, 4.0 * hd * tri,
                   4.0 * tri + 2.0 * bt * hd * (2.0 * Hq + 2.0 * Hkv) + 4.0 * bt * Hq,
@@ -608,14 +780,15 @@ extern "C" {
 
 int ta_sdpa_fwd(const uint16_t* Q, const uint16_t* K, const uint16_t* V, uint16_t* out,
                 float* attn_w, int B, int T, int Hq, int Hkv, int head_dim, void* stream) {
-    return ta::attn_fwd(Q, K, V, out, attn_w, B, T, Hq, Hkv, head_dim, true, (hipStream_t)stream);
+    return ta::attn_fwd(Q, K, V, out, nullptr, attn_w, B, T, Hq, Hkv, head_dim, true,
+                        (hipStream_t)stream);
 }
 
 int ta_sdpa_bwd(const uint16_t* dout, const uint16_t* Q, const uint16_t* K, const uint16_t* V,
                 const float* attn_w, uint16_t* dQ, uint16_t* dK, uint16_t* dV, int B, int T,
                 int Hq, int Hkv, int head_dim, void* stream) {
-    return ta::attn_bwd(dout, Q, K, V, attn_w, dQ, dK, dV, B, T, Hq, Hkv, head_dim, nullptr,
-                        nullptr, (hipStream_t)stream);
+    return ta::attn_bwd(dout, Q, K, V, attn_w, nullptr, dQ, dK, dV, B, T, Hq, Hkv, head_dim,
+                        nullptr, nullptr, (hipStream_t)stream);
 }
 
 }  // extern "C"

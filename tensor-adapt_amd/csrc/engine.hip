@@ -55,7 +55,7 @@ struct Layer {
     Pair pr[NPAIR];
     // forward cache
     bf16 *res_in, *xn, *Q, *K, *V, *ao, *res_mid, *xn2, *gate, *up, *act;
-    float *in_rms, *post_rms, *attn_w;
+    float *in_rms, *post_rms, *attn_w, *ao32;  // ao32: attention output in F32
 };
 
 struct Engine {
@@ -230,6 +230,7 @@ static int engine_alloc(Engine* e) {
         CK(alloc(e, &ly.V, (int64_t)BT * kvd, (p + "V").c_str(), 0));
         CK(alloc(e, &ly.ao, (int64_t)BT * qd, (p + "attn_out").c_str(), 0));
         CK(alloc(e, &ly.attn_w, (int64_t)e->B * c.n_q * e->T * e->T, (p + "attn_w").c_str(), 1));
+        CK(alloc(e, &ly.ao32, (int64_t)BT * qd, (p + "attn_out32").c_str(), 1));
         CK(alloc(e, &ly.res_mid, (int64_t)BT * H, (p + "res_mid").c_str(), 0));
         CK(alloc(e, &ly.post_rms, BT, (p + "post_rms").c_str(), 1));
         CK(alloc(e, &ly.xn2, (int64_t)BT * H, (p + "x_normed2").c_str(), 0));
@@ -451,9 +452,9 @@ static int forward(Engine* e) {
               ta_rope_fwd(ly.K, e->B, e->T, c.n_kv, c.head_dim, c.rope_theta, s));
         // the upper triangle of attn_w is never read by the backward: skip its fill
         TIMED(TA_CAT_ATTN_FWD, 4.0 * tri * c.head_dim,
-              tri * 4 + dBT * (2.0 * qd + 2.0 * kvd) * 2,
-              attn_fwd(ly.Q, ly.K, ly.V, ly.ao, ly.attn_w, e->B, e->T, c.n_q, c.n_kv, c.head_dim,
-                       false, s));
+              tri * 4 + dBT * (2.0 * qd + 2.0 * kvd) * 2 + dBT * qd * 4,
+              attn_fwd(ly.Q, ly.K, ly.V, ly.ao, ly.ao32, ly.attn_w, e->B, e->T, c.n_q, c.n_kv,
+                       c.head_dim, false, s));
         CK(lora_group_h(e, ly, {PO}, ly.ao, qd));
         {
             LoraEpi eo = fwd_epi(e, ly.pr[PO]);
@@ -536,9 +537,10 @@ static int backward(Engine* e) {
             CK(proj_bwd_x(e, ly.Wt[PO], e->g_res, e->dao, H, qd, 0.f, &ep));
         }
         TIMED(TA_CAT_ATTN_BWD, 8.0 * tri * c.head_dim,
-              tri * 4 + dBT * (2.0 * qd + 2.0 * kvd) * 2 + dBT * (qd + 2.0 * kvd) * 2,
-              attn_bwd(e->dao, ly.Q, ly.K, ly.V, ly.attn_w, e->dQ, e->dK, e->dV, e->B, e->T, c.n_q,
-                       c.n_kv, c.head_dim, e->Dbuf, e->dkv_part, s));
+              tri * 4 + dBT * (2.0 * qd + 2.0 * kvd) * 2 + dBT * (qd + 2.0 * kvd) * 2 +
+                  dBT * qd * 4,
+              attn_bwd(e->dao, ly.Q, ly.K, ly.V, ly.attn_w, ly.ao32, e->dQ, e->dK, e->dV, e->B,
+                       e->T, c.n_q, c.n_kv, c.head_dim, e->Dbuf, e->dkv_part, s));
         TIMED(TA_CAT_ELEMWISE, 0, dBT * qd * 4,
               ta_rope_bwd(e->dQ, e->B, e->T, c.n_q, c.head_dim, c.rope_theta, s));
         TIMED(TA_CAT_ELEMWISE, 0, dBT * kvd * 4,

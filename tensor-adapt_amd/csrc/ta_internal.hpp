@@ -59,11 +59,11 @@ struct LoraEpi {
 int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16* X, int64_t ldx,
                   const bf16* Y, int64_t ldy, float beta, void* C, int64_t ldc, const bf16* bias,
                   bool out_f32, hipStream_t s, int force_splits, const LoraEpi* lora);
-int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* P, int B, int T, int Hq,
-             int Hkv, int hd, bool zero_fill, hipStream_t s);
+int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* O32, float* P, int B,
+             int T, int Hq, int Hkv, int hd, bool zero_fill, hipStream_t s);
 int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const float* P,
-             bf16* dQ, bf16* dK, bf16* dV, int B, int T, int Hq, int Hkv, int hd, float* Dbuf,
-             float* part, hipStream_t s);
+             const float* O32, bf16* dQ, bf16* dK, bf16* dV, int B, int T, int Hq, int Hkv, int hd,
+             float* Dbuf, float* part, hipStream_t s);
 int transpose_bf16(const bf16* in, bf16* out, int64_t rows, int64_t cols, hipStream_t s);
 int fill_normal_bf16(bf16* out, int64_t n, uint64_t seed, uint64_t sid, float std, hipStream_t s);
 int fill_bf16(bf16* out, int64_t n, float v, hipStream_t s);
