@@ -303,6 +303,93 @@ __device__ __attribute__((always_inline)) inline void big_mma(floatx16 (&acc)[TM
     }
 }
 
+// Epilogue of the large GEMM kernels on the 32x32 MFMA accumulator layout
+// (lane: column l%32, rows 8*(r/4) + 4*(l/32) + r%4 of each fragment).
+template <int TM, int TN, int WTM, int WTN, int EPI>
+__device__ __attribute__((always_inline)) inline void big_epilogue(floatx16 (&acc)[TM][TN],
+                                                                   const GemmArgs& a, int m0,
+                                                                   int n0, int wm, int wn,
+                                                                   int lane) {
+    if constexpr (EPI == EPI_PARTIAL) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                int n = n0 + wn * WTN + j * 32 + (lane & 31);
+                if (n >= a.N) continue;
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    int m = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    if (m < a.M) a.part[((int64_t)blockIdx.z * a.M + m) * a.N + n] = acc[i][j][r];
+                }
+            }
+    } else {
+        // three small unrolled passes keep acc in registers: (1) base
+        // epilogue in place, (2) LoRA terms pair by pair, (3) store
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                int n = n0 + wn * WTN + j * 32 + (lane & 31);
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    int m = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    float o = a.alpha * acc[i][j][r];
+                    if (a.beta != 0.f && m < a.M && n < a.N)
+                        o += a.beta * bf2f(((const bf16*)a.C)[(int64_t)m * a.ldc + n]);
+                    if (a.bias && n < a.N) o = bf2f(f2bf(o)) + bf2f(a.bias[n]);
+                    acc[i][j][r] = bf2f(f2bf(o));
+                }
+            }
+        // LoRA terms: D = U V^T on the same 32x32 MFMA layout as acc; static
+        // pair indices (a runtime index into the by-value argument struct
+        // would move it to scratch)
+#pragma unroll
+        for (int p = 0; p < 3; p++) {
+            if (p >= a.lora_n) break;
+#pragma unroll
+            for (int i = 0; i < TM; i++)
+#pragma unroll
+                for (int j = 0; j < TN; j++) {
+                    int arow = min(m0 + wm * WTM + i * 32 + (lane & 31), a.M - 1);
+                    int bcol = min(n0 + wn * WTN + j * 32 + (lane & 31), a.N - 1);
+                    floatx16 d;
+#pragma unroll
+                    for (int r = 0; r < 16; r++) d[r] = 0.f;
+                    for (int k = 0; k < a.lora_r; k += 16) {
+                        int kk = k + 8 * (lane >> 5);
+                        bf16x8_t fa, fb;
+                        if (kk < a.lora_r) {
+                            fa = *(const bf16x8_t*)(a.lora_u[p] + (int64_t)arow * a.lora_ldu[p] + kk);
+                            fb = *(const bf16x8_t*)(a.lora_v[p] + (int64_t)bcol * a.lora_r + kk);
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 8; e++) fa[e] = fb[e] = (__bf16)0.f;
+                        }
+                        d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, fb, d, 0, 0, 0);
+                    }
+#pragma unroll
+                    for (int r = 0; r < 16; r++)
+                        acc[i][j][r] = a.lora_delta
+                                           ? bf2f(f2bf(acc[i][j][r] + a.lora_s * bf2f(f2bf(d[r]))))
+                                           : bf2f(f2bf(a.lora_s * d[r] + acc[i][j][r]));
+                }
+        }
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                int n = n0 + wn * WTN + j * 32 + (lane & 31);
+                if (n >= a.N) continue;
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    int m = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    if (m < a.M) ((bf16*)a.C)[(int64_t)m * a.ldc + n] = f2bf(acc[i][j][r]);
+                }
+            }
+    }
+}
+
 template <int BN, int WMW, int WNW, int EPI, int PIPE>
 __global__ __launch_bounds__(WMW * WNW * 64) void k_gemm_big(GemmArgs a) {
     constexpr int BM = 256, NTH = WMW * WNW * 64;
@@ -400,93 +487,149 @@ __global__ __launch_bounds__(WMW * WNW * 64) void k_gemm_big(GemmArgs a) {
         }
     }
 
-    if constexpr (EPI == EPI_PARTIAL) {
+    big_epilogue<TM, TN, WTM, WTN, EPI>(acc, a, m0, n0, wm, wn, lane);
+}
+
+#undef compute
+
+// ── k_gemm_dma: the same tiles fed by direct global->LDS loads ────────────
+// BK = 32 per stage (rows of 64 bytes = 4 chunks of 16 bytes) and NS stages
+// in LDS, so the loads of tile k + NS - 1 are in flight while tile k
+// computes, with no register staging.  One global_load_lds_dwordx4 fills 16
+// consecutive rows of a stage; chunk c of row R sits in slot c ^ dswz(R),
+// which keeps every 16-row fragment read free of bank conflicts.
+constexpr int DBK = 32;
+__device__ __forceinline__ int dswz(int R) { return ((R >> 1) ^ (R >> 3)) & 3; }
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// Issue this wave's share of the loads of one stage: operand rows
+// [row0, row0 + ROWS) (clamped to rows - 1), k range [k0, k0 + 32).
+// Wave-instruction j covers stage rows 16j..16j+15.  Every wave issues
+// exactly two (straight-line code, so the compiler's wait bookkeeping stays
+// exact): j = w and j = w + 8; with 12 instructions (ROWS = 192) waves 4-7
+// repeat the second load of waves 0-3, writing the same bytes.
+template <int ROWS>
+__device__ __forceinline__ void dma_stage(const bf16* __restrict__ P, int64_t ld, int row0,
+                                          int rows, int k0, bf16* stage, int w, int lane) {
+    constexpr int NI = ROWS / 16;
+    static_assert(NI >= 8 && NI <= 16, "two loads per wave per operand");
 #pragma unroll
-        for (int i = 0; i < TM; i++)
+    for (int h = 0; h < 2; h++) {
+        int j = h == 0 ? w : (w + 8 < NI ? w + 8 : w + NI - 8);
+        int r = 16 * j + (lane >> 2);
+        int c = (lane & 3) ^ dswz(r);
+        int grow = min(row0 + r, rows - 1);
+        const bf16* src = P + (int64_t)grow * ld + k0 + 8 * c;
+        __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr_t)(stage + 16 * j * DBK), 16, 0,
+                                         0);
+    }
+}
+
+// One 32-wide k slice of MFMAs for a wave from a swizzled stage.
+template <int TM, int TN, int WTM, int WTN>
+__device__ __attribute__((always_inline)) inline void dma_mma(floatx16 (&acc)[TM][TN],
+                                                              const bf16* sX, const bf16* sY,
+                                                              int wm, int wn, int lane) {
 #pragma unroll
-            for (int j = 0; j < TN; j++) {
-                int n = n0 + wn * WTN + j * 32 + (lane & 31);
-                if (n >= a.N) continue;
+    for (int kk = 0; kk < DBK / 16; kk++) {
+        const int c = 2 * kk + (lane >> 5);
+        bf16x8_t fx[TM], fy[TN];
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    int m = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    if (m < a.M) a.part[((int64_t)blockIdx.z * a.M + m) * a.N + n] = acc[i][j][r];
-                }
-            }
-    } else {
-        // three small unrolled passes keep acc in registers: (1) base
-        // epilogue in place, (2) LoRA terms pair by pair, (3) store
+        for (int i = 0; i < TM; i++) {
+            int R = wm * WTM + i * 32 + (lane & 31);
+            fx[i] = *(const bf16x8_t*)(sX + R * DBK + 8 * (c ^ dswz(R)));
+        }
 #pragma unroll
-        for (int i = 0; i < TM; i++)
-#pragma unroll
-            for (int j = 0; j < TN; j++) {
-                int n = n0 + wn * WTN + j * 32 + (lane & 31);
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    int m = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    float o = a.alpha * acc[i][j][r];
-                    if (a.beta != 0.f && m < a.M && n < a.N)
-                        o += a.beta * bf2f(((const bf16*)a.C)[(int64_t)m * a.ldc + n]);
-                    if (a.bias && n < a.N) o = bf2f(f2bf(o)) + bf2f(a.bias[n]);
-                    acc[i][j][r] = bf2f(f2bf(o));
-                }
-            }
-        // LoRA terms: D = U V^T on the same 32x32 MFMA layout as acc; static
-        // pair indices (a runtime index into the by-value argument struct
-        // would move it to scratch)
-#pragma unroll
-        for (int p = 0; p < 3; p++) {
-            if (p >= a.lora_n) break;
-#pragma unroll
-            for (int i = 0; i < TM; i++)
-#pragma unroll
-                for (int j = 0; j < TN; j++) {
-                    int arow = min(m0 + wm * WTM + i * 32 + (lane & 31), a.M - 1);
-                    int bcol = min(n0 + wn * WTN + j * 32 + (lane & 31), a.N - 1);
-                    floatx16 d;
-#pragma unroll
-                    for (int r = 0; r < 16; r++) d[r] = 0.f;
-                    for (int k = 0; k < a.lora_r; k += 16) {
-                        int kk = k + 8 * (lane >> 5);
-                        bf16x8_t fa, fb;
-                        if (kk < a.lora_r) {
-                            fa = *(const bf16x8_t*)(a.lora_u[p] + (int64_t)arow * a.lora_ldu[p] + kk);
-                            fb = *(const bf16x8_t*)(a.lora_v[p] + (int64_t)bcol * a.lora_r + kk);
-                        } else {
-#pragma unroll
-                            for (int e = 0; e < 8; e++) fa[e] = fb[e] = (__bf16)0.f;
-                        }
-                        d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, fb, d, 0, 0, 0);
-                    }
-#pragma unroll
-                    for (int r = 0; r < 16; r++)
-                        acc[i][j][r] = a.lora_delta
-                                           ? bf2f(f2bf(acc[i][j][r] + a.lora_s * bf2f(f2bf(d[r]))))
-                                           : bf2f(f2bf(a.lora_s * d[r] + acc[i][j][r]));
-                }
+        for (int j = 0; j < TN; j++) {
+            int R = wn * WTN + j * 32 + (lane & 31);
+            fy[j] = *(const bf16x8_t*)(sY + R * DBK + 8 * (c ^ dswz(R)));
         }
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
-            for (int j = 0; j < TN; j++) {
-                int n = n0 + wn * WTN + j * 32 + (lane & 31);
-                if (n >= a.N) continue;
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    int m = m0 + wm * WTM + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    if (m < a.M) ((bf16*)a.C)[(int64_t)m * a.ldc + n] = f2bf(acc[i][j][r]);
-                }
-            }
+            for (int j = 0; j < TN; j++)
+                acc[i][j] =
+                    __builtin_amdgcn_mfma_f32_32x32x16_bf16(fx[i], fy[j], acc[i][j], 0, 0, 0);
     }
 }
 
-#undef compute
+// s_waitcnt vmcnt(n) with the other counters left free (gfx9 encoding)
+#define TA_WAIT_VMCNT(n) \
+    __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+
+template <int BN, int EPI>
+__global__ __launch_bounds__(512) void k_gemm_dma(GemmArgs a) {
+    constexpr int NS = 4;  // stages
+    constexpr int BM = 256, WMW = 4, WNW = 2;
+    constexpr int WTM = BM / WMW, WTN = BN / WNW;
+    constexpr int TM = WTM / 32, TN = WTN / 32;
+    constexpr int SX = BM * DBK, SY = BN * DBK;  // elements per stage
+    // one LDS object per stage and operand: the compiler then only waits for
+    // the loads into the buffer a read touches
+    __shared__ __attribute__((aligned(1024))) bf16 sX0[SX], sX1[SX], sX2[SX], sX3[SX];
+    __shared__ __attribute__((aligned(1024))) bf16 sY0[SY], sY1[SY], sY2[SY], sY3[SY];
+
+    int nt = a.tiles_m * a.tiles_n;
+    int bid = blockIdx.x;
+    if ((nt & 7) == 0) bid = (bid & 7) * (nt >> 3) + (bid >> 3);
+    int tm_i = bid / a.tiles_n, tn_i = bid % a.tiles_n;
+    int m0 = tm_i * BM, n0 = tn_i * BN;
+    int kbeg = blockIdx.z * a.k_per_split;
+    int kend = min(a.K, kbeg + a.k_per_split);
+    int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int wm = w / WNW, wn = w % WNW;
+    w = __builtin_amdgcn_readfirstlane(w);  // wave-uniform
+
+    floatx16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+    const int nk = (kend - kbeg) / DBK;
+    // Every step issues one stage (tiles past the end reload the last tile
+    // into a buffer that is never read), so exactly NS - 2 stages are issued
+    // after the one a step computes: 4 loads per stage per wave.
+#define DMA_ISSUE(SXB, SYB, KT)                                                        \
+    do {                                                                               \
+        const int kk_ = min((KT), nk - 1);                                             \
+        dma_stage<BM>(a.X, a.ldx, m0, a.M, kbeg + kk_ * DBK, SXB, w, lane);            \
+        dma_stage<BN>(a.Y, a.ldy, n0, a.N, kbeg + kk_ * DBK, SYB, w, lane);            \
+    } while (0)
+    DMA_ISSUE(sX0, sY0, 0);
+    DMA_ISSUE(sX1, sY1, 1);
+    DMA_ISSUE(sX2, sY2, 2);
+    // step on stage buffer J: wait for its loads, barrier (also: every wave
+    // is done reading buffer JN), refill JN with tile kt + NS - 1, compute J
+    // (the dispatcher guarantees nk % NS == 0: no branch inside the loop
+    // body, which keeps the compiler's wait bookkeeping per buffer)
+#define DMA_STEP(J, SXJ, SYJ, SXN, SYN)                                                \
+    do {                                                                               \
+        TA_WAIT_VMCNT(4 * (NS - 2));                                                   \
+        __builtin_amdgcn_s_barrier();                                                  \
+        DMA_ISSUE(SXN, SYN, kt0 + (J) + NS - 1);                                       \
+        dma_mma<TM, TN, WTM, WTN>(acc, SXJ, SYJ, wm, wn, lane);                        \
+    } while (0)
+    for (int kt0 = 0; kt0 < nk; kt0 += NS) {
+        DMA_STEP(0, sX0, sY0, sX3, sY3);
+        DMA_STEP(1, sX1, sY1, sX0, sY0);
+        DMA_STEP(2, sX2, sY2, sX1, sY1);
+        DMA_STEP(3, sX3, sY3, sX2, sY2);
+    }
+    TA_WAIT_VMCNT(0);  // the surplus loads have landed before the block ends
+#undef DMA_STEP
+#undef DMA_ISSUE
+    big_epilogue<TM, TN, WTM, WTN, EPI>(acc, a, m0, n0, wm, wn, lane);
+}
 
 // Tile/pipeline variants of k_gemm_big; variant 0 is the default.
 static int g_big_variant = 0;
 static int big_bn(int variant) {
     return (variant == 1 || variant == 3) ? 128
-           : (variant == 4 || variant == 5 || variant == 6) ? 256
+           : (variant == 4 || variant == 5 || variant == 6 || variant == 8) ? 256
                                                                             : 192;
 }
 
@@ -500,6 +643,8 @@ static const char* big_name(int variant) {
         case 4: return "void ta::k_gemm_big<256, 4, 2, 0, 1>(ta::GemmArgs)";
         case 5: return "void ta::k_gemm_big<256, 2, 4, 0, 1>(ta::GemmArgs)";
         case 6: return "void ta::k_gemm_big<256, 2, 2, 0, 1>(ta::GemmArgs)";
+        case 7: return "void ta::k_gemm_dma<192, 0>(ta::GemmArgs)";
+        case 8: return "void ta::k_gemm_dma<256, 0>(ta::GemmArgs)";
         default: return "void ta::k_gemm_big<192, 4, 2, 0, 1>(ta::GemmArgs)";
     }
 }
@@ -513,6 +658,8 @@ static void launch_big(int variant, dim3 grid, const GemmArgs& a, hipStream_t s)
         case 4: k_gemm_big<256, 4, 2, EPI, 1><<<grid, 512, 0, s>>>(a); break;
         case 5: k_gemm_big<256, 2, 4, EPI, 1><<<grid, 512, 0, s>>>(a); break;
         case 6: k_gemm_big<256, 2, 2, EPI, 1><<<grid, 256, 0, s>>>(a); break;
+        case 7: k_gemm_dma<192, EPI><<<grid, 512, 0, s>>>(a); break;
+        case 8: k_gemm_dma<256, EPI><<<grid, 512, 0, s>>>(a); break;
         default: k_gemm_big<192, 4, 2, EPI, 1><<<grid, 512, 0, s>>>(a); break;
     }
 }
@@ -604,8 +751,13 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
     if (xk && yk && !out_f32 && M >= 1024 && N >= 1024 && (K % BK) == 0 && vx && vy) {
         // default: 256 x 192 tiles up to N = 3072 (N = 1536 gives one block per
         // CU at M = 8192), 256 x 256 for wider outputs
+        // default: the direct-to-LDS kernel (256 x 192 tiles; 256 x 256 for
+        // very wide outputs) when K is a multiple of its 128-wide trip,
+        // else the register-staged kernel (256 x 192, or 256 x 256 above
+        // N = 3072)
         int variant = g_big_variant;
-        if (variant == 0 && N > 3072) variant = 4;
+        if (variant == 0) variant = (K % 128) == 0 ? (N > 65536 ? 8 : 7) : (N > 3072 ? 4 : 0);
+        if ((variant == 7 || variant == 8) && (K % 128) != 0) variant = variant == 8 ? 4 : 0;
         const int BNb = big_bn(variant);
         a.tiles_m = (M + 255) / 256;
         a.tiles_n = (N + BNb - 1) / BNb;
@@ -618,6 +770,7 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
             splits = std::min((256 + tiles - 1) / tiles, ksteps / 16);
         if (splits < 1) splits = 1;
         int steps_per = (ksteps + splits - 1) / splits;
+        if (variant == 7 || variant == 8) steps_per = (steps_per + 1) & ~1;  // 128-multiples
         a.k_per_split = steps_per * BK;
         splits = (ksteps + steps_per - 1) / steps_per;
         dim3 grid(tiles, 1, splits);
@@ -749,7 +902,7 @@ using namespace ta;
 extern "C" {
 
 int ta_gemm_variant(int v) {
-    TA_REQUIRE(v >= 0 && v <= 6, "gemm_variant: %d out of range", v);
+    TA_REQUIRE(v >= 0 && v <= 8, "gemm_variant: %d out of range", v);
     g_big_variant = v;
     return 0;
 }
