@@ -390,6 +390,116 @@ __device__ __attribute__((always_inline)) inline void big_epilogue(floatx16 (&ac
     }
 }
 
+// BF16 epilogue through LDS for the direct-to-LDS kernel: each wave stages
+// its own 64 x WTN output sub-tile in a private LDS region `wb` (row stride
+// WTN), so C is read (beta != 0) and written with 16-byte row vectors
+// instead of 2-byte column-layout accesses.  Same arithmetic as
+// big_epilogue: (1) alpha acc + beta C (+ bias) rounded in place, (2) the
+// LoRA terms pair by pair, (3) the store.  Only this wave touches wb, and a
+// wave's LDS operations complete in order.
+template <int TM, int TN, int WTM, int WTN>
+__device__ __attribute__((always_inline)) inline void staged_epilogue(
+    floatx16 (&acc)[TM][TN], const GemmArgs& a, int m0, int n0, int wm, int wn, int lane,
+    bf16* __restrict__ wb) {
+    constexpr int CPR = WTN / 8;  // 16-byte chunks per sub-tile row
+    const int R0 = m0 + wm * WTM, C0 = n0 + wn * WTN;
+    bf16* C = (bf16*)a.C;
+    const bool vec = ((a.ldc & 7) == 0) && (((uintptr_t)C & 15) == 0);
+    if (a.beta != 0.f) {
+#pragma unroll 4
+        for (int q = lane; q < WTM * CPR; q += 64) {
+            int row = q / CPR, ch = q % CPR;
+            int gm = R0 + row, gn = C0 + 8 * ch;
+            bf16x8v v;
+            if (gm < a.M && vec && gn + 8 <= a.N) {
+                v = *(const bf16x8v*)(C + (int64_t)gm * a.ldc + gn);
+            } else {
+                uint16_t t[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    t[e] = (gm < a.M && gn + e < a.N) ? C[(int64_t)gm * a.ldc + gn + e] : (uint16_t)0;
+#pragma unroll
+                for (int e = 0; e < 4; e++) v.w[e] = (uint32_t)t[2 * e] | ((uint32_t)t[2 * e + 1] << 16);
+            }
+            *(bf16x8v*)(wb + row * WTN + 8 * ch) = v;
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            int lc = j * 32 + (lane & 31);
+            int n = C0 + lc;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                int lr = i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                float o = a.alpha * acc[i][j][r];
+                if (a.beta != 0.f) o += a.beta * bf2f(wb[lr * WTN + lc]);
+                if (a.bias && n < a.N) o = bf2f(f2bf(o)) + bf2f(a.bias[n]);
+                acc[i][j][r] = bf2f(f2bf(o));
+            }
+        }
+#pragma unroll
+    for (int p = 0; p < 3; p++) {
+        if (p >= a.lora_n) break;
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                int arow = min(R0 + i * 32 + (lane & 31), a.M - 1);
+                int bcol = min(C0 + j * 32 + (lane & 31), a.N - 1);
+                floatx16 d;
+#pragma unroll
+                for (int r = 0; r < 16; r++) d[r] = 0.f;
+                for (int k = 0; k < a.lora_r; k += 16) {
+                    int kk = k + 8 * (lane >> 5);
+                    bf16x8_t fa, fb;
+                    if (kk < a.lora_r) {
+                        fa = *(const bf16x8_t*)(a.lora_u[p] + (int64_t)arow * a.lora_ldu[p] + kk);
+                        fb = *(const bf16x8_t*)(a.lora_v[p] + (int64_t)bcol * a.lora_r + kk);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 8; e++) fa[e] = fb[e] = (__bf16)0.f;
+                    }
+                    d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa, fb, d, 0, 0, 0);
+                }
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    acc[i][j][r] = a.lora_delta
+                                       ? bf2f(f2bf(acc[i][j][r] + a.lora_s * bf2f(f2bf(d[r]))))
+                                       : bf2f(f2bf(a.lora_s * d[r] + acc[i][j][r]));
+            }
+    }
+    __builtin_amdgcn_wave_barrier();  // the beta reads of wb are done
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) {
+            int lc = j * 32 + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                int lr = i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                wb[lr * WTN + lc] = f2bf(acc[i][j][r]);
+            }
+        }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll 4
+    for (int q = lane; q < WTM * CPR; q += 64) {
+        int row = q / CPR, ch = q % CPR;
+        int gm = R0 + row, gn = C0 + 8 * ch;
+        if (gm >= a.M) continue;
+        bf16x8v v = *(const bf16x8v*)(wb + row * WTN + 8 * ch);
+        if (vec && gn + 8 <= a.N) {
+            *(bf16x8v*)(C + (int64_t)gm * a.ldc + gn) = v;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                if (gn + e < a.N) C[(int64_t)gm * a.ldc + gn + e] = (uint16_t)(v.w[e >> 1] >> ((e & 1) * 16));
+        }
+    }
+}
+
 template <int BN, int WMW, int WNW, int EPI, int PIPE>
 __global__ __launch_bounds__(WMW * WNW * 64) void k_gemm_big(GemmArgs a) {
     constexpr int BM = 256, NTH = WMW * WNW * 64;
@@ -505,18 +615,20 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // Issue this wave's share of the loads of one stage: operand rows
 // [row0, row0 + ROWS) (clamped to rows - 1), k range [k0, k0 + 32).
-// Wave-instruction j covers stage rows 16j..16j+15.  Every wave issues
-// exactly two (straight-line code, so the compiler's wait bookkeeping stays
-// exact): j = w and j = w + 8; with 12 instructions (ROWS = 192) waves 4-7
-// repeat the second load of waves 0-3, writing the same bytes.
-template <int ROWS>
+// Wave-instruction j covers stage rows 16j..16j+15.  Every one of the NW
+// waves issues the same number, PER = ceil(NI / NW), in straight-line code
+// (so the compiler's wait bookkeeping stays exact): j = w + NW h; an index
+// past the end repeats an instruction of a lower wave, writing the same
+// bytes.
+template <int ROWS, int NW>
 __device__ __forceinline__ void dma_stage(const bf16* __restrict__ P, int64_t ld, int row0,
                                           int rows, int k0, bf16* stage, int w, int lane) {
     constexpr int NI = ROWS / 16;
-    static_assert(NI >= 8 && NI <= 16, "two loads per wave per operand");
+    constexpr int PER = (NI + NW - 1) / NW;
 #pragma unroll
-    for (int h = 0; h < 2; h++) {
-        int j = h == 0 ? w : (w + 8 < NI ? w + 8 : w + NI - 8);
+    for (int h = 0; h < PER; h++) {
+        int j = w + NW * h;
+        j = j < NI ? j : j - NW;
         int r = 16 * j + (lane >> 2);
         int c = (lane & 3) ^ dswz(r);
         int grow = min(row0 + r, rows - 1);
@@ -558,10 +670,16 @@ __device__ __attribute__((always_inline)) inline void dma_mma(floatx16 (&acc)[TM
 #define TA_WAIT_VMCNT(n) \
     __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
 
-template <int BN, int EPI>
-__global__ __launch_bounds__(512) void k_gemm_dma(GemmArgs a) {
-    constexpr int NS = 4;  // stages
-    constexpr int BM = 256, WMW = 4, WNW = 2;
+// 1 KB of zeros: the source of the tiles that pad K up to a whole number
+// of trips (they add exact zeros)
+static __device__ __attribute__((aligned(16))) bf16 g_dma_zero[512] = {};
+
+template <int BN, int EPI, int NS, int WMW, int WNW>
+__global__ __launch_bounds__(WMW * WNW * 64) void k_gemm_dma(GemmArgs a) {
+    static_assert(NS == 4 || NS == 5, "4 or 5 stages");
+    constexpr int BM = 256, NW = WMW * WNW;
+    // loads per stage per wave
+    constexpr int LPS = (BM / 16 + NW - 1) / NW + (BN / 16 + NW - 1) / NW;
     constexpr int WTM = BM / WMW, WTN = BN / WNW;
     constexpr int TM = WTM / 32, TN = WTN / 32;
     constexpr int SX = BM * DBK, SY = BN * DBK;  // elements per stage
@@ -569,6 +687,7 @@ __global__ __launch_bounds__(512) void k_gemm_dma(GemmArgs a) {
     // the loads into the buffer a read touches
     __shared__ __attribute__((aligned(1024))) bf16 sX0[SX], sX1[SX], sX2[SX], sX3[SX];
     __shared__ __attribute__((aligned(1024))) bf16 sY0[SY], sY1[SY], sY2[SY], sY3[SY];
+    __shared__ __attribute__((aligned(1024))) bf16 sX4[NS == 5 ? SX : 16], sY4[NS == 5 ? SY : 16];
 
     int nt = a.tiles_m * a.tiles_n;
     int bid = blockIdx.x;
@@ -589,47 +708,76 @@ __global__ __launch_bounds__(512) void k_gemm_dma(GemmArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
+    // K runs as tiles kt = -pad .. nk-1 (pad makes the count a multiple of
+    // NS; padded tiles load zeros).  Every step issues one stage (tiles
+    // past the end reload the last tile into a buffer that is never read),
+    // so exactly NS - 2 stages are issued after the one a step computes:
+    // LPS loads per stage per wave.
     const int nk = (kend - kbeg) / DBK;
-    // Every step issues one stage (tiles past the end reload the last tile
-    // into a buffer that is never read), so exactly NS - 2 stages are issued
-    // after the one a step computes: 4 loads per stage per wave.
-#define DMA_ISSUE(SXB, SYB, KT)                                                        \
-    do {                                                                               \
-        const int kk_ = min((KT), nk - 1);                                             \
-        dma_stage<BM>(a.X, a.ldx, m0, a.M, kbeg + kk_ * DBK, SXB, w, lane);            \
-        dma_stage<BN>(a.Y, a.ldy, n0, a.N, kbeg + kk_ * DBK, SYB, w, lane);            \
+    const int pad = (NS - nk % NS) % NS;
+    // (a padded tile reads row 0 of the zero buffer with stride 0: uniform
+    // selects, no branch)
+#define DMA_ISSUE(SXB, SYB, KT)                                                          \
+    do {                                                                                 \
+        const int kq_ = (KT);                                                            \
+        const bool z_ = kq_ < 0;                                                         \
+        const int k_ = z_ ? 0 : kbeg + min(kq_, nk - 1) * DBK;                          \
+        dma_stage<BM, NW>(z_ ? g_dma_zero : a.X, z_ ? 0 : a.ldx, m0, a.M, k_, SXB, w,    \
+                          lane);                                                         \
+        dma_stage<BN, NW>(z_ ? g_dma_zero : a.Y, z_ ? 0 : a.ldy, n0, a.N, k_, SYB, w,    \
+                          lane);                                                         \
     } while (0)
-    DMA_ISSUE(sX0, sY0, 0);
-    DMA_ISSUE(sX1, sY1, 1);
-    DMA_ISSUE(sX2, sY2, 2);
+    DMA_ISSUE(sX0, sY0, 0 - pad);
+    DMA_ISSUE(sX1, sY1, 1 - pad);
+    DMA_ISSUE(sX2, sY2, 2 - pad);
+    if constexpr (NS == 5) DMA_ISSUE(sX3, sY3, 3 - pad);
     // step on stage buffer J: wait for its loads, barrier (also: every wave
     // is done reading buffer JN), refill JN with tile kt + NS - 1, compute J
-    // (the dispatcher guarantees nk % NS == 0: no branch inside the loop
-    // body, which keeps the compiler's wait bookkeeping per buffer)
-#define DMA_STEP(J, SXJ, SYJ, SXN, SYN)                                                \
-    do {                                                                               \
-        TA_WAIT_VMCNT(4 * (NS - 2));                                                   \
-        __builtin_amdgcn_s_barrier();                                                  \
-        DMA_ISSUE(SXN, SYN, kt0 + (J) + NS - 1);                                       \
-        dma_mma<TM, TN, WTM, WTN>(acc, SXJ, SYJ, wm, wn, lane);                        \
+    // (no branch inside the loop body keeps the compiler's wait bookkeeping
+    // per buffer)
+#define DMA_STEP(J, SXJ, SYJ, SXN, SYN)                                                  \
+    do {                                                                                 \
+        TA_WAIT_VMCNT(LPS * (NS - 2));                                                   \
+        __builtin_amdgcn_s_barrier();                                                    \
+        DMA_ISSUE(SXN, SYN, kt0 + (J) + NS - 1);                                         \
+        dma_mma<TM, TN, WTM, WTN>(acc, SXJ, SYJ, wm, wn, lane);                          \
     } while (0)
-    for (int kt0 = 0; kt0 < nk; kt0 += NS) {
-        DMA_STEP(0, sX0, sY0, sX3, sY3);
-        DMA_STEP(1, sX1, sY1, sX0, sY0);
-        DMA_STEP(2, sX2, sY2, sX1, sY1);
-        DMA_STEP(3, sX3, sY3, sX2, sY2);
+    for (int kt0 = -pad; kt0 < nk; kt0 += NS) {
+        if constexpr (NS == 4) {
+            DMA_STEP(0, sX0, sY0, sX3, sY3);
+            DMA_STEP(1, sX1, sY1, sX0, sY0);
+            DMA_STEP(2, sX2, sY2, sX1, sY1);
+            DMA_STEP(3, sX3, sY3, sX2, sY2);
+        } else {
+            DMA_STEP(0, sX0, sY0, sX4, sY4);
+            DMA_STEP(1, sX1, sY1, sX0, sY0);
+            DMA_STEP(2, sX2, sY2, sX1, sY1);
+            DMA_STEP(3, sX3, sY3, sX2, sY2);
+            DMA_STEP(4, sX4, sY4, sX3, sY3);
+        }
     }
     TA_WAIT_VMCNT(0);  // the surplus loads have landed before the block ends
 #undef DMA_STEP
 #undef DMA_ISSUE
-    big_epilogue<TM, TN, WTM, WTN, EPI>(acc, a, m0, n0, wm, wn, lane);
+    if constexpr (EPI == EPI_BF16 && WMW * WNW == 8) {
+        // every wave is done with the stage buffers: each takes one of the
+        // eight as its private output staging region (64 x WTN BF16 fits)
+        static_assert(64 * WTN * 2 <= SY * 2 && 64 * WTN * 2 <= SX * 2, "staging fits");
+        __syncthreads();
+        bf16* wb = w == 0 ? sX0 : w == 1 ? sX1 : w == 2 ? sX2 : w == 3 ? sX3
+                 : w == 4 ? sY0 : w == 5 ? sY1 : w == 6 ? sY2 : sY3;
+        staged_epilogue<TM, TN, WTM, WTN>(acc, a, m0, n0, wm, wn, lane, wb);
+    } else {
+        big_epilogue<TM, TN, WTM, WTN, EPI>(acc, a, m0, n0, wm, wn, lane);
+    }
 }
 
 // Tile/pipeline variants of k_gemm_big; variant 0 is the default.
 static int g_big_variant = 0;
 static int big_bn(int variant) {
     return (variant == 1 || variant == 3) ? 128
-           : (variant == 4 || variant == 5 || variant == 6 || variant == 8) ? 256
+           : (variant == 4 || variant == 5 || variant == 6 || variant == 8 || variant == 10)
+               ? 256
                                                                             : 192;
 }
 
@@ -643,8 +791,11 @@ static const char* big_name(int variant) {
         case 4: return "void ta::k_gemm_big<256, 4, 2, 0, 1>(ta::GemmArgs)";
         case 5: return "void ta::k_gemm_big<256, 2, 4, 0, 1>(ta::GemmArgs)";
         case 6: return "void ta::k_gemm_big<256, 2, 2, 0, 1>(ta::GemmArgs)";
-        case 7: return "void ta::k_gemm_dma<192, 0>(ta::GemmArgs)";
-        case 8: return "void ta::k_gemm_dma<256, 0>(ta::GemmArgs)";
+        case 7: return "void ta::k_gemm_dma<192, 0, 4, 4, 2>(ta::GemmArgs)";
+        case 8: return "void ta::k_gemm_dma<256, 0, 4, 4, 2>(ta::GemmArgs)";
+        case 9: return "void ta::k_gemm_dma<192, 0, 5, 4, 2>(ta::GemmArgs)";
+        case 10: return "void ta::k_gemm_dma<256, 0, 4, 2, 2>(ta::GemmArgs)";
+        case 11: return "void ta::k_gemm_dma<192, 0, 4, 2, 2>(ta::GemmArgs)";
         default: return "void ta::k_gemm_big<192, 4, 2, 0, 1>(ta::GemmArgs)";
     }
 }
@@ -658,8 +809,11 @@ static void launch_big(int variant, dim3 grid, const GemmArgs& a, hipStream_t s)
         case 4: k_gemm_big<256, 4, 2, EPI, 1><<<grid, 512, 0, s>>>(a); break;
         case 5: k_gemm_big<256, 2, 4, EPI, 1><<<grid, 512, 0, s>>>(a); break;
         case 6: k_gemm_big<256, 2, 2, EPI, 1><<<grid, 256, 0, s>>>(a); break;
-        case 7: k_gemm_dma<192, EPI><<<grid, 512, 0, s>>>(a); break;
-        case 8: k_gemm_dma<256, EPI><<<grid, 512, 0, s>>>(a); break;
+        case 7: k_gemm_dma<192, EPI, 4, 4, 2><<<grid, 512, 0, s>>>(a); break;
+        case 8: k_gemm_dma<256, EPI, 4, 4, 2><<<grid, 512, 0, s>>>(a); break;
+        case 9: k_gemm_dma<192, EPI, 5, 4, 2><<<grid, 512, 0, s>>>(a); break;
+        case 10: k_gemm_dma<256, EPI, 4, 2, 2><<<grid, 256, 0, s>>>(a); break;
+        case 11: k_gemm_dma<192, EPI, 4, 2, 2><<<grid, 256, 0, s>>>(a); break;
         default: k_gemm_big<192, 4, 2, EPI, 1><<<grid, 512, 0, s>>>(a); break;
     }
 }
@@ -751,13 +905,10 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
     if (xk && yk && !out_f32 && M >= 1024 && N >= 1024 && (K % BK) == 0 && vx && vy) {
         // default: 256 x 192 tiles up to N = 3072 (N = 1536 gives one block per
         // CU at M = 8192), 256 x 256 for wider outputs
-        // default: the direct-to-LDS kernel (256 x 192 tiles; 256 x 256 for
-        // very wide outputs) when K is a multiple of its 128-wide trip,
-        // else the register-staged kernel (256 x 192, or 256 x 256 above
-        // N = 3072)
+        // default: the direct-to-LDS kernel, 256 x 192 tiles up to N = 3072
+        // (N = 1536 gives one block per CU at M = 8192), 256 x 256 above
         int variant = g_big_variant;
-        if (variant == 0) variant = (K % 128) == 0 ? (N > 65536 ? 8 : 7) : (N > 3072 ? 4 : 0);
-        if ((variant == 7 || variant == 8) && (K % 128) != 0) variant = variant == 8 ? 4 : 0;
+        if (variant == 0) variant = N > 3072 ? 8 : 7;
         const int BNb = big_bn(variant);
         a.tiles_m = (M + 255) / 256;
         a.tiles_n = (N + BNb - 1) / BNb;
@@ -770,7 +921,6 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
             splits = std::min((256 + tiles - 1) / tiles, ksteps / 16);
         if (splits < 1) splits = 1;
         int steps_per = (ksteps + splits - 1) / splits;
-        if (variant == 7 || variant == 8) steps_per = (steps_per + 1) & ~1;  // 128-multiples
         a.k_per_split = steps_per * BK;
         splits = (ksteps + steps_per - 1) / steps_per;
         dim3 grid(tiles, 1, splits);
@@ -902,7 +1052,7 @@ using namespace ta;
 extern "C" {
 
 int ta_gemm_variant(int v) {
-    TA_REQUIRE(v >= 0 && v <= 8, "gemm_variant: %d out of range", v);
+    TA_REQUIRE(v >= 0 && v <= 11, "gemm_variant: %d out of range", v);
     g_big_variant = v;
     return 0;
 }
