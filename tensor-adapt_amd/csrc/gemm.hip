@@ -303,6 +303,22 @@ __device__ __attribute__((always_inline)) inline void big_mma(floatx16 (&acc)[TM
     }
 }
 
+// Tile of a block for the large kernels.  Blocks are dealt round-robin to
+// the 8 XCDs (each with its own L2); each XCD gets a contiguous range of
+// tile indices, walked in groups of GM tile-rows column by column, so the
+// ~32 tiles an XCD runs at once share GM row bands of X and a few column
+// bands of Y in its L2 instead of streaming all of Y.
+constexpr int TILE_GM = 4;
+__device__ __forceinline__ void big_tile(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+    int nt = tiles_m * tiles_n;
+    if ((nt & 7) == 0) bid = (bid & 7) * (nt >> 3) + (bid >> 3);
+    int gsz = TILE_GM * tiles_n;
+    int g = bid / gsz, idx = bid % gsz;
+    int rows = min(TILE_GM, tiles_m - g * TILE_GM);
+    tm = g * TILE_GM + idx % rows;
+    tn = idx / rows;
+}
+
 // Epilogue of the large GEMM kernels on the 32x32 MFMA accumulator layout
 // (lane: column l%32, rows 8*(r/4) + 4*(l/32) + r%4 of each fragment).
 template <int TM, int TN, int WTM, int WTN, int EPI>
@@ -406,7 +422,7 @@ __device__ __attribute__((always_inline)) inline void staged_epilogue(
     bf16* C = (bf16*)a.C;
     const bool vec = ((a.ldc & 7) == 0) && (((uintptr_t)C & 15) == 0);
     if (a.beta != 0.f) {
-#pragma unroll 4
+#pragma unroll
         for (int q = lane; q < WTM * CPR; q += 64) {
             int row = q / CPR, ch = q % CPR;
             int gm = R0 + row, gn = C0 + 8 * ch;
@@ -484,7 +500,7 @@ __device__ __attribute__((always_inline)) inline void staged_epilogue(
             }
         }
     __builtin_amdgcn_wave_barrier();
-#pragma unroll 4
+#pragma unroll
     for (int q = lane; q < WTM * CPR; q += 64) {
         int row = q / CPR, ch = q % CPR;
         int gm = R0 + row, gn = C0 + 8 * ch;
@@ -509,10 +525,8 @@ __global__ __launch_bounds__(WMW * WNW * 64) void k_gemm_big(GemmArgs a) {
     __shared__ __attribute__((aligned(16))) bf16 sX[2][BM * LDS_STRIDE];
     __shared__ __attribute__((aligned(16))) bf16 sY[2][BN * LDS_STRIDE];
 
-    int nt = a.tiles_m * a.tiles_n;
-    int bid = blockIdx.x;
-    if ((nt & 7) == 0) bid = (bid & 7) * (nt >> 3) + (bid >> 3);
-    int tm_i = bid / a.tiles_n, tn_i = bid % a.tiles_n;
+    int tm_i, tn_i;
+    big_tile(blockIdx.x, a.tiles_m, a.tiles_n, tm_i, tn_i);
     int m0 = tm_i * BM, n0 = tn_i * BN;
     int kbeg = blockIdx.z * a.k_per_split;
     int kend = min(a.K, kbeg + a.k_per_split);
@@ -689,10 +703,8 @@ __global__ __launch_bounds__(WMW * WNW * 64) void k_gemm_dma(GemmArgs a) {
     __shared__ __attribute__((aligned(1024))) bf16 sY0[SY], sY1[SY], sY2[SY], sY3[SY];
     __shared__ __attribute__((aligned(1024))) bf16 sX4[NS == 5 ? SX : 16], sY4[NS == 5 ? SY : 16];
 
-    int nt = a.tiles_m * a.tiles_n;
-    int bid = blockIdx.x;
-    if ((nt & 7) == 0) bid = (bid & 7) * (nt >> 3) + (bid >> 3);
-    int tm_i = bid / a.tiles_n, tn_i = bid % a.tiles_n;
+    int tm_i, tn_i;
+    big_tile(blockIdx.x, a.tiles_m, a.tiles_n, tm_i, tn_i);
     int m0 = tm_i * BM, n0 = tn_i * BN;
     int kbeg = blockIdx.z * a.k_per_split;
     int kend = min(a.K, kbeg + a.k_per_split);
