@@ -145,9 +145,11 @@ int ta_gemm_rm(int x_kmajor, int y_kmajor, int M, int N, int K, float alpha,
                const uint16_t* X, int ldx, const uint16_t* Y, int ldy, float beta,
                uint16_t* C, int ldc, const uint16_t* bias, void* stream);
 
-/* Tile/pipeline variant of the large K-contiguous GEMM kernel (0 = the
- * default; 1..3 alternatives kept for tuning sweeps).  No reference
- * counterpart. */
+/* Kernel variant of the large K-contiguous GEMMs, for tuning sweeps:
+ * 0 = the default (the 4-wave pipelined kernel, 192- or 256-wide tiles by
+ * N), 7..11 = the 8-/4-wave direct-to-LDS kernel shapes, 12/13 = the
+ * pipelined kernel with 192/256-wide tiles.  Other values return an error.
+ * No reference counterpart. */
 int ta_gemm_variant(int variant);
 
 /* ── centroid accumulator ───────────────────────────────────────────

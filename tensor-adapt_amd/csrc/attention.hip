@@ -548,7 +548,7 @@ __device__ __forceinline__ void load_p_cols(float (&p)[4][4], const float* __res
 // group sum of ops.cu:539-555 without atomics, so dK/dV are deterministic.
 // The next query tile's dO, Q, D and P are loaded while this one computes.
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_bwd_dkv(const bf16* __restrict__ dO,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_bwd_dkv(const bf16* __restrict__ dO,
                                                       const bf16* __restrict__ Q,
                                                       const bf16* __restrict__ V,
                                                       const float* __restrict__ P,

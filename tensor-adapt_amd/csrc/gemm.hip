@@ -25,6 +25,9 @@
 // rounding and rounded again — the reference's gemm + ops::add_bias), F32
 // (gemm_f32 semantics), or F32 partials for split-K with a separate
 // fixed-order reduction (deterministic).
+#include <algorithm>
+#include <type_traits>
+
 #include "ta_internal.hpp"
 
 namespace ta {
@@ -244,64 +247,7 @@ __global__ __launch_bounds__(256) void k_gemm(GemmArgs a, bool vecx, bool vecy) 
 }
 
 // ── Large K-contiguous GEMMs (every frozen-base projection, the LM head) ──
-// Block tile 256 x BN with NW = WMW x WNW waves (NW*64 threads), wave tile
-// (256/WMW) x (BN/WNW) of 32x32 MFMA tiles.  With 8 waves two share each
-// SIMD, which hides LDS and global latency without deep software
-// pipelining.  Two LDS stages and two register staging sets: the global
-// loads of tile k+2 are issued before the MFMAs of tile k and stored after
-// the MFMAs of tile k+1, so each load has two iterations of matrix work to
-// arrive.  Staging is branch-free: K is a multiple of 64 and rows are
-// 16-byte aligned (the dispatcher checks), and rows past the end are
-// clamped to the last row — their products land only in output rows and
-// columns that are never stored.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-template <int ROWS, int NTH>
-struct FastLoader {
-    static constexpr int PT = ROWS * BK / 8 / NTH;
-    static_assert(PT * NTH * 8 == ROWS * BK, "tile must split evenly over the threads");
-    u32x4 r[PT];  // a native vector type: stays in registers
-    __device__ __forceinline__ void load(const bf16* __restrict__ P, int64_t ld, int row0, int k0,
-                                         int rows) {
-#pragma unroll
-        for (int i = 0; i < PT; i++) {
-            int q = threadIdx.x + NTH * i;
-            int row = min(row0 + (q >> 3), rows - 1);
-            r[i] = *(const u32x4*)(P + (int64_t)row * ld + k0 + (q & 7) * 8);
-        }
-    }
-    __device__ __forceinline__ void store(bf16* __restrict__ S) {
-#pragma unroll
-        for (int i = 0; i < PT; i++) {
-            int q = threadIdx.x + NTH * i;
-            *(u32x4*)(S + (q >> 3) * LDS_STRIDE + (q & 7) * 8) = r[i];
-        }
-    }
-};
-
-// One BK slice of MFMAs for a wave (kept out of line of the loop body but
-// always inlined, so the accumulators stay in registers).
-template <int TM, int TN, int WTM, int WTN>
-__device__ __attribute__((always_inline)) inline void big_mma(floatx16 (&acc)[TM][TN],
-                                                              const bf16* SXb, const bf16* SYb,
-                                                              int wm, int wn, int lane) {
-    const bf16* SX = SXb + (wm * WTM + (lane & 31)) * LDS_STRIDE + (lane >> 5) * 8;
-    const bf16* SY = SYb + (wn * WTN + (lane & 31)) * LDS_STRIDE + (lane >> 5) * 8;
-#pragma unroll
-    for (int kk = 0; kk < BK / 16; kk++) {
-        bf16x8_t fx[TM], fy[TN];
-#pragma unroll
-        for (int i = 0; i < TM; i++) fx[i] = *(const bf16x8_t*)(SX + i * 32 * LDS_STRIDE + kk * 16);
-#pragma unroll
-        for (int j = 0; j < TN; j++) fy[j] = *(const bf16x8_t*)(SY + j * 32 * LDS_STRIDE + kk * 16);
-#pragma unroll
-        for (int i = 0; i < TM; i++)
-#pragma unroll
-            for (int j = 0; j < TN; j++)
-                acc[i][j] =
-                    __builtin_amdgcn_mfma_f32_32x32x16_bf16(fx[i], fy[j], acc[i][j], 0, 0, 0);
-    }
-}
 
 // Tile of a block for the large kernels.  Blocks are dealt round-robin to
 // the 8 XCDs (each with its own L2); each XCD gets a contiguous range of
@@ -362,7 +308,7 @@ __device__ __attribute__((always_inline)) inline void big_epilogue(floatx16 (&ac
         // would move it to scratch)
 #pragma unroll
         for (int p = 0; p < 3; p++) {
-            if (p >= a.lora_n) break;
+            if (p >= a.lora_n) continue;
 #pragma unroll
             for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -458,7 +404,7 @@ __device__ __attribute__((always_inline)) inline void staged_epilogue(
         }
 #pragma unroll
     for (int p = 0; p < 3; p++) {
-        if (p >= a.lora_n) break;
+        if (p >= a.lora_n) continue;
 #pragma unroll
         for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -515,106 +461,6 @@ __device__ __attribute__((always_inline)) inline void staged_epilogue(
         }
     }
 }
-
-template <int BN, int WMW, int WNW, int EPI, int PIPE>
-__global__ __launch_bounds__(WMW * WNW * 64) void k_gemm_big(GemmArgs a) {
-    constexpr int BM = 256, NTH = WMW * WNW * 64;
-    constexpr int WTM = BM / WMW, WTN = BN / WNW;
-    constexpr int TM = WTM / 32, TN = WTN / 32;
-    static_assert(TM * 32 == WTM && TN * 32 == WTN, "wave tile must be 32-aligned");
-    __shared__ __attribute__((aligned(16))) bf16 sX[2][BM * LDS_STRIDE];
-    __shared__ __attribute__((aligned(16))) bf16 sY[2][BN * LDS_STRIDE];
-
-    int tm_i, tn_i;
-    big_tile(blockIdx.x, a.tiles_m, a.tiles_n, tm_i, tn_i);
-    int m0 = tm_i * BM, n0 = tn_i * BN;
-    int kbeg = blockIdx.z * a.k_per_split;
-    int kend = min(a.K, kbeg + a.k_per_split);
-    int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-    int wm = wv / WNW, wn = wv % WNW;
-
-    floatx16 acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int j = 0; j < TN; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
-
-    FastLoader<BM, NTH> lx0;
-    FastLoader<BN, NTH> ly0;
-    FastLoader<BM, PIPE == 2 ? NTH : BM * BK / 8> lx1;  // unused when PIPE == 1
-    FastLoader<BN, PIPE == 2 ? NTH : BN * BK / 8> ly1;
-    const int nk = (kend - kbeg) / BK;
-
-#define compute(SXb, SYb) big_mma<TM, TN, WTM, WTN>(acc, SXb, SYb, wm, wn, lane)
-    if constexpr (PIPE == 1) {
-        // one staging set: tile k+1 is loaded while tile k feeds the MFMAs
-        if (nk > 0) {
-            lx0.load(a.X, a.ldx, m0, kbeg, a.M);
-            ly0.load(a.Y, a.ldy, n0, kbeg, a.N);
-            lx0.store(sX[0]);
-            ly0.store(sY[0]);
-        }
-        __syncthreads();
-        for (int kt = 0; kt < nk; kt++) {
-            const int cur = kt & 1;
-            const bool more = kt + 1 < nk;
-            if (more) {
-                lx0.load(a.X, a.ldx, m0, kbeg + (kt + 1) * BK, a.M);
-                ly0.load(a.Y, a.ldy, n0, kbeg + (kt + 1) * BK, a.N);
-            }
-            compute(sX[cur], sY[cur]);
-            if (more) {
-                lx0.store(sX[cur ^ 1]);
-                ly0.store(sY[cur ^ 1]);
-            }
-            __syncthreads();
-        }
-    } else {
-        if (nk > 0) {
-            lx0.load(a.X, a.ldx, m0, kbeg, a.M);
-            ly0.load(a.Y, a.ldy, n0, kbeg, a.N);
-            lx0.store(sX[0]);
-            ly0.store(sY[0]);
-            if (nk > 1) {
-                lx1.load(a.X, a.ldx, m0, kbeg + BK, a.M);
-                ly1.load(a.Y, a.ldy, n0, kbeg + BK, a.N);
-            }
-        }
-        __syncthreads();
-        // two k-tiles per trip so the staging set of each tile is static
-        for (int kt = 0; kt < nk; kt += 2) {
-            // even tile kt: data in LDS stage 0; tile kt+1 sits in set 1
-            if (kt + 2 < nk) {
-                lx0.load(a.X, a.ldx, m0, kbeg + (kt + 2) * BK, a.M);
-                ly0.load(a.Y, a.ldy, n0, kbeg + (kt + 2) * BK, a.N);
-            }
-            compute(sX[0], sY[0]);
-            if (kt + 1 < nk) {
-                lx1.store(sX[1]);
-                ly1.store(sY[1]);
-            }
-            __syncthreads();
-            if (kt + 1 >= nk) break;
-            // odd tile kt+1: LDS stage 1; tile kt+2 sits in set 0
-            if (kt + 3 < nk) {
-                lx1.load(a.X, a.ldx, m0, kbeg + (kt + 3) * BK, a.M);
-                ly1.load(a.Y, a.ldy, n0, kbeg + (kt + 3) * BK, a.N);
-            }
-            compute(sX[1], sY[1]);
-            if (kt + 2 < nk) {
-                lx0.store(sX[0]);
-                ly0.store(sY[0]);
-            }
-            __syncthreads();
-        }
-    }
-
-    big_epilogue<TM, TN, WTM, WTN, EPI>(acc, a, m0, n0, wm, wn, lane);
-}
-
-#undef compute
 
 // ── k_gemm_dma: the same tiles fed by direct global->LDS loads ────────────
 // BK = 32 per stage (rows of 64 bytes = 4 chunks of 16 bytes) and NS stages
@@ -784,49 +630,304 @@ __global__ __launch_bounds__(WMW * WNW * 64) void k_gemm_dma(GemmArgs a) {
     }
 }
 
-// Tile/pipeline variants of k_gemm_big; variant 0 is the default.
+// ── k_gemm_pipe: one wave per SIMD, fragment double buffering ───────────
+// The default kernel of the large GEMMs.  Block tile 256 x BN (BN = 192 or
+// 256), 4 wave64s in a 2 x 2 arrangement, each owning a 128 x BN/2 wave
+// tile: 4 x BN/64 accumulator fragments of v_mfma_f32_32x32x16_bf16 held in
+// AGPRs (192 or 256), so one wave per SIMD feeds the matrix core on its own.
+// The stages are the direct-to-LDS stages of k_gemm_dma (32-wide k slices,
+// 4 stages in flight, swizzled rows).  Each step of the loop computes one
+// stage in two 16-wide halves: the fragments of the second half are read
+// from LDS while the first half's MFMAs run, and the fragments of the next
+// stage's first half while the second half's run, so LDS latency never
+// sits between two MFMA batches.  One barrier per stage, placed between the
+// halves: after it the next stage has landed for every wave and the buffer
+// read two stages ago is free for the next DMA.
+template <int TM, int TN>
+struct Frags {
+    bf16x8_t a[TM], b[TN];
+};
+
+template <int TM, int TN, int WTM, int WTN>
+__device__ __forceinline__ void pipe_frags(Frags<TM, TN>& f, const bf16* sX, const bf16* sY,
+                                           int wm, int wn, int lane, int kk) {
+    const int c = 2 * kk + (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        int R = wm * WTM + i * 32 + (lane & 31);
+        f.a[i] = *(const bf16x8_t*)(sX + R * DBK + 8 * (c ^ dswz(R)));
+    }
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+        int R = wn * WTN + j * 32 + (lane & 31);
+        f.b[j] = *(const bf16x8_t*)(sY + R * DBK + 8 * (c ^ dswz(R)));
+    }
+}
+
+template <int TM, int TN>
+__device__ __forceinline__ void pipe_mma(floatx16 (&acc)[TM][TN], const Frags<TM, TN>& f) {
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+}
+
+// scheduling hint for the region just emitted: alternate one MFMA with one
+// LDS read while reads remain
+template <int NM, int ND>
+__device__ __forceinline__ void pipe_interleave() {
+#pragma unroll
+    for (int i = 0; i < NM; i++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);                // MFMA
+        if (i < ND) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);    // DS read
+    }
+}
+
+// compile-time loop: f(integral_constant<0>) ... f(integral_constant<N-1>)
+template <int N, typename F>
+__device__ __attribute__((always_inline)) inline void static_for(F&& f) {
+    if constexpr (N > 0) {
+        static_for<N - 1>(f);
+        f(std::integral_constant<int, N - 1>{});
+    }
+}
+
+// Epilogue of one 64-row half (row fragments I0, I0 + 1) of a wave tile,
+// staged in the wave's private LDS region wb (64 x WTN BF16).  Same
+// arithmetic as big_epilogue, fragment by fragment: alpha acc + beta C
+// (+ bias) rounded, then each LoRA term (rank <= 16: one MFMA k step, its
+// operand fragments loaded up front), then the BF16 value into wb; the half
+// leaves as 16-byte row vectors.  A lane reads and writes the same wb words
+// for a fragment, so only the final read-back needs the wave barrier.
+template <int TM, int TN, int WTN, int I0, int PF>
+__device__ __attribute__((always_inline)) inline void pipe_half_epilogue(
+    floatx16 (&acc)[TM][TN], const GemmArgs& a, int R0, int C0, int lane, bf16* __restrict__ wb) {
+    constexpr int CPR = WTN / 8;
+    bf16* C = (bf16*)a.C;
+    const bool vec = ((a.ldc & 7) == 0) && (((uintptr_t)C & 15) == 0);
+    if (a.beta != 0.f) {
+        for (int q = lane; q < 64 * CPR; q += 64) {
+            int row = q / CPR, ch = q % CPR;
+            int gm = R0 + row, gn = C0 + 8 * ch;
+            bf16x8v v;
+            if (gm < a.M && vec && gn + 8 <= a.N) {
+                v = *(const bf16x8v*)(C + (int64_t)gm * a.ldc + gn);
+            } else {
+                uint16_t t[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    t[e] = (gm < a.M && gn + e < a.N) ? C[(int64_t)gm * a.ldc + gn + e] : (uint16_t)0;
+#pragma unroll
+                for (int e = 0; e < 4; e++) v.w[e] = (uint32_t)t[2 * e] | ((uint32_t)t[2 * e + 1] << 16);
+            }
+            *(bf16x8v*)(wb + row * WTN + 8 * ch) = v;
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+    const int kk = 8 * (lane >> 5);
+    const bool kin = kk < a.lora_r;
+    bf16x8_t fu[PF][2], fv[PF][TN];
+#pragma unroll
+    for (int p = 0; p < PF; p++) {
+        if (p < a.lora_n) {
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                int row = min(R0 + 32 * i + (lane & 31), a.M - 1);
+                fu[p][i] = *(const bf16x8_t*)(a.lora_u[p] + (int64_t)row * a.lora_ldu[p] + (kin ? kk : 0));
+            }
+#pragma unroll
+            for (int j = 0; j < TN; j++) {
+                int col = min(C0 + 32 * j + (lane & 31), a.N - 1);
+                fv[p][j] = *(const bf16x8_t*)(a.lora_v[p] + (int64_t)col * a.lora_r + (kin ? kk : 0));
+            }
+            if (!kin) {
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    fu[p][0][e] = fu[p][1][e] = (__bf16)0.f;
+#pragma unroll
+                    for (int j = 0; j < TN; j++) fv[p][j][e] = (__bf16)0.f;
+                }
+            }
+        }
+    }
+    static_for<2 * TN>([&](auto ij) {
+        constexpr int i = decltype(ij)::value / TN, j = decltype(ij)::value % TN;
+        const int lc = j * 32 + (lane & 31);
+        const int n = C0 + lc;
+        const float bias = (a.bias && n < a.N) ? bf2f(a.bias[n]) : 0.f;
+        float v[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int lr = i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            float o = a.alpha * acc[I0 + i][j][r];
+            if (a.beta != 0.f) o += a.beta * bf2f(wb[lr * WTN + lc]);
+            if (a.bias) o = bf2f(f2bf(o)) + bias;
+            v[r] = bf2f(f2bf(o));
+        }
+#pragma unroll
+        for (int p = 0; p < 3; p++) {
+            if (p < a.lora_n) {
+                floatx16 d;
+#pragma unroll
+                for (int r = 0; r < 16; r++) d[r] = 0.f;
+                bf16x8_t ua, vb;
+                if (p < PF) {
+                    ua = fu[p < PF ? p : 0][i];
+                    vb = fv[p < PF ? p : 0][j];
+                } else {
+                    const int row = min(R0 + 32 * i + (lane & 31), a.M - 1);
+                    const int col = min(n, a.N - 1);
+                    ua = *(const bf16x8_t*)(a.lora_u[p] + (int64_t)row * a.lora_ldu[p] + (kin ? kk : 0));
+                    vb = *(const bf16x8_t*)(a.lora_v[p] + (int64_t)col * a.lora_r + (kin ? kk : 0));
+                    if (!kin) {
+#pragma unroll
+                        for (int e = 0; e < 8; e++) ua[e] = vb[e] = (__bf16)0.f;
+                    }
+                }
+                d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ua, vb, d, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    v[r] = a.lora_delta ? bf2f(f2bf(v[r] + a.lora_s * bf2f(f2bf(d[r]))))
+                                        : bf2f(f2bf(a.lora_s * d[r] + v[r]));
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int lr = i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+            wb[lr * WTN + lc] = f2bf(v[r]);
+        }
+    });
+    __builtin_amdgcn_wave_barrier();
+    for (int q = lane; q < 64 * CPR; q += 64) {
+        int row = q / CPR, ch = q % CPR;
+        int gm = R0 + row, gn = C0 + 8 * ch;
+        if (gm >= a.M) continue;
+        bf16x8v v = *(const bf16x8v*)(wb + row * WTN + 8 * ch);
+        if (vec && gn + 8 <= a.N) {
+            *(bf16x8v*)(C + (int64_t)gm * a.ldc + gn) = v;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+                if (gn + e < a.N) C[(int64_t)gm * a.ldc + gn + e] = (uint16_t)(v.w[e >> 1] >> ((e & 1) * 16));
+        }
+    }
+}
+
+template <int BN>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_gemm_pipe(
+    GemmArgs a) {
+    constexpr int NS = 4, BM = 256, NW = 4, WNW = 2;
+    constexpr int WTM = 128, WTN = BN / 2;
+    constexpr int TM = WTM / 32, TN = WTN / 32;
+    constexpr int LPS = BM / 16 / NW + BN / 16 / NW;  // DMA instructions per stage per wave
+    constexpr int SX = BM * DBK, SY = BN * DBK;
+    static_assert(BN == 192 || BN == 256, "tile width");
+    __shared__ __attribute__((aligned(1024))) bf16 sX0[SX], sX1[SX], sX2[SX], sX3[SX];
+    __shared__ __attribute__((aligned(1024))) bf16 sY0[SY], sY1[SY], sY2[SY], sY3[SY];
+
+    int tm_i, tn_i;
+    big_tile(blockIdx.x, a.tiles_m, a.tiles_n, tm_i, tn_i);
+    const int m0 = tm_i * BM, n0 = tn_i * BN;
+    int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int wm = w / WNW, wn = w % WNW;
+    w = __builtin_amdgcn_readfirstlane(w);
+
+    floatx16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+    // K runs as stages kt = -pad .. nk-1 (pad zero stages make the count a
+    // multiple of NS; stages past the end reload the last one into a buffer
+    // that is never read), as in k_gemm_dma
+    const int nk = a.K / DBK;
+    const int pad = (NS - nk % NS) % NS;
+#define PIPE_ISSUE(SXB, SYB, KT)                                                           \
+    do {                                                                                   \
+        const int kq_ = (KT);                                                              \
+        const bool z_ = kq_ < 0;                                                           \
+        const int k_ = z_ ? 0 : min(kq_, nk - 1) * DBK;                                    \
+        dma_stage<BM, NW>(z_ ? g_dma_zero : a.X, z_ ? 0 : a.ldx, m0, a.M, k_, SXB, w, lane); \
+        dma_stage<BN, NW>(z_ ? g_dma_zero : a.Y, z_ ? 0 : a.ldy, n0, a.N, k_, SYB, w, lane); \
+    } while (0)
+    PIPE_ISSUE(sX0, sY0, 0 - pad);
+    PIPE_ISSUE(sX1, sY1, 1 - pad);
+    PIPE_ISSUE(sX2, sY2, 2 - pad);
+    TA_WAIT_VMCNT(LPS * (NS - 2));
+    __builtin_amdgcn_s_barrier();
+    Frags<TM, TN> f0, f1;
+    pipe_frags<TM, TN, WTM, WTN>(f0, sX0, sY0, wm, wn, lane, 0);
+    // step J: second-half fragments of stage J while the first half
+    // computes; wait for stage J+1 (NS - 3 stages may stay in flight);
+    // barrier; refill the buffer of stage J-1 with stage J+NS-1; first-half
+    // fragments of stage J+1 while the second half computes
+#define PIPE_STEP(J, SXJ, SYJ, SXN, SYN, SXR, SYR)                                         \
+    do {                                                                                   \
+        pipe_frags<TM, TN, WTM, WTN>(f1, SXJ, SYJ, wm, wn, lane, 1);                       \
+        pipe_mma<TM, TN>(acc, f0);                                                         \
+        pipe_interleave<TM * TN, TM + TN>();                                               \
+        TA_WAIT_VMCNT(LPS * (NS - 3));                                                     \
+        __builtin_amdgcn_s_barrier();                                                      \
+        PIPE_ISSUE(SXR, SYR, kt0 + (J) + NS - 1);                                          \
+        pipe_frags<TM, TN, WTM, WTN>(f0, SXN, SYN, wm, wn, lane, 0);                       \
+        pipe_mma<TM, TN>(acc, f1);                                                         \
+        pipe_interleave<TM * TN, TM + TN>();                                               \
+    } while (0)
+    for (int kt0 = -pad; kt0 < nk; kt0 += NS) {
+        PIPE_STEP(0, sX0, sY0, sX1, sY1, sX3, sY3);
+        PIPE_STEP(1, sX1, sY1, sX2, sY2, sX0, sY0);
+        PIPE_STEP(2, sX2, sY2, sX3, sY3, sX1, sY1);
+        PIPE_STEP(3, sX3, sY3, sX0, sY0, sX2, sY2);
+    }
+    TA_WAIT_VMCNT(0);  // the surplus loads have landed before the buffers are reused
+#undef PIPE_STEP
+#undef PIPE_ISSUE
+    __syncthreads();
+    // each wave stages its two 64-row halves in two stage buffers of its own
+    bf16* wb0 = w == 0 ? sX0 : w == 1 ? sX1 : w == 2 ? sX2 : sX3;
+    bf16* wb1 = w == 0 ? sY0 : w == 1 ? sY1 : w == 2 ? sY2 : sY3;
+    static_assert(64 * WTN <= SX && 64 * WTN <= SY, "staging fits a stage buffer");
+    pipe_half_epilogue<TM, TN, WTN, 0, BN == 256 ? 1 : 3>(acc, a, m0 + wm * WTM, n0 + wn * WTN, lane, wb0);
+    pipe_half_epilogue<TM, TN, WTN, 2, BN == 256 ? 1 : 3>(acc, a, m0 + wm * WTM + 64, n0 + wn * WTN, lane, wb1);
+}
+
+// Kernel variants of the large GEMMs (ta_gemm_variant): 0 picks k_gemm_pipe
+// (256 x 192 tiles up to N = 3072, 256 x 256 above; N = 1536 then gives one
+// block per CU at M = 8192); 7..11 are k_gemm_dma shapes kept for sweeps
+// and for the split-K partials; 12/13 force k_gemm_pipe 192/256.
 static int g_big_variant = 0;
+static bool variant_ok(int v) { return v == 0 || (v >= 7 && v <= 13); }
+static bool is_pipe(int variant) { return variant == 12 || variant == 13; }
 static int big_bn(int variant) {
-    return (variant == 1 || variant == 3) ? 128
-           : (variant == 4 || variant == 5 || variant == 6 || variant == 8 || variant == 10)
-               ? 256
-                                                                            : 192;
+    return (variant == 8 || variant == 10 || variant == 13) ? 256 : 192;
 }
 
 // symbol of the unsplit BF16-output instance of each variant, as printed
 // by the profiler
 static const char* big_name(int variant) {
     switch (variant) {
-        case 1: return "void ta::k_gemm_big<128, 2, 2, 0, 1>(ta::GemmArgs)";
-        case 2: return "void ta::k_gemm_big<192, 2, 2, 0, 1>(ta::GemmArgs)";
-        case 3: return "void ta::k_gemm_big<128, 4, 2, 0, 2>(ta::GemmArgs)";
-        case 4: return "void ta::k_gemm_big<256, 4, 2, 0, 1>(ta::GemmArgs)";
-        case 5: return "void ta::k_gemm_big<256, 2, 4, 0, 1>(ta::GemmArgs)";
-        case 6: return "void ta::k_gemm_big<256, 2, 2, 0, 1>(ta::GemmArgs)";
         case 7: return "void ta::k_gemm_dma<192, 0, 4, 4, 2>(ta::GemmArgs)";
         case 8: return "void ta::k_gemm_dma<256, 0, 4, 4, 2>(ta::GemmArgs)";
         case 9: return "void ta::k_gemm_dma<192, 0, 5, 4, 2>(ta::GemmArgs)";
         case 10: return "void ta::k_gemm_dma<256, 0, 4, 2, 2>(ta::GemmArgs)";
         case 11: return "void ta::k_gemm_dma<192, 0, 4, 2, 2>(ta::GemmArgs)";
-        default: return "void ta::k_gemm_big<192, 4, 2, 0, 1>(ta::GemmArgs)";
+        case 13: return "void ta::k_gemm_pipe<256>(ta::GemmArgs)";
+        default: return "void ta::k_gemm_pipe<192>(ta::GemmArgs)";
     }
 }
 
 template <int EPI>
 static void launch_big(int variant, dim3 grid, const GemmArgs& a, hipStream_t s) {
     switch (variant) {
-        case 1: k_gemm_big<128, 2, 2, EPI, 1><<<grid, 256, 0, s>>>(a); break;
-        case 2: k_gemm_big<192, 2, 2, EPI, 1><<<grid, 256, 0, s>>>(a); break;
-        case 3: k_gemm_big<128, 4, 2, EPI, 2><<<grid, 512, 0, s>>>(a); break;
-        case 4: k_gemm_big<256, 4, 2, EPI, 1><<<grid, 512, 0, s>>>(a); break;
-        case 5: k_gemm_big<256, 2, 4, EPI, 1><<<grid, 512, 0, s>>>(a); break;
-        case 6: k_gemm_big<256, 2, 2, EPI, 1><<<grid, 256, 0, s>>>(a); break;
-        case 7: k_gemm_dma<192, EPI, 4, 4, 2><<<grid, 512, 0, s>>>(a); break;
         case 8: k_gemm_dma<256, EPI, 4, 4, 2><<<grid, 512, 0, s>>>(a); break;
         case 9: k_gemm_dma<192, EPI, 5, 4, 2><<<grid, 512, 0, s>>>(a); break;
         case 10: k_gemm_dma<256, EPI, 4, 2, 2><<<grid, 256, 0, s>>>(a); break;
         case 11: k_gemm_dma<192, EPI, 4, 2, 2><<<grid, 256, 0, s>>>(a); break;
-        default: k_gemm_big<192, 4, 2, EPI, 1><<<grid, 512, 0, s>>>(a); break;
+        default: k_gemm_dma<192, EPI, 4, 4, 2><<<grid, 512, 0, s>>>(a); break;
     }
 }
 
@@ -913,14 +1014,10 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
     bool vx = al16(X) && (ldx % 8) == 0;
     bool vy = al16(Y) && (ldy % 8) == 0;
 
-    // large K-contiguous BF16 GEMMs: 256 x 192 tiles, 8 waves
+    // large K-contiguous BF16 GEMMs: k_gemm_pipe (k_gemm_dma for split-K)
     if (xk && yk && !out_f32 && M >= 1024 && N >= 1024 && (K % BK) == 0 && vx && vy) {
-        // default: 256 x 192 tiles up to N = 3072 (N = 1536 gives one block per
-        // CU at M = 8192), 256 x 256 for wider outputs
-        // default: the direct-to-LDS kernel, 256 x 192 tiles up to N = 3072
-        // (N = 1536 gives one block per CU at M = 8192), 256 x 256 above
         int variant = g_big_variant;
-        if (variant == 0) variant = N > 3072 ? 8 : 7;
+        if (variant == 0) variant = N > 3072 ? 13 : 12;
         const int BNb = big_bn(variant);
         a.tiles_m = (M + 255) / 256;
         a.tiles_n = (N + BNb - 1) / BNb;
@@ -937,6 +1034,8 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
         splits = (ksteps + steps_per - 1) / steps_per;
         dim3 grid(tiles, 1, splits);
         if (splits > 1) {
+            // F32 partials from the 8-wave direct-to-LDS kernel of the same tile width
+            if (is_pipe(variant)) variant = BNb == 256 ? 8 : 7;
             size_t bytes = (size_t)splits * M * N * sizeof(float);
             a.part = (float*)scratch_get(bytes, s);
             if (!a.part) return set_error(-2, "gemm: scratch allocation of %zu bytes failed", bytes);
@@ -946,33 +1045,42 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
                                                                           ldc, alpha, beta, bias);
             int rc = check_launch("gemm");
             return rc ? rc : lora_after();
-        } else {
-            if (lora && lora->n > 0) {
-                a.lora_n = lora->n;
-                a.lora_r = lora->r;
-                a.lora_delta = lora->delta ? 1 : 0;
-                a.lora_s = lora->s;
-                for (int p = 0; p < lora->n; p++) {
-                    a.lora_u[p] = lora->u[p];
-                    a.lora_ldu[p] = lora->ldu[p];
-                    a.lora_v[p] = lora->v_nk[p];
-                }
-            }
-            // measurement hook: algorithmic work of the launch (MNK product,
-            // rank-r epilogue products; operands read once, C written once and
-            // read once more when beta != 0)
-            const int kid = BNb == 256 ? KP_GEMM_BIG_WIDE : KP_GEMM_BIG;
-            const bool timed = kprof_begin(kid, s);
-            launch_big<EPI_BF16>(variant, grid, a, s);
-            if (timed) {
-                double mn = (double)M * N;
-                double fl = 2.0 * mn * K + 2.0 * mn * a.lora_r * a.lora_n;
-                double by = 2.0 * ((double)M * K + (double)N * K + mn * (beta != 0.f ? 2 : 1)) +
-                            2.0 * a.lora_n * (double)(M + N) * a.lora_r;
-                kprof_end(kid, s, fl, by, big_name(variant));
+        }
+        // LoRA terms fuse into the epilogue up to rank 16 for k_gemm_pipe (one
+        // MFMA k step) and at any rank for k_gemm_dma; otherwise they run
+        // after the GEMM
+        const bool fuse = lora && lora->n > 0 && (!is_pipe(variant) || lora->r <= 16);
+        if (fuse) {
+            a.lora_n = lora->n;
+            a.lora_r = lora->r;
+            a.lora_delta = lora->delta ? 1 : 0;
+            a.lora_s = lora->s;
+            for (int p = 0; p < lora->n; p++) {
+                a.lora_u[p] = lora->u[p];
+                a.lora_ldu[p] = lora->ldu[p];
+                a.lora_v[p] = lora->v_nk[p];
             }
         }
-        return check_launch("gemm");
+        // measurement hook: algorithmic work of the launch (MNK product,
+        // rank-r epilogue products; operands read once, C written once and
+        // read once more when beta != 0)
+        const int kid = BNb == 256 ? KP_GEMM_BIG_WIDE : KP_GEMM_BIG;
+        const bool timed = kprof_begin(kid, s);
+        if (variant == 12)
+            k_gemm_pipe<192><<<grid, 256, 0, s>>>(a);
+        else if (variant == 13)
+            k_gemm_pipe<256><<<grid, 256, 0, s>>>(a);
+        else
+            launch_big<EPI_BF16>(variant, grid, a, s);
+        if (timed) {
+            double mn = (double)M * N;
+            double fl = 2.0 * mn * K + 2.0 * mn * a.lora_r * a.lora_n;
+            double by = 2.0 * ((double)M * K + (double)N * K + mn * (beta != 0.f ? 2 : 1)) +
+                        2.0 * a.lora_n * (double)(M + N) * a.lora_r;
+            kprof_end(kid, s, fl, by, big_name(variant));
+        }
+        int rc = check_launch("gemm");
+        return (rc || fuse) ? rc : lora_after();
     }
 
     // tile choice: wide-N tiles for big outputs, skinny tiles for N <= 32
@@ -1064,7 +1172,7 @@ using namespace ta;
 extern "C" {
 
 int ta_gemm_variant(int v) {
-    TA_REQUIRE(v >= 0 && v <= 11, "gemm_variant: %d out of range", v);
+    TA_REQUIRE(variant_ok(v), "gemm_variant: %d is not a kernel variant (0, 7..13)", v);
     g_big_variant = v;
     return 0;
 }
