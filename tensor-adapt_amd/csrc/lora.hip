@@ -47,6 +47,14 @@ __device__ __forceinline__ bf16x8_t ld8(const bf16* __restrict__ row, int k, int
         if (k + e < kend) v[e] = __builtin_bit_cast(__bf16, row[k + e]);
     return v;
 }
+// 8 consecutive k at row + k when ok, zero otherwise.  The load is issued
+// unconditionally (from row itself when !ok) and the zero is a select, so a
+// wave's loads go out back to back instead of one branch-guarded load at a
+// time.  row must be a valid 16-byte aligned address.
+__device__ __forceinline__ bf16x8_t ld8s(const bf16* __restrict__ row, int k, bool ok) {
+    bf16x8_t v = *(const bf16x8_t*)(row + (ok ? k : 0));
+    return ok ? v : zfrag();
+}
 
 struct Pairs3 {
     const bf16* y[3];  // k_skinny_nt: Y_p [r x K]; k_rank_update: V_p
@@ -86,24 +94,28 @@ __global__ __launch_bounds__(SK_W * 64) void k_skinny_nt(const bf16* __restrict_
         xr[g] = X + (int64_t)(rin[g] ? row : 0) * ldx;
     }
     const bf16* yr[NT];
+    bool yin[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) {
         int c = 16 * t + (lane & 15);
-        yr[t] = (c < ncat) ? p.y[c / r] + (int64_t)(c % r) * K : nullptr;
+        yin[t] = c < ncat;
+        yr[t] = yin[t] ? p.y[c / r] + (int64_t)(c % r) * K : p.y[0];
     }
     const int nks = (K + 31) / 32;
     const int ko = 8 * (lane >> 4);
+    // K is a multiple of 8 (checked by the launcher): a chunk of 8 at k < K
+    // is whole
     for (int ks0 = w; ks0 < nks; ks0 += SK_W * U) {
         bf16x8_t a[U][SK_RG], b[U][NT];
 #pragma unroll
         for (int u = 0; u < U; u++) {
             int ks = ks0 + SK_W * u;
             int k = 32 * ks + ko;
-            bool in = ks < nks;
+            bool in = ks < nks && k < K;
 #pragma unroll
-            for (int g = 0; g < SK_RG; g++) a[u][g] = (in && rin[g]) ? ld8(xr[g], k, K) : zfrag();
+            for (int g = 0; g < SK_RG; g++) a[u][g] = ld8s(xr[g], k, in && rin[g]);
 #pragma unroll
-            for (int t = 0; t < NT; t++) b[u][t] = (in && yr[t]) ? ld8(yr[t], k, K) : zfrag();
+            for (int t = 0; t < NT; t++) b[u][t] = ld8s(yr[t], k, in && yin[t]);
         }
 #pragma unroll
         for (int u = 0; u < U; u++)
@@ -234,15 +246,28 @@ __global__ __launch_bounds__(256) void k_rank_update(bf16* __restrict__ Y, int64
 
 // ── weight gradients: partial[z][l][s] = sum_{t in range z} L[t][l] * Sm[t][s]
 // L: [T x NL] (ldl), Sm: [T x NS] (lds), NS <= 192.  Block: 64 columns of L
-// (4 waves x 16), one token range; token tiles of 64 staged transposed.
+// (4 waves x 16), one token range, token tiles of 64.  Both tiles sit in LDS
+// in their natural layout ([token][column], 16-byte row chunks straight
+// from the global rows) and the MFMA operands, which need 8 consecutive
+// tokens per lane, come out of LDS through gfx950's transposing read
+// (ds_read_b64_tr_b16: 16 lanes that each read 4 consecutive columns of
+// rows k0 + lane/4 receive, lane i, column i of rows k0..k0+3).
 constexpr int WG_TK = 64;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t* lds_i16x4_p;
 
 // 8 consecutive BF16 of row `tok`, columns [c, c+8) (zero outside the
 // matrix), as a 16-byte vector
 __device__ __forceinline__ u32x4 ld8z(const bf16* __restrict__ P, int64_t ld, int tok, int t_end,
                                       int c, int ncols, bool vec) {
-    if (tok < t_end && vec && c + 8 <= ncols) return *(const u32x4*)(P + (int64_t)tok * ld + c);
+    if (vec) {
+        // rows 16-byte aligned and ncols a multiple of 8: one unconditional
+        // load (of row 0 when out of range) and a select, no branch
+        const bool ok = tok < t_end && c < ncols;
+        u32x4 v = *(const u32x4*)(P + (ok ? (int64_t)tok * ld + c : 0));
+        return ok ? v : u32x4{0u, 0u, 0u, 0u};
+    }
     uint16_t x[8];
 #pragma unroll
     for (int e = 0; e < 8; e++)
@@ -252,20 +277,49 @@ __device__ __forceinline__ u32x4 ld8z(const bf16* __restrict__ P, int64_t ld, in
     for (int e = 0; e < 4; e++) v[e] = x[2 * e] | ((uint32_t)x[2 * e + 1] << 16);
     return v;
 }
-// scatter the 8 values of v to S[(c + e) * (WG_TK + 8) + tt] (transposed)
-__device__ __forceinline__ void st8t(bf16* S, int c, int tt, u32x4 v) {
-#pragma unroll
-    for (int e = 0; e < 8; e++) S[(c + e) * (WG_TK + 8) + tt] = (uint16_t)(v[e >> 1] >> ((e & 1) * 16));
+
+// Byte offset of element (row r, column c) in a [WG_TK][16 * NSTP] BF16 LDS
+// tile (NSTP a power of two).  The 32-byte column units of a row are
+// XOR-permuted by row bits 1..3 so that the transposing reads of rows
+// {k0..k0+3, k0+8..k0+11} (one 32-lane phase) hit distinct banks; 16-byte
+// chunks (c % 8 == 0) stay contiguous.
+template <int NSTP>
+__device__ __forceinline__ int wg_off(int r, int c) {
+    const int st = c >> 4, in = (c & 15) * 2;
+    if constexpr (NSTP == 1) {
+        return ((r * 32 + in) ^ (((r >> 3) & 1) << 7));
+    } else {
+        int x;
+        if constexpr (NSTP == 2) x = (r >> 3) & 1;
+        else if constexpr (NSTP == 4) x = ((r >> 1) & 1) | (((r >> 3) & 1) << 1);
+        else x = (r & 3) | (((r >> 3) & 1) << 2);
+        return r * 32 * NSTP + 32 * (st ^ x) + in;
+    }
 }
 
-template <int NST>  // 16-column tiles of the small side
+// MFMA operand of 16 columns [c0, c0+16) x tokens [k0, k0+8) from a tile in
+// wg_off layout: lane l (group g = l/16, j = l%16) reads rows k0 + 8g + j/4
+// (and + 4), columns c0 + 4 (j%4) .. + 3; it receives column c0 + j of
+// rows k0 + 8g .. + 7, the 16x16x32 operand layout.
+template <int NSTP>
+__device__ __forceinline__ bf16x8_t wg_frag(const char* __restrict__ tile, int k0, int c0, int lane) {
+    const int g = lane >> 4, j = lane & 15;
+    const int r = k0 + 8 * g + (j >> 2), c = c0 + 4 * (j & 3);
+    i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_p)(tile + wg_off<NSTP>(r, c)));
+    i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_p)(tile + wg_off<NSTP>(r + 4, c)));
+    return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+template <int NST, bool VEC>  // 16-column tiles of the small side; VEC: 16-byte rows
 __global__ __launch_bounds__(256) void k_wgrad(const bf16* __restrict__ L, int64_t ldl, int NL,
                                                const bf16* __restrict__ Sm, int64_t lds, int NS,
                                                int T, int tokens_per_split,
                                                float* __restrict__ part) {
-    __shared__ __attribute__((aligned(16))) bf16 sL[64 * (WG_TK + 8)];        // [l][t]
-    __shared__ __attribute__((aligned(16))) bf16 sS[NST * 16 * (WG_TK + 8)];  // [s][t]
-    constexpr int SCH = NST * 2 * WG_TK;       // 16-byte chunks of the small tile
+    constexpr int NSTP = NST <= 1 ? 1 : NST <= 2 ? 2 : NST <= 4 ? 4 : NST <= 8 ? 8 : 16;
+    __shared__ __attribute__((aligned(16))) char sL[WG_TK * 64 * 2];           // [t][l]
+    __shared__ __attribute__((aligned(16))) char sS[WG_TK * NSTP * 16 * 2];    // [t][s]
+    constexpr int SCPR = NST * 2;              // 16-byte chunks per small-tile row
+    constexpr int SCH = SCPR * WG_TK;          // ... per tile
     constexpr int SPT = (SCH + 255) / 256;     // ... per thread
     int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     int l0 = blockIdx.x * 64;
@@ -274,48 +328,40 @@ __global__ __launch_bounds__(256) void k_wgrad(const bf16* __restrict__ L, int64
     floatx4 acc[NST];
 #pragma unroll
     for (int t = 0; t < NST; t++) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
-    const bool vecl = ((ldl & 7) == 0) && (((uintptr_t)L & 15) == 0);
-    const bool vecs = ((lds & 7) == 0) && (((uintptr_t)Sm & 15) == 0);
     // staging registers: the next token tile is loaded while this one computes
     u32x4 rl[2], rs[SPT];
 #define WG_LOAD(tb)                                                                         \
     do {                                                                                    \
         _Pragma("unroll") for (int i = 0; i < 2; i++) {                                     \
             int q = threadIdx.x + 256 * i;                                                  \
-            rl[i] = ld8z(L, ldl, (tb) + (q >> 3), t_end, l0 + (q & 7) * 8, NL, vecl);       \
+            rl[i] = ld8z(L, ldl, (tb) + (q >> 3), t_end, l0 + (q & 7) * 8, NL, VEC);        \
         }                                                                                   \
         _Pragma("unroll") for (int i = 0; i < SPT; i++) {                                   \
             int q = threadIdx.x + 256 * i;                                                  \
             if (q < SCH)                                                                    \
-                rs[i] = ld8z(Sm, lds, (tb) + q / (NST * 2), t_end, (q % (NST * 2)) * 8, NS, \
-                             vecs);                                                         \
+                rs[i] = ld8z(Sm, lds, (tb) + q / SCPR, t_end, (q % SCPR) * 8, NS, VEC);     \
         }                                                                                   \
     } while (0)
     if (t_beg < t_end) WG_LOAD(t_beg);
     for (int tb = t_beg; tb < t_end; tb += WG_TK) {
-        __syncthreads();  // the previous tile's MFMAs are done with LDS
+        __syncthreads();  // the previous tile's fragment reads are done
 #pragma unroll
         for (int i = 0; i < 2; i++) {
             int q = threadIdx.x + 256 * i;
-            st8t(sL, (q & 7) * 8, q >> 3, rl[i]);
+            *(u32x4*)(sL + wg_off<4>(q >> 3, (q & 7) * 8)) = rl[i];
         }
 #pragma unroll
         for (int i = 0; i < SPT; i++) {
             int q = threadIdx.x + 256 * i;
-            if (q < SCH) st8t(sS, (q % (NST * 2)) * 8, q / (NST * 2), rs[i]);
+            if (q < SCH) *(u32x4*)(sS + wg_off<NSTP>(q / SCPR, (q % SCPR) * 8)) = rs[i];
         }
         __syncthreads();
         if (tb + WG_TK < t_end) WG_LOAD(tb + WG_TK);
 #pragma unroll
         for (int kc = 0; kc < WG_TK / 32; kc++) {
-            bf16x8_t a =
-                *(const bf16x8_t*)(sL + (16 * w + (lane & 15)) * (WG_TK + 8) + 32 * kc + 8 * (lane >> 4));
+            bf16x8_t a = wg_frag<4>(sL, 32 * kc, 16 * w, lane);
 #pragma unroll
-            for (int t = 0; t < NST; t++) {
-                bf16x8_t b = *(const bf16x8_t*)(sS + (16 * t + (lane & 15)) * (WG_TK + 8) + 32 * kc +
-                                                8 * (lane >> 4));
-                acc[t] = mf16(a, b, acc[t]);
-            }
+            for (int t = 0; t < NST; t++) acc[t] = mf16(a, wg_frag<NSTP>(sS, 32 * kc, 16 * t, lane), acc[t]);
         }
     }
 #undef WG_LOAD
@@ -445,15 +491,26 @@ int lora_wgrad(const bf16* L, int64_t ldl, int NL, const bf16* Sm, int64_t lds, 
     dim3 grid(ltiles, splits);
     int nst = (NS + 15) / 16;
     const bool timed = kprof_begin(KP_LORA_WGRAD, s);
+    // 16-byte row loads need aligned rows and column counts in whole chunks
+    const bool vec = ((ldl & 7) == 0) && (((uintptr_t)L & 15) == 0) && ((lds & 7) == 0) &&
+                     (((uintptr_t)Sm & 15) == 0) && (NL % 8) == 0 && (NS % 8) == 0;
+#define WG(N)                                                                                  \
+    do {                                                                                       \
+        if (vec)                                                                               \
+            k_wgrad<N, true><<<grid, 256, 0, s>>>(L, ldl, NL, Sm, lds, NS, T, per, part);      \
+        else                                                                                   \
+            k_wgrad<N, false><<<grid, 256, 0, s>>>(L, ldl, NL, Sm, lds, NS, T, per, part);     \
+    } while (0)
     switch (nst) {
-        case 1: k_wgrad<1><<<grid, 256, 0, s>>>(L, ldl, NL, Sm, lds, NS, T, per, part); break;
-        case 2: k_wgrad<2><<<grid, 256, 0, s>>>(L, ldl, NL, Sm, lds, NS, T, per, part); break;
-        case 3: k_wgrad<3><<<grid, 256, 0, s>>>(L, ldl, NL, Sm, lds, NS, T, per, part); break;
-        case 4: k_wgrad<4><<<grid, 256, 0, s>>>(L, ldl, NL, Sm, lds, NS, T, per, part); break;
-        case 8: k_wgrad<8><<<grid, 256, 0, s>>>(L, ldl, NL, Sm, lds, NS, T, per, part); break;
-        case 12: k_wgrad<12><<<grid, 256, 0, s>>>(L, ldl, NL, Sm, lds, NS, T, per, part); break;
+        case 1: WG(1); break;
+        case 2: WG(2); break;
+        case 3: WG(3); break;
+        case 4: WG(4); break;
+        case 8: WG(8); break;
+        case 12: WG(12); break;
         default: return set_error(-1, "lora_wgrad: %d small columns unsupported", NS);
     }
+#undef WG
     int64_t n = (int64_t)NL * NS;
     int blocks = (int)((n + 255) / 256);
     if (trans)
