@@ -526,9 +526,6 @@ __device__ __attribute__((always_inline)) inline void dma_mma(floatx16 (&acc)[TM
     }
 }
 
-// s_waitcnt vmcnt(n) with the other counters left free (gfx9 encoding)
-#define TA_WAIT_VMCNT(n) \
-    __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
 
 // 1 KB of zeros: the source of the tiles that pad K up to a whole number
 // of trips (they add exact zeros)

@@ -67,10 +67,10 @@ struct Pairs3 {
 
 // ── C_p = bf16(X Y_p^T) ───────────────────────────────────────────────────
 // grid: ceil(M/32) blocks x 512 threads (8 waves).  Each wave covers all 32
-// rows of the block (2 groups of 16) for the 32-wide K chunks it takes round
-// robin, so one fragment of Y_p serves 32 rows; it issues the loads of U
-// chunks before their MFMAs (U 16-byte loads per lane and operand in
-// flight).  The waves' partial sums are added in wave order through LDS.
+// rows of the block (2 groups of 16) for runs of U consecutive 32-wide K
+// chunks taken round robin, so one fragment of Y_p serves 32 rows; it
+// issues the loads of its U chunks before their MFMAs (U 16-byte loads per
+// lane and operand in flight).  The waves' partial sums are added in wave order through LDS.
 // Column c of the concatenated output belongs to pair c / r, rank c % r.
 constexpr int SK_W = 8, SK_RG = 2;  // waves, 16-row groups per block
 template <int NT, int U>  // NT: 16-column tiles covering n*r columns
@@ -99,17 +99,21 @@ __global__ __launch_bounds__(SK_W * 64) void k_skinny_nt(const bf16* __restrict_
     for (int t = 0; t < NT; t++) {
         int c = 16 * t + (lane & 15);
         yin[t] = c < ncat;
-        yr[t] = yin[t] ? p.y[c / r] + (int64_t)(c % r) * K : p.y[0];
+        const int pr = c / r;
+        yr[t] = yin[t] ? (pr == 0 ? p.y[0] : pr == 1 ? p.y[1] : p.y[2]) + (int64_t)(c - pr * r) * K
+                       : p.y[0];
     }
     const int nks = (K + 31) / 32;
     const int ko = 8 * (lane >> 4);
     // K is a multiple of 8 (checked by the launcher): a chunk of 8 at k < K
     // is whole
-    for (int ks0 = w; ks0 < nks; ks0 += SK_W * U) {
+    // each wave takes U consecutive chunks per trip (U * 64 contiguous bytes
+    // of each of its rows), the waves interleaved at that granularity
+    for (int ks0 = w * U; ks0 < nks; ks0 += SK_W * U) {
         bf16x8_t a[U][SK_RG], b[U][NT];
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            int ks = ks0 + SK_W * u;
+            int ks = ks0 + u;
             int k = 32 * ks + ko;
             bool in = ks < nks && k < K;
 #pragma unroll
@@ -154,7 +158,159 @@ __global__ __launch_bounds__(SK_W * 64) void k_skinny_nt(const bf16* __restrict_
                 floatx4 v = acc[g][t];
                 int c = 16 * t + (lane & 15);
                 if (c >= ncat) continue;
-                bf16* out = p.c[c / r] + (c % r);
+                const int pr = c / r;  // selects, not an index into the argument struct
+                bf16* out = (pr == 0 ? p.c[0] : pr == 1 ? p.c[1] : p.c[2]) + (c - pr * r);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    int m = m0 + 16 * g + 4 * (lane >> 4) + i;
+                    if (m < M) out[(int64_t)m * p.ldc] = f2bf(v[i]);
+                }
+            }
+    }
+}
+
+// ── C_p = bf16(X Y_p^T) with X and Y streamed through LDS ────────────────
+// The same product for the common case (16-byte aligned rows, K a multiple
+// of 8, n * r <= 48) with direct-to-LDS loads: K runs in stages of 256; one
+// global_load_lds_dwordx4 moves 2 rows x 512 contiguous bytes (whole cache
+// lines, where k_skinny_nt's fragment-shaped loads take 64 bytes of each of
+// 16 rows), NS stages in flight.  Block: 32 rows of X, 8 waves; in each
+// stage wave w computes k chunk w (32 wide) for both 16-row groups and
+// every 16-column tile of the concatenated Y.  16-byte unit u of row R sits
+// in slot u ^ (R % 16), so the fragment reads of 16 consecutive rows hit
+// distinct banks.  Partial sums are added in wave order through LDS, as in
+// k_skinny_nt.  Stages before the first (padding K up to a multiple of
+// NS stages) and chunks past K load a zero page.
+constexpr int SKD_K = 256;  // k per stage
+static __device__ __attribute__((aligned(16))) bf16 g_skd_zero[8] = {};
+
+// One stage of DMA: NI instructions of 2 rows x 512 bytes, instruction i
+// (rows 2i, 2i+1) issued by wave i % 8.  X rows are m0 + row (clamped, their
+// products unused past M); Y rows are the concatenated rank rows c (pair
+// c / r, rank c % r), zero past n * r.
+template <int NI, bool ISX>
+__device__ __forceinline__ void skd_stage(const bf16* __restrict__ X, int64_t ldx, int m0, int M,
+                                          const Pairs3& p, int r, int kst, int K, bf16* buf, int w,
+                                          int lane) {
+    constexpr int PER = (NI + 7) / 8;
+#pragma unroll
+    for (int h = 0; h < PER; h++) {
+        int i = w + 8 * h;
+        i = i < NI ? i : i - 8;  // a surplus instruction repeats a lower wave's (same bytes)
+        const int row = 2 * i + (lane >> 5), slot = lane & 31;
+        const int k = kst + 8 * (slot ^ (row & 15));
+        bool ok = kst >= 0 && k < K;
+        const bf16* base;
+        if constexpr (ISX) {
+            base = X + (int64_t)min(m0 + row, M - 1) * ldx;
+        } else {
+            const int pr = row < r ? 0 : row < 2 * r ? 1 : 2;
+            ok = ok && row < p.n * r;
+            const bf16* y = pr == 0 ? p.y[0] : pr == 1 ? p.y[1] : p.y[2];
+            base = (ok ? y : g_skd_zero) + (int64_t)(row - pr * r) * K;
+        }
+        const bf16* src = ok ? base + k : g_skd_zero;
+        __builtin_amdgcn_global_load_lds((const void*)src,
+                                         (__attribute__((address_space(3))) void*)(buf + 512 * i),
+                                         16, 0, 0);
+    }
+}
+
+// 16x16x32 operand of stage rows [R0, R0+16), k chunk c (32 wide)
+__device__ __forceinline__ bf16x8_t skd_frag(const bf16* buf, int R0, int c, int lane) {
+    const int row = R0 + (lane & 15), u = 4 * c + (lane >> 4);
+    return *(const bf16x8_t*)(buf + row * SKD_K + 8 * (u ^ (row & 15)));
+}
+
+template <int NT, int NS>
+__global__ __launch_bounds__(512) void k_skinny_dma(const bf16* __restrict__ X, int64_t ldx, int M,
+                                                    int K, int r, Pairs3 p) {
+    constexpr int XE = 32 * SKD_K, YE = 16 * NT * SKD_K;  // elements per stage
+    constexpr int XI = 16, YI = 8 * NT;                   // DMA instructions per stage
+    constexpr int LPS = (XI + 7) / 8 + (YI + 7) / 8;      // ... per wave
+    __shared__ __attribute__((aligned(1024))) bf16 sX0[XE], sX1[XE], sX2[XE], sX3[NS == 4 ? XE : 8];
+    __shared__ __attribute__((aligned(1024))) bf16 sY0[YE], sY1[YE], sY2[YE], sY3[NS == 4 ? YE : 8];
+    __shared__ floatx4 red[SK_W / 2][SK_RG][NT][64];
+    const int lane = threadIdx.x & 63;
+    int w = threadIdx.x >> 6;
+    w = __builtin_amdgcn_readfirstlane(w);
+    const int m0 = blockIdx.x * 32;
+    floatx4 acc[SK_RG][NT];
+#pragma unroll
+    for (int g = 0; g < SK_RG; g++)
+#pragma unroll
+        for (int t = 0; t < NT; t++) acc[g][t] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int nst = (K + SKD_K - 1) / SKD_K;
+    const int pad = (NS - nst % NS) % NS;
+#define SKD_ISSUE(SXB, SYB, KS)                                                            \
+    do {                                                                                   \
+        const int ks_ = (KS);                                                              \
+        const int kst_ = ks_ < 0 ? -1 : min(ks_, nst - 1) * SKD_K;                         \
+        skd_stage<XI, true>(X, ldx, m0, M, p, r, kst_, K, SXB, w, lane);                    \
+        skd_stage<YI, false>(X, ldx, m0, M, p, r, kst_, K, SYB, w, lane);                   \
+    } while (0)
+#define SKD_STEP(J, SXJ, SYJ, SXN, SYN)                                                    \
+    do {                                                                                   \
+        TA_WAIT_VMCNT(LPS * (NS - 2));                                                     \
+        __builtin_amdgcn_s_barrier();                                                      \
+        SKD_ISSUE(SXN, SYN, ks0 + (J) + NS - 1);                                           \
+        bf16x8_t a_[SK_RG], b_[NT];                                                        \
+        _Pragma("unroll") for (int g = 0; g < SK_RG; g++) a_[g] = skd_frag(SXJ, 16 * g, w, lane); \
+        _Pragma("unroll") for (int t = 0; t < NT; t++) b_[t] = skd_frag(SYJ, 16 * t, w, lane);    \
+        _Pragma("unroll") for (int g = 0; g < SK_RG; g++)                                  \
+            _Pragma("unroll") for (int t = 0; t < NT; t++) acc[g][t] = mf16(a_[g], b_[t], acc[g][t]); \
+    } while (0)
+    SKD_ISSUE(sX0, sY0, 0 - pad);
+    SKD_ISSUE(sX1, sY1, 1 - pad);
+    if constexpr (NS == 4) SKD_ISSUE(sX2, sY2, 2 - pad);
+    for (int ks0 = -pad; ks0 < nst; ks0 += NS) {
+        if constexpr (NS == 4) {
+            SKD_STEP(0, sX0, sY0, sX3, sY3);
+            SKD_STEP(1, sX1, sY1, sX0, sY0);
+            SKD_STEP(2, sX2, sY2, sX1, sY1);
+            SKD_STEP(3, sX3, sY3, sX2, sY2);
+        } else {
+            SKD_STEP(0, sX0, sY0, sX2, sY2);
+            SKD_STEP(1, sX1, sY1, sX0, sY0);
+            SKD_STEP(2, sX2, sY2, sX1, sY1);
+        }
+    }
+    TA_WAIT_VMCNT(0);  // the surplus loads have landed before the block ends
+#undef SKD_STEP
+#undef SKD_ISSUE
+    // fixed-order tree over the waves: w += w + h for h = 4, 2, 1
+#pragma unroll
+    for (int h = SK_W / 2; h >= 1; h >>= 1) {
+        if (w >= h && w < 2 * h)
+#pragma unroll
+            for (int g = 0; g < SK_RG; g++)
+#pragma unroll
+                for (int t = 0; t < NT; t++) red[w - h][g][t][lane] = acc[g][t];
+        __syncthreads();
+        if (w < h)
+#pragma unroll
+            for (int g = 0; g < SK_RG; g++)
+#pragma unroll
+                for (int t = 0; t < NT; t++) {
+                    floatx4 o = red[w][g][t][lane];
+                    acc[g][t][0] += o[0];
+                    acc[g][t][1] += o[1];
+                    acc[g][t][2] += o[2];
+                    acc[g][t][3] += o[3];
+                }
+        __syncthreads();
+    }
+    if (w == 0) {
+        const int ncat = p.n * r;
+#pragma unroll
+        for (int g = 0; g < SK_RG; g++)
+#pragma unroll
+            for (int t = 0; t < NT; t++) {
+                floatx4 v = acc[g][t];
+                int c = 16 * t + (lane & 15);
+                if (c >= ncat) continue;
+                const int pr = c / r;  // selects, not an index into the argument struct
+                bf16* out = (pr == 0 ? p.c[0] : pr == 1 ? p.c[1] : p.c[2]) + (c - pr * r);
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     int m = m0 + 16 * g + 4 * (lane >> 4) + i;
@@ -432,7 +588,14 @@ int lora_skinny_nt(const bf16* X, int64_t ldx, int M, int K, int r, const bf16* 
     int nt = (n * r + 15) / 16;
     dim3 grid((M + 16 * SK_RG - 1) / (16 * SK_RG));
     const bool timed = kprof_begin(KP_LORA_SKINNY, s);
-    switch (nt) {
+    const bool dma = ((uintptr_t)X & 15) == 0 && (ldx & 7) == 0 && (K & 7) == 0 && nt <= 3;
+    if (dma) {
+        switch (nt) {
+            case 1: k_skinny_dma<1, 4><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
+            case 2: k_skinny_dma<2, 4><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
+            default: k_skinny_dma<3, 3><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
+        }
+    } else switch (nt) {
         case 1: k_skinny_nt<1, 4><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
         case 2: k_skinny_nt<2, 4><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
         case 3: k_skinny_nt<3, 3><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;

@@ -3,6 +3,10 @@
 #pragma once
 #include "ta_common.hpp"
 
+// s_waitcnt vmcnt(n) with the other counters left free (gfx9 encoding)
+#define TA_WAIT_VMCNT(n) \
+    __builtin_amdgcn_s_waitcnt(((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8))
+
 namespace ta {
 
 void* scratch_get(size_t bytes, hipStream_t s, int slot = 0);
