@@ -697,9 +697,14 @@ __device__ __attribute__((always_inline)) inline void static_for(F&& f) {
 // operand fragments loaded up front), then the BF16 value into wb; the half
 // leaves as 16-byte row vectors.  A lane reads and writes the same wb words
 // for a fragment, so only the final read-back needs the wave barrier.
+//
+// lu/lv/lb (may be null): the block's rank-16 LoRA operands of the first PF
+// pairs (U rows, V rows; 16 BF16 per row) and its bias, staged in LDS at the
+// start of the kernel; R0 - m0 / C0 - n0 index them.
 template <int TM, int TN, int WTN, int I0, int PF>
 __device__ __attribute__((always_inline)) inline void pipe_half_epilogue(
-    floatx16 (&acc)[TM][TN], const GemmArgs& a, int R0, int C0, int lane, bf16* __restrict__ wb) {
+    floatx16 (&acc)[TM][TN], const GemmArgs& a, int R0, int C0, int lane, bf16* __restrict__ wb,
+    const bf16* lu, const bf16* lv, const bf16* lb, int mloc, int nloc, int BMs, int BNs) {
     constexpr int CPR = WTN / 8;
     bf16* C = (bf16*)a.C;
     const bool vec = ((a.ldc & 7) == 0) && (((uintptr_t)C & 15) == 0);
@@ -727,7 +732,14 @@ __device__ __attribute__((always_inline)) inline void pipe_half_epilogue(
     bf16x8_t fu[PF][2], fv[PF][TN];
 #pragma unroll
     for (int p = 0; p < PF; p++) {
-        if (p < a.lora_n) {
+        if (p < a.lora_n && lu) {
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+                fu[p][i] = *(const bf16x8_t*)(lu + (p * BMs + mloc + 32 * i + (lane & 31)) * 16 + kk);
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+                fv[p][j] = *(const bf16x8_t*)(lv + (p * BNs + nloc + 32 * j + (lane & 31)) * 16 + kk);
+        } else if (p < a.lora_n) {
 #pragma unroll
             for (int i = 0; i < 2; i++) {
                 int row = min(R0 + 32 * i + (lane & 31), a.M - 1);
@@ -752,7 +764,7 @@ __device__ __attribute__((always_inline)) inline void pipe_half_epilogue(
         constexpr int i = decltype(ij)::value / TN, j = decltype(ij)::value % TN;
         const int lc = j * 32 + (lane & 31);
         const int n = C0 + lc;
-        const float bias = (a.bias && n < a.N) ? bf2f(a.bias[n]) : 0.f;
+        const float bias = (a.bias && n < a.N) ? bf2f(lb ? lb[nloc + lc] : a.bias[n]) : 0.f;
         float v[16];
 #pragma unroll
         for (int r = 0; r < 16; r++) {
@@ -822,6 +834,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     static_assert(BN == 192 || BN == 256, "tile width");
     __shared__ __attribute__((aligned(1024))) bf16 sX0[SX], sX1[SX], sX2[SX], sX3[SX];
     __shared__ __attribute__((aligned(1024))) bf16 sY0[SY], sY1[SY], sY2[SY], sY3[SY];
+    // epilogue operands staged at the start: rank-16 LoRA U/V rows of the
+    // first LP pairs and 512 bias entries (one DMA instruction)
+    constexpr int LP = BN == 256 ? 1 : 3;
+    __shared__ __attribute__((aligned(16))) bf16 sLU[LP * BM * 16], sLV[LP * BN * 16], sB[512];
 
     int tm_i, tn_i;
     big_tile(blockIdx.x, a.tiles_m, a.tiles_n, tm_i, tn_i);
@@ -829,6 +845,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int wm = w / WNW, wn = w % WNW;
     w = __builtin_amdgcn_readfirstlane(w);
+
+    // these loads are older than every stage load, so the prologue's wait
+    // for stage 0 covers them; the main loop's barriers publish them
+    const bool lds_lora = a.lora_n > 0 && a.lora_r == 16;
+    const bool lds_bias = a.bias != nullptr && (a.N & 7) == 0 && a.N >= 8;
+    if (lds_lora) {
+        // instruction q moves 32 rows x 32 bytes: lane l -> row l/2, half l%2
+        constexpr int UI = BM / 32, VI = BN / 32;
+        for (int q = w; q < LP * (UI + VI); q += NW) {
+            const int p = q / (UI + VI), qi = q % (UI + VI);
+            if (p >= a.lora_n) break;
+            const bf16* u = p == 0 ? a.lora_u[0] : p == 1 ? a.lora_u[1] : a.lora_u[2];
+            const bf16* v = p == 0 ? a.lora_v[0] : p == 1 ? a.lora_v[1] : a.lora_v[2];
+            const int64_t ldu = p == 0 ? a.lora_ldu[0] : p == 1 ? a.lora_ldu[1] : a.lora_ldu[2];
+            const bf16* src;
+            bf16* dst;
+            if (qi < UI) {
+                const int row = min(m0 + 32 * qi + (lane >> 1), a.M - 1);
+                src = u + (int64_t)row * ldu + 8 * (lane & 1);
+                dst = sLU + (p * BM + 32 * qi) * 16;
+            } else {
+                const int row = min(n0 + 32 * (qi - UI) + (lane >> 1), a.N - 1);
+                src = v + (int64_t)row * 16 + 8 * (lane & 1);
+                dst = sLV + (p * BN + 32 * (qi - UI)) * 16;
+            }
+            __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr_t)dst, 16, 0, 0);
+        }
+    }
+    if (lds_bias && w == NW - 1) {
+        const bf16* src = a.bias + min(n0 + 8 * lane, a.N - 8);
+        __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr_t)sB, 16, 0, 0);
+    }
 
     floatx16 acc[TM][TN];
 #pragma unroll
@@ -888,8 +936,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     bf16* wb0 = w == 0 ? sX0 : w == 1 ? sX1 : w == 2 ? sX2 : sX3;
     bf16* wb1 = w == 0 ? sY0 : w == 1 ? sY1 : w == 2 ? sY2 : sY3;
     static_assert(64 * WTN <= SX && 64 * WTN <= SY, "staging fits a stage buffer");
-    pipe_half_epilogue<TM, TN, WTN, 0, BN == 256 ? 1 : 3>(acc, a, m0 + wm * WTM, n0 + wn * WTN, lane, wb0);
-    pipe_half_epilogue<TM, TN, WTN, 2, BN == 256 ? 1 : 3>(acc, a, m0 + wm * WTM + 64, n0 + wn * WTN, lane, wb1);
+    const bf16* lu = lds_lora ? sLU : nullptr;
+    const bf16* lv = lds_lora ? sLV : nullptr;
+    const bf16* lb = lds_bias ? sB : nullptr;
+    pipe_half_epilogue<TM, TN, WTN, 0, LP>(acc, a, m0 + wm * WTM, n0 + wn * WTN, lane, wb0, lu, lv,
+                                           lb, wm * WTM, wn * WTN, BM, BN);
+    pipe_half_epilogue<TM, TN, WTN, 2, LP>(acc, a, m0 + wm * WTM + 64, n0 + wn * WTN, lane, wb1, lu,
+                                           lv, lb, wm * WTM + 64, wn * WTN, BM, BN);
 }
 
 // Kernel variants of the large GEMMs (ta_gemm_variant): 0 picks k_gemm_pipe
