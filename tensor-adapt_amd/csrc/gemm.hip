@@ -627,19 +627,20 @@ __global__ __launch_bounds__(WMW * WNW * 64) void k_gemm_dma(GemmArgs a) {
     }
 }
 
-// ── k_gemm_pipe: one wave per SIMD, fragment double buffering ───────────
+// ── k_gemm_pipe: fragment double buffering over direct-to-LDS stages ────
 // The default kernel of the large GEMMs.  Block tile 256 x BN (BN = 192 or
-// 256), 4 wave64s in a 2 x 2 arrangement, each owning a 128 x BN/2 wave
-// tile: 4 x BN/64 accumulator fragments of v_mfma_f32_32x32x16_bf16 held in
-// AGPRs (192 or 256), so one wave per SIMD feeds the matrix core on its own.
-// The stages are the direct-to-LDS stages of k_gemm_dma (32-wide k slices,
-// 4 stages in flight, swizzled rows).  Each step of the loop computes one
-// stage in two 16-wide halves: the fragments of the second half are read
-// from LDS while the first half's MFMAs run, and the fragments of the next
-// stage's first half while the second half's run, so LDS latency never
-// sits between two MFMA batches.  One barrier per stage, placed between the
-// halves: after it the next stage has landed for every wave and the buffer
-// read two stages ago is free for the next DMA.
+// 256) split over WMW x WNW wave64s.  The default layouts use 8 waves (two
+// per SIMD, 64 x 128 / 64 x 96 / 128 x 64 wave tiles, accumulators in VGPRs)
+// so that one wave's MFMAs cover the other's LDS and barrier waits; the
+// 4-wave layouts (128-row wave tiles, accumulators in AGPRs, one wave per
+// SIMD) remain as variants.  The stages are the direct-to-LDS stages of
+// k_gemm_dma (32-wide k slices, 4 stages in flight, swizzled rows).  Each
+// step of the loop computes one stage in two 16-wide halves: the fragments
+// of the second half are read from LDS while the first half's MFMAs run,
+// and the fragments of the next stage's first half while the second half's
+// run, so LDS latency never sits between two MFMA batches.  One barrier per
+// stage, placed between the halves: after it the next stage has landed for
+// every wave and the buffer read two stages ago is free for the next DMA.
 template <int TM, int TN>
 struct Frags {
     bf16x8_t a[TM], b[TN];
@@ -823,13 +824,15 @@ __device__ __attribute__((always_inline)) inline void pipe_half_epilogue(
     }
 }
 
-template <int BN>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_gemm_pipe(
-    GemmArgs a) {
-    constexpr int NS = 4, BM = 256, NW = 4, WNW = 2;
-    constexpr int WTM = 128, WTN = BN / 2;
+template <int BN, int WMW, int WNW>
+__global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
+    WMW * WNW / 4, WMW * WNW / 4))) void k_gemm_pipe(GemmArgs a) {
+    constexpr int NS = 4, BM = 256, NW = WMW * WNW;
+    constexpr int WTM = BM / WMW, WTN = BN / WNW;
     constexpr int TM = WTM / 32, TN = WTN / 32;
-    constexpr int LPS = BM / 16 / NW + BN / 16 / NW;  // DMA instructions per stage per wave
+    static_assert(TM * 32 == WTM && TN * 32 == WTN && TM % 2 == 0, "wave tile");
+    // DMA instructions per stage per wave
+    constexpr int LPS = (BM / 16 + NW - 1) / NW + (BN / 16 + NW - 1) / NW;
     constexpr int SX = BM * DBK, SY = BN * DBK;
     static_assert(BN == 192 || BN == 256, "tile width");
     __shared__ __attribute__((aligned(1024))) bf16 sX0[SX], sX1[SX], sX2[SX], sX3[SX];
@@ -932,28 +935,42 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #undef PIPE_STEP
 #undef PIPE_ISSUE
     __syncthreads();
-    // each wave stages its two 64-row halves in two stage buffers of its own
-    bf16* wb0 = w == 0 ? sX0 : w == 1 ? sX1 : w == 2 ? sX2 : sX3;
-    bf16* wb1 = w == 0 ? sY0 : w == 1 ? sY1 : w == 2 ? sY2 : sY3;
-    static_assert(64 * WTN <= SX && 64 * WTN <= SY, "staging fits a stage buffer");
+    // each wave stages its 64-row halves in LDS of its own: the 4-wave
+    // layouts use one X and one Y stage buffer per wave, the 8-wave layouts
+    // one stage buffer per wave (split in two when it holds two halves)
     const bf16* lu = lds_lora ? sLU : nullptr;
     const bf16* lv = lds_lora ? sLV : nullptr;
     const bf16* lb = lds_bias ? sB : nullptr;
+    bf16 *wb0, *wb1;
+    if constexpr (NW == 4) {
+        wb0 = w == 0 ? sX0 : w == 1 ? sX1 : w == 2 ? sX2 : sX3;
+        wb1 = w == 0 ? sY0 : w == 1 ? sY1 : w == 2 ? sY2 : sY3;
+        static_assert(64 * WTN <= SX && 64 * WTN <= SY, "staging fits a stage buffer");
+    } else {
+        bf16* b = w == 0 ? sX0 : w == 1 ? sX1 : w == 2 ? sX2 : w == 3 ? sX3
+                : w == 4 ? sY0 : w == 5 ? sY1 : w == 6 ? sY2 : sY3;
+        static_assert(64 * WTN * (TM / 2) <= SY, "staging fits a stage buffer");
+        wb0 = b;
+        wb1 = b + 64 * WTN;
+    }
     pipe_half_epilogue<TM, TN, WTN, 0, LP>(acc, a, m0 + wm * WTM, n0 + wn * WTN, lane, wb0, lu, lv,
                                            lb, wm * WTM, wn * WTN, BM, BN);
-    pipe_half_epilogue<TM, TN, WTN, 2, LP>(acc, a, m0 + wm * WTM + 64, n0 + wn * WTN, lane, wb1, lu,
-                                           lv, lb, wm * WTM + 64, wn * WTN, BM, BN);
+    if constexpr (TM == 4)
+        pipe_half_epilogue<TM, TN, WTN, 2, LP>(acc, a, m0 + wm * WTM + 64, n0 + wn * WTN, lane, wb1,
+                                               lu, lv, lb, wm * WTM + 64, wn * WTN, BM, BN);
 }
 
 // Kernel variants of the large GEMMs (ta_gemm_variant): 0 picks k_gemm_pipe
-// (256 x 192 tiles up to N = 3072, 256 x 256 above; N = 1536 then gives one
-// block per CU at M = 8192); 7..11 are k_gemm_dma shapes kept for sweeps
-// and for the split-K partials; 12/13 force k_gemm_pipe 192/256.
+// with 8 waves (256 x 192 tiles in a 4 x 2 wave layout up to N = 3072,
+// 256 x 256 in a 2 x 4 layout above; N = 1536 then gives one block per CU at
+// M = 8192); 7..11 are k_gemm_dma shapes kept for sweeps and for the split-K
+// partials; 12..16 force one k_gemm_pipe shape.
 static int g_big_variant = 0;
-static bool variant_ok(int v) { return v == 0 || (v >= 7 && v <= 13); }
-static bool is_pipe(int variant) { return variant == 12 || variant == 13; }
+static bool variant_ok(int v) { return v == 0 || (v >= 7 && v <= 16); }
+static bool is_pipe(int variant) { return variant >= 12; }
 static int big_bn(int variant) {
-    return (variant == 8 || variant == 10 || variant == 13) ? 256 : 192;
+    return (variant == 8 || variant == 10 || variant == 13 || variant == 14 || variant == 16) ? 256
+                                                                                              : 192;
 }
 
 // symbol of the unsplit BF16-output instance of each variant, as printed
@@ -965,8 +982,11 @@ static const char* big_name(int variant) {
         case 9: return "void ta::k_gemm_dma<192, 0, 5, 4, 2>(ta::GemmArgs)";
         case 10: return "void ta::k_gemm_dma<256, 0, 4, 2, 2>(ta::GemmArgs)";
         case 11: return "void ta::k_gemm_dma<192, 0, 4, 2, 2>(ta::GemmArgs)";
-        case 13: return "void ta::k_gemm_pipe<256>(ta::GemmArgs)";
-        default: return "void ta::k_gemm_pipe<192>(ta::GemmArgs)";
+        case 13: return "void ta::k_gemm_pipe<256, 2, 2>(ta::GemmArgs)";
+        case 14: return "void ta::k_gemm_pipe<256, 4, 2>(ta::GemmArgs)";
+        case 15: return "void ta::k_gemm_pipe<192, 4, 2>(ta::GemmArgs)";
+        case 16: return "void ta::k_gemm_pipe<256, 2, 4>(ta::GemmArgs)";
+        default: return "void ta::k_gemm_pipe<192, 2, 2>(ta::GemmArgs)";
     }
 }
 
@@ -1067,7 +1087,7 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
     // large K-contiguous BF16 GEMMs: k_gemm_pipe (k_gemm_dma for split-K)
     if (xk && yk && !out_f32 && M >= 1024 && N >= 1024 && (K % BK) == 0 && vx && vy) {
         int variant = g_big_variant;
-        if (variant == 0) variant = N > 3072 ? 13 : 12;
+        if (variant == 0) variant = N > 3072 ? 16 : 15;
         const int BNb = big_bn(variant);
         a.tiles_m = (M + 255) / 256;
         a.tiles_n = (N + BNb - 1) / BNb;
@@ -1117,9 +1137,15 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
         const int kid = BNb == 256 ? KP_GEMM_BIG_WIDE : KP_GEMM_BIG;
         const bool timed = kprof_begin(kid, s);
         if (variant == 12)
-            k_gemm_pipe<192><<<grid, 256, 0, s>>>(a);
+            k_gemm_pipe<192, 2, 2><<<grid, 256, 0, s>>>(a);
         else if (variant == 13)
-            k_gemm_pipe<256><<<grid, 256, 0, s>>>(a);
+            k_gemm_pipe<256, 2, 2><<<grid, 256, 0, s>>>(a);
+        else if (variant == 14)
+            k_gemm_pipe<256, 4, 2><<<grid, 512, 0, s>>>(a);
+        else if (variant == 15)
+            k_gemm_pipe<192, 4, 2><<<grid, 512, 0, s>>>(a);
+        else if (variant == 16)
+            k_gemm_pipe<256, 2, 4><<<grid, 512, 0, s>>>(a);
         else
             launch_big<EPI_BF16>(variant, grid, a, s);
         if (timed) {
@@ -1222,7 +1248,7 @@ using namespace ta;
 extern "C" {
 
 int ta_gemm_variant(int v) {
-    TA_REQUIRE(variant_ok(v), "gemm_variant: %d is not a kernel variant (0, 7..13)", v);
+    TA_REQUIRE(variant_ok(v), "gemm_variant: %d is not a kernel variant (0, 7..16)", v);
     g_big_variant = v;
     return 0;
 }
