@@ -9,6 +9,9 @@
 // RoPE: one thread per (token, 4 consecutive pairs) computes the 4 angles
 // once and rotates that slice of every head of the token, so sincos work is
 // amortised over H heads and the data moves as 16-byte vectors.
+#include <mutex>
+#include <vector>
+
 #include "ta_internal.hpp"
 
 namespace ta {
@@ -231,6 +234,67 @@ __global__ __launch_bounds__(256) void k_rope_v8(bf16* __restrict__ x, int64_t r
     }
 }
 
+// The same rotation from a table of (cos, sin) per (t, pair), built once per
+// (T, hd, theta, sign) with exactly the per-element expressions above, so
+// the results are the same bits; one thread per 16-byte chunk of a head.
+__global__ void k_rope_table(float2* __restrict__ tab, int T, int hd, float theta, float sign) {
+    int half = hd >> 1;
+    int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (gid >= (int64_t)T * half) return;
+    int t = (int)(gid / half), i = (int)(gid % half);
+    float freq = powf(theta, -2.f * (float)i / (float)hd);
+    float angle = (float)t * freq * sign;
+    float sn, cs;
+    sincosf(angle, &sn, &cs);
+    tab[gid] = make_float2(cs, sn);
+}
+__global__ __launch_bounds__(256) void k_rope_tab(bf16* __restrict__ x, int64_t rows, int T,
+                                                  int H, int hd, const float4* __restrict__ tab) {
+    const int qpr = hd >> 3;  // 16-byte chunks per head (4 pairs each)
+    int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    int64_t row = gid / (H * qpr);
+    int hq = (int)(gid % (H * qpr)), q = hq % qpr;
+    if (row >= rows) return;
+    int t = (int)(row % T);
+    // pairs 4q .. 4q+3 of position t: two float4 of (cos, sin, cos, sin)
+    const float4* tp = tab + ((int64_t)t * (hd >> 1) + 4 * q) / 2;
+    float4 c01 = tp[0], c23 = tp[1];
+    bf16x8v* p = (bf16x8v*)(x + row * (int64_t)H * hd) + hq;
+    float f[8], o[8];
+    unpack8(*p, f);
+    const float cs[4] = {c01.x, c01.z, c23.x, c23.z}, sn[4] = {c01.y, c01.w, c23.y, c23.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        o[2 * e] = f[2 * e] * cs[e] - f[2 * e + 1] * sn[e];
+        o[2 * e + 1] = f[2 * e] * sn[e] + f[2 * e + 1] * cs[e];
+    }
+    *p = pack8(o);
+}
+
+// Tables live for the process, one per (device, T, hd, theta, sign), built on
+// first use on the caller's stream.
+struct RopeTab {
+    int dev, T, hd;
+    float theta, sign;
+    float2* tab;
+};
+static std::vector<RopeTab> g_rope_tabs;
+static std::mutex g_rope_mu;
+static const float2* rope_table(int T, int hd, float theta, float sign, hipStream_t s) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lk(g_rope_mu);
+    for (const RopeTab& r : g_rope_tabs)
+        if (r.dev == dev && r.T == T && r.hd == hd && r.theta == theta && r.sign == sign)
+            return r.tab;
+    float2* tab = nullptr;
+    int64_t n = (int64_t)T * (hd >> 1);
+    if (hipMalloc((void**)&tab, n * sizeof(float2)) != hipSuccess) return nullptr;
+    k_rope_table<<<(int)((n + 255) / 256), 256, 0, s>>>(tab, T, hd, theta, sign);
+    g_rope_tabs.push_back({dev, T, hd, theta, sign, tab});
+    return tab;
+}
+
 __global__ void k_rope_scalar(bf16* __restrict__ x, int64_t rows, int T, int H, int hd,
                               float theta, float sign) {
     int half = hd >> 1;
@@ -316,8 +380,10 @@ static int rope(uint16_t* x, int B, int T, int H, int hd, float theta, float sig
     if (rows == 0) return 0;
     hipStream_t s = (hipStream_t)stream;
     if ((hd & 7) == 0 && al16(x)) {
-        int64_t n = rows * (hd >> 3);
-        k_rope_v8<<<(int)((n + 255) / 256), 256, 0, s>>>(x, rows, T, H, hd, theta, sign);
+        const float2* tab = rope_table(T, hd, theta, sign, s);
+        TA_REQUIRE(tab, "rope: table allocation failed");
+        int64_t n = rows * H * (hd >> 3);
+        k_rope_tab<<<(int)((n + 255) / 256), 256, 0, s>>>(x, rows, T, H, hd, (const float4*)tab);
     } else {
         int64_t n = rows * (hd >> 1);
         k_rope_scalar<<<(int)((n + 255) / 256), 256, 0, s>>>(x, rows, T, H, hd, theta, sign);
