@@ -77,6 +77,14 @@ struct Engine {
     bf16* shadowT = nullptr;       // A^T and B^T of every shadow (same offsets), per step
     void* tdesc = nullptr;         // device descriptors of those transposes
     int ntdesc = 0;
+    // LoRA weight-gradient partials of one step (one arena slice per
+    // product, in backward call order) and their batched reduction
+    float* wg_arena = nullptr;
+    WgradJob* wg_jobs = nullptr;   // device copy of wg_plan
+    std::vector<WgradJob> wg_plan;
+    int64_t wg_blocks = 0;
+    double wg_elems = 0;
+    size_t wg_cursor = 0;
 
     bf16 *x_final, *xfn, *logits, *g_res, *dres, *tmpH, *dact, *dgate, *dup, *dxn2, *dao, *dQ, *dK,
         *dV, *dxn, *delta, *dh, *dh_cat;
@@ -238,6 +246,57 @@ static int engine_alloc(Engine* e) {
         CK(alloc(e, &ly.up, (int64_t)BT * I, (p + "up").c_str(), 0));
         CK(alloc(e, &ly.act, (int64_t)BT * I, (p + "act").c_str(), 0));
     }
+    // weight-gradient jobs in the order lora_group_bwd issues them: layers
+    // L-1..0; groups down, gate/up, o, q/k/v; per group gB of each on-pair,
+    // then gA of the group
+    {
+        struct G {
+            std::initializer_list<int> pairs;
+            int in;
+        };
+        const G groups[4] = {{{PD}, I}, {{PG, PU}, H}, {{PO}, qd}, {{PQ, PK, PV}, H}};
+        int64_t off = 0, blk = 0;
+        auto add = [&](int NL, int NS, int trans, float* g0, float* g1, float* g2) {
+            int per = 0;
+            WgradJob j{};
+            j.splits = lora_wgrad_splits(NL, BT, &per);
+            j.NL = NL;
+            j.NS = NS;
+            j.r = r;
+            j.trans = trans;
+            j.scale = e->scale;
+            j.g[0] = g0;
+            j.g[1] = g1;
+            j.g[2] = g2;
+            j.n = (int64_t)NL * NS;
+            j.blk0 = blk;
+            j.part = (const float*)(intptr_t)off;  // arena offset until the arena exists
+            blk += (j.n + 255) / 256;
+            off += ((int64_t)j.splits * j.n + 63) / 64 * 64;
+            e->wg_elems += (double)j.n;
+            e->wg_plan.push_back(j);
+        };
+        for (int l = c.layers - 1; l >= 0; l--)
+            for (const G& g : groups) {
+                float* ga[3] = {nullptr, nullptr, nullptr};
+                int n = 0;
+                for (int p : g.pairs) {
+                    Pair& pr = e->L[l].pr[p];
+                    if (!pr.on) continue;
+                    add(pr.out, r, 0, e->grad + pr.offB, nullptr, nullptr);
+                    ga[n++] = e->grad + pr.offA;
+                }
+                if (n) add(g.in, n * r, 1, ga[0], ga[1] ? ga[1] : ga[0], ga[2] ? ga[2] : ga[0]);
+            }
+        e->wg_blocks = blk;
+        if (!e->wg_plan.empty()) {
+            CK(alloc(e, &e->wg_arena, off, "lora.wgrad_partials"));
+            for (WgradJob& j : e->wg_plan) j.part = e->wg_arena + (intptr_t)j.part;
+            CK(dmalloc(e, (void**)&e->wg_jobs, e->wg_plan.size() * sizeof(WgradJob), "wg_jobs"));
+            TA_HIP(hipMemcpy(e->wg_jobs, e->wg_plan.data(), e->wg_plan.size() * sizeof(WgradJob),
+                             hipMemcpyHostToDevice));
+        }
+    }
     int maxout = std::max(std::max(qd, H), I);
     CK(alloc(e, &e->x_final, (int64_t)BT * H, "x_final", 0));
     CK(alloc(e, &e->final_rms, BT, "final_rms", 1));
@@ -333,6 +392,19 @@ static LoraEpi fwd_epi(Engine* e, const Pair& pr) {
     return ep;
 }
 
+// Arena slice of the next weight-gradient product of the step; the call
+// sequence must be the one the plan was built from.
+static int next_wgrad(Engine* e, int NL, int NS, float** part) {
+    if (e->wg_cursor >= e->wg_plan.size())
+        return set_error(-1, "engine: more weight-gradient products than planned");
+    const WgradJob& j = e->wg_plan[e->wg_cursor++];
+    if (j.NL != NL || j.NS != NS)
+        return set_error(-1, "engine: weight-gradient product %zu is %dx%d, planned %dx%d",
+                         e->wg_cursor - 1, NL, NS, j.NL, j.NS);
+    *part = (float*)j.part;
+    return 0;
+}
+
 // LoRA backward for one group, adapter_model.cu:131-220, pairs in order:
 //   dh_p = bf16(go_p B_p)            (B^T shadow, one pass over go_p)
 //   gB_p += s * go_p^T h_p           (h_p cached by the forward)
@@ -361,25 +433,26 @@ static int lora_group_bwd(Engine* e, Layer& ly, std::initializer_list<int> group
         bf16* C[1] = {e->dh_cat + q * r};
         TIMED(TA_CAT_LORA, gflops(dBT, r, pr.out), dBT * pr.out * 2 + dBT * r * 2,
               lora_skinny_nt(go_on[q], pr.out, BT, pr.out, r, Yt, C, ldh, 1, e->s));
-        float* G[3] = {e->grad + pr.offB, nullptr, nullptr};
-        TIMED(TA_CAT_LORA, gflops(pr.out, r, dBT), dBT * (pr.out + r) * 2 + pr.out * r * 8.0,
-              lora_wgrad(go_on[q], pr.out, pr.out, pr.h, r, r, BT, r, e->scale, false, G, e->s));
+        float* part = nullptr;
+        CK(next_wgrad(e, pr.out, r, &part));
+        TIMED(TA_CAT_LORA, gflops(pr.out, r, dBT), dBT * (pr.out + r) * 2,
+              lora_wgrad_part(go_on[q], pr.out, pr.out, pr.h, r, r, BT, part, e->s));
     }
-    float* GA[3] = {nullptr, nullptr, nullptr};
     ep->n = n;
     ep->r = r;
     ep->delta = false;
     ep->s = e->scale;
     for (int q = 0; q < n; q++) {
         Pair& pr = ly.pr[on[q]];
-        GA[q] = e->grad + pr.offA;
         ep->u[q] = e->dh_cat + q * r;
         ep->ldu[q] = ldh;
         ep->v_nk[q] = e->shadowT + pr.offA;
         ep->v_alt[q] = e->shadow + pr.offA;
     }
-    TIMED(TA_CAT_LORA, gflops(ldh, in, dBT), dBT * (in + ldh) * 2 + ldh * in * 8.0,
-          lora_wgrad(x, in, in, e->dh_cat, ldh, (int)ldh, BT, r, e->scale, true, GA, e->s));
+    float* part = nullptr;
+    CK(next_wgrad(e, in, (int)ldh, &part));
+    TIMED(TA_CAT_LORA, gflops(ldh, in, dBT), dBT * (in + ldh) * 2,
+          lora_wgrad_part(x, in, in, e->dh_cat, ldh, (int)ldh, BT, part, e->s));
     return 0;
 }
 
@@ -499,6 +572,7 @@ static int backward(Engine* e) {
     const double dBT = BT, tri = (double)e->B * c.n_q * e->T * (e->T + 1) / 2.0;
     hipStream_t s = e->s;
     const double nrm_b = dBT * H * 6 + H * 2 + dBT * 4;
+    e->wg_cursor = 0;
     // dres = dlogits * W_lm (qwen2.cu:205); grad = rms_norm_bwd(final)
     TIMED(TA_CAT_LMHEAD, gflops(BT, H, e->V), gbytes(BT, H, e->V, 2, 2, false),
           gemm_dispatch(true, true, BT, H, e->V, 1.f, e->logits, e->V, e->lmT, e->V, 0.f, e->dres,
@@ -563,6 +637,12 @@ static int backward(Engine* e) {
         TIMED(TA_CAT_ELEMWISE, 0, dBT * H * 6,
               ta_add_inplace(e->g_res, e->tmpH, (int64_t)BT * H, s));
     }
+    // every gA / gB += scale * (its ordered partial sum), one launch
+    if (e->wg_cursor != e->wg_plan.size())
+        return set_error(-1, "engine: %zu weight-gradient products run, %zu planned", e->wg_cursor,
+                         e->wg_plan.size());
+    TIMED(TA_CAT_LORA, 0, e->wg_elems * 8.0,
+          lora_wgrad_reduce_jobs(e->wg_jobs, (int)e->wg_plan.size(), e->wg_blocks, e->wg_elems, s));
     return 0;
 }
 

@@ -535,23 +535,30 @@ __global__ __launch_bounds__(256) void k_wgrad(const bf16* __restrict__ L, int64
     }
 }
 
-// G += scale * sum_z partial[z] (z in order).  TRANS=false: G_p[l][s] for
-// one pair (gB: [out x r], NS = r).  TRANS=true: column s belongs to pair
-// s / r, G_p[s % r][l] (gA: [r x in]).
-template <bool TRANS>
-__global__ void k_wgrad_reduce(const float* __restrict__ part, int splits, int NL, int NS, int r,
-                               float scale, float* g0, float* g1, float* g2) {
-    int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-    int64_t n = (int64_t)NL * NS;
-    if (idx >= n) return;
-    float v = sum_splits(part, splits, n, idx);
-    int l = (int)(idx / NS), s = (int)(idx % NS);
-    if (!TRANS) {
-        g0[(int64_t)l * NS + s] += scale * v;
+// Deferred reduction of every weight-gradient product of a step in one
+// launch: job j adds scale * (sum of its partials, split order) into its
+// gradient, G_p[l][s] for one pair (gB: [out x r], NS = r) or, TRANS,
+// column s of pair s / r into G_p[s % r][l] (gA: [r x in]).  Jobs own
+// disjoint gradient elements; job j covers blocks [blk0, blk0 + n / 256).
+__global__ __launch_bounds__(256) void k_wgrad_reduce_jobs(const WgradJob* __restrict__ jobs,
+                                                           int njobs) {
+    const int64_t b = blockIdx.x;
+    int lo = 0, hi = njobs - 1;  // last job with blk0 <= b
+    while (lo < hi) {
+        int mid = (lo + hi + 1) >> 1;
+        if (jobs[mid].blk0 <= b) lo = mid; else hi = mid - 1;
+    }
+    const WgradJob& J = jobs[lo];
+    const int64_t idx = (b - J.blk0) * 256 + threadIdx.x;
+    if (idx >= J.n) return;
+    const float v = sum_splits(J.part, J.splits, J.n, idx);
+    const int l = (int)(idx / J.NS), sc = (int)(idx % J.NS);
+    if (!J.trans) {
+        J.g[0][(int64_t)l * J.NS + sc] += J.scale * v;
     } else {
-        int pp = s / r, j = s % r;
-        float* g = pp == 0 ? g0 : (pp == 1 ? g1 : g2);
-        g[(int64_t)j * NL + l] += scale * v;
+        const int pp = sc / J.r, j = sc % J.r;
+        float* g = pp == 0 ? J.g[0] : pp == 1 ? J.g[1] : J.g[2];
+        g[(int64_t)j * J.NL + l] += J.scale * v;
     }
 }
 
@@ -608,7 +615,7 @@ int lora_skinny_nt(const bf16* X, int64_t ldx, int M, int K, int r, const bf16* 
     if (timed)  // X and the Y_p read once, C_p written once
         kprof_end(KP_LORA_SKINNY, s, 2.0 * M * K * n * r,
                   2.0 * ((double)M * K + (double)n * r * K + (double)M * n * r),
-                  "ta::k_skinny_nt (all instances)");
+                  "ta::k_skinny_dma + ta::k_skinny_nt (all instances)");
     return check_launch("lora_skinny_nt");
 }
 
@@ -637,21 +644,29 @@ int lora_rank_update(bool delta, bf16* Y, int64_t ldy, int M, int N, int r, floa
     return check_launch("lora_rank_update");
 }
 
-// G (F32) += scale * L^T Sm over T tokens.  trans=false: one pair, G [NL x NS];
-// trans=true: NS = n*r columns, pair p's G_p is [r x NL].
-int lora_wgrad(const bf16* L, int64_t ldl, int NL, const bf16* Sm, int64_t lds, int NS, int T,
-               int r, float scale, bool trans, float* const* G, hipStream_t s) {
-    TA_REQUIRE(NL > 0 && NS > 0 && NS <= 192 && T > 0, "lora_wgrad: bad arguments");
+// Token splits of a weight-gradient product over T tokens with NL large-side
+// columns: enough blocks (64 columns x one token range each) to fill the
+// chip.  *per receives the tokens per split (a multiple of the tile).
+int lora_wgrad_splits(int NL, int T, int* per) {
     int ltiles = (NL + 63) / 64;
     int tiles_t = (T + WG_TK - 1) / WG_TK;
     int splits = (768 + ltiles - 1) / ltiles;
     if (splits > tiles_t) splits = tiles_t;
     if (splits < 1) splits = 1;
-    int per = (tiles_t + splits - 1) / splits * WG_TK;
-    splits = (T + per - 1) / per;
-    float* part = (float*)scratch_get((size_t)splits * NL * NS * sizeof(float), s);
-    TA_REQUIRE(part, "lora_wgrad: scratch allocation failed");
-    dim3 grid(ltiles, splits);
+    *per = (tiles_t + splits - 1) / splits * WG_TK;
+    return (T + *per - 1) / *per;
+}
+
+// partials part[z][l][s] = sum over the tokens of split z of L[t][l] Sm[t][s]
+// (part holds lora_wgrad_splits(NL, T) x NL x NS floats); the reduction into
+// the gradient runs later, for all products of the step at once
+// (lora_wgrad_reduce_jobs).
+int lora_wgrad_part(const bf16* L, int64_t ldl, int NL, const bf16* Sm, int64_t lds, int NS, int T,
+                    float* part, hipStream_t s) {
+    TA_REQUIRE(NL > 0 && NS > 0 && NS <= 192 && T > 0 && part, "lora_wgrad_part: bad arguments");
+    int per = 0;
+    const int splits = lora_wgrad_splits(NL, T, &per);
+    dim3 grid((NL + 63) / 64, splits);
     int nst = (NS + 15) / 16;
     const bool timed = kprof_begin(KP_LORA_WGRAD, s);
     // 16-byte row loads need aligned rows and column counts in whole chunks
@@ -671,22 +686,27 @@ int lora_wgrad(const bf16* L, int64_t ldl, int NL, const bf16* Sm, int64_t lds, 
         case 4: WG(4); break;
         case 8: WG(8); break;
         case 12: WG(12); break;
-        default: return set_error(-1, "lora_wgrad: %d small columns unsupported", NS);
+        default: return set_error(-1, "lora_wgrad_part: %d small columns unsupported", NS);
     }
 #undef WG
-    int64_t n = (int64_t)NL * NS;
-    int blocks = (int)((n + 255) / 256);
-    if (trans)
-        k_wgrad_reduce<true><<<blocks, 256, 0, s>>>(part, splits, NL, NS, r, scale, G[0],
-                                                    G[1] ? G[1] : G[0], G[2] ? G[2] : G[0]);
-    else
-        k_wgrad_reduce<false><<<blocks, 256, 0, s>>>(part, splits, NL, NS, r, scale, G[0], G[0],
-                                                     G[0]);
-    if (timed)  // L and Sm read once; G read and written once (F32)
-        kprof_end(KP_LORA_WGRAD, s, 2.0 * T * NL * NS,
-                  2.0 * ((double)T * NL + (double)T * NS) + 8.0 * NL * NS,
-                  "ta::k_wgrad + ta::k_wgrad_reduce (all instances)");
-    return check_launch("lora_wgrad");
+    if (timed)  // L and Sm read once
+        kprof_end(KP_LORA_WGRAD, s, 2.0 * T * NL * NS, 2.0 * ((double)T * NL + (double)T * NS),
+                  "ta::k_wgrad + ta::k_wgrad_reduce_jobs (all instances)");
+    return check_launch("lora_wgrad_part");
+}
+
+// jobs: device array of njobs WgradJob sorted by blk0, covering total_blocks
+int lora_wgrad_reduce_jobs(const WgradJob* jobs, int njobs, int64_t total_blocks, double elems,
+                           hipStream_t s) {
+    if (njobs <= 0) return 0;
+    TA_REQUIRE(total_blocks > 0 && total_blocks < (1ll << 31), "lora_wgrad_reduce_jobs: %lld blocks",
+               (long long)total_blocks);
+    const bool timed = kprof_begin(KP_LORA_WGRAD, s);
+    k_wgrad_reduce_jobs<<<(unsigned)total_blocks, 256, 0, s>>>(jobs, njobs);
+    if (timed)  // every gradient element read and written once (F32)
+        kprof_end(KP_LORA_WGRAD, s, 0.0, 8.0 * elems,
+                  "ta::k_wgrad + ta::k_wgrad_reduce_jobs (all instances)");
+    return check_launch("lora_wgrad_reduce_jobs");
 }
 
 int transpose_batch(const bf16* src, bf16* dst, const void* descs, int nd, hipStream_t s) {

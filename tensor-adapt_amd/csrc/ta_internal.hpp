@@ -80,8 +80,23 @@ int lora_skinny_nt(const bf16* X, int64_t ldx, int M, int K, int r, const bf16* 
 int lora_rank_update(bool delta, bf16* Y, int64_t ldy, int M, int N, int r, float scale,
                      const bf16* const* U, const int64_t* ldu, const bf16* const* V, int n,
                      hipStream_t s);
-int lora_wgrad(const bf16* L, int64_t ldl, int NL, const bf16* Sm, int64_t lds, int NS, int T,
-               int r, float scale, bool trans, float* const* G, hipStream_t s);
+// Weight-gradient products of the LoRA backward, reduced once per step:
+// lora_wgrad_part writes split partials of L^T Sm into part; one
+// lora_wgrad_reduce_jobs launch then adds scale * (ordered sum of each job's
+// partials) into its gradient (see k_wgrad_reduce_jobs).
+struct WgradJob {
+    const float* part;
+    float* g[3];
+    int64_t n;     // NL * NS
+    int64_t blk0;  // first block of this job in the reduce launch
+    int splits, NL, NS, r, trans;
+    float scale;
+};
+int lora_wgrad_splits(int NL, int T, int* per);
+int lora_wgrad_part(const bf16* L, int64_t ldl, int NL, const bf16* Sm, int64_t lds, int NS, int T,
+                    float* part, hipStream_t s);
+int lora_wgrad_reduce_jobs(const WgradJob* jobs, int njobs, int64_t total_blocks, double elems,
+                           hipStream_t s);
 int transpose_batch(const bf16* src, bf16* dst, const void* descs, int nd, hipStream_t s);
 
 }  // namespace ta
