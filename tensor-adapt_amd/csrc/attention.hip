@@ -35,9 +35,11 @@
 //   k_attn_dkv_reduce sums the heads of each GQA group in head order — the
 //   group sum of ops.cu:539-555 without atomics, so dK/dV are deterministic.
 #include <float.h>
+#include <math.h>
 
 #include <algorithm>
 
+#include "lds_tr.hpp"
 #include "ta_internal.hpp"
 
 namespace ta {
@@ -196,6 +198,16 @@ __device__ __forceinline__ float red16_sum(float v) {
 }
 
 // ── forward ───────────────────────────────────────────────────────────────
+// Scores are kept in base-2 units (S * scale * log2 e) so that every
+// exponential is one v_exp_f32.  Only the diagonal key tile needs the causal
+// (and T) mask: every key of an earlier tile precedes every query row.  P
+// leaves as F32 rows to global memory and, split into BF16 hi/lo, into a
+// per-wave LDS tile stored [key][row] (4 rows of one key per 8-byte write);
+// the P·V MFMA operands (8 consecutive keys per lane) come out of that tile
+// and out of V, staged in its natural [key][hd] layout, through the
+// transposing LDS read.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
                                                   const bf16* __restrict__ K,
@@ -203,9 +215,10 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
                                                   bf16* __restrict__ O, float* __restrict__ O32,
                                                   float* __restrict__ P, int T, int Hq, int Hkv,
                                                   float scale, int zero_fill) {
+    constexpr int VST = HD / 16;  // 32-byte units of a V row
     __shared__ __attribute__((aligned(16))) bf16 sK[TK * (HD + 8)];
-    __shared__ __attribute__((aligned(16))) bf16 sVt[HD * LDT];
-    __shared__ __attribute__((aligned(16))) bf16 sP[4][2][16 * LDT];
+    __shared__ __attribute__((aligned(16))) char sV[TK * HD * 2];
+    __shared__ __attribute__((aligned(16))) char sP[4][2][TK * 16 * 2];
     int nqt = (T + TQ - 1) / TQ;
     int nbh = gridDim.x / nqt;
     int qt = nqt - 1 - (int)(blockIdx.x / nbh);  // longest rows launch first
@@ -222,15 +235,15 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
     bf16x8_t qf[HD / 32];
 #pragma unroll
     for (int ks = 0; ks < HD / 32; ks++) qf[ks] = ld_head8(Qh, qs, rowA, T, 32 * ks + 8 * (lane >> 4));
-    int rbase = q0 + 16 * w + 4 * (lane >> 4);  // C-layout rows rbase + r
-    Rows64<HD> lk;
-    Rows64T<HD> lv;
+    const int rbase = q0 + 16 * w + 4 * (lane >> 4);  // C-layout rows rbase + r
+    const float sl2 = scale * kLog2e;
+    Rows64<HD> lk, lv;
 
-    // pass 1: online max / sum
+    // pass 1: online max / sum of exp2 (per-lane partial sums, shared max)
     float m[4], l[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
-        m[r] = -FLT_MAX;
+        m[r] = -INFINITY;
         l[r] = 0.f;
     }
     lk.load(Kh, ks_, 0, T);
@@ -241,32 +254,32 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
         if (kt < qt) lk.load(Kh, ks_, (kt + 1) * TK, T);
         floatx4 S[4];
         wave_qk<HD>(S, qf, sK, lane);
+        const bool diag = kt == qt;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            int row = rbase + r;
-            float tmax = -FLT_MAX;
+            const int row = rbase + r;
+            float v[4], tmax = -INFINITY;
 #pragma unroll
             for (int t = 0; t < 4; t++) {
-                int key = kt * TK + 16 * t + (lane & 15);
-                float sc = S[t][r] * scale;
-                S[t][r] = sc;
-                if (key <= row && key < T) tmax = fmaxf(tmax, sc);
+                const int key = kt * TK + 16 * t + (lane & 15);
+                v[t] = (!diag || (key <= row && key < T)) ? S[t][r] * sl2 : -INFINITY;
+                tmax = fmaxf(tmax, v[t]);
             }
-            tmax = red16_max(tmax);
-            float mn = fmaxf(m[r], tmax);
+            const float mn = fmaxf(m[r], red16_max(tmax));
             float add = 0.f;
 #pragma unroll
-            for (int t = 0; t < 4; t++) {
-                int key = kt * TK + 16 * t + (lane & 15);
-                if (key <= row && key < T) add += exp2f((S[t][r] - mn) * kLog2e);
-            }
-            l[r] = (m[r] == -FLT_MAX ? 0.f : l[r] * exp2f((m[r] - mn) * kLog2e)) + add;
+            for (int t = 0; t < 4; t++) add += exp2_fast(v[t] - mn);
+            l[r] = (m[r] == -INFINITY ? 0.f : l[r] * exp2_fast(m[r] - mn)) + add;
             m[r] = mn;
         }
     }
     float inv[4];
+    bool rowok[4];
 #pragma unroll
-    for (int r = 0; r < 4; r++) inv[r] = 1.f / red16_sum(l[r]);
+    for (int r = 0; r < 4; r++) {
+        inv[r] = 1.f / red16_sum(l[r]);
+        rowok[r] = rbase + r < T;
+    }
 
     // pass 2: P, O
     floatx4 acc[HD / 16];
@@ -274,10 +287,16 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
     for (int j = 0; j < HD / 16; j++) acc[j] = zero4();
     lk.load(Kh, ks_, 0, T);
     lv.load(Vh, ks_, 0, T);
+    char* sPh = sP[w][0];
+    char* sPl = sP[w][1];
     for (int kt = 0; kt <= qt; kt++) {
         __syncthreads();
         lk.store(sK);
-        lv.store_t(sVt);
+#pragma unroll
+        for (int i = 0; i < Rows64<HD>::NR; i++) {
+            int q = threadIdx.x + 256 * i;
+            *(u32x4*)(sV + tr_off<VST>(q / (HD / 8), (q % (HD / 8)) * 8)) = lv.v[i];
+        }
         __syncthreads();
         if (kt < qt) {
             lk.load(Kh, ks_, (kt + 1) * TK, T);
@@ -285,21 +304,39 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
         }
         floatx4 S[4];
         wave_qk<HD>(S, qf, sK, lane);
+        const bool diag = kt == qt;
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            int kl = 16 * t + (lane & 15);
-            int key = kt * TK + kl;
+            const int kl = 16 * t + (lane & 15);
+            const int key = kt * TK + kl;
+            float p[4];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                int row = rbase + r;
-                float p = 0.f;
-                if (key <= row && key < T) p = exp2f((S[t][r] * scale - m[r]) * kLog2e) * inv[r];
-                if (row < T && key < T) Ph[(int64_t)row * T + key] = p;
-                put_split(sP[w][0], sP[w][1], (4 * (lane >> 4) + r) * LDT + kl, p);
+                p[r] = exp2_fast(S[t][r] * sl2 - m[r]) * inv[r];
+                if (diag && !(key <= rbase + r && key < T)) p[r] = 0.f;
+                if (rowok[r] && (!diag || key < T)) Ph[(int64_t)(rbase + r) * T + key] = p[r];
             }
+            uint2 hi, lo;
+            hi.x = pack2(p[0], p[1]);
+            hi.y = pack2(p[2], p[3]);
+            lo.x = pack2(p[0] - lo2f(hi.x), p[1] - hi2f(hi.x));
+            lo.y = pack2(p[2] - lo2f(hi.y), p[3] - hi2f(hi.y));
+            const int off = tr_off<1>(kl, 4 * (lane >> 4));
+            *(uint2*)(sPh + off) = hi;
+            *(uint2*)(sPl + off) = lo;
         }
         wave_sync();  // sP[w] is this wave's own tile
-        wave_pv<HD>(acc, sP[w][0], sP[w][1], sVt, lane);
+#pragma unroll
+        for (int kc = 0; kc < TK / 32; kc++) {
+            const bf16x8_t ah = tr_frag<1>(sPh, 32 * kc, 0, lane);
+            const bf16x8_t al = tr_frag<1>(sPl, 32 * kc, 0, lane);
+#pragma unroll
+            for (int j = 0; j < HD / 16; j++) {
+                const bf16x8_t bv = tr_frag<VST>(sV, 32 * kc, 16 * j, lane);
+                acc[j] = mfma16(al, bv, acc[j]);
+                acc[j] = mfma16(ah, bv, acc[j]);
+            }
+        }
     }
     // zeros above the diagonal (ops.cu:352-396 leaves exact zeros there)
     if (zero_fill) {

@@ -23,6 +23,7 @@
 //
 // All MFMAs are v_mfma_f32_16x16x32_bf16; rank dimensions are zero-padded to
 // multiples of 32 (r = 8, 16) or looped (r = 64).
+#include "lds_tr.hpp"
 #include "ta_internal.hpp"
 
 namespace ta {
@@ -410,8 +411,6 @@ __global__ __launch_bounds__(256) void k_rank_update(bf16* __restrict__ Y, int64
 // rows k0 + lane/4 receive, lane i, column i of rows k0..k0+3).
 constexpr int WG_TK = 64;
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef short i16x4_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) i16x4_t* lds_i16x4_p;
 
 // 8 consecutive BF16 of row `tok`, columns [c, c+8) (zero outside the
 // matrix), as a 16-byte vector
@@ -432,38 +431,6 @@ __device__ __forceinline__ u32x4 ld8z(const bf16* __restrict__ P, int64_t ld, in
 #pragma unroll
     for (int e = 0; e < 4; e++) v[e] = x[2 * e] | ((uint32_t)x[2 * e + 1] << 16);
     return v;
-}
-
-// Byte offset of element (row r, column c) in a [WG_TK][16 * NSTP] BF16 LDS
-// tile (NSTP a power of two).  The 32-byte column units of a row are
-// XOR-permuted by row bits 1..3 so that the transposing reads of rows
-// {k0..k0+3, k0+8..k0+11} (one 32-lane phase) hit distinct banks; 16-byte
-// chunks (c % 8 == 0) stay contiguous.
-template <int NSTP>
-__device__ __forceinline__ int wg_off(int r, int c) {
-    const int st = c >> 4, in = (c & 15) * 2;
-    if constexpr (NSTP == 1) {
-        return ((r * 32 + in) ^ (((r >> 3) & 1) << 7));
-    } else {
-        int x;
-        if constexpr (NSTP == 2) x = (r >> 3) & 1;
-        else if constexpr (NSTP == 4) x = ((r >> 1) & 1) | (((r >> 3) & 1) << 1);
-        else x = (r & 3) | (((r >> 3) & 1) << 2);
-        return r * 32 * NSTP + 32 * (st ^ x) + in;
-    }
-}
-
-// MFMA operand of 16 columns [c0, c0+16) x tokens [k0, k0+8) from a tile in
-// wg_off layout: lane l (group g = l/16, j = l%16) reads rows k0 + 8g + j/4
-// (and + 4), columns c0 + 4 (j%4) .. + 3; it receives column c0 + j of
-// rows k0 + 8g .. + 7, the 16x16x32 operand layout.
-template <int NSTP>
-__device__ __forceinline__ bf16x8_t wg_frag(const char* __restrict__ tile, int k0, int c0, int lane) {
-    const int g = lane >> 4, j = lane & 15;
-    const int r = k0 + 8 * g + (j >> 2), c = c0 + 4 * (j & 3);
-    i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_p)(tile + wg_off<NSTP>(r, c)));
-    i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_p)(tile + wg_off<NSTP>(r + 4, c)));
-    return __builtin_bit_cast(bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
 template <int NST, bool VEC>  // 16-column tiles of the small side; VEC: 16-byte rows
@@ -504,20 +471,20 @@ __global__ __launch_bounds__(256) void k_wgrad(const bf16* __restrict__ L, int64
 #pragma unroll
         for (int i = 0; i < 2; i++) {
             int q = threadIdx.x + 256 * i;
-            *(u32x4*)(sL + wg_off<4>(q >> 3, (q & 7) * 8)) = rl[i];
+            *(u32x4*)(sL + tr_off<4>(q >> 3, (q & 7) * 8)) = rl[i];
         }
 #pragma unroll
         for (int i = 0; i < SPT; i++) {
             int q = threadIdx.x + 256 * i;
-            if (q < SCH) *(u32x4*)(sS + wg_off<NSTP>(q / SCPR, (q % SCPR) * 8)) = rs[i];
+            if (q < SCH) *(u32x4*)(sS + tr_off<NSTP>(q / SCPR, (q % SCPR) * 8)) = rs[i];
         }
         __syncthreads();
         if (tb + WG_TK < t_end) WG_LOAD(tb + WG_TK);
 #pragma unroll
         for (int kc = 0; kc < WG_TK / 32; kc++) {
-            bf16x8_t a = wg_frag<4>(sL, 32 * kc, 16 * w, lane);
+            bf16x8_t a = tr_frag<4>(sL, 32 * kc, 16 * w, lane);
 #pragma unroll
-            for (int t = 0; t < NST; t++) acc[t] = mf16(a, wg_frag<NSTP>(sS, 32 * kc, 16 * t, lane), acc[t]);
+            for (int t = 0; t < NST; t++) acc[t] = mf16(a, tr_frag<NSTP>(sS, 32 * kc, 16 * t, lane), acc[t]);
         }
     }
 #undef WG_LOAD
