@@ -473,6 +473,9 @@ __device__ __forceinline__ void load_p_rows(float (&p)[4][4], const float* __res
 // Per (b, hq, query tile), one pass over the key tiles at or below the
 // diagonal: dP = dO V^T, dS = P (dP - D) (ops.cu:405-435), dQ = scale dS K.
 // The next tile's V, K and P are loaded while the current one computes.
+// K is staged once, in its natural layout, and read as the dS·K operand
+// through the transposing LDS read; dS (hi/lo) goes to a per-wave
+// [key][row] tile like P in the forward.
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO,
                                                      const bf16* __restrict__ K,
@@ -481,9 +484,10 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO
                                                      const float* __restrict__ Dq,
                                                      bf16* __restrict__ dQ, int T, int Hq, int Hkv,
                                                      float scale) {
+    constexpr int VST = HD / 16;
     __shared__ __attribute__((aligned(16))) bf16 sV[TK * (HD + 8)];
-    __shared__ __attribute__((aligned(16))) bf16 sKt[HD * LDT];
-    __shared__ __attribute__((aligned(16))) bf16 sS[4][2][16 * LDT];
+    __shared__ __attribute__((aligned(16))) char sK[TK * HD * 2];
+    __shared__ __attribute__((aligned(16))) char sS[4][2][TK * 16 * 2];
     int nqt = (T + TQ - 1) / TQ;
     int nbh = gridDim.x / nqt;
     int qt = nqt - 1 - (int)(blockIdx.x / nbh);  // longest rows launch first
@@ -509,16 +513,21 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO
     floatx4 acc[HD / 16];
 #pragma unroll
     for (int j = 0; j < HD / 16; j++) acc[j] = zero4();
-    Rows64<HD> lv;
-    Rows64T<HD> lkt;
+    Rows64<HD> lv, lk;
     float pn[4][4];
     lv.load(Vh, ks_, 0, T);
-    lkt.load(Kh, ks_, 0, T);
+    lk.load(Kh, ks_, 0, T);
     load_p_rows(pn, Ph, T, rbase, 0, lane);
+    char* sSh = sS[w][0];
+    char* sSl = sS[w][1];
     for (int kt = 0; kt <= qt; kt++) {
         __syncthreads();
         lv.store(sV);
-        lkt.store_t(sKt);
+#pragma unroll
+        for (int i = 0; i < Rows64<HD>::NR; i++) {
+            int q = threadIdx.x + 256 * i;
+            *(u32x4*)(sK + tr_off<VST>(q / (HD / 8), (q % (HD / 8)) * 8)) = lk.v[i];
+        }
         float pc[4][4];
 #pragma unroll
         for (int t = 0; t < 4; t++)
@@ -527,21 +536,38 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO
         __syncthreads();
         if (kt < qt) {
             lv.load(Vh, ks_, (kt + 1) * TK, T);
-            lkt.load(Kh, ks_, (kt + 1) * TK, T);
+            lk.load(Kh, ks_, (kt + 1) * TK, T);
             load_p_rows(pn, Ph, T, rbase, (kt + 1) * TK, lane);
         }
         floatx4 dP[4];
         wave_qk<HD>(dP, of, sV, lane);
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            int kl = 16 * t + (lane & 15);
+            const int kl = 16 * t + (lane & 15);
+            float d[4];
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-                put_split(sS[w][0], sS[w][1], (4 * (lane >> 4) + r) * LDT + kl,
-                          pc[t][r] * (dP[t][r] - D[r]));
+            for (int r = 0; r < 4; r++) d[r] = pc[t][r] * (dP[t][r] - D[r]);
+            uint2 hi, lo;
+            hi.x = pack2(d[0], d[1]);
+            hi.y = pack2(d[2], d[3]);
+            lo.x = pack2(d[0] - lo2f(hi.x), d[1] - hi2f(hi.x));
+            lo.y = pack2(d[2] - lo2f(hi.y), d[3] - hi2f(hi.y));
+            const int off = tr_off<1>(kl, 4 * (lane >> 4));
+            *(uint2*)(sSh + off) = hi;
+            *(uint2*)(sSl + off) = lo;
         }
         wave_sync();
-        wave_pv<HD>(acc, sS[w][0], sS[w][1], sKt, lane);
+#pragma unroll
+        for (int kc = 0; kc < TK / 32; kc++) {
+            const bf16x8_t ah = tr_frag<1>(sSh, 32 * kc, 0, lane);
+            const bf16x8_t al = tr_frag<1>(sSl, 32 * kc, 0, lane);
+#pragma unroll
+            for (int j = 0; j < HD / 16; j++) {
+                const bf16x8_t bk = tr_frag<VST>(sK, 32 * kc, 16 * j, lane);
+                acc[j] = mfma16(al, bk, acc[j]);
+                acc[j] = mfma16(ah, bk, acc[j]);
+            }
+        }
     }
     bf16* dQh = dQ + (int64_t)b * T * qs + hq * HD;
 #pragma unroll
@@ -584,18 +610,19 @@ __device__ __forceinline__ void load_p_cols(float (&p)[4][4], const float* __res
 // dK then dV); k_attn_dkv_reduce sums the GQA group in head order — the
 // group sum of ops.cu:539-555 without atomics, so dK/dV are deterministic.
 // The next query tile's dO, Q, D and P are loaded while this one computes.
+// dO is staged twice: padded rows for dP^T (16-byte fragment reads) and in
+// the transposing-read layout for the P^T·dO operand, like Q for dS^T·Q;
+// P^T and dS^T (hi/lo) go to a per-wave [query][key] tile.
 template <int HD>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_bwd_dkv(const bf16* __restrict__ dO,
-                                                      const bf16* __restrict__ Q,
-                                                      const bf16* __restrict__ V,
-                                                      const float* __restrict__ P,
-                                                      const float* __restrict__ Dq,
-                                                      float* __restrict__ part, int T, int Hq,
-                                                      int Hkv) {
-    __shared__ __attribute__((aligned(16))) bf16 sO[TQ * (HD + 8)];     // dO [q][hd]
-    __shared__ __attribute__((aligned(16))) bf16 sOt[HD * LDT];         // dO^T [hd][q]
-    __shared__ __attribute__((aligned(16))) bf16 sQt[HD * LDT];         // Q^T [hd][q]
-    __shared__ __attribute__((aligned(16))) bf16 sA[4][2][16 * LDT];    // per-wave P^T / dS^T hi,lo
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_bwd_dkv(
+    const bf16* __restrict__ dO, const bf16* __restrict__ Q, const bf16* __restrict__ V,
+    const float* __restrict__ P, const float* __restrict__ Dq, float* __restrict__ part, int T,
+    int Hq, int Hkv) {
+    constexpr int VST = HD / 16;
+    __shared__ __attribute__((aligned(16))) bf16 sO[TQ * (HD + 8)];  // dO [q][hd], padded
+    __shared__ __attribute__((aligned(16))) char sOn[TQ * HD * 2];   // dO, tr_off layout
+    __shared__ __attribute__((aligned(16))) char sQn[TQ * HD * 2];   // Q, tr_off layout
+    __shared__ __attribute__((aligned(16))) char sA[4][2][TQ * 16 * 2];  // per wave [q][key] hi,lo
     __shared__ float sD[TQ];
     int nkt = (T + TK - 1) / TK;
     int nbh = gridDim.x / nkt;
@@ -623,18 +650,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         accV[j] = zero4();
     }
     int nqt = (T + TQ - 1) / TQ;
-    Rows64T<HD> ldo, lq;
+    Rows64<HD> ldo, lq;
     float pn[4][4];
     float dn = 0.f;
     ldo.load(dOh, qs, kt * TQ, T);
     lq.load(Qh, qs, kt * TQ, T);
     load_p_cols(pn, Ph, T, kt * TQ, kbase, lane);
     if (threadIdx.x < TQ) dn = (kt * TQ + threadIdx.x < T) ? Dh[kt * TQ + threadIdx.x] : 0.f;
+    char* sAh = sA[w][0];
+    char* sAl = sA[w][1];
     for (int qt = kt; qt < nqt; qt++) {
         __syncthreads();
-        ldo.store_rows(sO);
-        ldo.store_t(sOt);
-        lq.store_t(sQt);
+        ldo.store(sO);
+#pragma unroll
+        for (int i = 0; i < Rows64<HD>::NR; i++) {
+            int q = threadIdx.x + 256 * i;
+            const int off = tr_off<VST>(q / (HD / 8), (q % (HD / 8)) * 8);
+            *(u32x4*)(sOn + off) = ldo.v[i];
+            *(u32x4*)(sQn + off) = lq.v[i];
+        }
         if (threadIdx.x < TQ) sD[threadIdx.x] = dn;
         float pv[4][4];
 #pragma unroll
@@ -651,27 +685,60 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
         }
         floatx4 dPt[4];
         wave_qk<HD>(dPt, vf, sO, lane);  // rows = keys, cols = queries
-        // dV += P^T dO
+        // dV += P^T dO: lane holds keys kbase + r (4 consecutive) of query 16t + l%16
 #pragma unroll
-        for (int t = 0; t < 4; t++)
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-                put_split(sA[w][0], sA[w][1], (4 * (lane >> 4) + r) * LDT + 16 * t + (lane & 15),
-                          pv[t][r]);
+        for (int t = 0; t < 4; t++) {
+            uint2 hi, lo;
+            hi.x = pack2(pv[t][0], pv[t][1]);
+            hi.y = pack2(pv[t][2], pv[t][3]);
+            lo.x = pack2(pv[t][0] - lo2f(hi.x), pv[t][1] - hi2f(hi.x));
+            lo.y = pack2(pv[t][2] - lo2f(hi.y), pv[t][3] - hi2f(hi.y));
+            const int off = tr_off<1>(16 * t + (lane & 15), 4 * (lane >> 4));
+            *(uint2*)(sAh + off) = hi;
+            *(uint2*)(sAl + off) = lo;
+        }
         wave_sync();
-        wave_pv<HD>(accV, sA[w][0], sA[w][1], sOt, lane);
+#pragma unroll
+        for (int kc = 0; kc < TQ / 32; kc++) {
+            const bf16x8_t ah = tr_frag<1>(sAh, 32 * kc, 0, lane);
+            const bf16x8_t al = tr_frag<1>(sAl, 32 * kc, 0, lane);
+#pragma unroll
+            for (int j = 0; j < HD / 16; j++) {
+                const bf16x8_t bo = tr_frag<VST>(sOn, 32 * kc, 16 * j, lane);
+                accV[j] = mfma16(al, bo, accV[j]);
+                accV[j] = mfma16(ah, bo, accV[j]);
+            }
+        }
         wave_sync();
         // dK += dS^T Q
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            int ql = 16 * t + (lane & 15);
+            const int ql = 16 * t + (lane & 15);
+            const float dq = sD[ql];
+            float d[4];
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-                put_split(sA[w][0], sA[w][1], (4 * (lane >> 4) + r) * LDT + ql,
-                          pv[t][r] * (dPt[t][r] - sD[ql]));
+            for (int r = 0; r < 4; r++) d[r] = pv[t][r] * (dPt[t][r] - dq);
+            uint2 hi, lo;
+            hi.x = pack2(d[0], d[1]);
+            hi.y = pack2(d[2], d[3]);
+            lo.x = pack2(d[0] - lo2f(hi.x), d[1] - hi2f(hi.x));
+            lo.y = pack2(d[2] - lo2f(hi.y), d[3] - hi2f(hi.y));
+            const int off = tr_off<1>(ql, 4 * (lane >> 4));
+            *(uint2*)(sAh + off) = hi;
+            *(uint2*)(sAl + off) = lo;
         }
         wave_sync();
-        wave_pv<HD>(accK, sA[w][0], sA[w][1], sQt, lane);
+#pragma unroll
+        for (int kc = 0; kc < TQ / 32; kc++) {
+            const bf16x8_t ah = tr_frag<1>(sAh, 32 * kc, 0, lane);
+            const bf16x8_t al = tr_frag<1>(sAl, 32 * kc, 0, lane);
+#pragma unroll
+            for (int j = 0; j < HD / 16; j++) {
+                const bf16x8_t bq = tr_frag<VST>(sQn, 32 * kc, 16 * j, lane);
+                accK[j] = mfma16(al, bq, accK[j]);
+                accK[j] = mfma16(ah, bq, accK[j]);
+            }
+        }
     }
     float* pK = part + (int64_t)bh * T * HD;
     float* pV = part + ((int64_t)gridDim.x / nkt + bh) * T * HD;
