@@ -22,7 +22,7 @@
 
 namespace ta {
 
-constexpr int kTok = 64;  // tokens per block in the accumulate pass
+constexpr int kTok = 16;  // tokens per block in the accumulate pass (512 blocks at BT = 8192)
 
 // Per-block partial row: part[blk][d] = sum_{t in block} h[t][d] * n_t,
 // part[blk][D] = sum n_t.  Rows move as 16-byte vectors when D % 8 == 0.
@@ -36,18 +36,30 @@ __global__ __launch_bounds__(256) void k_centroid_part(const void* __restrict__ 
     int64_t t0 = (int64_t)blockIdx.x * kTok;
     int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const bool v8 = BF16IN && (D & 7) == 0;
-    // 1. per-token gradient norms (one wave per token)
+    // 1. per-token gradient norms (one wave per token; a wave's 16-byte
+    // loads of its rows are issued together)
     for (int j = wv; j < kTok; j += 4) {
         int64_t t = t0 + j;
         float ss = 0.f;
         if (t < BT && !nv) {
             if (v8) {
                 const bf16x8v* g = (const bf16x8v*)((const bf16*)gv + t * D);
-                for (int c = lane; c < (D >> 3); c += 64) {
-                    float f[8];
-                    unpack8(g[c], f);
+                constexpr int U = 4;
+                for (int c0 = lane; c0 < (D >> 3); c0 += 64 * U) {
+                    bf16x8v gg[U];
 #pragma unroll
-                    for (int e = 0; e < 8; e++) ss += f[e] * f[e];
+                    for (int u = 0; u < U; u++) {
+                        const int c = c0 + 64 * u;
+                        gg[u] = g[c < (D >> 3) ? c : c0];
+                    }
+#pragma unroll
+                    for (int u = 0; u < U; u++) {
+                        if (c0 + 64 * u >= (D >> 3)) continue;
+                        float f[8];
+                        unpack8(gg[u], f);
+#pragma unroll
+                        for (int e = 0; e < 8; e++) ss += f[e] * f[e];
+                    }
                 }
             } else if (BF16IN) {
                 const bf16* g = (const bf16*)gv + t * D;
@@ -69,11 +81,18 @@ __global__ __launch_bounds__(256) void k_centroid_part(const void* __restrict__ 
     if (v8) {
         for (int c = threadIdx.x; c < (D >> 3); c += 256) {
             float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+            // all kTok row loads first (rows past BT re-read the last row;
+            // their weight is 0), then the sums in token order
+            bf16x8v hh[kTok];
+#pragma unroll
             for (int j = 0; j < kTok; j++) {
-                int64_t t = t0 + j;
-                if (t >= BT) break;
+                const int64_t t = min(t0 + j, BT - 1);
+                hh[j] = ((const bf16x8v*)((const bf16*)hv + t * D))[c];
+            }
+#pragma unroll
+            for (int j = 0; j < kTok; j++) {
                 float f[8];
-                unpack8(((const bf16x8v*)((const bf16*)hv + t * D))[c], f);
+                unpack8(hh[j], f);
 #pragma unroll
                 for (int e = 0; e < 8; e++) acc[e] += f[e] * nrm[j];
             }
@@ -99,15 +118,24 @@ __global__ __launch_bounds__(256) void k_centroid_part(const void* __restrict__ 
     }
 }
 
-// acc[d] += sum over blocks (block order) of part[b][d], in F64.
-__global__ void k_centroid_reduce(const float* __restrict__ part, int nblk, int D1,
-                                  double* __restrict__ acc) {
-    int d = blockIdx.x * blockDim.x + threadIdx.x;
-    if (d >= D1) return;
+// acc[d] += sum over blocks of part[b][d], in F64: 64 columns per block
+// (lane = column), wave w sums the blocks of its quarter in block order and
+// the four quarter sums are added in wave order — a fixed order, so the
+// result is deterministic.
+__global__ __launch_bounds__(256) void k_centroid_reduce(const float* __restrict__ part, int nblk,
+                                                         int D1, double* __restrict__ acc) {
+    __shared__ double q[4][64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int d = blockIdx.x * 64 + lane;
+    const int per = (nblk + 3) / 4, b0 = w * per, b1 = min(nblk, b0 + per);
     double s = 0.0;
+    if (d < D1) {
 #pragma unroll 8
-    for (int b = 0; b < nblk; b++) s += (double)part[(int64_t)b * D1 + d];
-    acc[d] += s;
+        for (int b = b0; b < b1; b++) s += (double)part[(int64_t)b * D1 + d];
+    }
+    q[w][lane] = s;
+    __syncthreads();
+    if (w == 0 && d < D1) acc[d] += ((q[0][lane] + q[1][lane]) + q[2][lane]) + q[3][lane];
 }
 
 // ── k-means ────────────────────────────────────────────────────────────
@@ -298,7 +326,7 @@ static int centroid_acc(const void* h, const void* g, const float* n, int64_t BT
         k_centroid_part<true><<<(int)nblk, 256, 0, s>>>(h, g, nullptr, BT, D, part);
     else
         k_centroid_part<false><<<(int)nblk, 256, 0, s>>>(h, g, n, BT, D, part);
-    k_centroid_reduce<<<(D + 1 + 255) / 256, 256, 0, s>>>(part, (int)nblk, D + 1, acc);
+    k_centroid_reduce<<<(D + 1 + 63) / 64, 256, 0, s>>>(part, (int)nblk, D + 1, acc);
     return check_launch("centroid_accumulate");
 }
 
