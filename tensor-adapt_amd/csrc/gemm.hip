@@ -368,7 +368,6 @@ __device__ __attribute__((always_inline)) inline void staged_epilogue(
     bf16* C = (bf16*)a.C;
     const bool vec = ((a.ldc & 7) == 0) && (((uintptr_t)C & 15) == 0);
     if (a.beta != 0.f) {
-#pragma unroll
         for (int q = lane; q < WTM * CPR; q += 64) {
             int row = q / CPR, ch = q % CPR;
             int gm = R0 + row, gn = C0 + 8 * ch;
@@ -446,7 +445,6 @@ __device__ __attribute__((always_inline)) inline void staged_epilogue(
             }
         }
     __builtin_amdgcn_wave_barrier();
-#pragma unroll
     for (int q = lane; q < WTM * CPR; q += 64) {
         int row = q / CPR, ch = q % CPR;
         int gm = R0 + row, gn = C0 + 8 * ch;
