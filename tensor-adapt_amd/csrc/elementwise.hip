@@ -18,16 +18,7 @@ static inline int stream_blocks(int64_t nvec, int threads) {
 static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // ── SiLU-gated activation forward — ops.cu:913-923 ──────────────────────
-// exp(-g) as v_exp_f32 of -g log2(e) and the quotient as v_rcp_f32 (each
-// within 1 ulp of F32; the reference is built with --use_fast_math, whose
-// __expf and division are approximations of the same kind)
-__device__ __forceinline__ float sigmoid_f(float g) {
-    return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-g * kLog2e));
-}
-__device__ __forceinline__ float silu_mul_f(float g, float u) {
-    float s = g * sigmoid_f(g);
-    return s * u;
-}
+// silu_mul_f: ta_internal.hpp
 __global__ void k_silu_mul_fwd(const bf16* __restrict__ gate, const bf16* __restrict__ up,
                                bf16* __restrict__ out, int64_t N) {
     int64_t nv = N >> 3;
@@ -49,13 +40,7 @@ __global__ void k_silu_mul_fwd(const bf16* __restrict__ gate, const bf16* __rest
 }
 
 // ── SiLU-gated activation backward — ops.cu:925-940 ─────────────────────
-__device__ __forceinline__ void silu_bwd_f(float d, float g, float u, float& dg, float& du) {
-    float sig = sigmoid_f(g);
-    float s = g * sig;
-    float ds = sig * (1.f + g * (1.f - sig));
-    dg = d * u * ds;
-    du = d * s;
-}
+// silu_bwd_f: ta_internal.hpp
 __global__ void k_silu_mul_bwd(const bf16* __restrict__ dout, const bf16* __restrict__ gate,
                                const bf16* __restrict__ up, bf16* __restrict__ dgate,
                                bf16* __restrict__ dup, int64_t N) {

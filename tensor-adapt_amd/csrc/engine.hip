@@ -85,6 +85,11 @@ struct Engine {
     int64_t wg_blocks = 0;
     double wg_elems = 0;
     size_t wg_cursor = 0;
+    // SwiGLU backward fused with the gate/up LoRA backward (rank 16, both
+    // pairs on, BT and I multiples of 64): its dh partials, split counts
+    bool silu_fused = false;
+    int sl_st = 0, sl_so = 0;
+    float* dh_part = nullptr;
 
     bf16 *x_final, *xfn, *logits, *g_res, *dres, *tmpH, *dact, *dgate, *dup, *dxn2, *dao, *dQ, *dK,
         *dV, *dxn, *delta, *dh, *dh_cat;
@@ -246,6 +251,11 @@ static int engine_alloc(Engine* e) {
         CK(alloc(e, &ly.up, (int64_t)BT * I, (p + "up").c_str(), 0));
         CK(alloc(e, &ly.act, (int64_t)BT * I, (p + "act").c_str(), 0));
     }
+    e->silu_fused = r == 16 && BT % 64 == 0 && I % 64 == 0;
+    if (e->silu_fused) {
+        silu_lora_splits(BT, I, &e->sl_st, &e->sl_so);
+        CK(alloc(e, &e->dh_part, (int64_t)e->sl_so * 2 * BT * 16, "lora.dh_partials"));
+    }
     // weight-gradient jobs in the order lora_group_bwd issues them: layers
     // L-1..0; groups down, gate/up, o, q/k/v; per group gB of each on-pair,
     // then gA of the group
@@ -256,10 +266,11 @@ static int engine_alloc(Engine* e) {
         };
         const G groups[4] = {{{PD}, I}, {{PG, PU}, H}, {{PO}, qd}, {{PQ, PK, PV}, H}};
         int64_t off = 0, blk = 0;
-        auto add = [&](int NL, int NS, int trans, float* g0, float* g1, float* g2) {
+        auto add = [&](int NL, int NS, int trans, float* g0, float* g1, float* g2,
+                       int splits) {
             int per = 0;
             WgradJob j{};
-            j.splits = lora_wgrad_splits(NL, BT, &per);
+            j.splits = splits > 0 ? splits : lora_wgrad_splits(NL, BT, &per);
             j.NL = NL;
             j.NS = NS;
             j.r = r;
@@ -280,13 +291,17 @@ static int engine_alloc(Engine* e) {
             for (const G& g : groups) {
                 float* ga[3] = {nullptr, nullptr, nullptr};
                 int n = 0;
+                // gB of the gate/up pairs come token-split from the fused kernel
+                const bool fused = e->silu_fused && *g.pairs.begin() == PG &&
+                                   e->L[l].pr[PG].on && e->L[l].pr[PU].on;
                 for (int p : g.pairs) {
                     Pair& pr = e->L[l].pr[p];
                     if (!pr.on) continue;
-                    add(pr.out, r, 0, e->grad + pr.offB, nullptr, nullptr);
+                    add(pr.out, r, 0, e->grad + pr.offB, nullptr, nullptr, fused ? e->sl_st : 0);
                     ga[n++] = e->grad + pr.offA;
                 }
-                if (n) add(g.in, n * r, 1, ga[0], ga[1] ? ga[1] : ga[0], ga[2] ? ga[2] : ga[0]);
+                if (n)
+                    add(g.in, n * r, 1, ga[0], ga[1] ? ga[1] : ga[0], ga[2] ? ga[2] : ga[0], 0);
             }
         e->wg_blocks = blk;
         if (!e->wg_plan.empty()) {
@@ -410,9 +425,10 @@ static int next_wgrad(Engine* e, int NL, int NS, float** part) {
 //   gB_p += s * go_p^T h_p           (h_p cached by the forward)
 //   gA_p += s * dh_p^T x             (all pairs of the group in one pass over x)
 // and returns the terms gx = bf16(s * dh_p A_p + gx) (pairs in order) for
-// the epilogue of the last input-gradient GEMM of the group.
+// the epilogue of the last input-gradient GEMM of the group.  dh_ready: dh_p
+// and the gB products were made already (the fused SwiGLU backward).
 static int lora_group_bwd(Engine* e, Layer& ly, std::initializer_list<int> group, const bf16* x,
-                          int in, const bf16* const* gos, LoraEpi* ep) {
+                          int in, const bf16* const* gos, LoraEpi* ep, bool dh_ready = false) {
     *ep = LoraEpi{};
     int on[3], n = 0, i = 0;
     const bf16* go_on[3];
@@ -427,7 +443,7 @@ static int lora_group_bwd(Engine* e, Layer& ly, std::initializer_list<int> group
     const int BT = e->BT, r = e->r;
     const double dBT = BT;
     const int64_t ldh = (int64_t)n * r;
-    for (int q = 0; q < n; q++) {
+    for (int q = 0; q < n && !dh_ready; q++) {
         Pair& pr = ly.pr[on[q]];
         const bf16* Yt[1] = {e->shadowT + pr.offB};
         bf16* C[1] = {e->dh_cat + q * r};
@@ -589,12 +605,26 @@ static int backward(Engine* e) {
             CK(lora_group_bwd(e, ly, {PD}, ly.act, I, gos, &ep));
             CK(proj_bwd_x(e, ly.Wt[PD], e->g_res, e->dact, H, I, 0.f, &ep));
         }
-        TIMED(TA_CAT_ELEMWISE, 0, dBT * I * 10,
-              ta_silu_mul_bwd(e->dact, ly.gate, ly.up, e->dgate, e->dup, (int64_t)BT * I, s));
+        const bool fused = e->silu_fused && ly.pr[PG].on && ly.pr[PU].on;
+        if (fused) {
+            // dgate, dup, dh of both pairs and their gB partials in one pass
+            float *pg = nullptr, *pu = nullptr;
+            CK(next_wgrad(e, I, e->r, &pg));
+            CK(next_wgrad(e, I, e->r, &pu));
+            const Pair &PRg = ly.pr[PG], &PRu = ly.pr[PU];
+            TIMED(TA_CAT_ELEMWISE, 4.0 * gflops(BT, e->r, I), dBT * I * 10 + dBT * 64,
+                  silu_bwd_lora(e->dact, ly.gate, ly.up, e->dgate, e->dup, e->shadowT + PRg.offB,
+                                e->shadowT + PRu.offB, PRg.h, PRu.h, e->dh_part, pg, pu, BT, I, s));
+            TIMED(TA_CAT_LORA, 0, dBT * 128.0 * e->sl_so + dBT * 64,
+                  dh_reduce2(e->dh_part, e->sl_so, BT, e->dh_cat, 2 * e->r, s));
+        } else {
+            TIMED(TA_CAT_ELEMWISE, 0, dBT * I * 10,
+                  ta_silu_mul_bwd(e->dact, ly.gate, ly.up, e->dgate, e->dup, (int64_t)BT * I, s));
+        }
         {
             const bf16* gos[2] = {e->dgate, e->dup};
             LoraEpi ep;
-            CK(lora_group_bwd(e, ly, {PG, PU}, ly.xn2, H, gos, &ep));
+            CK(lora_group_bwd(e, ly, {PG, PU}, ly.xn2, H, gos, &ep, fused));
             CK(proj_bwd_x(e, ly.Wt[PG], e->dgate, e->dxn2, I, H, 0.f));
             CK(proj_bwd_x(e, ly.Wt[PU], e->dup, e->dxn2, I, H, 1.f, &ep));
         }

@@ -529,6 +529,163 @@ __global__ __launch_bounds__(256) void k_wgrad_reduce_jobs(const WgradJob* __res
     }
 }
 
+// ── SwiGLU backward fused with the gate/up LoRA backward (rank 16) ───────
+// One pass over dact, gate and up [BT x I] instead of silu_mul_bwd followed
+// by two passes each over dgate and dup (the dh product and the gB product
+// of adapter_model.cu:131-220 for the gate and up pairs):
+//   dgate, dup = silu_mul_bwd(dact, gate, up)                  (ops.cu:925-940)
+//   dh_p[t][j] partial over the block's columns of sum_c go_p[t][c] B_p[c][j]
+//   gB_p[c][j] partial over the block's tokens  of sum_t go_p[t][c] h_p[t][j]
+// with go_0 = bf16(dgate), go_1 = bf16(dup), as the reference's products see
+// them.  Block (x, y) covers columns [x CT 64, +CT 64) and tokens
+// [y TT, +TT) in 64 x 64 tiles, column tiles outer.  Lane (w, g, j) of a
+// tile computes token 16w + j, columns 8g + 32kc .. + 7: exactly its A
+// operand of v_mfma_f32_16x16x32_bf16 for the dh product (B^T shadow
+// fragments straight from global memory).  The go tile then goes through
+// LDS (two buffers, one barrier per tile) so that wave w takes columns
+// 16w .. 16w + 15 over all 64 tokens for the gB product, with h of the
+// block's tokens held in LDS all along.  The three input tiles are loaded
+// two tiles ahead into two register buffers: about 2 x 24 KB in flight per
+// block, which HBM latency needs at two blocks per CU.
+__device__ __forceinline__ void silu_bwd8(u32x4 d, u32x4 gt, u32x4 u, u32x4& dg, u32x4& du) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        float a0, b0, a1, b1;
+        silu_bwd_f(lo2f(d[i]), lo2f(gt[i]), lo2f(u[i]), a0, b0);
+        silu_bwd_f(hi2f(d[i]), hi2f(gt[i]), hi2f(u[i]), a1, b1);
+        dg[i] = pack2(a0, a1);
+        du[i] = pack2(b0, b1);
+    }
+}
+
+template <int TT>  // tokens per block (a multiple of 128)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_silu_bwd_lora(
+    const bf16* __restrict__ dact, const bf16* __restrict__ gate, const bf16* __restrict__ up,
+    bf16* __restrict__ dgate, bf16* __restrict__ dup, const bf16* __restrict__ bt_g,
+    const bf16* __restrict__ bt_u, const bf16* __restrict__ h_g, const bf16* __restrict__ h_u,
+    float* __restrict__ dh_part, float* __restrict__ gb_g, float* __restrict__ gb_u, int BT,
+    int I, int CT) {
+    constexpr int NTT = TT / 64;  // even: the register buffer of a tile is its index parity
+    static_assert(NTT % 2 == 0, "two register buffers alternate over the token tiles");
+    __shared__ __attribute__((aligned(16))) char sH[2][TT * 32];        // h_p [t][16]
+    __shared__ __attribute__((aligned(16))) char sD[2][2][64 * 128];    // go_p tile [t][64], 2 buffers
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int g = lane >> 4, j = lane & 15;
+    const int t_beg = blockIdx.y * TT, t_end = min(BT, t_beg + TT);
+    const int c_beg = blockIdx.x * (CT * 64), c_end = min(I, c_beg + CT * 64);
+    for (int q = threadIdx.x; q < TT * 4; q += 256) {
+        const int pp = q / (TT * 2), row = (q >> 1) % TT, half = q & 1;
+        if (t_beg + row < t_end) {
+            const bf16* h = pp ? h_u : h_g;
+            *(u32x4*)(sH[pp] + tr_off<1>(row, 8 * half)) =
+                *(const u32x4*)(h + (int64_t)(t_beg + row) * 16 + 8 * half);
+        }
+    }
+    floatx4 dh[2][NTT];
+#pragma unroll
+    for (int tt = 0; tt < NTT; tt++) dh[0][tt] = dh[1][tt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    // this lane's element of a tile at (tb, cb): token tb + 16w + j, column cb + 8g (+ 32 kc)
+    const int64_t lofs = (int64_t)(16 * w + j) * I + 8 * g;
+    u32x4 ra[2][2], rg[2][2], ru[2][2];  // [buffer][kc]
+#define SL_LOAD(B, tb, cb)                                                   \
+    do {                                                                     \
+        const int64_t o_ = (int64_t)(tb) * I + (cb) + lofs;                  \
+        _Pragma("unroll") for (int kc = 0; kc < 2; kc++) {                   \
+            ra[B][kc] = *(const u32x4*)(dact + o_ + 32 * kc);                \
+            rg[B][kc] = *(const u32x4*)(gate + o_ + 32 * kc);                \
+            ru[B][kc] = *(const u32x4*)(up + o_ + 32 * kc);                  \
+        }                                                                    \
+    } while (0)
+    SL_LOAD(0, t_beg, c_beg);
+    if (t_beg + 64 < t_end) SL_LOAD(1, t_beg + 64, c_beg);
+    int sb = 0;  // LDS buffer of the next tile
+    for (int cb = c_beg; cb < c_end; cb += 64) {
+        bf16x8_t fb[2][2];  // B^T shadow: row j, columns cb + 32 kc + 8g .. + 7
+#pragma unroll
+        for (int kc = 0; kc < 2; kc++) {
+            fb[0][kc] = *(const bf16x8_t*)(bt_g + (int64_t)j * I + cb + 32 * kc + 8 * g);
+            fb[1][kc] = *(const bf16x8_t*)(bt_u + (int64_t)j * I + cb + 32 * kc + 8 * g);
+        }
+        floatx4 gb[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int tt = 0; tt < NTT; tt++) {
+            const int tb = t_beg + 64 * tt;
+            const int B = tt & 1;
+            if (tb < t_end) {  // block-uniform
+                u32x4 og[2], ou[2];
+#pragma unroll
+                for (int kc = 0; kc < 2; kc++)
+                    silu_bwd8(ra[B][kc], rg[B][kc], ru[B][kc], og[kc], ou[kc]);
+                // two tiles ahead into this buffer: token tile tt + 2, else
+                // the next column tile's token tile tt + 2 - NTT
+                if (tt + 2 < NTT) {
+                    if (tb + 128 < t_end) SL_LOAD(B, tb + 128, cb);
+                } else if (cb + 64 < c_end && t_beg + 64 * (tt + 2 - NTT) < t_end) {
+                    SL_LOAD(B, t_beg + 64 * (tt + 2 - NTT), cb + 64);
+                }
+                const int64_t o = (int64_t)tb * I + cb + lofs;
+                char* sd0 = sD[sb][0];
+                char* sd1 = sD[sb][1];
+#pragma unroll
+                for (int kc = 0; kc < 2; kc++) {
+                    *(u32x4*)(dgate + o + 32 * kc) = og[kc];
+                    *(u32x4*)(dup + o + 32 * kc) = ou[kc];
+                    dh[0][tt] = mf16(__builtin_bit_cast(bf16x8_t, og[kc]), fb[0][kc], dh[0][tt]);
+                    dh[1][tt] = mf16(__builtin_bit_cast(bf16x8_t, ou[kc]), fb[1][kc], dh[1][tt]);
+                    *(u32x4*)(sd0 + tr_off<4>(16 * w + j, 32 * kc + 8 * g)) = og[kc];
+                    *(u32x4*)(sd1 + tr_off<4>(16 * w + j, 32 * kc + 8 * g)) = ou[kc];
+                }
+                // the other buffer's readers (the previous tile) are done once
+                // every wave has passed this barrier
+                __syncthreads();
+#pragma unroll
+                for (int kc = 0; kc < 2; kc++) {
+                    bf16x8_t a0 = tr_frag<4>(sd0, 32 * kc, 16 * w, lane);
+                    bf16x8_t b0 = tr_frag<1>(sH[0], tb - t_beg + 32 * kc, 0, lane);
+                    gb[0] = mf16(a0, b0, gb[0]);
+                    bf16x8_t a1 = tr_frag<4>(sd1, 32 * kc, 16 * w, lane);
+                    bf16x8_t b1 = tr_frag<1>(sH[1], tb - t_beg + 32 * kc, 0, lane);
+                    gb[1] = mf16(a1, b1, gb[1]);
+                }
+                sb ^= 1;
+            }
+        }
+        // gB partial of split y: rows (columns of I) cb + 16w + 4g + i, rank j
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int64_t o = ((int64_t)blockIdx.y * I + cb + 16 * w + 4 * g + i) * 16 + j;
+            gb_g[o] = gb[0][i];
+            gb_u[o] = gb[1][i];
+        }
+    }
+#undef SL_LOAD
+    // dh partial of column split x: tokens tb + 16w + 4g + i, rank j
+#pragma unroll
+    for (int tt = 0; tt < NTT; tt++) {
+        const int tb = t_beg + 64 * tt;
+        if (tb < t_end) {
+#pragma unroll
+            for (int pp = 0; pp < 2; pp++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    dh_part[(((int64_t)blockIdx.x * 2 + pp) * BT + tb + 16 * w + 4 * g + i) * 16 + j] =
+                        dh[pp][tt][i];
+        }
+    }
+}
+
+// dh[t][16p + j] = bf16(sum over the column splits, in order, of dh_part[s][p][t][j])
+__global__ __launch_bounds__(256) void k_dh_reduce2(const float* __restrict__ dh_part, int s_o,
+                                                    int BT, bf16* __restrict__ dh, int64_t ldh) {
+    const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (q >= (int64_t)BT * 32) return;
+    const int64_t t = q >> 5;
+    const int pp = (int)(q >> 4) & 1, jj = (int)q & 15;
+    float v = 0.f;
+    for (int s = 0; s < s_o; s++) v += dh_part[(((int64_t)s * 2 + pp) * BT + t) * 16 + jj];
+    dh[t * ldh + 16 * pp + jj] = f2bf(v);
+}
+
 // Batched transpose of the BF16 B shadows into B^T (one launch per step).
 struct TDesc {
     int64_t src, dst;
@@ -674,6 +831,46 @@ int lora_wgrad_reduce_jobs(const WgradJob* jobs, int njobs, int64_t total_blocks
         kprof_end(KP_LORA_WGRAD, s, 0.0, 8.0 * elems,
                   "ta::k_wgrad + ta::k_wgrad_reduce_jobs (all instances)");
     return check_launch("lora_wgrad_reduce_jobs");
+}
+
+// k_silu_bwd_lora: TT tokens per block; CT column tiles per block chosen
+// so that the grid is at most two blocks per CU (its occupancy), all
+// resident at once
+static constexpr int SL_TT = 256;
+static void silu_lora_plan(int BT, int I, int* s_t, int* s_o, int* ct) {
+    *s_t = (BT + SL_TT - 1) / SL_TT;
+    const int tiles = (I + 63) / 64;
+    int max_o = 512 / *s_t;
+    if (max_o < 1) max_o = 1;
+    *ct = (tiles + max_o - 1) / max_o;
+    *s_o = (tiles + *ct - 1) / *ct;
+}
+int silu_lora_splits(int BT, int I, int* s_t, int* s_o) {
+    int ct = 0;
+    silu_lora_plan(BT, I, s_t, s_o, &ct);
+    return 0;
+}
+
+int silu_bwd_lora(const bf16* dact, const bf16* gate, const bf16* up, bf16* dgate, bf16* dup,
+                  const bf16* bt_g, const bf16* bt_u, const bf16* h_g, const bf16* h_u,
+                  float* dh_part, float* gb_g, float* gb_u, int BT, int I, hipStream_t s) {
+    TA_REQUIRE(BT > 0 && I > 0 && BT % 64 == 0 && I % 64 == 0,
+               "silu_bwd_lora: BT %d and I %d must be positive multiples of 64", BT, I);
+    const void* ptrs[] = {dact, gate, up, dgate, dup, bt_g, bt_u, h_g, h_u, dh_part, gb_g, gb_u};
+    for (const void* q : ptrs)
+        TA_REQUIRE(q && ((uintptr_t)q & 15) == 0, "silu_bwd_lora: null or unaligned operand");
+    int s_t = 0, s_o = 0, ct = 0;
+    silu_lora_plan(BT, I, &s_t, &s_o, &ct);
+    k_silu_bwd_lora<SL_TT><<<dim3(s_o, s_t), 256, 0, s>>>(dact, gate, up, dgate, dup, bt_g, bt_u,
+                                                          h_g, h_u, dh_part, gb_g, gb_u, BT, I, ct);
+    return check_launch("silu_bwd_lora");
+}
+
+int dh_reduce2(const float* dh_part, int s_o, int BT, bf16* dh, int64_t ldh, hipStream_t s) {
+    TA_REQUIRE(dh_part && dh && s_o > 0 && BT > 0 && ldh >= 32, "dh_reduce2: bad arguments");
+    const int64_t n = (int64_t)BT * 32;
+    k_dh_reduce2<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(dh_part, s_o, BT, dh, ldh);
+    return check_launch("dh_reduce2");
 }
 
 int transpose_batch(const bf16* src, bf16* dst, const void* descs, int nd, hipStream_t s) {

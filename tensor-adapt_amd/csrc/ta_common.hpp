@@ -67,6 +67,26 @@ __device__ __forceinline__ double wave_sum_d(double v) {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// ── SwiGLU math (ops.cu:913-940), shared by the elementwise kernels and the
+// fused SwiGLU-backward + LoRA kernel.  exp(-g) as v_exp_f32 of -g log2(e)
+// and the quotient as v_rcp_f32 (each within 1 ulp of F32; the reference is
+// built with --use_fast_math, whose __expf and division are approximations
+// of the same kind).
+__device__ __forceinline__ float sigmoid_f(float g) {
+    return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-g * kLog2e));
+}
+__device__ __forceinline__ float silu_mul_f(float g, float u) {
+    float s = g * sigmoid_f(g);
+    return s * u;
+}
+__device__ __forceinline__ void silu_bwd_f(float d, float g, float u, float& dg, float& du) {
+    float sig = sigmoid_f(g);
+    float s = g * sig;
+    float ds = sig * (1.f + g * (1.f - sig));
+    dg = d * u * ds;
+    du = d * s;
+}
+
 }  // namespace ta
 
 // Launch-status plumbing for the C-ABI: every entry point returns 0 or a

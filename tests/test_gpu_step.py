@@ -147,3 +147,27 @@ def test_small_all_targets_multistep_matches_oracle():
     ca, cw = eng.centroid()
     oa, ow = orc.centroid()
     assert rel(ca, oa) < 1e-2 and abs(cw - ow) <= 1e-2 * ow
+
+
+def test_small_long_batch_matches_oracle():
+    """B*T = 1024 tokens: the fused SwiGLU backward + gate/up LoRA backward
+    splits the tokens over two blocks (512 each) and the intermediate width
+    over two column splits, so both of its partial reductions (dh over
+    columns, gB over tokens) run with more than one term.  Step 2 starts
+    from the oracle's state after step 1 (B != 0, so dh and gA are
+    nonzero)."""
+    mc, ac, B, T = SMALL_MODEL, SMALL_ADAPT, 2, 512
+    orc, eng = make_pair(mc, ac, B, T, seed=31)
+    rng = np.random.default_rng(13)
+    for step in range(2):
+        sync_state(orc, eng, mc, ac)
+        state = snapshot(orc, mc, ac)
+        toks = rng.integers(0, mc["vocab"], B * T + 1).astype(np.int32)
+        inp, tgt = toks[:-1].copy(), toks[1:].copy()
+        so = orc.step(inp, tgt, B, T)
+        sg = eng.step(inp, tgt)
+        assert abs(sg["loss"] - so["loss"]) <= 1e-3 * abs(so["loss"]), (step, sg, so)
+        assert abs(sg["gnorm_raw"] - so["gnorm_raw"]) <= 1e-2 * so["gnorm_raw"], (step, sg, so)
+        if so["gnorm_raw"] <= ac["grad_clip"]:
+            compare(orc, eng, mc, ac, ("gB",) if step == 0 else ("gA", "gB"))
+        check_adamw_of_own_grads(eng, mc, ac, state, sg["lr"], step + 1, sg["gnorm_raw"])
