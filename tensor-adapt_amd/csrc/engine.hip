@@ -253,7 +253,7 @@ static int engine_alloc(Engine* e) {
     }
     e->silu_fused = r == 16 && BT % 64 == 0 && I % 64 == 0;
     if (e->silu_fused) {
-        silu_lora_splits(BT, I, &e->sl_st, &e->sl_so);
+        CK(silu_lora_splits(BT, I, &e->sl_st, &e->sl_so));
         CK(alloc(e, &e->dh_part, (int64_t)e->sl_so * 2 * BT * 16, "lora.dh_partials"));
     }
     // weight-gradient jobs in the order lora_group_bwd issues them: layers

@@ -23,6 +23,8 @@
 //
 // All MFMAs are v_mfma_f32_16x16x32_bf16; rank dimensions are zero-padded to
 // multiples of 32 (r = 8, 16) or looped (r = 64).
+#include <algorithm>
+
 #include "lds_tr.hpp"
 #include "ta_internal.hpp"
 
@@ -537,16 +539,35 @@ __global__ __launch_bounds__(256) void k_wgrad_reduce_jobs(const WgradJob* __res
 //   dh_p[t][j] partial over the block's columns of sum_c go_p[t][c] B_p[c][j]
 //   gB_p[c][j] partial over the block's tokens  of sum_t go_p[t][c] h_p[t][j]
 // with go_0 = bf16(dgate), go_1 = bf16(dup), as the reference's products see
-// them.  Block (x, y) covers columns [x CT 64, +CT 64) and tokens
-// [y TT, +TT) in 64 x 64 tiles, column tiles outer.  Lane (w, g, j) of a
-// tile computes token 16w + j, columns 8g + 32kc .. + 7: exactly its A
-// operand of v_mfma_f32_16x16x32_bf16 for the dh product (B^T shadow
-// fragments straight from global memory).  The go tile then goes through
-// LDS (two buffers, one barrier per tile) so that wave w takes columns
-// 16w .. 16w + 15 over all 64 tokens for the gB product, with h of the
-// block's tokens held in LDS all along.  The three input tiles are loaded
-// two tiles ahead into two register buffers: about 2 x 24 KB in flight per
-// block, which HBM latency needs at two blocks per CU.
+// them.
+//
+// Block (x, y) of NW waves: columns [64 NW x, 64 NW (x + 1)) (wave w: 64 of
+// them) and token range y, walked in 16-token tiles.  Every global load and store of a
+// wave covers 8 rows x one whole 128-byte line (lane l: row l/8, columns
+// 8 (l%8) .. + 7): lines split between two instructions cost about 20% of
+// the bandwidth.  The go tile goes to wave-private LDS, from which the wave
+// reads its MFMA operands: rows as the 16x16x32 A operand of the dh product
+// (B^T shadow fragments of the wave's columns held in registers), columns
+// through transposing reads as the 16x16x16 A operand of the gB product (h
+// of the tile, also via wave-private LDS, as B).  gB accumulates in
+// registers over the block's tokens (each wave owns its columns); the NW
+// waves' dh partials of a tile are added in wave order through LDS (two
+// buffers, one barrier per tile).  Inputs are loaded two tiles ahead.
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+// byte offset of (row r < 16, column c < 64) in a wave's [16][64] BF16 tile:
+// 32-byte units XOR-permuted by (r >> 1) & 3 and their 16-byte halves by
+// (r >> 3) & 1, so that row reads (16 rows, 16 B each), transposing reads
+// (rows 4g'..4g'+3, g' = 0, 1) and line-shaped writes hit distinct banks
+__device__ __forceinline__ int sw_off(int r, int c) {
+    return r * 128 + 32 * ((c >> 4) ^ ((r >> 1) & 3)) + 16 * (((c >> 3) & 1) ^ ((r >> 3) & 1)) +
+           (c & 7) * 2;
+}
+__device__ __forceinline__ s16x4_t tr4(const char* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_p)p);
+}
+__device__ __forceinline__ floatx4 mf16k16(s16x4_t a, s16x4_t b, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
 __device__ __forceinline__ void silu_bwd8(u32x4 d, u32x4 gt, u32x4 u, u32x4& dg, u32x4& du) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -558,119 +579,127 @@ __device__ __forceinline__ void silu_bwd8(u32x4 d, u32x4 gt, u32x4 u, u32x4& dg,
     }
 }
 
-template <int TT>  // tokens per block (a multiple of 128)
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_silu_bwd_lora(
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void k_silu_bwd_lora(
     const bf16* __restrict__ dact, const bf16* __restrict__ gate, const bf16* __restrict__ up,
     bf16* __restrict__ dgate, bf16* __restrict__ dup, const bf16* __restrict__ bt_g,
     const bf16* __restrict__ bt_u, const bf16* __restrict__ h_g, const bf16* __restrict__ h_u,
     float* __restrict__ dh_part, float* __restrict__ gb_g, float* __restrict__ gb_u, int BT,
-    int I, int CT) {
-    constexpr int NTT = TT / 64;  // even: the register buffer of a tile is its index parity
-    static_assert(NTT % 2 == 0, "two register buffers alternate over the token tiles");
-    __shared__ __attribute__((aligned(16))) char sH[2][TT * 32];        // h_p [t][16]
-    __shared__ __attribute__((aligned(16))) char sD[2][2][64 * 128];    // go_p tile [t][64], 2 buffers
+    int I, int per) {
+    __shared__ __attribute__((aligned(16))) char sW[NW][2][16 * 128];  // go tiles per wave, pair
+    __shared__ __attribute__((aligned(16))) char sHw[NW][2][16 * 32];  // h tiles per wave, pair
+    __shared__ __attribute__((aligned(16))) float sDh[2][NW][8][64];   // dh partials [buf][wave]
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int g = lane >> 4, j = lane & 15;
-    const int t_beg = blockIdx.y * TT, t_end = min(BT, t_beg + TT);
-    const int c_beg = blockIdx.x * (CT * 64), c_end = min(I, c_beg + CT * 64);
-    for (int q = threadIdx.x; q < TT * 4; q += 256) {
-        const int pp = q / (TT * 2), row = (q >> 1) % TT, half = q & 1;
-        if (t_beg + row < t_end) {
-            const bf16* h = pp ? h_u : h_g;
-            *(u32x4*)(sH[pp] + tr_off<1>(row, 8 * half)) =
-                *(const u32x4*)(h + (int64_t)(t_beg + row) * 16 + 8 * half);
-        }
-    }
-    floatx4 dh[2][NTT];
-#pragma unroll
-    for (int tt = 0; tt < NTT; tt++) dh[0][tt] = dh[1][tt] = floatx4{0.f, 0.f, 0.f, 0.f};
-    // this lane's element of a tile at (tb, cb): token tb + 16w + j, column cb + 8g (+ 32 kc)
-    const int64_t lofs = (int64_t)(16 * w + j) * I + 8 * g;
-    u32x4 ra[2][2], rg[2][2], ru[2][2];  // [buffer][kc]
-#define SL_LOAD(B, tb, cb)                                                   \
-    do {                                                                     \
-        const int64_t o_ = (int64_t)(tb) * I + (cb) + lofs;                  \
-        _Pragma("unroll") for (int kc = 0; kc < 2; kc++) {                   \
-            ra[B][kc] = *(const u32x4*)(dact + o_ + 32 * kc);                \
-            rg[B][kc] = *(const u32x4*)(gate + o_ + 32 * kc);                \
-            ru[B][kc] = *(const u32x4*)(up + o_ + 32 * kc);                  \
-        }                                                                    \
+    const int t_beg = blockIdx.y * per, t_end = min(BT, t_beg + per);
+    const int c0 = blockIdx.x * (NW * 64), cw = c0 + 64 * w;
+    const bool act = cw < I;                    // wave-uniform: I is a multiple of 64
+    const int nact = min(NW, (I - c0) >> 6);     // active waves of the block
+    // line-shaped element of a tile at token tb: rows lane/8 (+ 8i), columns cw + 8 (lane%8)
+    const int64_t lofs = (int64_t)(lane >> 3) * I + cw + 8 * (lane & 7);
+    // h element of a tile: pair lane/32, row (lane/2)%16, half lane%2
+    const int hp = lane >> 5, hrow = (lane >> 1) & 15, hh = lane & 1;
+    const bf16* hsrc = (hp ? h_u : h_g) + hrow * 16 + 8 * hh;
+    char* const sw0 = sW[w][0];
+    char* const sw1 = sW[w][1];
+    char* const shw = sHw[w][0];
+    u32x4 ra[2][2], rg[2][2], ru[2][2], rh[2];  // [buffer][row half]
+#define SL_LOAD(B, tb)                                                        \
+    do {                                                                      \
+        const int64_t o_ = (int64_t)(tb) * I + lofs;                          \
+        _Pragma("unroll") for (int i = 0; i < 2; i++) {                       \
+            ra[B][i] = *(const u32x4*)(dact + o_ + 8 * (int64_t)I * i);       \
+            rg[B][i] = *(const u32x4*)(gate + o_ + 8 * (int64_t)I * i);       \
+            ru[B][i] = *(const u32x4*)(up + o_ + 8 * (int64_t)I * i);         \
+        }                                                                     \
+        rh[B] = *(const u32x4*)(hsrc + (int64_t)(tb) * 16);                   \
     } while (0)
-    SL_LOAD(0, t_beg, c_beg);
-    if (t_beg + 64 < t_end) SL_LOAD(1, t_beg + 64, c_beg);
-    int sb = 0;  // LDS buffer of the next tile
-    for (int cb = c_beg; cb < c_end; cb += 64) {
-        bf16x8_t fb[2][2];  // B^T shadow: row j, columns cb + 32 kc + 8g .. + 7
+    bf16x8_t fb[2][2];  // B^T shadow: row j, columns cw + 32 kc + 8g .. + 7
+    floatx4 gb[2][4];   // [pair][16-column group] over the block's tokens
+#pragma unroll
+    for (int ct = 0; ct < 4; ct++) gb[0][ct] = gb[1][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (act) {
 #pragma unroll
         for (int kc = 0; kc < 2; kc++) {
-            fb[0][kc] = *(const bf16x8_t*)(bt_g + (int64_t)j * I + cb + 32 * kc + 8 * g);
-            fb[1][kc] = *(const bf16x8_t*)(bt_u + (int64_t)j * I + cb + 32 * kc + 8 * g);
+            fb[0][kc] = *(const bf16x8_t*)(bt_g + (int64_t)j * I + cw + 32 * kc + 8 * g);
+            fb[1][kc] = *(const bf16x8_t*)(bt_u + (int64_t)j * I + cw + 32 * kc + 8 * g);
         }
-        floatx4 gb[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+        if (t_beg < t_end) SL_LOAD(0, t_beg);
+        if (t_beg + 16 < t_end) SL_LOAD(1, t_beg + 16);
+    }
+    // transposing-read lane offsets: row 4g + j/4, columns 4 (j%4) ..
+    const int rr = 4 * g + (j >> 2), cc = 4 * (j & 3);
+    for (int tb0 = t_beg; tb0 < t_end; tb0 += 32) {
 #pragma unroll
-        for (int tt = 0; tt < NTT; tt++) {
-            const int tb = t_beg + 64 * tt;
-            const int B = tt & 1;
+        for (int B = 0; B < 2; B++) {
+            const int tb = tb0 + 16 * B;
             if (tb < t_end) {  // block-uniform
-                u32x4 og[2], ou[2];
+                floatx4 dhw[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+                if (act) {
+                    u32x4 og[2], ou[2];
 #pragma unroll
-                for (int kc = 0; kc < 2; kc++)
-                    silu_bwd8(ra[B][kc], rg[B][kc], ru[B][kc], og[kc], ou[kc]);
-                // two tiles ahead into this buffer: token tile tt + 2, else
-                // the next column tile's token tile tt + 2 - NTT
-                if (tt + 2 < NTT) {
-                    if (tb + 128 < t_end) SL_LOAD(B, tb + 128, cb);
-                } else if (cb + 64 < c_end && t_beg + 64 * (tt + 2 - NTT) < t_end) {
-                    SL_LOAD(B, t_beg + 64 * (tt + 2 - NTT), cb + 64);
-                }
-                const int64_t o = (int64_t)tb * I + cb + lofs;
-                char* sd0 = sD[sb][0];
-                char* sd1 = sD[sb][1];
+                    for (int i = 0; i < 2; i++) silu_bwd8(ra[B][i], rg[B][i], ru[B][i], og[i], ou[i]);
+                    const u32x4 hv = rh[B];
+                    if (tb + 32 < t_end) SL_LOAD(B, tb + 32);
+                    const int64_t o = (int64_t)tb * I + lofs;
+                    const int lr = lane >> 3, lc = 8 * (lane & 7);
 #pragma unroll
-                for (int kc = 0; kc < 2; kc++) {
-                    *(u32x4*)(dgate + o + 32 * kc) = og[kc];
-                    *(u32x4*)(dup + o + 32 * kc) = ou[kc];
-                    dh[0][tt] = mf16(__builtin_bit_cast(bf16x8_t, og[kc]), fb[0][kc], dh[0][tt]);
-                    dh[1][tt] = mf16(__builtin_bit_cast(bf16x8_t, ou[kc]), fb[1][kc], dh[1][tt]);
-                    *(u32x4*)(sd0 + tr_off<4>(16 * w + j, 32 * kc + 8 * g)) = og[kc];
-                    *(u32x4*)(sd1 + tr_off<4>(16 * w + j, 32 * kc + 8 * g)) = ou[kc];
+                    for (int i = 0; i < 2; i++) {
+                        *(u32x4*)(dgate + o + 8 * (int64_t)I * i) = og[i];
+                        *(u32x4*)(dup + o + 8 * (int64_t)I * i) = ou[i];
+                        *(u32x4*)(sw0 + sw_off(lr + 8 * i, lc)) = og[i];
+                        *(u32x4*)(sw1 + sw_off(lr + 8 * i, lc)) = ou[i];
+                    }
+                    *(u32x4*)(shw + hp * 512 + tr_off<1>(hrow, 8 * hh)) = hv;
+                    // one wave's LDS instructions execute in order, so the
+                    // reads below see the writes above; keep the compiler
+                    // from moving them across
+                    asm volatile("" ::: "memory");
+#pragma unroll
+                    for (int kc = 0; kc < 2; kc++) {
+                        const bf16x8_t a0 = *(const bf16x8_t*)(sw0 + sw_off(j, 32 * kc + 8 * g));
+                        const bf16x8_t a1 = *(const bf16x8_t*)(sw1 + sw_off(j, 32 * kc + 8 * g));
+                        dhw[0] = mf16(a0, fb[0][kc], dhw[0]);
+                        dhw[1] = mf16(a1, fb[1][kc], dhw[1]);
+                    }
+                    const s16x4_t hb0 = tr4(shw + tr_off<1>(rr, cc));
+                    const s16x4_t hb1 = tr4(shw + 512 + tr_off<1>(rr, cc));
+#pragma unroll
+                    for (int ct = 0; ct < 4; ct++) {
+                        gb[0][ct] = mf16k16(tr4(sw0 + sw_off(rr, 16 * ct + cc)), hb0, gb[0][ct]);
+                        gb[1][ct] = mf16k16(tr4(sw1 + sw_off(rr, 16 * ct + cc)), hb1, gb[1][ct]);
+                    }
+                    asm volatile("" ::: "memory");
                 }
-                // the other buffer's readers (the previous tile) are done once
-                // every wave has passed this barrier
+                // dh of the tile over the block's columns: waves' partials in wave order
+#pragma unroll
+                for (int pp = 0; pp < 2; pp++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) sDh[B][w][pp * 4 + i][lane] = dhw[pp][i];
                 __syncthreads();
 #pragma unroll
-                for (int kc = 0; kc < 2; kc++) {
-                    bf16x8_t a0 = tr_frag<4>(sd0, 32 * kc, 16 * w, lane);
-                    bf16x8_t b0 = tr_frag<1>(sH[0], tb - t_beg + 32 * kc, 0, lane);
-                    gb[0] = mf16(a0, b0, gb[0]);
-                    bf16x8_t a1 = tr_frag<4>(sd1, 32 * kc, 16 * w, lane);
-                    bf16x8_t b1 = tr_frag<1>(sH[1], tb - t_beg + 32 * kc, 0, lane);
-                    gb[1] = mf16(a1, b1, gb[1]);
+                for (int k = 0; k < 512 / (NW * 64); k++) {
+                    const int e = threadIdx.x + NW * 64 * k;
+                    const int pp = e >> 8, i = (e >> 6) & 3, ln = e & 63;
+                    float v = sDh[B][0][pp * 4 + i][ln];
+                    for (int ww = 1; ww < nact; ww++) v += sDh[B][ww][pp * 4 + i][ln];
+                    dh_part[(((int64_t)blockIdx.x * 2 + pp) * BT + tb + 4 * (ln >> 4) + i) * 16 +
+                            (ln & 15)] = v;
                 }
-                sb ^= 1;
             }
-        }
-        // gB partial of split y: rows (columns of I) cb + 16w + 4g + i, rank j
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int64_t o = ((int64_t)blockIdx.y * I + cb + 16 * w + 4 * g + i) * 16 + j;
-            gb_g[o] = gb[0][i];
-            gb_u[o] = gb[1][i];
         }
     }
 #undef SL_LOAD
-    // dh partial of column split x: tokens tb + 16w + 4g + i, rank j
+    // gB partial of token range y: rows (columns of I) cw + 16ct + 4g + i, rank j
+    if (act) {
 #pragma unroll
-    for (int tt = 0; tt < NTT; tt++) {
-        const int tb = t_beg + 64 * tt;
-        if (tb < t_end) {
+        for (int ct = 0; ct < 4; ct++)
 #pragma unroll
-            for (int pp = 0; pp < 2; pp++)
-#pragma unroll
-                for (int i = 0; i < 4; i++)
-                    dh_part[(((int64_t)blockIdx.x * 2 + pp) * BT + tb + 16 * w + 4 * g + i) * 16 + j] =
-                        dh[pp][tt][i];
-        }
+            for (int i = 0; i < 4; i++) {
+                const int64_t o = ((int64_t)blockIdx.y * I + cw + 16 * ct + 4 * g + i) * 16 + j;
+                gb_g[o] = gb[0][ct][i];
+                gb_u[o] = gb[1][ct][i];
+            }
     }
 }
 
@@ -833,22 +862,30 @@ int lora_wgrad_reduce_jobs(const WgradJob* jobs, int njobs, int64_t total_blocks
     return check_launch("lora_wgrad_reduce_jobs");
 }
 
-// k_silu_bwd_lora: TT tokens per block; CT column tiles per block chosen
-// so that the grid is at most two blocks per CU (its occupancy), all
-// resident at once
-static constexpr int SL_TT = 256;
-static void silu_lora_plan(int BT, int I, int* s_t, int* s_o, int* ct) {
-    *s_t = (BT + SL_TT - 1) / SL_TT;
-    const int tiles = (I + 63) / 64;
-    int max_o = 512 / *s_t;
-    if (max_o < 1) max_o = 1;
-    *ct = (tiles + max_o - 1) / max_o;
-    *s_o = (tiles + *ct - 1) / *ct;
+// k_silu_bwd_lora grid: SL_NW waves of 64 columns per block (512 columns:
+// half the dh partials of 256-column blocks, measured a little faster); the
+// tokens are cut into as many ranges (multiples of 32 tokens) as keep every
+// block resident at once (blocks per CU from the occupancy query, once per
+// process): more blocks in flight than that were measured slower
+static constexpr int SL_NW = 8;
+static int silu_lora_plan(int BT, int I, int* s_t, int* s_o, int* per) {
+    static int resident = 0;
+    if (!resident) {
+        int nb = 0, dev = 0, ncu = 0;
+        TA_HIP(hipGetDevice(&dev));
+        TA_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
+        TA_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_silu_bwd_lora<SL_NW>, SL_NW * 64, 0));
+        resident = std::max(1, nb) * std::max(1, ncu);
+    }
+    *s_o = (I + SL_NW * 64 - 1) / (SL_NW * 64);
+    int ranges = std::max(1, std::min(resident / *s_o, BT / 32));
+    *per = (BT / ranges + 31) / 32 * 32;
+    *s_t = (BT + *per - 1) / *per;
+    return 0;
 }
 int silu_lora_splits(int BT, int I, int* s_t, int* s_o) {
-    int ct = 0;
-    silu_lora_plan(BT, I, s_t, s_o, &ct);
-    return 0;
+    int per = 0;
+    return silu_lora_plan(BT, I, s_t, s_o, &per);
 }
 
 int silu_bwd_lora(const bf16* dact, const bf16* gate, const bf16* up, bf16* dgate, bf16* dup,
@@ -859,10 +896,10 @@ int silu_bwd_lora(const bf16* dact, const bf16* gate, const bf16* up, bf16* dgat
     const void* ptrs[] = {dact, gate, up, dgate, dup, bt_g, bt_u, h_g, h_u, dh_part, gb_g, gb_u};
     for (const void* q : ptrs)
         TA_REQUIRE(q && ((uintptr_t)q & 15) == 0, "silu_bwd_lora: null or unaligned operand");
-    int s_t = 0, s_o = 0, ct = 0;
-    silu_lora_plan(BT, I, &s_t, &s_o, &ct);
-    k_silu_bwd_lora<SL_TT><<<dim3(s_o, s_t), 256, 0, s>>>(dact, gate, up, dgate, dup, bt_g, bt_u,
-                                                          h_g, h_u, dh_part, gb_g, gb_u, BT, I, ct);
+    int s_t = 0, s_o = 0, per = 0;
+    if (int rc = silu_lora_plan(BT, I, &s_t, &s_o, &per)) return rc;
+    k_silu_bwd_lora<SL_NW><<<dim3(s_o, s_t), SL_NW * 64, 0, s>>>(dact, gate, up, dgate, dup, bt_g, bt_u, h_g, h_u,
+                                                   dh_part, gb_g, gb_u, BT, I, per);
     return check_launch("silu_bwd_lora");
 }
 
