@@ -556,9 +556,12 @@ static int forward(Engine* e) {
                               s));
         CK(lora_group_h(e, ly, {PG, PU}, ly.xn2, H));
         {
+            // gate and up projections (qwen2.cu:21-30, each with its LoRA
+            // delta) in one launch over both weight matrices
             LoraEpi eg = fwd_epi(e, ly.pr[PG]), eu = fwd_epi(e, ly.pr[PU]);
-            CK(proj_fwd(e, ly.W[PG], ly.xn2, ly.gate, H, I, nullptr, &eg));
-            CK(proj_fwd(e, ly.W[PU], ly.xn2, ly.up, H, I, nullptr, &eu));
+            TIMED(TA_CAT_GEMM_FWD, 2.0 * gflops(BT, I, H), 2.0 * gbytes(BT, I, H, 2, 2, false),
+                  gemm_pair(BT, I, H, ly.xn2, H, ly.W[PG], ly.W[PU], H, ly.gate, ly.up, I, &eg,
+                            &eu, s));
         }
         TIMED(TA_CAT_ELEMWISE, 0, dBT * I * 6,
               ta_silu_mul_fwd(ly.gate, ly.up, ly.act, (int64_t)BT * I, s));

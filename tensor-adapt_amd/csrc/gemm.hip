@@ -62,6 +62,14 @@ struct GemmArgs {
     const bf16* lora_u[3];
     int64_t lora_ldu[3];
     const bf16* lora_v[3];
+    // N-concatenated pair (k_gemm_pipe only; tn_split = 0 otherwise): tile
+    // columns tn >= tn_split compute a second GEMM of the same shape and X,
+    // with Y2, C2 and the LoRA operands of its single pair (u2, v2)
+    int tn_split;
+    const bf16* Y2;
+    void* C2;
+    const bf16* lora_u2;
+    const bf16* lora_v2;
 };
 
 // Load one 16-byte chunk (8 bf16) of a K-contiguous operand row with
@@ -702,10 +710,10 @@ __device__ __attribute__((always_inline)) inline void static_for(F&& f) {
 // start of the kernel; R0 - m0 / C0 - n0 index them.
 template <int TM, int TN, int WTN, int I0, int PF>
 __device__ __attribute__((always_inline)) inline void pipe_half_epilogue(
-    floatx16 (&acc)[TM][TN], const GemmArgs& a, int R0, int C0, int lane, bf16* __restrict__ wb,
-    const bf16* lu, const bf16* lv, const bf16* lb, int mloc, int nloc, int BMs, int BNs) {
+    floatx16 (&acc)[TM][TN], const GemmArgs& a, bf16* __restrict__ C, int R0, int C0, int lane,
+    bf16* __restrict__ wb, const bf16* lu, const bf16* lv, const bf16* lb, int mloc, int nloc,
+    int BMs, int BNs) {
     constexpr int CPR = WTN / 8;
-    bf16* C = (bf16*)a.C;
     const bool vec = ((a.ldc & 7) == 0) && (((uintptr_t)C & 15) == 0);
     if (a.beta != 0.f) {
         for (int q = lane; q < 64 * CPR; q += 64) {
@@ -842,6 +850,11 @@ __global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
 
     int tm_i, tn_i;
     big_tile(blockIdx.x, a.tiles_m, a.tiles_n, tm_i, tn_i);
+    // N-concatenated pair: the tile columns past tn_split are the second GEMM's
+    const bool g2 = a.tn_split > 0 && tn_i >= a.tn_split;
+    if (g2) tn_i -= a.tn_split;
+    const bf16* const Yg = g2 ? a.Y2 : a.Y;
+    bf16* const Cg = (bf16*)(g2 ? a.C2 : a.C);
     const int m0 = tm_i * BM, n0 = tn_i * BN;
     int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int wm = w / WNW, wn = w % WNW;
@@ -857,8 +870,8 @@ __global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
         for (int q = w; q < LP * (UI + VI); q += NW) {
             const int p = q / (UI + VI), qi = q % (UI + VI);
             if (p >= a.lora_n) break;
-            const bf16* u = p == 0 ? a.lora_u[0] : p == 1 ? a.lora_u[1] : a.lora_u[2];
-            const bf16* v = p == 0 ? a.lora_v[0] : p == 1 ? a.lora_v[1] : a.lora_v[2];
+            const bf16* u = p == 0 ? (g2 ? a.lora_u2 : a.lora_u[0]) : p == 1 ? a.lora_u[1] : a.lora_u[2];
+            const bf16* v = p == 0 ? (g2 ? a.lora_v2 : a.lora_v[0]) : p == 1 ? a.lora_v[1] : a.lora_v[2];
             const int64_t ldu = p == 0 ? a.lora_ldu[0] : p == 1 ? a.lora_ldu[1] : a.lora_ldu[2];
             const bf16* src;
             bf16* dst;
@@ -898,7 +911,7 @@ __global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
         const bool z_ = kq_ < 0;                                                           \
         const int k_ = z_ ? 0 : min(kq_, nk - 1) * DBK;                                    \
         dma_stage<BM, NW>(z_ ? g_dma_zero : a.X, z_ ? 0 : a.ldx, m0, a.M, k_, SXB, w, lane); \
-        dma_stage<BN, NW>(z_ ? g_dma_zero : a.Y, z_ ? 0 : a.ldy, n0, a.N, k_, SYB, w, lane); \
+        dma_stage<BN, NW>(z_ ? g_dma_zero : Yg, z_ ? 0 : a.ldy, n0, a.N, k_, SYB, w, lane);  \
     } while (0)
     PIPE_ISSUE(sX0, sY0, 0 - pad);
     PIPE_ISSUE(sX1, sY1, 1 - pad);
@@ -951,11 +964,11 @@ __global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
         wb0 = b;
         wb1 = b + 64 * WTN;
     }
-    pipe_half_epilogue<TM, TN, WTN, 0, LP>(acc, a, m0 + wm * WTM, n0 + wn * WTN, lane, wb0, lu, lv,
-                                           lb, wm * WTM, wn * WTN, BM, BN);
+    pipe_half_epilogue<TM, TN, WTN, 0, LP>(acc, a, Cg, m0 + wm * WTM, n0 + wn * WTN, lane, wb0, lu,
+                                           lv, lb, wm * WTM, wn * WTN, BM, BN);
     if constexpr (TM == 4)
-        pipe_half_epilogue<TM, TN, WTN, 2, LP>(acc, a, m0 + wm * WTM + 64, n0 + wn * WTN, lane, wb1,
-                                               lu, lv, lb, wm * WTM + 64, wn * WTN, BM, BN);
+        pipe_half_epilogue<TM, TN, WTN, 2, LP>(acc, a, Cg, m0 + wm * WTM + 64, n0 + wn * WTN, lane,
+                                               wb1, lu, lv, lb, wm * WTM + 64, wn * WTN, BM, BN);
 }
 
 // Kernel variants of the large GEMMs (ta_gemm_variant): 0 picks k_gemm_pipe
@@ -1069,6 +1082,10 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
         a.lora_u[p] = a.lora_v[p] = nullptr;
         a.lora_ldu[p] = 0;
     }
+    a.tn_split = 0;
+    a.Y2 = nullptr;
+    a.C2 = nullptr;
+    a.lora_u2 = a.lora_v2 = nullptr;
     if (lora && lora->n > 0) {
         if (out_f32 || lora->n > 3 || (lora->r & 7) != 0)
             return set_error(-1, "gemm: unsupported LoRA epilogue (n=%d r=%d)", lora->n, lora->r);
@@ -1229,6 +1246,87 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
     }
     int rc = check_launch("gemm");
     return rc ? rc : lora_after();
+}
+
+// Two GEMMs of one shape over the same X, C_i = bf16(X Y_i^T) plus the LoRA
+// delta of pair i (none, or one rank-16 pair each, same scale), as ONE
+// k_gemm_pipe launch over the N-concatenated tile grid (tile columns
+// [0, tn) the first, [tn, 2 tn) the second).  Two launches would each end
+// on a partly filled wave of tiles; one launch runs across that boundary.
+// Shapes the pipe kernel does not take run as two gemm_dispatch calls.
+int gemm_pair(int M, int N, int K, const bf16* X, int64_t ldx, const bf16* Y0, const bf16* Y1,
+              int64_t ldy, bf16* C0, bf16* C1, int64_t ldc, const LoraEpi* l0, const LoraEpi* l1,
+              hipStream_t s) {
+    const int n0 = l0 ? l0->n : 0, n1 = l1 ? l1->n : 0;
+    int variant = g_big_variant;
+    if (variant == 0) variant = N > 3072 ? 16 : 15;
+    const int BNb = big_bn(variant);
+    const bool lora_ok = (n0 == 0 && n1 == 0) ||
+                         (n0 == 1 && n1 == 1 && l0->r == 16 && l1->r == 16 &&
+                          l0->delta == l1->delta && l0->s == l1->s);
+    const bool vx = al16(X) && (ldx % 8) == 0;
+    const bool vy = al16(Y0) && al16(Y1) && (ldy % 8) == 0;
+    // (as gemm_dispatch: few tiles and a long K go to split-K instead)
+    const int tiles = ((M + 255) / 256) * 2 * (N / BNb);
+    if (!(is_pipe(variant) && lora_ok && vx && vy && M >= 1024 && N >= 1024 && N % BNb == 0 &&
+          (K % BK) == 0 && (tiles >= 192 || K / BK < 32))) {
+        int rc = gemm_dispatch(true, true, M, N, K, 1.f, X, ldx, Y0, ldy, 0.f, C0, ldc, nullptr,
+                               false, s, 0, l0);
+        return rc ? rc : gemm_dispatch(true, true, M, N, K, 1.f, X, ldx, Y1, ldy, 0.f, C1, ldc,
+                                       nullptr, false, s, 0, l1);
+    }
+    GemmArgs a{};
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.X = X;
+    a.ldx = ldx;
+    a.Y = Y0;
+    a.ldy = ldy;
+    a.C = C0;
+    a.ldc = ldc;
+    a.alpha = 1.f;
+    a.beta = 0.f;
+    a.bias = nullptr;
+    a.part = nullptr;
+    a.k_per_split = K;
+    a.tiles_m = (M + 255) / 256;
+    a.tn_split = N / BNb;
+    a.tiles_n = 2 * a.tn_split;
+    a.Y2 = Y1;
+    a.C2 = C1;
+    if (n0) {
+        a.lora_n = 1;
+        a.lora_r = 16;
+        a.lora_delta = l0->delta ? 1 : 0;
+        a.lora_s = l0->s;
+        a.lora_u[0] = l0->u[0];
+        a.lora_ldu[0] = l0->ldu[0];
+        a.lora_v[0] = l0->v_nk[0];
+        a.lora_u2 = l1->u[0];
+        a.lora_v2 = l1->v_nk[0];
+        TA_REQUIRE(l0->ldu[0] == l1->ldu[0], "gemm_pair: LoRA U strides differ");
+    }
+    const int kid = BNb == 256 ? KP_GEMM_BIG_WIDE : KP_GEMM_BIG;
+    const bool timed = kprof_begin(kid, s);
+    dim3 grid(a.tiles_m * a.tiles_n);
+    if (variant == 12)
+        k_gemm_pipe<192, 2, 2><<<grid, 256, 0, s>>>(a);
+    else if (variant == 13)
+        k_gemm_pipe<256, 2, 2><<<grid, 256, 0, s>>>(a);
+    else if (variant == 14)
+        k_gemm_pipe<256, 4, 2><<<grid, 512, 0, s>>>(a);
+    else if (variant == 15)
+        k_gemm_pipe<192, 4, 2><<<grid, 512, 0, s>>>(a);
+    else
+        k_gemm_pipe<256, 2, 4><<<grid, 512, 0, s>>>(a);
+    if (timed) {
+        double mn = 2.0 * M * N;
+        double fl = 2.0 * mn * K + 2.0 * mn * a.lora_r * a.lora_n;
+        double by = 2.0 * ((double)M * K + 2.0 * N * K + mn) + 2.0 * a.lora_n * (double)(2 * M + 2 * N) * 16;
+        kprof_end(kid, s, fl, by, big_name(variant));
+    }
+    return check_launch("gemm_pair");
 }
 
 // F32 -> BF16 staging for gemm_f32 operands (the LoRA path feeds it values

@@ -171,3 +171,31 @@ def test_small_long_batch_matches_oracle():
         if so["gnorm_raw"] <= ac["grad_clip"]:
             compare(orc, eng, mc, ac, ("gB",) if step == 0 else ("gA", "gB"))
         check_adamw_of_own_grads(eng, mc, ac, state, sg["lr"], step + 1, sg["gnorm_raw"])
+
+
+MID_MODEL = dict(vocab=2048, hidden=1024, layers=1, n_q=8, n_kv=2, head_dim=128, inter=3328,
+                 rms_eps=1e-6, rope_theta=1e6, tie=1)
+
+
+def test_mid_pipe_gemm_paths_match_oracle():
+    """Sizes that take the large-GEMM kernel (M, N >= 1024) with its fused
+    LoRA epilogues: the gate/up projections as one N-concatenated launch,
+    the q/o/lm-head projections and the down-projection input gradient with
+    rank-16 terms in the epilogue, split-K for the long-K products; and the
+    fused SwiGLU backward with a partly filled last column block (3328 =
+    6.5 x 512).  Step 2 starts from the oracle's state after step 1."""
+    mc, ac, B, T = MID_MODEL, SMALL_ADAPT, 1, 1024
+    orc, eng = make_pair(mc, ac, B, T, seed=41)
+    rng = np.random.default_rng(17)
+    for step in range(2):
+        sync_state(orc, eng, mc, ac)
+        state = snapshot(orc, mc, ac)
+        toks = rng.integers(0, mc["vocab"], B * T + 1).astype(np.int32)
+        inp, tgt = toks[:-1].copy(), toks[1:].copy()
+        so = orc.step(inp, tgt, B, T)
+        sg = eng.step(inp, tgt)
+        assert abs(sg["loss"] - so["loss"]) <= 1e-3 * abs(so["loss"]), (step, sg, so)
+        assert abs(sg["gnorm_raw"] - so["gnorm_raw"]) <= 1e-2 * so["gnorm_raw"], (step, sg, so)
+        if so["gnorm_raw"] <= ac["grad_clip"]:
+            compare(orc, eng, mc, ac, ("gB",) if step == 0 else ("gA", "gB"))
+        check_adamw_of_own_grads(eng, mc, ac, state, sg["lr"], step + 1, sg["gnorm_raw"])
