@@ -530,10 +530,15 @@ static int forward(Engine* e) {
               ta_rms_norm_fwd(ly.res_in, ly.in_norm, ly.xn, ly.in_rms, 1, BT, H, c.rms_eps, s));
         CK(lora_group_h(e, ly, {PQ, PK, PV}, ly.xn, H));
         {
+            // q, k and v projections (qwen2.cu:21-30, each with its bias and
+            // LoRA delta) in one launch over the three weight matrices
             LoraEpi eq = fwd_epi(e, ly.pr[PQ]), ek = fwd_epi(e, ly.pr[PK]), ev = fwd_epi(e, ly.pr[PV]);
-            CK(proj_fwd(e, ly.W[PQ], ly.xn, ly.Q, H, qd, ly.bias[0], &eq));
-            CK(proj_fwd(e, ly.W[PK], ly.xn, ly.K, H, kvd, ly.bias[1], &ek));
-            CK(proj_fwd(e, ly.W[PV], ly.xn, ly.V, H, kvd, ly.bias[2], &ev));
+            const GemmGroup gr[3] = {{qd, ly.W[PQ], ly.Q, qd, ly.bias[0], &eq},
+                                     {kvd, ly.W[PK], ly.K, kvd, ly.bias[1], &ek},
+                                     {kvd, ly.W[PV], ly.V, kvd, ly.bias[2], &ev}};
+            TIMED(TA_CAT_GEMM_FWD, gflops(BT, qd + 2.0 * kvd, H),
+                  gbytes(BT, qd + 2.0 * kvd, H, 2, 2, false),
+                  gemm_groups(BT, H, ly.xn, H, H, gr, 3, s));
         }
         TIMED(TA_CAT_ELEMWISE, 0, dBT * qd * 4,
               ta_rope_fwd(ly.Q, e->B, e->T, c.n_q, c.head_dim, c.rope_theta, s));
@@ -559,9 +564,10 @@ static int forward(Engine* e) {
             // gate and up projections (qwen2.cu:21-30, each with its LoRA
             // delta) in one launch over both weight matrices
             LoraEpi eg = fwd_epi(e, ly.pr[PG]), eu = fwd_epi(e, ly.pr[PU]);
+            const GemmGroup gr[2] = {{I, ly.W[PG], ly.gate, I, nullptr, &eg},
+                                     {I, ly.W[PU], ly.up, I, nullptr, &eu}};
             TIMED(TA_CAT_GEMM_FWD, 2.0 * gflops(BT, I, H), 2.0 * gbytes(BT, I, H, 2, 2, false),
-                  gemm_pair(BT, I, H, ly.xn2, H, ly.W[PG], ly.W[PU], H, ly.gate, ly.up, I, &eg,
-                            &eu, s));
+                  gemm_groups(BT, H, ly.xn2, H, H, gr, 2, s));
         }
         TIMED(TA_CAT_ELEMWISE, 0, dBT * I * 6,
               ta_silu_mul_fwd(ly.gate, ly.up, ly.act, (int64_t)BT * I, s));

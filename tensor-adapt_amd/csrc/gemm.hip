@@ -62,14 +62,22 @@ struct GemmArgs {
     const bf16* lora_u[3];
     int64_t lora_ldu[3];
     const bf16* lora_v[3];
-    // N-concatenated pair (k_gemm_pipe only; tn_split = 0 otherwise): tile
-    // columns tn >= tn_split compute a second GEMM of the same shape and X,
-    // with Y2, C2 and the LoRA operands of its single pair (u2, v2)
-    int tn_split;
-    const bf16* Y2;
-    void* C2;
-    const bf16* lora_u2;
-    const bf16* lora_v2;
+    // N-concatenated groups (k_gemm_pipe only; ngroups <= 1 otherwise):
+    // tile columns [tn0[g], tn0[g + 1]) compute group g's own GEMM over the
+    // same X: gN[g] output columns of gY[g], written to gC[g] (row stride
+    // gldc[g]) with bias gbias[g] and, when glora[g], the LoRA pair gu/gv[g]
+    // (rank 16, lora_delta and lora_s shared).  The fields above describe
+    // group 0 only as far as they are shared (M, K, X, ldy, alpha, beta).
+    int ngroups;
+    int tn0[3];
+    int gN[3];
+    int glora[3];
+    const bf16* gY[3];
+    void* gC[3];
+    int64_t gldc[3];
+    const bf16* gbias[3];
+    const bf16* gu[3];
+    const bf16* gv[3];
 };
 
 // Load one 16-byte chunk (8 bf16) of a K-contiguous operand row with
@@ -832,7 +840,7 @@ __device__ __attribute__((always_inline)) inline void pipe_half_epilogue(
 
 template <int BN, int WMW, int WNW>
 __global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
-    WMW * WNW / 4, WMW * WNW / 4))) void k_gemm_pipe(GemmArgs a) {
+    WMW * WNW / 4, WMW * WNW / 4))) void k_gemm_pipe(GemmArgs a0) {
     constexpr int NS = 4, BM = 256, NW = WMW * WNW;
     constexpr int WTM = BM / WMW, WTN = BN / WNW;
     constexpr int TM = WTM / 32, TN = WTN / 32;
@@ -849,12 +857,21 @@ __global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
     __shared__ __attribute__((aligned(16))) bf16 sLU[LP * BM * 16], sLV[LP * BN * 16], sB[512];
 
     int tm_i, tn_i;
-    big_tile(blockIdx.x, a.tiles_m, a.tiles_n, tm_i, tn_i);
-    // N-concatenated pair: the tile columns past tn_split are the second GEMM's
-    const bool g2 = a.tn_split > 0 && tn_i >= a.tn_split;
-    if (g2) tn_i -= a.tn_split;
-    const bf16* const Yg = g2 ? a.Y2 : a.Y;
-    bf16* const Cg = (bf16*)(g2 ? a.C2 : a.C);
+    big_tile(blockIdx.x, a0.tiles_m, a0.tiles_n, tm_i, tn_i);
+    // N-concatenated groups: this tile's group supplies Y, C, N, bias, LoRA
+    GemmArgs a = a0;
+    if (a0.ngroups > 1) {
+        const int g = (a0.ngroups > 2 && tn_i >= a0.tn0[2]) ? 2 : tn_i >= a0.tn0[1] ? 1 : 0;
+        tn_i -= g == 2 ? a0.tn0[2] : g == 1 ? a0.tn0[1] : 0;
+        a.N = g == 2 ? a0.gN[2] : g == 1 ? a0.gN[1] : a0.gN[0];
+        a.Y = g == 2 ? a0.gY[2] : g == 1 ? a0.gY[1] : a0.gY[0];
+        a.C = g == 2 ? a0.gC[2] : g == 1 ? a0.gC[1] : a0.gC[0];
+        a.ldc = g == 2 ? a0.gldc[2] : g == 1 ? a0.gldc[1] : a0.gldc[0];
+        a.bias = g == 2 ? a0.gbias[2] : g == 1 ? a0.gbias[1] : a0.gbias[0];
+        a.lora_n = g == 2 ? a0.glora[2] : g == 1 ? a0.glora[1] : a0.glora[0];
+        a.lora_u[0] = g == 2 ? a0.gu[2] : g == 1 ? a0.gu[1] : a0.gu[0];
+        a.lora_v[0] = g == 2 ? a0.gv[2] : g == 1 ? a0.gv[1] : a0.gv[0];
+    }
     const int m0 = tm_i * BM, n0 = tn_i * BN;
     int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int wm = w / WNW, wn = w % WNW;
@@ -870,8 +887,8 @@ __global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
         for (int q = w; q < LP * (UI + VI); q += NW) {
             const int p = q / (UI + VI), qi = q % (UI + VI);
             if (p >= a.lora_n) break;
-            const bf16* u = p == 0 ? (g2 ? a.lora_u2 : a.lora_u[0]) : p == 1 ? a.lora_u[1] : a.lora_u[2];
-            const bf16* v = p == 0 ? (g2 ? a.lora_v2 : a.lora_v[0]) : p == 1 ? a.lora_v[1] : a.lora_v[2];
+            const bf16* u = p == 0 ? a.lora_u[0] : p == 1 ? a.lora_u[1] : a.lora_u[2];
+            const bf16* v = p == 0 ? a.lora_v[0] : p == 1 ? a.lora_v[1] : a.lora_v[2];
             const int64_t ldu = p == 0 ? a.lora_ldu[0] : p == 1 ? a.lora_ldu[1] : a.lora_ldu[2];
             const bf16* src;
             bf16* dst;
@@ -911,7 +928,7 @@ __global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
         const bool z_ = kq_ < 0;                                                           \
         const int k_ = z_ ? 0 : min(kq_, nk - 1) * DBK;                                    \
         dma_stage<BM, NW>(z_ ? g_dma_zero : a.X, z_ ? 0 : a.ldx, m0, a.M, k_, SXB, w, lane); \
-        dma_stage<BN, NW>(z_ ? g_dma_zero : Yg, z_ ? 0 : a.ldy, n0, a.N, k_, SYB, w, lane);  \
+        dma_stage<BN, NW>(z_ ? g_dma_zero : a.Y, z_ ? 0 : a.ldy, n0, a.N, k_, SYB, w, lane); \
     } while (0)
     PIPE_ISSUE(sX0, sY0, 0 - pad);
     PIPE_ISSUE(sX1, sY1, 1 - pad);
@@ -964,10 +981,10 @@ __global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
         wb0 = b;
         wb1 = b + 64 * WTN;
     }
-    pipe_half_epilogue<TM, TN, WTN, 0, LP>(acc, a, Cg, m0 + wm * WTM, n0 + wn * WTN, lane, wb0, lu,
+    pipe_half_epilogue<TM, TN, WTN, 0, LP>(acc, a, (bf16*)a.C, m0 + wm * WTM, n0 + wn * WTN, lane, wb0, lu,
                                            lv, lb, wm * WTM, wn * WTN, BM, BN);
     if constexpr (TM == 4)
-        pipe_half_epilogue<TM, TN, WTN, 2, LP>(acc, a, Cg, m0 + wm * WTM + 64, n0 + wn * WTN, lane,
+        pipe_half_epilogue<TM, TN, WTN, 2, LP>(acc, a, (bf16*)a.C, m0 + wm * WTM + 64, n0 + wn * WTN, lane,
                                                wb1, lu, lv, lb, wm * WTM + 64, wn * WTN, BM, BN);
 }
 
@@ -1082,10 +1099,7 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
         a.lora_u[p] = a.lora_v[p] = nullptr;
         a.lora_ldu[p] = 0;
     }
-    a.tn_split = 0;
-    a.Y2 = nullptr;
-    a.C2 = nullptr;
-    a.lora_u2 = a.lora_v2 = nullptr;
+    a.ngroups = 1;
     if (lora && lora->n > 0) {
         if (out_f32 || lora->n > 3 || (lora->r & 7) != 0)
             return set_error(-1, "gemm: unsupported LoRA epilogue (n=%d r=%d)", lora->n, lora->r);
@@ -1248,65 +1262,90 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
     return rc ? rc : lora_after();
 }
 
-// Two GEMMs of one shape over the same X, C_i = bf16(X Y_i^T) plus the LoRA
-// delta of pair i (none, or one rank-16 pair each, same scale), as ONE
-// k_gemm_pipe launch over the N-concatenated tile grid (tile columns
-// [0, tn) the first, [tn, 2 tn) the second).  Two launches would each end
-// on a partly filled wave of tiles; one launch runs across that boundary.
-// Shapes the pipe kernel does not take run as two gemm_dispatch calls.
-int gemm_pair(int M, int N, int K, const bf16* X, int64_t ldx, const bf16* Y0, const bf16* Y1,
-              int64_t ldy, bf16* C0, bf16* C1, int64_t ldc, const LoraEpi* l0, const LoraEpi* l1,
-              hipStream_t s) {
-    const int n0 = l0 ? l0->n : 0, n1 = l1 ? l1->n : 0;
+// Up to three GEMMs over the same X [M x K], C_g = bf16(X Y_g^T (+ bias_g))
+// plus the LoRA delta of group g's pair (none, or one rank-16 pair; delta
+// kind and scale shared), as ONE k_gemm_pipe launch over the N-concatenated
+// tile grid: q/k/v or gate/up projections.  Separate launches would each
+// end on a partly filled wave of tiles, and the narrow k/v projections
+// would run on the small-GEMM path; every output keeps its own epilogue, so
+// the results are those of separate launches.  Shapes the pipe kernel does
+// not take run as separate gemm_dispatch calls.
+int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const GemmGroup* gr,
+                int ng, hipStream_t s) {
+    TA_REQUIRE(ng >= 1 && ng <= 3, "gemm_groups: %d groups", ng);
+    int Ntot = 0;
+    bool all256 = true, all192 = true, lora_ok = true, vy = (ldy % 8) == 0;
+    const LoraEpi* l0 = nullptr;
+    for (int g = 0; g < ng; g++) {
+        Ntot += gr[g].N;
+        all256 &= gr[g].N % 256 == 0;
+        all192 &= gr[g].N % 192 == 0;
+        vy &= al16(gr[g].Y);
+        const LoraEpi* l = gr[g].lora;
+        if (l && l->n > 0) {
+            lora_ok &= l->n == 1 && l->r == 16;
+            if (l0) lora_ok &= l->delta == l0->delta && l->s == l0->s;
+            else l0 = l;
+        }
+    }
     int variant = g_big_variant;
-    if (variant == 0) variant = N > 3072 ? 16 : 15;
+    if (variant == 0) variant = all256 ? 16 : 15;
     const int BNb = big_bn(variant);
-    const bool lora_ok = (n0 == 0 && n1 == 0) ||
-                         (n0 == 1 && n1 == 1 && l0->r == 16 && l1->r == 16 &&
-                          l0->delta == l1->delta && l0->s == l1->s);
+    const bool tiles_ok = BNb == 256 ? all256 : all192;
+    const int tiles = ((M + 255) / 256) * (Ntot / BNb);
     const bool vx = al16(X) && (ldx % 8) == 0;
-    const bool vy = al16(Y0) && al16(Y1) && (ldy % 8) == 0;
     // (as gemm_dispatch: few tiles and a long K go to split-K instead)
-    const int tiles = ((M + 255) / 256) * 2 * (N / BNb);
-    if (!(is_pipe(variant) && lora_ok && vx && vy && M >= 1024 && N >= 1024 && N % BNb == 0 &&
-          (K % BK) == 0 && (tiles >= 192 || K / BK < 32))) {
-        int rc = gemm_dispatch(true, true, M, N, K, 1.f, X, ldx, Y0, ldy, 0.f, C0, ldc, nullptr,
-                               false, s, 0, l0);
-        return rc ? rc : gemm_dispatch(true, true, M, N, K, 1.f, X, ldx, Y1, ldy, 0.f, C1, ldc,
-                                       nullptr, false, s, 0, l1);
+    if (!(ng > 1 && is_pipe(variant) && tiles_ok && lora_ok && vx && vy && M >= 1024 &&
+          Ntot >= 1024 && (K % BK) == 0 && (tiles >= 192 || K / BK < 32))) {
+        for (int g = 0; g < ng; g++) {
+            int rc = gemm_dispatch(true, true, M, gr[g].N, K, 1.f, X, ldx, gr[g].Y, ldy, 0.f,
+                                   gr[g].C, gr[g].ldc, gr[g].bias, false, s, 0, gr[g].lora);
+            if (rc) return rc;
+        }
+        return 0;
     }
     GemmArgs a{};
     a.M = M;
-    a.N = N;
+    a.N = gr[0].N;
     a.K = K;
     a.X = X;
     a.ldx = ldx;
-    a.Y = Y0;
+    a.Y = gr[0].Y;
     a.ldy = ldy;
-    a.C = C0;
-    a.ldc = ldc;
+    a.C = gr[0].C;
+    a.ldc = gr[0].ldc;
     a.alpha = 1.f;
     a.beta = 0.f;
-    a.bias = nullptr;
-    a.part = nullptr;
+    a.bias = gr[0].bias;
     a.k_per_split = K;
     a.tiles_m = (M + 255) / 256;
-    a.tn_split = N / BNb;
-    a.tiles_n = 2 * a.tn_split;
-    a.Y2 = Y1;
-    a.C2 = C1;
-    if (n0) {
-        a.lora_n = 1;
-        a.lora_r = 16;
-        a.lora_delta = l0->delta ? 1 : 0;
-        a.lora_s = l0->s;
-        a.lora_u[0] = l0->u[0];
-        a.lora_ldu[0] = l0->ldu[0];
-        a.lora_v[0] = l0->v_nk[0];
-        a.lora_u2 = l1->u[0];
-        a.lora_v2 = l1->v_nk[0];
-        TA_REQUIRE(l0->ldu[0] == l1->ldu[0], "gemm_pair: LoRA U strides differ");
+    a.tiles_n = Ntot / BNb;
+    a.ngroups = ng;
+    a.lora_r = l0 ? 16 : 0;
+    a.lora_delta = l0 && l0->delta ? 1 : 0;
+    a.lora_s = l0 ? l0->s : 0.f;
+    int tn = 0;
+    for (int g = 0; g < ng; g++) {
+        const LoraEpi* l = gr[g].lora;
+        const bool on = l && l->n > 0;
+        a.tn0[g] = tn;
+        tn += gr[g].N / BNb;
+        a.gN[g] = gr[g].N;
+        a.gY[g] = gr[g].Y;
+        a.gC[g] = gr[g].C;
+        a.gldc[g] = gr[g].ldc;
+        a.gbias[g] = gr[g].bias;
+        a.glora[g] = on ? 1 : 0;
+        a.gu[g] = on ? l->u[0] : nullptr;
+        a.gv[g] = on ? l->v_nk[0] : nullptr;
+        if (on) {
+            TA_REQUIRE(l->ldu[0] == 16, "gemm_groups: LoRA U rows must hold rank 16");
+            a.lora_ldu[0] = 16;
+        }
     }
+    a.lora_n = a.glora[0];
+    a.lora_u[0] = a.gu[0];
+    a.lora_v[0] = a.gv[0];
     const int kid = BNb == 256 ? KP_GEMM_BIG_WIDE : KP_GEMM_BIG;
     const bool timed = kprof_begin(kid, s);
     dim3 grid(a.tiles_m * a.tiles_n);
@@ -1321,12 +1360,15 @@ int gemm_pair(int M, int N, int K, const bf16* X, int64_t ldx, const bf16* Y0, c
     else
         k_gemm_pipe<256, 2, 4><<<grid, 512, 0, s>>>(a);
     if (timed) {
-        double mn = 2.0 * M * N;
-        double fl = 2.0 * mn * K + 2.0 * mn * a.lora_r * a.lora_n;
-        double by = 2.0 * ((double)M * K + 2.0 * N * K + mn) + 2.0 * a.lora_n * (double)(2 * M + 2 * N) * 16;
+        double mn = (double)M * Ntot, fl = 2.0 * mn * K, by = 2.0 * ((double)M * K + (double)Ntot * K + mn);
+        for (int g = 0; g < ng; g++)
+            if (a.glora[g]) {
+                fl += 2.0 * M * gr[g].N * 16;
+                by += 2.0 * (double)(M + gr[g].N) * 16;
+            }
         kprof_end(kid, s, fl, by, big_name(variant));
     }
-    return check_launch("gemm_pair");
+    return check_launch("gemm_groups");
 }
 
 // F32 -> BF16 staging for gemm_f32 operands (the LoRA path feeds it values

@@ -63,11 +63,19 @@ struct LoraEpi {
 int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16* X, int64_t ldx,
                   const bf16* Y, int64_t ldy, float beta, void* C, int64_t ldc, const bf16* bias,
                   bool out_f32, hipStream_t s, int force_splits, const LoraEpi* lora);
-// two GEMMs of one shape sharing X (C_i = bf16(X Y_i^T) + LoRA delta of pair i)
-// in one launch over the N-concatenated tile grid
-int gemm_pair(int M, int N, int K, const bf16* X, int64_t ldx, const bf16* Y0, const bf16* Y1,
-              int64_t ldy, bf16* C0, bf16* C1, int64_t ldc, const LoraEpi* l0, const LoraEpi* l1,
-              hipStream_t s);
+// one of up to three GEMMs sharing X in gemm_groups: C = bf16(X Y^T (+ bias))
+// (+ LoRA delta), N output columns, row stride ldc
+struct GemmGroup {
+    int N;
+    const bf16* Y;
+    bf16* C;
+    int64_t ldc;
+    const bf16* bias;
+    const LoraEpi* lora;
+};
+// the groups' GEMMs in one launch over the N-concatenated tile grid
+int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const GemmGroup* gr,
+                int ng, hipStream_t s);
 int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* O32, float* P, int B,
              int T, int Hq, int Hkv, int hd, bool zero_fill, hipStream_t s);
 int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const float* P,
