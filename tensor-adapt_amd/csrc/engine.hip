@@ -634,8 +634,10 @@ static int backward(Engine* e) {
             const bf16* gos[2] = {e->dgate, e->dup};
             LoraEpi ep;
             CK(lora_group_bwd(e, ly, {PG, PU}, ly.xn2, H, gos, &ep, fused));
-            CK(proj_bwd_x(e, ly.Wt[PG], e->dgate, e->dxn2, I, H, 0.f));
-            CK(proj_bwd_x(e, ly.Wt[PU], e->dup, e->dxn2, I, H, 1.f, &ep));
+            // proj_bwd_x of gate (beta 0) then up (beta 1), qwen2.cu:233-234
+            const GemmSeg sg[2] = {{I, e->dgate, I, ly.Wt[PG], I}, {I, e->dup, I, ly.Wt[PU], I}};
+            TIMED(TA_CAT_GEMM_DX, 2.0 * gflops(BT, H, I), 2.0 * gbytes(BT, H, I, 2, 2, false),
+                  gemm_chain(BT, H, sg, 2, e->dxn2, H, ep.n ? &ep : nullptr, s));
         }
         TIMED(TA_CAT_NORM, 0, nrm_b,
               ta_rms_norm_bwd(e->dxn2, ly.res_mid, ly.post_norm, ly.post_rms, e->tmpH, nullptr, 1,
@@ -662,9 +664,13 @@ static int backward(Engine* e) {
             const bf16* gos[3] = {e->dQ, e->dK, e->dV};
             LoraEpi ep;
             CK(lora_group_bwd(e, ly, {PQ, PK, PV}, ly.xn, H, gos, &ep));
-            CK(proj_bwd_x(e, ly.Wt[PQ], e->dQ, e->dxn, qd, H, 0.f));
-            CK(proj_bwd_x(e, ly.Wt[PK], e->dK, e->dxn, kvd, H, 1.f));
-            CK(proj_bwd_x(e, ly.Wt[PV], e->dV, e->dxn, kvd, H, 1.f, &ep));
+            // proj_bwd_x of q (beta 0), k and v (beta 1), qwen2.cu:283-285
+            const GemmSeg sg[3] = {{qd, e->dQ, qd, ly.Wt[PQ], qd},
+                                   {kvd, e->dK, kvd, ly.Wt[PK], kvd},
+                                   {kvd, e->dV, kvd, ly.Wt[PV], kvd}};
+            TIMED(TA_CAT_GEMM_DX, gflops(BT, H, qd + 2.0 * kvd),
+                  gbytes(BT, H, qd + 2.0 * kvd, 2, 2, false),
+                  gemm_chain(BT, H, sg, 3, e->dxn, H, ep.n ? &ep : nullptr, s));
         }
         // centroid side channel (adapt_trainer.cu:210-232): h = x_normed,
         // g = dx_attn_in of this layer

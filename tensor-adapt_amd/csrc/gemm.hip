@@ -78,6 +78,16 @@ struct GemmArgs {
     const bf16* gbias[3];
     const bf16* gu[3];
     const bf16* gv[3];
+    // K segments (k_gemm_pipe only; nseg <= 1 otherwise): k in [kseg[s],
+    // kseg[s + 1]) runs over X_s Y_s^T (sX, sldx, sY, sldy; k relative to
+    // kseg[s]) and the accumulators are rounded to BF16 where a segment
+    // ends: the chain C = bf16(X_s Y_s^T + C), s = 0, 1, .., in one launch
+    int nseg;
+    int kseg[3];
+    const bf16* sX[3];
+    int64_t sldx[3];
+    const bf16* sY[3];
+    int64_t sldy[3];
 };
 
 // Load one 16-byte chunk (8 bf16) of a K-contiguous operand row with
@@ -838,9 +848,19 @@ __device__ __attribute__((always_inline)) inline void pipe_half_epilogue(
     }
 }
 
-template <int BN, int WMW, int WNW>
-__global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
-    WMW * WNW / 4, WMW * WNW / 4))) void k_gemm_pipe(GemmArgs a0) {
+// accumulators rounded to BF16 values (the end of one GEMM of a chain)
+template <int TM, int TN>
+__device__ __forceinline__ void round_acc(floatx16 (&acc)[TM][TN]) {
+#pragma unroll
+    for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = bf2f(f2bf(acc[i][j][r]));
+}
+
+template <int BN, int WMW, int WNW, bool CHAIN>  // CHAIN: K segments (a.nseg > 1)
+__device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmArgs& a0) {
     constexpr int NS = 4, BM = 256, NW = WMW * WNW;
     constexpr int WTM = BM / WMW, WTN = BN / WNW;
     constexpr int TM = WTM / 32, TN = WTN / 32;
@@ -922,13 +942,32 @@ __global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
     // that is never read), as in k_gemm_dma
     const int nk = a.K / DBK;
     const int pad = (NS - nk % NS) % NS;
+    // K segments: stage kt (global k) belongs to segment s; the accumulators
+    // are rounded after the last stage of every segment but the last
+    const int kb1 = CHAIN ? a.kseg[1] / DBK : -99, kb2 = CHAIN && a.nseg > 2 ? a.kseg[2] / DBK : -99;
 #define PIPE_ISSUE(SXB, SYB, KT)                                                           \
     do {                                                                                   \
         const int kq_ = (KT);                                                              \
         const bool z_ = kq_ < 0;                                                           \
-        const int k_ = z_ ? 0 : min(kq_, nk - 1) * DBK;                                    \
-        dma_stage<BM, NW>(z_ ? g_dma_zero : a.X, z_ ? 0 : a.ldx, m0, a.M, k_, SXB, w, lane); \
-        dma_stage<BN, NW>(z_ ? g_dma_zero : a.Y, z_ ? 0 : a.ldy, n0, a.N, k_, SYB, w, lane); \
+        int k_ = z_ ? 0 : min(kq_, nk - 1) * DBK;                                          \
+        const bf16* x_ = a.X;                                                              \
+        const bf16* y_ = a.Y;                                                              \
+        int64_t lx_ = a.ldx, ly_ = a.ldy;                                                  \
+        if constexpr (CHAIN) {                                                             \
+            const int s_ = (a.nseg > 2 && k_ >= a.kseg[2]) ? 2 : k_ >= a.kseg[1] ? 1 : 0;  \
+            x_ = s_ == 2 ? a.sX[2] : s_ == 1 ? a.sX[1] : a.sX[0];                          \
+            y_ = s_ == 2 ? a.sY[2] : s_ == 1 ? a.sY[1] : a.sY[0];                          \
+            lx_ = s_ == 2 ? a.sldx[2] : s_ == 1 ? a.sldx[1] : a.sldx[0];                   \
+            ly_ = s_ == 2 ? a.sldy[2] : s_ == 1 ? a.sldy[1] : a.sldy[0];                   \
+            k_ -= s_ == 2 ? a.kseg[2] : s_ == 1 ? a.kseg[1] : 0;                           \
+        }                                                                                  \
+        dma_stage<BM, NW>(z_ ? g_dma_zero : x_, z_ ? 0 : lx_, m0, a.M, k_, SXB, w, lane);  \
+        dma_stage<BN, NW>(z_ ? g_dma_zero : y_, z_ ? 0 : ly_, n0, a.N, k_, SYB, w, lane);  \
+    } while (0)
+#define PIPE_ROUND(KT)                                                                     \
+    do {                                                                                   \
+        if constexpr (CHAIN)                                                               \
+            if ((KT) + 1 == kb1 || (KT) + 1 == kb2) round_acc<TM, TN>(acc);                \
     } while (0)
     PIPE_ISSUE(sX0, sY0, 0 - pad);
     PIPE_ISSUE(sX1, sY1, 1 - pad);
@@ -955,11 +994,16 @@ __global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
     } while (0)
     for (int kt0 = -pad; kt0 < nk; kt0 += NS) {
         PIPE_STEP(0, sX0, sY0, sX1, sY1, sX3, sY3);
+        PIPE_ROUND(kt0 + 0);
         PIPE_STEP(1, sX1, sY1, sX2, sY2, sX0, sY0);
+        PIPE_ROUND(kt0 + 1);
         PIPE_STEP(2, sX2, sY2, sX3, sY3, sX1, sY1);
+        PIPE_ROUND(kt0 + 2);
         PIPE_STEP(3, sX3, sY3, sX0, sY0, sX2, sY2);
+        PIPE_ROUND(kt0 + 3);
     }
     TA_WAIT_VMCNT(0);  // the surplus loads have landed before the buffers are reused
+#undef PIPE_ROUND
 #undef PIPE_STEP
 #undef PIPE_ISSUE
     __syncthreads();
@@ -986,6 +1030,17 @@ __global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
     if constexpr (TM == 4)
         pipe_half_epilogue<TM, TN, WTN, 2, LP>(acc, a, (bf16*)a.C, m0 + wm * WTM + 64, n0 + wn * WTN, lane,
                                                wb1, lu, lv, lb, wm * WTM + 64, wn * WTN, BM, BN);
+}
+
+template <int BN, int WMW, int WNW>
+__global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
+    WMW * WNW / 4, WMW * WNW / 4))) void k_gemm_pipe(GemmArgs a) {
+    gemm_pipe_body<BN, WMW, WNW, false>(a);
+}
+template <int BN, int WMW, int WNW>
+__global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
+    WMW * WNW / 4, WMW * WNW / 4))) void k_gemm_pipe_chain(GemmArgs a) {
+    gemm_pipe_body<BN, WMW, WNW, true>(a);
 }
 
 // Kernel variants of the large GEMMs (ta_gemm_variant): 0 picks k_gemm_pipe
@@ -1100,6 +1155,7 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
         a.lora_ldu[p] = 0;
     }
     a.ngroups = 1;
+    a.nseg = 1;
     if (lora && lora->n > 0) {
         if (out_f32 || lora->n > 3 || (lora->r & 7) != 0)
             return set_error(-1, "gemm: unsupported LoRA epilogue (n=%d r=%d)", lora->n, lora->r);
@@ -1260,6 +1316,93 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
     }
     int rc = check_launch("gemm");
     return rc ? rc : lora_after();
+}
+
+// The chain C = bf16(X_0 Y_0^T), C = bf16(X_s Y_s^T + C) for s = 1, 2, then
+// the LoRA terms (the q/k/v or gate/up input gradients, proj_bwd_x with
+// beta 0, 1, 1: qwen2.cu:233-234, 283-285) as ONE k_gemm_pipe launch over
+// the concatenated K: the accumulators are rounded to BF16 where each
+// GEMM of the chain ends, so the rounding points are those of the
+// separate GEMMs (only the F32 summation order inside a GEMM differs).
+// Shapes the pipe kernel does not take run as separate gemm_dispatch calls.
+int gemm_chain(int M, int N, const GemmSeg* sg, int ns, bf16* C, int64_t ldc, const LoraEpi* lora,
+               hipStream_t s) {
+    TA_REQUIRE(ns >= 1 && ns <= 3, "gemm_chain: %d segments", ns);
+    int variant = g_big_variant;
+    if (variant == 0) variant = N > 3072 ? 16 : 15;
+    const int BNb = big_bn(variant);  // the chain kernel comes in the two default shapes
+    int Ktot = 0;
+    bool ok = ns > 1 && (variant == 15 || variant == 16) && M >= 1024 && N >= 1024;
+    for (int q = 0; q < ns; q++) {
+        Ktot += sg[q].K;
+        ok &= sg[q].K % BK == 0 && al16(sg[q].X) && al16(sg[q].Y) && sg[q].ldx % 8 == 0 &&
+              sg[q].ldy % 8 == 0;
+    }
+    const int tiles = ((M + 255) / 256) * ((N + BNb - 1) / BNb);
+    // (as gemm_dispatch: few tiles and a long K go to split-K instead)
+    ok &= tiles >= 192 || Ktot / BK < 32;
+    ok &= !lora || lora->n == 0 || lora->r <= 16;
+    if (!ok) {
+        for (int q = 0; q < ns; q++) {
+            int rc = gemm_dispatch(true, true, M, N, sg[q].K, 1.f, sg[q].X, sg[q].ldx, sg[q].Y,
+                                   sg[q].ldy, q ? 1.f : 0.f, C, ldc, nullptr, false, s, 0,
+                                   q == ns - 1 ? lora : nullptr);
+            if (rc) return rc;
+        }
+        return 0;
+    }
+    GemmArgs a{};
+    a.M = M;
+    a.N = N;
+    a.K = Ktot;
+    a.X = sg[0].X;
+    a.ldx = sg[0].ldx;
+    a.Y = sg[0].Y;
+    a.ldy = sg[0].ldy;
+    a.C = C;
+    a.ldc = ldc;
+    a.alpha = 1.f;
+    a.beta = 0.f;
+    a.k_per_split = Ktot;
+    a.tiles_m = (M + 255) / 256;
+    a.tiles_n = (N + BNb - 1) / BNb;
+    a.ngroups = 1;
+    a.nseg = ns;
+    int k = 0;
+    for (int q = 0; q < ns; q++) {
+        a.kseg[q] = k;
+        k += sg[q].K;
+        a.sX[q] = sg[q].X;
+        a.sldx[q] = sg[q].ldx;
+        a.sY[q] = sg[q].Y;
+        a.sldy[q] = sg[q].ldy;
+    }
+    if (lora && lora->n > 0) {
+        a.lora_n = lora->n;
+        a.lora_r = lora->r;
+        a.lora_delta = lora->delta ? 1 : 0;
+        a.lora_s = lora->s;
+        for (int p = 0; p < lora->n; p++) {
+            a.lora_u[p] = lora->u[p];
+            a.lora_ldu[p] = lora->ldu[p];
+            a.lora_v[p] = lora->v_nk[p];
+        }
+    }
+    const int kid = BNb == 256 ? KP_GEMM_BIG_WIDE : KP_GEMM_BIG;
+    const bool timed = kprof_begin(kid, s);
+    dim3 grid(a.tiles_m * a.tiles_n);
+    if (BNb == 192)
+        k_gemm_pipe_chain<192, 4, 2><<<grid, 512, 0, s>>>(a);
+    else
+        k_gemm_pipe_chain<256, 2, 4><<<grid, 512, 0, s>>>(a);
+    if (timed) {
+        double mn = (double)M * N;
+        double fl = 2.0 * mn * Ktot + 2.0 * mn * a.lora_r * a.lora_n;
+        double by = 2.0 * ((double)M * Ktot + (double)N * Ktot + mn) +
+                    2.0 * a.lora_n * (double)(M + N) * a.lora_r;
+        kprof_end(kid, s, fl, by, big_name(variant));
+    }
+    return check_launch("gemm_chain");
 }
 
 // Up to three GEMMs over the same X [M x K], C_g = bf16(X Y_g^T (+ bias_g))

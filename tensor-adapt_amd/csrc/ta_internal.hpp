@@ -73,6 +73,18 @@ struct GemmGroup {
     const bf16* bias;
     const LoraEpi* lora;
 };
+// one GEMM of a gemm_chain: X [M x K] (row stride ldx) times Y [N x K]^T
+struct GemmSeg {
+    int K;
+    const bf16* X;
+    int64_t ldx;
+    const bf16* Y;
+    int64_t ldy;
+};
+// C = bf16(X_0 Y_0^T), then C = bf16(X_s Y_s^T + C), then the LoRA terms, in
+// one launch over the concatenated K (rounded to BF16 between the GEMMs)
+int gemm_chain(int M, int N, const GemmSeg* sg, int ns, bf16* C, int64_t ldc, const LoraEpi* lora,
+               hipStream_t s);
 // the groups' GEMMs in one launch over the N-concatenated tile grid
 int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const GemmGroup* gr,
                 int ng, hipStream_t s);
