@@ -300,8 +300,12 @@ static int engine_alloc(Engine* e) {
                     add(pr.out, r, 0, e->grad + pr.offB, nullptr, nullptr, fused ? e->sl_st : 0);
                     ga[n++] = e->grad + pr.offA;
                 }
+                // gA of the down pair comes token-split from the fused kernel too
+                const bool fused_d = e->silu_fused && *g.pairs.begin() == PD &&
+                                     e->L[l].pr[PG].on && e->L[l].pr[PU].on;
                 if (n)
-                    add(g.in, n * r, 1, ga[0], ga[1] ? ga[1] : ga[0], ga[2] ? ga[2] : ga[0], 0);
+                    add(g.in, n * r, 1, ga[0], ga[1] ? ga[1] : ga[0], ga[2] ? ga[2] : ga[0],
+                        fused_d ? e->sl_st : 0);
             }
         e->wg_blocks = blk;
         if (!e->wg_plan.empty()) {
@@ -426,9 +430,12 @@ static int next_wgrad(Engine* e, int NL, int NS, float** part) {
 //   gA_p += s * dh_p^T x             (all pairs of the group in one pass over x)
 // and returns the terms gx = bf16(s * dh_p A_p + gx) (pairs in order) for
 // the epilogue of the last input-gradient GEMM of the group.  dh_ready: dh_p
-// and the gB products were made already (the fused SwiGLU backward).
+// and the gB products were made already (the fused SwiGLU backward);
+// gA_part: the gA product is left to the caller, which receives its
+// partials slice (the fused SwiGLU backward makes it for the down pair).
 static int lora_group_bwd(Engine* e, Layer& ly, std::initializer_list<int> group, const bf16* x,
-                          int in, const bf16* const* gos, LoraEpi* ep, bool dh_ready = false) {
+                          int in, const bf16* const* gos, LoraEpi* ep, bool dh_ready = false,
+                          float** gA_part = nullptr) {
     *ep = LoraEpi{};
     int on[3], n = 0, i = 0;
     const bf16* go_on[3];
@@ -467,6 +474,10 @@ static int lora_group_bwd(Engine* e, Layer& ly, std::initializer_list<int> group
     }
     float* part = nullptr;
     CK(next_wgrad(e, in, (int)ldh, &part));
+    if (gA_part) {
+        *gA_part = part;
+        return 0;
+    }
     TIMED(TA_CAT_LORA, gflops(ldh, in, dBT), dBT * (in + ldh) * 2,
           lora_wgrad_part(x, in, in, e->dh_cat, ldh, (int)ldh, BT, part, e->s));
     return 0;
@@ -608,22 +619,26 @@ static int backward(Engine* e) {
     for (int l = c.layers - 1; l >= 0; l--) {
         Layer& ly = e->L[l];
         // FFN (qwen2.cu:222-246)
+        const bool fused = e->silu_fused && ly.pr[PG].on && ly.pr[PU].on;
+        float* ga_down = nullptr;  // the down pair's gA partials, made by the fused kernel
         {
             const bf16* gos[1] = {e->g_res};
             LoraEpi ep;
-            CK(lora_group_bwd(e, ly, {PD}, ly.act, I, gos, &ep));
+            CK(lora_group_bwd(e, ly, {PD}, ly.act, I, gos, &ep, false, fused ? &ga_down : nullptr));
             CK(proj_bwd_x(e, ly.Wt[PD], e->g_res, e->dact, H, I, 0.f, &ep));
         }
-        const bool fused = e->silu_fused && ly.pr[PG].on && ly.pr[PU].on;
         if (fused) {
             // dgate, dup, dh of both pairs and their gB partials in one pass
+            // (and the down pair's gA = act^T dh_down, act recomputed)
             float *pg = nullptr, *pu = nullptr;
             CK(next_wgrad(e, I, e->r, &pg));
             CK(next_wgrad(e, I, e->r, &pu));
             const Pair &PRg = ly.pr[PG], &PRu = ly.pr[PU];
-            TIMED(TA_CAT_ELEMWISE, 4.0 * gflops(BT, e->r, I), dBT * I * 10 + dBT * 64,
+            TIMED(TA_CAT_ELEMWISE, (ga_down ? 5.0 : 4.0) * gflops(BT, e->r, I),
+                  dBT * I * 10 + dBT * 96,
                   silu_bwd_lora(e->dact, ly.gate, ly.up, e->dgate, e->dup, e->shadowT + PRg.offB,
-                                e->shadowT + PRu.offB, PRg.h, PRu.h, e->dh_part, pg, pu, BT, I, s));
+                                e->shadowT + PRu.offB, PRg.h, PRu.h, e->dh_part, pg, pu,
+                                ga_down ? e->dh_cat : nullptr, ga_down, BT, I, s));
             TIMED(TA_CAT_LORA, 0, dBT * 128.0 * e->sl_so + dBT * 64,
                   dh_reduce2(e->dh_part, e->sl_so, BT, e->dh_cat, 2 * e->r, s));
         } else {

@@ -568,6 +568,13 @@ __device__ __forceinline__ s16x4_t tr4(const char* p) {
 __device__ __forceinline__ floatx4 mf16k16(s16x4_t a, s16x4_t b, floatx4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
 }
+__device__ __forceinline__ u32x4 silu_fwd8(u32x4 gt, u32x4 u) {
+    u32x4 o;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        o[i] = pack2(silu_mul_f(lo2f(gt[i]), lo2f(u[i])), silu_mul_f(hi2f(gt[i]), hi2f(u[i])));
+    return o;
+}
 __device__ __forceinline__ void silu_bwd8(u32x4 d, u32x4 gt, u32x4 u, u32x4& dg, u32x4& du) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
@@ -579,15 +586,16 @@ __device__ __forceinline__ void silu_bwd8(u32x4 d, u32x4 gt, u32x4 u, u32x4& dg,
     }
 }
 
-template <int NW>
+template <int NW, bool DG>  // DG: also the down pair's gA partial act^T dh_down
 __global__ __launch_bounds__(NW * 64) void k_silu_bwd_lora(
     const bf16* __restrict__ dact, const bf16* __restrict__ gate, const bf16* __restrict__ up,
     bf16* __restrict__ dgate, bf16* __restrict__ dup, const bf16* __restrict__ bt_g,
     const bf16* __restrict__ bt_u, const bf16* __restrict__ h_g, const bf16* __restrict__ h_u,
-    float* __restrict__ dh_part, float* __restrict__ gb_g, float* __restrict__ gb_u, int BT,
-    int I, int per) {
-    __shared__ __attribute__((aligned(16))) char sW[NW][2][16 * 128];  // go tiles per wave, pair
-    __shared__ __attribute__((aligned(16))) char sHw[NW][2][16 * 32];  // h tiles per wave, pair
+    float* __restrict__ dh_part, float* __restrict__ gb_g, float* __restrict__ gb_u,
+    const bf16* __restrict__ dh_d, float* __restrict__ ga_d, int BT, int I, int per) {
+    constexpr int NP = DG ? 3 : 2;  // transposed products: gate gB, up gB (, down gA)
+    __shared__ __attribute__((aligned(16))) char sW[NW][NP][16 * 128];  // go (act) tiles per wave
+    __shared__ __attribute__((aligned(16))) char sHw[NW][NP][16 * 32];  // h (dh_down) tiles per wave
     __shared__ __attribute__((aligned(16))) float sDh[2][NW][8][64];   // dh partials [buf][wave]
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int g = lane >> 4, j = lane & 15;
@@ -600,10 +608,12 @@ __global__ __launch_bounds__(NW * 64) void k_silu_bwd_lora(
     // h element of a tile: pair lane/32, row (lane/2)%16, half lane%2
     const int hp = lane >> 5, hrow = (lane >> 1) & 15, hh = lane & 1;
     const bf16* hsrc = (hp ? h_u : h_g) + hrow * 16 + 8 * hh;
+    const bf16* dsrc = dh_d + hrow * 16 + 8 * hh;  // (lanes 32.. repeat lanes 0..31)
     char* const sw0 = sW[w][0];
     char* const sw1 = sW[w][1];
+    char* const sw2 = sW[w][NP - 1];
     char* const shw = sHw[w][0];
-    u32x4 ra[2][2], rg[2][2], ru[2][2], rh[2];  // [buffer][row half]
+    u32x4 ra[2][2], rg[2][2], ru[2][2], rh[2], rd[2];  // [buffer][row half]
 #define SL_LOAD(B, tb)                                                        \
     do {                                                                      \
         const int64_t o_ = (int64_t)(tb) * I + lofs;                          \
@@ -613,11 +623,14 @@ __global__ __launch_bounds__(NW * 64) void k_silu_bwd_lora(
             ru[B][i] = *(const u32x4*)(up + o_ + 8 * (int64_t)I * i);         \
         }                                                                     \
         rh[B] = *(const u32x4*)(hsrc + (int64_t)(tb) * 16);                   \
+        if constexpr (DG) rd[B] = *(const u32x4*)(dsrc + (int64_t)(tb) * 16); \
     } while (0)
     bf16x8_t fb[2][2];  // B^T shadow: row j, columns cw + 32 kc + 8g .. + 7
-    floatx4 gb[2][4];   // [pair][16-column group] over the block's tokens
+    floatx4 gb[NP][4];  // [product][16-column group] over the block's tokens
 #pragma unroll
-    for (int ct = 0; ct < 4; ct++) gb[0][ct] = gb[1][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < NP; q++)
+#pragma unroll
+        for (int ct = 0; ct < 4; ct++) gb[q][ct] = floatx4{0.f, 0.f, 0.f, 0.f};
     if (act) {
 #pragma unroll
         for (int kc = 0; kc < 2; kc++) {
@@ -636,10 +649,15 @@ __global__ __launch_bounds__(NW * 64) void k_silu_bwd_lora(
             if (tb < t_end) {  // block-uniform
                 floatx4 dhw[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
                 if (act) {
-                    u32x4 og[2], ou[2];
+                    u32x4 og[2], ou[2], oa[2];
 #pragma unroll
-                    for (int i = 0; i < 2; i++) silu_bwd8(ra[B][i], rg[B][i], ru[B][i], og[i], ou[i]);
+                    for (int i = 0; i < 2; i++) {
+                        silu_bwd8(ra[B][i], rg[B][i], ru[B][i], og[i], ou[i]);
+                        // act = silu_mul(gate, up) exactly as the forward computed it
+                        if constexpr (DG) oa[i] = silu_fwd8(rg[B][i], ru[B][i]);
+                    }
                     const u32x4 hv = rh[B];
+                    const u32x4 dv = rd[B];
                     if (tb + 32 < t_end) SL_LOAD(B, tb + 32);
                     const int64_t o = (int64_t)tb * I + lofs;
                     const int lr = lane >> 3, lc = 8 * (lane & 7);
@@ -649,8 +667,10 @@ __global__ __launch_bounds__(NW * 64) void k_silu_bwd_lora(
                         *(u32x4*)(dup + o + 8 * (int64_t)I * i) = ou[i];
                         *(u32x4*)(sw0 + sw_off(lr + 8 * i, lc)) = og[i];
                         *(u32x4*)(sw1 + sw_off(lr + 8 * i, lc)) = ou[i];
+                        if constexpr (DG) *(u32x4*)(sw2 + sw_off(lr + 8 * i, lc)) = oa[i];
                     }
                     *(u32x4*)(shw + hp * 512 + tr_off<1>(hrow, 8 * hh)) = hv;
+                    if (DG && hp == 0) *(u32x4*)(shw + 1024 + tr_off<1>(hrow, 8 * hh)) = dv;
                     // one wave's LDS instructions execute in order, so the
                     // reads below see the writes above; keep the compiler
                     // from moving them across
@@ -668,6 +688,13 @@ __global__ __launch_bounds__(NW * 64) void k_silu_bwd_lora(
                     for (int ct = 0; ct < 4; ct++) {
                         gb[0][ct] = mf16k16(tr4(sw0 + sw_off(rr, 16 * ct + cc)), hb0, gb[0][ct]);
                         gb[1][ct] = mf16k16(tr4(sw1 + sw_off(rr, 16 * ct + cc)), hb1, gb[1][ct]);
+                    }
+                    if constexpr (DG) {
+                        const s16x4_t hb2 = tr4(shw + 1024 + tr_off<1>(rr, cc));
+#pragma unroll
+                        for (int ct = 0; ct < 4; ct++)
+                            gb[NP - 1][ct] =
+                                mf16k16(tr4(sw2 + sw_off(rr, 16 * ct + cc)), hb2, gb[NP - 1][ct]);
                     }
                     asm volatile("" ::: "memory");
                 }
@@ -699,6 +726,7 @@ __global__ __launch_bounds__(NW * 64) void k_silu_bwd_lora(
                 const int64_t o = ((int64_t)blockIdx.y * I + cw + 16 * ct + 4 * g + i) * 16 + j;
                 gb_g[o] = gb[0][ct][i];
                 gb_u[o] = gb[1][ct][i];
+                if constexpr (DG) ga_d[o] = gb[NP - 1][ct][i];
             }
     }
 }
@@ -874,7 +902,8 @@ static int silu_lora_plan(int BT, int I, int* s_t, int* s_o, int* per) {
         int nb = 0, dev = 0, ncu = 0;
         TA_HIP(hipGetDevice(&dev));
         TA_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
-        TA_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_silu_bwd_lora<SL_NW>, SL_NW * 64, 0));
+        TA_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_silu_bwd_lora<SL_NW, true>,
+                                                            SL_NW * 64, 0));
         resident = std::max(1, nb) * std::max(1, ncu);
     }
     *s_o = (I + SL_NW * 64 - 1) / (SL_NW * 64);
@@ -890,16 +919,26 @@ int silu_lora_splits(int BT, int I, int* s_t, int* s_o) {
 
 int silu_bwd_lora(const bf16* dact, const bf16* gate, const bf16* up, bf16* dgate, bf16* dup,
                   const bf16* bt_g, const bf16* bt_u, const bf16* h_g, const bf16* h_u,
-                  float* dh_part, float* gb_g, float* gb_u, int BT, int I, hipStream_t s) {
+                  float* dh_part, float* gb_g, float* gb_u, const bf16* dh_d, float* ga_d, int BT,
+                  int I, hipStream_t s) {
     TA_REQUIRE(BT > 0 && I > 0 && BT % 64 == 0 && I % 64 == 0,
                "silu_bwd_lora: BT %d and I %d must be positive multiples of 64", BT, I);
     const void* ptrs[] = {dact, gate, up, dgate, dup, bt_g, bt_u, h_g, h_u, dh_part, gb_g, gb_u};
     for (const void* q : ptrs)
         TA_REQUIRE(q && ((uintptr_t)q & 15) == 0, "silu_bwd_lora: null or unaligned operand");
+    TA_REQUIRE(!dh_d == !ga_d && ((uintptr_t)dh_d & 15) == 0 && ((uintptr_t)ga_d & 15) == 0,
+               "silu_bwd_lora: the down pair's dh and gA partials come together, aligned");
     int s_t = 0, s_o = 0, per = 0;
     if (int rc = silu_lora_plan(BT, I, &s_t, &s_o, &per)) return rc;
-    k_silu_bwd_lora<SL_NW><<<dim3(s_o, s_t), SL_NW * 64, 0, s>>>(dact, gate, up, dgate, dup, bt_g, bt_u, h_g, h_u,
-                                                   dh_part, gb_g, gb_u, BT, I, per);
+    const dim3 grid(s_o, s_t);
+    if (ga_d)
+        k_silu_bwd_lora<SL_NW, true><<<grid, SL_NW * 64, 0, s>>>(
+            dact, gate, up, dgate, dup, bt_g, bt_u, h_g, h_u, dh_part, gb_g, gb_u, dh_d, ga_d, BT, I,
+            per);
+    else
+        k_silu_bwd_lora<SL_NW, false><<<grid, SL_NW * 64, 0, s>>>(
+            dact, gate, up, dgate, dup, bt_g, bt_u, h_g, h_u, dh_part, gb_g, gb_u, dh_d, ga_d, BT, I,
+            per);
     return check_launch("silu_bwd_lora");
 }
 

@@ -123,11 +123,14 @@ int lora_wgrad_part(const bf16* L, int64_t ldl, int NL, const bf16* Sm, int64_t 
 // Fused SwiGLU backward + gate/up LoRA backward (rank 16): dgate/dup as
 // silu_mul_bwd, the dh products of both pairs as column-split partials
 // (dh_part [S_o][2][BT][16]) and their gB products as token-split partials
-// (gb_g/gb_u [S_t][I][16], deferred-reduce layout).  BT and I multiples of 64.
+// (gb_g/gb_u [S_t][I][16], deferred-reduce layout); with dh_d/ga_d also the
+// down pair's gA product act^T dh_down (act recomputed from gate and up) as
+// token-split partials ga_d [S_t][I][16].  BT and I multiples of 64.
 int silu_lora_splits(int BT, int I, int* s_t, int* s_o);
 int silu_bwd_lora(const bf16* dact, const bf16* gate, const bf16* up, bf16* dgate, bf16* dup,
                   const bf16* bt_g, const bf16* bt_u, const bf16* h_g, const bf16* h_u,
-                  float* dh_part, float* gb_g, float* gb_u, int BT, int I, hipStream_t s);
+                  float* dh_part, float* gb_g, float* gb_u, const bf16* dh_d, float* ga_d, int BT,
+                  int I, hipStream_t s);
 // dh[t][p*16 + j] = bf16(sum over the S_o column splits of dh_part[s][p][t][j]), p = 0, 1
 int dh_reduce2(const float* dh_part, int s_o, int BT, bf16* dh, int64_t ldh, hipStream_t s);
 int lora_wgrad_reduce_jobs(const WgradJob* jobs, int njobs, int64_t total_blocks, double elems,
