@@ -118,7 +118,9 @@ int ta_engine_write_adapter(void* engine, int layer, int target, int which, cons
 int ta_engine_centroid(void* engine, double* host_out);
 
 /* Device pointer of a cached activation, for parity checks: "l3.x_normed",
- * "l3.Q", "l3.attn_w", "logits" (holds dlogits after a step), "loss_tok",
+ * "l3.Q", "l3.attn_stats" (each attention row's max in base-2 units and
+ * 1/sum: the probabilities are recomputed from them, not stored), "logits"
+ * (holds dlogits after a step), "loss_tok",
  * "targets" (the masked int32 targets of the last step; is_f32 = 1 marks its
  * 4-byte elements), ... */
 void* ta_engine_buffer(void* engine, const char* name, int64_t* n_elems, int* is_f32);

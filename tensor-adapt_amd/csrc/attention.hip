@@ -157,6 +157,24 @@ __device__ __forceinline__ void wave_qk(floatx4 (&S)[4], const bf16x8_t (&af)[HD
     }
 }
 
+// wave_qk with the B rows read from a tile in the tr_off<HD/16> layout (the
+// transposing-read layout, rows kept whole): the same values in the same
+// MFMA order, so the same S bit for bit.
+template <int HD>
+__device__ __forceinline__ void wave_qk_tr(floatx4 (&S)[4], const bf16x8_t (&af)[HD / 32],
+                                           const char* __restrict__ sB, int lane) {
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+        S[t] = zero4();
+        const int row = 16 * t + (lane & 15);
+#pragma unroll
+        for (int ks = 0; ks < HD / 32; ks++)
+            S[t] = mfma16(af[ks],
+                          *(const bf16x8_t*)(sB + tr_off<HD / 16>(row, 32 * ks + 8 * (lane >> 4))),
+                          S[t]);
+    }
+}
+
 // acc[16 x HD] += A[16 x 64] * B[64 x HD]; A (an F32 quantity: P or dS)
 // arrives as two BF16 tiles, hi = bf16(a) and lo = bf16(a - hi), in this
 // wave's LDS slots sA[0], sA[1] ([16][LDT], k contiguous), so the product
@@ -208,13 +226,14 @@ __device__ __forceinline__ float red16_sum(float v) {
 // transposing LDS read.
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-template <int HD>
+template <int HD, bool SP>  // SP: store P (else only the row statistics)
 __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
                                                   const bf16* __restrict__ K,
                                                   const bf16* __restrict__ V,
                                                   bf16* __restrict__ O, float* __restrict__ O32,
-                                                  float* __restrict__ P, int T, int Hq, int Hkv,
-                                                  float scale, int zero_fill) {
+                                                  float* __restrict__ P, float2* __restrict__ stats,
+                                                  int T, int Hq, int Hkv, float scale,
+                                                  int zero_fill) {
     constexpr int VST = HD / 16;  // 32-byte units of a V row
     __shared__ __attribute__((aligned(16))) bf16 sK[TK * (HD + 8)];
     __shared__ __attribute__((aligned(16))) char sV[TK * HD * 2];
@@ -229,7 +248,7 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
     const bf16* Qh = Q + (int64_t)b * T * qs + hq * HD;
     const bf16* Kh = K + (int64_t)b * T * ks_ + hkv * HD;
     const bf16* Vh = V + (int64_t)b * T * ks_ + hkv * HD;
-    float* Ph = P + (int64_t)bh * T * T;
+    float* Ph = SP ? P + (int64_t)bh * T * T : nullptr;
     int q0 = qt * TQ;
     int rowA = q0 + 16 * w + (lane & 15);  // A-operand row of this lane
     bf16x8_t qf[HD / 32];
@@ -279,6 +298,10 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
     for (int r = 0; r < 4; r++) {
         inv[r] = 1.f / red16_sum(l[r]);
         rowok[r] = rbase + r < T;
+        // (max, 1 / sum) of the row: P = exp2(S scale log2e - max) / sum is
+        // recomputed from them, bit for bit, where P is not stored
+        if (stats && rowok[r] && (lane & 15) == 0)
+            stats[(int64_t)bh * T + rbase + r] = make_float2(m[r], inv[r]);
     }
 
     // pass 2: P, O
@@ -314,7 +337,8 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
             for (int r = 0; r < 4; r++) {
                 p[r] = exp2_fast(S[t][r] * sl2 - m[r]) * inv[r];
                 if (diag && !(key <= rbase + r && key < T)) p[r] = 0.f;
-                if (rowok[r] && (!diag || key < T)) Ph[(int64_t)(rbase + r) * T + key] = p[r];
+                if constexpr (SP)
+                    if (rowok[r] && (!diag || key < T)) Ph[(int64_t)(rbase + r) * T + key] = p[r];
             }
             uint2 hi, lo;
             hi.x = pack2(p[0], p[1]);
@@ -339,7 +363,7 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
         }
     }
     // zeros above the diagonal (ops.cu:352-396 leaves exact zeros there)
-    if (zero_fill) {
+    if (SP && zero_fill) {
         int k0 = (qt + 1) * TK;
         int width = T - k0;
         if (width > 0) {
@@ -476,11 +500,13 @@ __device__ __forceinline__ void load_p_rows(float (&p)[4][4], const float* __res
 // K is staged once, in its natural layout, and read as the dS·K operand
 // through the transposing LDS read; dS (hi/lo) goes to a per-wave
 // [key][row] tile like P in the forward.
-template <int HD>
+template <int HD, bool RC>  // RC: recompute P from Q, K and the forward's row statistics
 __global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO,
+                                                     const bf16* __restrict__ Q,
                                                      const bf16* __restrict__ K,
                                                      const bf16* __restrict__ V,
                                                      const float* __restrict__ P,
+                                                     const float2* __restrict__ stats,
                                                      const float* __restrict__ Dq,
                                                      bf16* __restrict__ dQ, int T, int Hq, int Hkv,
                                                      float scale) {
@@ -498,7 +524,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO
     const bf16* dOh = dO + (int64_t)b * T * qs + hq * HD;
     const bf16* Kh = K + (int64_t)b * T * ks_ + hkv * HD;
     const bf16* Vh = V + (int64_t)b * T * ks_ + hkv * HD;
-    const float* Ph = P + (int64_t)bh * T * T;
+    const float* Ph = RC ? nullptr : P + (int64_t)bh * T * T;
     int q0 = qt * TQ;
     int rowA = q0 + 16 * w + (lane & 15);
     bf16x8_t of[HD / 32];
@@ -509,6 +535,23 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO
     float D[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) D[r] = (rbase + r < T) ? Dq[(int64_t)bh * T + rbase + r] : 0.f;
+    // recompute: Q fragments and the rows' (max, 1/sum), as in the forward
+    // (rows past T: 1/sum = 0, so P = 0 there)
+    bf16x8_t qf[RC ? HD / 32 : 1];
+    float sm[4], si[4];
+    const float sl2 = scale * kLog2e;
+    if constexpr (RC) {
+        const bf16* Qh = Q + (int64_t)b * T * qs + hq * HD;
+#pragma unroll
+        for (int ks = 0; ks < HD / 32; ks++)
+            qf[ks] = ld_head8(Qh, qs, rowA, T, 32 * ks + 8 * (lane >> 4));
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float2 st = (rbase + r < T) ? stats[(int64_t)bh * T + rbase + r] : make_float2(0.f, 0.f);
+            sm[r] = st.x;
+            si[r] = st.y;
+        }
+    }
 
     floatx4 acc[HD / 16];
 #pragma unroll
@@ -517,7 +560,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO
     float pn[4][4];
     lv.load(Vh, ks_, 0, T);
     lk.load(Kh, ks_, 0, T);
-    load_p_rows(pn, Ph, T, rbase, 0, lane);
+    if constexpr (!RC) load_p_rows(pn, Ph, T, rbase, 0, lane);
     char* sSh = sS[w][0];
     char* sSl = sS[w][1];
     for (int kt = 0; kt <= qt; kt++) {
@@ -529,15 +572,32 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO
             *(u32x4*)(sK + tr_off<VST>(q / (HD / 8), (q % (HD / 8)) * 8)) = lk.v[i];
         }
         float pc[4][4];
+        if constexpr (!RC) {
 #pragma unroll
-        for (int t = 0; t < 4; t++)
+            for (int t = 0; t < 4; t++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) pc[t][r] = pn[t][r];
+                for (int r = 0; r < 4; r++) pc[t][r] = pn[t][r];
+        }
         __syncthreads();
         if (kt < qt) {
             lv.load(Vh, ks_, (kt + 1) * TK, T);
             lk.load(Kh, ks_, (kt + 1) * TK, T);
-            load_p_rows(pn, Ph, T, rbase, (kt + 1) * TK, lane);
+            if constexpr (!RC) load_p_rows(pn, Ph, T, rbase, (kt + 1) * TK, lane);
+        }
+        if constexpr (RC) {
+            // P of this tile exactly as the forward computed it
+            floatx4 S[4];
+            wave_qk_tr<HD>(S, qf, sK, lane);
+            const bool diag = kt == qt;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int key = kt * TK + 16 * t + (lane & 15);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    pc[t][r] = exp2_fast(S[t][r] * sl2 - sm[r]) * si[r];
+                    if (diag && !(key <= rbase + r && key < T)) pc[t][r] = 0.f;
+                }
+            }
         }
         floatx4 dP[4];
         wave_qk<HD>(dP, of, sV, lane);
@@ -613,17 +673,18 @@ __device__ __forceinline__ void load_p_cols(float (&p)[4][4], const float* __res
 // dO is staged twice: padded rows for dP^T (16-byte fragment reads) and in
 // the transposing-read layout for the P^T·dO operand, like Q for dS^T·Q;
 // P^T and dS^T (hi/lo) go to a per-wave [query][key] tile.
-template <int HD>
+template <int HD, bool RC>  // RC: recompute P from Q, K and the forward's row statistics
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_bwd_dkv(
-    const bf16* __restrict__ dO, const bf16* __restrict__ Q, const bf16* __restrict__ V,
-    const float* __restrict__ P, const float* __restrict__ Dq, float* __restrict__ part, int T,
-    int Hq, int Hkv) {
+    const bf16* __restrict__ dO, const bf16* __restrict__ Q, const bf16* __restrict__ K,
+    const bf16* __restrict__ V, const float* __restrict__ P, const float2* __restrict__ stats,
+    const float* __restrict__ Dq, float* __restrict__ part, int T, int Hq, int Hkv, float scale) {
     constexpr int VST = HD / 16;
     __shared__ __attribute__((aligned(16))) bf16 sO[TQ * (HD + 8)];  // dO [q][hd], padded
     __shared__ __attribute__((aligned(16))) char sOn[TQ * HD * 2];   // dO, tr_off layout
     __shared__ __attribute__((aligned(16))) char sQn[TQ * HD * 2];   // Q, tr_off layout
     __shared__ __attribute__((aligned(16))) char sA[4][2][TQ * 16 * 2];  // per wave [q][key] hi,lo
     __shared__ float sD[TQ];
+    __shared__ float2 sSt[TQ];  // (max, 1/sum) of the tile's query rows (RC)
     int nkt = (T + TK - 1) / TK;
     int nbh = gridDim.x / nkt;
     int kt = (int)(blockIdx.x / nbh);  // low kt = most query tiles: they launch first
@@ -634,13 +695,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const bf16* Vh = V + (int64_t)b * T * ks_ + hkv * HD;
     const bf16* dOh = dO + (int64_t)b * T * qs + hq * HD;
     const bf16* Qh = Q + (int64_t)b * T * qs + hq * HD;
-    const float* Ph = P + (int64_t)bh * T * T;
+    const float* Ph = RC ? nullptr : P + (int64_t)bh * T * T;
     const float* Dh = Dq + (int64_t)bh * T;
     int k0 = kt * TK;
     int keyA = k0 + 16 * w + (lane & 15);  // A-operand row (key) of this lane
     bf16x8_t vf[HD / 32];
 #pragma unroll
     for (int s = 0; s < HD / 32; s++) vf[s] = ld_head8(Vh, ks_, keyA, T, 32 * s + 8 * (lane >> 4));
+    // recompute: K fragments for S^T = K Q^T (the forward's S, transposed)
+    bf16x8_t kf[RC ? HD / 32 : 1];
+    const float sl2 = scale * kLog2e;
+    if constexpr (RC) {
+        const bf16* Kh = K + (int64_t)b * T * ks_ + hkv * HD;
+#pragma unroll
+        for (int s = 0; s < HD / 32; s++) kf[s] = ld_head8(Kh, ks_, keyA, T, 32 * s + 8 * (lane >> 4));
+    }
+    const float2* Sth = RC ? stats + (int64_t)bh * T : nullptr;
     int kbase = k0 + 16 * w + 4 * (lane >> 4);  // C-layout key rows kbase + r
 
     floatx4 accK[HD / 16], accV[HD / 16];
@@ -653,10 +723,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     Rows64<HD> ldo, lq;
     float pn[4][4];
     float dn = 0.f;
+    float2 stn = make_float2(0.f, 0.f);
     ldo.load(dOh, qs, kt * TQ, T);
     lq.load(Qh, qs, kt * TQ, T);
-    load_p_cols(pn, Ph, T, kt * TQ, kbase, lane);
+    if constexpr (!RC) load_p_cols(pn, Ph, T, kt * TQ, kbase, lane);
     if (threadIdx.x < TQ) dn = (kt * TQ + threadIdx.x < T) ? Dh[kt * TQ + threadIdx.x] : 0.f;
+    if (RC && threadIdx.x < TQ && kt * TQ + threadIdx.x < T) stn = Sth[kt * TQ + threadIdx.x];
     char* sAh = sA[w][0];
     char* sAl = sA[w][1];
     for (int qt = kt; qt < nqt; qt++) {
@@ -670,18 +742,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             *(u32x4*)(sQn + off) = lq.v[i];
         }
         if (threadIdx.x < TQ) sD[threadIdx.x] = dn;
+        if (RC && threadIdx.x < TQ) sSt[threadIdx.x] = stn;
         float pv[4][4];
+        if constexpr (!RC) {
 #pragma unroll
-        for (int t = 0; t < 4; t++)
+            for (int t = 0; t < 4; t++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) pv[t][r] = pn[t][r];
+                for (int r = 0; r < 4; r++) pv[t][r] = pn[t][r];
+        }
         __syncthreads();
         if (qt + 1 < nqt) {
             int qn = (qt + 1) * TQ;
             ldo.load(dOh, qs, qn, T);
             lq.load(Qh, qs, qn, T);
-            load_p_cols(pn, Ph, T, qn, kbase, lane);
+            if constexpr (!RC) load_p_cols(pn, Ph, T, qn, kbase, lane);
             if (threadIdx.x < TQ) dn = (qn + threadIdx.x < T) ? Dh[qn + threadIdx.x] : 0.f;
+            if (RC && threadIdx.x < TQ) stn = (qn + threadIdx.x < T) ? Sth[qn + threadIdx.x] : make_float2(0.f, 0.f);
+        }
+        if constexpr (RC) {
+            // P^T of this tile: the forward's P[query][key] from S^T = K Q^T
+            // (query rows past T have 1/sum = 0); keys above a query are
+            // masked on the diagonal tile only
+            floatx4 St[4];
+            wave_qk_tr<HD>(St, kf, sQn, lane);
+            const bool diag = qt == kt;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int ql = 16 * t + (lane & 15);
+                const float2 st = sSt[ql];
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    pv[t][r] = exp2_fast(St[t][r] * sl2 - st.x) * st.y;
+                    if (diag && kbase + r > qt * TQ + ql) pv[t][r] = 0.f;
+                }
+            }
         }
         floatx4 dPt[4];
         wave_qk<HD>(dPt, vf, sO, lane);  // rows = keys, cols = queries
@@ -782,32 +876,37 @@ __global__ void k_attn_dkv_reduce(const float* __restrict__ part, bf16* __restri
 
 static inline bool a16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* O32, float* P, int B,
-             int T, int Hq, int Hkv, int hd, bool zero_fill, hipStream_t s) {
+int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* O32, float* P,
+             float* stats, int B, int T, int Hq, int Hkv, int hd, bool zero_fill, hipStream_t s) {
     TA_REQUIRE(B > 0 && T > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0,
                "sdpa_fwd: bad shape B=%d T=%d Hq=%d Hkv=%d", B, T, Hq, Hkv);
+    TA_REQUIRE(P || stats, "sdpa_fwd: neither probabilities nor row statistics requested");
     TA_REQUIRE(hd == 64 || hd == 128, "sdpa_fwd: head_dim %d not supported (64 or 128)", hd);
     TA_REQUIRE(a16(Q) && a16(K) && a16(V) && a16(O), "sdpa_fwd: tensors must be 16-byte aligned");
     int nqt = (T + TQ - 1) / TQ;
     int64_t blocks = (int64_t)B * Hq * nqt;
     float scale = 1.f / sqrtf((float)hd);
     const bool timed = kprof_begin(KP_ATTN_FWD, s);
-    if (hd == 64)
-        k_attn_fwd<64><<<(int)blocks, 256, 0, s>>>(Q, K, V, O, O32, P, T, Hq, Hkv, scale,
-                                                   zero_fill);
-    else
-        k_attn_fwd<128><<<(int)blocks, 256, 0, s>>>(Q, K, V, O, O32, P, T, Hq, Hkv, scale,
-                                                    zero_fill);
+    float2* st = (float2*)stats;
+#define AF(H, SPv) \
+    k_attn_fwd<H, SPv><<<(int)blocks, 256, 0, s>>>(Q, K, V, O, O32, P, st, T, Hq, Hkv, scale, zero_fill)
+    if (hd == 64) {
+        if (P) AF(64, true); else AF(64, false);
+    } else {
+        if (P) AF(128, true); else AF(128, false);
+    }
+#undef AF
     if (timed) {
         // causal S = QK^T and O = PV; Q, K, V read, O written (and O32),
         // P written (causal half, or all of it when the upper triangle is
         // zero-filled)
         double tri = (double)B * Hq * T * (T + 1) / 2.0, bt = (double)B * T;
-        double pbytes = zero_fill ? 4.0 * B * Hq * (double)T * T : 4.0 * tri;
+        double pbytes = !P ? 8.0 * B * Hq * (double)T : zero_fill ? 4.0 * B * Hq * (double)T * T : 4.0 * tri;
         kprof_end(KP_ATTN_FWD, s, 4.0 * hd * tri,
                   2.0 * bt * hd * (2.0 * Hq + 2.0 * Hkv) + (O32 ? 4.0 * bt * Hq * hd : 0.0) +
                       pbytes,
-                  hd == 64 ? "void ta::k_attn_fwd<64>" : "void ta::k_attn_fwd<128>");
+                  hd == 64 ? (P ? "void ta::k_attn_fwd<64, true>" : "void ta::k_attn_fwd<64, false>")
+                           : (P ? "void ta::k_attn_fwd<128, true>" : "void ta::k_attn_fwd<128, false>"));
     }
     return check_launch("sdpa_fwd");
 }
@@ -815,9 +914,12 @@ int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* O32, f
 // Dbuf: [B*Hq*T] F32 row dots; part: [2*B*Hq*T*hd] F32 per-head dK/dV
 // contributions (both drawn from the scratch pool when NULL).  O32: the
 // forward's F32 output [B*T, Hq*hd] (NULL: the row dots are formed from P).
+// P NULL: the probabilities are recomputed from Q, K and the forward's row
+// statistics (stats, [B*Hq*T] (max, 1/sum) pairs), which needs O32.
 int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const float* P,
-             const float* O32, bf16* dQ, bf16* dK, bf16* dV, int B, int T, int Hq, int Hkv, int hd,
-             float* Dbuf, float* part, hipStream_t s) {
+             const float* stats, const float* O32, bf16* dQ, bf16* dK, bf16* dV, int B, int T,
+             int Hq, int Hkv, int hd, float* Dbuf, float* part, hipStream_t s) {
+    TA_REQUIRE(P || (stats && O32), "sdpa_bwd: without P, the row statistics and O32 are needed");
     TA_REQUIRE(B > 0 && T > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0,
                "sdpa_bwd: bad shape B=%d T=%d Hq=%d Hkv=%d", B, T, Hq, Hkv);
     TA_REQUIRE(hd == 64 || hd == 128, "sdpa_bwd: head_dim %d not supported (64 or 128)", hd);
@@ -853,25 +955,39 @@ int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const 
     // pass dP again, dV = P^T dO, dK = dS^T Q.  Bytes: BF16 operands, P and
     // the row dots read once, outputs written once (dkv: F32 partials)
     const double tri = (double)B * Hq * T * (T + 1) / 2.0, bt = (double)B * T;
+    const float2* st = (const float2*)stats;
+    const bool rc = P == nullptr;
+    // with recomputation each pass also forms S = QK^T again (2 hd flops per
+    // causal element) and reads the row statistics instead of P
+    const double pb = rc ? 8.0 * B * Hq * (double)T : 4.0 * tri, rf = rc ? 2.0 * hd * tri : 0.0;
     bool timed = kprof_begin(KP_ATTN_BWD_DQ, s);
-    if (hd == 64)
-        k_attn_bwd_dq<64><<<(int)b1, 256, 0, s>>>(dO, K, V, P, Dbuf, dQ, T, Hq, Hkv, scale);
-    else
-        k_attn_bwd_dq<128><<<(int)b1, 256, 0, s>>>(dO, K, V, P, Dbuf, dQ, T, Hq, Hkv, scale);
+#define DQ(H, R) \
+    k_attn_bwd_dq<H, R><<<(int)b1, 256, 0, s>>>(dO, Q, K, V, P, st, Dbuf, dQ, T, Hq, Hkv, scale)
+    if (hd == 64) {
+        if (rc) DQ(64, true); else DQ(64, false);
+    } else {
+        if (rc) DQ(128, true); else DQ(128, false);
+    }
+#undef DQ
     if (timed)
-        kprof_end(KP_ATTN_BWD_DQ, s, 4.0 * hd * tri,
-                  4.0 * tri + 2.0 * bt * hd * (2.0 * Hq + 2.0 * Hkv) + 4.0 * bt * Hq,
-                  hd == 64 ? "void ta::k_attn_bwd_dq<64>" : "void ta::k_attn_bwd_dq<128>");
+        kprof_end(KP_ATTN_BWD_DQ, s, 4.0 * hd * tri + rf,
+                  pb + 2.0 * bt * hd * (2.0 * Hq + 2.0 * Hkv) + 4.0 * bt * Hq,
+                  hd == 64 ? (rc ? "void ta::k_attn_bwd_dq<64, true>" : "void ta::k_attn_bwd_dq<64, false>")
+                           : (rc ? "void ta::k_attn_bwd_dq<128, true>" : "void ta::k_attn_bwd_dq<128, false>"));
     timed = kprof_begin(KP_ATTN_BWD_DKV, s);
-    if (hd == 64)
-        k_attn_bwd_dkv<64><<<(int)b1, 256, 0, s>>>(dO, Q, V, P, Dbuf, part, T, Hq, Hkv);
-    else
-        k_attn_bwd_dkv<128><<<(int)b1, 256, 0, s>>>(dO, Q, V, P, Dbuf, part, T, Hq, Hkv);
+#define DKV(H, R) \
+    k_attn_bwd_dkv<H, R><<<(int)b1, 256, 0, s>>>(dO, Q, K, V, P, st, Dbuf, part, T, Hq, Hkv, scale)
+    if (hd == 64) {
+        if (rc) DKV(64, true); else DKV(64, false);
+    } else {
+        if (rc) DKV(128, true); else DKV(128, false);
+    }
+#undef DKV
     if (timed)
-        kprof_end(KP_ATTN_BWD_DKV, s, 6.0 * hd * tri,
-                  4.0 * tri + 2.0 * bt * hd * (2.0 * Hq + Hkv) + 4.0 * bt * Hq +
-                      8.0 * bt * Hq * hd,
-                  hd == 64 ? "void ta::k_attn_bwd_dkv<64>" : "void ta::k_attn_bwd_dkv<128>");
+        kprof_end(KP_ATTN_BWD_DKV, s, 6.0 * hd * tri + rf,
+                  pb + 2.0 * bt * hd * (2.0 * Hq + Hkv) + 4.0 * bt * Hq + 8.0 * bt * Hq * hd,
+                  hd == 64 ? (rc ? "void ta::k_attn_bwd_dkv<64, true>" : "void ta::k_attn_bwd_dkv<64, false>")
+                           : (rc ? "void ta::k_attn_bwd_dkv<128, true>" : "void ta::k_attn_bwd_dkv<128, false>"));
     int64_t n = (int64_t)B * T * Hkv * hd;
     int rb = (int)std::min<int64_t>((n + 255) / 256, 4096);
     k_attn_dkv_reduce<<<rb, 256, 0, s>>>(part, dK, dV, B, T, Hq, Hkv, hd, scale);
@@ -884,15 +1000,15 @@ extern "C" {
 
 int ta_sdpa_fwd(const uint16_t* Q, const uint16_t* K, const uint16_t* V, uint16_t* out,
                 float* attn_w, int B, int T, int Hq, int Hkv, int head_dim, void* stream) {
-    return ta::attn_fwd(Q, K, V, out, nullptr, attn_w, B, T, Hq, Hkv, head_dim, true,
+    return ta::attn_fwd(Q, K, V, out, nullptr, attn_w, nullptr, B, T, Hq, Hkv, head_dim, true,
                         (hipStream_t)stream);
 }
 
 int ta_sdpa_bwd(const uint16_t* dout, const uint16_t* Q, const uint16_t* K, const uint16_t* V,
                 const float* attn_w, uint16_t* dQ, uint16_t* dK, uint16_t* dV, int B, int T,
                 int Hq, int Hkv, int head_dim, void* stream) {
-    return ta::attn_bwd(dout, Q, K, V, attn_w, nullptr, dQ, dK, dV, B, T, Hq, Hkv, head_dim,
-                        nullptr, nullptr, (hipStream_t)stream);
+    return ta::attn_bwd(dout, Q, K, V, attn_w, nullptr, nullptr, dQ, dK, dV, B, T, Hq, Hkv,
+                        head_dim, nullptr, nullptr, (hipStream_t)stream);
 }
 
 }  // extern "C"

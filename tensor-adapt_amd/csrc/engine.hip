@@ -55,7 +55,7 @@ struct Layer {
     Pair pr[NPAIR];
     // forward cache
     bf16 *res_in, *xn, *Q, *K, *V, *ao, *res_mid, *xn2, *gate, *up, *act;
-    float *in_rms, *post_rms, *attn_w, *ao32;  // ao32: attention output in F32
+    float *in_rms, *post_rms, *attn_st, *ao32;  // attn_st: rows' (max, 1/sum); ao32: output in F32
 };
 
 struct Engine {
@@ -242,7 +242,9 @@ static int engine_alloc(Engine* e) {
         CK(alloc(e, &ly.K, (int64_t)BT * kvd, (p + "K").c_str(), 0));
         CK(alloc(e, &ly.V, (int64_t)BT * kvd, (p + "V").c_str(), 0));
         CK(alloc(e, &ly.ao, (int64_t)BT * qd, (p + "attn_out").c_str(), 0));
-        CK(alloc(e, &ly.attn_w, (int64_t)e->B * c.n_q * e->T * e->T, (p + "attn_w").c_str(), 1));
+        // the attention probabilities are not kept: the backward recomputes
+        // them from Q, K and each row's (max, 1/sum)
+        CK(alloc(e, &ly.attn_st, (int64_t)2 * e->B * c.n_q * e->T, (p + "attn_stats").c_str(), 1));
         CK(alloc(e, &ly.ao32, (int64_t)BT * qd, (p + "attn_out32").c_str(), 1));
         CK(alloc(e, &ly.res_mid, (int64_t)BT * H, (p + "res_mid").c_str(), 0));
         CK(alloc(e, &ly.post_rms, BT, (p + "post_rms").c_str(), 1));
@@ -555,11 +557,12 @@ static int forward(Engine* e) {
               ta_rope_fwd(ly.Q, e->B, e->T, c.n_q, c.head_dim, c.rope_theta, s));
         TIMED(TA_CAT_ELEMWISE, 0, dBT * kvd * 4,
               ta_rope_fwd(ly.K, e->B, e->T, c.n_kv, c.head_dim, c.rope_theta, s));
-        // the upper triangle of attn_w is never read by the backward: skip its fill
+        // sdpa_fwd (ops.cu:578-681) without the probabilities buffer: the
+        // rows' (max, 1/sum) are kept instead
         TIMED(TA_CAT_ATTN_FWD, 4.0 * tri * c.head_dim,
-              tri * 4 + dBT * (2.0 * qd + 2.0 * kvd) * 2 + dBT * qd * 4,
-              attn_fwd(ly.Q, ly.K, ly.V, ly.ao, ly.ao32, ly.attn_w, e->B, e->T, c.n_q, c.n_kv,
-                       c.head_dim, false, s));
+              dBT * (2.0 * qd + 2.0 * kvd) * 2 + dBT * qd * 4 + 8.0 * e->B * c.n_q * e->T,
+              attn_fwd(ly.Q, ly.K, ly.V, ly.ao, ly.ao32, nullptr, ly.attn_st, e->B, e->T, c.n_q,
+                       c.n_kv, c.head_dim, false, s));
         CK(lora_group_h(e, ly, {PO}, ly.ao, qd));
         {
             LoraEpi eo = fwd_epi(e, ly.pr[PO]);
@@ -666,11 +669,11 @@ static int backward(Engine* e) {
             CK(lora_group_bwd(e, ly, {PO}, ly.ao, qd, gos, &ep));
             CK(proj_bwd_x(e, ly.Wt[PO], e->g_res, e->dao, H, qd, 0.f, &ep));
         }
-        TIMED(TA_CAT_ATTN_BWD, 8.0 * tri * c.head_dim,
-              tri * 4 + dBT * (2.0 * qd + 2.0 * kvd) * 2 + dBT * (qd + 2.0 * kvd) * 2 +
-                  dBT * qd * 4,
-              attn_bwd(e->dao, ly.Q, ly.K, ly.V, ly.attn_w, ly.ao32, e->dQ, e->dK, e->dV, e->B,
-                       e->T, c.n_q, c.n_kv, c.head_dim, e->Dbuf, e->dkv_part, s));
+        TIMED(TA_CAT_ATTN_BWD, 12.0 * tri * c.head_dim,
+              16.0 * e->B * c.n_q * e->T + dBT * (2.0 * qd + 2.0 * kvd) * 2 +
+                  dBT * (qd + 2.0 * kvd) * 2 + dBT * qd * 4,
+              attn_bwd(e->dao, ly.Q, ly.K, ly.V, nullptr, ly.attn_st, ly.ao32, e->dQ, e->dK, e->dV,
+                       e->B, e->T, c.n_q, c.n_kv, c.head_dim, e->Dbuf, e->dkv_part, s));
         TIMED(TA_CAT_ELEMWISE, 0, dBT * qd * 4,
               ta_rope_bwd(e->dQ, e->B, e->T, c.n_q, c.head_dim, c.rope_theta, s));
         TIMED(TA_CAT_ELEMWISE, 0, dBT * kvd * 4,

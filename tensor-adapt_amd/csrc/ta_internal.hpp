@@ -88,11 +88,14 @@ int gemm_chain(int M, int N, const GemmSeg* sg, int ns, bf16* C, int64_t ldc, co
 // the groups' GEMMs in one launch over the N-concatenated tile grid
 int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const GemmGroup* gr,
                 int ng, hipStream_t s);
-int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* O32, float* P, int B,
-             int T, int Hq, int Hkv, int hd, bool zero_fill, hipStream_t s);
+// causal GQA attention; P [B*Hq, T, T] F32 probabilities, or (P NULL) only
+// the rows' (max, 1/sum) in stats [B*Hq*T] float pairs, from which the
+// backward recomputes P
+int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* O32, float* P,
+             float* stats, int B, int T, int Hq, int Hkv, int hd, bool zero_fill, hipStream_t s);
 int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const float* P,
-             const float* O32, bf16* dQ, bf16* dK, bf16* dV, int B, int T, int Hq, int Hkv, int hd,
-             float* Dbuf, float* part, hipStream_t s);
+             const float* stats, const float* O32, bf16* dQ, bf16* dK, bf16* dV, int B, int T,
+             int Hq, int Hkv, int hd, float* Dbuf, float* part, hipStream_t s);
 int transpose_bf16(const bf16* in, bf16* out, int64_t rows, int64_t cols, hipStream_t s);
 int fill_normal_bf16(bf16* out, int64_t n, uint64_t seed, uint64_t sid, float std, hipStream_t s);
 int fill_bf16(bf16* out, int64_t n, float v, hipStream_t s);
