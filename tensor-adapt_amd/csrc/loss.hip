@@ -1,10 +1,13 @@
 // loss.hip — per-token cross entropy with the reference's gradient
 // convention (src/backend/cuda/ops.cu:958-1020).
 //
-// One 512-thread block per token row.  Pass 1 is an online max/sum over the
-// row (each lane keeps a running max and a rescaled sum of exp, 16-byte
-// loads), so the row is read twice in total instead of the reference's
-// three times; pass 2 writes dlogits = bf16((softmax - onehot) / N).
+// k_cross_entropy_reg: one 1024-thread block per token row holds the whole
+// row in registers (16-byte loads, all issued at once: up to 20 x 8 values
+// per lane, V <= 163840), takes the block max, then the sum of exp, then
+// writes dlogits = bf16((softmax - onehot) / N): the logits are read once
+// and dlogits written once (the reference reads the row three times).
+// k_cross_entropy (one 512-thread block per row, online max/sum, two reads)
+// serves rows too long for registers and unaligned or ragged V.
 #include <float.h>
 
 #include "ta_common.hpp"
@@ -91,6 +94,101 @@ __global__ __launch_bounds__(512) void k_cross_entropy(const bf16* __restrict__ 
     }
 }
 
+// block-wide reductions over 16 waves, in wave order
+__device__ __forceinline__ float block_max16(float v, float* red) {
+    v = wave_max(v);
+    __syncthreads();  // red is free (a previous reduction's readers are done)
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int k = 1; k < 16; k++) r = fmaxf(r, red[k]);
+    return r;
+}
+__device__ __forceinline__ float block_sum16(float v, float* red) {
+    v = wave_sum(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int k = 1; k < 16; k++) r += red[k];
+    return r;
+}
+
+template <int CPT>  // 16-byte chunks per lane: V <= 8 * 1024 * CPT, V % 8 == 0
+__global__ __launch_bounds__(1024) void k_cross_entropy_reg(const bf16* __restrict__ logits,
+                                                            const int32_t* __restrict__ targets,
+                                                            float* __restrict__ loss,
+                                                            bf16* __restrict__ dlogits, int V,
+                                                            float inv_N) {
+    __shared__ float red[16], tls;
+    const int64_t n = blockIdx.x;
+    const bf16x8v* L = (const bf16x8v*)(logits + n * (int64_t)V);
+    const int nv = V >> 3, tgt = targets[n];
+    bf16x8v r[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; k++) {
+        const int c = threadIdx.x + 1024 * k;
+        if (c < nv) r[k] = L[c];
+    }
+    float m = -FLT_MAX;
+#pragma unroll
+    for (int k = 0; k < CPT; k++) {
+        const int c = threadIdx.x + 1024 * k;
+        if (c < nv) {
+            float f[8];
+            unpack8(r[k], f);
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                m = fmaxf(m, f[e]);
+                // the target's logit, from the lane that holds it (dlogits may
+                // overwrite the row in place once the sums are known)
+                if (c * 8 + e == tgt) tls = f[e];
+            }
+        }
+    }
+    // exp as one v_exp_f32 of x log2(e) - M log2(e) (results below the
+    // normal range flush to zero, as the reference's fast-math __expf does)
+    const float M = block_max16(m, red);
+    const float M2 = M * kLog2e;
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < CPT; k++) {
+        if (threadIdx.x + 1024 * k < nv) {
+            float f[8];
+            unpack8(r[k], f);
+#pragma unroll
+            for (int e = 0; e < 8; e++) sum += __builtin_amdgcn_exp2f(fmaf(f[e], kLog2e, -M2));
+        }
+    }
+    const float S = block_sum16(sum, red);
+    const float log_sum = logf(S) + M;
+    if (threadIdx.x == 0) {
+        // a target outside [0, V) reads nothing (the reference would read out
+        // of bounds for tgt >= V; ids come from a vocab-sized tokenizer)
+        const float tl = (tgt >= 0 && tgt < V) ? tls : 0.f;
+        loss[n] = -(tl - log_sum);
+    }
+    if (!dlogits) return;
+    bf16x8v* dL = (bf16x8v*)(dlogits + n * (int64_t)V);
+    const float ls2 = log_sum * kLog2e;
+#pragma unroll
+    for (int k = 0; k < CPT; k++) {
+        const int c = threadIdx.x + 1024 * k;
+        if (c < nv) {
+            float f[8];
+            unpack8(r[k], f);
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float p = __builtin_amdgcn_exp2f(fmaf(f[e], kLog2e, -ls2));
+                f[e] = (p - (float)(c * 8 + e == tgt)) * inv_N;
+            }
+            dL[c] = pack8(f);
+        }
+    }
+}
+
 }  // namespace ta
 
 using namespace ta;
@@ -104,9 +202,21 @@ extern "C" int ta_cross_entropy_fwd(const uint16_t* logits, const int32_t* targe
     // divisor = number of rows, masked rows included (gridDim.x in ops.cu:1005)
     float inv_N = 1.f / (float)N;
     bool vec = (V & 7) == 0 && (((uintptr_t)logits | (uintptr_t)dlogits) & 15u) == 0;
-    if (vec)
+    const int cpt = (V / 8 + 1023) / 1024;
+    // dlogits may overwrite logits in place: every lane reads its whole row
+    // share before the block's first barrier, and writes only its own chunks
+    // (up to 20 chunks per lane fit the 128 registers of a 16-wave block)
+    if (vec && cpt <= 20) {
+#define CE(C) k_cross_entropy_reg<C><<<N, 1024, 0, s>>>(logits, targets, loss_out, dlogits, V, inv_N)
+        if (cpt <= 4) CE(4);
+        else if (cpt <= 8) CE(8);
+        else if (cpt <= 16) CE(16);
+        else CE(20);
+#undef CE
+    } else if (vec) {
         k_cross_entropy<true><<<N, 512, 0, s>>>(logits, targets, loss_out, dlogits, V, inv_N);
-    else
+    } else {
         k_cross_entropy<false><<<N, 512, 0, s>>>(logits, targets, loss_out, dlogits, V, inv_N);
+    }
     return check_launch("cross_entropy_fwd");
 }

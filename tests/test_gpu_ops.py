@@ -118,14 +118,19 @@ def test_rope(B, T, H, hd, inverse):
 
 
 # ── cross entropy ─────────────────────────────────────────────────────────
-@pytest.mark.parametrize("N,V", [(48, 151936), (7, 1001)])
-def test_cross_entropy(N, V):
+# register-resident rows (V = 151936, 2048), the two-read kernel for rows
+# too long for registers (200000) and ragged V (1001); in place as the
+# engine calls it (dlogits over the logits)
+@pytest.mark.parametrize("N,V,inplace", [(48, 151936, 0), (48, 151936, 1), (9, 2048, 1),
+                                         (6, 200000, 1), (7, 1001, 0)])
+def test_cross_entropy(N, V, inplace):
     logits = rbf(N, V, scale=2.0)
     tgt = RNG.integers(0, V, N).astype(np.int32)
     tgt[::3] = -1
     loss = torch.empty(N, dtype=torch.float32, device=DEV)
-    dl = empty_bf16(N, V)
-    call("ta_cross_entropy_fwd", P(dev(logits)), P(dev(tgt)), P(loss), P(dl), N, V, S())
+    lg = dev(logits)
+    dl = lg if inplace else empty_bf16(N, V)
+    call("ta_cross_entropy_fwd", P(lg), P(dev(tgt)), P(loss), P(dl), N, V, S())
     rl, rd = O.cross_entropy(logits, tgt)
     assert np.allclose(host(loss), rl, rtol=1e-5, atol=1e-5)
     assert_bf16_close(host(dl), rd, what="dlogits")
