@@ -539,8 +539,11 @@ static int forward(Engine* e) {
     for (int l = 0; l < c.layers; l++) {
         Layer& ly = e->L[l];
         bf16* res_out = (l + 1 < c.layers) ? e->L[l + 1].res_in : e->x_final;
-        TIMED(TA_CAT_NORM, 0, nrm_b,
-              ta_rms_norm_fwd(ly.res_in, ly.in_norm, ly.xn, ly.in_rms, 1, BT, H, c.rms_eps, s));
+        // (the input norm of layers after the first runs fused with the
+        // previous layer's residual add, below)
+        if (l == 0)
+            TIMED(TA_CAT_NORM, 0, nrm_b,
+                  ta_rms_norm_fwd(ly.res_in, ly.in_norm, ly.xn, ly.in_rms, 1, BT, H, c.rms_eps, s));
         CK(lora_group_h(e, ly, {PQ, PK, PV}, ly.xn, H));
         {
             // q, k and v projections (qwen2.cu:21-30, each with its bias and
@@ -568,11 +571,10 @@ static int forward(Engine* e) {
             LoraEpi eo = fwd_epi(e, ly.pr[PO]);
             CK(proj_fwd(e, ly.W[PO], ly.ao, e->tmpH, qd, H, nullptr, &eo));
         }
-        TIMED(TA_CAT_ELEMWISE, 0, dBT * H * 6,
-              add2_bf16(ly.res_mid, ly.res_in, e->tmpH, (int64_t)BT * H, s));
-        TIMED(TA_CAT_NORM, 0, nrm_b,
-              ta_rms_norm_fwd(ly.res_mid, ly.post_norm, ly.xn2, ly.post_rms, 1, BT, H, c.rms_eps,
-                              s));
+        // res_mid = bf16(res_in + o_proj) and its post-attention norm, one pass
+        TIMED(TA_CAT_NORM, 0, nrm_b + dBT * H * 4,
+              rms_fwd_res(ly.res_in, e->tmpH, ly.res_mid, ly.post_norm, ly.xn2, ly.post_rms, BT, H,
+                          c.rms_eps, s));
         CK(lora_group_h(e, ly, {PG, PU}, ly.xn2, H));
         {
             // gate and up projections (qwen2.cu:21-30, each with its LoRA
@@ -590,11 +592,14 @@ static int forward(Engine* e) {
             LoraEpi ed = fwd_epi(e, ly.pr[PD]);
             CK(proj_fwd(e, ly.W[PD], ly.act, e->tmpH, I, H, nullptr, &ed));
         }
-        TIMED(TA_CAT_ELEMWISE, 0, dBT * H * 6,
-              add2_bf16(res_out, ly.res_mid, e->tmpH, (int64_t)BT * H, s));
+        // res_out = bf16(res_mid + down_proj) and the next norm (the next
+        // layer's input norm, or the final norm), one pass
+        const bool last = l + 1 == c.layers;
+        TIMED(TA_CAT_NORM, 0, nrm_b + dBT * H * 4,
+              rms_fwd_res(ly.res_mid, e->tmpH, res_out, last ? e->final_norm : e->L[l + 1].in_norm,
+                          last ? e->xfn : e->L[l + 1].xn, last ? e->final_rms : e->L[l + 1].in_rms,
+                          BT, H, c.rms_eps, s));
     }
-    TIMED(TA_CAT_NORM, 0, nrm_b,
-          ta_rms_norm_fwd(e->x_final, e->final_norm, e->xfn, e->final_rms, 1, BT, H, c.rms_eps, s));
     // LM head (qwen2.cu:163-175), tied to the embedding when c.tie
     TIMED(TA_CAT_LMHEAD, gflops(BT, e->V, H), gbytes(BT, e->V, H, 2, 2, false),
           gemm_dispatch(true, true, BT, e->V, H, 1.f, e->xfn, H, e->lm, H, 0.f, e->logits, e->V,
@@ -657,11 +662,10 @@ static int backward(Engine* e) {
             TIMED(TA_CAT_GEMM_DX, 2.0 * gflops(BT, H, I), 2.0 * gbytes(BT, H, I, 2, 2, false),
                   gemm_chain(BT, H, sg, 2, e->dxn2, H, ep.n ? &ep : nullptr, s));
         }
-        TIMED(TA_CAT_NORM, 0, nrm_b,
-              ta_rms_norm_bwd(e->dxn2, ly.res_mid, ly.post_norm, ly.post_rms, e->tmpH, nullptr, 1,
-                              BT, H, c.rms_eps, s));
-        TIMED(TA_CAT_ELEMWISE, 0, dBT * H * 6,
-              ta_add_inplace(e->g_res, e->tmpH, (int64_t)BT * H, s));
+        // grad += bf16(rms_norm_bwd(dx_normed2)), one pass
+        TIMED(TA_CAT_NORM, 0, nrm_b + dBT * H * 2,
+              rms_bwd_acc(e->dxn2, ly.res_mid, ly.post_norm, ly.post_rms, e->g_res, e->tmpH, BT, H,
+                          s));
         // attention (qwen2.cu:250-304)
         {
             const bf16* gos[1] = {e->g_res};
@@ -694,11 +698,9 @@ static int backward(Engine* e) {
         // g = dx_attn_in of this layer
         TIMED(TA_CAT_CENTROID, 0, dBT * H * 4,
               ta_centroid_accumulate_bf16(ly.xn, e->dxn, BT, H, e->cacc, s));
-        TIMED(TA_CAT_NORM, 0, nrm_b,
-              ta_rms_norm_bwd(e->dxn, ly.res_in, ly.in_norm, ly.in_rms, e->tmpH, nullptr, 1, BT, H,
-                              c.rms_eps, s));
-        TIMED(TA_CAT_ELEMWISE, 0, dBT * H * 6,
-              ta_add_inplace(e->g_res, e->tmpH, (int64_t)BT * H, s));
+        // grad += bf16(rms_norm_bwd(dx_normed)), one pass
+        TIMED(TA_CAT_NORM, 0, nrm_b + dBT * H * 2,
+              rms_bwd_acc(e->dxn, ly.res_in, ly.in_norm, ly.in_rms, e->g_res, e->tmpH, BT, H, s));
     }
     // every gA / gB += scale * (its ordered partial sum), one launch
     if (e->wg_cursor != e->wg_plan.size())

@@ -12,6 +12,7 @@
 #include <mutex>
 #include <vector>
 
+#include "ta_backend.h"
 #include "ta_internal.hpp"
 
 namespace ta {
@@ -21,12 +22,16 @@ constexpr int kMaxChunks = 8;  // 8 chunks x 8 elems x 64 lanes = D <= 4096 in r
 // ── RMSNorm forward — ops.cu:59-97 ──────────────────────────────────────
 // inv = 1/sqrt(mean(x^2) + eps) is stored (the reference stores the inverse,
 // ops.cu:84-86); out = bf16(x * inv * w).
-template <int MAXC>
+// RES: the normalised row is x = bf16(x + x2), the residual add of
+// qwen2.cu (add2, ops.cu:1087-1094) fused in; x is also written to xs.
+template <int MAXC, bool RES = false>
 __global__ __launch_bounds__(256) void k_rms_fwd_v8(const bf16* __restrict__ x,
                                                     const bf16* __restrict__ w,
                                                     bf16* __restrict__ out,
                                                     float* __restrict__ rms_out, int64_t rows,
-                                                    int D, float eps) {
+                                                    int D, float eps,
+                                                    const bf16* __restrict__ x2 = nullptr,
+                                                    bf16* __restrict__ xs = nullptr) {
     int lane = threadIdx.x & 63;
     int64_t row = blockIdx.x * 4ll + (threadIdx.x >> 6);
     if (row >= rows) return;
@@ -39,6 +44,15 @@ __global__ __launch_bounds__(256) void k_rms_fwd_v8(const bf16* __restrict__ x,
         int c = lane + 64 * j;
         if (c < nc) {
             v[j] = xr[c];
+            if constexpr (RES) {
+                float a[8], b[8];
+                unpack8(v[j], a);
+                unpack8(((const bf16x8v*)(x2 + row * D))[c], b);
+#pragma unroll
+                for (int e = 0; e < 8; e++) a[e] = a[e] + b[e];
+                v[j] = pack8(a);
+                ((bf16x8v*)(xs + row * D))[c] = v[j];
+            }
             float f[8];
             unpack8(v[j], f);
 #pragma unroll
@@ -88,7 +102,9 @@ __global__ __launch_bounds__(256) void k_rms_fwd_scalar(const bf16* __restrict__
 // With dw requested, each block folds its rows' dy*xhat into a per-block
 // partial row (fixed order: waves, then rows) and a second kernel sums the
 // partials in block order, so dw is deterministic.
-template <int MAXC, bool DW>
+// ACC: dx is not stored but added into the residual gradient,
+// dx_acc = bf16(dx_acc + bf16(dx)) (add_inplace, ops.cu:1087-1094, fused in).
+template <int MAXC, bool DW, bool ACC = false>
 __global__ __launch_bounds__(256) void k_rms_bwd_v8(const bf16* __restrict__ dy,
                                                     const bf16* __restrict__ x,
                                                     const bf16* __restrict__ w,
@@ -141,6 +157,13 @@ __global__ __launch_bounds__(256) void k_rms_bwd_v8(const bf16* __restrict__ dy,
                     float xh = b[e] * inv;
                     o[e] = inv * (g[e] * a[e] - xh * corr);
                     if (DW) dwacc[j * 8 + e] += a[e] * xh;
+                }
+                if constexpr (ACC) {
+                    float q[8];
+                    unpack8(pack8(o), o);
+                    unpack8(dxr[c], q);
+#pragma unroll
+                    for (int e = 0; e < 8; e++) o[e] = q[e] + o[e];
                 }
                 dxr[c] = pack8(o);
             }
@@ -320,6 +343,37 @@ __global__ void k_rope_scalar(bf16* __restrict__ x, int64_t rows, int T, int H, 
 using namespace ta;
 
 static inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+namespace ta {
+// xs = bf16(a + b); out = rms_norm(xs) (add2 then rms_norm_fwd in one pass)
+int rms_fwd_res(const bf16* a, const bf16* b, bf16* xs, const bf16* w, bf16* out, float* rms_out,
+                int64_t rows, int D, float eps, hipStream_t s) {
+    if (rows == 0) return 0;
+    if (!((D & 7) == 0 && D <= 64 * 8 * kMaxChunks && al16(a) && al16(b) && al16(xs) && al16(w) &&
+          al16(out))) {
+        if (int rc = add2_bf16(xs, a, b, rows * D, s)) return rc;
+        return ta_rms_norm_fwd(xs, w, out, rms_out, 1, (int)rows, D, eps, s);
+    }
+    k_rms_fwd_v8<kMaxChunks, true><<<(int)((rows + 3) / 4), 256, 0, s>>>(a, w, out, rms_out, rows,
+                                                                       D, eps, b, xs);
+    return check_launch("rms_fwd_res");
+}
+// acc = bf16(acc + bf16(rms_norm_bwd(dy))) (rms_norm_bwd then add_inplace in
+// one pass); tmp: [rows x D] scratch for shapes the fused kernel does not take
+int rms_bwd_acc(const bf16* dy, const bf16* x, const bf16* w, const float* rms, bf16* acc,
+                bf16* tmp, int64_t rows, int D, hipStream_t s) {
+    if (rows == 0) return 0;
+    if (!((D & 7) == 0 && D <= 64 * 8 * kMaxChunks && al16(dy) && al16(x) && al16(w) &&
+          al16(acc))) {
+        if (int rc = ta_rms_norm_bwd(dy, x, w, rms, tmp, nullptr, 1, (int)rows, D, 0.f, s))
+            return rc;
+        return ta_add_inplace(acc, tmp, rows * D, s);
+    }
+    k_rms_bwd_v8<kMaxChunks, false, true><<<(int)((rows + 3) / 4), 256, 0, s>>>(
+        dy, x, w, rms, acc, nullptr, rows, D, 4);
+    return check_launch("rms_bwd_acc");
+}
+}  // namespace ta
 
 extern "C" {
 

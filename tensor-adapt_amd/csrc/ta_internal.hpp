@@ -101,6 +101,12 @@ int fill_normal_bf16(bf16* out, int64_t n, uint64_t seed, uint64_t sid, float st
 int fill_bf16(bf16* out, int64_t n, float v, hipStream_t s);
 int kaiming_init(float* a32, bf16* a16, int64_t n, int in_dim, hipStream_t s);
 int add2_bf16(bf16* out, const bf16* a, const bf16* b, int64_t n, hipStream_t s);
+// xs = bf16(a + b), then the RMSNorm forward of xs (out, inverse rms), in one pass
+int rms_fwd_res(const bf16* a, const bf16* b, bf16* xs, const bf16* w, bf16* out, float* rms_out,
+                int64_t rows, int D, float eps, hipStream_t s);
+// acc = bf16(acc + bf16(RMSNorm backward dx)), in one pass (tmp: fallback scratch)
+int rms_bwd_acc(const bf16* dy, const bf16* x, const bf16* w, const float* rms, bf16* acc,
+                bf16* tmp, int64_t rows, int D, hipStream_t s);
 int mask_targets_dev(const int32_t* in, const int32_t* tgt_in, int32_t* tgt, int B, int T,
                      hipStream_t s);
 int lora_skinny_nt(const bf16* X, int64_t ldx, int M, int K, int r, const bf16* const* Y,
