@@ -52,6 +52,7 @@ struct Layer {
     bf16 *in_norm = nullptr, *post_norm = nullptr, *bias[3] = {nullptr, nullptr, nullptr};
     bf16* W[NPAIR] = {};
     bf16* Wt[NPAIR] = {};
+    bf16* Wgu = nullptr;  // gate/up weights interleaved in 128-row blocks (gemm_swiglu)
     Pair pr[NPAIR];
     // forward cache
     bf16 *res_in, *xn, *Q, *K, *V, *ao, *res_mid, *xn2, *gate, *up, *act;
@@ -235,6 +236,7 @@ static int engine_alloc(Engine* e) {
             CK(alloc(e, &ly.Wt[q], (int64_t)outs[q] * ins[q], "wt"));
             if (ly.pr[q].on) CK(alloc(e, &ly.pr[q].h, (int64_t)BT * r, "lora.h"));
         }
+        if (I % 128 == 0) CK(alloc(e, &ly.Wgu, (int64_t)2 * I * H, "wgu"));
         CK(alloc(e, &ly.res_in, (int64_t)BT * H, (p + "res_in").c_str(), 0));
         CK(alloc(e, &ly.in_rms, BT, (p + "in_rms").c_str(), 1));
         CK(alloc(e, &ly.xn, (int64_t)BT * H, (p + "x_normed").c_str(), 0));
@@ -578,15 +580,14 @@ static int forward(Engine* e) {
         CK(lora_group_h(e, ly, {PG, PU}, ly.xn2, H));
         {
             // gate and up projections (qwen2.cu:21-30, each with its LoRA
-            // delta) in one launch over both weight matrices
+            // delta) and act = silu_mul_fwd(gate, up) (ops.cu:913-923) in one
+            // launch over the interleaved gate/up weights
             LoraEpi eg = fwd_epi(e, ly.pr[PG]), eu = fwd_epi(e, ly.pr[PU]);
-            const GemmGroup gr[2] = {{I, ly.W[PG], ly.gate, I, nullptr, &eg},
-                                     {I, ly.W[PU], ly.up, I, nullptr, &eu}};
-            TIMED(TA_CAT_GEMM_FWD, 2.0 * gflops(BT, I, H), 2.0 * gbytes(BT, I, H, 2, 2, false),
-                  gemm_groups(BT, H, ly.xn2, H, H, gr, 2, s));
+            TIMED(TA_CAT_GEMM_FWD, 2.0 * gflops(BT, I, H),
+                  2.0 * gbytes(BT, I, H, 2, 2, false) + dBT * I * 2,
+                  gemm_swiglu(BT, H, ly.xn2, H, ly.Wgu, ly.W[PG], ly.W[PU], ly.gate, ly.up, ly.act,
+                              I, &eg, &eu, s));
         }
-        TIMED(TA_CAT_ELEMWISE, 0, dBT * I * 6,
-              ta_silu_mul_fwd(ly.gate, ly.up, ly.act, (int64_t)BT * I, s));
         CK(lora_group_h(e, ly, {PD}, ly.act, I));
         {
             LoraEpi ed = fwd_epi(e, ly.pr[PD]);
@@ -825,8 +826,16 @@ static bf16** weight_slot(Engine* e, const std::string& name, int64_t* n, int* l
 // after a projection (or the LM head / embedding) changes: refresh W^T
 static int refresh_transpose(Engine* e, const std::string& name, int layer, int proj) {
     if (proj >= 0) {
-        Pair& p = e->L[layer].pr[proj];
-        return transpose_bf16(e->L[layer].W[proj], e->L[layer].Wt[proj], p.out, p.in, e->s);
+        Layer& ly = e->L[layer];
+        Pair& p = ly.pr[proj];
+        if ((proj == PG || proj == PU) && ly.Wgu) {
+            // 128-row blocks of gate and up alternate in Wgu
+            const size_t blk = (size_t)128 * p.in * sizeof(bf16);
+            TA_HIP(hipMemcpy2DAsync(ly.Wgu + (proj == PU ? (size_t)128 * p.in : 0), 2 * blk,
+                                    ly.W[proj], blk, blk, p.out / 128, hipMemcpyDeviceToDevice,
+                                    e->s));
+        }
+        return transpose_bf16(ly.W[proj], ly.Wt[proj], p.out, p.in, e->s);
     }
     if (name == "model.embed_tokens.weight" && e->mc.tie)
         return transpose_bf16(e->embed, e->embedT, e->V, e->H, e->s);

@@ -28,6 +28,7 @@
 #include <algorithm>
 #include <type_traits>
 
+#include "ta_backend.h"
 #include "ta_internal.hpp"
 
 namespace ta {
@@ -859,7 +860,13 @@ __device__ __forceinline__ void round_acc(floatx16 (&acc)[TM][TN]) {
             for (int r = 0; r < 16; r++) acc[i][j][r] = bf2f(f2bf(acc[i][j][r]));
 }
 
-template <int BN, int WMW, int WNW, bool CHAIN>  // CHAIN: K segments (a.nseg > 1)
+// CHAIN: K segments (a.nseg > 1).  SWIGLU: Y is the gate/up weight pair
+// interleaved in blocks of 128 rows, so tile tn holds gate and up columns
+// [128 tn, 128 tn + 128); gate waves (wn < 2) write gate, up waves up, each
+// with its pair's LoRA delta, and then every gate/up wave pair writes
+// act = silu(gate) * up from the two staged BF16 halves (gC[0..2] = gate,
+// up, act; gu/gv[0..1] the pairs' h and B; gN[0] = gldc[0] = I).
+template <int BN, int WMW, int WNW, bool CHAIN, bool SWIGLU = false>
 __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmArgs& a0) {
     constexpr int NS = 4, BM = 256, NW = WMW * WNW;
     constexpr int WTM = BM / WMW, WTN = BN / WNW;
@@ -874,7 +881,9 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
     // epilogue operands staged at the start: rank-16 LoRA U/V rows of the
     // first LP pairs and 512 bias entries (one DMA instruction)
     constexpr int LP = BN == 256 ? 1 : 3;
-    __shared__ __attribute__((aligned(16))) bf16 sLU[LP * BM * 16], sLV[LP * BN * 16], sB[512];
+    constexpr int LPU = SWIGLU ? 2 : LP;  // U rows: both pairs' h in the SwiGLU form
+    static_assert(!SWIGLU || (BN == 256 && WNW == 4 && WMW == 2), "SwiGLU tile layout");
+    __shared__ __attribute__((aligned(16))) bf16 sLU[LPU * BM * 16], sLV[LP * BN * 16], sB[512];
 
     int tm_i, tn_i;
     big_tile(blockIdx.x, a0.tiles_m, a0.tiles_n, tm_i, tn_i);
@@ -901,7 +910,28 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
     // for stage 0 covers them; the main loop's barriers publish them
     const bool lds_lora = a.lora_n > 0 && a.lora_r == 16;
     const bool lds_bias = a.bias != nullptr && (a.N & 7) == 0 && a.N >= 8;
-    if (lds_lora) {
+    if (SWIGLU && lds_lora) {
+        // U: gate then up h rows of the tile; V: gate B rows of columns
+        // [128 tn, +128) then the up pair's (instruction q: 32 rows x 32 B)
+        constexpr int UI = BM / 32, VI = BN / 32;
+        const int cb = 128 * tn_i;
+        for (int q = w; q < 2 * UI + VI; q += NW) {
+            const bf16* src;
+            bf16* dst;
+            if (q < 2 * UI) {
+                const int pp = q / UI, qi = q % UI;
+                const int row = min(m0 + 32 * qi + (lane >> 1), a.M - 1);
+                src = (pp ? a0.gu[1] : a0.gu[0]) + (int64_t)row * 16 + 8 * (lane & 1);
+                dst = sLU + (pp * BM + 32 * qi) * 16;
+            } else {
+                const int qi = q - 2 * UI, r = 32 * qi + (lane >> 1);
+                src = (qi < VI / 2 ? a0.gv[0] : a0.gv[1]) + (int64_t)(cb + (r & 127)) * 16 +
+                      8 * (lane & 1);
+                dst = sLV + 32 * qi * 16;
+            }
+            __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr_t)dst, 16, 0, 0);
+        }
+    } else if (lds_lora) {
         // instruction q moves 32 rows x 32 bytes: lane l -> row l/2, half l%2
         constexpr int UI = BM / 32, VI = BN / 32;
         for (int q = w; q < LP * (UI + VI); q += NW) {
@@ -1025,11 +1055,49 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
         wb0 = b;
         wb1 = b + 64 * WTN;
     }
-    pipe_half_epilogue<TM, TN, WTN, 0, LP>(acc, a, (bf16*)a.C, m0 + wm * WTM, n0 + wn * WTN, lane, wb0, lu,
-                                           lv, lb, wm * WTM, wn * WTN, BM, BN);
-    if constexpr (TM == 4)
-        pipe_half_epilogue<TM, TN, WTN, 2, LP>(acc, a, (bf16*)a.C, m0 + wm * WTM + 64, n0 + wn * WTN, lane,
-                                               wb1, lu, lv, lb, wm * WTM + 64, wn * WTN, BM, BN);
+    if constexpr (SWIGLU) {
+        // gate waves write gate, up waves up (I columns, row stride I), each
+        // with its own pair's h rows
+        const bool upw = wn >= 2;
+        GemmArgs ae = a;
+        ae.N = a0.gN[0];
+        ae.ldc = a0.gldc[0];
+        bf16* Cw = (bf16*)(upw ? a0.gC[1] : a0.gC[0]);
+        const int cg = 128 * tn_i + 64 * (wn & 1);
+        const bf16* luw = lu ? lu + (upw ? BM * 16 : 0) : nullptr;
+        pipe_half_epilogue<TM, TN, WTN, 0, LP>(acc, ae, Cw, m0 + wm * WTM, cg, lane, wb0, luw, lv,
+                                               nullptr, wm * WTM, wn * WTN, BM, BN);
+        pipe_half_epilogue<TM, TN, WTN, 2, LP>(acc, ae, Cw, m0 + wm * WTM + 64, cg, lane, wb1, luw,
+                                               lv, nullptr, wm * WTM + 64, wn * WTN, BM, BN);
+        __syncthreads();  // the partner wave's halves are staged
+        // act = silu(gate) * up: the gate wave takes the first 64 rows, the
+        // up wave (w ^ 2) the second, each from both waves' staging
+        const int pw = w ^ 2;
+        bf16* pb = pw == 0 ? sX0 : pw == 1 ? sX1 : pw == 2 ? sX2 : pw == 3 ? sX3
+                 : pw == 4 ? sY0 : pw == 5 ? sY1 : pw == 6 ? sY2 : sY3;
+        const bf16* gst = upw ? pb + 64 * WTN : wb0;
+        const bf16* ust = upw ? wb1 : pb;
+        const int rb = m0 + wm * WTM + (upw ? 64 : 0);
+        bf16* actp = (bf16*)a0.gC[2];
+        const int64_t I = a0.gldc[0];
+        for (int q = lane; q < 64 * (WTN / 8); q += 64) {
+            const int row = q / (WTN / 8), ch = q % (WTN / 8);
+            if (rb + row >= a.M) continue;
+            float g[8], u[8], o[8];
+            unpack8(*(const bf16x8v*)(gst + row * WTN + 8 * ch), g);
+            unpack8(*(const bf16x8v*)(ust + row * WTN + 8 * ch), u);
+#pragma unroll
+            for (int e = 0; e < 8; e++) o[e] = silu_mul_f(g[e], u[e]);
+            *(bf16x8v*)(actp + (int64_t)(rb + row) * I + cg + 8 * ch) = pack8(o);
+        }
+    } else {
+        pipe_half_epilogue<TM, TN, WTN, 0, LP>(acc, a, (bf16*)a.C, m0 + wm * WTM, n0 + wn * WTN,
+                                               lane, wb0, lu, lv, lb, wm * WTM, wn * WTN, BM, BN);
+        if constexpr (TM == 4)
+            pipe_half_epilogue<TM, TN, WTN, 2, LP>(acc, a, (bf16*)a.C, m0 + wm * WTM + 64,
+                                                   n0 + wn * WTN, lane, wb1, lu, lv, lb,
+                                                   wm * WTM + 64, wn * WTN, BM, BN);
+    }
 }
 
 template <int BN, int WMW, int WNW>
@@ -1041,6 +1109,11 @@ template <int BN, int WMW, int WNW>
 __global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
     WMW * WNW / 4, WMW * WNW / 4))) void k_gemm_pipe_chain(GemmArgs a) {
     gemm_pipe_body<BN, WMW, WNW, true>(a);
+}
+template <int BN, int WMW, int WNW>
+__global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
+    WMW * WNW / 4, WMW * WNW / 4))) void k_gemm_pipe_swiglu(GemmArgs a) {
+    gemm_pipe_body<BN, WMW, WNW, false, true>(a);
 }
 
 // Kernel variants of the large GEMMs (ta_gemm_variant): 0 picks k_gemm_pipe
@@ -1504,6 +1577,69 @@ int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const Gem
         kprof_end(kid, s, fl, by, big_name(variant));
     }
     return check_launch("gemm_groups");
+}
+
+// gate = bf16(X Wg^T) + LoRA delta, up likewise, act = bf16(silu(gate) up)
+// (qwen2.cu:21-30 twice, then silu_mul_fwd, ops.cu:913-923) as ONE launch
+// over Wgu, the gate/up weights interleaved in blocks of 128 rows
+// ([Wg rows 0..127; Wu rows 0..127; Wg rows 128..255; ...], [2I x K]): the
+// act pass reads the BF16 gate/up tiles from LDS instead of HBM.  The
+// LoRA pairs are both on (rank 16) or both off.  Other shapes run as the
+// grouped launch plus silu_mul_fwd.
+int gemm_swiglu(int M, int K, const bf16* X, int64_t ldx, const bf16* Wgu, const bf16* Wg,
+                const bf16* Wu, bf16* gate, bf16* up, bf16* act, int I, const LoraEpi* lg,
+                const LoraEpi* lu, hipStream_t s) {
+    const bool on = lg && lg->n > 0;
+    const bool lora_ok = on ? (lu && lu->n == 1 && lg->n == 1 && lg->r == 16 && lu->r == 16 &&
+                               lg->delta == lu->delta && lg->s == lu->s && lg->ldu[0] == 16 &&
+                               lu->ldu[0] == 16)
+                            : !(lu && lu->n > 0);
+    const int tiles = ((M + 255) / 256) * (2 * I / 256);
+    const bool ok = Wgu && lora_ok && (g_big_variant == 0 || g_big_variant == 16) && M >= 1024 &&
+                    I % 128 == 0 && 2 * I >= 1024 && K % BK == 0 && al16(X) && ldx % 8 == 0 &&
+                    al16(Wgu) && al16(gate) && al16(up) && al16(act) && I % 8 == 0 &&
+                    (tiles >= 192 || K / BK < 32);
+    if (!ok) {
+        const GemmGroup gr[2] = {{I, Wg, gate, I, nullptr, lg}, {I, Wu, up, I, nullptr, lu}};
+        if (int rc = gemm_groups(M, K, X, ldx, K, gr, 2, s)) return rc;
+        return ta_silu_mul_fwd(gate, up, act, (int64_t)M * I, s);
+    }
+    GemmArgs a{};
+    a.M = M;
+    a.N = 2 * I;
+    a.K = K;
+    a.X = X;
+    a.ldx = ldx;
+    a.Y = Wgu;
+    a.ldy = K;
+    a.C = gate;
+    a.ldc = I;
+    a.alpha = 1.f;
+    a.beta = 0.f;
+    a.k_per_split = K;
+    a.tiles_m = (M + 255) / 256;
+    a.tiles_n = 2 * I / 256;
+    a.ngroups = 1;
+    a.nseg = 1;
+    a.gN[0] = I;
+    a.gldc[0] = I;
+    a.gC[0] = gate;
+    a.gC[1] = up;
+    a.gC[2] = act;
+    if (on) {
+        a.lora_n = 1;
+        a.lora_r = 16;
+        a.lora_delta = lg->delta ? 1 : 0;
+        a.lora_s = lg->s;
+        a.lora_ldu[0] = 16;
+        a.gu[0] = lg->u[0];
+        a.gu[1] = lu->u[0];
+        a.gv[0] = lg->v_nk[0];
+        a.gv[1] = lu->v_nk[0];
+    }
+    // (not under the kernel-level timer: its ids cover k_gemm_pipe launches only)
+    k_gemm_pipe_swiglu<256, 2, 4><<<tiles, 512, 0, s>>>(a);
+    return check_launch("gemm_swiglu");
 }
 
 // F32 -> BF16 staging for gemm_f32 operands (the LoRA path feeds it values

@@ -85,6 +85,12 @@ struct GemmSeg {
 // one launch over the concatenated K (rounded to BF16 between the GEMMs)
 int gemm_chain(int M, int N, const GemmSeg* sg, int ns, bf16* C, int64_t ldc, const LoraEpi* lora,
                hipStream_t s);
+// gate/up projections (+ LoRA deltas) and act = silu(gate) up in one launch
+// over Wgu, the gate/up weights interleaved in 128-row blocks ([2I x K]);
+// falls back to gemm_groups + silu_mul_fwd for other shapes (Wgu may be NULL)
+int gemm_swiglu(int M, int K, const bf16* X, int64_t ldx, const bf16* Wgu, const bf16* Wg,
+                const bf16* Wu, bf16* gate, bf16* up, bf16* act, int I, const LoraEpi* lg,
+                const LoraEpi* lu, hipStream_t s);
 // the groups' GEMMs in one launch over the N-concatenated tile grid
 int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const GemmGroup* gr,
                 int ng, hipStream_t s);
