@@ -389,6 +389,145 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
         }
 }
 
+// Single-pass forward for the engine (P not stored): online softmax over
+// the key tiles, O rescaled by exp2(m_old - m_new) whenever a row's running
+// max grows, O = (sum_k exp2(s_k - m) V_k) / l at the end.  The rows' final
+// (max, 1/sum) are kept for the backward, which recomputes P from them
+// exactly as the two-pass form would have produced it.  exp2(s - m) <= 1
+// enters the P.V MFMAs as a BF16 hi/lo pair, as in the two-pass form.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_fwd1(const bf16* __restrict__ Q,
+                                                   const bf16* __restrict__ K,
+                                                   const bf16* __restrict__ V,
+                                                   bf16* __restrict__ O, float* __restrict__ O32,
+                                                   float2* __restrict__ stats, int T, int Hq,
+                                                   int Hkv, float scale) {
+    constexpr int VST = HD / 16;
+    __shared__ __attribute__((aligned(16))) bf16 sK[TK * (HD + 8)];
+    __shared__ __attribute__((aligned(16))) char sV[TK * HD * 2];
+    __shared__ __attribute__((aligned(16))) char sP[4][2][TK * 16 * 2];
+    int nqt = (T + TQ - 1) / TQ;
+    int nbh = gridDim.x / nqt;
+    int qt = nqt - 1 - (int)(blockIdx.x / nbh);  // longest rows launch first
+    int bh = (int)(blockIdx.x % nbh);
+    int b = bh / Hq, hq = bh % Hq, hkv = hq / (Hq / Hkv);
+    int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    int64_t qs = (int64_t)Hq * HD, ks_ = (int64_t)Hkv * HD;
+    const bf16* Qh = Q + (int64_t)b * T * qs + hq * HD;
+    const bf16* Kh = K + (int64_t)b * T * ks_ + hkv * HD;
+    const bf16* Vh = V + (int64_t)b * T * ks_ + hkv * HD;
+    int q0 = qt * TQ;
+    int rowA = q0 + 16 * w + (lane & 15);
+    bf16x8_t qf[HD / 32];
+#pragma unroll
+    for (int ks = 0; ks < HD / 32; ks++) qf[ks] = ld_head8(Qh, qs, rowA, T, 32 * ks + 8 * (lane >> 4));
+    const int rbase = q0 + 16 * w + 4 * (lane >> 4);
+    const float sl2 = scale * kLog2e;
+    Rows64<HD> lk, lv;
+    float m[4], l[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        m[r] = -INFINITY;
+        l[r] = 0.f;
+    }
+    floatx4 acc[HD / 16];
+#pragma unroll
+    for (int j = 0; j < HD / 16; j++) acc[j] = zero4();
+    lk.load(Kh, ks_, 0, T);
+    lv.load(Vh, ks_, 0, T);
+    char* sPh = sP[w][0];
+    char* sPl = sP[w][1];
+    for (int kt = 0; kt <= qt; kt++) {
+        __syncthreads();
+        lk.store(sK);
+#pragma unroll
+        for (int i = 0; i < Rows64<HD>::NR; i++) {
+            int q = threadIdx.x + 256 * i;
+            *(u32x4*)(sV + tr_off<VST>(q / (HD / 8), (q % (HD / 8)) * 8)) = lv.v[i];
+        }
+        __syncthreads();
+        if (kt < qt) {
+            lk.load(Kh, ks_, (kt + 1) * TK, T);
+            lv.load(Vh, ks_, (kt + 1) * TK, T);
+        }
+        floatx4 S[4];
+        wave_qk<HD>(S, qf, sK, lane);
+        const bool diag = kt == qt;
+        // scores in base-2 units, masked on the diagonal tile; new row max
+        float v[4][4], al[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float tmax = -INFINITY;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int key = kt * TK + 16 * t + (lane & 15);
+                v[t][r] = (!diag || (key <= rbase + r && key < T)) ? S[t][r] * sl2 : -INFINITY;
+                tmax = fmaxf(tmax, v[t][r]);
+            }
+            const float mn = fmaxf(m[r], red16_max(tmax));
+            al[r] = m[r] == -INFINITY ? 0.f : exp2_fast(m[r] - mn);
+            m[r] = mn;
+        }
+        float add[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int kl = 16 * t + (lane & 15);
+            float p[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                p[r] = exp2_fast(v[t][r] - m[r]);  // 0 where masked
+                add[r] += p[r];
+            }
+            uint2 hi, lo;
+            hi.x = pack2(p[0], p[1]);
+            hi.y = pack2(p[2], p[3]);
+            lo.x = pack2(p[0] - lo2f(hi.x), p[1] - hi2f(hi.x));
+            lo.y = pack2(p[2] - lo2f(hi.y), p[3] - hi2f(hi.y));
+            const int off = tr_off<1>(kl, 4 * (lane >> 4));
+            *(uint2*)(sPh + off) = hi;
+            *(uint2*)(sPl + off) = lo;
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) l[r] = l[r] * al[r] + add[r];
+#pragma unroll
+        for (int j = 0; j < HD / 16; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[j][r] *= al[r];
+        wave_sync();  // sP[w] is this wave's own tile
+#pragma unroll
+        for (int kc = 0; kc < TK / 32; kc++) {
+            const bf16x8_t ah = tr_frag<1>(sPh, 32 * kc, 0, lane);
+            const bf16x8_t alo = tr_frag<1>(sPl, 32 * kc, 0, lane);
+#pragma unroll
+            for (int j = 0; j < HD / 16; j++) {
+                const bf16x8_t bv = tr_frag<VST>(sV, 32 * kc, 16 * j, lane);
+                acc[j] = mfma16(alo, bv, acc[j]);
+                acc[j] = mfma16(ah, bv, acc[j]);
+            }
+        }
+    }
+    float inv[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        inv[r] = 1.f / red16_sum(l[r]);
+        if (rbase + r < T && (lane & 15) == 0)
+            stats[(int64_t)bh * T + rbase + r] = make_float2(m[r], inv[r]);
+    }
+    bf16* Oh = O + (int64_t)b * T * qs + hq * HD;
+    float* O32h = O32 ? O32 + (int64_t)b * T * qs + hq * HD : nullptr;
+#pragma unroll
+    for (int j = 0; j < HD / 16; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            int row = rbase + r;
+            if (row < T) {
+                const float o = acc[j][r] * inv[r];
+                Oh[(int64_t)row * qs + 16 * j + (lane & 15)] = f2bf(o);
+                if (O32h) O32h[(int64_t)row * qs + 16 * j + (lane & 15)] = o;
+            }
+        }
+}
+
 // ── backward: the row dots D = sum_k P * dP ──────────────────────────────
 // From the forward's F32 output: D[bh, t] = dO[t, h, :] . O[t, h, :], since
 // sum_k P dP = sum_k P (dO V_k) = dO (sum_k P V_k).  HD/8 lanes per row.
@@ -888,14 +1027,17 @@ int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* O32, f
     float scale = 1.f / sqrtf((float)hd);
     const bool timed = kprof_begin(KP_ATTN_FWD, s);
     float2* st = (float2*)stats;
-#define AF(H, SPv) \
-    k_attn_fwd<H, SPv><<<(int)blocks, 256, 0, s>>>(Q, K, V, O, O32, P, st, T, Hq, Hkv, scale, zero_fill)
+#define AF(H) \
+    k_attn_fwd<H, true><<<(int)blocks, 256, 0, s>>>(Q, K, V, O, O32, P, st, T, Hq, Hkv, scale, zero_fill)
+#define AF1(H) k_attn_fwd1<H><<<(int)blocks, 256, 0, s>>>(Q, K, V, O, O32, st, T, Hq, Hkv, scale)
+    // with P: two passes (P normalised when it is written); without: one
     if (hd == 64) {
-        if (P) AF(64, true); else AF(64, false);
+        if (P) AF(64); else AF1(64);
     } else {
-        if (P) AF(128, true); else AF(128, false);
+        if (P) AF(128); else AF1(128);
     }
 #undef AF
+#undef AF1
     if (timed) {
         // causal S = QK^T and O = PV; Q, K, V read, O written (and O32),
         // P written (causal half, or all of it when the upper triangle is
@@ -905,8 +1047,8 @@ int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* O32, f
         kprof_end(KP_ATTN_FWD, s, 4.0 * hd * tri,
                   2.0 * bt * hd * (2.0 * Hq + 2.0 * Hkv) + (O32 ? 4.0 * bt * Hq * hd : 0.0) +
                       pbytes,
-                  hd == 64 ? (P ? "void ta::k_attn_fwd<64, true>" : "void ta::k_attn_fwd<64, false>")
-                           : (P ? "void ta::k_attn_fwd<128, true>" : "void ta::k_attn_fwd<128, false>"));
+                  hd == 64 ? (P ? "void ta::k_attn_fwd<64, true>" : "void ta::k_attn_fwd1<64>")
+                           : (P ? "void ta::k_attn_fwd<128, true>" : "void ta::k_attn_fwd1<128>"));
     }
     return check_launch("sdpa_fwd");
 }
