@@ -646,7 +646,8 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO
                                                      const bf16* __restrict__ V,
                                                      const float* __restrict__ P,
                                                      const float2* __restrict__ stats,
-                                                     const float* __restrict__ Dq,
+                                                     float* __restrict__ Dq,
+                                                     const float* __restrict__ O32,
                                                      bf16* __restrict__ dQ, int T, int Hq, int Hkv,
                                                      float scale) {
     constexpr int VST = HD / 16;
@@ -672,8 +673,33 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO
         of[ks] = ld_head8(dOh, qs, rowA, T, 32 * ks + 8 * (lane >> 4));
     int rbase = q0 + 16 * w + 4 * (lane >> 4);
     float D[4];
+    if (O32) {
+        // row dots D = dO . O (the forward's F32 output) for this wave's 16
+        // rows from the dO fragments already in registers: lane (g, j) holds
+        // row j, columns 32 ks + 8 g .. + 7; the 4 g-lanes of a row combine,
+        // then each lane takes the rows of its C layout.  D also goes to Dq
+        // for the dK/dV pass.
+        const float* orow = O32 + ((int64_t)b * T + rowA) * qs + hq * HD;
+        float dsum = 0.f;
+        if (rowA < T) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) D[r] = (rbase + r < T) ? Dq[(int64_t)bh * T + rbase + r] : 0.f;
+            for (int ks = 0; ks < HD / 32; ks++) {
+                const float4 o0 = *(const float4*)(orow + 32 * ks + 8 * (lane >> 4));
+                const float4 o1 = *(const float4*)(orow + 32 * ks + 8 * (lane >> 4) + 4);
+                const float ov[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
+#pragma unroll
+                for (int e = 0; e < 8; e++) dsum += (float)of[ks][e] * ov[e];
+            }
+        }
+        dsum += __shfl_xor(dsum, 16, 64);
+        dsum += __shfl_xor(dsum, 32, 64);
+        if ((lane >> 4) == 0 && rowA < T) Dq[(int64_t)bh * T + rowA] = dsum;
+#pragma unroll
+        for (int r = 0; r < 4; r++) D[r] = __shfl(dsum, 4 * (lane >> 4) + r, 64);
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; r++) D[r] = (rbase + r < T) ? Dq[(int64_t)bh * T + rbase + r] : 0.f;
+    }
     // recompute: Q fragments and the rows' (max, 1/sum), as in the forward
     // (rows past T: 1/sum = 0, so P = 0 there)
     bf16x8_t qf[RC ? HD / 32 : 1];
@@ -1079,8 +1105,10 @@ int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const 
     int nqt = (T + TQ - 1) / TQ;
     float scale = 1.f / sqrtf((float)hd);
     int64_t b1 = (int64_t)B * Hq * nqt;
-    // row dots D
-    if (O32) {
+    const bool rc = P == nullptr;
+    // row dots D: formed inside the dQ pass on the recompute path; otherwise here
+    if (rc) {
+    } else if (O32) {
         int64_t thr = (int64_t)B * T * Hq * (hd / 8);
         int blocks = (int)((thr + 255) / 256);
         if (hd == 64)
@@ -1098,13 +1126,13 @@ int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const 
     // the row dots read once, outputs written once (dkv: F32 partials)
     const double tri = (double)B * Hq * T * (T + 1) / 2.0, bt = (double)B * T;
     const float2* st = (const float2*)stats;
-    const bool rc = P == nullptr;
     // with recomputation each pass also forms S = QK^T again (2 hd flops per
     // causal element) and reads the row statistics instead of P
     const double pb = rc ? 8.0 * B * Hq * (double)T : 4.0 * tri, rf = rc ? 2.0 * hd * tri : 0.0;
     bool timed = kprof_begin(KP_ATTN_BWD_DQ, s);
-#define DQ(H, R) \
-    k_attn_bwd_dq<H, R><<<(int)b1, 256, 0, s>>>(dO, Q, K, V, P, st, Dbuf, dQ, T, Hq, Hkv, scale)
+#define DQ(H, R)                                                                          \
+    k_attn_bwd_dq<H, R><<<(int)b1, 256, 0, s>>>(dO, Q, K, V, P, st, Dbuf, rc ? O32 : nullptr, dQ, \
+                                                T, Hq, Hkv, scale)
     if (hd == 64) {
         if (rc) DQ(64, true); else DQ(64, false);
     } else {
