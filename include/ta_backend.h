@@ -205,7 +205,8 @@ int ta_mem_trim(int device);
  * large K-contiguous GEMM, 1 its wide-N tile shape, 2 attention forward,
  * 3 attention backward dQ pass, 4 attention backward dK/dV pass, 5 the LoRA
  * skinny products h = xA^T / dh = goB, 6 the LoRA weight gradients with
- * their reduction; -1 stops)
+ * their reduction, 7 the chained input-gradient GEMMs, 8 the gate/up
+ * projections with the SwiGLU product; -1 stops)
  * with events recorded on the launch's own stream.  ta_kprof_read waits for
  * the recorded launches and returns their summed time, count, algorithmic
  * flops and HBM bytes, then clears them; ta_kprof_name gives the timed

@@ -1461,12 +1461,22 @@ int gemm_chain(int M, int N, const GemmSeg* sg, int ns, bf16* C, int64_t ldc, co
             a.lora_v[p] = lora->v_nk[p];
         }
     }
-    // (not under the kernel-level timer: its ids cover k_gemm_pipe launches only)
     dim3 grid(a.tiles_m * a.tiles_n);
+    const bool timed = kprof_begin(KP_GEMM_CHAIN, s);
     if (BNb == 192)
         k_gemm_pipe_chain<192, 4, 2><<<grid, 512, 0, s>>>(a);
     else
         k_gemm_pipe_chain<256, 2, 4><<<grid, 512, 0, s>>>(a);
+    if (timed) {
+        // every link's operands read once, C written once, rank-r epilogue products
+        double mn = (double)M * N;
+        double fl = 2.0 * mn * Ktot + 2.0 * mn * a.lora_r * a.lora_n;
+        double by = 2.0 * ((double)M * Ktot + (double)N * Ktot + mn) +
+                    2.0 * a.lora_n * (double)(M + N) * a.lora_r;
+        kprof_end(KP_GEMM_CHAIN, s, fl, by,
+                  BNb == 192 ? "void ta::k_gemm_pipe_chain<192, 4, 2>(ta::GemmArgs)"
+                             : "void ta::k_gemm_pipe_chain<256, 2, 4>(ta::GemmArgs)");
+    }
     return check_launch("gemm_chain");
 }
 
@@ -1637,8 +1647,16 @@ int gemm_swiglu(int M, int K, const bf16* X, int64_t ldx, const bf16* Wgu, const
         a.gv[0] = lg->v_nk[0];
         a.gv[1] = lu->v_nk[0];
     }
-    // (not under the kernel-level timer: its ids cover k_gemm_pipe launches only)
+    const bool timed = kprof_begin(KP_GEMM_SWIGLU, s);
     k_gemm_pipe_swiglu<256, 2, 4><<<tiles, 512, 0, s>>>(a);
+    if (timed) {
+        // X and both weights read once; gate, up and act written once
+        const double mn = 2.0 * M * I;
+        const double fl = 2.0 * mn * K + (on ? 2.0 * mn * 16 : 0.0);
+        const double by = 2.0 * ((double)M * K + 2.0 * I * (double)K + 1.5 * mn) +
+                          (on ? 2.0 * 2.0 * (M + I) * 16 : 0.0);
+        kprof_end(KP_GEMM_SWIGLU, s, fl, by, "void ta::k_gemm_pipe_swiglu<256, 2, 4>(ta::GemmArgs)");
+    }
     return check_launch("gemm_swiglu");
 }
 

@@ -20,7 +20,9 @@ enum KernelId {
     KP_ATTN_BWD_DKV = 4,
     KP_LORA_SKINNY = 5,  // h = x A^T / dh = go B
     KP_LORA_WGRAD = 6,   // gB = go^T h / gA = dh^T x partials
-    KP_COUNT = 7
+    KP_GEMM_CHAIN = 7,   // chained input-gradient GEMMs (k_gemm_pipe_chain)
+    KP_GEMM_SWIGLU = 8,  // gate/up projections with act (k_gemm_pipe_swiglu)
+    KP_COUNT = 9
 };
 // Bracket one launch of kernel `kid` on stream s when that kernel is being
 // timed; name is the kernel's symbol as a profiler prints it.

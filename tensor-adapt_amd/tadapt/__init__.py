@@ -114,7 +114,7 @@ def stream():
 
 # ── kernel-level timer (ta_kprof_*) ─────────────────────────────────────
 KPROF_KERNELS = ["gemm_big", "gemm_big_wide", "attn_fwd", "attn_bwd_dq", "attn_bwd_dkv",
-                 "lora_skinny", "lora_wgrad"]
+                 "lora_skinny", "lora_wgrad", "gemm_chain", "gemm_swiglu"]
 
 
 def kprof_select(kid):
