@@ -91,6 +91,8 @@ struct Engine {
     bool silu_fused = false;
     int sl_st = 0, sl_so = 0;
     float* dh_part = nullptr;
+    // dh and gB of a group's pairs in one pass over their go (go_lora)
+    float* go_part = nullptr;
 
     bf16 *x_final, *xfn, *logits, *g_res, *dres, *tmpH, *dact, *dgate, *dup, *dxn2, *dao, *dQ, *dK,
         *dV, *dxn, *delta, *dh, *dh_cat;
@@ -166,6 +168,23 @@ static int alloc(Engine* e, T** p, int64_t n, const char* name, int is_f32 = -1)
     CK(dmalloc(e, (void**)p, (size_t)n * sizeof(T), name));
     if (is_f32 >= 0) e->named[name] = {(void*)*p, {n, is_f32}};
     return 0;
+}
+
+// Token splits of the gB partials when go_lora makes a group's dh and gB
+// (rank 16, every on-pair's output a multiple of 64, BT a multiple of 32);
+// 0 when the group runs the per-pair kernels.  Used by the plan and the step.
+static int go_group_splits(Engine* e, const Layer& ly, std::initializer_list<int> group) {
+    if (e->r != 16 || e->BT % 32 != 0) return 0;
+    int ntot = 0;
+    for (int p : group) {
+        if (!ly.pr[p].on) continue;
+        if (ly.pr[p].out % 64 != 0) return 0;
+        ntot += ly.pr[p].out;
+    }
+    if (!ntot) return 0;
+    int s_t = 0, s_o = 0;
+    if (go_lora_splits(e->BT, ntot, &s_t, &s_o)) return 0;
+    return s_t;
 }
 
 static int engine_alloc(Engine* e) {
@@ -298,10 +317,12 @@ static int engine_alloc(Engine* e) {
                 // gB of the gate/up pairs come token-split from the fused kernel
                 const bool fused = e->silu_fused && *g.pairs.begin() == PG &&
                                    e->L[l].pr[PG].on && e->L[l].pr[PU].on;
+                const int go_st = fused ? 0 : go_group_splits(e, e->L[l], g.pairs);
                 for (int p : g.pairs) {
                     Pair& pr = e->L[l].pr[p];
                     if (!pr.on) continue;
-                    add(pr.out, r, 0, e->grad + pr.offB, nullptr, nullptr, fused ? e->sl_st : 0);
+                    add(pr.out, r, 0, e->grad + pr.offB, nullptr, nullptr,
+                        fused ? e->sl_st : go_st);
                     ga[n++] = e->grad + pr.offA;
                 }
                 // gA of the down pair comes token-split from the fused kernel too
@@ -321,6 +342,11 @@ static int engine_alloc(Engine* e) {
         }
     }
     int maxout = std::max(std::max(qd, H), I);
+    {
+        // go_lora partials: [column blocks][3][BT][16] for the widest group
+        const int wide = std::max(std::max(H, qd + 2 * kvd), 2 * I);
+        CK(alloc(e, &e->go_part, (int64_t)((wide + 511) / 512) * 3 * BT * 16, "lora.go_partials"));
+    }
     CK(alloc(e, &e->x_final, (int64_t)BT * H, "x_final", 0));
     CK(alloc(e, &e->final_rms, BT, "final_rms", 1));
     CK(alloc(e, &e->xfn, (int64_t)BT * H, "xfn", 0));
@@ -454,7 +480,28 @@ static int lora_group_bwd(Engine* e, Layer& ly, std::initializer_list<int> group
     const int BT = e->BT, r = e->r;
     const double dBT = BT;
     const int64_t ldh = (int64_t)n * r;
-    for (int q = 0; q < n && !dh_ready; q++) {
+    if (!dh_ready && go_group_splits(e, ly, group) > 0) {
+        // dh and gB of every pair in one pass over their go
+        const bf16* bt[3];
+        const bf16* hs[3];
+        float* parts[3];
+        int64_t ld[3];
+        int outs[3];
+        double bytes = 0.0, fl = 0.0;
+        for (int q = 0; q < n; q++) {
+            Pair& pr = ly.pr[on[q]];
+            CK(next_wgrad(e, pr.out, r, &parts[q]));
+            bt[q] = e->shadowT + pr.offB;
+            hs[q] = pr.h;
+            ld[q] = pr.out;
+            outs[q] = pr.out;
+            bytes += dBT * pr.out * 2 + dBT * r * 4;
+            fl += 2.0 * gflops(dBT, r, pr.out);
+        }
+        TIMED(TA_CAT_LORA, fl, bytes,
+              go_lora(go_on, ld, bt, hs, parts, outs, n, BT, e->go_part, e->dh_cat, ldh, e->s));
+    }
+    for (int q = 0; q < n && !dh_ready && go_group_splits(e, ly, group) == 0; q++) {
         Pair& pr = ly.pr[on[q]];
         const bf16* Yt[1] = {e->shadowT + pr.offB};
         bf16* C[1] = {e->dh_cat + q * r};

@@ -731,6 +731,143 @@ __global__ __launch_bounds__(NW * 64) void k_silu_bwd_lora(
     }
 }
 
+// ── one pass over go for the dh and gB products of up to three pairs ─────
+// (adapter_model.cu:131-220, rank 16): dh_p = go_p B_p (column-split
+// partials, dh_part [S_o][3][BT][16]) and gB_p = go_p^T h_p (token-split
+// partials, gb_p [S_t][N_p][16]).  The pairs' columns are concatenated
+// (pair p at columns [c0_p, c0_p + N_p), N_p a multiple of 64), so a wave's
+// 64 columns belong to one pair: down or o alone (go = the residual
+// gradient), or q, k, v with their own go = dQ, dK, dV.  Same tiling as
+// k_silu_bwd_lora: 8 waves x 64 columns per block, 16-token tiles, whole-line
+// global loads, wave-private LDS for the MFMA operands, the waves' dh
+// partials of one pair added in wave order through LDS.
+struct GoPairs {
+    const bf16* go[3];
+    int64_t ldgo[3];
+    const bf16* bt[3];  // B^T shadow [16 x N_p]
+    const bf16* h[3];   // [BT x 16]
+    float* gb[3];       // [S_t][N_p][16]
+    int n[3], c0[3], np, ntot;
+};
+
+template <int NW>
+__global__ __launch_bounds__(NW * 64) void k_go_lora(GoPairs P, float* __restrict__ dh_part,
+                                                     int BT, int per) {
+    __shared__ __attribute__((aligned(16))) char sW[NW][16 * 128];  // go tile per wave
+    __shared__ __attribute__((aligned(16))) char sHw[NW][16 * 32];  // h tile per wave
+    __shared__ __attribute__((aligned(16))) float sDh[2][NW][4][64]; // dh partials [buf][wave]
+    __shared__ int sPair[NW];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int g = lane >> 4, j = lane & 15;
+    const int t_beg = blockIdx.y * per, t_end = min(BT, t_beg + per);
+    const int cw = blockIdx.x * (NW * 64) + 64 * w;  // concatenated column of this wave
+    const bool act = cw < P.ntot;                    // wave-uniform
+    const int pp = (P.np > 2 && cw >= P.c0[2]) ? 2 : (P.np > 1 && cw >= P.c0[1]) ? 1 : 0;
+    const bf16* go = pp == 2 ? P.go[2] : pp == 1 ? P.go[1] : P.go[0];
+    const int64_t ld = pp == 2 ? P.ldgo[2] : pp == 1 ? P.ldgo[1] : P.ldgo[0];
+    const bf16* bt = pp == 2 ? P.bt[2] : pp == 1 ? P.bt[1] : P.bt[0];
+    const bf16* hh = pp == 2 ? P.h[2] : pp == 1 ? P.h[1] : P.h[0];
+    float* gbp = pp == 2 ? P.gb[2] : pp == 1 ? P.gb[1] : P.gb[0];
+    const int np_ = pp == 2 ? P.n[2] : pp == 1 ? P.n[1] : P.n[0];
+    const int lc = cw - (pp == 2 ? P.c0[2] : pp == 1 ? P.c0[1] : P.c0[0]);  // column in pair
+    if (lane == 0) sPair[w] = act ? pp : -1;
+    // whole-line element of a tile at token tb: rows lane/8 (+ 8i), columns lc + 8 (lane%8)
+    const int64_t lofs = (int64_t)(lane >> 3) * ld + lc + 8 * (lane & 7);
+    const int hrow = (lane >> 1) & 15, hh8 = lane & 1;  // h tile: lanes 0..31 load
+    char* const sw = sW[w];
+    char* const shw = sHw[w];
+    u32x4 rg[2][2], rh[2];
+#define GO_LOAD(B, tb)                                                       \
+    do {                                                                     \
+        const int64_t o_ = (int64_t)(tb) * ld + lofs;                        \
+        rg[B][0] = *(const u32x4*)(go + o_);                                 \
+        rg[B][1] = *(const u32x4*)(go + o_ + 8 * ld);                        \
+        rh[B] = *(const u32x4*)(hh + (int64_t)((tb) + hrow) * 16 + 8 * hh8); \
+    } while (0)
+    bf16x8_t fb[2];  // B^T: row j, columns lc + 32 kc + 8g .. + 7
+    floatx4 gb[4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ct++) gb[ct] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (act) {
+#pragma unroll
+        for (int kc = 0; kc < 2; kc++)
+            fb[kc] = *(const bf16x8_t*)(bt + (int64_t)j * np_ + lc + 32 * kc + 8 * g);
+        if (t_beg < t_end) GO_LOAD(0, t_beg);
+        if (t_beg + 16 < t_end) GO_LOAD(1, t_beg + 16);
+    }
+    __syncthreads();  // sPair
+    const int rr = 4 * g + (j >> 2), cc = 4 * (j & 3);
+    for (int tb0 = t_beg; tb0 < t_end; tb0 += 32) {
+#pragma unroll
+        for (int B = 0; B < 2; B++) {
+            const int tb = tb0 + 16 * B;
+            if (tb < t_end) {  // block-uniform
+                floatx4 dhw = floatx4{0.f, 0.f, 0.f, 0.f};
+                if (act) {
+                    const u32x4 v0 = rg[B][0], v1 = rg[B][1], hv = rh[B];
+                    if (tb + 32 < t_end) GO_LOAD(B, tb + 32);
+                    const int lr = lane >> 3, lcc = 8 * (lane & 7);
+                    *(u32x4*)(sw + sw_off(lr, lcc)) = v0;
+                    *(u32x4*)(sw + sw_off(lr + 8, lcc)) = v1;
+                    if (lane < 32) *(u32x4*)(shw + tr_off<1>(hrow, 8 * hh8)) = hv;
+                    // one wave's LDS instructions execute in order
+                    asm volatile("" ::: "memory");
+#pragma unroll
+                    for (int kc = 0; kc < 2; kc++)
+                        dhw = mf16(*(const bf16x8_t*)(sw + sw_off(j, 32 * kc + 8 * g)), fb[kc], dhw);
+                    const s16x4_t hb = tr4(shw + tr_off<1>(rr, cc));
+#pragma unroll
+                    for (int ct = 0; ct < 4; ct++)
+                        gb[ct] = mf16k16(tr4(sw + sw_off(rr, 16 * ct + cc)), hb, gb[ct]);
+                    asm volatile("" ::: "memory");
+                }
+                // dh of the tile per pair over the block's columns, waves in order
+#pragma unroll
+                for (int i = 0; i < 4; i++) sDh[B][w][i][lane] = dhw[i];
+                __syncthreads();
+                for (int e = threadIdx.x; e < 3 * 256; e += NW * 64) {
+                    const int q = e >> 8, i = (e >> 6) & 3, ln = e & 63;
+                    float v = 0.f;
+                    bool any = false;
+                    for (int ww = 0; ww < NW; ww++)
+                        if (sPair[ww] == q) {
+                            v = any ? v + sDh[B][ww][i][ln] : sDh[B][ww][i][ln];
+                            any = true;
+                        }
+                    if (any)
+                        dh_part[(((int64_t)blockIdx.x * 3 + q) * BT + tb + 4 * (ln >> 4) + i) * 16 +
+                                (ln & 15)] = v;
+                }
+            }
+        }
+    }
+#undef GO_LOAD
+    if (act) {
+#pragma unroll
+        for (int ct = 0; ct < 4; ct++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                gbp[((int64_t)blockIdx.y * np_ + lc + 16 * ct + 4 * g + i) * 16 + j] = gb[ct][i];
+    }
+}
+
+// dh[t][16p + j] = bf16(sum over the column blocks holding pair p, in order,
+// of dh_part[s][p][t][j])
+__global__ __launch_bounds__(256) void k_dh_reduce_go(const float* __restrict__ dh_part, GoPairs P,
+                                                      int bcols, int BT, bf16* __restrict__ dh,
+                                                      int64_t ldh) {
+    const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (q >= (int64_t)BT * 16 * P.np) return;
+    const int64_t t = q / (16 * P.np);
+    const int pp = (int)(q / 16 % P.np), jj = (int)(q & 15);
+    const int c0 = pp == 2 ? P.c0[2] : pp == 1 ? P.c0[1] : P.c0[0];
+    const int n = pp == 2 ? P.n[2] : pp == 1 ? P.n[1] : P.n[0];
+    float v = 0.f;
+    for (int sb = c0 / bcols; sb <= (c0 + n - 1) / bcols; sb++)
+        v += dh_part[(((int64_t)sb * 3 + pp) * BT + t) * 16 + jj];
+    dh[t * ldh + 16 * pp + jj] = f2bf(v);
+}
+
 // dh[t][16p + j] = bf16(sum over the column splits, in order, of dh_part[s][p][t][j])
 __global__ __launch_bounds__(256) void k_dh_reduce2(const float* __restrict__ dh_part, int s_o,
                                                     int BT, bf16* __restrict__ dh, int64_t ldh) {
@@ -947,6 +1084,64 @@ int dh_reduce2(const float* dh_part, int s_o, int BT, bf16* dh, int64_t ldh, hip
     const int64_t n = (int64_t)BT * 32;
     k_dh_reduce2<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(dh_part, s_o, BT, dh, ldh);
     return check_launch("dh_reduce2");
+}
+
+// k_go_lora grid: 8 waves x 64 columns per block over the pairs'
+// concatenated columns; token ranges (multiples of 32) sized so that every
+// block is resident at once.  *s_t: token splits (the gB partials' count),
+// *s_o: column blocks.
+static constexpr int GL_NW = 8;
+static int go_lora_plan(int BT, int ntot, int* s_t, int* s_o, int* per) {
+    static int resident = 0;
+    if (!resident) {
+        int nb = 0, dev = 0, ncu = 0;
+        TA_HIP(hipGetDevice(&dev));
+        TA_HIP(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
+        TA_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, k_go_lora<GL_NW>, GL_NW * 64, 0));
+        resident = std::max(1, nb) * std::max(1, ncu);
+    }
+    *s_o = (ntot + GL_NW * 64 - 1) / (GL_NW * 64);
+    const int ranges = std::max(1, std::min(resident / *s_o, BT / 32));
+    *per = (BT / ranges + 31) / 32 * 32;
+    *s_t = (BT + *per - 1) / *per;
+    return 0;
+}
+int go_lora_splits(int BT, int ntot, int* s_t, int* s_o) {
+    int per = 0;
+    return go_lora_plan(BT, ntot, s_t, s_o, &per);
+}
+
+int go_lora(const bf16* const* go, const int64_t* ldgo, const bf16* const* bt, const bf16* const* h,
+            float* const* gb, const int* n, int np, int BT, float* dh_part, bf16* dh, int64_t ldh,
+            hipStream_t s) {
+    TA_REQUIRE(np >= 1 && np <= 3 && BT > 0 && BT % 32 == 0 && dh_part && dh,
+               "go_lora: bad arguments (np %d, BT %d)", np, BT);
+    GoPairs P{};
+    int c = 0;
+    for (int q = 0; q < np; q++) {
+        TA_REQUIRE(n[q] > 0 && n[q] % 64 == 0 && ldgo[q] % 8 == 0 && go[q] && bt[q] && h[q] &&
+                       gb[q] && ((uintptr_t)go[q] & 15) == 0 && ((uintptr_t)bt[q] & 15) == 0 &&
+                       ((uintptr_t)h[q] & 15) == 0,
+                   "go_lora: pair %d: N %d must be a multiple of 64, operands 16-byte aligned", q,
+                   n[q]);
+        P.go[q] = go[q];
+        P.ldgo[q] = ldgo[q];
+        P.bt[q] = bt[q];
+        P.h[q] = h[q];
+        P.gb[q] = gb[q];
+        P.n[q] = n[q];
+        P.c0[q] = c;
+        c += n[q];
+    }
+    P.np = np;
+    P.ntot = c;
+    int s_t = 0, s_o = 0, per = 0;
+    if (int rc = go_lora_plan(BT, c, &s_t, &s_o, &per)) return rc;
+    k_go_lora<GL_NW><<<dim3(s_o, s_t), GL_NW * 64, 0, s>>>(P, dh_part, BT, per);
+    const int64_t nel = (int64_t)BT * 16 * np;
+    k_dh_reduce_go<<<(unsigned)((nel + 255) / 256), 256, 0, s>>>(dh_part, P, GL_NW * 64, BT, dh,
+                                                                  ldh);
+    return check_launch("go_lora");
 }
 
 int transpose_batch(const bf16* src, bf16* dst, const void* descs, int nd, hipStream_t s) {

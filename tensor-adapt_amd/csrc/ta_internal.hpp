@@ -150,6 +150,14 @@ int silu_bwd_lora(const bf16* dact, const bf16* gate, const bf16* up, bf16* dgat
                   int I, hipStream_t s);
 // dh[t][p*16 + j] = bf16(sum over the S_o column splits of dh_part[s][p][t][j]), p = 0, 1
 int dh_reduce2(const float* dh_part, int s_o, int BT, bf16* dh, int64_t ldh, hipStream_t s);
+// dh_p = bf16(go_p B_p) into dh (columns 16p.., row stride ldh) and the gB
+// partials gb_p [S_t][N_p][16] of up to three rank-16 pairs in one pass over
+// their go_p [BT x N_p] (N_p multiples of 64, BT a multiple of 32); bt_p the
+// B^T shadows [16 x N_p], h_p [BT x 16]; dh_part: [S_o][3][BT][16] F32
+int go_lora_splits(int BT, int ntot, int* s_t, int* s_o);
+int go_lora(const bf16* const* go, const int64_t* ldgo, const bf16* const* bt, const bf16* const* h,
+            float* const* gb, const int* n, int np, int BT, float* dh_part, bf16* dh, int64_t ldh,
+            hipStream_t s);
 int lora_wgrad_reduce_jobs(const WgradJob* jobs, int njobs, int64_t total_blocks, double elems,
                            hipStream_t s);
 int transpose_batch(const bf16* src, bf16* dst, const void* descs, int nd, hipStream_t s);
