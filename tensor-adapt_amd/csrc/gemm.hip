@@ -687,13 +687,17 @@ __device__ __forceinline__ void pipe_frags(Frags<TM, TN>& f, const bf16* sX, con
     }
 }
 
+// The accumulators hold the transposed fragments (Y rows as the MFMA's A
+// operand): lane l of acc[i][j] has output row 32i + l%32 and columns
+// 32j + 8(r/4) + 4(l/32) + r%4, i.e. four consecutive columns per register
+// group, which the epilogue packs into 8-byte words.
 template <int TM, int TN>
 __device__ __forceinline__ void pipe_mma(floatx16 (&acc)[TM][TN], const Frags<TM, TN>& f) {
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
         for (int j = 0; j < TN; j++)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[j], f.a[i], acc[i][j], 0, 0, 0);
 }
 
 // scheduling hint for the region just emitted: alternate one MFMA with one
@@ -716,13 +720,24 @@ __device__ __attribute__((always_inline)) inline void static_for(F&& f) {
     }
 }
 
+// Element offset of (row, col) in a wave's 64 x WTN BF16 output staging:
+// 16-byte chunks XOR-swizzled by row bits 1..3 (1..2 for WTN = 96), so the
+// 8-byte writes of 32 rows at one column land in distinct banks and every
+// 16-byte chunk stays contiguous for the row read-out.
+template <int WTN>
+__device__ __forceinline__ int stg_off(int row, int col) {
+    constexpr int X = WTN == 96 ? 3 : 7;
+    return row * WTN + ((((col >> 3) ^ ((row >> 1) & X)) << 3) | (col & 7));
+}
+
 // Epilogue of one 64-row half (row fragments I0, I0 + 1) of a wave tile,
-// staged in the wave's private LDS region wb (64 x WTN BF16).  Same
-// arithmetic as big_epilogue, fragment by fragment: alpha acc + beta C
-// (+ bias) rounded, then each LoRA term (rank <= 16: one MFMA k step, its
-// operand fragments loaded up front), then the BF16 value into wb; the half
-// leaves as 16-byte row vectors.  A lane reads and writes the same wb words
-// for a fragment, so only the final read-back needs the wave barrier.
+// staged in the wave's private LDS region wb (64 x WTN BF16, stg_off
+// layout).  Same arithmetic as big_epilogue, fragment by fragment: alpha acc
+// + beta C (+ bias) rounded, then each LoRA term (rank <= 16: one MFMA k
+// step, its operand fragments loaded up front), then the BF16 values into
+// wb, four columns per 8-byte write; the half leaves as 16-byte row vectors.
+// A lane reads and writes the same wb words for a fragment, so only the
+// final read-back needs the wave barrier.
 //
 // lu/lv/lb (may be null): the block's rank-16 LoRA operands of the first PF
 // pairs (U rows, V rows; 16 BF16 per row) and its bias, staged in LDS at the
@@ -749,7 +764,7 @@ __device__ __attribute__((always_inline)) inline void pipe_half_epilogue(
 #pragma unroll
                 for (int e = 0; e < 4; e++) v.w[e] = (uint32_t)t[2 * e] | ((uint32_t)t[2 * e + 1] << 16);
             }
-            *(bf16x8v*)(wb + row * WTN + 8 * ch) = v;
+            *(bf16x8v*)(wb + stg_off<WTN>(row, 8 * ch)) = v;
         }
         __builtin_amdgcn_wave_barrier();
     }
@@ -786,19 +801,46 @@ __device__ __attribute__((always_inline)) inline void pipe_half_epilogue(
             }
         }
     }
+    const int c4 = 4 * (lane >> 5);  // first of the lane's 4 columns in each 8-column group
     static_for<2 * TN>([&](auto ij) {
         constexpr int i = decltype(ij)::value / TN, j = decltype(ij)::value % TN;
-        const int lc = j * 32 + (lane & 31);
-        const int n = C0 + lc;
-        const float bias = (a.bias && n < a.N) ? bf2f(lb ? lb[nloc + lc] : a.bias[n]) : 0.f;
+        const int lr = i * 32 + (lane & 31);
+        // v[4g + e]: column 32j + 8g + c4 + e of row lr
         float v[16];
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int lr = i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            float o = a.alpha * acc[I0 + i][j][r];
-            if (a.beta != 0.f) o += a.beta * bf2f(wb[lr * WTN + lc]);
-            if (a.bias) o = bf2f(f2bf(o)) + bias;
-            v[r] = bf2f(f2bf(o));
+        for (int r = 0; r < 16; r++) v[r] = a.alpha * acc[I0 + i][j][r];
+        if (a.beta != 0.f) {
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const uint2 cw = *(const uint2*)(wb + stg_off<WTN>(lr, 32 * j + 8 * g + c4));
+                v[4 * g] += a.beta * lo2f(cw.x);
+                v[4 * g + 1] += a.beta * hi2f(cw.x);
+                v[4 * g + 2] += a.beta * lo2f(cw.y);
+                v[4 * g + 3] += a.beta * hi2f(cw.y);
+            }
+        }
+        if (a.bias) {
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int lc = 32 * j + 8 * g + c4;
+                float bb[4];
+                if (lb) {
+                    const uint2 bw = *(const uint2*)(lb + nloc + lc);
+                    bb[0] = lo2f(bw.x), bb[1] = hi2f(bw.x), bb[2] = lo2f(bw.y), bb[3] = hi2f(bw.y);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) bb[e] = C0 + lc + e < a.N ? bf2f(a.bias[C0 + lc + e]) : 0.f;
+                }
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const float bias = C0 + lc + e < a.N ? bb[e] : 0.f;
+                    v[4 * g + e] = bf2f(f2bf(v[4 * g + e])) + bias;
+                }
+            }
+        }
+        if (a.lora_n > 0) {
+#pragma unroll
+            for (int r = 0; r < 16; r++) v[r] = bf2f(f2bf(v[r]));
         }
 #pragma unroll
         for (int p = 0; p < 3; p++) {
@@ -812,7 +854,7 @@ __device__ __attribute__((always_inline)) inline void pipe_half_epilogue(
                     vb = fv[p < PF ? p : 0][j];
                 } else {
                     const int row = min(R0 + 32 * i + (lane & 31), a.M - 1);
-                    const int col = min(n, a.N - 1);
+                    const int col = min(C0 + 32 * j + (lane & 31), a.N - 1);
                     ua = *(const bf16x8_t*)(a.lora_u[p] + (int64_t)row * a.lora_ldu[p] + (kin ? kk : 0));
                     vb = *(const bf16x8_t*)(a.lora_v[p] + (int64_t)col * a.lora_r + (kin ? kk : 0));
                     if (!kin) {
@@ -820,17 +862,21 @@ __device__ __attribute__((always_inline)) inline void pipe_half_epilogue(
                         for (int e = 0; e < 8; e++) ua[e] = vb[e] = (__bf16)0.f;
                     }
                 }
-                d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ua, vb, d, 0, 0, 0);
+                // transposed like the accumulators: V rows as the A operand
+                d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vb, ua, d, 0, 0, 0);
 #pragma unroll
                 for (int r = 0; r < 16; r++)
                     v[r] = a.lora_delta ? bf2f(f2bf(v[r] + a.lora_s * bf2f(f2bf(d[r]))))
                                         : bf2f(f2bf(a.lora_s * d[r] + v[r]));
             }
         }
+        // the packing rounds to BF16 (exact when v is a BF16 value already)
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int lr = i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-            wb[lr * WTN + lc] = f2bf(v[r]);
+        for (int g = 0; g < 4; g++) {
+            uint2 w;
+            w.x = pack2(v[4 * g], v[4 * g + 1]);
+            w.y = pack2(v[4 * g + 2], v[4 * g + 3]);
+            *(uint2*)(wb + stg_off<WTN>(lr, 32 * j + 8 * g + c4)) = w;
         }
     });
     __builtin_amdgcn_wave_barrier();
@@ -838,7 +884,7 @@ __device__ __attribute__((always_inline)) inline void pipe_half_epilogue(
         int row = q / CPR, ch = q % CPR;
         int gm = R0 + row, gn = C0 + 8 * ch;
         if (gm >= a.M) continue;
-        bf16x8v v = *(const bf16x8v*)(wb + row * WTN + 8 * ch);
+        bf16x8v v = *(const bf16x8v*)(wb + stg_off<WTN>(row, 8 * ch));
         if (vec && gn + 8 <= a.N) {
             *(bf16x8v*)(C + (int64_t)gm * a.ldc + gn) = v;
         } else {
@@ -1084,8 +1130,8 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
             const int row = q / (WTN / 8), ch = q % (WTN / 8);
             if (rb + row >= a.M) continue;
             float g[8], u[8], o[8];
-            unpack8(*(const bf16x8v*)(gst + row * WTN + 8 * ch), g);
-            unpack8(*(const bf16x8v*)(ust + row * WTN + 8 * ch), u);
+            unpack8(*(const bf16x8v*)(gst + stg_off<WTN>(row, 8 * ch)), g);
+            unpack8(*(const bf16x8v*)(ust + stg_off<WTN>(row, 8 * ch)), u);
 #pragma unroll
             for (int e = 0; e < 8; e++) o[e] = silu_mul_f(g[e], u[e]);
             *(bf16x8v*)(actp + (int64_t)(rb + row) * I + cg + 8 * ch) = pack8(o);
