@@ -305,7 +305,7 @@ static int engine_alloc(Engine* e) {
             j.n = (int64_t)NL * NS;
             j.blk0 = blk;
             j.part = (const float*)(intptr_t)off;  // arena offset until the arena exists
-            blk += (j.n + 255) / 256;
+            blk += (j.n + 1023) / 1024;  // k_wgrad_reduce_jobs: 1024 elements per block
             off += ((int64_t)j.splits * j.n + 63) / 64 * 64;
             e->wg_elems += (double)j.n;
             e->wg_plan.push_back(j);
