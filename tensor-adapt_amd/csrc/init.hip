@@ -127,30 +127,51 @@ int add2_bf16(bf16* out, const bf16* a, const bf16* b, int64_t n, hipStream_t s)
 }
 
 // Assistant-span masking of src/trainer/adapt_trainer.cu:145-182 on device
-// tokens: one thread per batch row walks its T tokens in order (the state
-// machine is sequential along t); targets outside assistant spans become -1.
-__global__ void k_mask_targets(const int32_t* __restrict__ in, const int32_t* __restrict__ tgt_in,
-                               int32_t* __restrict__ tgt, int B, int T) {
-    int b = blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= B) return;
-    bool in_asst = false;
-    int64_t off = (int64_t)b * T;
-    for (int t = 0; t < T; ++t) {
-        int64_t idx = off + t;
-        int tok = in[idx];
-        if (tok == 151644) in_asst = (t + 1 < T && in[off + t + 1] == 77091);
+// tokens.  The reference's state machine is sequential along t, but its
+// state after token t depends only on the last event e <= t (a token
+// 151644, which sets in_asst = (tokens[e + 1] == 77091), or 151645, which
+// clears it; false before any event).  One 1024-thread block per batch row
+// takes e as an inclusive prefix max of the event positions (wave shuffles,
+// then the waves in order), 1024 tokens at a time with the running e
+// carried over; every thread then applies the reference's per-token rule.
+// Targets outside assistant spans become -1.
+__global__ __launch_bounds__(1024) void k_mask_targets(const int32_t* __restrict__ in,
+                                                       const int32_t* __restrict__ tgt_in,
+                                                       int32_t* __restrict__ tgt, int B, int T) {
+    __shared__ int wmax[16];
+    __shared__ int carry_s;
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int64_t off = (int64_t)blockIdx.x * T;
+    int carry = -1;  // last event before this chunk
+    for (int c0 = 0; c0 < T; c0 += 1024) {
+        const int t = c0 + (int)threadIdx.x;
+        const int tok = t < T ? in[off + t] : 0;
+        int v = (t < T && (tok == 151644 || tok == 151645)) ? t : -1;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int u = __shfl_up(v, o, 64);
+            if (lane >= o) v = max(v, u);
+        }
+        if (lane == 63) wmax[wv] = v;
+        __syncthreads();
+        int pre = carry;
+        for (int k = 0; k < wv; k++) pre = max(pre, wmax[k]);
+        v = max(v, pre);
+        bool in_asst = false;
+        if (v >= 0) in_asst = in[off + v] == 151644 && v + 1 < T && in[off + v + 1] == 77091;
         bool mask = !in_asst;
         if (tok == 151644 || tok == 77091) mask = true;
-        if (tok == 151645) {
-            in_asst = false;
-            mask = false;
-        }
-        tgt[idx] = mask ? -1 : tgt_in[idx];
+        if (tok == 151645) mask = false;
+        if (t < T) tgt[off + t] = mask ? -1 : tgt_in[off + t];
+        if (threadIdx.x == 1023) carry_s = v;
+        __syncthreads();  // carry_s written, wmax free for the next chunk
+        carry = carry_s;
     }
 }
 int mask_targets_dev(const int32_t* in, const int32_t* tgt_in, int32_t* tgt, int B, int T,
                      hipStream_t s) {
-    k_mask_targets<<<(B + 63) / 64, 64, 0, s>>>(in, tgt_in, tgt, B, T);
+    if (B <= 0 || T <= 0) return 0;
+    k_mask_targets<<<B, 1024, 0, s>>>(in, tgt_in, tgt, B, T);
     return check_launch("mask_targets");
 }
 

@@ -267,3 +267,39 @@ def _gpu_step(p, x, want):
         assert (~sure).mean() < 0.25, t
         bg = e.adapter(l, t, "B").reshape(go.shape)
         assert _rel(bg[sure], want[f"B_{t}"][sure]) <= 1e-2, t
+
+
+@pytest.mark.gpu
+def test_gpu_mask_targets_multichunk():
+    """Device masking over rows longer than one 1024-token scan chunk, with
+    an assistant header split across each chunk seam and at the row end,
+    bit-exact against the oracle's sequential state machine
+    (adapt_trainer.cu:145-182)."""
+    import torch
+    import oracle as O
+    B, T = 2, 2112  # chunks of 1024, 1024, 64
+    print(f"case: mask_targets multichunk B={B} T={T}", flush=True)
+    rng = np.random.default_rng(11)
+    vocab = np.array([151644, 77091, 151645, 5, 6, 7, 8, 9], np.int32)
+    prob = np.array([0.02, 0.03, 0.02, 0.23, 0.2, 0.2, 0.15, 0.15])
+    inputs = rng.choice(vocab, size=(B, T), p=prob).astype(np.int32)
+    # header opening at the last token of a chunk, role token in the next
+    inputs[0, 1023], inputs[0, 1024] = 151644, 77091
+    inputs[0, 1025:1500] = 5
+    inputs[1, 2047], inputs[1, 2048] = 151644, 77091
+    inputs[1, 2049:2111] = 6
+    inputs[1, T - 1] = 151644  # opening at the row end: no next token
+    inputs[0, 1024 - 3:1024 - 1] = (151645, 5)
+    targets = rng.integers(0, 151936, size=(B, T), dtype=np.int32)
+    want = O.mask_targets(inputs.ravel(), targets.ravel(), B, T).reshape(B, T)
+    assert (want >= 0).sum() > 100 and (want < 0).sum() > 100
+    mc = dict(vocab=151936, hidden=256, layers=1, n_q=4, n_kv=2, head_dim=64, inter=512,
+              rms_eps=1e-6, rope_theta=1e6, tie=1)
+    ac = dict(rank=8, alpha=16.0, inject_mask=0b1, lr=1e-4, grad_clip=1.0, warmup=0,
+              total_steps=4, b1=0.9, b2=0.999, eps=1e-8, wd=0.0)
+    e = _engine(mc, ac, B, T)
+    e.init_random(seed=5, std=0.02)
+    e.step_resident(torch.from_numpy(inputs).cuda(), torch.from_numpy(targets).cuda())
+    torch.cuda.synchronize()
+    got = e.read_buffer("targets").view(np.int32).reshape(B, T)
+    assert np.array_equal(got, want)
