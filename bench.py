@@ -35,6 +35,27 @@ C3_MODEL = dict(vocab=151936, hidden=1536, layers=28, n_q=12, n_kv=2, head_dim=1
 C3_ADAPT = dict(rank=16, alpha=32.0, inject_mask=0b1111111, lr=1e-4, grad_clip=1.0, warmup=5,
                 total_steps=50, b1=0.9, b2=0.999, eps=1e-8, wd=0.0)
 C3_B, C3_T = 8, 1024
+C3_WORK = ("c3: Qwen2-1.5B shape, LoRA r=16 alpha=32 on q,k,v,o,gate,up,down, batch 8 x seq 1024, "
+           "AdamW, centroid accumulator on")
+METRIC = "train tokens/s Qwen2-1.5B LoRA r=16 seq1024; bwd MFMA util %, HBM GB/s"
+# the other BASELINE configs, for secondary measurements (--config); the
+# headline line is c3
+C2_MODEL = dict(vocab=151936, hidden=896, layers=24, n_q=14, n_kv=2, head_dim=64, inter=4864,
+                rms_eps=1e-6, rope_theta=1e6, tie=1)
+C2_ADAPT = dict(C3_ADAPT, inject_mask=0b0001111, total_steps=20)
+C4_MODEL = dict(vocab=152064, hidden=3584, layers=28, n_q=28, n_kv=4, head_dim=128, inter=18944,
+                rms_eps=1e-6, rope_theta=1e6, tie=0)
+C4_ADAPT = dict(C3_ADAPT, rank=64, alpha=128.0, total_steps=20)
+CONFIGS = {
+    # name: (model, adapt, B, T, per-layer recompute, workload)
+    "c3": (C3_MODEL, C3_ADAPT, C3_B, C3_T, False, C3_WORK),
+    "c2": (C2_MODEL, C2_ADAPT, 4, 512, False,
+           "c2: Qwen2-0.5B, tied embedding, LoRA r=16 alpha=32 on q,k,v,o, batch 4 x seq 512, "
+           "AdamW, centroid accumulator on"),
+    "c4": (C4_MODEL, C4_ADAPT, 4, 2048, True,
+           "c4: Qwen2-7B shape, untied LM head, LoRA r=64 alpha=128 on q,k,v,o,gate,up,down, "
+           "batch 4 x seq 2048, per-layer activation recompute, AdamW, centroid accumulator on"),
+}
 
 CAT_NAMES = ["gemm_fwd", "gemm_dx", "lm_head", "lora", "attn_fwd", "attn_bwd", "norm",
              "elementwise", "cross_entropy", "adamw_tail", "centroid"]
@@ -79,14 +100,14 @@ def measured_traffic(kernel):
     return None
 
 
-def cpu_baseline(model, adapt):
+def cpu_baseline(model, adapt, cname="c3"):
     """Oracle (CPU restatement of the reference step) on this host, bounded
-    sample: (A) one c3 transformer layer, forward+backward+AdamW, B=1 x
-    T=1024, with a 2048-entry vocabulary so the LM head is negligible;
-    (B) the c3 LM head + cross entropy + final norm alone (0 layers, full
-    151936 vocabulary) on 256 tokens.  Per-token cost of the c3 model =
-    28 * A/1024 + B/256 (the head is linear in tokens, a layer is linear in
-    B at fixed T=1024)."""
+    sample: (A) one transformer layer of the config, forward+backward+AdamW,
+    B=1 x T=1024, with a 2048-entry vocabulary so the LM head is negligible;
+    (B) the LM head + cross entropy + final norm alone (0 layers, full
+    vocabulary) on 256 tokens.  Per-token cost of the model =
+    layers * A/1024 + B/256 (the head is linear in tokens, a layer is linear
+    in B at fixed T=1024)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import numpy as np
     import oracle as O
@@ -100,6 +121,8 @@ def cpu_baseline(model, adapt):
         ones = O.bf16_from_f32(np.ones(H, np.float32))
         m.set_weight("model.embed_tokens.weight", w(V, H))
         m.set_weight("model.norm.weight", ones)
+        if not mc["tie"]:
+            m.set_weight("lm_head.weight", w(V, H))
         for l in range(mc["layers"]):
             p = f"model.layers.{l}."
             for n, a in (("input_layernorm.weight", ones), ("post_attention_layernorm.weight", ones),
@@ -123,8 +146,9 @@ def cpu_baseline(model, adapt):
     per_tok = model["layers"] * t_layer / 1024.0 + t_head / 256.0
     cores = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     return {"value": round(1.0 / per_tok, 3), "unit": "tokens/s", "cores": cores, "kind": "port",
-            "sample": ("oracle step on one c3 layer (B=1, T=1024, %.1f s) and the c3 LM head + "
-                       "CE on 256 tokens (%.1f s), extrapolated to 28 layers" % (t_layer, t_head))}
+            "sample": ("oracle step on one %s layer (B=1, T=1024, %.1f s) and the %s LM head + "
+                       "CE on 256 tokens (%.1f s), extrapolated to %d layers"
+                       % (cname, t_layer, cname, t_head, model["layers"]))}
 
 
 def main():
@@ -133,6 +157,8 @@ def main():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--config", choices=sorted(CONFIGS), default="c3",
+                    help="workload (default c3, the headline metric's config)")
     ap.add_argument("--categories", action="store_true",
                     help="print the per-kernel-class time split to stderr")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -146,8 +172,8 @@ def main():
     import torch
     import tadapt
 
-    model, adapt, B, T = C3_MODEL, C3_ADAPT, C3_B, C3_T
-    eng = tadapt.Engine(model, adapt, B, T)
+    model, adapt, B, T, recompute, workload = CONFIGS[args.config]
+    eng = tadapt.Engine(model, adapt, B, T, recompute=recompute)
     eng.init_random(seed=20261201, std=0.02)
     nb = args.warmup + args.steps + len(CAT_NAMES) + len(tadapt.KPROF_KERNELS)
     batches = token_batches(nb, B, T, model["vocab"], 1)
@@ -219,7 +245,8 @@ def main():
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                 "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4)}
     name = tadapt.kprof_name(dom)
-    roof["traffic"] = measured_traffic(name)
+    # the recorded counter runs are of the c3 step
+    roof["traffic"] = measured_traffic(name) if args.config == "c3" else None
     roof["kernel"] = name
     roof["launches"] = prof["launches"]
     roof["avg_launch_us"] = round(prof["ms"] * 1e3 / max(prof["launches"], 1), 1)
@@ -229,7 +256,7 @@ def main():
     roof["share_of_step"] = round(sec / dt, 4)
 
     out = {
-        "metric": "train tokens/s Qwen2-1.5B LoRA r=16 seq1024; bwd MFMA util %, HBM GB/s",
+        "metric": METRIC if args.config == "c3" else f"train tokens/s ({args.config})",
         "value": round(value, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -241,8 +268,7 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (uniform random token ids; random-init N(0,0.02) BF16 base)",
-        "config": {"workload": "c3: Qwen2-1.5B shape, LoRA r=16 alpha=32 on q,k,v,o,gate,up,down, "
-                               "batch 8 x seq 1024, AdamW, centroid accumulator on",
+        "config": {"workload": workload,
                    "global_batch": B, "seq_len": T, "layers": model["layers"],
                    "hidden": model["hidden"], "parallelism": "single GPU"},
         "roofline": roof,
@@ -250,7 +276,7 @@ def main():
     }
     del eng
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(model, adapt)
+        out["cpu_baseline"] = cpu_baseline(model, adapt, args.config)
     print(json.dumps(out), flush=True)
 
 

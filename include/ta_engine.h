@@ -58,6 +58,19 @@ typedef struct ta_step_metrics {
  * Returns NULL on failure. */
 void* ta_engine_create(const ta_model_config* model, const ta_adapt_config* adapt, int B, int T,
                        void* stream);
+
+/* ta_engine_create with creation flags.  No counterpart in the reference,
+ * which caches every layer's activations (Qwen2LayerCache,
+ * include/tensor/base/arch/qwen2.hpp:17-35); it is for long-sequence and
+ * large-model runs such as the Qwen2-7B-shaped config at B=4 x T=2048.
+ *   TA_ENGINE_RECOMPUTE: keep only each layer's input per layer; the
+ *   backward reruns a layer's forward into one shared activation set just
+ *   before that layer's backward.  Results are bit-identical to the cached
+ *   step; the cost is one more forward of every layer but the last.
+ * Named buffers of the shared set read as "work.<name>" ("work.x_normed"). */
+enum { TA_ENGINE_RECOMPUTE = 1 };
+void* ta_engine_create_ex(const ta_model_config* model, const ta_adapt_config* adapt, int B, int T,
+                          void* stream, int flags);
 int ta_engine_destroy(void* engine);
 
 /* Upload one base tensor by its HF name (e.g. "model.layers.3.mlp.up_proj.weight"),

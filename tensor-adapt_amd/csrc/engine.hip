@@ -64,6 +64,10 @@ struct Engine {
     ta_adapt_config ac;
     int B, T, BT, H, qd, kvd, I, V, r;
     float scale;  // alpha / r
+    // per-layer activation recompute: only each layer's input (res_in) is
+    // kept per layer; the other cached activations live in one shared set
+    // that the backward refills by rerunning the layer's forward
+    bool recompute = false;
     hipStream_t s = nullptr;
     bool own_stream = false;
     std::vector<void*> allocs;
@@ -257,6 +261,16 @@ static int engine_alloc(Engine* e) {
         }
         if (I % 128 == 0) CK(alloc(e, &ly.Wgu, (int64_t)2 * I * H, "wgu"));
         CK(alloc(e, &ly.res_in, (int64_t)BT * H, (p + "res_in").c_str(), 0));
+        if (e->recompute && l > 0) {
+            // the shared activation set of layer 0 ("work." buffers)
+            const Layer& l0 = e->L[0];
+            ly.in_rms = l0.in_rms, ly.xn = l0.xn, ly.Q = l0.Q, ly.K = l0.K, ly.V = l0.V;
+            ly.ao = l0.ao, ly.attn_st = l0.attn_st, ly.ao32 = l0.ao32, ly.res_mid = l0.res_mid;
+            ly.post_rms = l0.post_rms, ly.xn2 = l0.xn2, ly.gate = l0.gate, ly.up = l0.up;
+            ly.act = l0.act;
+            continue;
+        }
+        if (e->recompute) p = "work.";
         CK(alloc(e, &ly.in_rms, BT, (p + "in_rms").c_str(), 1));
         CK(alloc(e, &ly.xn, (int64_t)BT * H, (p + "x_normed").c_str(), 0));
         CK(alloc(e, &ly.Q, (int64_t)BT * qd, (p + "Q").c_str(), 0));
@@ -578,10 +592,65 @@ static float cosine_lr(float base, int64_t warmup, int64_t total, float floor_fr
     return cs.lr_at((size_t)step);
 }
 
-static int forward(Engine* e) {
+// One layer's forward (qwen2.cu:80-157) from its normed input ly.xn up to
+// act and the down pair's h: everything the layer's backward reads.  The
+// down projection and the residual add follow in forward().
+static int layer_fwd_body(Engine* e, Layer& ly) {
     const ta_model_config& c = e->mc;
     const int BT = e->BT, H = e->H, qd = e->qd, kvd = e->kvd, I = e->I;
     const double dBT = BT, tri = (double)e->B * c.n_q * e->T * (e->T + 1) / 2.0;
+    hipStream_t s = e->s;
+    const double nrm_b = dBT * H * 4 + H * 2 + dBT * 4;
+    CK(lora_group_h(e, ly, {PQ, PK, PV}, ly.xn, H));
+    {
+        // q, k and v projections (qwen2.cu:21-30, each with its bias and
+        // LoRA delta) in one launch over the three weight matrices
+        LoraEpi eq = fwd_epi(e, ly.pr[PQ]), ek = fwd_epi(e, ly.pr[PK]), ev = fwd_epi(e, ly.pr[PV]);
+        const GemmGroup gr[3] = {{qd, ly.W[PQ], ly.Q, qd, ly.bias[0], &eq},
+                                 {kvd, ly.W[PK], ly.K, kvd, ly.bias[1], &ek},
+                                 {kvd, ly.W[PV], ly.V, kvd, ly.bias[2], &ev}};
+        TIMED(TA_CAT_GEMM_FWD, gflops(BT, qd + 2.0 * kvd, H),
+              gbytes(BT, qd + 2.0 * kvd, H, 2, 2, false),
+              gemm_groups(BT, H, ly.xn, H, H, gr, 3, s));
+    }
+    TIMED(TA_CAT_ELEMWISE, 0, dBT * qd * 4,
+          ta_rope_fwd(ly.Q, e->B, e->T, c.n_q, c.head_dim, c.rope_theta, s));
+    TIMED(TA_CAT_ELEMWISE, 0, dBT * kvd * 4,
+          ta_rope_fwd(ly.K, e->B, e->T, c.n_kv, c.head_dim, c.rope_theta, s));
+    // sdpa_fwd (ops.cu:578-681) without the probabilities buffer: the
+    // rows' (max, 1/sum) are kept instead
+    TIMED(TA_CAT_ATTN_FWD, 4.0 * tri * c.head_dim,
+          dBT * (2.0 * qd + 2.0 * kvd) * 2 + dBT * qd * 4 + 8.0 * e->B * c.n_q * e->T,
+          attn_fwd(ly.Q, ly.K, ly.V, ly.ao, ly.ao32, nullptr, ly.attn_st, e->B, e->T, c.n_q,
+                   c.n_kv, c.head_dim, false, s));
+    CK(lora_group_h(e, ly, {PO}, ly.ao, qd));
+    {
+        LoraEpi eo = fwd_epi(e, ly.pr[PO]);
+        CK(proj_fwd(e, ly.W[PO], ly.ao, e->tmpH, qd, H, nullptr, &eo));
+    }
+    // res_mid = bf16(res_in + o_proj) and its post-attention norm, one pass
+    TIMED(TA_CAT_NORM, 0, nrm_b + dBT * H * 4,
+          rms_fwd_res(ly.res_in, e->tmpH, ly.res_mid, ly.post_norm, ly.xn2, ly.post_rms, BT, H,
+                      c.rms_eps, s));
+    CK(lora_group_h(e, ly, {PG, PU}, ly.xn2, H));
+    {
+        // gate and up projections (qwen2.cu:21-30, each with its LoRA
+        // delta) and act = silu_mul_fwd(gate, up) (ops.cu:913-923) in one
+        // launch over the interleaved gate/up weights
+        LoraEpi eg = fwd_epi(e, ly.pr[PG]), eu = fwd_epi(e, ly.pr[PU]);
+        TIMED(TA_CAT_GEMM_FWD, 2.0 * gflops(BT, I, H),
+              2.0 * gbytes(BT, I, H, 2, 2, false) + dBT * I * 2,
+              gemm_swiglu(BT, H, ly.xn2, H, ly.Wgu, ly.W[PG], ly.W[PU], ly.gate, ly.up, ly.act,
+                          I, &eg, &eu, s));
+    }
+    CK(lora_group_h(e, ly, {PD}, ly.act, I));
+    return 0;
+}
+
+static int forward(Engine* e) {
+    const ta_model_config& c = e->mc;
+    const int BT = e->BT, H = e->H, I = e->I;
+    const double dBT = BT;
     hipStream_t s = e->s;
     TIMED(TA_CAT_ELEMWISE, 0, dBT * H * 4, ta_embed_fwd(e->embed, e->tok_cur, e->L[0].res_in, BT, H, s));
     const double nrm_b = dBT * H * 4 + H * 2 + dBT * 4;
@@ -593,49 +662,7 @@ static int forward(Engine* e) {
         if (l == 0)
             TIMED(TA_CAT_NORM, 0, nrm_b,
                   ta_rms_norm_fwd(ly.res_in, ly.in_norm, ly.xn, ly.in_rms, 1, BT, H, c.rms_eps, s));
-        CK(lora_group_h(e, ly, {PQ, PK, PV}, ly.xn, H));
-        {
-            // q, k and v projections (qwen2.cu:21-30, each with its bias and
-            // LoRA delta) in one launch over the three weight matrices
-            LoraEpi eq = fwd_epi(e, ly.pr[PQ]), ek = fwd_epi(e, ly.pr[PK]), ev = fwd_epi(e, ly.pr[PV]);
-            const GemmGroup gr[3] = {{qd, ly.W[PQ], ly.Q, qd, ly.bias[0], &eq},
-                                     {kvd, ly.W[PK], ly.K, kvd, ly.bias[1], &ek},
-                                     {kvd, ly.W[PV], ly.V, kvd, ly.bias[2], &ev}};
-            TIMED(TA_CAT_GEMM_FWD, gflops(BT, qd + 2.0 * kvd, H),
-                  gbytes(BT, qd + 2.0 * kvd, H, 2, 2, false),
-                  gemm_groups(BT, H, ly.xn, H, H, gr, 3, s));
-        }
-        TIMED(TA_CAT_ELEMWISE, 0, dBT * qd * 4,
-              ta_rope_fwd(ly.Q, e->B, e->T, c.n_q, c.head_dim, c.rope_theta, s));
-        TIMED(TA_CAT_ELEMWISE, 0, dBT * kvd * 4,
-              ta_rope_fwd(ly.K, e->B, e->T, c.n_kv, c.head_dim, c.rope_theta, s));
-        // sdpa_fwd (ops.cu:578-681) without the probabilities buffer: the
-        // rows' (max, 1/sum) are kept instead
-        TIMED(TA_CAT_ATTN_FWD, 4.0 * tri * c.head_dim,
-              dBT * (2.0 * qd + 2.0 * kvd) * 2 + dBT * qd * 4 + 8.0 * e->B * c.n_q * e->T,
-              attn_fwd(ly.Q, ly.K, ly.V, ly.ao, ly.ao32, nullptr, ly.attn_st, e->B, e->T, c.n_q,
-                       c.n_kv, c.head_dim, false, s));
-        CK(lora_group_h(e, ly, {PO}, ly.ao, qd));
-        {
-            LoraEpi eo = fwd_epi(e, ly.pr[PO]);
-            CK(proj_fwd(e, ly.W[PO], ly.ao, e->tmpH, qd, H, nullptr, &eo));
-        }
-        // res_mid = bf16(res_in + o_proj) and its post-attention norm, one pass
-        TIMED(TA_CAT_NORM, 0, nrm_b + dBT * H * 4,
-              rms_fwd_res(ly.res_in, e->tmpH, ly.res_mid, ly.post_norm, ly.xn2, ly.post_rms, BT, H,
-                          c.rms_eps, s));
-        CK(lora_group_h(e, ly, {PG, PU}, ly.xn2, H));
-        {
-            // gate and up projections (qwen2.cu:21-30, each with its LoRA
-            // delta) and act = silu_mul_fwd(gate, up) (ops.cu:913-923) in one
-            // launch over the interleaved gate/up weights
-            LoraEpi eg = fwd_epi(e, ly.pr[PG]), eu = fwd_epi(e, ly.pr[PU]);
-            TIMED(TA_CAT_GEMM_FWD, 2.0 * gflops(BT, I, H),
-                  2.0 * gbytes(BT, I, H, 2, 2, false) + dBT * I * 2,
-                  gemm_swiglu(BT, H, ly.xn2, H, ly.Wgu, ly.W[PG], ly.W[PU], ly.gate, ly.up, ly.act,
-                              I, &eg, &eu, s));
-        }
-        CK(lora_group_h(e, ly, {PD}, ly.act, I));
+        CK(layer_fwd_body(e, ly));
         {
             LoraEpi ed = fwd_epi(e, ly.pr[PD]);
             CK(proj_fwd(e, ly.W[PD], ly.act, e->tmpH, I, H, nullptr, &ed));
@@ -674,6 +701,15 @@ static int backward(Engine* e) {
                           BT, H, c.rms_eps, s));
     for (int l = c.layers - 1; l >= 0; l--) {
         Layer& ly = e->L[l];
+        if (e->recompute && l + 1 < c.layers) {
+            // refill the shared activation set with this layer's forward
+            // (the last layer's is still there from the forward).  The
+            // input norm gives the same bits as the fused residual-add form
+            // that made it in the forward: both normalise the stored BF16 row.
+            TIMED(TA_CAT_NORM, 0, dBT * H * 4 + H * 2 + dBT * 4,
+                  ta_rms_norm_fwd(ly.res_in, ly.in_norm, ly.xn, ly.in_rms, 1, BT, H, c.rms_eps, s));
+            CK(layer_fwd_body(e, ly));
+        }
         // FFN (qwen2.cu:222-246)
         const bool fused = e->silu_fused && ly.pr[PG].on && ly.pr[PU].on;
         float* ga_down = nullptr;  // the down pair's gA partials, made by the fused kernel
@@ -898,7 +934,12 @@ extern "C" {
 
 void* ta_engine_create(const ta_model_config* mc, const ta_adapt_config* ac, int B, int T,
                        void* stream) {
-    if (!mc || !ac || B <= 0 || T <= 0) {
+    return ta_engine_create_ex(mc, ac, B, T, stream, 0);
+}
+
+void* ta_engine_create_ex(const ta_model_config* mc, const ta_adapt_config* ac, int B, int T,
+                          void* stream, int flags) {
+    if (!mc || !ac || B <= 0 || T <= 0 || (flags & ~TA_ENGINE_RECOMPUTE) != 0) {
         set_error(-1, "engine_create: bad arguments");
         return nullptr;
     }
@@ -920,6 +961,7 @@ void* ta_engine_create(const ta_model_config* mc, const ta_adapt_config* ac, int
     e->V = mc->vocab;
     e->r = ac->rank;
     e->scale = ac->alpha / (float)ac->rank;  // adapter_model.cu:139
+    e->recompute = (flags & TA_ENGINE_RECOMPUTE) != 0;
     if (stream) {
         e->s = (hipStream_t)stream;
     } else {

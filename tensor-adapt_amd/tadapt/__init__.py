@@ -163,11 +163,15 @@ WHICH = {"A": 0, "B": 1, "mA": 2, "vA": 3, "mB": 4, "vB": 5, "gA": 6, "gB": 7,
 class Engine:
     """Owner of one ta_engine_* handle (the MI355X LoRA step)."""
 
-    def __init__(self, model: dict, adapt: dict, B: int, T: int):
+    RECOMPUTE = 1  # TA_ENGINE_RECOMPUTE
+
+    def __init__(self, model: dict, adapt: dict, B: int, T: int, recompute: bool = False):
         self.mc = ModelConfig(**model)
         self.ac = AdaptConfig(**adapt)
         self.B, self.T = B, T
-        h = lib().ta_engine_create(ctypes.byref(self.mc), ctypes.byref(self.ac), B, T, None)
+        self.recompute = bool(recompute)
+        h = lib().ta_engine_create_ex(ctypes.byref(self.mc), ctypes.byref(self.ac), B, T, None,
+                                      self.RECOMPUTE if recompute else 0)
         if not h:
             raise BackendError("ta_engine_create failed: " + last_error())
         self.h = h

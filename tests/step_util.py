@@ -18,6 +18,8 @@ def base_tensors(mc, seed):
     one = lambda n: O.bf16_from_f32(np.ones(n, np.float32))
     zero = lambda n: np.zeros(n, np.uint16)
     t = {"model.embed_tokens.weight": w(V, H), "model.norm.weight": one(H)}
+    if not mc.get("tie", 1):
+        t["lm_head.weight"] = w(V, H)
     for l in range(mc["layers"]):
         p = f"model.layers.{l}."
         t[p + "input_layernorm.weight"] = one(H)
@@ -35,11 +37,11 @@ def base_tensors(mc, seed):
     return t
 
 
-def make_pair(mc, ac, B, T, seed):
+def make_pair(mc, ac, B, T, seed, recompute=False):
     tensors = base_tensors(mc, seed)
     orc = O.OracleModel(mc, ac)
     import tadapt
-    eng = tadapt.Engine(mc, ac, B, T)
+    eng = tadapt.Engine(mc, ac, B, T, recompute=recompute)
     for name, arr in tensors.items():
         orc.set_weight(name, arr)
         eng.set_weight(name, arr)

@@ -1,0 +1,167 @@
+"""Per-layer activation recompute (TA_ENGINE_RECOMPUTE) and the
+Qwen2-7B-shaped config (H=3584, 28 Q / 4 KV heads, head_dim 128,
+I=18944, V=152064 untied, LoRA r=64 alpha=128 on all seven projections,
+B=4 x T=2048).
+
+- Recompute changes only where activations live, so the step must give the
+  cached step's bits: loss, norm, every gradient, master, moment and the
+  centroid sums are compared for equality, at small shapes (rank 16 with the
+  fused LoRA kernels, rank 64 with the generic ones) and at the 7B layer
+  shapes.
+- The 7B layer shapes at rank 64 against the CPU oracle (one layer, T=2048,
+  the full vocabulary), to the step bars: loss 1e-3 relative, gradients
+  1e-2 relative L2.
+- The whole 28-layer 7B-shaped step with recompute, through properties that
+  hold at any size: B = 0 at the first step makes every gA exactly zero and
+  every gB nonzero and finite; with logits x W^T of unit-RMS rows x and
+  W ~ N(0, 0.02^2), the initial loss is ln V + sigma^2/2 with
+  sigma^2 = 0.02^2 * H (Gaussian logits, V >> 1); AdamW's first update
+  of B is -lr * g / (|g| + eps) element by element.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+import tadapt
+from step_util import base_tensors, make_pair, pairs, rel
+from test_gpu_step import check_adamw_of_own_grads, compare, snapshot, sync_state
+
+pytestmark = pytest.mark.gpu
+
+C4_MODEL = dict(vocab=152064, hidden=3584, layers=28, n_q=28, n_kv=4, head_dim=128, inter=18944,
+                rms_eps=1e-6, rope_theta=1e6, tie=0)
+C4_ADAPT = dict(rank=64, alpha=128.0, inject_mask=0b1111111, lr=1e-4, grad_clip=1.0, warmup=0,
+                total_steps=20, b1=0.9, b2=0.999, eps=1e-8, wd=0.01)
+SMALL_MODEL = dict(vocab=2048, hidden=256, layers=3, n_q=4, n_kv=2, head_dim=64, inter=512,
+                   rms_eps=1e-6, rope_theta=1e6, tie=1)
+SMALL_ADAPT = dict(rank=16, alpha=32.0, inject_mask=0b1111111, lr=1e-3, grad_clip=1.0, warmup=1,
+                   total_steps=4, b1=0.9, b2=0.999, eps=1e-8, wd=0.01)
+STATE = ("A", "B", "gA", "gB", "mA", "vA", "mB", "vB", "A16", "B16")
+
+
+# after a step both engines hold layer 0's activations and backward scratch
+LAYER0 = ("in_rms", "x_normed", "Q", "K", "V", "attn_out", "attn_stats", "attn_out32", "res_mid",
+          "post_rms", "x_normed2", "gate", "up", "act")
+SCRATCH = ("dx_normed", "dQ", "dK", "dV", "dattn_out", "dx_normed2", "grad", "logits", "loss_tok")
+
+
+def assert_same_bits(e1, e2, mc, ac):
+    for l, t in pairs(mc, ac):
+        for w in STATE:
+            a, b = e1.adapter(l, t, w), e2.adapter(l, t, w)
+            assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), (l, t, w)
+    bad = [n for n in LAYER0
+           if not np.array_equal(e1.read_buffer("l0." + n), e2.read_buffer("work." + n))]
+    bad += [n for n in SCRATCH if not np.array_equal(e1.read_buffer(n), e2.read_buffer(n))]
+    assert not bad, bad
+    (c1, w1), (c2, w2) = e1.centroid(), e2.centroid()
+    assert np.array_equal(c1, c2) and w1 == w2 and w1 > 0
+
+
+def run_identical(mc, ac, B, T, steps, seed, init_random=False):
+    engines = []
+    for rc in (False, True):
+        e = tadapt.Engine(mc, ac, B, T, recompute=rc)
+        if init_random:
+            e.init_random(seed)
+        else:
+            for name, arr in base_tensors(mc, seed).items():
+                e.set_weight(name, arr)
+        engines.append(e)
+    rng = np.random.default_rng(seed + 1)
+    for step in range(steps):
+        toks = rng.integers(0, mc["vocab"], B * T + 1).astype(np.int32)
+        inp, tgt = toks[:-1].copy(), toks[1:].copy()
+        m0, m1 = engines[0].step(inp, tgt), engines[1].step(inp, tgt)
+        print(f"step {step}: loss {m0['loss']:.6f} / {m1['loss']:.6f}", flush=True)
+        for k in ("loss", "gnorm_raw", "valid_tokens", "lr"):
+            assert m0[k] == m1[k], (step, k, m0[k], m1[k])
+        assert_same_bits(engines[0], engines[1], mc, ac)
+    for e in engines:
+        e.close()
+
+
+@pytest.mark.parametrize("rank", [16, 64])
+def test_recompute_bit_identical_small(rank):
+    ac = dict(SMALL_ADAPT, rank=rank, alpha=2.0 * rank)
+    run_identical(SMALL_MODEL, ac, 2, 256, 3, seed=5)
+
+
+def test_recompute_bit_identical_c4_layer_shapes():
+    """Three 7B-shaped layers (the middle one sits between two recomputed
+    neighbours) at B=4 x T=2048, rank 64, untied head, two steps."""
+    mc = dict(C4_MODEL, layers=3)
+    run_identical(mc, C4_ADAPT, 4, 2048, 2, seed=9, init_random=True)
+
+
+def span_tokens(B, T, rng):
+    """Uniform ids with one assistant span (<|im_start|> assistant ...
+    <|im_end|>) over almost every row, so the trainer's masking keeps
+    nearly all targets."""
+    toks = rng.integers(0, 150000, B * T + 1).astype(np.int32)
+    for b in range(B):
+        toks[b * T + 3], toks[b * T + 4] = 151644, 77091
+        toks[b * T + T - 8] = 151645
+    return toks
+
+
+def test_c4_layer_matches_oracle():
+    """One 7B-shaped layer at T=2048 and rank 64 (generic-rank LoRA paths:
+    rank updates after the projection GEMMs, per-pair dh/gB/gA products,
+    unfused SwiGLU backward), untied LM head over the full 152064 ids, with
+    recompute on.  Step 2 starts from the oracle's state after step 1, so gA
+    is checked with B != 0.  Clipping is off here (the clip is checked by
+    the AdamW test and the smaller step tests) so both steps compare raw
+    gradients.
+
+    The targets are kept (assistant spans): with every target masked the
+    gradient is softmax(logits)/BT alone, whose sensitivity to one-ulp BF16
+    differences in logits of std 0.02 * sqrt(3584) = 1.2 puts the q/k
+    gradients of any two BF16 pipelines about 1.1e-2 apart (measured; the
+    7B layer's other gradients 3e-3 to 6e-3)."""
+    mc = dict(C4_MODEL, layers=1)
+    ac, B, T = dict(C4_ADAPT, grad_clip=1e3), 1, 2048
+    orc, eng = make_pair(mc, ac, B, T, seed=23, recompute=True)
+    rng = np.random.default_rng(29)
+    for step in range(2):
+        sync_state(orc, eng, mc, ac)
+        state = snapshot(orc, mc, ac)
+        toks = span_tokens(B, T, rng)
+        inp, tgt = toks[:-1].copy(), toks[1:].copy()
+        so = orc.step(inp, tgt, B, T)
+        sg = eng.step(inp, tgt)
+        print(f"step {step}: loss {sg['loss']:.6f} oracle {so['loss']:.6f}", flush=True)
+        assert abs(sg["loss"] - so["loss"]) <= 1e-3 * abs(so["loss"]), (step, sg, so)
+        assert abs(sg["gnorm_raw"] - so["gnorm_raw"]) <= 1e-2 * so["gnorm_raw"], (step, sg, so)
+        assert so["gnorm_raw"] <= ac["grad_clip"]
+        compare(orc, eng, mc, ac, ("gB",) if step == 0 else ("gA", "gB"))
+        check_adamw_of_own_grads(eng, mc, ac, state, sg["lr"], step + 1, sg["gnorm_raw"])
+    eng.close()
+
+
+def test_c4_full_step_properties():
+    mc, ac, B, T = C4_MODEL, C4_ADAPT, 4, 2048
+    eng = tadapt.Engine(mc, ac, B, T, recompute=True)
+    eng.init_random(31)
+    rng = np.random.default_rng(37)
+    toks = rng.integers(0, mc["vocab"], B * T + 1).astype(np.int32)
+    m = eng.step(toks[:-1].copy(), toks[1:].copy(), lr_override=ac["lr"])
+    print(f"c4 step: loss {m['loss']:.5f} gnorm {m['gnorm_raw']:.4e} {m['step_ms']:.1f} ms",
+          flush=True)
+    expect = math.log(mc["vocab"]) + 0.5 * 0.02 ** 2 * mc["hidden"]
+    assert abs(m["loss"] - expect) <= 0.02 * expect, (m["loss"], expect)
+    assert m["valid_tokens"] == B * T
+    for l, t in pairs(mc, ac):
+        gA, gB = eng.adapter(l, t, "gA"), eng.adapter(l, t, "gB")
+        assert not np.any(gA), (l, t)
+        assert np.all(np.isfinite(gB)) and np.any(gB), (l, t)
+        # first AdamW update of B (zero moments, B = 0): m_hat = g and
+        # sqrt(v_hat) = |g|, so B = -lr * g / (|g| + eps) with g the clipped
+        # gradient (weight decay acts on B = 0)
+        b = eng.adapter(l, t, "B").astype(np.float64)
+        g = gB.astype(np.float64) * min(1.0, ac["grad_clip"] / (m["gnorm_raw"] + 1e-6))
+        want = -ac["lr"] * g / (np.abs(g) + ac["eps"])
+        np.testing.assert_allclose(b, want, rtol=1e-4, atol=1e-6 * ac["lr"])
+    eng.close()
