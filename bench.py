@@ -151,13 +151,106 @@ def cpu_baseline(model, adapt, cname="c3"):
                        % (cname, t_layer, cname, t_head, model["layers"]))}
 
 
+C5 = dict(tokens=4 << 20, dim=512, chunk=65536, comps=16, k=32, iters=25)
+C5_WORK = ("c5: centroid accumulator + merge stress, 4M F32 hidden states of dim 512 from a "
+           "16-component Gaussian mixture, lognormal gradient norms, 64 cumulative snapshots, "
+           "k-means++ k=32 with 25 Lloyd iterations")
+
+
+def bench_c5(args):
+    """c5: the Centroid Accumulator over 4M token states resident in HBM
+    (one ta_centroid_accumulate_f32n call per 65536-token snapshot, each
+    snapshot's sums copied to host memory), then the k-means merge on the 64
+    snapshots.  A step is the whole job; tokens/s = 4M / step time.  The
+    roofline is the accumulate call (partial-row and reduce launches),
+    timed with events on the stream it is launched on; algorithmic bytes
+    per call = chunk * (dim + 1) * 4 (h and n read once)."""
+    import ctypes
+    import numpy as np
+    import torch
+    import tadapt
+    c = C5
+    nchunk = c["tokens"] // c["chunk"]
+    g = torch.Generator(device="cuda")
+    g.manual_seed(2026)
+    means = torch.randn(c["comps"], c["dim"], generator=g, device="cuda")
+    h = torch.empty(c["tokens"], c["dim"], device="cuda")
+    for i in range(nchunk):
+        sl = slice(i * c["chunk"], (i + 1) * c["chunk"])
+        lab = torch.randint(0, c["comps"], (c["chunk"],), generator=g, device="cuda")
+        h[sl] = means[lab] + 0.3 * torch.randn(c["chunk"], c["dim"], generator=g, device="cuda")
+    n = torch.exp(torch.randn(c["tokens"], generator=g, device="cuda"))  # lognormal(0, 1)
+    acc = torch.zeros(c["dim"] + 1, dtype=torch.float64, device="cuda")
+    snap_acc = torch.empty(nchunk, c["dim"] + 1, dtype=torch.float64, pin_memory=True)
+    C = torch.empty(c["k"] * c["dim"], device="cuda")
+    A = torch.empty(nchunk, dtype=torch.int32, device="cuda")
+    M = torch.empty(c["k"], dtype=torch.float64, device="cuda")
+    Sd = torch.empty(c["k"], dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream()
+    sp = stream.cuda_stream
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(nchunk)]
+
+    def job(timed):
+        acc.zero_()
+        for i in range(nchunk):
+            off = i * c["chunk"]
+            if timed:
+                ev[i][0].record(stream)
+            tadapt.call("ta_centroid_accumulate_f32n", h[off].data_ptr(), n[off:].data_ptr(),
+                        c["chunk"], c["dim"], acc.data_ptr(), sp)
+            if timed:
+                ev[i][1].record(stream)
+            snap_acc[i].copy_(acc, non_blocking=True)
+        torch.cuda.synchronize()
+        a = snap_acc.numpy()
+        X = torch.from_numpy((a[:, :-1] / a[:, -1:]).astype(np.float32)).cuda()
+        W = torch.from_numpy(a[:, -1].astype(np.float32)).cuda()
+        tadapt.call("ta_kmeans_pp", X.data_ptr(), W.data_ptr(), nchunk, c["dim"], c["k"],
+                    c["iters"], ctypes.c_uint64(5), C.data_ptr(), A.data_ptr(), M.data_ptr(),
+                    Sd.data_ptr(), sp)
+
+    for _ in range(args.warmup):
+        job(False)
+    launch_ms = 0.0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        job(True)
+        torch.cuda.synchronize()
+        launch_ms += sum(a.elapsed_time(b) for a, b in ev)
+    dt = time.perf_counter() - t0
+    calls = nchunk * args.steps
+    per_call = launch_ms / calls
+    bytes_call = c["chunk"] * (c["dim"] + 1) * 4
+    achieved = bytes_call / (per_call * 1e-3) / 1e9
+    out = {
+        "metric": "c5 centroid accumulate + merge tokens/s",
+        "value": round(c["tokens"] * args.steps / dt, 1),
+        "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / args.steps, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32/f64",
+        "data": "synthetic (seeded Gaussian mixture generated on the device)",
+        "config": {"workload": C5_WORK, "tokens": c["tokens"], "dim": c["dim"],
+                   "snapshots": nchunk, "k": c["k"], "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "ta::k_centroid_part<false> + ta::k_centroid_reduce (one call)",
+                     "launches": calls, "avg_launch_us": round(per_call * 1e3, 1),
+                     "algorithmic_per_launch": {"bytes": bytes_call},
+                     "share_of_step": round(launch_ms * 1e-3 / dt, 4)},
+        "mass_top3": [round(float(x), 3) for x in M.cpu().numpy()[:3]],
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--config", choices=sorted(CONFIGS), default="c3",
+    ap.add_argument("--config", choices=sorted(CONFIGS) + ["c5"], default="c3",
                     help="workload (default c3, the headline metric's config)")
     ap.add_argument("--categories", action="store_true",
                     help="print the per-kernel-class time split to stderr")
@@ -169,6 +262,8 @@ def main():
               f"--gpus {args.gpus} is not supported", file=sys.stderr)
         sys.exit(2)
 
+    if args.config == "c5":
+        return bench_c5(args)
     import torch
     import tadapt
 
