@@ -6,9 +6,10 @@
 // The reference synchronises, copies two [BT, D] F32 tensors to the host per
 // layer and loops on one core.  Here one launch reads h and g once (BF16,
 // straight from the step's activations, no cast kernels), each block folds
-// kTok tokens into an F32 partial row, and a second launch adds the partial
-// rows in block order into an F64 accumulator [D+1] (entry D holds W).  The
-// result is deterministic and within 1e-7 relative of an F64 evaluation.
+// 16 (BF16) or 64 (F32) tokens into an F32 partial row, and a second launch
+// adds the partial rows in block order into an F64 accumulator [D+1] (entry
+// D holds W).  The result is deterministic and within 1e-7 relative of an
+// F64 evaluation.
 //
 // k-means (centroid_accumulator.cpp:114-157 and the stress mode): one
 // workgroup runs every iteration in a single launch.  Squared distances are
@@ -22,23 +23,25 @@
 
 namespace ta {
 
-constexpr int kTok = 16;  // tokens per block in the accumulate pass (512 blocks at BT = 8192)
+constexpr int kTok = 16;   // tokens per block, BF16 inputs (512 blocks at BT = 8192)
+constexpr int kTokF = 64;  // tokens per block, F32 inputs (1024 blocks per 65536 tokens)
 
 // Per-block partial row: part[blk][d] = sum_{t in block} h[t][d] * n_t,
 // part[blk][D] = sum n_t.  Rows move as 16-byte vectors when D % 8 == 0.
-template <bool BF16IN>
+template <bool BF16IN, int KT = BF16IN ? kTok : kTokF>
 __global__ __launch_bounds__(256) void k_centroid_part(const void* __restrict__ hv,
                                                        const void* __restrict__ gv,
                                                        const float* __restrict__ nv,
                                                        int64_t BT, int D,
                                                        float* __restrict__ part) {
-    __shared__ float nrm[kTok];
-    int64_t t0 = (int64_t)blockIdx.x * kTok;
+    __shared__ float nrm[KT];
+    int64_t t0 = (int64_t)blockIdx.x * KT;
     int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const bool v8 = BF16IN && (D & 7) == 0;
+    const bool v4 = !BF16IN && (D & 3) == 0;
     // 1. per-token gradient norms (one wave per token; a wave's 16-byte
     // loads of its rows are issued together)
-    for (int j = wv; j < kTok; j += 4) {
+    for (int j = wv; j < KT; j += 4) {
         int64_t t = t0 + j;
         float ss = 0.f;
         if (t < BT && !nv) {
@@ -67,6 +70,15 @@ __global__ __launch_bounds__(256) void k_centroid_part(const void* __restrict__ 
                     float f = bf2f(g[d]);
                     ss += f * f;
                 }
+            } else if (v4) {
+                const float4* g = (const float4*)((const float*)gv + t * D);
+                for (int c = lane; c < (D >> 2); c += 64) {
+                    const float4 f = g[c];
+                    ss += f.x * f.x;
+                    ss += f.y * f.y;
+                    ss += f.z * f.z;
+                    ss += f.w * f.w;
+                }
             } else {
                 const float* g = (const float*)gv + t * D;
                 for (int d = lane; d < D; d += 64) ss += g[d] * g[d];
@@ -81,16 +93,16 @@ __global__ __launch_bounds__(256) void k_centroid_part(const void* __restrict__ 
     if (v8) {
         for (int c = threadIdx.x; c < (D >> 3); c += 256) {
             float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            // all kTok row loads first (rows past BT re-read the last row;
+            // all KT row loads first (rows past BT re-read the last row;
             // their weight is 0), then the sums in token order
-            bf16x8v hh[kTok];
+            bf16x8v hh[KT];
 #pragma unroll
-            for (int j = 0; j < kTok; j++) {
+            for (int j = 0; j < KT; j++) {
                 const int64_t t = min(t0 + j, BT - 1);
                 hh[j] = ((const bf16x8v*)((const bf16*)hv + t * D))[c];
             }
 #pragma unroll
-            for (int j = 0; j < kTok; j++) {
+            for (int j = 0; j < KT; j++) {
                 float f[8];
                 unpack8(hh[j], f);
 #pragma unroll
@@ -99,10 +111,37 @@ __global__ __launch_bounds__(256) void k_centroid_part(const void* __restrict__ 
 #pragma unroll
             for (int e = 0; e < 8; e++) out[c * 8 + e] = acc[e];
         }
+    } else if (v4) {
+        // F32 rows as 16-byte vectors; 16 row loads in flight per batch,
+        // sums in token order
+        for (int c = threadIdx.x; c < (D >> 2); c += 256) {
+            float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int j0 = 0; j0 < KT; j0 += 16) {
+                float4 hh[16];
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    const int64_t t = min(t0 + j0 + j, BT - 1);
+                    hh[j] = ((const float4*)((const float*)hv + t * D))[c];
+                }
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    const float w = nrm[j0 + j];
+                    acc.x += hh[j].x * w;
+                    acc.y += hh[j].y * w;
+                    acc.z += hh[j].z * w;
+                    acc.w += hh[j].w * w;
+                }
+            }
+            // (partial rows are D + 1 floats apart: 4-byte stores)
+            out[4 * c + 0] = acc.x;
+            out[4 * c + 1] = acc.y;
+            out[4 * c + 2] = acc.z;
+            out[4 * c + 3] = acc.w;
+        }
     } else {
         for (int d = threadIdx.x; d < D; d += 256) {
             float acc = 0.f;
-            for (int j = 0; j < kTok; j++) {
+            for (int j = 0; j < KT; j++) {
                 int64_t t = t0 + j;
                 if (t >= BT) break;
                 float h = BF16IN ? bf2f(((const bf16*)hv)[t * D + d]) : ((const float*)hv)[t * D + d];
@@ -113,21 +152,23 @@ __global__ __launch_bounds__(256) void k_centroid_part(const void* __restrict__ 
     }
     if (threadIdx.x == 0) {
         float w = 0.f;
-        for (int j = 0; j < kTok; j++) w += nrm[j];
+        for (int j = 0; j < KT; j++) w += nrm[j];
         out[D] = w;
     }
 }
 
 // acc[d] += sum over blocks of part[b][d], in F64: 64 columns per block
-// (lane = column), wave w sums the blocks of its quarter in block order and
-// the four quarter sums are added in wave order — a fixed order, so the
-// result is deterministic.
-__global__ __launch_bounds__(256) void k_centroid_reduce(const float* __restrict__ part, int nblk,
-                                                         int D1, double* __restrict__ acc) {
-    __shared__ double q[4][64];
+// (lane = column), wave w of kRW sums the blocks of its slice in block order
+// and the slice sums are added in wave order — a fixed order, so the result
+// is deterministic.
+constexpr int kRW = 16;
+__global__ __launch_bounds__(64 * kRW) void k_centroid_reduce(const float* __restrict__ part,
+                                                              int nblk, int D1,
+                                                              double* __restrict__ acc) {
+    __shared__ double q[kRW][64];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int d = blockIdx.x * 64 + lane;
-    const int per = (nblk + 3) / 4, b0 = w * per, b1 = min(nblk, b0 + per);
+    const int per = (nblk + kRW - 1) / kRW, b0 = w * per, b1 = min(nblk, b0 + per);
     double s = 0.0;
     if (d < D1) {
 #pragma unroll 8
@@ -135,14 +176,37 @@ __global__ __launch_bounds__(256) void k_centroid_reduce(const float* __restrict
     }
     q[w][lane] = s;
     __syncthreads();
-    if (w == 0 && d < D1) acc[d] += ((q[0][lane] + q[1][lane]) + q[2][lane]) + q[3][lane];
+    if (w == 0 && d < D1) {
+        double t = q[0][lane];
+        for (int i = 1; i < kRW; i++) t += q[i][lane];
+        acc[d] += t;
+    }
 }
 
 // ── k-means ────────────────────────────────────────────────────────────
+// Squared distance summed sequentially over i in F32 without contraction.
+// Operands are loaded 32 elements at a time (independent loads in flight)
+// before the dependent chain over them; the order of the additions is the
+// plain loop's.
 __device__ __forceinline__ float sqdist_seq(const float* __restrict__ a,
                                            const float* __restrict__ b, int D) {
+    constexpr int CH = 32;
     float d = 0.f;
-    for (int i = 0; i < D; i++) {
+    int i = 0;
+    for (; i + CH <= D; i += CH) {
+        float av[CH], bv[CH];
+#pragma unroll
+        for (int j = 0; j < CH; j++) {
+            av[j] = a[i + j];
+            bv[j] = b[i + j];
+        }
+#pragma unroll
+        for (int j = 0; j < CH; j++) {
+            float v = __fsub_rn(av[j], bv[j]);
+            d = __fadd_rn(d, __fmul_rn(v, v));
+        }
+    }
+    for (; i < D; i++) {
         float v = __fsub_rn(a[i], b[i]);
         d = __fadd_rn(d, __fmul_rn(v, v));
     }
@@ -192,7 +256,25 @@ __device__ void kmeans_update(const float* __restrict__ X, float* __restrict__ C
         int c = p / D, d = p % D;
         float s = 0.f;
         int cnt = 0;
-        for (int n = 0; n < N; n++)
+        // members' values loaded 16 snapshots at a time, added in index order
+        constexpr int CH = 16;
+        int n = 0;
+        for (; n + CH <= N; n += CH) {
+            float xv[CH];
+            int av[CH];
+#pragma unroll
+            for (int j = 0; j < CH; j++) {
+                xv[j] = X[(int64_t)(n + j) * D + d];
+                av[j] = asg[n + j];
+            }
+#pragma unroll
+            for (int j = 0; j < CH; j++)
+                if (av[j] == c) {
+                    s = __fadd_rn(s, xv[j]);
+                    cnt++;
+                }
+        }
+        for (; n < N; n++)
             if (asg[n] == c) {
                 s = __fadd_rn(s, X[(int64_t)n * D + d]);
                 cnt++;
@@ -318,7 +400,8 @@ static int centroid_acc(const void* h, const void* g, const float* n, int64_t BT
     TA_REQUIRE(BT >= 0 && D > 0, "centroid_accumulate: bad shape BT=%lld D=%d", (long long)BT, D);
     if (BT == 0) return 0;
     hipStream_t s = (hipStream_t)stream;
-    int64_t nblk = (BT + kTok - 1) / kTok;
+    const int kt = bf16in ? kTok : kTokF;
+    int64_t nblk = (BT + kt - 1) / kt;
     TA_REQUIRE(nblk < (1ll << 31), "centroid_accumulate: BT too large");
     float* part = (float*)scratch_get((size_t)nblk * (D + 1) * sizeof(float), s);
     TA_REQUIRE(part, "centroid_accumulate: scratch allocation failed");
@@ -326,7 +409,7 @@ static int centroid_acc(const void* h, const void* g, const float* n, int64_t BT
         k_centroid_part<true><<<(int)nblk, 256, 0, s>>>(h, g, nullptr, BT, D, part);
     else
         k_centroid_part<false><<<(int)nblk, 256, 0, s>>>(h, g, n, BT, D, part);
-    k_centroid_reduce<<<(D + 1 + 63) / 64, 256, 0, s>>>(part, (int)nblk, D + 1, acc);
+    k_centroid_reduce<<<(D + 1 + 63) / 64, 64 * kRW, 0, s>>>(part, (int)nblk, D + 1, acc);
     return check_launch("centroid_accumulate");
 }
 
