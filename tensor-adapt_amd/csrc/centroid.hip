@@ -224,7 +224,7 @@ __device__ __forceinline__ double u01(uint64_t& s) {
 }
 
 // assignment pass: dist[n*k + c] for all pairs, then argmin per n (strict <)
-__device__ int kmeans_assign(const float* __restrict__ X, const float* __restrict__ C, int N,
+__device__ __forceinline__ int kmeans_assign(const float* __restrict__ X, const float* __restrict__ C, int N,
                              int D, int k, float* __restrict__ dist, int32_t* __restrict__ asg) {
     for (int p = threadIdx.x; p < N * k; p += blockDim.x)
         dist[p] = sqdist_seq(X + (int64_t)(p / k) * D, C + (int64_t)(p % k) * D, D);
@@ -250,7 +250,7 @@ __device__ int kmeans_assign(const float* __restrict__ X, const float* __restric
 
 // update pass: center c = mean of members (sequential over n); empty ->
 // zero (reference mode) or unchanged (stress mode)
-__device__ void kmeans_update(const float* __restrict__ X, float* __restrict__ C, int N, int D,
+__device__ __forceinline__ void kmeans_update(const float* __restrict__ X, float* __restrict__ C, int N, int D,
                               int k, const int32_t* __restrict__ asg, bool empty_to_zero) {
     for (int p = threadIdx.x; p < k * D; p += blockDim.x) {
         int c = p / D, d = p % D;
@@ -287,12 +287,28 @@ __device__ void kmeans_update(const float* __restrict__ X, float* __restrict__ C
     __syncthreads();
 }
 
-__global__ __launch_bounds__(1024) void k_kmeans_ref(const float* __restrict__ X, int N, int D,
+// Snapshots that fit kXs floats are copied into LDS once (XL): the
+// distance chains and the center sums then read them from LDS.
+constexpr int kXs = 32768;  // 128 KB
+
+template <bool XL>
+__device__ __forceinline__ const float* stage_snapshots(const float* __restrict__ Xg, float* xs,
+                                                        int N, int D) {
+    if constexpr (!XL) return Xg;
+    for (int p = threadIdx.x; p < N * D; p += blockDim.x) xs[p] = Xg[p];
+    __syncthreads();
+    return xs;
+}
+
+template <bool XL>
+__global__ __launch_bounds__(1024) void k_kmeans_ref(const float* __restrict__ Xg, int N, int D,
                                                      int k, int max_iters,
                                                      float* __restrict__ C,
                                                      int32_t* __restrict__ asg,
                                                      float* __restrict__ dist,
                                                      int32_t* __restrict__ iters_out) {
+    __shared__ float xs[XL ? kXs : 1];
+    const float* __restrict__ X = stage_snapshots<XL>(Xg, xs, N, D);
     for (int p = threadIdx.x; p < k * D; p += blockDim.x) {
         int c = p / D, d = p % D;
         C[p] = X[(int64_t)(((int64_t)c * N) / k) * D + d];
@@ -308,7 +324,8 @@ __global__ __launch_bounds__(1024) void k_kmeans_ref(const float* __restrict__ X
     if (threadIdx.x == 0 && iters_out) *iters_out = it;
 }
 
-__global__ __launch_bounds__(1024) void k_kmeans_pp(const float* __restrict__ X,
+template <bool XL>
+__global__ __launch_bounds__(1024) void k_kmeans_pp(const float* __restrict__ Xg,
                                                     const float* __restrict__ W, int N, int D,
                                                     int k, int iters, uint64_t seed,
                                                     float* __restrict__ Cw,  // [k*D] work
@@ -324,6 +341,8 @@ __global__ __launch_bounds__(1024) void k_kmeans_pp(const float* __restrict__ X,
     __shared__ int order[1024];
     __shared__ int rank_of[1024];
     __shared__ uint64_t rng;
+    __shared__ float xs[XL ? kXs : 1];
+    const float* __restrict__ X = stage_snapshots<XL>(Xg, xs, N, D);
     if (threadIdx.x == 0) {
         rng = seed;
         int first = (int)(u01(rng) * N);
@@ -439,7 +458,12 @@ int ta_kmeans_ref(const float* snaps, int N, int D, int k, int max_iters, float*
     hipStream_t s = (hipStream_t)stream;
     float* dist = (float*)scratch_get((size_t)N * k * sizeof(float), s);
     TA_REQUIRE(dist, "kmeans_ref: scratch allocation failed");
-    k_kmeans_ref<<<1, 1024, 0, s>>>(snaps, N, D, k, max_iters, centers, assign, dist, iters_out);
+    if ((int64_t)N * D <= kXs)
+        k_kmeans_ref<true><<<1, 1024, 0, s>>>(snaps, N, D, k, max_iters, centers, assign, dist,
+                                              iters_out);
+    else
+        k_kmeans_ref<false><<<1, 1024, 0, s>>>(snaps, N, D, k, max_iters, centers, assign, dist,
+                                               iters_out);
     return check_launch("kmeans_ref");
 }
 
@@ -457,9 +481,16 @@ int ta_kmeans_pp(const float* snaps, const float* weights, int N, int D, int k, 
     size_t total = off_asg + (size_t)N * sizeof(int32_t);
     char* base = (char*)scratch_get(total, s);
     TA_REQUIRE(base, "kmeans_pp: scratch allocation failed");
-    k_kmeans_pp<<<1, 1024, 0, s>>>(snaps, weights, N, D, k, iters, seed, (float*)base,
-                                   (float*)(base + off_d2), (float*)(base + off_dist),
-                                   (int32_t*)(base + off_asg), centers, assign, mass, seeds);
+    if ((int64_t)N * D <= kXs)
+        k_kmeans_pp<true><<<1, 1024, 0, s>>>(snaps, weights, N, D, k, iters, seed, (float*)base,
+                                             (float*)(base + off_d2), (float*)(base + off_dist),
+                                             (int32_t*)(base + off_asg), centers, assign, mass,
+                                             seeds);
+    else
+        k_kmeans_pp<false><<<1, 1024, 0, s>>>(snaps, weights, N, D, k, iters, seed, (float*)base,
+                                              (float*)(base + off_d2), (float*)(base + off_dist),
+                                              (int32_t*)(base + off_asg), centers, assign, mass,
+                                              seeds);
     return check_launch("kmeans_pp");
 }
 
