@@ -190,6 +190,9 @@ __global__ __launch_bounds__(64 * kRW) void k_centroid_reduce(const float* __res
 // plain loop's.
 __device__ __forceinline__ float sqdist_seq(const float* __restrict__ a,
                                            const float* __restrict__ b, int D) {
+    // hipcc would contract v * v + d into one FMA (one rounding where the
+    // sequential form rounds twice): each product passes through an empty
+    // asm statement, which no instruction combiner can look through
     constexpr int CH = 32;
     float d = 0.f;
     int i = 0;
@@ -203,12 +206,16 @@ __device__ __forceinline__ float sqdist_seq(const float* __restrict__ a,
 #pragma unroll
         for (int j = 0; j < CH; j++) {
             float v = __fsub_rn(av[j], bv[j]);
-            d = __fadd_rn(d, __fmul_rn(v, v));
+            float q = __fmul_rn(v, v);
+            asm volatile("" : "+v"(q));
+            d = __fadd_rn(d, q);
         }
     }
     for (; i < D; i++) {
         float v = __fsub_rn(a[i], b[i]);
-        d = __fadd_rn(d, __fmul_rn(v, v));
+        float q = __fmul_rn(v, v);
+        asm volatile("" : "+v"(q));
+        d = __fadd_rn(d, q);
     }
     return d;
 }
@@ -290,6 +297,7 @@ __device__ __forceinline__ void kmeans_update(const float* __restrict__ X, float
 // Snapshots that fit kXs floats are copied into LDS once (XL): the
 // distance chains and the center sums then read them from LDS.
 constexpr int kXs = 32768;  // 128 KB
+constexpr int kDs = 4096;   // distances held in LDS by k_kmeans_pp<true>
 
 template <bool XL>
 __device__ __forceinline__ const float* stage_snapshots(const float* __restrict__ Xg, float* xs,
@@ -329,20 +337,31 @@ __global__ __launch_bounds__(1024) void k_kmeans_pp(const float* __restrict__ Xg
                                                     const float* __restrict__ W, int N, int D,
                                                     int k, int iters, uint64_t seed,
                                                     float* __restrict__ Cw,  // [k*D] work
-                                                    float* __restrict__ d2,  // [N]
-                                                    float* __restrict__ dist,  // [N*k]
-                                                    int32_t* __restrict__ asg,  // [N]
+                                                    float* __restrict__ d2g,  // [N]
+                                                    float* __restrict__ distg,  // [N*k]
+                                                    int32_t* __restrict__ asgg,  // [N]
                                                     float* __restrict__ C_out,
                                                     int32_t* __restrict__ asg_out,
                                                     double* __restrict__ mass_out,
                                                     int32_t* __restrict__ seeds_out) {
+    // XL (N*D <= kXs, N <= 1024, N*k <= kDs): snapshots, assignments,
+    // distances and the seeding distances in LDS; the ranking arrays reuse
+    // the snapshot region once the last assignment pass has read it
     __shared__ int chosen[1024];
-    __shared__ double mass[1024];
-    __shared__ int order[1024];
-    __shared__ int rank_of[1024];
     __shared__ uint64_t rng;
-    __shared__ float xs[XL ? kXs : 1];
+    __shared__ __attribute__((aligned(16))) float xs[XL ? kXs : 1];
+    __shared__ int sasg[XL ? 1024 : 1];
+    __shared__ float sdist[XL ? kDs : 1];
+    __shared__ float sd2[XL ? 1024 : 1];
+    __shared__ double smass[XL ? 1 : 1024];
+    __shared__ int sorder[XL ? 1 : 1024], srank[XL ? 1 : 1024];
     const float* __restrict__ X = stage_snapshots<XL>(Xg, xs, N, D);
+    int32_t* asg = XL ? sasg : asgg;
+    float* dist = XL ? sdist : distg;
+    float* d2 = XL ? sd2 : d2g;
+    double* mass = XL ? (double*)xs : smass;
+    int* order = XL ? (int*)(xs + 2 * 1024) : sorder;
+    int* rank_of = XL ? (int*)(xs + 3 * 1024) : srank;
     if (threadIdx.x == 0) {
         rng = seed;
         int first = (int)(u01(rng) * N);
@@ -481,7 +500,7 @@ int ta_kmeans_pp(const float* snaps, const float* weights, int N, int D, int k, 
     size_t total = off_asg + (size_t)N * sizeof(int32_t);
     char* base = (char*)scratch_get(total, s);
     TA_REQUIRE(base, "kmeans_pp: scratch allocation failed");
-    if ((int64_t)N * D <= kXs)
+    if ((int64_t)N * D <= kXs && N <= 1024 && (int64_t)N * k <= kDs)
         k_kmeans_pp<true><<<1, 1024, 0, s>>>(snaps, weights, N, D, k, iters, seed, (float*)base,
                                              (float*)(base + off_d2), (float*)(base + off_dist),
                                              (int32_t*)(base + off_asg), centers, assign, mass,
