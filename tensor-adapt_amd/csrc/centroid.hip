@@ -112,31 +112,59 @@ __global__ __launch_bounds__(256) void k_centroid_part(const void* __restrict__ 
             for (int e = 0; e < 8; e++) out[c * 8 + e] = acc[e];
         }
     } else if (v4) {
-        // F32 rows as 16-byte vectors; 16 row loads in flight per batch,
-        // sums in token order
-        for (int c = threadIdx.x; c < (D >> 2); c += 256) {
+        // F32 rows as 16-byte vectors.  When D/4 columns leave threads over
+        // (D = 512: 128 columns), the block's G = 256 / (D/4) thread groups
+        // take consecutive token ranges of KT/G tokens each; each group sums
+        // its range in token order (16 row loads in flight per batch) and the
+        // group sums are added in group order.
+        __shared__ float4 gsum[256];
+        const int nc4 = D >> 2;
+        const int G = (nc4 <= 128 && 256 % nc4 == 0 && KT % (16 * (256 / nc4)) == 0)
+                          ? 256 / nc4 : 1;
+        const int TG = KT / G;
+        for (int base = 0; base < nc4 * G; base += 256) {
+            const int q = base + threadIdx.x, c = q % nc4, g = q / nc4;
             float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-            for (int j0 = 0; j0 < KT; j0 += 16) {
-                float4 hh[16];
+            if (q < nc4 * G) {
+                for (int j0 = g * TG; j0 < (g + 1) * TG; j0 += 16) {
+                    float4 hh[16];
 #pragma unroll
-                for (int j = 0; j < 16; j++) {
-                    const int64_t t = min(t0 + j0 + j, BT - 1);
-                    hh[j] = ((const float4*)((const float*)hv + t * D))[c];
-                }
+                    for (int j = 0; j < 16; j++) {
+                        const int64_t t = min(t0 + j0 + j, BT - 1);
+                        hh[j] = ((const float4*)((const float*)hv + t * D))[c];
+                    }
 #pragma unroll
-                for (int j = 0; j < 16; j++) {
-                    const float w = nrm[j0 + j];
-                    acc.x += hh[j].x * w;
-                    acc.y += hh[j].y * w;
-                    acc.z += hh[j].z * w;
-                    acc.w += hh[j].w * w;
+                    for (int j = 0; j < 16; j++) {
+                        const float w = nrm[j0 + j];
+                        acc.x += hh[j].x * w;
+                        acc.y += hh[j].y * w;
+                        acc.z += hh[j].z * w;
+                        acc.w += hh[j].w * w;
+                    }
                 }
             }
-            // (partial rows are D + 1 floats apart: 4-byte stores)
-            out[4 * c + 0] = acc.x;
-            out[4 * c + 1] = acc.y;
-            out[4 * c + 2] = acc.z;
-            out[4 * c + 3] = acc.w;
+            if (G > 1) {
+                gsum[threadIdx.x] = acc;
+                __syncthreads();
+                if (threadIdx.x < nc4) {
+                    acc = gsum[threadIdx.x];
+                    for (int gg = 1; gg < G; gg++) {
+                        const float4 o = gsum[gg * nc4 + threadIdx.x];
+                        acc.x += o.x;
+                        acc.y += o.y;
+                        acc.z += o.z;
+                        acc.w += o.w;
+                    }
+                }
+            }
+            if ((G > 1 ? threadIdx.x < nc4 : q < nc4)) {
+                const int cc = G > 1 ? threadIdx.x : c;
+                // (partial rows are D + 1 floats apart: 4-byte stores)
+                out[4 * cc + 0] = acc.x;
+                out[4 * cc + 1] = acc.y;
+                out[4 * cc + 2] = acc.z;
+                out[4 * cc + 3] = acc.w;
+            }
         }
     } else {
         for (int d = threadIdx.x; d < D; d += 256) {
