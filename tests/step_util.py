@@ -60,6 +60,17 @@ def chat_tokens(V, B, T, rng):
     return toks
 
 
+def span_tokens(B, T, rng):
+    """Uniform ids with one assistant span (<|im_start|> assistant ...
+    <|im_end|>) over almost every row, so the trainer's masking keeps
+    nearly all targets."""
+    toks = rng.integers(0, 150000, B * T + 1).astype(np.int32)
+    for b in range(B):
+        toks[b * T + 3], toks[b * T + 4] = 151644, 77091
+        toks[b * T + T - 8] = 151645
+    return toks
+
+
 def rel(a, b):
     a = np.asarray(a, np.float64).ravel()
     b = np.asarray(b, np.float64).ravel()

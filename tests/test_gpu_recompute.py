@@ -25,7 +25,7 @@ import pytest
 
 import oracle as O
 import tadapt
-from step_util import base_tensors, make_pair, pairs, rel
+from step_util import base_tensors, make_pair, pairs, rel, span_tokens
 from test_gpu_step import check_adamw_of_own_grads, compare, snapshot, sync_state
 
 pytestmark = pytest.mark.gpu
@@ -94,17 +94,6 @@ def test_recompute_bit_identical_c4_layer_shapes():
     neighbours) at B=4 x T=2048, rank 64, untied head, two steps."""
     mc = dict(C4_MODEL, layers=3)
     run_identical(mc, C4_ADAPT, 4, 2048, 2, seed=9, init_random=True)
-
-
-def span_tokens(B, T, rng):
-    """Uniform ids with one assistant span (<|im_start|> assistant ...
-    <|im_end|>) over almost every row, so the trainer's masking keeps
-    nearly all targets."""
-    toks = rng.integers(0, 150000, B * T + 1).astype(np.int32)
-    for b in range(B):
-        toks[b * T + 3], toks[b * T + 4] = 151644, 77091
-        toks[b * T + T - 8] = 151645
-    return toks
 
 
 def test_c4_layer_matches_oracle():
