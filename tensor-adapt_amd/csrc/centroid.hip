@@ -258,11 +258,70 @@ __device__ __forceinline__ double u01(uint64_t& s) {
     return (double)(splitmix64(s) >> 11) * (1.0 / 9007199254740992.0);
 }
 
+// Up to J distance chains against one center b (rows a0 + i * astride,
+// i < na), each chain in the order of sqdist_seq: every center chunk is
+// loaded once for all rows.
+template <int J>
+__device__ __forceinline__ void sqdist_seq_rows(const float* __restrict__ a0, int64_t astride,
+                                                int na, const float* __restrict__ b, int D,
+                                                float* __restrict__ out) {
+    constexpr int CH = 32;
+    float d[J];
+#pragma unroll
+    for (int r = 0; r < J; r++) d[r] = 0.f;
+    int i = 0;
+    for (; i + CH <= D; i += CH) {
+        float bv[CH];
+#pragma unroll
+        for (int j = 0; j < CH; j++) bv[j] = b[i + j];
+#pragma unroll
+        for (int r = 0; r < J; r++) {
+            if (r >= na) break;
+            const float* a = a0 + r * astride + i;
+            float av[CH];
+#pragma unroll
+            for (int j = 0; j < CH; j++) av[j] = a[j];
+#pragma unroll
+            for (int j = 0; j < CH; j++) {
+                float v = __fsub_rn(av[j], bv[j]);
+                float q = __fmul_rn(v, v);
+                asm volatile("" : "+v"(q));
+                d[r] = __fadd_rn(d[r], q);
+            }
+        }
+    }
+    for (; i < D; i++)
+#pragma unroll
+        for (int r = 0; r < J; r++) {
+            if (r >= na) break;
+            float v = __fsub_rn(a0[r * astride + i], b[i]);
+            float q = __fmul_rn(v, v);
+            asm volatile("" : "+v"(q));
+            d[r] = __fadd_rn(d[r], q);
+        }
+#pragma unroll
+    for (int r = 0; r < J; r++)
+        if (r < na) out[r] = d[r];
+}
+
 // assignment pass: dist[n*k + c] for all pairs, then argmin per n (strict <)
 __device__ __forceinline__ int kmeans_assign(const float* __restrict__ X, const float* __restrict__ C, int N,
                              int D, int k, float* __restrict__ dist, int32_t* __restrict__ asg) {
-    for (int p = threadIdx.x; p < N * k; p += blockDim.x)
-        dist[p] = sqdist_seq(X + (int64_t)(p / k) * D, C + (int64_t)(p % k) * D, D);
+    const int nt = blockDim.x;
+    if (nt % k == 0 && (int64_t)N * k <= 2ll * nt) {
+        // a thread's pairs p = tid + j * nt share the center c = tid % k:
+        // rows n0 and n0 + nt / k
+        const int c = threadIdx.x % k, n0 = threadIdx.x / k, st = nt / k;
+        const int na = n0 < N ? (n0 + st < N ? 2 : 1) : 0;
+        float dd[2];
+        if (na > 0)
+            sqdist_seq_rows<2>(X + (int64_t)n0 * D, (int64_t)st * D, na, C + (int64_t)c * D, D, dd);
+        if (na > 0) dist[(int64_t)n0 * k + c] = dd[0];
+        if (na > 1) dist[(int64_t)(n0 + st) * k + c] = dd[1];
+    } else {
+        for (int p = threadIdx.x; p < N * k; p += blockDim.x)
+            dist[p] = sqdist_seq(X + (int64_t)(p / k) * D, C + (int64_t)(p % k) * D, D);
+    }
     __syncthreads();
     int changed = 0;
     for (int n = threadIdx.x; n < N; n += blockDim.x) {
