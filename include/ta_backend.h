@@ -7,7 +7,8 @@
  * status; ta_last_error() then holds the message.  BF16 tensors are passed as
  * uint16_t bit patterns.  Nothing here allocates on the caller's behalf unless
  * the comment says so; ops that need scratch memory draw it from the
- * library's per-device, stream-ordered pool (grow-only, freed at exit).
+ * library's pool, one set of grow-only buffers per (device, stream), so
+ * calls on different streams never share scratch (freed at exit).
  *
  * Each declaration names the reference function it replaces (paths are in
  * carbon-os/tensor-adapt).  Layout conventions are the reference's: activations
@@ -109,11 +110,12 @@ int ta_sum_sq_into(const float* g, float* accum, int64_t N, void* stream);
  * (replaces compute_grad_norm + clip_gradients + AdamW::step_all,
  * src/trainer/adapt_trainer.cu:32-70,248-253 and src/trainer/adamw.cu:9-38):
  *   norm = ||grad||_2 over all n elements;
- *   if norm > max_norm: grad is scaled by max_norm/(norm+1e-6) (in registers);
+ *   if norm > max_norm: grad is scaled by max_norm/(norm+1e-6) IN PLACE,
+ *     as clip_gradients leaves gA/gB (adapt_trainer.cu:55-70);
  *   AdamW on every element; BF16 shadow written.
  * norm_out (device float, may be NULL) receives the unclipped norm.  The
  * whole tail runs on the device: no host synchronisation. */
-int ta_adamw_fused(float* master, uint16_t* working, float* m, float* v, const float* grad,
+int ta_adamw_fused(float* master, uint16_t* working, float* m, float* v, float* grad,
                    int64_t N, float lr, float beta1, float beta2, float eps,
                    float weight_decay, int step, float max_norm, float* norm_out,
                    void* stream);
@@ -124,9 +126,12 @@ int ta_adamw_fused(float* master, uint16_t* working, float* m, float* v, const f
  *   C(MxN, ldc) = alpha * op(A) * op(B) + beta * C,
  *   op(A)(i,k) = transA ? A[k + i*lda] : A[i + k*lda]
  *   op(B)(k,j) = transB ? B[j + k*ldb] : B[k + j*ldb]
- * BF16 inputs, FP32 accumulation on MFMA, output rounded once to BF16
- * (gemm_bf16) or kept F32 (gemm_f32: F32 inputs are rounded to BF16 for
- * the MFMA, exact for values that came from BF16, as on the LoRA path).
+ * gemm_bf16: BF16 inputs, FP32 accumulation on MFMA, output rounded once
+ * to BF16.  gemm_f32: F32 inputs and output with F32 accuracy (cublasSgemm
+ * semantics): each operand is split into three BF16 parts carrying its 24
+ * significand bits and the six part products down to 2^-24 relative are
+ * accumulated in F32 on the BF16 MFMA; it stages the split operands in the
+ * scratch pool (at most 256 MB per call, K taken in chunks).
  * Returns -1 for M,N,K,ld <= 0 (tensor.cu:134-142). */
 int ta_gemm_bf16(int transA, int transB, int M, int N, int K, float alpha,
                  const uint16_t* A, int lda, const uint16_t* B, int ldb, float beta,

@@ -89,7 +89,11 @@ int ta_engine_step(void* engine, const int32_t* inputs, const int32_t* targets,
 
 /* Same step with the batch already resident in device memory (int32 [B*T]
  * each; the assistant-span masking runs on the device).  No host-to-device
- * transfer happens inside the step. */
+ * transfer happens inside the step.  Token ids are checked on the device:
+ * an id outside [0, vocab) is never used as an index, and the call then
+ * returns an error with the adapter state, the step count and the centroid
+ * sums unchanged (targets outside [0, vocab) contribute only logsumexp to
+ * the loss, as target -1 does). */
 int ta_engine_step_resident(void* engine, const int32_t* d_inputs, const int32_t* d_targets,
                             float lr_override, ta_step_metrics* metrics);
 

@@ -65,7 +65,7 @@ void sum_sq_into(const float* g, float* accum, int N, hipStream_t s);
 // ── additions of this backend (no reference counterpart) ──────────────
 // Grad norm, clip and AdamW over one flat parameter arena in one pass
 // (replaces compute_grad_norm + clip_gradients + AdamW::step_all).
-void adamw_fused(float* master, bf16_t* working, float* m, float* v, const float* grad,
+void adamw_fused(float* master, bf16_t* working, float* m, float* v, float* grad,
                  std::int64_t N, float lr, float beta1, float beta2, float eps,
                  float weight_decay, int step, float max_norm, float* norm_out,
                  hipStream_t stream);

@@ -63,6 +63,19 @@ extern "C" void or_f32_from_bf16(const bf16_t* x, float* y, i64 n);
 template <typename LoadA, typename LoadB, typename Store>
 static void gemm_core(int M, int N, int K, LoadA la, LoadB lb, Store st);
 
+// Accumulation mode of the GEMM core and of the attention contractions.
+//   0 (default): FP64 accumulation, rounded once — the exact side of every
+//     parity check.
+//   1: FP32 accumulators fed by 16-wide K blocks, each block's products
+//     summed in k order in FP32 and added to the running FP32 sum (the
+//     accumulation a tiled matrix-core GEMM performs, with every rounding
+//     point of the reference unchanged).  It exists to measure how far two
+//     FP32-accumulating implementations of the same step drift apart over
+//     depth; no check uses it as the reference side.
+static int g_accum = 0;
+extern "C" void or_set_accum_mode(int mode) { g_accum = mode; }
+extern "C" int or_get_accum_mode(void) { return g_accum; }
+
 extern "C" {
 
 void or_bf16_from_f32(const float* x, bf16_t* y, i64 n) {
@@ -95,6 +108,38 @@ static void gemm_core(int M, int N, int K, LoadA la, LoadB lb, Store st) {
         for (i64 k = 0; k < K; k++) Bc[(size_t)j * K + k] = lb(k, j);
     const int IB = 32, JB = 32, KB = 2048;
     i64 nib = (M + IB - 1) / IB, njb = (N + JB - 1) / JB;
+    if (g_accum == 1) {
+        // FP32 blocked accumulation: per output, acc += (sum of 16 products
+        // in k order), block after block.  Vectorised across the 32 outputs
+        // of a row of the tile; each output's own order is sequential.
+        const int KS = 16;
+#pragma omp parallel for schedule(dynamic)
+        for (i64 blk = 0; blk < nib * njb; blk++) {
+            i64 i0 = (blk / njb) * IB, j0 = (blk % njb) * JB;
+            i64 i1 = std::min<i64>(i0 + IB, M), j1 = std::min<i64>(j0 + JB, N);
+            std::vector<float> bt((size_t)K * JB, 0.f);
+            for (i64 j = j0; j < j1; j++)
+                for (i64 k = 0; k < K; k++) bt[(size_t)k * JB + (j - j0)] = Bc[(size_t)j * K + k];
+            for (i64 i = i0; i < i1; i++) {
+                const float* a = &Ar[(size_t)i * K];
+                float acc[JB], s[JB];
+                for (int b = 0; b < JB; b++) acc[b] = 0.f;
+                for (i64 k0 = 0; k0 < K; k0 += KS) {
+                    i64 k1 = std::min<i64>(k0 + KS, K);
+                    for (int b = 0; b < JB; b++) s[b] = 0.f;
+                    for (i64 k = k0; k < k1; k++) {
+                        const float av = a[k];
+                        const float* br = &bt[(size_t)k * JB];
+#pragma omp simd
+                        for (int b = 0; b < JB; b++) s[b] += av * br[b];
+                    }
+                    for (int b = 0; b < JB; b++) acc[b] += s[b];
+                }
+                for (i64 j = j0; j < j1; j++) st(i, j, (double)acc[j - j0]);
+            }
+        }
+        return;
+    }
 #pragma omp parallel for schedule(dynamic)
     for (i64 blk = 0; blk < nib * njb; blk++) {
         i64 i0 = (blk / njb) * IB, j0 = (blk % njb) * JB;
@@ -245,7 +290,10 @@ void or_rope(bf16_t* x, int B, int T, int H, int hd, float theta, int inverse) {
 //  P saved to attn_w [B*Hq, T, T] (zeros above the diagonal);
 //  O = P.V rounded to BF16 into out [BT, Hq*hd].  kv head = hq/(Hq/Hkv).
 // ─────────────────────────────────────────────────────────────
-void or_sdpa_fwd(const bf16_t* Q, const bf16_t* K, const bf16_t* V, bf16_t* out,
+}  // extern "C"
+
+template <typename Acc>
+static void sdpa_fwd_t(const bf16_t* Q, const bf16_t* K, const bf16_t* V, bf16_t* out,
                  float* attn_w, int B, int T, int Hq, int Hkv, int hd) {
     float scale = 1.f / sqrtf((float)hd);
     int grp = Hq / Hkv;
@@ -259,13 +307,13 @@ void or_sdpa_fwd(const bf16_t* Q, const bf16_t* K, const bf16_t* V, bf16_t* out,
                 const bf16_t* q = Q + ((i64)(b * T + tq) * Hq + hq) * hd;
                 for (int tk = 0; tk <= tq; tk++) {
                     const bf16_t* k = K + ((i64)(b * T + tk) * Hkv + hkv) * hd;
-                    double d = 0.0;
-                    for (int i = 0; i < hd; i++) d += (double)bf2f(q[i]) * bf2f(k[i]);
+                    Acc d = 0;
+                    for (int i = 0; i < hd; i++) d += (Acc)bf2f(q[i]) * (Acc)bf2f(k[i]);
                     s[tk] = scale * (float)d;
                 }
                 float mx = -3.402823466e38f;
                 for (int tk = 0; tk <= tq; tk++) mx = std::max(mx, s[tk]);
-                double sum = 0.0;
+                Acc sum = 0;
                 for (int tk = 0; tk <= tq; tk++) {
                     s[tk] = expf(s[tk] - mx);
                     sum += s[tk];
@@ -275,9 +323,9 @@ void or_sdpa_fwd(const bf16_t* Q, const bf16_t* K, const bf16_t* V, bf16_t* out,
                 for (int tk = 0; tk < T; tk++) prow[tk] = (tk <= tq) ? s[tk] * inv : 0.f;
                 bf16_t* o = out + ((i64)(b * T + tq) * Hq + hq) * hd;
                 for (int i = 0; i < hd; i++) {
-                    double acc = 0.0;
+                    Acc acc = 0;
                     for (int tk = 0; tk <= tq; tk++)
-                        acc += (double)prow[tk] * bf2f(V[((i64)(b * T + tk) * Hkv + hkv) * hd + i]);
+                        acc += (Acc)prow[tk] * (Acc)bf2f(V[((i64)(b * T + tk) * Hkv + hkv) * hd + i]);
                     o[i] = f2bf((float)acc);
                 }
             }
@@ -291,7 +339,8 @@ void or_sdpa_fwd(const bf16_t* Q, const bf16_t* K, const bf16_t* V, bf16_t* out,
 //  dV = sum_group P^T dO ; dP = dO V^T ; dS = P*(dP - sum_j P dP) ;
 //  dQ = dS K / sqrt(hd) ; dK = sum_group dS^T Q / sqrt(hd).
 // ─────────────────────────────────────────────────────────────
-void or_sdpa_bwd(const bf16_t* dout, const bf16_t* Q, const bf16_t* K, const bf16_t* V,
+template <typename Acc>
+static void sdpa_bwd_t(const bf16_t* dout, const bf16_t* Q, const bf16_t* K, const bf16_t* V,
                  const float* attn_w, bf16_t* dQ, bf16_t* dK, bf16_t* dV,
                  int B, int T, int Hq, int Hkv, int hd) {
     float rs = 1.f / sqrtf((float)hd);
@@ -302,34 +351,34 @@ void or_sdpa_bwd(const bf16_t* dout, const bf16_t* Q, const bf16_t* K, const bf1
     auto ki = [&](int b, int t, int h) { return ((i64)(b * T + t) * Hkv + h) * hd; };
     for (int b = 0; b < B; b++)
         for (int hkv = 0; hkv < Hkv; hkv++) {
-            // per query head in the group: compute dS, dQ; accumulate dK, dV in fp64
-            std::vector<std::vector<double>> dKh(grp), dVh(grp);
+            // per query head in the group: compute dS, dQ; accumulate dK, dV in Acc
+            std::vector<std::vector<Acc>> dKh(grp), dVh(grp);
 #pragma omp parallel for schedule(dynamic)
             for (int g = 0; g < grp; g++) {
                 int hq = hkv * grp + g;
                 const float* P = attn_w + ((i64)b * Hq + hq) * T * T;
-                std::vector<double>& dKl = dKh[g];
-                std::vector<double>& dVl = dVh[g];
-                dKl.assign((size_t)T * hd, 0.0);
-                dVl.assign((size_t)T * hd, 0.0);
+                std::vector<Acc>& dKl = dKh[g];
+                std::vector<Acc>& dVl = dVh[g];
+                dKl.assign((size_t)T * hd, (Acc)0);
+                dVl.assign((size_t)T * hd, (Acc)0);
                 std::vector<float> dP(T), dS(T);
                 for (int tq = 0; tq < T; tq++) {
                     const bf16_t* dO = dout + qi(b, tq, hq);
                     const float* prow = P + (i64)tq * T;
                     for (int tk = 0; tk <= tq; tk++) {
                         const bf16_t* v = V + ki(b, tk, hkv);
-                        double d = 0.0;
-                        for (int i = 0; i < hd; i++) d += (double)bf2f(dO[i]) * bf2f(v[i]);
+                        Acc d = 0;
+                        for (int i = 0; i < hd; i++) d += (Acc)bf2f(dO[i]) * (Acc)bf2f(v[i]);
                         dP[tk] = (float)d;
                     }
-                    double dot = 0.0;
-                    for (int tk = 0; tk <= tq; tk++) dot += (double)prow[tk] * dP[tk];
+                    Acc dot = 0;
+                    for (int tk = 0; tk <= tq; tk++) dot += (Acc)prow[tk] * (Acc)dP[tk];
                     for (int tk = 0; tk < T; tk++)
                         dS[tk] = (tk <= tq) ? prow[tk] * (dP[tk] - (float)dot) : 0.f;
                     for (int i = 0; i < hd; i++) {
-                        double acc = 0.0;
+                        Acc acc = 0;
                         for (int tk = 0; tk <= tq; tk++)
-                            acc += (double)dS[tk] * bf2f(K[ki(b, tk, hkv) + i]);
+                            acc += (Acc)dS[tk] * (Acc)bf2f(K[ki(b, tk, hkv) + i]);
                         dQ[qi(b, tq, hq) + i] = f2bf(rs * (float)acc);
                     }
                     float qv[1024];
@@ -338,18 +387,18 @@ void or_sdpa_bwd(const bf16_t* dout, const bf16_t* Q, const bf16_t* K, const bf1
                         float p = prow[tk], ds = dS[tk];
                         if (p == 0.f && ds == 0.f) continue;
                         for (int i = 0; i < hd; i++) {
-                            dVl[(size_t)tk * hd + i] += (double)p * bf2f(dO[i]);
-                            dKl[(size_t)tk * hd + i] += (double)ds * qv[i];
+                            dVl[(size_t)tk * hd + i] += (Acc)p * (Acc)bf2f(dO[i]);
+                            dKl[(size_t)tk * hd + i] += (Acc)ds * (Acc)qv[i];
                         }
                     }
                 }
             }
             for (int tk = 0; tk < T; tk++)
                 for (int i = 0; i < hd; i++) {
-                    double sv = 0.0, sk = 0.0;
+                    Acc sv = 0, sk = 0;
                     for (int g = 0; g < grp; g++) {
-                        sv += (double)(float)dVh[g][(size_t)tk * hd + i];
-                        sk += (double)(rs * (float)dKh[g][(size_t)tk * hd + i]);
+                        sv += (Acc)(float)dVh[g][(size_t)tk * hd + i];
+                        sk += (Acc)(rs * (float)dKh[g][(size_t)tk * hd + i]);
                     }
                     dVacc[ki(b, tk, hkv) + i] = sv;
                     dKacc[ki(b, tk, hkv) + i] = sk;
@@ -359,6 +408,20 @@ void or_sdpa_bwd(const bf16_t* dout, const bf16_t* Q, const bf16_t* K, const bf1
         dV[i] = f2bf((float)dVacc[i]);
         dK[i] = f2bf((float)dKacc[i]);
     }
+}
+
+extern "C" {
+
+void or_sdpa_fwd(const bf16_t* Q, const bf16_t* K, const bf16_t* V, bf16_t* out,
+                 float* attn_w, int B, int T, int Hq, int Hkv, int hd) {
+    if (g_accum == 1) sdpa_fwd_t<float>(Q, K, V, out, attn_w, B, T, Hq, Hkv, hd);
+    else sdpa_fwd_t<double>(Q, K, V, out, attn_w, B, T, Hq, Hkv, hd);
+}
+void or_sdpa_bwd(const bf16_t* dout, const bf16_t* Q, const bf16_t* K, const bf16_t* V,
+                 const float* attn_w, bf16_t* dQ, bf16_t* dK, bf16_t* dV,
+                 int B, int T, int Hq, int Hkv, int hd) {
+    if (g_accum == 1) sdpa_bwd_t<float>(dout, Q, K, V, attn_w, dQ, dK, dV, B, T, Hq, Hkv, hd);
+    else sdpa_bwd_t<double>(dout, Q, K, V, attn_w, dQ, dK, dV, B, T, Hq, Hkv, hd);
 }
 
 // ─────────────────────────────────────────────────────────────

@@ -66,6 +66,13 @@ def lib():
     return _LIB
 
 
+def set_accum_mode(mode):
+    """0: FP64 accumulation (default, the exact side of every check);
+    1: FP32 accumulation in 16-wide K blocks, for measuring how far two
+    FP32-accumulating implementations drift apart (process-wide)."""
+    lib().or_set_accum_mode(c_int(mode))
+
+
 def P(a):
     """data pointer of a contiguous numpy array (or None)."""
     if a is None:

@@ -192,7 +192,9 @@ __global__ __launch_bounds__(256) void k_centroid_part(const void* __restrict__ 
 constexpr int kRW = 16;
 __global__ __launch_bounds__(64 * kRW) void k_centroid_reduce(const float* __restrict__ part,
                                                               int nblk, int D1,
-                                                              double* __restrict__ acc) {
+                                                              double* __restrict__ acc,
+                                                              const int32_t* __restrict__ skip) {
+    if (skip && *skip) return;
     __shared__ double q[kRW][64];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int d = blockIdx.x * 64 + lane;
@@ -521,7 +523,7 @@ __global__ __launch_bounds__(1024) void k_kmeans_pp(const float* __restrict__ Xg
 using namespace ta;
 
 static int centroid_acc(const void* h, const void* g, const float* n, int64_t BT, int D,
-                        double* acc, bool bf16in, void* stream) {
+                        double* acc, bool bf16in, void* stream, const int32_t* skip = nullptr) {
     TA_REQUIRE(BT >= 0 && D > 0, "centroid_accumulate: bad shape BT=%lld D=%d", (long long)BT, D);
     if (BT == 0) return 0;
     hipStream_t s = (hipStream_t)stream;
@@ -534,9 +536,16 @@ static int centroid_acc(const void* h, const void* g, const float* n, int64_t BT
         k_centroid_part<true><<<(int)nblk, 256, 0, s>>>(h, g, nullptr, BT, D, part);
     else
         k_centroid_part<false><<<(int)nblk, 256, 0, s>>>(h, g, n, BT, D, part);
-    k_centroid_reduce<<<(D + 1 + 63) / 64, 64 * kRW, 0, s>>>(part, (int)nblk, D + 1, acc);
+    k_centroid_reduce<<<(D + 1 + 63) / 64, 64 * kRW, 0, s>>>(part, (int)nblk, D + 1, acc, skip);
     return check_launch("centroid_accumulate");
 }
+
+namespace ta {
+int centroid_acc_bf16(const bf16* h, const bf16* g, int64_t BT, int D, double* acc,
+                      const int32_t* skip, hipStream_t s) {
+    return centroid_acc(h, g, nullptr, BT, D, acc, true, s, skip);
+}
+}  // namespace ta
 
 extern "C" {
 

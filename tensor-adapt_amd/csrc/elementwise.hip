@@ -162,6 +162,42 @@ __global__ void k_embed_fwd(const bf16* __restrict__ table, const int32_t* __res
     }
 }
 
+// The step engine's embedding gather for token ids that no host has
+// checked (ids resident in device memory): an id outside [0, V) reads
+// nothing, its row is written as zeros and *bad is set to 1 (a plain store;
+// every writer stores the same value).
+__global__ void k_embed_fwd_checked(const bf16* __restrict__ table,
+                                    const int32_t* __restrict__ tokens, bf16* __restrict__ out,
+                                    int64_t BT, int D, int V, bool vec, int32_t* __restrict__ bad) {
+    int lane = threadIdx.x & 63;
+    int64_t row = blockIdx.x * (int64_t)(blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (row >= BT) return;
+    int64_t tok = tokens[row];
+    bf16* dst = out + row * D;
+    if (tok < 0 || tok >= V) {
+        if (lane == 0) *bad = 1;
+        for (int c = lane; c < D; c += 64) dst[c] = 0;
+        return;
+    }
+    const bf16* src = table + tok * D;
+    if (vec) {
+        for (int c = lane; c < (D >> 3); c += 64)
+            ((bf16x8v*)dst)[c] = ((const bf16x8v*)src)[c];
+    } else {
+        for (int c = lane; c < D; c += 64) dst[c] = src[c];
+    }
+}
+
+int embed_fwd_checked(const bf16* table, const int32_t* tokens, bf16* out, int64_t BT, int D,
+                      int V, int32_t* bad, hipStream_t s) {
+    TA_REQUIRE(BT >= 0 && D > 0 && V > 0 && bad, "embed_fwd_checked: bad arguments");
+    if (BT == 0) return 0;
+    bool vec = (D & 7) == 0 && aligned16(table) && aligned16(out);
+    k_embed_fwd_checked<<<(int)((BT + 3) / 4), 256, 0, s>>>(table, tokens, out, BT, D, V, vec,
+                                                            bad);
+    return check_launch("embed_fwd_checked");
+}
+
 // ── embedding scatter-add — ops.cu:1037-1046 (F32 atomics, as the reference;
 //    dead code in the reference trainer, kept for API completeness) ────────
 __global__ void k_embed_bwd(const bf16* __restrict__ dout, const int32_t* __restrict__ tokens,

@@ -105,6 +105,9 @@ struct Engine {
     int32_t *tok_dev, *tgt_dev;
     int32_t *tok_host, *tgt_host;  // pinned
     float *loss_host, *norm_host;  // pinned
+    // set on the device when a token id of the batch lies outside [0, V):
+    // the embedding then reads nothing for it, and the tail changes no state
+    int32_t* bad_dev = nullptr;
     hipEvent_t ev[4];
     int64_t step_count = 0;
     float phase[3] = {0, 0, 0};
@@ -384,6 +387,7 @@ static int engine_alloc(Engine* e) {
     CK(alloc(e, &e->Dbuf, (int64_t)e->B * c.n_q * e->T, "Dbuf", 1));
     CK(alloc(e, &e->dkv_part, (int64_t)2 * e->B * c.n_q * e->T * c.head_dim, "dkv_part", 1));
     CK(alloc(e, &e->norm_dev, 64, "norm", 1));
+    e->bad_dev = (int32_t*)(e->norm_dev + 1);
     CK(alloc(e, &e->cacc, H + 1, "centroid"));
     CK(alloc(e, &e->tok_dev, BT, "tok"));
     CK(alloc(e, &e->tgt_dev, BT, "targets", 1));  // int32, 4-byte elements
@@ -652,7 +656,8 @@ static int forward(Engine* e) {
     const int BT = e->BT, H = e->H, I = e->I;
     const double dBT = BT;
     hipStream_t s = e->s;
-    TIMED(TA_CAT_ELEMWISE, 0, dBT * H * 4, ta_embed_fwd(e->embed, e->tok_cur, e->L[0].res_in, BT, H, s));
+    TIMED(TA_CAT_ELEMWISE, 0, dBT * H * 4,
+          embed_fwd_checked(e->embed, e->tok_cur, e->L[0].res_in, BT, H, e->V, e->bad_dev, s));
     const double nrm_b = dBT * H * 4 + H * 2 + dBT * 4;
     for (int l = 0; l < c.layers; l++) {
         Layer& ly = e->L[l];
@@ -781,7 +786,7 @@ static int backward(Engine* e) {
         // centroid side channel (adapt_trainer.cu:210-232): h = x_normed,
         // g = dx_attn_in of this layer
         TIMED(TA_CAT_CENTROID, 0, dBT * H * 4,
-              ta_centroid_accumulate_bf16(ly.xn, e->dxn, BT, H, e->cacc, s));
+              centroid_acc_bf16(ly.xn, e->dxn, BT, H, e->cacc, e->bad_dev, s));
         // grad += bf16(rms_norm_bwd(dx_normed)), one pass
         TIMED(TA_CAT_NORM, 0, nrm_b + dBT * H * 2,
               rms_bwd_acc(e->dxn, ly.res_in, ly.in_norm, ly.in_rms, e->g_res, e->tmpH, BT, H, s));
@@ -801,6 +806,7 @@ static int engine_step_body(Engine* e, float lr_override, ta_step_metrics* m,
     const int BT = e->BT;
     // zero_grad (adapter_model.cu:222-229)
     TA_HIP(hipMemsetAsync(e->grad, 0, e->nparam * sizeof(float), e->s));
+    TA_HIP(hipMemsetAsync(e->bad_dev, 0, sizeof(int32_t), e->s));
     // B^T shadows for dh = go B (the shadows changed in the last AdamW)
     CK(transpose_batch(e->shadow, e->shadowT, e->tdesc, e->ntdesc, e->s));
     TA_HIP(hipEventRecord(e->ev[0], e->s));
@@ -815,9 +821,11 @@ static int engine_step_body(Engine* e, float lr_override, ta_step_metrics* m,
                    : cosine_lr(e->ac.lr, e->ac.warmup, e->ac.total_steps, 0.1f, e->step_count);
     int t = (int)e->step_count + 1;
     TIMED(TA_CAT_TAIL, 0, (double)e->nparam * 34,
-          ta_adamw_fused(e->master, e->shadow, e->mom, e->vel, e->grad, e->nparam, lr, e->ac.b1,
-                         e->ac.b2, e->ac.eps, e->ac.wd, t, e->ac.grad_clip, e->norm_dev, e->s));
-    TA_HIP(hipMemcpyAsync(e->norm_host, e->norm_dev, 4, hipMemcpyDeviceToHost, e->s));
+          adamw_fused_impl(e->master, e->shadow, e->mom, e->vel, e->grad, e->nparam, lr,
+                           e->ac.b1, e->ac.b2, e->ac.eps, e->ac.wd, t, e->ac.grad_clip,
+                           e->norm_dev, e->bad_dev, e->s));
+    // the norm and the bad-id flag behind it
+    TA_HIP(hipMemcpyAsync(e->norm_host, e->norm_dev, 8, hipMemcpyDeviceToHost, e->s));
     TA_HIP(hipEventRecord(e->ev[3], e->s));
     TA_HIP(hipStreamSynchronize(e->s));
     for (int i = 0; i < 3; i++) TA_HIP(hipEventElapsedTime(&e->phase[i], e->ev[i], e->ev[i + 1]));
@@ -832,6 +840,13 @@ static int engine_step_body(Engine* e, float lr_override, ta_step_metrics* m,
         }
     if (valid > 0) mean /= (float)valid;
     float norm = e->norm_host[0];
+    int32_t bad;
+    memcpy(&bad, e->norm_host + 1, sizeof bad);
+    if (bad)
+        return set_error(-1,
+                         "engine_step: a token id of the batch lies outside [0, %d); the step was "
+                         "not applied (adapter state, step count and centroid unchanged)",
+                         e->V);
     e->step_count++;
     if (m) {
         m->loss = mean;

@@ -1706,12 +1706,40 @@ int gemm_swiglu(int M, int K, const bf16* X, int64_t ldx, const bf16* Wgu, const
     return check_launch("gemm_swiglu");
 }
 
-// F32 -> BF16 staging for gemm_f32 operands (the LoRA path feeds it values
-// that came from BF16, for which the rounding is exact).
-__global__ void k_f32_to_bf16_2d(const float* __restrict__ s, int64_t n, bf16* __restrict__ d) {
+// Operand staging of gemm_f32.  Each F32 value is split into three BF16
+// parts, s0 = bf16(s), s1 = bf16(s - s0), s2 = bf16(s - s0 - s1), whose sum
+// carries s to about 2^-24 relative (24 bits of significand).  A product
+// a*b is formed as the six part products whose magnitude reaches 2^-24 of
+// it, a2 b0 + a1 b1 + a0 b2 + a1 b0 + a0 b1 + a0 b0 (smallest first, so the
+// F32 accumulator adds the small terms before the large ones); each part
+// product is exact in the MFMA's F32 arithmetic.  The parts are laid out
+// K-contiguous as six segments of kp columns per row (the segment q of a
+// row holds part (code >> 2q) & 3 of columns k0 .. k0 + kc, zero padded to
+// kp), so that one BF16 GEMM over K = 6 kp adds exactly those products.
+__global__ void k_split3(const float* __restrict__ S, int64_t ld, bool kcontig, int rows,
+                         int64_t k0, int kc, int kp, unsigned code, bf16* __restrict__ dst) {
+    const int64_t n = (int64_t)rows * kp;
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
-         i += (int64_t)gridDim.x * blockDim.x)
-        d[i] = f2bf(s[i]);
+         i += (int64_t)gridDim.x * blockDim.x) {
+        int64_t r, k;
+        if (kcontig) {
+            r = i / kp;
+            k = i - r * kp;
+        } else {
+            k = i / rows;
+            r = i - k * rows;
+        }
+        float v = 0.f;
+        if (k < kc) v = kcontig ? S[r * ld + k0 + k] : S[(k0 + k) * ld + r];
+        bf16 p[3];
+        p[0] = f2bf(v);
+        const float r1 = v - bf2f(p[0]);
+        p[1] = f2bf(r1);
+        p[2] = f2bf(r1 - bf2f(p[1]));
+        bf16* row = dst + r * (int64_t)(6 * kp) + k;
+#pragma unroll
+        for (int q = 0; q < 6; q++) row[(int64_t)q * kp] = p[(code >> (2 * q)) & 3u];
+    }
 }
 
 }  // namespace ta
@@ -1746,23 +1774,42 @@ int ta_gemm_bf16(int transA, int transB, int M, int N, int K, float alpha, const
                          nullptr, false, (hipStream_t)stream, 0, nullptr);
 }
 
+// cublasSgemm semantics (tensor.cu:168-182): F32 operands, F32 result.  The
+// operands are split into BF16 parts (k_split3) and multiplied on the BF16
+// MFMA with F32 accumulation, K in chunks whose staging stays within 256 MB;
+// each chunk after the first adds into C (beta 1), as a split-K SGEMM does.
 int ta_gemm_f32(int transA, int transB, int M, int N, int K, float alpha, const float* A, int lda,
                 const float* B, int ldb, float beta, float* C, int ldc, void* stream) {
     TA_REQUIRE(M > 0 && N > 0 && K > 0, "gemm_f32: M/N/K must be > 0");
     TA_REQUIRE(lda > 0 && ldb > 0 && ldc > 0, "gemm_f32: leading dims must be > 0");
     hipStream_t s = (hipStream_t)stream;
-    // stage both operands as BF16 (footprint = the stored extent of each) in
-    // the pool's staging slot; the split-K partials use the default slot
-    int64_t na = transA ? (int64_t)(M - 1) * lda + K : (int64_t)(K - 1) * lda + M;
-    int64_t nb = transB ? (int64_t)(K - 1) * ldb + N : (int64_t)(N - 1) * ldb + K;
-    size_t offb = ((size_t)na * 2 + 255) & ~(size_t)255;
-    bf16* a16 = (bf16*)scratch_get(offb + (size_t)nb * 2, s, 1);
-    TA_REQUIRE(a16, "gemm_f32: scratch allocation failed");
-    bf16* b16 = (bf16*)((char*)a16 + offb);
-    k_f32_to_bf16_2d<<<1024, 256, 0, s>>>(A, na, a16);
-    k_f32_to_bf16_2d<<<1024, 256, 0, s>>>(B, nb, b16);
-    return gemm_dispatch(!transB, transA != 0, N, M, K, alpha, b16, ldb, a16, lda, beta, C, ldc,
-                         nullptr, true, s, 0, nullptr);
+    // rows of the row-major form: X = op(B) by output column j (N rows, K
+    // contiguous when !transB), Y = op(A) by output row i (M rows, K
+    // contiguous when transA); part codes pair a2 b0, a1 b1, a0 b2, a1 b0,
+    // a0 b1, a0 b0 segment by segment
+    const unsigned code_x = 0u | 1u << 2 | 2u << 4 | 0u << 6 | 1u << 8 | 0u << 10;
+    const unsigned code_y = 2u | 1u << 2 | 0u << 4 | 1u << 6 | 0u << 8 | 0u << 10;
+    const int64_t budget = (int64_t)256 << 20;
+    int64_t kc_max = budget / (12 * ((int64_t)M + N));
+    kc_max = kc_max < 32 ? 32 : (kc_max & ~(int64_t)31);
+    const int kcap = (int)std::min<int64_t>(kc_max, ((int64_t)K + 31) & ~(int64_t)31);
+    const size_t offy = ((size_t)N * 6 * kcap * 2 + 255) & ~(size_t)255;
+    bf16* x16 = (bf16*)scratch_get(offy + (size_t)M * 6 * kcap * 2, s, 1);
+    TA_REQUIRE(x16, "gemm_f32: scratch allocation failed");
+    bf16* y16 = (bf16*)((char*)x16 + offy);
+    for (int64_t k0 = 0; k0 < K; k0 += kcap) {
+        const int kc = (int)std::min<int64_t>(kcap, K - k0);
+        const int kp = (kc + 31) & ~31;
+        const int64_t nx = (int64_t)N * kp, ny = (int64_t)M * kp;
+        k_split3<<<(int)std::min<int64_t>((nx + 255) / 256, 4096), 256, 0, s>>>(
+            B, ldb, transB == 0, N, k0, kc, kp, code_x, x16);
+        k_split3<<<(int)std::min<int64_t>((ny + 255) / 256, 4096), 256, 0, s>>>(
+            A, lda, transA != 0, M, k0, kc, kp, code_y, y16);
+        const int rc = gemm_dispatch(true, true, N, M, 6 * kp, alpha, x16, 6 * kp, y16, 6 * kp,
+                                     k0 == 0 ? beta : 1.f, C, ldc, nullptr, true, s, 0, nullptr);
+        if (rc != 0) return rc;
+    }
+    return check_launch("gemm_f32");
 }
 
 }  // extern "C"

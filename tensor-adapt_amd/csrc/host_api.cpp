@@ -282,7 +282,7 @@ void adamw_step(float* master, bf16_t* working, float* m, float* v, const float*
 void sum_sq_into(const float* g, float* accum, int N, hipStream_t s) {
     check_status(ta_sum_sq_into(g, accum, N, s), "sum_sq_into");
 }
-void adamw_fused(float* master, bf16_t* working, float* m, float* v, const float* grad,
+void adamw_fused(float* master, bf16_t* working, float* m, float* v, float* grad,
                  int64_t N, float lr, float b1, float b2, float eps, float wd, int step,
                  float max_norm, float* norm_out, hipStream_t s) {
     check_status(ta_adamw_fused(master, working, m, v, grad, N, lr, b1, b2, eps, wd, step,

@@ -9,7 +9,10 @@
 //      grid-stride slice (deterministic order);
 //   2. k_adamw_fused: every block re-reduces the partials in the same order
 //      (so all blocks agree on the norm bit for bit), derives the clip
-//      factor, and applies AdamW (ops.cu:1139-1158) to its elements.
+//      factor, and applies AdamW (ops.cu:1139-1158) to its elements.  When
+//      the clip fires, the scaled gradient is also stored back, so the
+//      gradient arena ends the step holding what clip_gradients leaves in
+//      gA/gB (adapt_trainer.cu:55-70: g *= clip / (norm + 1e-6) in place).
 #include "ta_internal.hpp"
 
 namespace ta {
@@ -68,22 +71,28 @@ __device__ __forceinline__ float adamw_elem(float p, float g, float& m, float& v
 
 __global__ __launch_bounds__(256) void k_adamw(float* __restrict__ master, bf16* __restrict__ work,
                                                float* __restrict__ m, float* __restrict__ v,
-                                               const float* __restrict__ grad, int64_t N,
+                                               float* __restrict__ grad, int64_t N,
                                                float lr, float b1, float b2, float eps, float wd,
                                                float bc1, float bc2,
                                                const float* __restrict__ part, int nparts,
-                                               float max_norm, float* __restrict__ norm_out) {
+                                               float max_norm, float* __restrict__ norm_out,
+                                               const int32_t* __restrict__ skip) {
     float gscale = 1.f;
     if (part) {
         double ss = reduce_partials(part, nparts);
         float norm = (float)sqrt(ss);
         if (norm_out && blockIdx.x == 0 && threadIdx.x == 0) *norm_out = norm;
+        if (skip && *skip) return;  // a failed step: report the norm, change nothing
         // clip_gradients, adapt_trainer.cu:55-70
         if (norm > max_norm) gscale = max_norm / (norm + 1e-6f);
     }
+    const bool clipped = gscale != 1.f;
     for (int64_t i = blockIdx.x * 256ll + threadIdx.x; i < N; i += (int64_t)gridDim.x * 256) {
         float g = grad[i];
-        if (part) g = g * gscale;
+        if (clipped) {
+            g = g * gscale;
+            grad[i] = g;
+        }
         float mi = m[i], vi = v[i];
         float p = adamw_elem(master[i], g, mi, vi, lr, b1, b2, eps, wd, bc1, bc2);
         m[i] = mi;
@@ -112,9 +121,11 @@ int ta_adamw_step(float* master, uint16_t* working, float* m, float* v, const fl
     if (N == 0) return 0;
     float bc1 = 1.f - powf(beta1, (float)step);
     float bc2 = 1.f - powf(beta2, (float)step);
-    k_adamw<<<adam_blocks(N), 256, 0, (hipStream_t)stream>>>(master, working, m, v, grad, N, lr,
+    k_adamw<<<adam_blocks(N), 256, 0, (hipStream_t)stream>>>(master, working, m, v,
+                                                             const_cast<float*>(grad), N, lr,
                                                              beta1, beta2, eps, weight_decay,
-                                                             bc1, bc2, nullptr, 0, 0.f, nullptr);
+                                                             bc1, bc2, nullptr, 0, 0.f, nullptr,
+                                                             nullptr);
     return check_launch("adamw_step");
 }
 
@@ -129,13 +140,23 @@ int ta_sum_sq_into(const float* g, float* accum, int64_t N, void* stream) {
     return check_launch("sum_sq_into");
 }
 
-int ta_adamw_fused(float* master, uint16_t* working, float* m, float* v, const float* grad,
+int ta_adamw_fused(float* master, uint16_t* working, float* m, float* v, float* grad,
                    int64_t N, float lr, float beta1, float beta2, float eps,
                    float weight_decay, int step, float max_norm, float* norm_out,
                    void* stream) {
+    return adamw_fused_impl(master, working, m, v, grad, N, lr, beta1, beta2, eps, weight_decay,
+                            step, max_norm, norm_out, nullptr, (hipStream_t)stream);
+}
+
+}  // extern "C"
+
+namespace ta {
+
+int adamw_fused_impl(float* master, bf16* working, float* m, float* v, float* grad, int64_t N,
+                     float lr, float beta1, float beta2, float eps, float weight_decay, int step,
+                     float max_norm, float* norm_out, const int32_t* skip, hipStream_t s) {
     TA_REQUIRE(N >= 0 && step >= 1, "adamw_fused: bad N=%lld step=%d", (long long)N, step);
     if (N == 0) return 0;
-    hipStream_t s = (hipStream_t)stream;
     float* part = (float*)scratch_get(kNormBlocks * sizeof(float), s);
     TA_REQUIRE(part, "adamw_fused: scratch allocation failed");
     float bc1 = 1.f - powf(beta1, (float)step);
@@ -143,8 +164,12 @@ int ta_adamw_fused(float* master, uint16_t* working, float* m, float* v, const f
     k_sumsq_partials<<<kNormBlocks, 256, 0, s>>>(grad, N, part);
     k_adamw<<<adam_blocks(N), 256, 0, s>>>(master, working, m, v, grad, N, lr, beta1, beta2,
                                            eps, weight_decay, bc1, bc2, part, kNormBlocks,
-                                           max_norm, norm_out);
+                                           max_norm, norm_out, skip);
     return check_launch("adamw_fused");
 }
+
+}  // namespace ta
+
+extern "C" {
 
 }  // extern "C"

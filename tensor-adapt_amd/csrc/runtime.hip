@@ -2,9 +2,10 @@
 // C-ABI.
 //
 // Scratch: ops that need temporary device memory (reduction partials) take
-// it from one grow-only buffer per device.  Work on one stream is ordered,
-// so reusing the buffer across calls on the same stream is safe; growing it
-// synchronises the device before freeing the old buffer.  This replaces the
+// it from grow-only buffers kept per (device, stream).  Work on one stream
+// is ordered, so reusing a stream's buffers across its calls is safe, and
+// ops on two streams of one device never share one; growing a buffer
+// synchronises its stream before freeing the old one.  This replaces the
 // reference's per-call cudaMalloc/cudaFree inside sdpa_* (ops.cu:595-680,
 // 727-869), which synchronised the device on every attention call.
 #include <stdarg.h>
@@ -44,23 +45,25 @@ struct Scratch {
 };
 static std::mutex g_scratch_mu;
 constexpr int kSlots = 4;  // 0: reduction partials, 1: operand staging, 2-3: spare
-static Scratch g_scratch[64][kSlots];
+struct ScratchSet {
+    Scratch slot[kSlots];
+};
+static std::map<std::pair<int, hipStream_t>, ScratchSet> g_scratch;
 
-// Slot `slot` of the current device's pool, at least `bytes` long.  Two
-// buffers an op needs at once must come from different slots.
+// Slot `slot` of the pool of (current device, stream s), at least `bytes`
+// long.  Two buffers an op needs at once must come from different slots.
 void* scratch_get(size_t bytes, hipStream_t s, int slot) {
-    (void)s;
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return nullptr;
     if (slot < 0 || slot >= kSlots) return nullptr;
     std::lock_guard<std::mutex> lk(g_scratch_mu);
-    Scratch& sc = g_scratch[dev][slot];
+    Scratch& sc = g_scratch[{dev, s}].slot[slot];
     if (sc.bytes >= bytes && sc.ptr) return sc.ptr;
     size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
     want = (want + 255) & ~(size_t)255;
     if (sc.ptr) {
-        // earlier launches on any stream may still read the old buffer
-        if (hipDeviceSynchronize() != hipSuccess) return nullptr;
+        // earlier launches on this stream may still read the old buffer
+        if (hipStreamSynchronize(s) != hipSuccess) return nullptr;
         (void)hipFree(sc.ptr);
         sc.ptr = nullptr;
         sc.bytes = 0;

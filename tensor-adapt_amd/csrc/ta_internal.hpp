@@ -115,6 +115,19 @@ int rms_fwd_res(const bf16* a, const bf16* b, bf16* xs, const bf16* w, bf16* out
 // acc = bf16(acc + bf16(RMSNorm backward dx)), in one pass (tmp: fallback scratch)
 int rms_bwd_acc(const bf16* dy, const bf16* x, const bf16* w, const float* rms, bf16* acc,
                 bf16* tmp, int64_t rows, int D, hipStream_t s);
+// embedding gather that checks ids against V: an id outside [0, V) gets a
+// zero row and sets *bad = 1 (ids resident in device memory)
+int embed_fwd_checked(const bf16* table, const int32_t* tokens, bf16* out, int64_t BT, int D,
+                      int V, int32_t* bad, hipStream_t s);
+// the fused norm / clip / AdamW tail; when skip (device int, may be NULL)
+// holds a nonzero value the norm is still reported but no state changes
+int adamw_fused_impl(float* master, bf16* working, float* m, float* v, float* grad, int64_t N,
+                     float lr, float b1, float b2, float eps, float wd, int step, float max_norm,
+                     float* norm_out, const int32_t* skip, hipStream_t s);
+// centroid accumulate of BF16 h, g; when skip (device int, may be NULL) holds
+// a nonzero value nothing is added
+int centroid_acc_bf16(const bf16* h, const bf16* g, int64_t BT, int D, double* acc,
+                      const int32_t* skip, hipStream_t s);
 int mask_targets_dev(const int32_t* in, const int32_t* tgt_in, int32_t* tgt, int B, int T,
                      hipStream_t s);
 int lora_skinny_nt(const bf16* X, int64_t ldx, int M, int K, int r, const bf16* const* Y,

@@ -50,7 +50,6 @@ def test_c2_full_model_matches_oracle():
               f"gnorm {sg['gnorm_raw']:.5e} / {so['gnorm_raw']:.5e}", flush=True)
         assert abs(sg["loss"] - so["loss"]) <= 1e-3 * abs(so["loss"]), (step, sg, so)
         assert abs(sg["gnorm_raw"] - so["gnorm_raw"]) <= 1e-2 * so["gnorm_raw"], (step, sg, so)
-        if so["gnorm_raw"] <= ac["grad_clip"]:
-            compare(orc, eng, mc, ac, ("gB",) if step == 0 else ("gA", "gB"), bar=4e-2)
+        compare(orc, eng, mc, ac, ("gB",) if step == 0 else ("gA", "gB"), bar=4e-2)
         check_adamw_of_own_grads(eng, mc, ac, state, sg["lr"], step + 1, sg["gnorm_raw"])
     eng.close()

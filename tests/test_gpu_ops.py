@@ -162,14 +162,22 @@ def test_adamw_fused_norm_clip(scale, clip):
     p = RNG.standard_normal(n).astype(np.float32) * 0.1
     g = RNG.standard_normal(n).astype(np.float32) * scale
     z = np.zeros(n, np.float32)
-    tp, tm, tv, tw = dev(p), dev(z), dev(z), empty_bf16(n)
+    tp, tm, tv, tw, tg = dev(p), dev(z), dev(z), empty_bf16(n), dev(g)
     norm = torch.zeros(1, dtype=torch.float32, device=DEV)
-    call("ta_adamw_fused", P(tp), P(tw), P(tm), P(tv), P(dev(g)), n, ctypes.c_float(1e-4),
+    call("ta_adamw_fused", P(tp), P(tw), P(tm), P(tv), P(tg), n, ctypes.c_float(1e-4),
          ctypes.c_float(0.9), ctypes.c_float(0.999), ctypes.c_float(1e-8), ctypes.c_float(0.01),
          1, ctypes.c_float(clip), P(norm), S())
     rn = float(np.sqrt(O.sum_sq(g)))
-    assert abs(host(norm)[0] - rn) <= 1e-5 * rn
+    gn = np.float32(host(norm)[0])
+    assert abs(gn - rn) <= 1e-5 * rn
     gc = g * np.float32(clip / (rn + 1e-6)) if rn > clip else g
+    # the gradient is left clipped in place, as clip_gradients leaves gA/gB
+    # (adapt_trainer.cu:55-70): g * (clip / (norm + 1e-6)) in F32, bit for bit
+    if rn > clip:
+        sc = np.float32(clip) / (gn + np.float32(1e-6))
+        assert np.array_equal(host(tg), (g * sc).astype(np.float32))
+    else:
+        assert np.array_equal(host(tg), g)
     rp, rm, rv, rw = p.copy(), z.copy(), z.copy(), np.empty(n, np.uint16)
     O.adamw_step(rp, rw, rm, rv, np.ascontiguousarray(gc, np.float32), 1e-4, 0.9, 0.999,
                  1e-8, 0.01, 1)
@@ -251,6 +259,42 @@ def test_gemm_f32_weight_gradient_layouts(M, N, K):
     ref = C.copy()
     O.gemm_f32(0, 1, M, N, K, 0.5, A, M, Bm, N, 1.0, ref, M)
     assert rel_l2(host(tc), ref) < 1e-5
+
+
+def _cm_op(X, trans, rows, K, ld):
+    """op(X) as a dense [rows, K] array from a column-major buffer."""
+    if trans:  # op(X)(i,k) = X[k + i*ld]
+        return X.reshape(rows, ld)[:, :K]
+    return X.reshape(K, ld)[:, :rows].T  # op(X)(i,k) = X[i + k*ld]
+
+
+@pytest.mark.parametrize("tA,tB,M,N,K", [(0, 0, 129, 67, 1000), (1, 0, 64, 300, 777),
+                                         (0, 1, 1536, 16, 8192), (1, 1, 200, 130, 64),
+                                         (0, 1, 8960, 40, 5000)])
+def test_gemm_f32_general_operands(tA, tB, M, N, K):
+    """gemm_f32 on F32 data that is not BF16-valued has cublasSgemm accuracy
+    (tensor.cu:168-182): within 1e-5 relative L2 of the FP64-accumulated
+    oracle, and each element within 1e-6 of alpha * sum_k |a||b| + |beta c|
+    (BF16-rounded operands would miss both by about 3e-3).  Padded leading
+    dimensions; the last shape takes three K chunks of the staging."""
+    lda, ldb, ldc = (K if tA else M) + 3, (N if tB else K) + 2, M + 1
+    A = RNG.standard_normal((M if tA else K) * lda).astype(np.float32)
+    Bm = (RNG.standard_normal((K if tB else N) * ldb) * 1e-3).astype(np.float32)
+    C = RNG.standard_normal(N * ldc).astype(np.float32)
+    alpha, beta = 0.75, -0.5
+    tc = dev(C)
+    call("ta_gemm_f32", tA, tB, M, N, K, ctypes.c_float(alpha), P(dev(A)), lda, P(dev(Bm)), ldb,
+         ctypes.c_float(beta), P(tc), ldc, S())
+    ref = C.copy()
+    assert O.gemm_f32(tA, tB, M, N, K, alpha, A, lda, Bm, ldb, beta, ref, ldc) == 0
+    got = host(tc).reshape(N, ldc)[:, :M]
+    want = ref.reshape(N, ldc)[:, :M]
+    assert np.array_equal(host(tc).reshape(N, ldc)[:, M:], C.reshape(N, ldc)[:, M:])
+    assert rel_l2(got, want) < 1e-5
+    opa = _cm_op(A, tA, M, K, lda).astype(np.float64)            # [M, K]
+    opb = _cm_op(Bm, not tB, N, K, ldb).astype(np.float64)       # [N, K]: op(B)(k,j) by j
+    mag = abs(alpha) * (np.abs(opb) @ np.abs(opa).T) + abs(beta) * np.abs(C.reshape(N, ldc)[:, :M])
+    assert np.all(np.abs(got.astype(np.float64) - want) <= 1e-6 * mag)
 
 
 # ── centroid accumulate / k-means ─────────────────────────────────────────

@@ -64,15 +64,19 @@ def check_band(orc, eng, mc, ac, before=None):
 
 
 def check_adamw_of_own_grads(eng, mc, ac, state, lr, t, gnorm_raw):
-    """The engine's update is exactly AdamW (clip, bias correction, weight
-    decay; ops.cu:1139-1158, adapt_trainer.cu:55-70) of its own gradients
-    from the given starting state."""
-    scale = np.float32(ac["grad_clip"] / (gnorm_raw + 1e-6)) if gnorm_raw > ac["grad_clip"] else None
+    """The engine's update is exactly AdamW (bias correction, weight decay;
+    ops.cu:1139-1158) of its own gradients from the given starting state.
+    The gradients it holds after the step are the clipped ones, as
+    clip_gradients leaves gA/gB (adapt_trainer.cu:55-70), so AdamW is
+    applied to them as read; when the clip fired their global norm is
+    clip * raw / (raw + 1e-6)."""
+    if gnorm_raw > ac["grad_clip"]:
+        ss = sum(O.sum_sq(eng.adapter(l, tg, "g" + w)) for l, tg in pairs(mc, ac) for w in "AB")
+        want = ac["grad_clip"] * gnorm_raw / (gnorm_raw + 1e-6)
+        assert abs(np.sqrt(ss) - want) <= 1e-5 * want, (np.sqrt(ss), want)
     for l, tg in pairs(mc, ac):
         for w in ("A", "B"):
             g = eng.adapter(l, tg, "g" + w)
-            if scale is not None:
-                g = (g * scale).astype(np.float32)
             p = state[(l, tg, w)].copy()
             m = state[(l, tg, "m" + w)].copy()
             v = state[(l, tg, "v" + w)].copy()
@@ -140,13 +144,38 @@ def test_small_all_targets_multistep_matches_oracle():
         assert abs(sg["lr"] - so["lr"]) <= 1e-7 * so["lr"]
         assert abs(sg["loss"] - so["loss"]) <= 1e-3 * abs(so["loss"]), (step, sg, so)
         assert abs(sg["gnorm_raw"] - so["gnorm_raw"]) <= 1e-2 * so["gnorm_raw"], (step, sg, so)
-        if so["gnorm_raw"] <= ac["grad_clip"]:
-            compare(orc, eng, mc, ac, ("gB",) if step == 0 else ("gA", "gB"))
+        compare(orc, eng, mc, ac, ("gB",) if step == 0 else ("gA", "gB"))
         check_adamw_of_own_grads(eng, mc, ac, state, sg["lr"], step + 1, sg["gnorm_raw"])
         check_band(orc, eng, mc, ac, before={k: v for k, v in state.items() if k[2] in "AB"})
     ca, cw = eng.centroid()
     oa, ow = orc.centroid()
     assert rel(ca, oa) < 1e-2 and abs(cw - ow) <= 1e-2 * ow
+
+
+def test_small_clipped_steps_match_oracle():
+    """grad_clip far below the gradient norm, so clip_gradients fires on both
+    steps (adapt_trainer.cu:55-70).  The engine's gA/gB after a step are the
+    clipped gradients, as the reference leaves them, and are compared with
+    the oracle's clipped ones; the reported norm is min(norm, clip)
+    (adapt_trainer.cu:250).  Step 2 starts from the oracle's state after
+    step 1 (B != 0)."""
+    mc, ac, B, T = SMALL_MODEL, dict(SMALL_ADAPT, grad_clip=1e-3), 2, 64
+    orc, eng = make_pair(mc, ac, B, T, seed=27)
+    rng = np.random.default_rng(19)
+    for step in range(2):
+        sync_state(orc, eng, mc, ac)
+        state = snapshot(orc, mc, ac)
+        toks = rng.integers(0, mc["vocab"], B * T + 1).astype(np.int32)
+        inp, tgt = toks[:-1].copy(), toks[1:].copy()
+        so = orc.step(inp, tgt, B, T)
+        sg = eng.step(inp, tgt)
+        assert so["gnorm_raw"] > 10 * ac["grad_clip"] and sg["gnorm_raw"] > 10 * ac["grad_clip"]
+        assert sg["gnorm"] == so["gnorm"] == np.float32(ac["grad_clip"])
+        assert abs(sg["loss"] - so["loss"]) <= 1e-3 * abs(so["loss"]), (step, sg, so)
+        assert abs(sg["gnorm_raw"] - so["gnorm_raw"]) <= 1e-2 * so["gnorm_raw"], (step, sg, so)
+        compare(orc, eng, mc, ac, ("gB",) if step == 0 else ("gA", "gB"))
+        check_adamw_of_own_grads(eng, mc, ac, state, sg["lr"], step + 1, sg["gnorm_raw"])
+        check_band(orc, eng, mc, ac, before={k: v for k, v in state.items() if k[2] in "AB"})
 
 
 def test_small_long_batch_matches_oracle():
@@ -168,8 +197,7 @@ def test_small_long_batch_matches_oracle():
         sg = eng.step(inp, tgt)
         assert abs(sg["loss"] - so["loss"]) <= 1e-3 * abs(so["loss"]), (step, sg, so)
         assert abs(sg["gnorm_raw"] - so["gnorm_raw"]) <= 1e-2 * so["gnorm_raw"], (step, sg, so)
-        if so["gnorm_raw"] <= ac["grad_clip"]:
-            compare(orc, eng, mc, ac, ("gB",) if step == 0 else ("gA", "gB"))
+        compare(orc, eng, mc, ac, ("gB",) if step == 0 else ("gA", "gB"))
         check_adamw_of_own_grads(eng, mc, ac, state, sg["lr"], step + 1, sg["gnorm_raw"])
 
 
@@ -196,6 +224,40 @@ def test_mid_pipe_gemm_paths_match_oracle():
         sg = eng.step(inp, tgt)
         assert abs(sg["loss"] - so["loss"]) <= 1e-3 * abs(so["loss"]), (step, sg, so)
         assert abs(sg["gnorm_raw"] - so["gnorm_raw"]) <= 1e-2 * so["gnorm_raw"], (step, sg, so)
-        if so["gnorm_raw"] <= ac["grad_clip"]:
-            compare(orc, eng, mc, ac, ("gB",) if step == 0 else ("gA", "gB"))
+        compare(orc, eng, mc, ac, ("gB",) if step == 0 else ("gA", "gB"))
         check_adamw_of_own_grads(eng, mc, ac, state, sg["lr"], step + 1, sg["gnorm_raw"])
+
+
+def test_resident_step_rejects_out_of_range_ids():
+    """Token ids resident in device memory are checked on the device (the
+    host-buffer entry checks them on the host): an id outside [0, V) is
+    never used as an index, the step returns an error and leaves the adapter
+    state, step count and centroid sums as they were; the next valid batch
+    then steps exactly as the host-buffer entry does."""
+    import torch
+    mc, ac, B, T = SMALL_MODEL, SMALL_ADAPT, 2, 64
+    e_res, e_host = tadapt.Engine(mc, ac, B, T), tadapt.Engine(mc, ac, B, T)
+    e_res.init_random(7)
+    e_host.init_random(7)
+    rng = np.random.default_rng(3)
+    toks = rng.integers(0, mc["vocab"], B * T + 1).astype(np.int32)
+    inp, tgt = toks[:-1].copy(), toks[1:].copy()
+    bad = inp.copy()
+    bad[5], bad[B * T - 2] = mc["vocab"] + 7, -3
+    d_tgt = torch.from_numpy(tgt).cuda()
+    before = {w: e_res.adapter(0, "q", w).copy() for w in ("A", "B", "mA", "A16")}
+    c_before = e_res.centroid()[0].copy()
+    with pytest.raises(tadapt.BackendError, match="outside"):
+        e_res.step_resident(torch.from_numpy(bad).cuda(), d_tgt)
+    for w, v in before.items():
+        assert np.array_equal(e_res.adapter(0, "q", w), v), w
+    assert np.array_equal(e_res.centroid()[0], c_before)
+    m_res = e_res.step_resident(torch.from_numpy(inp).cuda(), d_tgt)
+    m_host = e_host.step(inp, tgt)
+    assert m_res["step"] == m_host["step"] == 1
+    assert m_res["loss"] == m_host["loss"] and m_res["gnorm_raw"] == m_host["gnorm_raw"]
+    for l, t in pairs(mc, ac):
+        for w in ("A", "B", "gA", "gB"):
+            assert np.array_equal(e_res.adapter(l, t, w), e_host.adapter(l, t, w)), (l, t, w)
+    e_res.close()
+    e_host.close()
