@@ -168,6 +168,18 @@ int ta_gemm_variant(int variant);
  * F64 vector of D+1 entries, accumulated in a fixed order. */
 int ta_centroid_accumulate_bf16(const uint16_t* h, const uint16_t* g, int64_t BT, int D,
                                 double* acc, void* stream);
+/* ta_centroid_accumulate_bf16 without any allocation: no counterpart in the
+ * reference.  It is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same kernels, same order, same bits as
+ * ta_centroid_accumulate_bf16; its partial rows live in a static 8 MiB device
+ * array per GPU, held until the process ends, so ceil(BT/16) * (D+1) * 4
+ * bytes must fit 8 MiB (BT <= 21824 at D = 1536, 9360 at D = 3584), else it
+ * returns an error before launching anything.  Every call on one GPU shares
+ * that array: calls that overlap on one GPU (on different streams, or from
+ * different threads) race and must be ordered by the caller. */
+int ta_centroid_accumulate_bf16_noalloc(const uint16_t* h, const uint16_t* g, int64_t BT, int D,
+                                        double* acc, void* stream);
 /* Same with F32 h and g (the dtype the reference trainer hands over,
  * adapt_trainer.cu:215-231). */
 int ta_centroid_accumulate_f32(const float* h, const float* g, int64_t BT, int D, double* acc,

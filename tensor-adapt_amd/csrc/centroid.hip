@@ -19,7 +19,17 @@
 // by max_iters / iters, so the launch always drains.
 #include <float.h>
 
+#include <mutex>
+
 #include "ta_internal.hpp"
+
+// Partial rows of ta_centroid_accumulate_bf16_noalloc, in a file-scope device
+// array instead of allocated memory: every GPU the library runs on holds its
+// own copy until the process ends.  In host code this name is a host-side
+// stand-in, not a device address; host code uses only the per-device address
+// from hipGetSymbolAddress (noalloc_scratch below).
+constexpr size_t kNoAllocScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
 
 namespace ta {
 
@@ -547,11 +557,56 @@ int centroid_acc_bf16(const bf16* h, const bf16* g, int64_t BT, int D, double* a
 }
 }  // namespace ta
 
+// Device address of `scratch` on device dev, looked up once per device with
+// that device current (the caller's current device) and kept.
+static std::mutex g_na_mu;
+static float* g_na_ptr[64];
+
+static int noalloc_scratch(float** out) {
+    int dev = 0;
+    TA_HIP(hipGetDevice(&dev));
+    TA_REQUIRE(dev >= 0 && dev < 64, "centroid_accumulate_bf16_noalloc: device %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_na_mu);
+    if (!g_na_ptr[dev]) {
+        void* p = nullptr;
+        TA_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        TA_REQUIRE(p, "centroid_accumulate_bf16_noalloc: no device address for the scratch");
+        g_na_ptr[dev] = (float*)p;
+    }
+    *out = g_na_ptr[dev];
+    return 0;
+}
+
 extern "C" {
 
 int ta_centroid_accumulate_bf16(const uint16_t* h, const uint16_t* g, int64_t BT, int D,
                                 double* acc, void* stream) {
     return centroid_acc(h, g, nullptr, BT, D, acc, true, stream);
+}
+
+int ta_centroid_accumulate_bf16_noalloc(const uint16_t* h, const uint16_t* g, int64_t BT, int D,
+                                        double* acc, void* stream) {
+    TA_REQUIRE(h && g && acc, "centroid_accumulate_bf16_noalloc: null argument");
+    TA_REQUIRE(BT >= 0 && D > 0, "centroid_accumulate_bf16_noalloc: bad shape BT=%lld D=%d",
+               (long long)BT, D);
+    if (BT == 0) return 0;
+    const int64_t nblk = (BT + kTok - 1) / kTok;
+    const int64_t max_blk = (int64_t)(kNoAllocScratchBytes / sizeof(float)) / (D + 1);
+    TA_REQUIRE(nblk <= max_blk,
+               "centroid_accumulate_bf16_noalloc: BT=%lld at D=%d needs %lld partial rows of "
+               "D+1 floats, over the %zu-byte static scratch (at most BT=%lld at this D)",
+               (long long)BT, D, (long long)nblk, kNoAllocScratchBytes,
+               (long long)(max_blk * kTok));
+    float* part = nullptr;
+    const int rc = noalloc_scratch(&part);
+    if (rc != 0) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    // the same kernels and order as ta_centroid_accumulate_bf16: every
+    // partial row is written in full before the reduce reads it
+    k_centroid_part<true><<<(int)nblk, 256, 0, s>>>(h, g, nullptr, BT, D, part);
+    k_centroid_reduce<<<(D + 1 + 63) / 64, 64 * kRW, 0, s>>>(part, (int)nblk, D + 1, acc,
+                                                             nullptr);
+    return check_launch("centroid_accumulate_bf16_noalloc");
 }
 
 int ta_centroid_accumulate_f32(const float* h, const float* g, int64_t BT, int D, double* acc,
