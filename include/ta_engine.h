@@ -77,6 +77,24 @@ int ta_engine_destroy(void* engine);
  * BF16 bits from host memory, n elements (BaseLoader::load, src/base/base_loader.cpp:75-172). */
 int ta_engine_set_weight(void* engine, const char* name, const uint16_t* host_data, int64_t n);
 
+/* ta_engine_set_weight from device memory: n BF16 elements at src, copied on
+ * the engine's stream (the caller makes sure src is ready on that stream;
+ * the C++ AdaptTrainer loads its FrozenBase's device tensors this way). */
+int ta_engine_set_weight_device(void* engine, const char* name, const uint16_t* src, int64_t n);
+
+/* Add the centroid side channel of every later step into the caller's
+ * device F64 vector [hidden + 1] (sums, then total weight) instead of the
+ * engine's own; NULL returns to the engine's own.  The vector is updated on
+ * the engine's stream.  (AdaptTrainer points it at its CentroidAccumulator,
+ * as the reference's trainer feeds CentroidAccumulator::accumulate,
+ * src/trainer/adapt_trainer.cu:210-232.) */
+int ta_engine_set_centroid(void* engine, double* d_acc);
+
+/* Set the number of steps already taken (0 after create): the next step
+ * uses the schedule's lr_at(step) and AdamW's t = step + 1
+ * (adapt_trainer.cu:252-253).  For resuming from a saved state. */
+int ta_engine_set_step(void* engine, int64_t step);
+
 /* Synthetic base on the device: every linear weight and the embedding
  * ~ N(0, std) from `seed` (per-tensor streams), norm weights 1, biases 0. */
 int ta_engine_init_random(void* engine, uint64_t seed, float std);

@@ -35,7 +35,8 @@ public:
                     const backend::cuda::Tensor& grad_signal,
                     const backend::cuda::Device& dev);
 
-    // Writes step-<step>.centroid (nothing while W == 0).
+    // Writes step-<step>.centroid (nothing while W == 0).  Writing the same
+    // step again replaces that snapshot, as rewriting its file does.
     void write_snapshot(std::size_t step);
 
     // k-means over the snapshots taken (or, if none, those in the
@@ -45,6 +46,11 @@ public:
     // Current sums (C[0..D-1], W) as F64; waits for the device.
     std::vector<double> sums() const;
 
+    // The device F64 vector [D + 1] (sums, then W) that accumulate() adds
+    // into, allocated and zeroed on dev at the first call; for producers
+    // that add into it on dev's stream (the step engine behind AdaptTrainer).
+    double* device_sums(const backend::cuda::Device& dev);
+
 private:
     int D_;
     std::string dir_;
@@ -52,6 +58,7 @@ private:
     hipStream_t stream_ = nullptr;
     double* acc_ = nullptr;  // device [D + 1]
     std::vector<std::vector<float>> snapshots_;
+    std::vector<std::size_t> snapshot_steps_;
 };
 
 }  // namespace tensor::centroid

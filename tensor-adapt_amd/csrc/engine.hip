@@ -101,7 +101,8 @@ struct Engine {
     bf16 *x_final, *xfn, *logits, *g_res, *dres, *tmpH, *dact, *dgate, *dup, *dxn2, *dao, *dQ, *dK,
         *dV, *dxn, *delta, *dh, *dh_cat;
     float *final_rms, *loss_tok, *norm_dev, *Dbuf, *dkv_part;
-    double* cacc;
+    double* cacc;          // the centroid sums the step adds into (own_cacc or the caller's)
+    double* own_cacc = nullptr;
     int32_t *tok_dev, *tgt_dev;
     int32_t *tok_host, *tgt_host;  // pinned
     float *loss_host, *norm_host;  // pinned
@@ -388,7 +389,8 @@ static int engine_alloc(Engine* e) {
     CK(alloc(e, &e->dkv_part, (int64_t)2 * e->B * c.n_q * e->T * c.head_dim, "dkv_part", 1));
     CK(alloc(e, &e->norm_dev, 64, "norm", 1));
     e->bad_dev = (int32_t*)(e->norm_dev + 1);
-    CK(alloc(e, &e->cacc, H + 1, "centroid"));
+    CK(alloc(e, &e->own_cacc, H + 1, "centroid"));
+    e->cacc = e->own_cacc;
     CK(alloc(e, &e->tok_dev, BT, "tok"));
     CK(alloc(e, &e->tgt_dev, BT, "targets", 1));  // int32, 4-byte elements
     TA_HIP(hipHostMalloc((void**)&e->tok_host, BT * sizeof(int32_t)));
@@ -1024,6 +1026,34 @@ int ta_engine_set_weight(void* ep, const char* name, const uint16_t* host, int64
     TA_HIP(hipMemcpyAsync(*slot, host, n * 2, hipMemcpyHostToDevice, e->s));
     CK(refresh_transpose(e, name, layer, proj));
     TA_HIP(hipStreamSynchronize(e->s));
+    return 0;
+}
+
+int ta_engine_set_weight_device(void* ep, const char* name, const uint16_t* src, int64_t n) {
+    Engine* e = (Engine*)ep;
+    TA_REQUIRE(e && name && src, "engine_set_weight_device: null argument");
+    int64_t want = 0;
+    int layer, proj;
+    bf16** slot = weight_slot(e, name, &want, &layer, &proj);
+    TA_REQUIRE(slot, "engine_set_weight_device: unknown tensor '%s'", name);
+    TA_REQUIRE(n == want, "engine_set_weight_device: '%s' has %lld elements, expected %lld", name,
+               (long long)n, (long long)want);
+    TA_HIP(hipMemcpyAsync(*slot, src, n * 2, hipMemcpyDeviceToDevice, e->s));
+    CK(refresh_transpose(e, name, layer, proj));
+    return 0;
+}
+
+int ta_engine_set_centroid(void* ep, double* acc) {
+    Engine* e = (Engine*)ep;
+    TA_REQUIRE(e, "engine_set_centroid: null engine");
+    e->cacc = acc ? acc : e->own_cacc;
+    return 0;
+}
+
+int ta_engine_set_step(void* ep, int64_t step) {
+    Engine* e = (Engine*)ep;
+    TA_REQUIRE(e && step >= 0, "engine_set_step: bad arguments");
+    e->step_count = step;
     return 0;
 }
 

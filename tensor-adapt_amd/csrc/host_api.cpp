@@ -322,6 +322,22 @@ void CentroidAccumulator::accumulate(const backend::cuda::Tensor& hidden,
     if (hidden.rank() != 2 || grad.shape() != hidden.shape()) return;
     const int64_t BT = (int64_t)hidden.shape()[0];
     if ((int)hidden.shape()[1] != D_) return;
+    device_sums(dev);
+    using backend::cuda::DType;
+    if (hidden.dtype() == DType::BF16 && grad.dtype() == DType::BF16)
+        check_status(ta_centroid_accumulate_bf16(hidden.bf16(), grad.bf16(), BT, D_, acc_,
+                                                 dev.stream()),
+                     "CentroidAccumulator::accumulate");
+    else if (hidden.dtype() == DType::F32 && grad.dtype() == DType::F32)
+        check_status(ta_centroid_accumulate_f32(hidden.f32(), grad.f32(), BT, D_, acc_,
+                                                dev.stream()),
+                     "CentroidAccumulator::accumulate");
+    else
+        throw CudaError("CentroidAccumulator::accumulate: hidden and grad_signal must both be "
+                        "BF16 or both F32");
+}
+
+double* CentroidAccumulator::device_sums(const backend::cuda::Device& dev) {
     if (acc_ && dev.id() != device_)
         throw CudaError("CentroidAccumulator: accumulate on device " + std::to_string(dev.id()) +
                         " after device " + std::to_string(device_));
@@ -335,18 +351,7 @@ void CentroidAccumulator::accumulate(const backend::cuda::Tensor& hidden,
             throw CudaError("CentroidAccumulator: clearing the accumulator failed");
     }
     stream_ = dev.stream();
-    using backend::cuda::DType;
-    if (hidden.dtype() == DType::BF16 && grad.dtype() == DType::BF16)
-        check_status(ta_centroid_accumulate_bf16(hidden.bf16(), grad.bf16(), BT, D_, acc_,
-                                                 dev.stream()),
-                     "CentroidAccumulator::accumulate");
-    else if (hidden.dtype() == DType::F32 && grad.dtype() == DType::F32)
-        check_status(ta_centroid_accumulate_f32(hidden.f32(), grad.f32(), BT, D_, acc_,
-                                                dev.stream()),
-                     "CentroidAccumulator::accumulate");
-    else
-        throw CudaError("CentroidAccumulator::accumulate: hidden and grad_signal must both be "
-                        "BF16 or both F32");
+    return acc_;
 }
 
 std::vector<double> CentroidAccumulator::sums() const {
@@ -371,7 +376,12 @@ void CentroidAccumulator::write_snapshot(std::size_t step) {
     f.write(reinterpret_cast<const char*>(&D), sizeof D);
     f.write(reinterpret_cast<const char*>(c.data()), (std::streamsize)(c.size() * sizeof(float)));
     f.write(reinterpret_cast<const char*>(&w), sizeof w);
-    snapshots_.push_back(std::move(c));
+    if (!snapshot_steps_.empty() && snapshot_steps_.back() == step) {
+        snapshots_.back() = std::move(c);
+    } else {
+        snapshots_.push_back(std::move(c));
+        snapshot_steps_.push_back(step);
+    }
     std::cerr << "[centroid] snapshot -> " << path << " (weight=" << w << ")\n";
 }
 

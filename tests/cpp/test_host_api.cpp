@@ -19,6 +19,7 @@
 #include <vector>
 
 #include "ta_backend.h"
+#include "ta_engine.h"
 #include <tensor/backend/cuda/device.hpp>
 #include <tensor/backend/cuda/ops.hpp>
 #include <tensor/backend/cuda/tensor.hpp>
@@ -26,6 +27,10 @@
 #include <tensor/centroid/centroid_merge.hpp>
 #include <tensor/core/tensor_view.hpp>
 #include <tensor/data/dataset.hpp>
+#include <tensor/adapter/adapter_config.hpp>
+#include <tensor/base/frozen_base.hpp>
+#include <tensor/checkpoint/adapter_writer.hpp>
+#include <tensor/trainer/adapt_trainer.hpp>
 #include <tensor/trainer/cosine_schedule.hpp>
 
 namespace fs = std::filesystem;
@@ -85,6 +90,8 @@ static std::vector<char> read_file(const fs::path& p) {
     std::ifstream f(p, std::ios::binary);
     return std::vector<char>(std::istreambuf_iterator<char>(f), {});
 }
+
+static void writer_tests(const fs::path& dir);
 
 static void cpu_tests(const fs::path& dir) {
     // core types
@@ -148,7 +155,75 @@ static void cpu_tests(const fs::path& dir) {
     CHECK(throws<std::runtime_error>(
         [&] { centroid::CentroidMerge::run((dir / "no_snapshots").string(), "x", 4); },
         "No .centroid files"));
+
+    writer_tests(dir / "writer");
 }
+
+// AdapterWriter: a checkpoint and a final adapter from known tensors (the
+// Python side checks the files against independent readers), and the
+// checkpoint read back exactly.
+static void writer_tests(const fs::path& dir) {
+    using checkpoint::AdapterTensor;
+    std::vector<AdapterTensor> ts;
+    uint32_t s = 11;
+    for (int l = 0; l < 2; l++)
+        for (int p : {0, 2, 6})
+            for (int ab = 0; ab < 2; ab++) {
+                AdapterTensor t;
+                t.name = checkpoint::lora_prefix(l, p) + (ab ? ".lora_B" : ".lora_A");
+                const size_t n = 8 + 3 * l + p + ab;
+                for (size_t i = 0; i < n; i++) {
+                    t.value.push_back(urand(s) * 0.05f);
+                    t.exp_avg.push_back(urand(s) * 1e-3f);
+                    t.exp_avg_sq.push_back(std::fabs(urand(s)) * 1e-6f);
+                }
+                // BF16 ties: 1 + 2^-8 rounds down to even, 1 + 3*2^-8 up to even
+                t.value[0] = 1.00390625f;
+                t.value[1] = -1.01171875f;
+                ts.push_back(std::move(t));
+            }
+    std::vector<double> sums(17);
+    for (auto& v : sums) v = urand(s) * 1e3;
+    adapter::AdapterConfig cfg;
+    cfg.rank = 4;
+    cfg.alpha = 0.1f;
+    cfg.inject_k = false;
+    cfg.inject_down = true;
+    base::FrozenBase fb;
+    fb.config.arch_name = "qwen2";
+    fb.config.base_sha = "abc123";
+    fb.config.num_layers = 2;
+    fb.config.hidden_size = 16;
+    checkpoint::AdapterWriter w(dir.string());
+    w.save_checkpoint(ts, sums, cfg, fb, "golang/gin \"x\"", 7, 3584, (dir / "ckpt").string());
+    w.save_final(ts, cfg, fb, "golang/gin", 9, 4608, (dir / "final").string());
+    checkpoint::TrainState st = checkpoint::load_checkpoint((dir / "ckpt").string());
+    CHECK(st.step == 7 && st.tokens_consumed == 3584 && st.centroid_sums == sums);
+    CHECK(st.tensors.size() == ts.size());
+    for (const auto& t : ts) {
+        bool found = false;
+        for (const auto& r : st.tensors)
+            if (r.name == t.name) {
+                found = true;
+                CHECK(r.value == t.value && r.exp_avg == t.exp_avg && r.exp_avg_sq == t.exp_avg_sq);
+            }
+        CHECK(found);
+    }
+    CHECK(!fs::exists(dir / "final" / "train_state.json"));
+    CHECK(throws<std::runtime_error>(
+        [&] { (void)checkpoint::load_checkpoint((dir / "absent").string()); }));
+    // the tensors' names and F32 values, in order, for the Python side
+    std::ofstream names(dir / "names.txt");
+    std::vector<float> vals;
+    for (const auto& t : ts) {
+        names << t.name << " " << t.value.size() << "\n";
+        vals.insert(vals.end(), t.value.begin(), t.value.end());
+    }
+    write_file(dir / "values.bin", vals);
+    write_file(dir / "sums.bin", sums);
+}
+
+static void trainer_tests(const Device& dev, const fs::path& dir);
 
 static void gpu_tests(const fs::path& dir) {
     Device dev = Device::open("hip:0");
@@ -346,6 +421,164 @@ static void gpu_tests(const fs::path& dir) {
         CHECK(ta_mem_free(&p, 0) != 0);  // not ours: rejected
     }
     dev.sync();
+    trainer_tests(dev, dir / "trainer");
+}
+
+// A small Qwen2 base (V=1024, H=256, 2 layers, 4 Q / 2 KV heads of 64,
+// I=512) in device tensors, N(0, 0.02) weights, unit norms, zero biases.
+static base::FrozenBase small_base(const Device& dev) {
+    base::FrozenBase b;
+    base::BaseConfig& c = b.config;
+    c.arch_name = "qwen2";
+    c.arch = base::ArchType::Qwen2;
+    c.vocab_size = 1024;
+    c.hidden_size = 256;
+    c.num_layers = 2;
+    c.num_q_heads = 4;
+    c.num_kv_heads = 2;
+    c.head_dim = 64;
+    c.intermediate_size = 512;
+    c.rms_norm_eps = 1e-6f;
+    c.rope_theta = 1e6f;
+    c.tie_embeddings = true;
+    uint32_t s = 17;
+    auto mk = [&](std::initializer_list<size_t> shape, float scale, float fill) {
+        Shape sh(shape);
+        std::vector<uint16_t> h(sh.numel());
+        for (auto& v : h) v = f2bf(scale > 0 ? urand(s) * scale * 1.7320508f : fill);
+        return Tensor::from_host(TensorView{h.data(), DType::BF16, sh}, dev);
+    };
+    const size_t H = 256, q = 256, kv = 128, I = 512;
+    b.embed_w = mk({1024, H}, 0.02f, 0.f);
+    b.final_norm_w = mk({H}, 0.f, 1.f);
+    for (int l = 0; l < 2; l++) {
+        base::LayerWeights w;
+        w.input_norm_w = mk({H}, 0.f, 1.f);
+        w.post_norm_w = mk({H}, 0.f, 1.f);
+        w.q_proj_w = mk({q, H}, 0.02f, 0.f);
+        w.q_proj_b = mk({q}, 0.f, 0.f);
+        w.k_proj_w = mk({kv, H}, 0.02f, 0.f);
+        w.k_proj_b = mk({kv}, 0.f, 0.f);
+        w.v_proj_w = mk({kv, H}, 0.02f, 0.f);
+        w.v_proj_b = mk({kv}, 0.f, 0.f);
+        w.o_proj_w = mk({H, q}, 0.02f, 0.f);
+        w.gate_proj_w = mk({I, H}, 0.02f, 0.f);
+        w.up_proj_w = mk({I, H}, 0.02f, 0.f);
+        w.down_proj_w = mk({H, I}, 0.02f, 0.f);
+        b.layers.push_back(std::move(w));
+    }
+    return b;
+}
+
+// every adapter tensor of a trainer's engine (masters, moments, shadows)
+static std::vector<std::vector<char>> adapter_state(void* eng, int mask, const base::BaseConfig& c,
+                                                    int r) {
+    std::vector<std::vector<char>> out;
+    const int64_t H = c.hidden_size, q = c.num_q_heads * c.head_dim,
+                  kv = c.num_kv_heads * c.head_dim, I = c.intermediate_size;
+    const int64_t in[7] = {H, H, H, q, H, H, I}, o[7] = {q, kv, kv, H, I, I, H};
+    for (int l = 0; l < (int)c.num_layers; l++)
+        for (int p = 0; p < 7; p++) {
+            if (!((mask >> p) & 1)) continue;
+            for (int which = 0; which < 10; which++) {
+                const bool isA = which == 0 || which == 2 || which == 3 || which == 6 || which == 8;
+                const int64_t n = isA ? r * in[p] : o[p] * r;
+                std::vector<char> buf(n * (which >= 8 ? 2 : 4));
+                CHECK(ta_engine_read_adapter(eng, l, p, which, buf.data(), n) == 0);
+                out.push_back(std::move(buf));
+            }
+        }
+    return out;
+}
+
+// AdaptTrainer driven as tools/tensor-adapt.cpp drives it (Device, an
+// in-memory FrozenBase, AdapterConfig, Dataset, AdaptOptions, run()), then
+// checkpoint + resume: a trainer resumed from the step-2 checkpoint takes
+// step 3 to exactly the state, loss and centroid sums of the original run.
+static void trainer_tests(const Device& dev, const fs::path& dir) {
+    fs::create_directories(dir / "data");
+    std::vector<uint32_t> toks(5000);
+    uint32_t s = 23;
+    for (auto& t : toks) t = lcg(s) % 1024u;
+    write_file(dir / "data" / "tokens.bin", toks);
+    base::FrozenBase fb = small_base(dev);
+    adapter::AdapterConfig cfg;
+    cfg.rank = 8;
+    cfg.alpha = 16.f;
+    cfg.inject_k = cfg.inject_o = false;
+    cfg.inject_gate = cfg.inject_down = true;
+    cfg.lr = 1e-3f;
+    cfg.warmup_steps = 1;
+    cfg.weight_decay = 0.01f;
+    cfg.batch_size = 2;
+    cfg.seq_len = 64;
+    const size_t bt = 128;
+
+    {  // run() to the token budget: 5 steps, checkpoints at 2 and 4
+        auto ds = data::Dataset::load((dir / "data").string());
+        trainer::AdaptOptions opts;
+        opts.domain = "test/domain";
+        opts.output_dir = (dir / "run").string();
+        opts.checkpoint_every = 2;
+        opts.tokens = 5 * bt;
+        opts.log_to_stdout = false;
+        auto tr = trainer::AdaptTrainer::create(fb, cfg, ds, opts, dev);
+        CHECK(!tr.done());
+        tr.run();
+        CHECK(tr.done() && ds.tokens_consumed() == 5 * bt);
+        for (const char* f : {"adapter.safetensors", "adapter.json", "adapter.centroid",
+                              "centroids/step-2.centroid", "centroids/step-4.centroid",
+                              "centroids/step-5.centroid", "step-2/optimizer.safetensors",
+                              "step-4/train_state.json"})
+            CHECK(fs::exists(dir / "run" / f));
+        auto js = read_file(dir / "run" / "adapter.json");
+        std::string j(js.begin(), js.end());
+        CHECK(j.find("\"step\": 5") != std::string::npos &&
+              j.find("\"tokens_trained\": 640") != std::string::npos);
+    }
+    // step by step, checkpoint at 2; then a trainer resumed from it
+    auto dsA = data::Dataset::load((dir / "data").string());
+    trainer::AdaptOptions oa;
+    oa.output_dir = (dir / "a").string();
+    oa.checkpoint_every = 2;
+    oa.tokens = 10 * bt;
+    oa.log_to_stdout = false;
+    auto A = trainer::AdaptTrainer::create(fb, cfg, dsA, oa, dev);
+    trainer::StepMetrics ma{};
+    for (int i = 0; i < 3; i++) {
+        ma = A.step();
+        CHECK(ma.step == (size_t)i + 1 && ma.tokens_consumed == (i + 1) * bt);
+        CHECK(std::isfinite(ma.loss) && ma.loss > 0.f && ma.grad_norm > 0.f);
+        CHECK(ma.grad_norm <= cfg.grad_clip && ma.learning_rate > 0.f);
+    }
+    CHECK(fs::exists(dir / "a" / "step-2" / "optimizer.safetensors"));
+    auto stA = adapter_state(A.engine(), cfg.inject_mask(), fb.config, cfg.rank);
+    std::vector<double> cA(257);
+    CHECK(ta_engine_centroid(A.engine(), cA.data()) == 0);
+
+    auto dsB = data::Dataset::load((dir / "data").string());
+    trainer::AdaptOptions ob = oa;
+    ob.output_dir = (dir / "b").string();
+    ob.resume_from = (dir / "a" / "step-2").string();
+    auto Bt = trainer::AdaptTrainer::create(fb, cfg, dsB, ob, dev);
+    trainer::StepMetrics mb = Bt.step();
+    CHECK(mb.step == 3 && mb.tokens_consumed == 3 * bt && dsB.tokens_consumed() == 3 * bt);
+    CHECK(mb.loss == ma.loss && mb.grad_norm == ma.grad_norm &&
+          mb.learning_rate == ma.learning_rate);
+    auto stB = adapter_state(Bt.engine(), cfg.inject_mask(), fb.config, cfg.rank);
+    CHECK(stA.size() == stB.size());
+    size_t diff = 0;
+    for (size_t i = 0; i < stA.size() && i < stB.size(); i++) diff += stA[i] != stB[i];
+    CHECK(diff == 0);
+    std::vector<double> cB(257);
+    CHECK(ta_engine_centroid(Bt.engine(), cB.data()) == 0);
+    CHECK(cA == cB && cA[256] > 0);
+    // a checkpoint of another configuration is refused
+    adapter::AdapterConfig other = cfg;
+    other.inject_k = true;
+    auto dsC = data::Dataset::load((dir / "data").string());
+    CHECK(throws<std::runtime_error>(
+        [&] { (void)trainer::AdaptTrainer::create(fb, other, dsC, ob, dev); }, "resume:"));
 }
 
 int main(int argc, char** argv) {

@@ -34,7 +34,7 @@ def compare(orc, eng, mc, ac, what, bar=1e-2):
     assert not bad, "; ".join(bad)
 
 
-def check_band(orc, eng, mc, ac, before=None):
+def check_band(orc, eng, mc, ac, before=None, bar=1e-2):
     """Updated adapters vs the oracle where the update is determined.
 
     An AdamW update m_hat/(sqrt(v_hat)+eps) is a sign function of the
@@ -43,7 +43,8 @@ def check_band(orc, eng, mc, ac, before=None):
     GPU-vs-oracle gradient error band can legitimately move the other way.
     Checked per tensor: over the elements where |g_oracle| exceeds 4x the
     RMS gradient difference, the update (updated - before; before = 0 for B
-    at step 1) has relative L2 <= 1e-2 against the oracle's; as a sanity
+    at step 1) has relative L2 <= bar (1e-2, or a per-tensor bar given as
+    bar(layer, target, "gA" | "gB")) against the oracle's; as a sanity
     bound on the gradient error, fewer
     than 25% of elements are excluded (measured on MI355X: ~1% at c1, 3-10%
     on the 2-layer config whose gradients differ from the oracle by up to
@@ -54,12 +55,13 @@ def check_band(orc, eng, mc, ac, before=None):
             go, gg = orc.adapter(l, t, "g" + w), eng.adapter(l, t, "g" + w)
             if not np.any(go):
                 continue
+            b = bar(l, t, "g" + w) if callable(bar) else bar
             band = 4.0 * float(np.sqrt(np.mean((gg.astype(np.float64) - go) ** 2)))
             sure = np.abs(go) > band
             b0 = before[(l, t, w)] if before else np.zeros_like(go)
             uo = (orc.adapter(l, t, w).astype(np.float64) - b0)[sure]
             ug = (eng.adapter(l, t, w).astype(np.float64) - b0)[sure]
-            assert rel(ug, uo) <= 1e-2, (l, t, w, rel(ug, uo))
+            assert rel(ug, uo) <= b, (l, t, w, rel(ug, uo), b)
             assert (~sure).mean() < 0.25, (l, t, w, float((~sure).mean()))
 
 

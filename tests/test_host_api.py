@@ -99,6 +99,67 @@ def test_cosine_schedule_bit_exact_vs_reference(cpu_run):
     np.testing.assert_array_equal(np.array(orc, np.float32).view(np.uint32), ref.view(np.uint32))
 
 
+def test_adapter_files_match_independent_readers(cpu_run):
+    """The writer's files (src/checkpoint/adapter_writer.cpp:30-150 formats),
+    read back with the safetensors library and compared with Python's json:
+    adapter.safetensors holds every tensor as flat 1-D BF16 (round to
+    nearest even, ties included), its header is the compact JSON with
+    sorted keys padded with spaces to a multiple of 8 and the data follow in
+    tensor order; optimizer.safetensors holds the exact F32 masters, their
+    moments and the F64 centroid sums; adapter.json and train_state.json are
+    2-space-indented JSON with sorted keys, byte for byte."""
+    import json
+
+    import torch
+    from safetensors.torch import load_file
+
+    w = cpu_run / "writer"
+    names = [(ln.split()[0], int(ln.split()[1])) for ln in open(w / "names.txt")]
+    vals = np.fromfile(w / "values.bin", np.float32)
+    sums = np.fromfile(w / "sums.bin", np.float64)
+    expect, off = {}, 0
+    for n, c in names:
+        expect[n] = vals[off:off + c]
+        off += c
+    assert off == vals.size
+    for d in ("ckpt", "final"):
+        raw = open(w / d / "adapter.safetensors", "rb").read()
+        hl = int.from_bytes(raw[:8], "little")
+        hdr, o = {}, 0
+        for n, c in names:
+            hdr[n] = {"data_offsets": [o, o + 2 * c], "dtype": "BF16", "shape": [c]}
+            o += 2 * c
+        text = json.dumps(hdr, separators=(",", ":"), sort_keys=True)
+        text += " " * (-len(text) % 8)
+        assert raw[8:8 + hl].decode() == text and len(raw) == 8 + hl + o
+        t = load_file(str(w / d / "adapter.safetensors"))
+        assert sorted(t) == sorted(expect)
+        for n, c in names:
+            want = torch.from_numpy(expect[n].copy()).to(torch.bfloat16)
+            assert t[n].dtype == torch.bfloat16 and tuple(t[n].shape) == (c,)
+            assert torch.equal(t[n].view(torch.int16), want.view(torch.int16)), n
+            # the two ties the C++ side planted: 1 + 2^-8 -> 1, -(1 + 3 * 2^-8) -> -(1 + 2^-6)
+            assert t[n][0].item() == 1.0 and t[n][1].item() == -1.015625
+    opt = load_file(str(w / "ckpt" / "optimizer.safetensors"))
+    assert len(opt) == 3 * len(names) + 1
+    for n, c in names:
+        assert torch.equal(opt[n], torch.from_numpy(expect[n].copy()))
+        for m in (".exp_avg", ".exp_avg_sq"):
+            assert opt[n + m].dtype == torch.float32 and tuple(opt[n + m].shape) == (c,)
+    assert opt["centroid.sums"].dtype == torch.float64
+    np.testing.assert_array_equal(opt["centroid.sums"].numpy(), sums)
+    meta = dict(domain='golang/gin "x"', architecture="qwen2", base_model="unknown",
+                base_sha="abc123", rank=4, alpha=float(np.float32(0.1)), target_begin=0,
+                target_end=1, inject_q=True, inject_k=False, inject_v=True, inject_o=True,
+                inject_up=False, inject_down=True, tokens_trained=3584, centroid_dim=16,
+                centroid_count=16, step=7, tensor_adapt_version="0.1.0")
+    assert open(w / "ckpt" / "adapter.json").read() == json.dumps(meta, indent=2, sort_keys=True)
+    meta.update(domain="golang/gin", step=9, tokens_trained=4608)
+    assert open(w / "final" / "adapter.json").read() == json.dumps(meta, indent=2, sort_keys=True)
+    assert open(w / "ckpt" / "train_state.json").read() == json.dumps(
+        {"step": 7, "tokens_consumed": 3584}, indent=2)
+
+
 @pytest.mark.gpu
 def test_host_api_gpu(tmp_path):
     print("case: test_host_api gpu", flush=True)

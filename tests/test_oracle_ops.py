@@ -104,6 +104,57 @@ def test_gemm_f32_vs_numpy():
     assert rel_l2(C.T, ref) < 1e-6
 
 
+def test_fp32_accumulation_mode_matches_blocked_float32_sums():
+    """The oracle's measurement mode (FP32 accumulators fed by 16-wide K
+    blocks, oracle/accum_floor.py) against a numpy restatement: each block's
+    products (exact in float32 for BF16-valued operands) summed in k order
+    in float32 (cumsum is sequential), then added to the float32 running
+    sum.  Bit for bit; the default FP64 mode is restored afterwards and
+    differs from it by accumulation rounding only."""
+    M, N, K = 5, 7, 70  # K not a multiple of 16: a short last block
+    A = O.f32_from_bf16(O.bf16_from_f32(RNG.standard_normal((K, M)).astype(np.float32)))
+    B = O.f32_from_bf16(O.bf16_from_f32(RNG.standard_normal((K, N)).astype(np.float32)))
+    A, B = np.ascontiguousarray(A), np.ascontiguousarray(B)
+    want = np.empty((N, M), np.float32)
+    for i in range(M):
+        for j in range(N):
+            acc = np.float32(0)
+            for k0 in range(0, K, 16):
+                prod = (A[k0:k0 + 16, i] * B[k0:k0 + 16, j]).astype(np.float32)
+                acc = np.float32(acc + np.cumsum(prod, dtype=np.float32)[-1])
+            want[j, i] = acc
+    C32 = np.zeros((N, M), np.float32)
+    C64 = np.zeros((N, M), np.float32)
+    try:
+        O.set_accum_mode(1)
+        assert O.gemm_f32(0, 1, M, N, K, 1.0, A, M, B, N, 0.0, C32, M) == 0
+    finally:
+        O.set_accum_mode(0)
+    assert O.gemm_f32(0, 1, M, N, K, 1.0, A, M, B, N, 0.0, C64, M) == 0
+    np.testing.assert_array_equal(C32.view(np.uint32), want.view(np.uint32))
+    exact = (A.astype(np.float64).T @ B.astype(np.float64)).T
+    assert np.max(np.abs(C64 - exact)) <= 1e-6 * np.abs(exact).max()
+    assert 0 < np.max(np.abs(C32 - exact)) <= 1e-5 * np.abs(exact).max()
+
+
+def test_c2_accumulation_floor_fixture():
+    """tests/golden/c2_accum_floor.json (oracle/accum_floor.py): every gB of
+    step 1 and every gA and gB of step 2 of c2's 24 x 4 pairs, each floor a
+    positive distance well below the loss-level scale, the losses of the two
+    accumulations within 1e-4 of each other (measured 1.9e-5 and 3.4e-6)."""
+    import json
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                        "c2_accum_floor.json")
+    f = json.load(open(path))
+    assert [len(s["floor"]) for s in f["steps"]] == [96, 192]
+    for s in f["steps"]:
+        v = np.array(list(s["floor"].values()))
+        assert np.all(v > 1e-3) and np.all(v < 0.1)
+        a, b = s["loss"]
+        assert abs(a - b) <= 1e-4 * abs(a)
+
+
 # ── RMSNorm ──────────────────────────────────────────────────
 def test_rms_norm_fwd_vs_torch():
     rows, D, eps = 64, 896, 1e-6
