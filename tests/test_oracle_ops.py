@@ -420,23 +420,40 @@ def test_sum_sq():
 
 
 # ── LoRA A init hash (adapter_model.cu:15-39) ────────────────
-def kaiming_py(in_dim, rank, seed=0x1234):
-    out = []
-    for i in range(in_dim * rank):
-        r = (seed ^ ((i * 2654435761) & 0xFFFFFFFF)) & 0xFFFFFFFF
-        r ^= r >> 16
-        r = (r * 0x45D9F3B) & 0xFFFFFFFF
-        r ^= r >> 16
-        u = np.float32(r & 0xFFFFFF) / np.float32(0xFFFFFF) * np.float32(2) - np.float32(1)
-        out.append(u * np.sqrt(np.float32(1) / np.float32(in_dim)))
-    return np.array(out, np.float32)
+def test_kaiming_init_hash_known_answers():
+    """A-init hash of adapter_model.cu:15-39 (seed 0x1234, in_dim 96, rank 4),
+    element by element, against values worked out by hand from its steps:
 
+        r = seed ^ (i * 2654435761)   (32-bit)
+        r ^= r >> 16;  r *= 0x45d9f3b (32-bit);  r ^= r >> 16
+        u = (float)(r & 0xFFFFFF) / (float)0xFFFFFF * 2 - 1   (F32 ops)
+        A = u * sqrtf(1 / (float)in_dim)
 
-def test_kaiming_init_hash():
+    i = 0:  r = 0x1234;  0x1234 ^ 0 = 0x1234;  0x1234 * 0x45d9f3b
+            = 4660 * 73244475 = 341319253500 = 79 * 2^32 + 2016837116
+            -> 0x78367dfc;  ^ 0x7836 -> 0x783605ca;  low 24 bits 0x3605ca
+            = 3540426;  u = 3540426 / 16777215 * 2 - 1 = -0.57794833
+            (F32 0xbf13f46c);  sqrtf(1/96) = 0.10206207 (0x3dd105ec);
+            A = 0xbd719bf1.
+    The other rows follow the same steps (i * 2654435761 mod 2^32 in the
+    first column).  A wrong multiplier, shift or mask changes every one."""
+    table = [  # i, i*2654435761 mod 2^32, r after xor-shift, after multiply, final r, A (F32 bits)
+        (0, 0x00000000, 0x00001234, 0x78367dfc, 0x783605ca, 0xbd719bf1),
+        (1, 0x9e3779b1, 0x9e37f5b2, 0x42292e06, 0x42296c2f, 0xbd8d615d),
+        (2, 0x3c6ef362, 0x3c6edd38, 0x064ac3e8, 0x064ac5a2, 0xbd2dd786),
+        (95, 0xb69628af, 0xb6968c0d, 0xaa6759ff, 0xaa67f398, 0xbc9d1577),
+        (383, 0xb4ff0fcf, 0xb4ffa904, 0xf7596fec, 0xf75998b5, 0xbcfad9ba),
+    ]
     a16, a32 = O.kaiming_init(96, 4)
-    ref = kaiming_py(96, 4)
-    assert np.array_equal(a32.ravel(), ref)
+    bits = a32.ravel().view(np.uint32)
+    for i, prod, r1, r2, r3, want in table:
+        # the table's own arithmetic, so a typo in it cannot pass silently
+        assert prod == (i * 2654435761) & 0xFFFFFFFF
+        assert r1 == (0x1234 ^ prod) ^ ((0x1234 ^ prod) >> 16)
+        assert r2 == (r1 * 0x45D9F3B) & 0xFFFFFFFF and r3 == r2 ^ (r2 >> 16)
+        assert int(bits[i]) == want, (i, hex(int(bits[i])), hex(want))
     assert np.array_equal(a16, O.bf16_from_f32(a32))
+    assert a16.ravel()[0] == 0xbd72  # 0xbd719bf1 rounded to nearest even BF16
     big16, big32 = O.kaiming_init(896, 8)
     bound = math.sqrt(1 / 896)
     assert np.all(np.abs(big32) <= bound + 1e-7)
