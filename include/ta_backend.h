@@ -61,6 +61,22 @@ int ta_sdpa_bwd(const uint16_t* dout, const uint16_t* Q, const uint16_t* K,
                 const uint16_t* V, const float* attn_w, uint16_t* dQ, uint16_t* dK,
                 uint16_t* dV, int B, int T, int Hq, int Hkv, int head_dim, void* stream);
 
+/* The step engine's attention, which keeps no probabilities (no
+ * counterpart in the reference, whose sdpa_fwd stores P for sdpa_bwd):
+ * the forward writes O [B*T, Hq*hd] BF16, its F32 copy O32 (may be NULL)
+ * and, per (b, hq, query row), the row's score maximum in base-2 units and
+ * 1/sum of its exponentials as an F32 pair in stats [B*Hq*T][2]; the
+ * backward recomputes P = exp2(S*scale*log2(e) - max) * (1/sum) from Q, K
+ * and those pairs, takes the row dots dO.O from O32 (required), and
+ * overwrites dQ/dK/dV as ta_sdpa_bwd does. */
+int ta_attn_fwd_rowstats(const uint16_t* Q, const uint16_t* K, const uint16_t* V, uint16_t* O,
+                         float* O32, float* stats, int B, int T, int Hq, int Hkv, int head_dim,
+                         void* stream);
+int ta_attn_bwd_rowstats(const uint16_t* dout, const uint16_t* Q, const uint16_t* K,
+                         const uint16_t* V, const float* stats, const float* O32, uint16_t* dQ,
+                         uint16_t* dK, uint16_t* dV, int B, int T, int Hq, int Hkv, int head_dim,
+                         void* stream);
+
 /* ── gated SiLU ─────────────────────────────────────────────────────
  * replaces ops::silu_mul_fwd / silu_mul_bwd  ops.hpp:72-86 (ops.cu:913-952). */
 int ta_silu_mul_fwd(const uint16_t* gate, const uint16_t* up, uint16_t* out, int64_t N,

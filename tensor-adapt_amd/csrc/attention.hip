@@ -17,7 +17,9 @@
 // Every loop over tiles loads the next tile's operands into registers while
 // the current tile computes, so global latency overlaps the MFMAs.
 //
-// Forward (per b, hq, query tile; heaviest tiles launch first):
+// Forward with stored probabilities (the C-ABI's sdpa_fwd; per b, hq,
+// query tile; heaviest tiles launch first; the engine's forward, which
+// stores no P, is k_attn_fwd_t below):
 //   pass 1: online row max / sum of exp over key tiles 0..diag;
 //   pass 2: recompute S, P = exp(S - max) / sum (the reference's softmax,
 //   ops.cu:352-396), store P (F32), O += P*V; O is stored in BF16 and, for
@@ -389,142 +391,278 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
         }
 }
 
-// Single-pass forward for the engine (P not stored): online softmax over
-// the key tiles, O rescaled by exp2(m_old - m_new) whenever a row's running
-// max grows, O = (sum_k exp2(s_k - m) V_k) / l at the end.  The rows' final
-// (max, 1/sum) are kept for the backward, which recomputes P from them
-// exactly as the two-pass form would have produced it.  exp2(s - m) <= 1
-// enters the P.V MFMAs as a BF16 hi/lo pair, as in the two-pass form.
+// ── forward, transposed scores (the engine's form: P not stored) ───────────
+// Per block: 128 queries of one (b, hq), 4 waves of 32; key tiles of 64,
+// staged in LDS in the transposing-read layout.  Each wave computes
+// S^T = K Q^T with 32x32x16 MFMAs (K rows as the A operand, the wave's Q
+// rows as the B operand, held in registers): lane l then holds the scores
+// of query l%32 for keys 8(r/4) + 4(l/32) + r%4 (r < 16) of each 32-key
+// half of the tile, so a query's softmax statistics combine over its own
+// registers and one exchange with lane l^32.  With the keys of a 16-wide
+// k step taken in that order (r < 8: keys 0..15 of a half, r >= 8: keys
+// 16..31), the probabilities in registers are directly the B operand of
+// O^T += V^T P^T, whose A operand (V^T, the same key order) comes from the
+// V tile through two transposing reads per fragment.  P never passes
+// through LDS.  Single pass with an online softmax: O is rescaled by
+// exp2(m_old - m_new) when some query's running max grows (skipped when
+// none did: a factor of exactly 1); P = exp2(S scale log2(e) - m) enters the
+// MFMAs as a BF16 hi/lo pair; the rows' final (max, 1/sum) are kept, and
+// the backward recomputes P from them.
+constexpr int TQ2 = 128;  // queries per block (4 waves x 32)
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ floatx16 mfma32(bf16x8_t a, bf16x8_t b, floatx16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ floatx16 zero16() {
+    floatx16 z;
+#pragma unroll
+    for (int i = 0; i < 16; i++) z[i] = 0.f;
+    return z;
+}
+
+typedef __attribute__((address_space(3))) void* lds_vptr_t;
+
+// Loads of one 64-row x HD tile (rows row0.., row stride rs) from global
+// memory straight into LDS in the tr_off<HD/16> layout, as buffer loads:
+// each buffer_load_dwordx4 ... lds fills 1 KB of the tile (lane i writes
+// bytes 16i..16i+15, so lane i fetches the 16-byte chunk that tr_off places
+// there); wave w issues instructions w, w + 4, ...  Rows at or past T read
+// as zeros through the buffer's bounds (the resource covers rows 0..T-1);
+// the lane offsets are fixed for the kernel and a tile's row offset is one
+// scalar.
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_fwd1(const bf16* __restrict__ Q,
-                                                   const bf16* __restrict__ K,
-                                                   const bf16* __restrict__ V,
-                                                   bf16* __restrict__ O, float* __restrict__ O32,
-                                                   float2* __restrict__ stats, int T, int Hq,
-                                                   int Hkv, float scale) {
-    constexpr int VST = HD / 16;
-    __shared__ __attribute__((aligned(16))) bf16 sK[TK * (HD + 8)];
-    __shared__ __attribute__((aligned(16))) char sV[TK * HD * 2];
-    __shared__ __attribute__((aligned(16))) char sP[4][2][TK * 16 * 2];
-    int nqt = (T + TQ - 1) / TQ;
-    int nbh = gridDim.x / nqt;
-    int qt = nqt - 1 - (int)(blockIdx.x / nbh);  // longest rows launch first
-    int bh = (int)(blockIdx.x % nbh);
-    int b = bh / Hq, hq = bh % Hq, hkv = hq / (Hq / Hkv);
-    int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    int64_t qs = (int64_t)Hq * HD, ks_ = (int64_t)Hkv * HD;
+struct AttnDma {
+    static constexpr int RB = HD * 2, RPI = 1024 / RB, NI = 64 / RPI, PER = NI / 4;
+    int voff[PER];
+    __device__ __forceinline__ void init(int64_t rs, int w, int lane) {
+#pragma unroll
+        for (int h = 0; h < PER; h++) {
+            const int r = (w + 4 * h) * RPI + (lane * 16) / RB, ib = (lane * 16) % RB;
+            const int col = 16 * ((ib >> 5) ^ tr_x<HD / 16>(r)) + 8 * ((ib >> 4) & 1);
+            voff[h] = (int)((r * rs + col) * 2);
+        }
+    }
+    // tile rows row0 .. row0 + 63 of the buffer into `tile`.  The loads are
+    // issued from inline assembly so that the compiler's wait insertion does
+    // not pair later LDS reads of other tiles with them (it cannot tell the
+    // buffers' loads apart and would wait for every one); the kernel orders
+    // them with explicit vmcnt waits and barriers.
+    __device__ __forceinline__ void issue(i32x4_t rsrc, int64_t rs, int row0, char* tile,
+                                          int w) const {
+        const int so = (int)(row0 * rs * 2);
+#pragma unroll
+        for (int h = 0; h < PER; h++) {
+            const uint32_t la = (uint32_t)(uintptr_t)(tile + (w + 4 * h) * 1024);
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                         :
+                         : "s"(__builtin_amdgcn_readfirstlane(la)), "v"(voff[h]), "s"(rsrc),
+                           "s"(so)
+                         : "memory", "m0");
+#pragma clang diagnostic pop
+        }
+    }
+};
+
+// Buffer resource over rows 0..T-1 of a [rows, rs] BF16 tensor at base:
+// 64-bit base, stride 0, T*rs*2 bytes (reads past them return zeros).
+__device__ __forceinline__ i32x4_t rows_rsrc(const bf16* base, int T, int64_t rs) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    i32x4_t r;
+    r[0] = (int)(uint32_t)a;
+    r[1] = (int)(uint32_t)(a >> 32);
+    r[2] = (int)(T * rs * 2);
+    r[3] = 0x00020000;
+    return r;
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_fwd_t(const bf16* __restrict__ Q,
+                                                    const bf16* __restrict__ K,
+                                                    const bf16* __restrict__ V,
+                                                    bf16* __restrict__ O, float* __restrict__ O32,
+                                                    float2* __restrict__ stats, int T, int Hq,
+                                                    int Hkv, float scale) {
+    constexpr int NST = HD / 16, NDB = HD / 32;
+    // Three K/V buffer pairs, each its own array (so the compiler can match
+    // each LDS read with the loads that fill that buffer and waits for no
+    // other), used round-robin by a loop unrolled three times: tile kt + 2
+    // is loaded into the buffers of tile kt - 1 once every wave is done
+    // with it.
+    constexpr int TB = TK * HD * 2, LPT = 2 * (TB / 1024) / 4;  // DMA per wave per tile
+    __shared__ __attribute__((aligned(1024))) char sK0[TB], sK1[TB], sK2[TB];
+    __shared__ __attribute__((aligned(1024))) char sV0[TB], sV1[TB], sV2[TB];
+    const int nqt = (T + TQ2 - 1) / TQ2;
+    const int nbh = gridDim.x / nqt;
+    const int qt = nqt - 1 - (int)(blockIdx.x / nbh);  // longest rows launch first
+    const int bh = (int)(blockIdx.x % nbh);
+    const int b = bh / Hq, hq = bh % Hq, hkv = hq / (Hq / Hkv);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t qs = (int64_t)Hq * HD, ks_ = (int64_t)Hkv * HD;
     const bf16* Qh = Q + (int64_t)b * T * qs + hq * HD;
     const bf16* Kh = K + (int64_t)b * T * ks_ + hkv * HD;
     const bf16* Vh = V + (int64_t)b * T * ks_ + hkv * HD;
-    int q0 = qt * TQ;
-    int rowA = q0 + 16 * w + (lane & 15);
-    bf16x8_t qf[HD / 32];
+    const int q0 = qt * TQ2, qw0 = q0 + 32 * w;
+    const int qrow = qw0 + (lane & 31);  // this lane's query
+    bf16x8_t qf[NST];
 #pragma unroll
-    for (int ks = 0; ks < HD / 32; ks++) qf[ks] = ld_head8(Qh, qs, rowA, T, 32 * ks + 8 * (lane >> 4));
-    const int rbase = q0 + 16 * w + 4 * (lane >> 4);
+    for (int st = 0; st < NST; st++) qf[st] = ld_head8(Qh, qs, qrow, T, 16 * st + 8 * (lane >> 5));
+    // per-lane LDS offsets within a tile (the tile-, half- and step-dependent
+    // parts are multiples of 16 rows, which the row XOR of tr_off ignores):
+    // K rows for S^T, and the two transposing reads of each 32-wide V^T block
+    int koff[NST], voff[NDB][2];
+#pragma unroll
+    for (int st = 0; st < NST; st++) koff[st] = tr_off<NST>(lane & 31, 16 * st + 8 * (lane >> 5));
+    {
+        const int g = lane >> 4, j = lane & 15;
+        const int r = 4 * (g >> 1) + (j >> 2), c = 16 * (g & 1) + 4 * (j & 3);
+#pragma unroll
+        for (int db = 0; db < NDB; db++) {
+            voff[db][0] = tr_off<NST>(r, 32 * db + c);
+            voff[db][1] = tr_off<NST>(r + 8, 32 * db + c);
+        }
+    }
     const float sl2 = scale * kLog2e;
-    Rows64<HD> lk, lv;
-    float m[4], l[4];
+    float m = -INFINITY, l = 0.f;
+    floatx16 acc[NDB];
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        m[r] = -INFINITY;
-        l[r] = 0.f;
+    for (int db = 0; db < NDB; db++) acc[db] = zero16();
+    // key tiles holding keys <= the block's last query
+    const int nkt = min((T + TK - 1) / TK, (min(q0 + TQ2, T) - 1) / TK + 1);
+    // tiles past the last one reload it into a buffer that is never read,
+    // so every wave issues the same number of loads per step
+    AttnDma<HD> dma;
+    dma.init(ks_, w, lane);
+    const i32x4_t rK = rows_rsrc(Kh, T, ks_), rV = rows_rsrc(Vh, T, ks_);
+    auto issue = [&](int kt, char* dK, char* dV) {
+        const int kq = min(kt, nkt - 1);
+        dma.issue(rK, ks_, kq * TK, dK, w);
+        dma.issue(rV, ks_, kq * TK, dV, w);
+    };
+    auto tile = [&](const char* __restrict__ sK, const char* __restrict__ sV, int kt) {
+        const int k0 = kt * TK;
+        if (k0 > qw0 + 31 || qw0 >= T) return;  // every key follows every query of this wave
+        floatx16 s[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            s[h] = zero16();
+#pragma unroll
+            for (int st = 0; st < NST; st++)
+                s[h] = mfma32(*(const bf16x8_t*)(sK + h * 32 * 32 * NST + koff[st]), qf[st], s[h]);
+        }
+        // scores in base-2 units; on a tile reaching past this wave's first
+        // query (or past T), keys after the query are masked
+        float mx = -INFINITY;
+        if (k0 + TK - 1 > qw0) {
+            const int kl = k0 + 4 * (lane >> 5);
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int key = kl + 32 * h + 8 * (r >> 2) + (r & 3);
+                    const bool ok = (key <= qrow) & (key < T);
+                    s[h][r] = ok ? s[h][r] * sl2 : -INFINITY;
+                    mx = fmaxf(mx, s[h][r]);
+                }
+        } else {
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    s[h][r] *= sl2;
+                    mx = fmaxf(mx, s[h][r]);
+                }
+        }
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mn = fmaxf(m, mx);
+        const float al = m == -INFINITY ? 0.f : exp2_fast(m - mn);
+        m = mn;
+        // rescaling by exactly 1 changes nothing: skipped unless some query's
+        // running max grew
+        if (__ballot(al != 1.f) != 0) {
+#pragma unroll
+            for (int db = 0; db < NDB; db++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[db][r] *= al;
+        }
+        float add = 0.f;
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int hf = 0; hf < 2; hf++) {
+                // k step (h, hf): keys 32h + 16hf .. +15, registers r = 8hf .. 8hf + 7
+                float p[8];
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    p[e] = exp2_fast(s[h][8 * hf + e] - m);  // 0 where masked
+                    add += p[e];
+                }
+                bf16x8_t ph, pl;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const bf16 hb = f2bf(p[e]);
+                    ph[e] = __builtin_bit_cast(__bf16, hb);
+                    pl[e] = __builtin_bit_cast(__bf16, f2bf(p[e] - bf2f(hb)));
+                }
+                const char* vt = sV + (32 * h + 16 * hf) * 32 * NST;
+#pragma unroll
+                for (int db = 0; db < NDB; db++) {
+                    i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_i16x4_p)(vt + voff[db][0]));
+                    i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_i16x4_p)(vt + voff[db][1]));
+                    const bf16x8_t va = __builtin_bit_cast(
+                        bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                    acc[db] = mfma32(va, pl, acc[db]);
+                    acc[db] = mfma32(va, ph, acc[db]);
+                }
+            }
+        l = l * al + add;
+    };
+    TA_WAIT_VMCNT(0);  // the Q fragments are in; only tile loads are counted below
+    issue(0, sK0, sV0);
+    issue(1, sK1, sV1);
+    // one step: wait for this wave's loads of the tile (one later tile stays
+    // in flight), barrier (after it every wave's loads have landed and every
+    // wave is done reading the previous tile's buffers), refill those
+    // buffers, compute
+#define ATT_STEP(KT, SK, SV, RK, RV)          \
+    if ((KT) < nkt) {                         \
+        TA_WAIT_VMCNT(LPT);                   \
+        __builtin_amdgcn_s_barrier();         \
+        issue((KT) + 2, RK, RV);              \
+        tile(SK, SV, (KT));                   \
     }
-    floatx4 acc[HD / 16];
-#pragma unroll
-    for (int j = 0; j < HD / 16; j++) acc[j] = zero4();
-    lk.load(Kh, ks_, 0, T);
-    lv.load(Vh, ks_, 0, T);
-    char* sPh = sP[w][0];
-    char* sPl = sP[w][1];
-    for (int kt = 0; kt <= qt; kt++) {
-        __syncthreads();
-        lk.store(sK);
-#pragma unroll
-        for (int i = 0; i < Rows64<HD>::NR; i++) {
-            int q = threadIdx.x + 256 * i;
-            *(u32x4*)(sV + tr_off<VST>(q / (HD / 8), (q % (HD / 8)) * 8)) = lv.v[i];
-        }
-        __syncthreads();
-        if (kt < qt) {
-            lk.load(Kh, ks_, (kt + 1) * TK, T);
-            lv.load(Vh, ks_, (kt + 1) * TK, T);
-        }
-        floatx4 S[4];
-        wave_qk<HD>(S, qf, sK, lane);
-        const bool diag = kt == qt;
-        // scores in base-2 units, masked on the diagonal tile; new row max
-        float v[4][4], al[4];
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            float tmax = -INFINITY;
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const int key = kt * TK + 16 * t + (lane & 15);
-                v[t][r] = (!diag || (key <= rbase + r && key < T)) ? S[t][r] * sl2 : -INFINITY;
-                tmax = fmaxf(tmax, v[t][r]);
-            }
-            const float mn = fmaxf(m[r], red16_max(tmax));
-            al[r] = m[r] == -INFINITY ? 0.f : exp2_fast(m[r] - mn);
-            m[r] = mn;
-        }
-        float add[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int t = 0; t < 4; t++) {
-            const int kl = 16 * t + (lane & 15);
-            float p[4];
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                p[r] = exp2_fast(v[t][r] - m[r]);  // 0 where masked
-                add[r] += p[r];
-            }
-            uint2 hi, lo;
-            hi.x = pack2(p[0], p[1]);
-            hi.y = pack2(p[2], p[3]);
-            lo.x = pack2(p[0] - lo2f(hi.x), p[1] - hi2f(hi.x));
-            lo.y = pack2(p[2] - lo2f(hi.y), p[3] - hi2f(hi.y));
-            const int off = tr_off<1>(kl, 4 * (lane >> 4));
-            *(uint2*)(sPh + off) = hi;
-            *(uint2*)(sPl + off) = lo;
-        }
-#pragma unroll
-        for (int r = 0; r < 4; r++) l[r] = l[r] * al[r] + add[r];
-#pragma unroll
-        for (int j = 0; j < HD / 16; j++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) acc[j][r] *= al[r];
-        wave_sync();  // sP[w] is this wave's own tile
-#pragma unroll
-        for (int kc = 0; kc < TK / 32; kc++) {
-            const bf16x8_t ah = tr_frag<1>(sPh, 32 * kc, 0, lane);
-            const bf16x8_t alo = tr_frag<1>(sPl, 32 * kc, 0, lane);
-#pragma unroll
-            for (int j = 0; j < HD / 16; j++) {
-                const bf16x8_t bv = tr_frag<VST>(sV, 32 * kc, 16 * j, lane);
-                acc[j] = mfma16(alo, bv, acc[j]);
-                acc[j] = mfma16(ah, bv, acc[j]);
-            }
-        }
+    for (int kt = 0; kt < nkt; kt += 3) {
+        ATT_STEP(kt, sK0, sV0, sK2, sV2);
+        ATT_STEP(kt + 1, sK1, sV1, sK0, sV0);
+        ATT_STEP(kt + 2, sK2, sV2, sK1, sV1);
     }
-    float inv[4];
+#undef ATT_STEP
+    TA_WAIT_VMCNT(0);  // the surplus loads have landed before the block ends
+    if (qw0 >= T) return;
+    const float inv = 1.f / (l + __shfl_xor(l, 32, 64));
+    if (qrow < T && lane < 32) stats[(int64_t)bh * T + qrow] = make_float2(m, inv);
+    if (qrow >= T) return;
+    bf16* orow = O + ((int64_t)b * T + qrow) * qs + hq * HD;
+    float* o32row = O32 ? O32 + ((int64_t)b * T + qrow) * qs + hq * HD : nullptr;
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        inv[r] = 1.f / red16_sum(l[r]);
-        if (rbase + r < T && (lane & 15) == 0)
-            stats[(int64_t)bh * T + rbase + r] = make_float2(m[r], inv[r]);
-    }
-    bf16* Oh = O + (int64_t)b * T * qs + hq * HD;
-    float* O32h = O32 ? O32 + (int64_t)b * T * qs + hq * HD : nullptr;
+    for (int db = 0; db < NDB; db++)
 #pragma unroll
-    for (int j = 0; j < HD / 16; j++)
+        for (int j = 0; j < 4; j++) {
+            // d = 32 db + 8 j + 4 (lane / 32) + 0..3
+            const int d = 32 * db + 8 * j + 4 * (lane >> 5);
+            float o[4];
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            int row = rbase + r;
-            if (row < T) {
-                const float o = acc[j][r] * inv[r];
-                Oh[(int64_t)row * qs + 16 * j + (lane & 15)] = f2bf(o);
-                if (O32h) O32h[(int64_t)row * qs + 16 * j + (lane & 15)] = o;
-            }
+            for (int i = 0; i < 4; i++) o[i] = acc[db][4 * j + i] * inv;
+            uint2 pk;
+            pk.x = pack2(o[0], o[1]);
+            pk.y = pack2(o[2], o[3]);
+            *(uint2*)(orow + d) = pk;
+            if (o32row) *(float4*)(o32row + d) = make_float4(o[0], o[1], o[2], o[3]);
         }
 }
 
@@ -1055,7 +1193,9 @@ int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* O32, f
     float2* st = (float2*)stats;
 #define AF(H) \
     k_attn_fwd<H, true><<<(int)blocks, 256, 0, s>>>(Q, K, V, O, O32, P, st, T, Hq, Hkv, scale, zero_fill)
-#define AF1(H) k_attn_fwd1<H><<<(int)blocks, 256, 0, s>>>(Q, K, V, O, O32, st, T, Hq, Hkv, scale)
+#define AF1(H)                                                                             \
+    k_attn_fwd_t<H><<<(int)((int64_t)B * Hq * ((T + TQ2 - 1) / TQ2)), 256, 0, s>>>(         \
+        Q, K, V, O, O32, st, T, Hq, Hkv, scale)
     // with P: two passes (P normalised when it is written); without: one
     if (hd == 64) {
         if (P) AF(64); else AF1(64);
@@ -1073,8 +1213,8 @@ int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* O32, f
         kprof_end(KP_ATTN_FWD, s, 4.0 * hd * tri,
                   2.0 * bt * hd * (2.0 * Hq + 2.0 * Hkv) + (O32 ? 4.0 * bt * Hq * hd : 0.0) +
                       pbytes,
-                  hd == 64 ? (P ? "void ta::k_attn_fwd<64, true>" : "void ta::k_attn_fwd1<64>")
-                           : (P ? "void ta::k_attn_fwd<128, true>" : "void ta::k_attn_fwd1<128>"));
+                  hd == 64 ? (P ? "void ta::k_attn_fwd<64, true>" : "void ta::k_attn_fwd_t<64>")
+                           : (P ? "void ta::k_attn_fwd<128, true>" : "void ta::k_attn_fwd_t<128>"));
     }
     return check_launch("sdpa_fwd");
 }
@@ -1172,6 +1312,24 @@ int ta_sdpa_fwd(const uint16_t* Q, const uint16_t* K, const uint16_t* V, uint16_
                 float* attn_w, int B, int T, int Hq, int Hkv, int head_dim, void* stream) {
     return ta::attn_fwd(Q, K, V, out, nullptr, attn_w, nullptr, B, T, Hq, Hkv, head_dim, true,
                         (hipStream_t)stream);
+}
+
+int ta_attn_fwd_rowstats(const uint16_t* Q, const uint16_t* K, const uint16_t* V, uint16_t* O,
+                         float* O32, float* stats, int B, int T, int Hq, int Hkv, int head_dim,
+                         void* stream) {
+    TA_REQUIRE(Q && K && V && O && stats, "attn_fwd_rowstats: null argument");
+    return ta::attn_fwd(Q, K, V, O, O32, nullptr, stats, B, T, Hq, Hkv, head_dim, false,
+                    (hipStream_t)stream);
+}
+
+int ta_attn_bwd_rowstats(const uint16_t* dout, const uint16_t* Q, const uint16_t* K,
+                         const uint16_t* V, const float* stats, const float* O32, uint16_t* dQ,
+                         uint16_t* dK, uint16_t* dV, int B, int T, int Hq, int Hkv, int head_dim,
+                         void* stream) {
+    TA_REQUIRE(dout && Q && K && V && stats && O32 && dQ && dK && dV,
+               "attn_bwd_rowstats: null argument");
+    return ta::attn_bwd(dout, Q, K, V, nullptr, stats, O32, dQ, dK, dV, B, T, Hq, Hkv, head_dim,
+                    nullptr, nullptr, (hipStream_t)stream);
 }
 
 int ta_sdpa_bwd(const uint16_t* dout, const uint16_t* Q, const uint16_t* K, const uint16_t* V,

@@ -19,17 +19,21 @@ typedef __attribute__((address_space(3))) i16x4_t* lds_i16x4_p;
 // XOR-permuted by row bits 1..3 so that the transposing reads of rows
 // {k0..k0+3, k0+8..k0+11} (one 32-lane phase) hit distinct banks; 16-byte
 // chunks (c % 8 == 0) stay contiguous.
+// the XOR applied to the 32-byte column unit of row r (NSTP > 1)
+template <int NSTP>
+__device__ __forceinline__ int tr_x(int r) {
+    if constexpr (NSTP == 2) return (r >> 3) & 1;
+    else if constexpr (NSTP == 4) return ((r >> 1) & 1) | (((r >> 3) & 1) << 1);
+    else return (r & 3) | (((r >> 3) & 1) << 2);
+}
+
 template <int NSTP>
 __device__ __forceinline__ int tr_off(int r, int c) {
     const int st = c >> 4, in = (c & 15) * 2;
     if constexpr (NSTP == 1) {
         return ((r * 32 + in) ^ (((r >> 3) & 1) << 7));
     } else {
-        int x;
-        if constexpr (NSTP == 2) x = (r >> 3) & 1;
-        else if constexpr (NSTP == 4) x = ((r >> 1) & 1) | (((r >> 3) & 1) << 1);
-        else x = (r & 3) | (((r >> 3) & 1) << 2);
-        return r * 32 * NSTP + 32 * (st ^ x) + in;
+        return r * 32 * NSTP + 32 * (st ^ tr_x<NSTP>(r)) + in;
     }
 }
 

@@ -362,6 +362,58 @@ def test_kmeans_pp_bit_exact():
 
 # ── attention ─────────────────────────────────────────────────────────────
 ATTN_SHAPES = [(1, 128, 14, 2, 64), (2, 256, 12, 2, 128), (1, 100, 4, 2, 64), (1, 512, 14, 2, 64)]
+ROWSTAT_SHAPES = [(1, 1024, 12, 2, 128), (2, 200, 14, 2, 64), (1, 100, 4, 2, 128),
+                  (1, 512, 14, 2, 64), (1, 2048, 28, 4, 128)]
+
+
+def _scores64(Q, K, B, T, Hq, Hkv, hd):
+    """causal scores S * scale * log2(e) in float64, [B, Hq, T, T] (-inf above the diagonal)"""
+    q = f32(Q).reshape(B, T, Hq, hd).astype(np.float64).transpose(0, 2, 1, 3)
+    k = f32(K).reshape(B, T, Hkv, hd).astype(np.float64).transpose(0, 2, 3, 1)
+    k = np.repeat(k, Hq // Hkv, axis=1)
+    s = (q @ k) * (1.0 / np.sqrt(hd)) * np.log2(np.e)
+    s[:, :, np.triu(np.ones((T, T), bool), 1)] = -np.inf
+    return s
+
+
+@pytest.mark.parametrize("B,T,Hq,Hkv,hd", ROWSTAT_SHAPES)
+def test_attn_rowstats_fwd_bwd(B, T, Hq, Hkv, hd):
+    """The step engine's attention (probabilities recomputed from each row's
+    (max, 1/sum), never stored) against the oracle's sdpa_fwd/bwd
+    (ops.cu:578-870): O as ta_sdpa_fwd's bar, O32 within 1e-4 relative L2
+    of the float64 P.V, the row maximum (base-2 units) within 1e-5 of the
+    float64 one and 1/sum within 1e-5 relative, dQ/dK/dV within the 1e-2
+    gradient bar.  Shapes: the headline layer (T=1024, 12/2 heads of 128),
+    ragged T (100, 200), head_dim 64 and the 7B-shaped T=2048, 28/4."""
+    print(f"case: attn rowstats B={B} T={T} Hq={Hq} Hkv={Hkv} hd={hd}", flush=True)
+    Q, K, V = rbf(B * T, Hq * hd), rbf(B * T, Hkv * hd), rbf(B * T, Hkv * hd)
+    dO = rbf(B * T, Hq * hd)
+    tQ, tK, tV = dev(Q), dev(K), dev(V)
+    out = empty_bf16(B * T, Hq * hd)
+    o32 = torch.empty(B * T * Hq * hd, dtype=torch.float32, device=DEV)
+    st = torch.empty(B * Hq * T * 2, dtype=torch.float32, device=DEV)
+    call("ta_attn_fwd_rowstats", P(tQ), P(tK), P(tV), P(out), P(o32), P(st), B, T, Hq, Hkv, hd,
+         S())
+    rO, rP = O.sdpa_fwd(Q, K, V, B, T, Hq, Hkv, hd)
+    assert_bf16_close(host(out), rO, max_ulp=2, frac_exact=0.5, rl2=1e-2, floor=2.0 ** -7,
+                      what="attn O")
+    s64 = _scores64(Q, K, B, T, Hq, Hkv, hd)
+    m64 = s64.max(axis=-1)
+    inv64 = 1.0 / np.exp2(s64 - m64[..., None]).sum(axis=-1)
+    gst = host(st).reshape(B, Hq, T, 2)
+    assert np.all(np.abs(gst[..., 0] - m64) <= 1e-5 * np.abs(m64) + 1e-5)
+    np.testing.assert_allclose(gst[..., 1], inv64, rtol=1e-5)
+    p64 = np.exp2(s64 - m64[..., None]) * inv64[..., None]
+    v = f32(V).reshape(B, T, Hkv, hd).astype(np.float64).transpose(0, 2, 1, 3)
+    o64 = (p64 @ np.repeat(v, Hq // Hkv, axis=1)).transpose(0, 2, 1, 3).reshape(B * T, Hq * hd)
+    assert rel_l2(host(o32).reshape(B * T, Hq * hd), o64) < 1e-4
+    dQ, dK, dV = empty_bf16(B * T, Hq * hd), empty_bf16(B * T, Hkv * hd), empty_bf16(B * T, Hkv * hd)
+    call("ta_attn_bwd_rowstats", P(dev(dO)), P(tQ), P(tK), P(tV), P(st), P(o32), P(dQ), P(dK),
+         P(dV), B, T, Hq, Hkv, hd, S())
+    rdQ, rdK, rdV = O.sdpa_bwd(dO, Q, K, V, rP, B, T, Hq, Hkv, hd)
+    for got, want, name in ((dQ, rdQ, "dQ"), (dK, rdK, "dK"), (dV, rdV, "dV")):
+        r = rel_l2(f32(host(got)), f32(want))
+        assert r < 1e-2, f"{name}: rel-L2 {r:.3e}"
 
 
 @pytest.mark.parametrize("B,T,Hq,Hkv,hd", ATTN_SHAPES)
