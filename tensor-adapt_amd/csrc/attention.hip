@@ -666,6 +666,180 @@ __global__ __launch_bounds__(256) void k_attn_fwd_t(const bf16* __restrict__ Q,
         }
 }
 
+// ── backward dQ, transposed scores (the engine's form: P recomputed) ─────
+// Per block: 128 queries of one (b, hq), 4 waves of 32; key tiles of 64 in
+// three LDS buffer pairs, as in k_attn_fwd_t.  Per tile each wave forms
+// S^T = K Q^T exactly as the forward did (same operands, same MFMA order,
+// so the same bits) and dP^T = V dO^T, both with lane l holding query l%32;
+// P = exp2(S scale log2(e) - max) (1/sum) from the forward's row statistics
+// and dS = P (dP - D) (ops.cu:405-435) stay in registers and enter
+// dQ^T += K^T dS^T as its B operand (BF16 hi/lo), K^T coming from the K tile
+// through transposing reads in the scores' key order.  The row dots
+// D = dO . O are formed at the start from the dO fragments and the forward's
+// F32 output, and also stored for the dK/dV pass.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_bwd_dq_t(const bf16* __restrict__ dO,
+                                                       const bf16* __restrict__ Q,
+                                                       const bf16* __restrict__ K,
+                                                       const bf16* __restrict__ V,
+                                                       const float2* __restrict__ stats,
+                                                       float* __restrict__ Dq,
+                                                       const float* __restrict__ O32,
+                                                       bf16* __restrict__ dQ, int T, int Hq,
+                                                       int Hkv, float scale) {
+    constexpr int NST = HD / 16, NDB = HD / 32;
+    constexpr int TB = TK * HD * 2, LPT = 2 * (TB / 1024) / 4;  // DMA per wave per tile
+    __shared__ __attribute__((aligned(1024))) char sK0[TB], sK1[TB], sK2[TB];
+    __shared__ __attribute__((aligned(1024))) char sV0[TB], sV1[TB], sV2[TB];
+    const int nqt = (T + TQ2 - 1) / TQ2;
+    const int nbh = gridDim.x / nqt;
+    const int qt = nqt - 1 - (int)(blockIdx.x / nbh);  // longest rows launch first
+    const int bh = (int)(blockIdx.x % nbh);
+    const int b = bh / Hq, hq = bh % Hq, hkv = hq / (Hq / Hkv);
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int64_t qs = (int64_t)Hq * HD, ks_ = (int64_t)Hkv * HD;
+    const bf16* Qh = Q + (int64_t)b * T * qs + hq * HD;
+    const bf16* dOh = dO + (int64_t)b * T * qs + hq * HD;
+    const bf16* Kh = K + (int64_t)b * T * ks_ + hkv * HD;
+    const bf16* Vh = V + (int64_t)b * T * ks_ + hkv * HD;
+    const int q0 = qt * TQ2, qw0 = q0 + 32 * w;
+    const int qrow = qw0 + (lane & 31);
+    bf16x8_t qf[NST], of[NST];
+#pragma unroll
+    for (int st = 0; st < NST; st++) {
+        qf[st] = ld_head8(Qh, qs, qrow, T, 16 * st + 8 * (lane >> 5));
+        of[st] = ld_head8(dOh, qs, qrow, T, 16 * st + 8 * (lane >> 5));
+    }
+    // row dot D = dO . O (F32 O of the forward) over this lane's half of the
+    // head dims, then the other half from lane l ^ 32; row statistics
+    float D = 0.f, sm = 0.f, si = 0.f;
+    if (qrow < T) {
+        const float* orow = O32 + ((int64_t)b * T + qrow) * qs + hq * HD;
+#pragma unroll
+        for (int st = 0; st < NST; st++) {
+            const float4 o0 = *(const float4*)(orow + 16 * st + 8 * (lane >> 5));
+            const float4 o1 = *(const float4*)(orow + 16 * st + 8 * (lane >> 5) + 4);
+            const float ov[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) D += (float)of[st][e] * ov[e];
+        }
+        const float2 st = stats[(int64_t)bh * T + qrow];
+        sm = st.x;
+        si = st.y;
+    }
+    D += __shfl_xor(D, 32, 64);
+    if (lane < 32 && qrow < T) Dq[(int64_t)bh * T + qrow] = D;
+    int koff[NST], voff[NDB][2];
+#pragma unroll
+    for (int st = 0; st < NST; st++) koff[st] = tr_off<NST>(lane & 31, 16 * st + 8 * (lane >> 5));
+    {
+        const int g = lane >> 4, j = lane & 15;
+        const int r = 4 * (g >> 1) + (j >> 2), c = 16 * (g & 1) + 4 * (j & 3);
+#pragma unroll
+        for (int db = 0; db < NDB; db++) {
+            voff[db][0] = tr_off<NST>(r, 32 * db + c);
+            voff[db][1] = tr_off<NST>(r + 8, 32 * db + c);
+        }
+    }
+    const float sl2 = scale * kLog2e;
+    floatx16 acc[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; db++) acc[db] = zero16();
+    const int nkt = min((T + TK - 1) / TK, (min(q0 + TQ2, T) - 1) / TK + 1);
+    AttnDma<HD> dma;
+    dma.init(ks_, w, lane);
+    const i32x4_t rK = rows_rsrc(Kh, T, ks_), rV = rows_rsrc(Vh, T, ks_);
+    auto issue = [&](int kt, char* dK, char* dV) {
+        const int kq = min(kt, nkt - 1);
+        dma.issue(rK, ks_, kq * TK, dK, w);
+        dma.issue(rV, ks_, kq * TK, dV, w);
+    };
+    auto tile = [&](const char* __restrict__ sK, const char* __restrict__ sV, int kt) {
+        const int k0 = kt * TK;
+        if (k0 > qw0 + 31 || qw0 >= T) return;  // every key follows every query of this wave
+        floatx16 sT[2], dp[2];
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            sT[h] = zero16();
+            dp[h] = zero16();
+#pragma unroll
+            for (int st = 0; st < NST; st++)
+                sT[h] = mfma32(*(const bf16x8_t*)(sK + h * 32 * 32 * NST + koff[st]), qf[st], sT[h]);
+#pragma unroll
+            for (int st = 0; st < NST; st++)
+                dp[h] = mfma32(*(const bf16x8_t*)(sV + h * 32 * 32 * NST + koff[st]), of[st], dp[h]);
+        }
+        // P exactly as the forward's statistics define it; dS = P (dP - D)
+        const bool diag = k0 + TK - 1 > qw0;
+        const int kl = k0 + 4 * (lane >> 5);
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                float p = exp2_fast(sT[h][r] * sl2 - sm) * si;
+                if (diag) {
+                    const int key = kl + 32 * h + 8 * (r >> 2) + (r & 3);
+                    p = ((key <= qrow) & (key < T)) ? p : 0.f;
+                }
+                dp[h][r] = p * (dp[h][r] - D);
+            }
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int hf = 0; hf < 2; hf++) {
+                bf16x8_t dh, dl;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float d = dp[h][8 * hf + e];
+                    const bf16 hb = f2bf(d);
+                    dh[e] = __builtin_bit_cast(__bf16, hb);
+                    dl[e] = __builtin_bit_cast(__bf16, f2bf(d - bf2f(hb)));
+                }
+                const char* kt_ = sK + (32 * h + 16 * hf) * 32 * NST;
+#pragma unroll
+                for (int db = 0; db < NDB; db++) {
+                    i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_i16x4_p)(kt_ + voff[db][0]));
+                    i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (lds_i16x4_p)(kt_ + voff[db][1]));
+                    const bf16x8_t ka = __builtin_bit_cast(
+                        bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                    acc[db] = mfma32(ka, dl, acc[db]);
+                    acc[db] = mfma32(ka, dh, acc[db]);
+                }
+            }
+    };
+    TA_WAIT_VMCNT(0);  // Q, dO, O and the statistics are in; only tile loads are counted below
+    issue(0, sK0, sV0);
+    issue(1, sK1, sV1);
+#define ATT_STEP(KT, SK, SV, RK, RV)          \
+    if ((KT) < nkt) {                         \
+        TA_WAIT_VMCNT(LPT);                   \
+        __builtin_amdgcn_s_barrier();         \
+        issue((KT) + 2, RK, RV);              \
+        tile(SK, SV, (KT));                   \
+    }
+    for (int kt = 0; kt < nkt; kt += 3) {
+        ATT_STEP(kt, sK0, sV0, sK2, sV2);
+        ATT_STEP(kt + 1, sK1, sV1, sK0, sV0);
+        ATT_STEP(kt + 2, sK2, sV2, sK1, sV1);
+    }
+#undef ATT_STEP
+    TA_WAIT_VMCNT(0);  // the surplus loads have landed before the block ends
+    if (qrow >= T) return;
+    bf16* drow = dQ + ((int64_t)b * T + qrow) * qs + hq * HD;
+#pragma unroll
+    for (int db = 0; db < NDB; db++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int d = 32 * db + 8 * j + 4 * (lane >> 5);
+            uint2 pk;
+            pk.x = pack2(scale * acc[db][4 * j + 0], scale * acc[db][4 * j + 1]);
+            pk.y = pack2(scale * acc[db][4 * j + 2], scale * acc[db][4 * j + 3]);
+            *(uint2*)(drow + d) = pk;
+        }
+}
+
 // ── backward: the row dots D = sum_k P * dP ──────────────────────────────
 // From the forward's F32 output: D[bh, t] = dO[t, h, :] . O[t, h, :], since
 // sum_k P dP = sum_k P (dO V_k) = dO (sum_k P V_k).  HD/8 lanes per row.
@@ -1270,20 +1444,26 @@ int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const 
     // causal element) and reads the row statistics instead of P
     const double pb = rc ? 8.0 * B * Hq * (double)T : 4.0 * tri, rf = rc ? 2.0 * hd * tri : 0.0;
     bool timed = kprof_begin(KP_ATTN_BWD_DQ, s);
-#define DQ(H, R)                                                                          \
-    k_attn_bwd_dq<H, R><<<(int)b1, 256, 0, s>>>(dO, Q, K, V, P, st, Dbuf, rc ? O32 : nullptr, dQ, \
-                                                T, Hq, Hkv, scale)
+    // stored P: the reference's form (64-query tiles); recompute: the
+    // transposed-score kernel (128-query blocks)
+#define DQ(H)                                                                             \
+    k_attn_bwd_dq<H, false><<<(int)b1, 256, 0, s>>>(dO, Q, K, V, P, st, Dbuf, nullptr, dQ, T, \
+                                                    Hq, Hkv, scale)
+#define DQT(H)                                                                            \
+    k_attn_bwd_dq_t<H><<<(int)((int64_t)B * Hq * ((T + TQ2 - 1) / TQ2)), 256, 0, s>>>(        \
+        dO, Q, K, V, st, Dbuf, O32, dQ, T, Hq, Hkv, scale)
     if (hd == 64) {
-        if (rc) DQ(64, true); else DQ(64, false);
+        if (rc) DQT(64); else DQ(64);
     } else {
-        if (rc) DQ(128, true); else DQ(128, false);
+        if (rc) DQT(128); else DQ(128);
     }
 #undef DQ
+#undef DQT
     if (timed)
         kprof_end(KP_ATTN_BWD_DQ, s, 4.0 * hd * tri + rf,
                   pb + 2.0 * bt * hd * (2.0 * Hq + 2.0 * Hkv) + 4.0 * bt * Hq,
-                  hd == 64 ? (rc ? "void ta::k_attn_bwd_dq<64, true>" : "void ta::k_attn_bwd_dq<64, false>")
-                           : (rc ? "void ta::k_attn_bwd_dq<128, true>" : "void ta::k_attn_bwd_dq<128, false>"));
+                  hd == 64 ? (rc ? "void ta::k_attn_bwd_dq_t<64>" : "void ta::k_attn_bwd_dq<64, false>")
+                           : (rc ? "void ta::k_attn_bwd_dq_t<128>" : "void ta::k_attn_bwd_dq<128, false>"));
     timed = kprof_begin(KP_ATTN_BWD_DKV, s);
 #define DKV(H, R) \
     k_attn_bwd_dkv<H, R><<<(int)b1, 256, 0, s>>>(dO, Q, K, V, P, st, Dbuf, part, T, Hq, Hkv, scale)
