@@ -17,6 +17,13 @@ Prints one JSON line.  Besides tokens/s it carries:
                  per launch / average launch time, against MI355X peak
                  (2.5 PFLOP/s dense BF16, 8 TB/s HBM); the bound is the
                  resource whose peak gives the longer time for that work.
+  bwd_gemm_mfma_util, hbm_gbs, classes
+               — the metric's other quantities: every kernel class of the
+                 step (ta_engine_profile categories) event-timed for one
+                 step each, with its algorithmic TFLOP/s and GB/s and their
+                 fractions of the peaks; bwd_gemm_mfma_util is the
+                 frozen-base input-gradient GEMMs' MFMA fraction, hbm_gbs
+                 the norm, attention-backward and AdamW bandwidths.
   cpu_baseline — the CPU restatement of the reference step (oracle/, a
                  port: the reference has no CPU path) on this host's cores,
                  on a bounded sample, extrapolated to the c3 model.
@@ -288,14 +295,24 @@ def main():
 
     for _ in range(args.warmup):
         eng.step_resident(*next(it))
-    if args.categories:
-        # one step per kernel class with that class timed (not timed region)
-        for c in range(len(CAT_NAMES)):
-            eng.profile(c)
-            eng.step_resident(*next(it))
-            v = eng.profile_read()
-            print(f"  {CAT_NAMES[c]:14s} {v['ms']:8.2f} ms  {v['launches']:5d} launches", file=sys.stderr)
-        eng.profile(-1)
+    # one step per kernel class with that class's launches event-timed (not
+    # part of the timed region): per-class time, algorithmic TFLOP/s and
+    # GB/s against the MI355X peaks
+    classes = {}
+    for c in range(len(CAT_NAMES)):
+        eng.profile(c)
+        eng.step_resident(*next(it))
+        v = eng.profile_read()
+        sec = max(v["ms"], 1e-9) * 1e-3
+        tf, gb = v["flops"] / sec / 1e12, v["bytes"] / sec / 1e9
+        classes[CAT_NAMES[c]] = {"ms": round(v["ms"], 3), "launches": v["launches"],
+                                 "tflops": round(tf, 1), "gbs": round(gb, 1),
+                                 "mfma_frac": round(tf / PEAK_BF16_TFLOPS, 4),
+                                 "hbm_frac": round(gb / PEAK_HBM_GBS, 4)}
+        if args.categories:
+            print(f"  {CAT_NAMES[c]:14s} {v['ms']:8.2f} ms  {v['launches']:5d} launches  "
+                  f"{tf:7.1f} TFLOP/s  {gb:7.1f} GB/s", file=sys.stderr)
+    eng.profile(-1)
     # survey: one step per instrumented kernel, to find the kernel with the
     # largest share of the step (not part of the timed region)
     split = {}
@@ -367,6 +384,16 @@ def main():
                    "global_batch": B, "seq_len": T, "layers": model["layers"],
                    "hidden": model["hidden"], "parallelism": "single GPU"},
         "roofline": roof,
+        # the metric's other two quantities, from the per-class timing:
+        # MFMA utilisation of the frozen-base input-gradient GEMMs (the
+        # backward GEMMs; the LM head's forward and backward GEMMs are their
+        # own class) and achieved HBM bandwidth of the norm, attention
+        # backward and AdamW kernels, each against the MI355X peak
+        "bwd_gemm_mfma_util": classes["gemm_dx"]["mfma_frac"],
+        "hbm_gbs": {k: {"gbs": classes[c]["gbs"], "frac": classes[c]["hbm_frac"]}
+                    for k, c in (("norm", "norm"), ("attention_bwd", "attn_bwd"),
+                                 ("adamw", "adamw_tail"))},
+        "classes": classes,
         "loss": round(last["loss"], 4),
     }
     del eng
