@@ -393,7 +393,7 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
 
 // ── forward, transposed scores (the engine's form: P not stored) ───────────
 // Per block: 128 queries of one (b, hq), 4 waves of 32; key tiles of 64,
-// staged in LDS in the transposing-read layout.  Each wave computes
+// staged in LDS in the xr_off layout.  Each wave computes
 // S^T = K Q^T with 32x32x16 MFMAs (K rows as the A operand, the wave's Q
 // rows as the B operand, held in registers): lane l then holds the scores
 // of query l%32 for keys 8(r/4) + 4(l/32) + r%4 (r < 16) of each 32-key
@@ -409,6 +409,10 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
 // MFMAs as a BF16 hi/lo pair; the rows' final (max, 1/sum) are kept, and
 // the backward recomputes P from them.
 constexpr int TQ2 = 128;  // queries per block (4 waves x 32)
+// per (b, hq) and 64-query tile, the backward's per-query values as one
+// 1 KB block: [0, 64) the row's log2 normaliser lse2 = max + log2(sum) (so
+// P = exp2(S scale log2(e) - lse2)), [64, 128) the row dot D
+constexpr int QST = 256;
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 __device__ __forceinline__ floatx16 mfma32(bf16x8_t a, bf16x8_t b, floatx16 c) {
@@ -423,16 +427,48 @@ __device__ __forceinline__ floatx16 zero16() {
 
 typedef __attribute__((address_space(3))) void* lds_vptr_t;
 
+// 8 F32 values as the BF16 pair hi = bf16(v), lo = bf16(v - hi) (round to
+// nearest even), as MFMA operands; values converted two at a time (one
+// v_cvt_pk_bf16_f32 per pair for hi and one for lo)
+__device__ __forceinline__ void split8(const float* v, bf16x8_t& hi, bf16x8_t& lo) {
+    u32x4 h, l;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        h[i] = pack2(v[2 * i], v[2 * i + 1]);
+        l[i] = pack2(v[2 * i] - lo2f(h[i]), v[2 * i + 1] - hi2f(h[i]));
+    }
+    hi = __builtin_bit_cast(bf16x8_t, h);
+    lo = __builtin_bit_cast(bf16x8_t, l);
+}
+
 // Loads of one 64-row x HD tile (rows row0.., row stride rs) from global
-// memory straight into LDS in the tr_off<HD/16> layout, as buffer loads:
-// each buffer_load_dwordx4 ... lds fills 1 KB of the tile (lane i writes
-// bytes 16i..16i+15, so lane i fetches the 16-byte chunk that tr_off places
-// there); wave w issues instructions w, w + 4, ...  Rows at or past T read
+// memory straight into LDS in the xr_off (or tr_off) layout, as buffer
+// loads: each buffer_load_dwordx4 ... lds fills 1 KB of the tile (lane i
+// writes bytes 16i..16i+15, so lane i fetches the 16-byte chunk that the
+// layout places there); wave w issues instructions w, w + 4, ...  Rows at or past T read
 // as zeros through the buffer's bounds (the resource covers rows 0..T-1);
 // the lane offsets are fixed for the kernel and a tile's row offset is one
 // scalar.
 typedef int i32x4_t __attribute__((ext_vector_type(4)));
-template <int HD>
+
+// A second tile layout, [row][HD] BF16 with the 16-byte chunks of row r
+// XOR-permuted by xr_g(r): over any 16 consecutive rows (HD 128; any 8 of
+// one parity for HD 64) the permutation is a bijection, so 16 lanes reading
+// the same chunk of 16 rows (the MFMA A/B operand of rows) hit 16 distinct
+// bank groups; and any 4 consecutive rows x 4 aligned chunks land on
+// distinct banks, which keeps the transposing reads of 4 rows x 32 columns
+// per half-wave conflict free as well.
+template <int NCH>  // 16-byte chunks per row (HD / 8)
+__device__ __forceinline__ int xr_g(int r) {
+    if constexpr (NCH == 16) return 4 * (r & 3) + ((r >> 2) & 3);
+    else return 4 * ((r >> 1) & 1) + ((r >> 2) & 3);
+}
+template <int NCH>
+__device__ __forceinline__ int xr_off(int r, int c) {
+    return r * NCH * 16 + (((c >> 3) ^ xr_g<NCH>(r)) << 4) + (c & 7) * 2;
+}
+
+template <int HD, bool XR = false>  // XR: the xr_off layout (else tr_off)
 struct AttnDma {
     static constexpr int RB = HD * 2, RPI = 1024 / RB, NI = 64 / RPI, PER = NI / 4;
     int voff[PER];
@@ -440,7 +476,8 @@ struct AttnDma {
 #pragma unroll
         for (int h = 0; h < PER; h++) {
             const int r = (w + 4 * h) * RPI + (lane * 16) / RB, ib = (lane * 16) % RB;
-            const int col = 16 * ((ib >> 5) ^ tr_x<HD / 16>(r)) + 8 * ((ib >> 4) & 1);
+            const int col = XR ? 8 * ((ib >> 4) ^ xr_g<HD / 8>(r))
+                               : 16 * ((ib >> 5) ^ tr_x<HD / 16>(r)) + 8 * ((ib >> 4) & 1);
             voff[h] = (int)((r * rs + col) * 2);
         }
     }
@@ -500,7 +537,8 @@ __global__ __launch_bounds__(256) void k_attn_fwd_t(const bf16* __restrict__ Q,
     const int qt = nqt - 1 - (int)(blockIdx.x / nbh);  // longest rows launch first
     const int bh = (int)(blockIdx.x % nbh);
     const int b = bh / Hq, hq = bh % Hq, hkv = hq / (Hq / Hkv);
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    // the wave index as a scalar: conditions on it are uniform branches
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t qs = (int64_t)Hq * HD, ks_ = (int64_t)Hkv * HD;
     const bf16* Qh = Q + (int64_t)b * T * qs + hq * HD;
     const bf16* Kh = K + (int64_t)b * T * ks_ + hkv * HD;
@@ -511,18 +549,18 @@ __global__ __launch_bounds__(256) void k_attn_fwd_t(const bf16* __restrict__ Q,
 #pragma unroll
     for (int st = 0; st < NST; st++) qf[st] = ld_head8(Qh, qs, qrow, T, 16 * st + 8 * (lane >> 5));
     // per-lane LDS offsets within a tile (the tile-, half- and step-dependent
-    // parts are multiples of 16 rows, which the row XOR of tr_off ignores):
+    // parts are multiples of 16 rows, which the row XOR of xr_off ignores):
     // K rows for S^T, and the two transposing reads of each 32-wide V^T block
     int koff[NST], voff[NDB][2];
 #pragma unroll
-    for (int st = 0; st < NST; st++) koff[st] = tr_off<NST>(lane & 31, 16 * st + 8 * (lane >> 5));
+    for (int st = 0; st < NST; st++) koff[st] = xr_off<HD / 8>(lane & 31, 16 * st + 8 * (lane >> 5));
     {
         const int g = lane >> 4, j = lane & 15;
         const int r = 4 * (g >> 1) + (j >> 2), c = 16 * (g & 1) + 4 * (j & 3);
 #pragma unroll
         for (int db = 0; db < NDB; db++) {
-            voff[db][0] = tr_off<NST>(r, 32 * db + c);
-            voff[db][1] = tr_off<NST>(r + 8, 32 * db + c);
+            voff[db][0] = xr_off<HD / 8>(r, 32 * db + c);
+            voff[db][1] = xr_off<HD / 8>(r + 8, 32 * db + c);
         }
     }
     const float sl2 = scale * kLog2e;
@@ -534,7 +572,7 @@ __global__ __launch_bounds__(256) void k_attn_fwd_t(const bf16* __restrict__ Q,
     const int nkt = min((T + TK - 1) / TK, (min(q0 + TQ2, T) - 1) / TK + 1);
     // tiles past the last one reload it into a buffer that is never read,
     // so every wave issues the same number of loads per step
-    AttnDma<HD> dma;
+    AttnDma<HD, true> dma;
     dma.init(ks_, w, lane);
     const i32x4_t rK = rows_rsrc(Kh, T, ks_), rV = rows_rsrc(Vh, T, ks_);
     auto issue = [&](int kt, char* dK, char* dV) {
@@ -554,28 +592,28 @@ __global__ __launch_bounds__(256) void k_attn_fwd_t(const bf16* __restrict__ Q,
                 s[h] = mfma32(*(const bf16x8_t*)(sK + h * 32 * 32 * NST + koff[st]), qf[st], s[h]);
         }
         // scores in base-2 units; on a tile reaching past this wave's first
-        // query (or past T), keys after the query are masked
+        // query, keys after the query are masked (which covers keys past T
+        // for every row below T; rows past T are never stored).  The mask
+        // is a real branch: the empty asm keeps its compares from being
+        // speculated into every tile.
         float mx = -INFINITY;
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) s[h][r] *= sl2;
         if (k0 + TK - 1 > qw0) {
-            const int kl = k0 + 4 * (lane >> 5);
+            int kq = qrow - k0 - 4 * (lane >> 5);  // query - key of register 0
+            asm volatile("" : "+v"(kq));
 #pragma unroll
             for (int h = 0; h < 2; h++)
 #pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int key = kl + 32 * h + 8 * (r >> 2) + (r & 3);
-                    const bool ok = (key <= qrow) & (key < T);
-                    s[h][r] = ok ? s[h][r] * sl2 : -INFINITY;
-                    mx = fmaxf(mx, s[h][r]);
-                }
-        } else {
-#pragma unroll
-            for (int h = 0; h < 2; h++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    s[h][r] *= sl2;
-                    mx = fmaxf(mx, s[h][r]);
-                }
+                for (int r = 0; r < 16; r++)
+                    s[h][r] = 32 * h + 8 * (r >> 2) + (r & 3) <= kq ? s[h][r] : -INFINITY;
         }
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[h][r]);
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
         const float mn = fmaxf(m, mx);
         const float al = m == -INFINITY ? 0.f : exp2_fast(m - mn);
@@ -601,12 +639,7 @@ __global__ __launch_bounds__(256) void k_attn_fwd_t(const bf16* __restrict__ Q,
                     add += p[e];
                 }
                 bf16x8_t ph, pl;
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const bf16 hb = f2bf(p[e]);
-                    ph[e] = __builtin_bit_cast(__bf16, hb);
-                    pl[e] = __builtin_bit_cast(__bf16, f2bf(p[e] - bf2f(hb)));
-                }
+                split8(p, ph, pl);
                 const char* vt = sV + (32 * h + 16 * hf) * 32 * NST;
 #pragma unroll
                 for (int db = 0; db < NDB; db++) {
@@ -671,19 +704,19 @@ __global__ __launch_bounds__(256) void k_attn_fwd_t(const bf16* __restrict__ Q,
 // three LDS buffer pairs, as in k_attn_fwd_t.  Per tile each wave forms
 // S^T = K Q^T exactly as the forward did (same operands, same MFMA order,
 // so the same bits) and dP^T = V dO^T, both with lane l holding query l%32;
-// P = exp2(S scale log2(e) - max) (1/sum) from the forward's row statistics
-// and dS = P (dP - D) (ops.cu:405-435) stay in registers and enter
+// P = exp2(S scale log2(e) - lse2), lse2 = max + log2(sum) from the forward's
+// row statistics, and dS = P (dP - D) (ops.cu:405-435) stay in registers and enter
 // dQ^T += K^T dS^T as its B operand (BF16 hi/lo), K^T coming from the K tile
 // through transposing reads in the scores' key order.  The row dots
 // D = dO . O are formed at the start from the dO fragments and the forward's
-// F32 output, and also stored for the dK/dV pass.
+// F32 output, and stored with the row statistics for the dK/dV pass.
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_bwd_dq_t(const bf16* __restrict__ dO,
                                                        const bf16* __restrict__ Q,
                                                        const bf16* __restrict__ K,
                                                        const bf16* __restrict__ V,
                                                        const float2* __restrict__ stats,
-                                                       float* __restrict__ Dq,
+                                                       float* __restrict__ qst,
                                                        const float* __restrict__ O32,
                                                        bf16* __restrict__ dQ, int T, int Hq,
                                                        int Hkv, float scale) {
@@ -696,7 +729,8 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq_t(const bf16* __restrict__ 
     const int qt = nqt - 1 - (int)(blockIdx.x / nbh);  // longest rows launch first
     const int bh = (int)(blockIdx.x % nbh);
     const int b = bh / Hq, hq = bh % Hq, hkv = hq / (Hq / Hkv);
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    // the wave index as a scalar: conditions on it are uniform branches
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t qs = (int64_t)Hq * HD, ks_ = (int64_t)Hkv * HD;
     const bf16* Qh = Q + (int64_t)b * T * qs + hq * HD;
     const bf16* dOh = dO + (int64_t)b * T * qs + hq * HD;
@@ -711,8 +745,9 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq_t(const bf16* __restrict__ 
         of[st] = ld_head8(dOh, qs, qrow, T, 16 * st + 8 * (lane >> 5));
     }
     // row dot D = dO . O (F32 O of the forward) over this lane's half of the
-    // head dims, then the other half from lane l ^ 32; row statistics
-    float D = 0.f, sm = 0.f, si = 0.f;
+    // head dims, then the other half from lane l ^ 32; the row's log2
+    // normaliser from its statistics (+inf past T: P = 0 there)
+    float D = 0.f, lse = INFINITY;
     if (qrow < T) {
         const float* orow = O32 + ((int64_t)b * T + qrow) * qs + hq * HD;
 #pragma unroll
@@ -724,21 +759,27 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq_t(const bf16* __restrict__ 
             for (int e = 0; e < 8; e++) D += (float)of[st][e] * ov[e];
         }
         const float2 st = stats[(int64_t)bh * T + qrow];
-        sm = st.x;
-        si = st.y;
+        lse = st.x - __builtin_amdgcn_logf(st.y);
     }
     D += __shfl_xor(D, 32, 64);
-    if (lane < 32 && qrow < T) Dq[(int64_t)bh * T + qrow] = D;
+    // the dK/dV pass reads (lse2, D) per 64-query tile; rows past T inside
+    // the last tile get (+inf, 0), which make their P and dS zero there
+    const int nq64 = (T + TQ - 1) / TQ;
+    if (lane < 32 && qrow < nq64 * TQ) {
+        float* t = qst + ((int64_t)bh * nq64 + (qrow >> 6)) * QST + (qrow & 63);
+        t[0] = lse;
+        t[64] = D;
+    }
     int koff[NST], voff[NDB][2];
 #pragma unroll
-    for (int st = 0; st < NST; st++) koff[st] = tr_off<NST>(lane & 31, 16 * st + 8 * (lane >> 5));
+    for (int st = 0; st < NST; st++) koff[st] = xr_off<HD / 8>(lane & 31, 16 * st + 8 * (lane >> 5));
     {
         const int g = lane >> 4, j = lane & 15;
         const int r = 4 * (g >> 1) + (j >> 2), c = 16 * (g & 1) + 4 * (j & 3);
 #pragma unroll
         for (int db = 0; db < NDB; db++) {
-            voff[db][0] = tr_off<NST>(r, 32 * db + c);
-            voff[db][1] = tr_off<NST>(r + 8, 32 * db + c);
+            voff[db][0] = xr_off<HD / 8>(r, 32 * db + c);
+            voff[db][1] = xr_off<HD / 8>(r + 8, 32 * db + c);
         }
     }
     const float sl2 = scale * kLog2e;
@@ -746,7 +787,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq_t(const bf16* __restrict__ 
 #pragma unroll
     for (int db = 0; db < NDB; db++) acc[db] = zero16();
     const int nkt = min((T + TK - 1) / TK, (min(q0 + TQ2, T) - 1) / TK + 1);
-    AttnDma<HD> dma;
+    AttnDma<HD, true> dma;
     dma.init(ks_, w, lane);
     const i32x4_t rK = rows_rsrc(Kh, T, ks_), rV = rows_rsrc(Vh, T, ks_);
     auto issue = [&](int kt, char* dK, char* dV) {
@@ -769,32 +810,36 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq_t(const bf16* __restrict__ 
             for (int st = 0; st < NST; st++)
                 dp[h] = mfma32(*(const bf16x8_t*)(sV + h * 32 * 32 * NST + koff[st]), of[st], dp[h]);
         }
-        // P exactly as the forward's statistics define it; dS = P (dP - D)
-        const bool diag = k0 + TK - 1 > qw0;
-        const int kl = k0 + 4 * (lane >> 5);
+        // P exactly as the forward's statistics define it (keys after the
+        // query masked on a tile reaching past the wave's first query, a
+        // real branch as in the forward); dS = P (dP - D)
+        float p[2][16];
 #pragma unroll
         for (int h = 0; h < 2; h++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                float p = exp2_fast(sT[h][r] * sl2 - sm) * si;
-                if (diag) {
-                    const int key = kl + 32 * h + 8 * (r >> 2) + (r & 3);
-                    p = ((key <= qrow) & (key < T)) ? p : 0.f;
-                }
-                dp[h][r] = p * (dp[h][r] - D);
-            }
+            for (int r = 0; r < 16; r++) p[h][r] = exp2_fast(sT[h][r] * sl2 - lse);
+        if (k0 + TK - 1 > qw0) {
+            int kq = qrow - k0 - 4 * (lane >> 5);  // query - key of register 0
+            asm volatile("" : "+v"(kq));
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int r = 0; r < 16; r++)
+                    p[h][r] = 32 * h + 8 * (r >> 2) + (r & 3) <= kq ? p[h][r] : 0.f;
+        }
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) dp[h][r] = p[h][r] * (dp[h][r] - D);
 #pragma unroll
         for (int h = 0; h < 2; h++)
 #pragma unroll
             for (int hf = 0; hf < 2; hf++) {
                 bf16x8_t dh, dl;
+                float d8[8];
 #pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const float d = dp[h][8 * hf + e];
-                    const bf16 hb = f2bf(d);
-                    dh[e] = __builtin_bit_cast(__bf16, hb);
-                    dl[e] = __builtin_bit_cast(__bf16, f2bf(d - bf2f(hb)));
-                }
+                for (int e = 0; e < 8; e++) d8[e] = dp[h][8 * hf + e];
+                split8(d8, dh, dl);
                 const char* kt_ = sK + (32 * h + 16 * hf) * 32 * NST;
 #pragma unroll
                 for (int db = 0; db < NDB; db++) {
@@ -838,6 +883,340 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq_t(const bf16* __restrict__ 
             pk.y = pack2(scale * acc[db][4 * j + 2], scale * acc[db][4 * j + 3]);
             *(uint2*)(drow + d) = pk;
         }
+}
+
+// ── backward dK/dV, keys on the lanes (the engine's form: P recomputed) ───
+// Per block: 128 keys of one (b, kv head), 4 waves of 32, and a run of the
+// query heads of its GQA group [h0, h1).  The block walks (head, 64-query
+// tile) steps; each step's Q and dO tiles (xr_off layout) and the tile's
+// 1 KB of per-query values come straight into LDS by buffer-load DMA, three
+// buffer sets deep, as the K/V tiles of k_attn_fwd_t.  The wave's K and V
+// rows stay in accumulation registers as MFMA B operands: S = Q K^T and dP = dO V^T
+// (32 queries x 32 keys per MFMA tile, Q and dO rows read as A operands),
+// so lane l holds key l%32 and queries 8(r/4) + 4(l/32) + r%4 of each
+// 32-query half.  P = exp2(S scale log2(e) - lse2), exactly as the dQ pass
+// forms it, and dS = P (dP - D) (ops.cu:405-435) stay in registers
+// and, with the queries of a 16-wide k step taken in that order, are the B
+// operands (BF16 hi/lo) of dV^T += dO^T P and dK^T += Q^T dS, whose A
+// operands come from the same tiles through transposing reads.  The run's
+// heads accumulate in registers; a run covering the whole group writes dK
+// (times scale) and dV in BF16, otherwise each run writes F32 partials that
+// k_attn_dkv_sum adds in run order — the group sum of ops.cu:539-555 with
+// no atomics, so dK/dV are deterministic.
+template <int HD>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_attn_bwd_dkv_t(
+    const bf16* __restrict__ dO, const bf16* __restrict__ Q, const bf16* __restrict__ K,
+    const bf16* __restrict__ V, const float* __restrict__ qst, float* __restrict__ part,
+    bf16* __restrict__ dK, bf16* __restrict__ dV, int T, int Hq, int Hkv, int nsplit,
+    float scale) {
+    constexpr int NST = HD / 16, NDB = HD / 32;
+    constexpr int TB = TQ * HD * 2;
+    // DMA instructions per wave per step: Q and dO tiles, a quarter of the
+    // per-query block
+    constexpr int LPT = 2 * (TB / 1024) / 4 + 1;
+    __shared__ __attribute__((aligned(1024))) char sQ0[TB], sQ1[TB], sQ2[TB];
+    __shared__ __attribute__((aligned(1024))) char sO0[TB], sO1[TB], sO2[TB];
+    __shared__ __attribute__((aligned(1024))) float sS0[QST], sS1[QST], sS2[QST];
+    const int nkb = (T + 127) / 128, nqt = (T + TQ - 1) / TQ, grp = Hq / Hkv;
+    const int per = gridDim.x / nkb;               // B * Hkv * nsplit blocks per key block
+    const int kb = (int)(blockIdx.x / per);       // low kb = most query tiles: launch first
+    const int rem = (int)(blockIdx.x % per);
+    const int sp = rem % nsplit, bkv = rem / nsplit;
+    const int B = per / (Hkv * nsplit), b = bkv / Hkv, hkv = bkv % Hkv;
+    const int h0 = sp * grp / nsplit, h1 = (sp + 1) * grp / nsplit;
+    // the wave index as a scalar: conditions on it are uniform branches
+    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t qs = (int64_t)Hq * HD, ks_ = (int64_t)Hkv * HD;
+    const int kw0 = kb * 128 + 32 * w, key = kw0 + (lane & 31);
+    bf16x8_t kf[NST], vf[NST];
+    {
+        const bf16* Kh = K + (int64_t)b * T * ks_ + hkv * HD;
+        const bf16* Vh = V + (int64_t)b * T * ks_ + hkv * HD;
+#pragma unroll
+        for (int st = 0; st < NST; st++) {
+            kf[st] = ld_head8(Kh, ks_, key, T, 16 * st + 8 * (lane >> 5));
+            vf[st] = ld_head8(Vh, ks_, key, T, 16 * st + 8 * (lane >> 5));
+        }
+        // K and V stay in accumulation registers for the whole kernel (the
+        // MFMAs read them there), leaving the vector registers to the
+        // pipelined Q / dO fragments
+#pragma unroll
+        for (int st = 0; st < NST; st++) asm volatile("" : "+a"(kf[st]), "+a"(vf[st]));
+    }
+    // per-lane LDS offsets within a tile: Q / dO rows for S and dP, and the
+    // two transposing reads of each 32-wide block of dO^T / Q^T
+    int qoff[NST], toff[NDB][2];
+#pragma unroll
+    for (int st = 0; st < NST; st++) qoff[st] = xr_off<HD / 8>(lane & 31, 16 * st + 8 * (lane >> 5));
+    {
+        const int g = lane >> 4, j = lane & 15;
+        const int r = 4 * (g >> 1) + (j >> 2), c = 16 * (g & 1) + 4 * (j & 3);
+#pragma unroll
+        for (int db = 0; db < NDB; db++) {
+            toff[db][0] = xr_off<HD / 8>(r, 32 * db + c);
+            toff[db][1] = xr_off<HD / 8>(r + 8, 32 * db + c);
+        }
+    }
+    floatx16 aK[NDB], aV[NDB];
+#pragma unroll
+    for (int db = 0; db < NDB; db++) {
+        aK[db] = zero16();
+        aV[db] = zero16();
+    }
+    const int qt0 = (kb * 128) / TQ, nqh = nqt - qt0, nst = (h1 - h0) * nqh;
+    AttnDma<HD, true> dma;
+    dma.init(qs, w, lane);
+    const bf16* Qb = Q + (int64_t)b * T * qs;
+    const bf16* Ob = dO + (int64_t)b * T * qs;
+    const float* Sb = qst + (int64_t)b * Hq * nqt * QST;
+    const int soff = 4 * (64 * w + 4 * lane);  // bytes: lanes 0..15 of wave w fill floats 64w..
+    // the loads of step j (Q tile, dO tile, per-query block); past the last
+    // step the last is loaded again into a buffer that is never read, so
+    // every wave issues the same number of loads per step
+    auto step_head = [&](int j, int& qt) {
+        const int jj = min(j, nst - 1);
+        qt = qt0 + jj % nqh;
+        return hkv * grp + h0 + jj / nqh;
+    };
+    auto issue_q = [&](int j, char* tQ) {
+        int qt;
+        const int hq = step_head(j, qt);
+        dma.issue(rows_rsrc(Qb + hq * HD, T, qs), qs, qt * TQ, tQ, w);
+    };
+    auto issue_o = [&](int j, char* tO) {
+        int qt;
+        const int hq = step_head(j, qt);
+        dma.issue(rows_rsrc(Ob + hq * HD, T, qs), qs, qt * TQ, tO, w);
+    };
+    auto issue_s = [&](int j, float* tS) {
+        int qt;
+        const int hq = step_head(j, qt);
+        const uint64_t a = (uint64_t)(uintptr_t)(Sb + ((int64_t)hq * nqt + qt) * QST);
+        i32x4_t rs;
+        rs[0] = (int)(uint32_t)a;
+        rs[1] = (int)(uint32_t)(a >> 32);
+        rs[2] = QST * 4;
+        rs[3] = 0x00020000;
+        const uint32_t la = (uint32_t)(uintptr_t)(tS + 64 * w);
+        const int zero = 0;
+        if (lane < 16) {
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                         :
+                         : "s"(__builtin_amdgcn_readfirstlane(la)), "v"(soff), "s"(rs),
+                           "s"(zero)
+                         : "memory", "m0");
+#pragma clang diagnostic pop
+        }
+    };
+    auto issue = [&](int j, char* tQ, char* tO, float* tS) {
+        issue_q(j, tQ);
+        issue_o(j, tO);
+        issue_s(j, tS);
+    };
+    const float sl2 = scale * kLog2e;
+    // Q / dO rows of half h (queries 32h..32h+31 of the tile): the A operands
+    // of S and dP
+    auto frags = [&](const char* __restrict__ tQ, const char* __restrict__ tO, int h,
+                     bf16x8_t (&qa)[NST], bf16x8_t (&oa)[NST]) {
+#pragma unroll
+        for (int st = 0; st < NST; st++) {
+            qa[st] = *(const bf16x8_t*)(tQ + h * 32 * 32 * NST + qoff[st]);
+            oa[st] = *(const bf16x8_t*)(tO + h * 32 * 32 * NST + qoff[st]);
+        }
+    };
+    auto sdp = [&](const bf16x8_t (&qa)[NST], const bf16x8_t (&oa)[NST], floatx16& S,
+                   floatx16& dP) {
+        S = zero16();
+        dP = zero16();
+#pragma unroll
+        for (int st = 0; st < NST; st++) {
+            S = mfma32(qa[st], kf[st], S);
+            dP = mfma32(oa[st], vf[st], dP);
+        }
+    };
+    // P and dS of half h (query rows 32h + 8(r/4) + 4(lane/32) + r%4, from
+    // the tile's per-query block), as BF16 hi/lo B operands of the two k
+    // steps; on a diagonal tile keys after a query are masked
+    auto pds = [&](bool diag, const float* __restrict__ tS, int q0, int h, const floatx16& S,
+                   const floatx16& dP, bf16x8_t (&pb)[2][2], bf16x8_t (&eb)[2][2]) {
+        float p[16], d[16], dq[16];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int ql = 32 * h + 8 * c + 4 * (lane >> 5);
+            const float4 lx = *(const float4*)(tS + ql);
+            const float4 dd = *(const float4*)(tS + 64 + ql);
+            const float l4[4] = {lx.x, lx.y, lx.z, lx.w}, d4[4] = {dd.x, dd.y, dd.z, dd.w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                p[4 * c + e] = exp2_fast(S[4 * c + e] * sl2 - l4[e]);
+                dq[4 * c + e] = d4[e];
+            }
+        }
+        if (diag) {
+            // a real branch (the empty asm cannot be speculated): only the
+            // diagonal block pays for the mask
+            int kq = (lane & 31) - 4 * (lane >> 5);  // key - query offset of register 0
+            asm volatile("" : "+v"(kq));  // and the compares stay in the branch
+#pragma unroll
+            for (int r = 0; r < 16; r++) p[r] = kq <= 8 * (r >> 2) + (r & 3) ? p[r] : 0.f;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; r++) d[r] = p[r] * (dP[r] - dq[r]);
+#pragma unroll
+        for (int hf = 0; hf < 2; hf++) {
+            split8(p + 8 * hf, pb[hf][0], pb[hf][1]);
+            split8(d + 8 * hf, eb[hf][0], eb[hf][1]);
+        }
+    };
+    // dV^T += dO^T P and dK^T += Q^T dS over half h's two k steps (queries
+    // 32h + 16hf .. +15, registers 8hf .. 8hf + 7), the A operands read
+    // transposed from the tiles in that query order.  All 8 NDB transposing
+    // reads of the half are issued before its MFMAs (the scheduling barrier
+    // keeps the compiler from recycling one operand's registers, which would
+    // expose the LDS latency per 32-column block), and the MFMAs alternate
+    // between accumulators so that no two consecutive ones depend.
+    auto dkv = [&](const char* __restrict__ tQ, const char* __restrict__ tO, int h,
+                   const bf16x8_t (&pb)[2][2], const bf16x8_t (&eb)[2][2]) {
+        bf16x8_t oa[2][NDB], qa[2][NDB];
+#pragma unroll
+        for (int hf = 0; hf < 2; hf++) {
+            const char* ot = tO + (32 * h + 16 * hf) * 32 * NST;
+            const char* qt_ = tQ + (32 * h + 16 * hf) * 32 * NST;
+#pragma unroll
+            for (int db = 0; db < NDB; db++) {
+                i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_p)(ot + toff[db][0]));
+                i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_p)(ot + toff[db][1]));
+                oa[hf][db] = __builtin_bit_cast(
+                    bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+                lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_p)(qt_ + toff[db][0]));
+                hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_p)(qt_ + toff[db][1]));
+                qa[hf][db] = __builtin_bit_cast(
+                    bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int hf = 0; hf < 2; hf++) {
+#pragma unroll
+            for (int db = 0; db < NDB; db++) {
+                aV[db] = mfma32(oa[hf][db], pb[hf][1], aV[db]);
+                aK[db] = mfma32(qa[hf][db], eb[hf][1], aK[db]);
+            }
+#pragma unroll
+            for (int db = 0; db < NDB; db++) {
+                aV[db] = mfma32(oa[hf][db], pb[hf][0], aV[db]);
+                aK[db] = mfma32(qa[hf][db], eb[hf][0], aK[db]);
+            }
+        }
+    };
+    // One step: the tile half by half (the half's 2 NST fragment reads are
+    // issued together ahead of its MFMAs; the scheduling barriers keep the
+    // compiler from spreading them one per MFMA).
+    auto step = [&](const char* __restrict__ tQ, const char* __restrict__ tO,
+                    const float* __restrict__ tS, int j) {
+        const int q0 = (qt0 + j % nqh) * TQ;
+        if (kw0 > q0 + TQ - 1 || kw0 >= T) return;  // every key follows every query
+        // key and query offsets are multiples of 32: a half is wholly after
+        // the wave's keys (no mask), the diagonal block (keys after a query
+        // masked) or wholly before them (skipped)
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int qh0 = q0 + 32 * h;
+            if (kw0 > qh0) continue;
+            bf16x8_t qa[NST], oa[NST];
+            floatx16 S0, D0;
+            bf16x8_t p0[2][2], e0[2][2];
+            frags(tQ, tO, h, qa, oa);
+            __builtin_amdgcn_sched_barrier(0);
+            sdp(qa, oa, S0, D0);
+            pds(kw0 == qh0, tS, q0, h, S0, D0, p0, e0);
+            dkv(tQ, tO, h, p0, e0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    TA_WAIT_VMCNT(0);  // K and V are in; only tile loads are counted below
+    issue(0, sQ0, sO0, sS0);
+    issue(1, sQ1, sO1, sS1);
+#define ATT_STEP(J, TQ_, TO_, TS_, RQ, RO, RS) \
+    if ((J) < nst) {                           \
+        TA_WAIT_VMCNT(LPT);                    \
+        __builtin_amdgcn_s_barrier();          \
+        issue((J) + 2, RQ, RO, RS);            \
+        step(TQ_, TO_, TS_, (J));              \
+    }
+    for (int j = 0; j < nst; j += 3) {
+        ATT_STEP(j, sQ0, sO0, sS0, sQ2, sO2, sS2);
+        ATT_STEP(j + 1, sQ1, sO1, sS1, sQ0, sO0, sS0);
+        ATT_STEP(j + 2, sQ2, sO2, sS2, sQ1, sO1, sS1);
+    }
+#undef ATT_STEP
+    TA_WAIT_VMCNT(0);  // the surplus loads have landed before the block ends
+    if (key >= T) return;
+    // accumulator rows are head dims 32 db + 8 j + 4 (lane / 32) + 0..3
+    if (nsplit == 1) {
+        bf16* krow = dK + ((int64_t)b * T + key) * ks_ + hkv * HD;
+        bf16* vrow = dV + ((int64_t)b * T + key) * ks_ + hkv * HD;
+#pragma unroll
+        for (int db = 0; db < NDB; db++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int d = 32 * db + 8 * j + 4 * (lane >> 5);
+                uint2 pk;
+                pk.x = pack2(scale * aK[db][4 * j], scale * aK[db][4 * j + 1]);
+                pk.y = pack2(scale * aK[db][4 * j + 2], scale * aK[db][4 * j + 3]);
+                *(uint2*)(krow + d) = pk;
+                pk.x = pack2(aV[db][4 * j], aV[db][4 * j + 1]);
+                pk.y = pack2(aV[db][4 * j + 2], aV[db][4 * j + 3]);
+                *(uint2*)(vrow + d) = pk;
+            }
+    } else {
+        // partials [nsplit][2][B*T][Hkv*HD]: dK (unscaled) then dV of run sp
+        const int64_t n = (int64_t)B * T * ks_;
+        float* krow = part + 2 * sp * n + ((int64_t)b * T + key) * ks_ + hkv * HD;
+        float* vrow = krow + n;
+#pragma unroll
+        for (int db = 0; db < NDB; db++)
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int d = 32 * db + 8 * j + 4 * (lane >> 5);
+                *(float4*)(krow + d) = make_float4(aK[db][4 * j], aK[db][4 * j + 1],
+                                                   aK[db][4 * j + 2], aK[db][4 * j + 3]);
+                *(float4*)(vrow + d) = make_float4(aV[db][4 * j], aV[db][4 * j + 1],
+                                                   aV[db][4 * j + 2], aV[db][4 * j + 3]);
+            }
+    }
+}
+
+// dK = bf16(scale * sum_s partK[s]), dV = bf16(sum_s partV[s]), runs added
+// in order; n4 groups of 4 elements.
+__global__ __launch_bounds__(256) void k_attn_dkv_sum(const float4* __restrict__ part,
+                                                      uint2* __restrict__ dK,
+                                                      uint2* __restrict__ dV, int64_t n4,
+                                                      int nsplit, float scale) {
+    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n4;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        float4 k = part[i], v = part[n4 + i];
+        for (int sp = 1; sp < nsplit; sp++) {
+            const float4 a = part[2 * sp * n4 + i], c = part[(2 * sp + 1) * n4 + i];
+            k.x += a.x;
+            k.y += a.y;
+            k.z += a.z;
+            k.w += a.w;
+            v.x += c.x;
+            v.y += c.y;
+            v.z += c.z;
+            v.w += c.w;
+        }
+        uint2 pk;
+        pk.x = pack2(scale * k.x, scale * k.y);
+        pk.y = pack2(scale * k.z, scale * k.w);
+        dK[i] = pk;
+        pk.x = pack2(v.x, v.y);
+        pk.y = pack2(v.z, v.w);
+        dV[i] = pk;
+    }
 }
 
 // ── backward: the row dots D = sum_k P * dP ──────────────────────────────
@@ -1393,11 +1772,17 @@ int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* O32, f
     return check_launch("sdpa_fwd");
 }
 
-// Dbuf: [B*Hq*T] F32 row dots; part: [2*B*Hq*T*hd] F32 per-head dK/dV
-// contributions (both drawn from the scratch pool when NULL).  O32: the
-// forward's F32 output [B*T, Hq*hd] (NULL: the row dots are formed from P).
-// P NULL: the probabilities are recomputed from Q, K and the forward's row
-// statistics (stats, [B*Hq*T] (max, 1/sum) pairs), which needs O32.
+int64_t attn_bwd_rowbuf_floats(int B, int T, int Hq) {
+    return (int64_t)B * Hq * ((T + TQ - 1) / TQ) * QST;
+}
+
+// Dbuf: attn_bwd_rowbuf_floats(B, T, Hq) floats: the row dots [B*Hq*T], or
+// on the recompute path the per-tile (max, 1/sum, D) blocks; part: up to
+// [2*B*Hq*T*hd] F32 dK/dV partials (both drawn from the scratch pool when
+// NULL).  O32: the forward's F32 output [B*T, Hq*hd] (NULL: the row dots
+// are formed from P).  P NULL: the probabilities are recomputed from Q, K
+// and the forward's row statistics (stats, [B*Hq*T] (max, 1/sum) pairs),
+// which needs O32.
 int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const float* P,
              const float* stats, const float* O32, bf16* dQ, bf16* dK, bf16* dV, int B, int T,
              int Hq, int Hkv, int hd, float* Dbuf, float* part, hipStream_t s) {
@@ -1409,17 +1794,24 @@ int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const 
                "sdpa_bwd: tensors must be 16-byte aligned");
     TA_REQUIRE(!O32 || a16(O32), "sdpa_bwd: O32 must be 16-byte aligned");
     if (!Dbuf) {
-        Dbuf = (float*)scratch_get((size_t)B * Hq * T * sizeof(float), s);
+        Dbuf = (float*)scratch_get((size_t)attn_bwd_rowbuf_floats(B, T, Hq) * sizeof(float), s);
         TA_REQUIRE(Dbuf, "sdpa_bwd: scratch allocation failed");
-    }
-    if (!part) {
-        part = (float*)scratch_get((size_t)2 * B * Hq * T * hd * sizeof(float), s, 2);
-        TA_REQUIRE(part, "sdpa_bwd: scratch allocation failed");
     }
     int nqt = (T + TQ - 1) / TQ;
     float scale = 1.f / sqrtf((float)hd);
     int64_t b1 = (int64_t)B * Hq * nqt;
     const bool rc = P == nullptr;
+    const int grp = Hq / Hkv, nkb = (T + 127) / 128;
+    // recompute path: the query heads of a GQA group split into runs so that
+    // the grid holds about 384 blocks (1.5 per CU); one run per group writes
+    // dK/dV directly, several add their F32 partials afterwards
+    const int nsplit = rc ? std::max(1, std::min(grp, (int)((384 + (int64_t)B * Hkv * nkb - 1) /
+                                                           ((int64_t)B * Hkv * nkb))))
+                          : grp;
+    if (!part && (!rc || nsplit > 1)) {
+        part = (float*)scratch_get((size_t)2 * B * Hq * T * hd * sizeof(float), s, 2);
+        TA_REQUIRE(part, "sdpa_bwd: scratch allocation failed");
+    }
     // row dots D: formed inside the dQ pass on the recompute path; otherwise here
     if (rc) {
     } else if (O32) {
@@ -1437,7 +1829,8 @@ int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const 
     }
     // algorithmic work (causal half): dq pass dP = dO V^T, dQ = dS K; dkv
     // pass dP again, dV = P^T dO, dK = dS^T Q.  Bytes: BF16 operands, P and
-    // the row dots read once, outputs written once (dkv: F32 partials)
+    // the row dots read once, outputs written once (stored-P dkv: F32
+    // partials)
     const double tri = (double)B * Hq * T * (T + 1) / 2.0, bt = (double)B * T;
     const float2* st = (const float2*)stats;
     // with recomputation each pass also forms S = QK^T again (2 hd flops per
@@ -1465,22 +1858,37 @@ int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const 
                   hd == 64 ? (rc ? "void ta::k_attn_bwd_dq_t<64>" : "void ta::k_attn_bwd_dq<64, false>")
                            : (rc ? "void ta::k_attn_bwd_dq_t<128>" : "void ta::k_attn_bwd_dq<128, false>"));
     timed = kprof_begin(KP_ATTN_BWD_DKV, s);
-#define DKV(H, R) \
-    k_attn_bwd_dkv<H, R><<<(int)b1, 256, 0, s>>>(dO, Q, K, V, P, st, Dbuf, part, T, Hq, Hkv, scale)
-    if (hd == 64) {
-        if (rc) DKV(64, true); else DKV(64, false);
+    if (rc) {
+        const int blocks = nkb * B * Hkv * nsplit;
+        if (hd == 64)
+            k_attn_bwd_dkv_t<64><<<blocks, 256, 0, s>>>(dO, Q, K, V, Dbuf, part, dK, dV, T, Hq,
+                                                         Hkv, nsplit, scale);
+        else
+            k_attn_bwd_dkv_t<128><<<blocks, 256, 0, s>>>(dO, Q, K, V, Dbuf, part, dK, dV, T, Hq,
+                                                          Hkv, nsplit, scale);
+    } else if (hd == 64) {
+        k_attn_bwd_dkv<64, false><<<(int)b1, 256, 0, s>>>(dO, Q, K, V, P, st, Dbuf, part, T, Hq,
+                                                          Hkv, scale);
     } else {
-        if (rc) DKV(128, true); else DKV(128, false);
+        k_attn_bwd_dkv<128, false><<<(int)b1, 256, 0, s>>>(dO, Q, K, V, P, st, Dbuf, part, T, Hq,
+                                                           Hkv, scale);
     }
-#undef DKV
     if (timed)
         kprof_end(KP_ATTN_BWD_DKV, s, 6.0 * hd * tri + rf,
-                  pb + 2.0 * bt * hd * (2.0 * Hq + Hkv) + 4.0 * bt * Hq + 8.0 * bt * Hq * hd,
-                  hd == 64 ? (rc ? "void ta::k_attn_bwd_dkv<64, true>" : "void ta::k_attn_bwd_dkv<64, false>")
-                           : (rc ? "void ta::k_attn_bwd_dkv<128, true>" : "void ta::k_attn_bwd_dkv<128, false>"));
-    int64_t n = (int64_t)B * T * Hkv * hd;
-    int rb = (int)std::min<int64_t>((n + 255) / 256, 4096);
-    k_attn_dkv_reduce<<<rb, 256, 0, s>>>(part, dK, dV, B, T, Hq, Hkv, hd, scale);
+                  rc ? 12.0 * B * Hq * (double)T + 2.0 * bt * hd * (2.0 * Hq + 4.0 * Hkv)
+                     : pb + 2.0 * bt * hd * (2.0 * Hq + Hkv) + 4.0 * bt * Hq + 8.0 * bt * Hq * hd,
+                  hd == 64 ? (rc ? "void ta::k_attn_bwd_dkv_t<64>" : "void ta::k_attn_bwd_dkv<64, false>")
+                           : (rc ? "void ta::k_attn_bwd_dkv_t<128>" : "void ta::k_attn_bwd_dkv<128, false>"));
+    if (!rc) {
+        int64_t n = (int64_t)B * T * Hkv * hd;
+        int rb = (int)std::min<int64_t>((n + 255) / 256, 4096);
+        k_attn_dkv_reduce<<<rb, 256, 0, s>>>(part, dK, dV, B, T, Hq, Hkv, hd, scale);
+    } else if (nsplit > 1) {
+        const int64_t n4 = (int64_t)B * T * Hkv * hd / 4;
+        const int rb = (int)std::min<int64_t>((n4 + 255) / 256, 4096);
+        k_attn_dkv_sum<<<rb, 256, 0, s>>>((const float4*)part, (uint2*)dK, (uint2*)dV, n4,
+                                          nsplit, scale);
+    }
     return check_launch("sdpa_bwd");
 }
 

@@ -385,7 +385,7 @@ static int engine_alloc(Engine* e) {
     CK(alloc(e, &e->delta, (int64_t)BT * maxout, "delta", 0));
     CK(alloc(e, &e->dh, (int64_t)BT * r, "dh", 0));
     CK(alloc(e, &e->dh_cat, (int64_t)BT * r * 3, "dh_cat", 0));
-    CK(alloc(e, &e->Dbuf, (int64_t)e->B * c.n_q * e->T, "Dbuf", 1));
+    CK(alloc(e, &e->Dbuf, attn_bwd_rowbuf_floats(e->B, e->T, c.n_q), "Dbuf", 1));
     CK(alloc(e, &e->dkv_part, (int64_t)2 * e->B * c.n_q * e->T * c.head_dim, "dkv_part", 1));
     CK(alloc(e, &e->norm_dev, 64, "norm", 1));
     e->bad_dev = (int32_t*)(e->norm_dev + 1);

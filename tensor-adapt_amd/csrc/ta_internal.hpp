@@ -101,9 +101,13 @@ int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const Gem
 // backward recomputes P
 int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* O32, float* P,
              float* stats, int B, int T, int Hq, int Hkv, int hd, bool zero_fill, hipStream_t s);
+// Dbuf: attn_bwd_rowbuf_floats(B, T, Hq) floats of per-query values; part:
+// 2 B T Hq hd floats of dK/dV partials (each drawn from the scratch pool
+// when NULL)
 int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const float* P,
              const float* stats, const float* O32, bf16* dQ, bf16* dK, bf16* dV, int B, int T,
              int Hq, int Hkv, int hd, float* Dbuf, float* part, hipStream_t s);
+int64_t attn_bwd_rowbuf_floats(int B, int T, int Hq);
 int transpose_bf16(const bf16* in, bf16* out, int64_t rows, int64_t cols, hipStream_t s);
 int fill_normal_bf16(bf16* out, int64_t n, uint64_t seed, uint64_t sid, float std, hipStream_t s);
 int fill_bf16(bf16* out, int64_t n, float v, hipStream_t s);
