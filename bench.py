@@ -22,8 +22,9 @@ Prints one JSON line.  Besides tokens/s it carries:
                  step (ta_engine_profile categories) event-timed for one
                  step each, with its algorithmic TFLOP/s and GB/s and their
                  fractions of the peaks; bwd_gemm_mfma_util is the
-                 frozen-base input-gradient GEMMs' MFMA fraction, hbm_gbs
-                 the norm, attention-backward and AdamW bandwidths.
+                 backward GEMMs' MFMA fraction (frozen-base input gradients
+                 and the LM head's input gradient together), hbm_gbs the
+                 norm, attention-backward and AdamW bandwidths.
   cpu_baseline — the CPU restatement of the reference step (oracle/, a
                  port: the reference has no CPU path) on this host's cores,
                  on a bounded sample, extrapolated to the c3 model.
@@ -65,7 +66,7 @@ CONFIGS = {
 }
 
 CAT_NAMES = ["gemm_fwd", "gemm_dx", "lm_head", "lora", "attn_fwd", "attn_bwd", "norm",
-             "elementwise", "cross_entropy", "adamw_tail", "centroid"]
+             "elementwise", "cross_entropy", "adamw_tail", "centroid", "lm_head_bwd"]
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 
@@ -298,7 +299,7 @@ def main():
     # one step per kernel class with that class's launches event-timed (not
     # part of the timed region): per-class time, algorithmic TFLOP/s and
     # GB/s against the MI355X peaks
-    classes = {}
+    classes, raw = {}, {}
     for c in range(len(CAT_NAMES)):
         eng.profile(c)
         eng.step_resident(*next(it))
@@ -309,10 +310,14 @@ def main():
                                  "tflops": round(tf, 1), "gbs": round(gb, 1),
                                  "mfma_frac": round(tf / PEAK_BF16_TFLOPS, 4),
                                  "hbm_frac": round(gb / PEAK_HBM_GBS, 4)}
+        raw[CAT_NAMES[c]] = v
         if args.categories:
             print(f"  {CAT_NAMES[c]:14s} {v['ms']:8.2f} ms  {v['launches']:5d} launches  "
                   f"{tf:7.1f} TFLOP/s  {gb:7.1f} GB/s", file=sys.stderr)
     eng.profile(-1)
+    bwd = [raw["gemm_dx"], raw["lm_head_bwd"]]
+    bwd_util = round(sum(v["flops"] for v in bwd) / max(sum(v["ms"] for v in bwd), 1e-9) / 1e9
+                     / PEAK_BF16_TFLOPS, 4)
     # survey: one step per instrumented kernel, to find the kernel with the
     # largest share of the step (not part of the timed region)
     split = {}
@@ -385,11 +390,11 @@ def main():
                    "hidden": model["hidden"], "parallelism": "single GPU"},
         "roofline": roof,
         # the metric's other two quantities, from the per-class timing:
-        # MFMA utilisation of the frozen-base input-gradient GEMMs (the
-        # backward GEMMs; the LM head's forward and backward GEMMs are their
-        # own class) and achieved HBM bandwidth of the norm, attention
-        # backward and AdamW kernels, each against the MI355X peak
-        "bwd_gemm_mfma_util": classes["gemm_dx"]["mfma_frac"],
+        # MFMA utilisation of the backward GEMMs (the frozen-base input
+        # gradients and the LM head's input gradient, flops over time) and
+        # achieved HBM bandwidth of the norm, attention backward and AdamW
+        # kernels, each against the MI355X peak
+        "bwd_gemm_mfma_util": bwd_util,
         "hbm_gbs": {k: {"gbs": classes[c]["gbs"], "frac": classes[c]["hbm_frac"]}
                     for k, c in (("norm", "norm"), ("attention_bwd", "attn_bwd"),
                                  ("adamw", "adamw_tail"))},

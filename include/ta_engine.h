@@ -123,7 +123,7 @@ int ta_engine_step_resident(void* engine, const int32_t* d_inputs, const int32_t
 enum {
     TA_CAT_GEMM_FWD = 0, /* frozen-base projections, forward: x W^T        */
     TA_CAT_GEMM_DX = 1,  /* frozen-base input gradients: dY W              */
-    TA_CAT_LMHEAD = 2,   /* LM head forward + backward GEMMs              */
+    TA_CAT_LMHEAD = 2,   /* LM head forward GEMM (logits)                 */
     TA_CAT_LORA = 3,     /* every LoRA GEMM (fwd h, delta; bwd gB, dh, gA, dx) */
     TA_CAT_ATTN_FWD = 4,
     TA_CAT_ATTN_BWD = 5,
@@ -132,7 +132,8 @@ enum {
     TA_CAT_CE = 8,
     TA_CAT_TAIL = 9,     /* grad norm + clip + AdamW                      */
     TA_CAT_CENTROID = 10,
-    TA_NCAT = 11
+    TA_CAT_LMHEAD_BWD = 11, /* LM head input-gradient GEMM: dlogits W     */
+    TA_NCAT = 12
 };
 int ta_engine_profile(void* engine, int category);
 int ta_engine_profile_read(void* engine, double* total_ms, int64_t* launches, double* flops,

@@ -700,7 +700,7 @@ static int backward(Engine* e) {
     const double nrm_b = dBT * H * 6 + H * 2 + dBT * 4;
     e->wg_cursor = 0;
     // dres = dlogits * W_lm (qwen2.cu:205); grad = rms_norm_bwd(final)
-    TIMED(TA_CAT_LMHEAD, gflops(BT, H, e->V), gbytes(BT, H, e->V, 2, 2, false),
+    TIMED(TA_CAT_LMHEAD_BWD, gflops(BT, H, e->V), gbytes(BT, H, e->V, 2, 2, false),
           gemm_dispatch(true, true, BT, H, e->V, 1.f, e->logits, e->V, e->lmT, e->V, 0.f, e->dres,
                         H, nullptr, false, s, 0, nullptr));
     TIMED(TA_CAT_NORM, 0, nrm_b,
