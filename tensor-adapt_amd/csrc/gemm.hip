@@ -523,6 +523,40 @@ __device__ __forceinline__ void dma_stage(const bf16* __restrict__ P, int64_t ld
     }
 }
 
+// dma_stage split in two for operands whose base and row stride change
+// during the loop (the K segments of a chain): dma_offsets computes, once,
+// this lane's element offset (clamped row x ld + swizzled chunk) for each of
+// the wave's PER instructions; dma_stage_at issues them for one stage from a
+// base pointer and k0.  Same addresses as dma_stage.
+template <int ROWS, int NW>
+struct DmaOffs {
+    static constexpr int NI = ROWS / 16, PER = (NI + NW - 1) / NW;
+    int o[PER];
+};
+template <int ROWS, int NW>
+__device__ __forceinline__ void dma_offsets(DmaOffs<ROWS, NW>& d, int64_t ld, int row0, int rows,
+                                            int w, int lane) {
+#pragma unroll
+    for (int h = 0; h < DmaOffs<ROWS, NW>::PER; h++) {
+        int j = w + NW * h;
+        j = j < DmaOffs<ROWS, NW>::NI ? j : j - NW;
+        const int r = 16 * j + (lane >> 2);
+        const int c = (lane & 3) ^ dswz(r);
+        d.o[h] = (int)((int64_t)min(row0 + r, rows - 1) * ld) + 8 * c;
+    }
+}
+template <int ROWS, int NW>
+__device__ __forceinline__ void dma_stage_at(const bf16* __restrict__ P, const DmaOffs<ROWS, NW>& d,
+                                             int k0, bf16* stage, int w) {
+#pragma unroll
+    for (int h = 0; h < DmaOffs<ROWS, NW>::PER; h++) {
+        int j = w + NW * h;
+        j = j < DmaOffs<ROWS, NW>::NI ? j : j - NW;
+        __builtin_amdgcn_global_load_lds((const void*)(P + d.o[h] + k0),
+                                         (lds_ptr_t)(stage + 16 * j * DBK), 16, 0, 0);
+    }
+}
+
 // One 32-wide k slice of MFMAs for a wave from a swizzled stage.
 template <int TM, int TN, int WTM, int WTN>
 __device__ __attribute__((always_inline)) inline void dma_mma(floatx16 (&acc)[TM][TN],
@@ -1021,6 +1055,16 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
     // K segments: stage kt (global k) belongs to segment s; the accumulators
     // are rounded after the last stage of every segment but the last
     const int kb1 = CHAIN ? a.kseg[1] / DBK : -99, kb2 = CHAIN && a.nseg > 2 ? a.kseg[2] / DBK : -99;
+    DmaOffs<BM, NW> ox0, ox1, ox2;
+    DmaOffs<BN, NW> oy0, oy1, oy2;
+    if constexpr (CHAIN) {
+        dma_offsets<BM, NW>(ox0, a.sldx[0], m0, a.M, w, lane);
+        dma_offsets<BN, NW>(oy0, a.sldy[0], n0, a.N, w, lane);
+        dma_offsets<BM, NW>(ox1, a.sldx[1], m0, a.M, w, lane);
+        dma_offsets<BN, NW>(oy1, a.sldy[1], n0, a.N, w, lane);
+        dma_offsets<BM, NW>(ox2, a.nseg > 2 ? a.sldx[2] : 0, m0, a.M, w, lane);
+        dma_offsets<BN, NW>(oy2, a.nseg > 2 ? a.sldy[2] : 0, n0, a.N, w, lane);
+    }
 #define PIPE_ISSUE(SXB, SYB, KT)                                                           \
     do {                                                                                   \
         const int kq_ = (KT);                                                              \
@@ -1030,16 +1074,28 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
         const bf16* y_ = a.Y;                                                              \
         int64_t lx_ = a.ldx, ly_ = a.ldy;                                                  \
         if constexpr (CHAIN) {                                                             \
+            /* the segment's precomputed row offsets: no per-stage multiply */             \
             const int s_ = (a.nseg > 2 && k_ >= a.kseg[2]) ? 2 : k_ >= a.kseg[1] ? 1 : 0;  \
             x_ = s_ == 2 ? a.sX[2] : s_ == 1 ? a.sX[1] : a.sX[0];                          \
             y_ = s_ == 2 ? a.sY[2] : s_ == 1 ? a.sY[1] : a.sY[0];                          \
-            lx_ = s_ == 2 ? a.sldx[2] : s_ == 1 ? a.sldx[1] : a.sldx[0];                   \
-            ly_ = s_ == 2 ? a.sldy[2] : s_ == 1 ? a.sldy[1] : a.sldy[0];                   \
             k_ -= s_ == 2 ? a.kseg[2] : s_ == 1 ? a.kseg[1] : 0;                           \
+            if (z_) {                                                                      \
+                dma_stage<BM, NW>(g_dma_zero, 0, m0, a.M, 0, SXB, w, lane);                \
+                dma_stage<BN, NW>(g_dma_zero, 0, n0, a.N, 0, SYB, w, lane);                \
+            } else {                                                                       \
+                dma_stage_at<BM, NW>(x_, s_ == 2 ? ox2 : s_ == 1 ? ox1 : ox0, k_, SXB, w); \
+                dma_stage_at<BN, NW>(y_, s_ == 2 ? oy2 : s_ == 1 ? oy1 : oy0, k_, SYB, w); \
+            }                                                                              \
+        } else {                                                                           \
+            dma_stage<BM, NW>(z_ ? g_dma_zero : x_, z_ ? 0 : lx_, m0, a.M, k_, SXB, w,     \
+                              lane);                                                       \
+            dma_stage<BN, NW>(z_ ? g_dma_zero : y_, z_ ? 0 : ly_, n0, a.N, k_, SYB, w,     \
+                              lane);                                                       \
         }                                                                                  \
-        dma_stage<BM, NW>(z_ ? g_dma_zero : x_, z_ ? 0 : lx_, m0, a.M, k_, SXB, w, lane);  \
-        dma_stage<BN, NW>(z_ ? g_dma_zero : y_, z_ ? 0 : ly_, n0, a.N, k_, SYB, w, lane);  \
     } while (0)
+// (chains start every segment on a loop trip of NS stages, which the host
+// checks, so the rounding test sits between trips and the NS steps of a
+// trip stay one straight-line region)
 #define PIPE_ROUND(KT)                                                                     \
     do {                                                                                   \
         if constexpr (CHAIN)                                                               \
@@ -1070,11 +1126,8 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
     } while (0)
     for (int kt0 = -pad; kt0 < nk; kt0 += NS) {
         PIPE_STEP(0, sX0, sY0, sX1, sY1, sX3, sY3);
-        PIPE_ROUND(kt0 + 0);
         PIPE_STEP(1, sX1, sY1, sX2, sY2, sX0, sY0);
-        PIPE_ROUND(kt0 + 1);
         PIPE_STEP(2, sX2, sY2, sX3, sY3, sX1, sY1);
-        PIPE_ROUND(kt0 + 2);
         PIPE_STEP(3, sX3, sY3, sX0, sY0, sX2, sY2);
         PIPE_ROUND(kt0 + 3);
     }
@@ -1456,10 +1509,22 @@ int gemm_chain(int M, int N, const GemmSeg* sg, int ns, bf16* C, int64_t ldc, co
         Ktot += sg[q].K;
         ok &= sg[q].K % BK == 0 && al16(sg[q].X) && al16(sg[q].Y) && sg[q].ldx % 8 == 0 &&
               sg[q].ldy % 8 == 0;
+        // the kernel keeps each segment's row offsets as 32-bit element counts
+        ok &= (int64_t)M * sg[q].ldx < INT32_MAX && (int64_t)N * sg[q].ldy < INT32_MAX;
     }
     const int tiles = ((M + 255) / 256) * ((N + BNb - 1) / BNb);
     // (as gemm_dispatch: few tiles and a long K go to split-K instead)
     ok &= tiles >= 192 || Ktot / BK < 32;
+    // every segment must start on a loop trip of the kernel (4 stages of 32
+    // k after the leading zero stages), where the kernel rounds
+    {
+        const int nk = Ktot / 32, pad = (4 - nk % 4) % 4;
+        int kb = 0;
+        for (int q = 0; q + 1 < ns; q++) {
+            kb += sg[q].K;
+            ok &= (kb / 32 + pad) % 4 == 0;
+        }
+    }
     ok &= !lora || lora->n == 0 || lora->r <= 16;
     if (!ok) {
         for (int q = 0; q < ns; q++) {
