@@ -159,24 +159,6 @@ __device__ __forceinline__ void wave_qk(floatx4 (&S)[4], const bf16x8_t (&af)[HD
     }
 }
 
-// wave_qk with the B rows read from a tile in the tr_off<HD/16> layout (the
-// transposing-read layout, rows kept whole): the same values in the same
-// MFMA order, so the same S bit for bit.
-template <int HD>
-__device__ __forceinline__ void wave_qk_tr(floatx4 (&S)[4], const bf16x8_t (&af)[HD / 32],
-                                           const char* __restrict__ sB, int lane) {
-#pragma unroll
-    for (int t = 0; t < 4; t++) {
-        S[t] = zero4();
-        const int row = 16 * t + (lane & 15);
-#pragma unroll
-        for (int ks = 0; ks < HD / 32; ks++)
-            S[t] = mfma16(af[ks],
-                          *(const bf16x8_t*)(sB + tr_off<HD / 16>(row, 32 * ks + 8 * (lane >> 4))),
-                          S[t]);
-    }
-}
-
 // acc[16 x HD] += A[16 x 64] * B[64 x HD]; A (an F32 quantity: P or dS)
 // arrives as two BF16 tiles, hi = bf16(a) and lo = bf16(a - hi), in this
 // wave's LDS slots sA[0], sA[1] ([16][LDT], k contiguous), so the product
@@ -1330,15 +1312,12 @@ __device__ __forceinline__ void load_p_rows(float (&p)[4][4], const float* __res
 // K is staged once, in its natural layout, and read as the dS·K operand
 // through the transposing LDS read; dS (hi/lo) goes to a per-wave
 // [key][row] tile like P in the forward.
-template <int HD, bool RC>  // RC: recompute P from Q, K and the forward's row statistics
+template <int HD>
 __global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO,
-                                                     const bf16* __restrict__ Q,
                                                      const bf16* __restrict__ K,
                                                      const bf16* __restrict__ V,
                                                      const float* __restrict__ P,
-                                                     const float2* __restrict__ stats,
-                                                     float* __restrict__ Dq,
-                                                     const float* __restrict__ O32,
+                                                     const float* __restrict__ Dq,
                                                      bf16* __restrict__ dQ, int T, int Hq, int Hkv,
                                                      float scale) {
     constexpr int VST = HD / 16;
@@ -1355,7 +1334,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO
     const bf16* dOh = dO + (int64_t)b * T * qs + hq * HD;
     const bf16* Kh = K + (int64_t)b * T * ks_ + hkv * HD;
     const bf16* Vh = V + (int64_t)b * T * ks_ + hkv * HD;
-    const float* Ph = RC ? nullptr : P + (int64_t)bh * T * T;
+    const float* Ph = P + (int64_t)bh * T * T;
     int q0 = qt * TQ;
     int rowA = q0 + 16 * w + (lane & 15);
     bf16x8_t of[HD / 32];
@@ -1364,50 +1343,8 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO
         of[ks] = ld_head8(dOh, qs, rowA, T, 32 * ks + 8 * (lane >> 4));
     int rbase = q0 + 16 * w + 4 * (lane >> 4);
     float D[4];
-    if (O32) {
-        // row dots D = dO . O (the forward's F32 output) for this wave's 16
-        // rows from the dO fragments already in registers: lane (g, j) holds
-        // row j, columns 32 ks + 8 g .. + 7; the 4 g-lanes of a row combine,
-        // then each lane takes the rows of its C layout.  D also goes to Dq
-        // for the dK/dV pass.
-        const float* orow = O32 + ((int64_t)b * T + rowA) * qs + hq * HD;
-        float dsum = 0.f;
-        if (rowA < T) {
 #pragma unroll
-            for (int ks = 0; ks < HD / 32; ks++) {
-                const float4 o0 = *(const float4*)(orow + 32 * ks + 8 * (lane >> 4));
-                const float4 o1 = *(const float4*)(orow + 32 * ks + 8 * (lane >> 4) + 4);
-                const float ov[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
-#pragma unroll
-                for (int e = 0; e < 8; e++) dsum += (float)of[ks][e] * ov[e];
-            }
-        }
-        dsum += __shfl_xor(dsum, 16, 64);
-        dsum += __shfl_xor(dsum, 32, 64);
-        if ((lane >> 4) == 0 && rowA < T) Dq[(int64_t)bh * T + rowA] = dsum;
-#pragma unroll
-        for (int r = 0; r < 4; r++) D[r] = __shfl(dsum, 4 * (lane >> 4) + r, 64);
-    } else {
-#pragma unroll
-        for (int r = 0; r < 4; r++) D[r] = (rbase + r < T) ? Dq[(int64_t)bh * T + rbase + r] : 0.f;
-    }
-    // recompute: Q fragments and the rows' (max, 1/sum), as in the forward
-    // (rows past T: 1/sum = 0, so P = 0 there)
-    bf16x8_t qf[RC ? HD / 32 : 1];
-    float sm[4], si[4];
-    const float sl2 = scale * kLog2e;
-    if constexpr (RC) {
-        const bf16* Qh = Q + (int64_t)b * T * qs + hq * HD;
-#pragma unroll
-        for (int ks = 0; ks < HD / 32; ks++)
-            qf[ks] = ld_head8(Qh, qs, rowA, T, 32 * ks + 8 * (lane >> 4));
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const float2 st = (rbase + r < T) ? stats[(int64_t)bh * T + rbase + r] : make_float2(0.f, 0.f);
-            sm[r] = st.x;
-            si[r] = st.y;
-        }
-    }
+    for (int r = 0; r < 4; r++) D[r] = (rbase + r < T) ? Dq[(int64_t)bh * T + rbase + r] : 0.f;
 
     floatx4 acc[HD / 16];
 #pragma unroll
@@ -1416,7 +1353,7 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO
     float pn[4][4];
     lv.load(Vh, ks_, 0, T);
     lk.load(Kh, ks_, 0, T);
-    if constexpr (!RC) load_p_rows(pn, Ph, T, rbase, 0, lane);
+    load_p_rows(pn, Ph, T, rbase, 0, lane);
     char* sSh = sS[w][0];
     char* sSl = sS[w][1];
     for (int kt = 0; kt <= qt; kt++) {
@@ -1428,32 +1365,15 @@ __global__ __launch_bounds__(256) void k_attn_bwd_dq(const bf16* __restrict__ dO
             *(u32x4*)(sK + tr_off<VST>(q / (HD / 8), (q % (HD / 8)) * 8)) = lk.v[i];
         }
         float pc[4][4];
-        if constexpr (!RC) {
 #pragma unroll
-            for (int t = 0; t < 4; t++)
+        for (int t = 0; t < 4; t++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) pc[t][r] = pn[t][r];
-        }
+            for (int r = 0; r < 4; r++) pc[t][r] = pn[t][r];
         __syncthreads();
         if (kt < qt) {
             lv.load(Vh, ks_, (kt + 1) * TK, T);
             lk.load(Kh, ks_, (kt + 1) * TK, T);
-            if constexpr (!RC) load_p_rows(pn, Ph, T, rbase, (kt + 1) * TK, lane);
-        }
-        if constexpr (RC) {
-            // P of this tile exactly as the forward computed it
-            floatx4 S[4];
-            wave_qk_tr<HD>(S, qf, sK, lane);
-            const bool diag = kt == qt;
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const int key = kt * TK + 16 * t + (lane & 15);
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    pc[t][r] = exp2_fast(S[t][r] * sl2 - sm[r]) * si[r];
-                    if (diag && !(key <= rbase + r && key < T)) pc[t][r] = 0.f;
-                }
-            }
+            load_p_rows(pn, Ph, T, rbase, (kt + 1) * TK, lane);
         }
         floatx4 dP[4];
         wave_qk<HD>(dP, of, sV, lane);
@@ -1529,18 +1449,17 @@ __device__ __forceinline__ void load_p_cols(float (&p)[4][4], const float* __res
 // dO is staged twice: padded rows for dP^T (16-byte fragment reads) and in
 // the transposing-read layout for the P^T·dO operand, like Q for dS^T·Q;
 // P^T and dS^T (hi/lo) go to a per-wave [query][key] tile.
-template <int HD, bool RC>  // RC: recompute P from Q, K and the forward's row statistics
+template <int HD>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k_attn_bwd_dkv(
-    const bf16* __restrict__ dO, const bf16* __restrict__ Q, const bf16* __restrict__ K,
-    const bf16* __restrict__ V, const float* __restrict__ P, const float2* __restrict__ stats,
-    const float* __restrict__ Dq, float* __restrict__ part, int T, int Hq, int Hkv, float scale) {
+    const bf16* __restrict__ dO, const bf16* __restrict__ Q, const bf16* __restrict__ V,
+    const float* __restrict__ P, const float* __restrict__ Dq, float* __restrict__ part, int T,
+    int Hq, int Hkv) {
     constexpr int VST = HD / 16;
     __shared__ __attribute__((aligned(16))) bf16 sO[TQ * (HD + 8)];  // dO [q][hd], padded
     __shared__ __attribute__((aligned(16))) char sOn[TQ * HD * 2];   // dO, tr_off layout
     __shared__ __attribute__((aligned(16))) char sQn[TQ * HD * 2];   // Q, tr_off layout
     __shared__ __attribute__((aligned(16))) char sA[4][2][TQ * 16 * 2];  // per wave [q][key] hi,lo
     __shared__ float sD[TQ];
-    __shared__ float2 sSt[TQ];  // (max, 1/sum) of the tile's query rows (RC)
     int nkt = (T + TK - 1) / TK;
     int nbh = gridDim.x / nkt;
     int kt = (int)(blockIdx.x / nbh);  // low kt = most query tiles: they launch first
@@ -1551,22 +1470,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     const bf16* Vh = V + (int64_t)b * T * ks_ + hkv * HD;
     const bf16* dOh = dO + (int64_t)b * T * qs + hq * HD;
     const bf16* Qh = Q + (int64_t)b * T * qs + hq * HD;
-    const float* Ph = RC ? nullptr : P + (int64_t)bh * T * T;
+    const float* Ph = P + (int64_t)bh * T * T;
     const float* Dh = Dq + (int64_t)bh * T;
     int k0 = kt * TK;
     int keyA = k0 + 16 * w + (lane & 15);  // A-operand row (key) of this lane
     bf16x8_t vf[HD / 32];
 #pragma unroll
     for (int s = 0; s < HD / 32; s++) vf[s] = ld_head8(Vh, ks_, keyA, T, 32 * s + 8 * (lane >> 4));
-    // recompute: K fragments for S^T = K Q^T (the forward's S, transposed)
-    bf16x8_t kf[RC ? HD / 32 : 1];
-    const float sl2 = scale * kLog2e;
-    if constexpr (RC) {
-        const bf16* Kh = K + (int64_t)b * T * ks_ + hkv * HD;
-#pragma unroll
-        for (int s = 0; s < HD / 32; s++) kf[s] = ld_head8(Kh, ks_, keyA, T, 32 * s + 8 * (lane >> 4));
-    }
-    const float2* Sth = RC ? stats + (int64_t)bh * T : nullptr;
     int kbase = k0 + 16 * w + 4 * (lane >> 4);  // C-layout key rows kbase + r
 
     floatx4 accK[HD / 16], accV[HD / 16];
@@ -1579,12 +1489,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
     Rows64<HD> ldo, lq;
     float pn[4][4];
     float dn = 0.f;
-    float2 stn = make_float2(0.f, 0.f);
     ldo.load(dOh, qs, kt * TQ, T);
     lq.load(Qh, qs, kt * TQ, T);
-    if constexpr (!RC) load_p_cols(pn, Ph, T, kt * TQ, kbase, lane);
+    load_p_cols(pn, Ph, T, kt * TQ, kbase, lane);
     if (threadIdx.x < TQ) dn = (kt * TQ + threadIdx.x < T) ? Dh[kt * TQ + threadIdx.x] : 0.f;
-    if (RC && threadIdx.x < TQ && kt * TQ + threadIdx.x < T) stn = Sth[kt * TQ + threadIdx.x];
     char* sAh = sA[w][0];
     char* sAl = sA[w][1];
     for (int qt = kt; qt < nqt; qt++) {
@@ -1598,40 +1506,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void k
             *(u32x4*)(sQn + off) = lq.v[i];
         }
         if (threadIdx.x < TQ) sD[threadIdx.x] = dn;
-        if (RC && threadIdx.x < TQ) sSt[threadIdx.x] = stn;
         float pv[4][4];
-        if constexpr (!RC) {
 #pragma unroll
-            for (int t = 0; t < 4; t++)
+        for (int t = 0; t < 4; t++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) pv[t][r] = pn[t][r];
-        }
+            for (int r = 0; r < 4; r++) pv[t][r] = pn[t][r];
         __syncthreads();
         if (qt + 1 < nqt) {
             int qn = (qt + 1) * TQ;
             ldo.load(dOh, qs, qn, T);
             lq.load(Qh, qs, qn, T);
-            if constexpr (!RC) load_p_cols(pn, Ph, T, qn, kbase, lane);
+            load_p_cols(pn, Ph, T, qn, kbase, lane);
             if (threadIdx.x < TQ) dn = (qn + threadIdx.x < T) ? Dh[qn + threadIdx.x] : 0.f;
-            if (RC && threadIdx.x < TQ) stn = (qn + threadIdx.x < T) ? Sth[qn + threadIdx.x] : make_float2(0.f, 0.f);
-        }
-        if constexpr (RC) {
-            // P^T of this tile: the forward's P[query][key] from S^T = K Q^T
-            // (query rows past T have 1/sum = 0); keys above a query are
-            // masked on the diagonal tile only
-            floatx4 St[4];
-            wave_qk_tr<HD>(St, kf, sQn, lane);
-            const bool diag = qt == kt;
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const int ql = 16 * t + (lane & 15);
-                const float2 st = sSt[ql];
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    pv[t][r] = exp2_fast(St[t][r] * sl2 - st.x) * st.y;
-                    if (diag && kbase + r > qt * TQ + ql) pv[t][r] = 0.f;
-                }
-            }
         }
         floatx4 dPt[4];
         wave_qk<HD>(dPt, vf, sO, lane);  // rows = keys, cols = queries
@@ -1840,8 +1726,7 @@ int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const 
     // stored P: the reference's form (64-query tiles); recompute: the
     // transposed-score kernel (128-query blocks)
 #define DQ(H)                                                                             \
-    k_attn_bwd_dq<H, false><<<(int)b1, 256, 0, s>>>(dO, Q, K, V, P, st, Dbuf, nullptr, dQ, T, \
-                                                    Hq, Hkv, scale)
+    k_attn_bwd_dq<H><<<(int)b1, 256, 0, s>>>(dO, K, V, P, Dbuf, dQ, T, Hq, Hkv, scale)
 #define DQT(H)                                                                            \
     k_attn_bwd_dq_t<H><<<(int)((int64_t)B * Hq * ((T + TQ2 - 1) / TQ2)), 256, 0, s>>>(        \
         dO, Q, K, V, st, Dbuf, O32, dQ, T, Hq, Hkv, scale)
@@ -1855,8 +1740,8 @@ int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const 
     if (timed)
         kprof_end(KP_ATTN_BWD_DQ, s, 4.0 * hd * tri + rf,
                   pb + 2.0 * bt * hd * (2.0 * Hq + 2.0 * Hkv) + 4.0 * bt * Hq,
-                  hd == 64 ? (rc ? "void ta::k_attn_bwd_dq_t<64>" : "void ta::k_attn_bwd_dq<64, false>")
-                           : (rc ? "void ta::k_attn_bwd_dq_t<128>" : "void ta::k_attn_bwd_dq<128, false>"));
+                  hd == 64 ? (rc ? "void ta::k_attn_bwd_dq_t<64>" : "void ta::k_attn_bwd_dq<64>")
+                           : (rc ? "void ta::k_attn_bwd_dq_t<128>" : "void ta::k_attn_bwd_dq<128>"));
     timed = kprof_begin(KP_ATTN_BWD_DKV, s);
     if (rc) {
         const int blocks = nkb * B * Hkv * nsplit;
@@ -1867,18 +1752,16 @@ int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const 
             k_attn_bwd_dkv_t<128><<<blocks, 256, 0, s>>>(dO, Q, K, V, Dbuf, part, dK, dV, T, Hq,
                                                           Hkv, nsplit, scale);
     } else if (hd == 64) {
-        k_attn_bwd_dkv<64, false><<<(int)b1, 256, 0, s>>>(dO, Q, K, V, P, st, Dbuf, part, T, Hq,
-                                                          Hkv, scale);
+        k_attn_bwd_dkv<64><<<(int)b1, 256, 0, s>>>(dO, Q, V, P, Dbuf, part, T, Hq, Hkv);
     } else {
-        k_attn_bwd_dkv<128, false><<<(int)b1, 256, 0, s>>>(dO, Q, K, V, P, st, Dbuf, part, T, Hq,
-                                                           Hkv, scale);
+        k_attn_bwd_dkv<128><<<(int)b1, 256, 0, s>>>(dO, Q, V, P, Dbuf, part, T, Hq, Hkv);
     }
     if (timed)
         kprof_end(KP_ATTN_BWD_DKV, s, 6.0 * hd * tri + rf,
                   rc ? 12.0 * B * Hq * (double)T + 2.0 * bt * hd * (2.0 * Hq + 4.0 * Hkv)
                      : pb + 2.0 * bt * hd * (2.0 * Hq + Hkv) + 4.0 * bt * Hq + 8.0 * bt * Hq * hd,
-                  hd == 64 ? (rc ? "void ta::k_attn_bwd_dkv_t<64>" : "void ta::k_attn_bwd_dkv<64, false>")
-                           : (rc ? "void ta::k_attn_bwd_dkv_t<128>" : "void ta::k_attn_bwd_dkv<128, false>"));
+                  hd == 64 ? (rc ? "void ta::k_attn_bwd_dkv_t<64>" : "void ta::k_attn_bwd_dkv<64>")
+                           : (rc ? "void ta::k_attn_bwd_dkv_t<128>" : "void ta::k_attn_bwd_dkv<128>"));
     if (!rc) {
         int64_t n = (int64_t)B * T * Hkv * hd;
         int rb = (int)std::min<int64_t>((n + 255) / 256, 4096);
