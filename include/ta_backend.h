@@ -170,8 +170,9 @@ int ta_gemm_rm(int x_kmajor, int y_kmajor, int M, int N, int K, float alpha,
  * 0 = the default (the pipelined kernel, 192- or 256-wide tiles by N),
  * 7..11 = the 8-/4-wave direct-to-LDS kernel shapes, 12/13 = the 4-wave
  * pipelined kernel with 192/256-wide tiles, 14/15 = its 8-wave 4x2 layout
- * with 256/192-wide tiles, 16 = its 8-wave 2x4 layout (256-wide).  Other
- * values return an error.
+ * with 256/192-wide tiles, 16 = its 8-wave 2x4 layout (256-wide), 17/18 =
+ * the forms of 15/16 with 64-k stages (whole 128-byte operand lines per
+ * direct-to-LDS row).  Other values return an error.
  * No reference counterpart. */
 int ta_gemm_variant(int variant);
 

@@ -496,6 +496,18 @@ __device__ __attribute__((always_inline)) inline void staged_epilogue(
 constexpr int DBK = 32;
 __device__ __forceinline__ int dswz(int R) { return ((R >> 1) ^ (R >> 3)) & 3; }
 
+// Stage rows of KD = 32 k (64 bytes: 4 chunks, above) or KD = 64 k (128
+// bytes, one whole line: 8 chunks, slot c ^ ((R ^ R >> 3) & 7); any 8 or 16
+// consecutive rows then read one chunk each from distinct banks).  One
+// DMA instruction fills 64 / (KD / 8) consecutive rows.
+template <int KD>
+__device__ __forceinline__ int stage_swz(int R) {
+    if constexpr (KD == 32)
+        return dswz(R);
+    else
+        return (R ^ (R >> 3)) & 7;
+}
+
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // Issue this wave's share of the loads of one stage: operand rows
@@ -505,20 +517,21 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 // (so the compiler's wait bookkeeping stays exact): j = w + NW h; an index
 // past the end repeats an instruction of a lower wave, writing the same
 // bytes.
-template <int ROWS, int NW>
+template <int ROWS, int NW, int KD = DBK>
 __device__ __forceinline__ void dma_stage(const bf16* __restrict__ P, int64_t ld, int row0,
                                           int rows, int k0, bf16* stage, int w, int lane) {
-    constexpr int NI = ROWS / 16;
+    constexpr int LPR = KD / 8, RPI = 64 / LPR;  // lanes per row, rows per instruction
+    constexpr int NI = ROWS / RPI;
     constexpr int PER = (NI + NW - 1) / NW;
 #pragma unroll
     for (int h = 0; h < PER; h++) {
         int j = w + NW * h;
         j = j < NI ? j : j - NW;
-        int r = 16 * j + (lane >> 2);
-        int c = (lane & 3) ^ dswz(r);
+        int r = RPI * j + lane / LPR;
+        int c = (lane % LPR) ^ stage_swz<KD>(r);
         int grow = min(row0 + r, rows - 1);
         const bf16* src = P + (int64_t)grow * ld + k0 + 8 * c;
-        __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr_t)(stage + 16 * j * DBK), 16, 0,
+        __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr_t)(stage + RPI * j * KD), 16, 0,
                                          0);
     }
 }
@@ -528,32 +541,36 @@ __device__ __forceinline__ void dma_stage(const bf16* __restrict__ P, int64_t ld
 // this lane's element offset (clamped row x ld + swizzled chunk) for each of
 // the wave's PER instructions; dma_stage_at issues them for one stage from a
 // base pointer and k0.  Same addresses as dma_stage.
-template <int ROWS, int NW>
+template <int ROWS, int NW, int KD = DBK>
 struct DmaOffs {
-    static constexpr int NI = ROWS / 16, PER = (NI + NW - 1) / NW;
+    static constexpr int LPR = KD / 8, RPI = 64 / LPR;
+    static constexpr int NI = ROWS / RPI, PER = (NI + NW - 1) / NW;
     int o[PER];
 };
-template <int ROWS, int NW>
-__device__ __forceinline__ void dma_offsets(DmaOffs<ROWS, NW>& d, int64_t ld, int row0, int rows,
-                                            int w, int lane) {
+template <int ROWS, int NW, int KD>
+__device__ __forceinline__ void dma_offsets(DmaOffs<ROWS, NW, KD>& d, int64_t ld, int row0,
+                                            int rows, int w, int lane) {
+    using D = DmaOffs<ROWS, NW, KD>;
 #pragma unroll
-    for (int h = 0; h < DmaOffs<ROWS, NW>::PER; h++) {
+    for (int h = 0; h < D::PER; h++) {
         int j = w + NW * h;
-        j = j < DmaOffs<ROWS, NW>::NI ? j : j - NW;
-        const int r = 16 * j + (lane >> 2);
-        const int c = (lane & 3) ^ dswz(r);
+        j = j < D::NI ? j : j - NW;
+        const int r = D::RPI * j + lane / D::LPR;
+        const int c = (lane % D::LPR) ^ stage_swz<KD>(r);
         d.o[h] = (int)((int64_t)min(row0 + r, rows - 1) * ld) + 8 * c;
     }
 }
-template <int ROWS, int NW>
-__device__ __forceinline__ void dma_stage_at(const bf16* __restrict__ P, const DmaOffs<ROWS, NW>& d,
-                                             int k0, bf16* stage, int w) {
+template <int ROWS, int NW, int KD>
+__device__ __forceinline__ void dma_stage_at(const bf16* __restrict__ P,
+                                             const DmaOffs<ROWS, NW, KD>& d, int k0, bf16* stage,
+                                             int w) {
+    using D = DmaOffs<ROWS, NW, KD>;
 #pragma unroll
-    for (int h = 0; h < DmaOffs<ROWS, NW>::PER; h++) {
+    for (int h = 0; h < D::PER; h++) {
         int j = w + NW * h;
-        j = j < DmaOffs<ROWS, NW>::NI ? j : j - NW;
+        j = j < D::NI ? j : j - NW;
         __builtin_amdgcn_global_load_lds((const void*)(P + d.o[h] + k0),
-                                         (lds_ptr_t)(stage + 16 * j * DBK), 16, 0, 0);
+                                         (lds_ptr_t)(stage + D::RPI * j * KD), 16, 0, 0);
     }
 }
 
@@ -705,19 +722,19 @@ struct Frags {
     bf16x8_t a[TM], b[TN];
 };
 
-template <int TM, int TN, int WTM, int WTN>
+template <int TM, int TN, int WTM, int WTN, int KD = DBK>
 __device__ __forceinline__ void pipe_frags(Frags<TM, TN>& f, const bf16* sX, const bf16* sY,
                                            int wm, int wn, int lane, int kk) {
     const int c = 2 * kk + (lane >> 5);
 #pragma unroll
     for (int i = 0; i < TM; i++) {
         int R = wm * WTM + i * 32 + (lane & 31);
-        f.a[i] = *(const bf16x8_t*)(sX + R * DBK + 8 * (c ^ dswz(R)));
+        f.a[i] = *(const bf16x8_t*)(sX + R * KD + 8 * (c ^ stage_swz<KD>(R)));
     }
 #pragma unroll
     for (int j = 0; j < TN; j++) {
         int R = wn * WTN + j * 32 + (lane & 31);
-        f.b[j] = *(const bf16x8_t*)(sY + R * DBK + 8 * (c ^ dswz(R)));
+        f.b[j] = *(const bf16x8_t*)(sY + R * KD + 8 * (c ^ stage_swz<KD>(R)));
     }
 }
 
@@ -946,18 +963,30 @@ __device__ __forceinline__ void round_acc(floatx16 (&acc)[TM][TN]) {
 // with its pair's LoRA delta, and then every gate/up wave pair writes
 // act = silu(gate) * up from the two staged BF16 halves (gC[0..2] = gate,
 // up, act; gu/gv[0..1] the pairs' h and B; gN[0] = gldc[0] = I).
-template <int BN, int WMW, int WNW, bool CHAIN, bool SWIGLU = false>
+//
+// KD: stage depth.  KD = 32: four stages of 32 k (rows of half a line).
+// KD = 64: two stages of 64 k in the same LDS, rows of one whole 128-byte
+// line, so every line of an operand is fetched once; the next stage's load
+// has the same 64 k of compute to land in as with four 32-k stages.
+template <int BN, int WMW, int WNW, bool CHAIN, bool SWIGLU = false, int KD = 32>
 __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmArgs& a0) {
-    constexpr int NS = 4, BM = 256, NW = WMW * WNW;
+    static_assert(KD == 32 || KD == 64, "stage depth");
+    constexpr int NS = KD == 32 ? 4 : 2, BM = 256, NW = WMW * WNW;
     constexpr int WTM = BM / WMW, WTN = BN / WNW;
     constexpr int TM = WTM / 32, TN = WTN / 32;
     static_assert(TM * 32 == WTM && TN * 32 == WTN && TM % 2 == 0, "wave tile");
+    static_assert(KD == 32 || NW == 8, "64-k stages: 8-wave layouts");
     // DMA instructions per stage per wave
-    constexpr int LPS = (BM / 16 + NW - 1) / NW + (BN / 16 + NW - 1) / NW;
-    constexpr int SX = BM * DBK, SY = BN * DBK;
+    constexpr int RPI = 64 / (KD / 8);  // stage rows per DMA instruction
+    constexpr int LPS = (BM / RPI + NW - 1) / NW + (BN / RPI + NW - 1) / NW;
+    constexpr int SX = BM * KD, SY = BN * KD;
     static_assert(BN == 192 || BN == 256, "tile width");
-    __shared__ __attribute__((aligned(1024))) bf16 sX0[SX], sX1[SX], sX2[SX], sX3[SX];
-    __shared__ __attribute__((aligned(1024))) bf16 sY0[SY], sY1[SY], sY2[SY], sY3[SY];
+    __shared__ __attribute__((aligned(1024))) bf16 sXs[NS][SX];
+    __shared__ __attribute__((aligned(1024))) bf16 sYs[NS][SY];
+    bf16* const sX0 = sXs[0];
+    bf16* const sX1 = sXs[1];
+    bf16* const sY0 = sYs[0];
+    bf16* const sY1 = sYs[1];
     // epilogue operands staged at the start: rank-16 LoRA U/V rows of the
     // first LP pairs and 512 bias entries (one DMA instruction)
     constexpr int LP = BN == 256 ? 1 : 3;
@@ -1050,13 +1079,13 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
     // K runs as stages kt = -pad .. nk-1 (pad zero stages make the count a
     // multiple of NS; stages past the end reload the last one into a buffer
     // that is never read), as in k_gemm_dma
-    const int nk = a.K / DBK;
+    const int nk = a.K / KD;
     const int pad = (NS - nk % NS) % NS;
     // K segments: stage kt (global k) belongs to segment s; the accumulators
     // are rounded after the last stage of every segment but the last
-    const int kb1 = CHAIN ? a.kseg[1] / DBK : -99, kb2 = CHAIN && a.nseg > 2 ? a.kseg[2] / DBK : -99;
-    DmaOffs<BM, NW> ox0, ox1, ox2;
-    DmaOffs<BN, NW> oy0, oy1, oy2;
+    const int kb1 = CHAIN ? a.kseg[1] / KD : -99, kb2 = CHAIN && a.nseg > 2 ? a.kseg[2] / KD : -99;
+    DmaOffs<BM, NW, KD> ox0, ox1, ox2;
+    DmaOffs<BN, NW, KD> oy0, oy1, oy2;
     if constexpr (CHAIN) {
         dma_offsets<BM, NW>(ox0, a.sldx[0], m0, a.M, w, lane);
         dma_offsets<BN, NW>(oy0, a.sldy[0], n0, a.N, w, lane);
@@ -1069,7 +1098,7 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
     do {                                                                                   \
         const int kq_ = (KT);                                                              \
         const bool z_ = kq_ < 0;                                                           \
-        int k_ = z_ ? 0 : min(kq_, nk - 1) * DBK;                                          \
+        int k_ = z_ ? 0 : min(kq_, nk - 1) * KD;                                           \
         const bf16* x_ = a.X;                                                              \
         const bf16* y_ = a.Y;                                                              \
         int64_t lx_ = a.ldx, ly_ = a.ldy;                                                  \
@@ -1080,17 +1109,19 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
             y_ = s_ == 2 ? a.sY[2] : s_ == 1 ? a.sY[1] : a.sY[0];                          \
             k_ -= s_ == 2 ? a.kseg[2] : s_ == 1 ? a.kseg[1] : 0;                           \
             if (z_) {                                                                      \
-                dma_stage<BM, NW>(g_dma_zero, 0, m0, a.M, 0, SXB, w, lane);                \
-                dma_stage<BN, NW>(g_dma_zero, 0, n0, a.N, 0, SYB, w, lane);                \
+                dma_stage<BM, NW, KD>(g_dma_zero, 0, m0, a.M, 0, SXB, w, lane);            \
+                dma_stage<BN, NW, KD>(g_dma_zero, 0, n0, a.N, 0, SYB, w, lane);            \
             } else {                                                                       \
-                dma_stage_at<BM, NW>(x_, s_ == 2 ? ox2 : s_ == 1 ? ox1 : ox0, k_, SXB, w); \
-                dma_stage_at<BN, NW>(y_, s_ == 2 ? oy2 : s_ == 1 ? oy1 : oy0, k_, SYB, w); \
+                dma_stage_at<BM, NW, KD>(x_, s_ == 2 ? ox2 : s_ == 1 ? ox1 : ox0, k_, SXB, \
+                                         w);                                               \
+                dma_stage_at<BN, NW, KD>(y_, s_ == 2 ? oy2 : s_ == 1 ? oy1 : oy0, k_, SYB, \
+                                         w);                                               \
             }                                                                              \
         } else {                                                                           \
-            dma_stage<BM, NW>(z_ ? g_dma_zero : x_, z_ ? 0 : lx_, m0, a.M, k_, SXB, w,     \
-                              lane);                                                       \
-            dma_stage<BN, NW>(z_ ? g_dma_zero : y_, z_ ? 0 : ly_, n0, a.N, k_, SYB, w,     \
-                              lane);                                                       \
+            dma_stage<BM, NW, KD>(z_ ? g_dma_zero : x_, z_ ? 0 : lx_, m0, a.M, k_, SXB, w, \
+                                  lane);                                                   \
+            dma_stage<BN, NW, KD>(z_ ? g_dma_zero : y_, z_ ? 0 : ly_, n0, a.N, k_, SYB, w, \
+                                  lane);                                                   \
         }                                                                                  \
     } while (0)
 // (chains start every segment on a loop trip of NS stages, which the host
@@ -1101,12 +1132,17 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
         if constexpr (CHAIN)                                                               \
             if ((KT) + 1 == kb1 || (KT) + 1 == kb2) round_acc<TM, TN>(acc);                \
     } while (0)
+    Frags<TM, TN> f0, f1;
+    if constexpr (KD == 32) {
+    bf16* const sX2 = sXs[2];
+    bf16* const sX3 = sXs[3];
+    bf16* const sY2 = sYs[2];
+    bf16* const sY3 = sYs[3];
     PIPE_ISSUE(sX0, sY0, 0 - pad);
     PIPE_ISSUE(sX1, sY1, 1 - pad);
     PIPE_ISSUE(sX2, sY2, 2 - pad);
     TA_WAIT_VMCNT(LPS * (NS - 2));
     __builtin_amdgcn_s_barrier();
-    Frags<TM, TN> f0, f1;
     pipe_frags<TM, TN, WTM, WTN>(f0, sX0, sY0, wm, wn, lane, 0);
     // step J: second-half fragments of stage J while the first half
     // computes; wait for stage J+1 (NS - 3 stages may stay in flight);
@@ -1131,9 +1167,57 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
         PIPE_STEP(3, sX3, sY3, sX0, sY0, sX2, sY2);
         PIPE_ROUND(kt0 + 3);
     }
+#undef PIPE_STEP
+    } else {
+    // 64-k stages: step J computes stage J (k steps 0..3) from buffer J % 2;
+    // its k step 3 fragments are read before the barrier that frees the
+    // buffer for stage J + 2 (waited for: the DMA must not overwrite them),
+    // after which the next stage's first fragments are read while k step 3
+    // computes.  The only loads in flight at a step's wait are stage J + 1's.
+    // Waves 0..NW/2-1 issue their share of stage J + 2 right after the
+    // barrier that frees its buffer, the other half after their first k step
+    // of stage J + 1.  A wave cannot issue while its direct-to-LDS loads
+    // queue for the address unit (about 25 cycles per 1 KB instruction per
+    // CU), so when all eight waves issue at once every SIMD sits idle for the
+    // queue; staggered, each SIMD's other wave keeps the matrix core busy.
+    const bool lo_ = w < NW / 2;  // (wave-uniform)
+    PIPE_ISSUE(sX0, sY0, 0 - pad);
+    if (lo_) {
+        PIPE_ISSUE(sX1, sY1, 1 - pad);
+        TA_WAIT_VMCNT(LPS);
+    } else {
+        TA_WAIT_VMCNT(0);
+    }
+    __builtin_amdgcn_s_barrier();
+    pipe_frags<TM, TN, WTM, WTN, KD>(f0, sX0, sY0, wm, wn, lane, 0);
+#define PIPE_STEP(J, SXJ, SYJ, SXN, SYN)                                                   \
+    do {                                                                                   \
+        pipe_frags<TM, TN, WTM, WTN, KD>(f1, SXJ, SYJ, wm, wn, lane, 1);                   \
+        pipe_mma<TM, TN>(acc, f0);                                                         \
+        pipe_interleave<TM * TN, TM + TN>();                                               \
+        if (!lo_) PIPE_ISSUE(SXN, SYN, kt0 + (J) + 1);                                     \
+        pipe_frags<TM, TN, WTM, WTN, KD>(f0, SXJ, SYJ, wm, wn, lane, 2);                   \
+        pipe_mma<TM, TN>(acc, f1);                                                         \
+        pipe_interleave<TM * TN, TM + TN>();                                               \
+        pipe_frags<TM, TN, WTM, WTN, KD>(f1, SXJ, SYJ, wm, wn, lane, 3);                   \
+        pipe_mma<TM, TN>(acc, f0);                                                         \
+        pipe_interleave<TM * TN, TM + TN>();                                               \
+        __builtin_amdgcn_s_waitcnt(0x0070); /* vmcnt(0) lgkmcnt(0) */                      \
+        __builtin_amdgcn_s_barrier();                                                      \
+        if (lo_) PIPE_ISSUE(SXJ, SYJ, kt0 + (J) + 2);                                      \
+        pipe_frags<TM, TN, WTM, WTN, KD>(f0, SXN, SYN, wm, wn, lane, 0);                   \
+        pipe_mma<TM, TN>(acc, f1);                                                         \
+        pipe_interleave<TM * TN, TM + TN>();                                               \
+    } while (0)
+    for (int kt0 = -pad; kt0 < nk; kt0 += NS) {
+        PIPE_STEP(0, sX0, sY0, sX1, sY1);
+        PIPE_STEP(1, sX1, sY1, sX0, sY0);
+        PIPE_ROUND(kt0 + 1);
+    }
+#undef PIPE_STEP
+    }
     TA_WAIT_VMCNT(0);  // the surplus loads have landed before the buffers are reused
 #undef PIPE_ROUND
-#undef PIPE_STEP
 #undef PIPE_ISSUE
     __syncthreads();
     // each wave stages its 64-row halves in LDS of its own: the 4-wave
@@ -1142,14 +1226,24 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
     const bf16* lu = lds_lora ? sLU : nullptr;
     const bf16* lv = lds_lora ? sLV : nullptr;
     const bf16* lb = lds_bias ? sB : nullptr;
+    // (64-k stages: two waves per stage buffer)
+    auto wave_stage = [&](int v) -> bf16* {
+        if constexpr (KD == 32) {
+            return v == 0 ? sXs[0] : v == 1 ? sXs[1] : v == 2 ? sXs[2] : v == 3 ? sXs[3]
+                 : v == 4 ? sYs[0] : v == 5 ? sYs[1] : v == 6 ? sYs[2] : sYs[3];
+        } else {
+            static_assert(2 * 64 * WTN * (TM / 2) <= SY, "staging fits half a stage buffer");
+            bf16* b = (v >> 1) == 0 ? sXs[0] : (v >> 1) == 1 ? sXs[1] : (v >> 1) == 2 ? sYs[0] : sYs[1];
+            return b + (v & 1) * (64 * WTN * (TM / 2));
+        }
+    };
     bf16 *wb0, *wb1;
     if constexpr (NW == 4) {
-        wb0 = w == 0 ? sX0 : w == 1 ? sX1 : w == 2 ? sX2 : sX3;
-        wb1 = w == 0 ? sY0 : w == 1 ? sY1 : w == 2 ? sY2 : sY3;
+        wb0 = sXs[w];
+        wb1 = sYs[w];
         static_assert(64 * WTN <= SX && 64 * WTN <= SY, "staging fits a stage buffer");
     } else {
-        bf16* b = w == 0 ? sX0 : w == 1 ? sX1 : w == 2 ? sX2 : w == 3 ? sX3
-                : w == 4 ? sY0 : w == 5 ? sY1 : w == 6 ? sY2 : sY3;
+        bf16* b = wave_stage(w);
         static_assert(64 * WTN * (TM / 2) <= SY, "staging fits a stage buffer");
         wb0 = b;
         wb1 = b + 64 * WTN;
@@ -1171,9 +1265,7 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
         __syncthreads();  // the partner wave's halves are staged
         // act = silu(gate) * up: the gate wave takes the first 64 rows, the
         // up wave (w ^ 2) the second, each from both waves' staging
-        const int pw = w ^ 2;
-        bf16* pb = pw == 0 ? sX0 : pw == 1 ? sX1 : pw == 2 ? sX2 : pw == 3 ? sX3
-                 : pw == 4 ? sY0 : pw == 5 ? sY1 : pw == 6 ? sY2 : sY3;
+        bf16* pb = wave_stage(w ^ 2);
         const bf16* gst = upw ? pb + 64 * WTN : wb0;
         const bf16* ust = upw ? wb1 : pb;
         const int rb = m0 + wm * WTM + (upw ? 64 : 0);
@@ -1199,34 +1291,39 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
     }
 }
 
-template <int BN, int WMW, int WNW>
+template <int BN, int WMW, int WNW, int KD = 32>
 __global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
     WMW * WNW / 4, WMW * WNW / 4))) void k_gemm_pipe(GemmArgs a) {
-    gemm_pipe_body<BN, WMW, WNW, false>(a);
+    gemm_pipe_body<BN, WMW, WNW, false, false, KD>(a);
 }
-template <int BN, int WMW, int WNW>
+template <int BN, int WMW, int WNW, int KD = 32>
 __global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
     WMW * WNW / 4, WMW * WNW / 4))) void k_gemm_pipe_chain(GemmArgs a) {
-    gemm_pipe_body<BN, WMW, WNW, true>(a);
+    gemm_pipe_body<BN, WMW, WNW, true, false, KD>(a);
 }
-template <int BN, int WMW, int WNW>
+template <int BN, int WMW, int WNW, int KD = 32>
 __global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
     WMW * WNW / 4, WMW * WNW / 4))) void k_gemm_pipe_swiglu(GemmArgs a) {
-    gemm_pipe_body<BN, WMW, WNW, false, true>(a);
+    gemm_pipe_body<BN, WMW, WNW, false, true, KD>(a);
 }
 
 // Kernel variants of the large GEMMs (ta_gemm_variant): 0 picks k_gemm_pipe
-// with 8 waves (256 x 192 tiles in a 4 x 2 wave layout up to N = 3072,
-// 256 x 256 in a 2 x 4 layout above; N = 1536 then gives one block per CU at
-// M = 8192); 7..11 are k_gemm_dma shapes kept for sweeps and for the split-K
-// partials; 12..16 force one k_gemm_pipe shape.
+// with 8 waves and 64-k stages (256 x 192 tiles in a 4 x 2 wave layout up
+// to N = 3072, 256 x 256 in a 2 x 4 layout above; N = 1536 then gives one
+// block per CU at M = 8192): variants 17 and 18.  7..11 are k_gemm_dma
+// shapes kept for sweeps and for the split-K partials; 12..16 force one
+// k_gemm_pipe shape with 32-k stages (15, 16: the 32-k forms of 17, 18).
 static int g_big_variant = 0;
-static bool variant_ok(int v) { return v == 0 || (v >= 7 && v <= 16); }
+static bool variant_ok(int v) { return v == 0 || (v >= 7 && v <= 18); }
 static bool is_pipe(int variant) { return variant >= 12; }
 static int big_bn(int variant) {
-    return (variant == 8 || variant == 10 || variant == 13 || variant == 14 || variant == 16) ? 256
-                                                                                              : 192;
+    return (variant == 8 || variant == 10 || variant == 13 || variant == 14 || variant == 16 ||
+            variant == 18)
+               ? 256
+               : 192;
 }
+// stage depth of a pipe variant (17, 18: the 64-k forms of 15, 16)
+static int pipe_kd(int variant) { return variant >= 17 ? 64 : 32; }
 
 // symbol of the unsplit BF16-output instance of each variant, as printed
 // by the profiler
@@ -1241,6 +1338,8 @@ static const char* big_name(int variant) {
         case 14: return "void ta::k_gemm_pipe<256, 4, 2>(ta::GemmArgs)";
         case 15: return "void ta::k_gemm_pipe<192, 4, 2>(ta::GemmArgs)";
         case 16: return "void ta::k_gemm_pipe<256, 2, 4>(ta::GemmArgs)";
+        case 17: return "void ta::k_gemm_pipe<192, 4, 2, 64>(ta::GemmArgs)";
+        case 18: return "void ta::k_gemm_pipe<256, 2, 4, 64>(ta::GemmArgs)";
         default: return "void ta::k_gemm_pipe<192, 2, 2>(ta::GemmArgs)";
     }
 }
@@ -1344,7 +1443,7 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
     // large K-contiguous BF16 GEMMs: k_gemm_pipe (k_gemm_dma for split-K)
     if (xk && yk && !out_f32 && M >= 1024 && N >= 1024 && (K % BK) == 0 && vx && vy) {
         int variant = g_big_variant;
-        if (variant == 0) variant = N > 3072 ? 16 : 15;
+        if (variant == 0) variant = N > 3072 ? 18 : 17;
         const int BNb = big_bn(variant);
         a.tiles_m = (M + 255) / 256;
         a.tiles_n = (N + BNb - 1) / BNb;
@@ -1403,6 +1502,10 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
             k_gemm_pipe<192, 4, 2><<<grid, 512, 0, s>>>(a);
         else if (variant == 16)
             k_gemm_pipe<256, 2, 4><<<grid, 512, 0, s>>>(a);
+        else if (variant == 17)
+            k_gemm_pipe<192, 4, 2, 64><<<grid, 512, 0, s>>>(a);
+        else if (variant == 18)
+            k_gemm_pipe<256, 2, 4, 64><<<grid, 512, 0, s>>>(a);
         else
             launch_big<EPI_BF16>(variant, grid, a, s);
         if (timed) {
@@ -1501,10 +1604,11 @@ int gemm_chain(int M, int N, const GemmSeg* sg, int ns, bf16* C, int64_t ldc, co
                hipStream_t s) {
     TA_REQUIRE(ns >= 1 && ns <= 3, "gemm_chain: %d segments", ns);
     int variant = g_big_variant;
-    if (variant == 0) variant = N > 3072 ? 16 : 15;
+    if (variant == 0) variant = N > 3072 ? 18 : 17;
     const int BNb = big_bn(variant);  // the chain kernel comes in the two default shapes
     int Ktot = 0;
-    bool ok = ns > 1 && (variant == 15 || variant == 16) && M >= 1024 && N >= 1024;
+    const int KD = pipe_kd(variant), NS = KD == 32 ? 4 : 2;
+    bool ok = ns > 1 && variant >= 15 && variant <= 18 && M >= 1024 && N >= 1024;
     for (int q = 0; q < ns; q++) {
         Ktot += sg[q].K;
         ok &= sg[q].K % BK == 0 && al16(sg[q].X) && al16(sg[q].Y) && sg[q].ldx % 8 == 0 &&
@@ -1516,13 +1620,13 @@ int gemm_chain(int M, int N, const GemmSeg* sg, int ns, bf16* C, int64_t ldc, co
     // (as gemm_dispatch: few tiles and a long K go to split-K instead)
     ok &= tiles >= 192 || Ktot / BK < 32;
     // every segment must start on a loop trip of the kernel (4 stages of 32
-    // k after the leading zero stages), where the kernel rounds
+    // k or 2 of 64 after the leading zero stages), where the kernel rounds
     {
-        const int nk = Ktot / 32, pad = (4 - nk % 4) % 4;
+        const int nk = Ktot / KD, pad = (NS - nk % NS) % NS;
         int kb = 0;
         for (int q = 0; q + 1 < ns; q++) {
             kb += sg[q].K;
-            ok &= (kb / 32 + pad) % 4 == 0;
+            ok &= (kb / KD + pad) % NS == 0;
         }
     }
     ok &= !lora || lora->n == 0 || lora->r <= 16;
@@ -1574,7 +1678,11 @@ int gemm_chain(int M, int N, const GemmSeg* sg, int ns, bf16* C, int64_t ldc, co
     }
     dim3 grid(a.tiles_m * a.tiles_n);
     const bool timed = kprof_begin(KP_GEMM_CHAIN, s);
-    if (BNb == 192)
+    if (BNb == 192 && KD == 64)
+        k_gemm_pipe_chain<192, 4, 2, 64><<<grid, 512, 0, s>>>(a);
+    else if (KD == 64)
+        k_gemm_pipe_chain<256, 2, 4, 64><<<grid, 512, 0, s>>>(a);
+    else if (BNb == 192)
         k_gemm_pipe_chain<192, 4, 2><<<grid, 512, 0, s>>>(a);
     else
         k_gemm_pipe_chain<256, 2, 4><<<grid, 512, 0, s>>>(a);
@@ -1585,8 +1693,10 @@ int gemm_chain(int M, int N, const GemmSeg* sg, int ns, bf16* C, int64_t ldc, co
         double by = 2.0 * ((double)M * Ktot + (double)N * Ktot + mn) +
                     2.0 * a.lora_n * (double)(M + N) * a.lora_r;
         kprof_end(KP_GEMM_CHAIN, s, fl, by,
-                  BNb == 192 ? "void ta::k_gemm_pipe_chain<192, 4, 2>(ta::GemmArgs)"
-                             : "void ta::k_gemm_pipe_chain<256, 2, 4>(ta::GemmArgs)");
+                  KD == 64 ? (BNb == 192 ? "void ta::k_gemm_pipe_chain<192, 4, 2, 64>(ta::GemmArgs)"
+                                         : "void ta::k_gemm_pipe_chain<256, 2, 4, 64>(ta::GemmArgs)")
+                           : (BNb == 192 ? "void ta::k_gemm_pipe_chain<192, 4, 2>(ta::GemmArgs)"
+                                         : "void ta::k_gemm_pipe_chain<256, 2, 4>(ta::GemmArgs)"));
     }
     return check_launch("gemm_chain");
 }
@@ -1618,7 +1728,7 @@ int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const Gem
         }
     }
     int variant = g_big_variant;
-    if (variant == 0) variant = all256 ? 16 : 15;
+    if (variant == 0) variant = all256 ? 18 : 17;
     const int BNb = big_bn(variant);
     const bool tiles_ok = BNb == 256 ? all256 : all192;
     const int tiles = ((M + 255) / 256) * (Ntot / BNb);
@@ -1686,6 +1796,10 @@ int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const Gem
         k_gemm_pipe<256, 4, 2><<<grid, 512, 0, s>>>(a);
     else if (variant == 15)
         k_gemm_pipe<192, 4, 2><<<grid, 512, 0, s>>>(a);
+    else if (variant == 17)
+        k_gemm_pipe<192, 4, 2, 64><<<grid, 512, 0, s>>>(a);
+    else if (variant == 18)
+        k_gemm_pipe<256, 2, 4, 64><<<grid, 512, 0, s>>>(a);
     else
         k_gemm_pipe<256, 2, 4><<<grid, 512, 0, s>>>(a);
     if (timed) {
@@ -1716,7 +1830,8 @@ int gemm_swiglu(int M, int K, const bf16* X, int64_t ldx, const bf16* Wgu, const
                                lu->ldu[0] == 16)
                             : !(lu && lu->n > 0);
     const int tiles = ((M + 255) / 256) * (2 * I / 256);
-    const bool ok = Wgu && lora_ok && (g_big_variant == 0 || g_big_variant == 16) && M >= 1024 &&
+    const bool ok = Wgu && lora_ok &&
+                    (g_big_variant == 0 || g_big_variant == 16 || g_big_variant == 18) && M >= 1024 &&
                     I % 128 == 0 && 2 * I >= 1024 && K % BK == 0 && al16(X) && ldx % 8 == 0 &&
                     al16(Wgu) && al16(gate) && al16(up) && al16(act) && I % 8 == 0 &&
                     (tiles >= 192 || K / BK < 32);
@@ -1759,14 +1874,20 @@ int gemm_swiglu(int M, int K, const bf16* X, int64_t ldx, const bf16* Wgu, const
         a.gv[1] = lu->v_nk[0];
     }
     const bool timed = kprof_begin(KP_GEMM_SWIGLU, s);
-    k_gemm_pipe_swiglu<256, 2, 4><<<tiles, 512, 0, s>>>(a);
+    const bool kd64 = g_big_variant != 16;
+    if (kd64)
+        k_gemm_pipe_swiglu<256, 2, 4, 64><<<tiles, 512, 0, s>>>(a);
+    else
+        k_gemm_pipe_swiglu<256, 2, 4><<<tiles, 512, 0, s>>>(a);
     if (timed) {
         // X and both weights read once; gate, up and act written once
         const double mn = 2.0 * M * I;
         const double fl = 2.0 * mn * K + (on ? 2.0 * mn * 16 : 0.0);
         const double by = 2.0 * ((double)M * K + 2.0 * I * (double)K + 1.5 * mn) +
                           (on ? 2.0 * 2.0 * (M + I) * 16 : 0.0);
-        kprof_end(KP_GEMM_SWIGLU, s, fl, by, "void ta::k_gemm_pipe_swiglu<256, 2, 4>(ta::GemmArgs)");
+        kprof_end(KP_GEMM_SWIGLU, s, fl, by,
+                  kd64 ? "void ta::k_gemm_pipe_swiglu<256, 2, 4, 64>(ta::GemmArgs)"
+                       : "void ta::k_gemm_pipe_swiglu<256, 2, 4>(ta::GemmArgs)");
     }
     return check_launch("gemm_swiglu");
 }
@@ -1814,7 +1935,7 @@ using namespace ta;
 extern "C" {
 
 int ta_gemm_variant(int v) {
-    TA_REQUIRE(variant_ok(v), "gemm_variant: %d is not a kernel variant (0, 7..16)", v);
+    TA_REQUIRE(variant_ok(v), "gemm_variant: %d is not a kernel variant (0, 7..18)", v);
     g_big_variant = v;
     return 0;
 }
