@@ -1094,7 +1094,7 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
         dma_offsets<BM, NW>(ox2, a.nseg > 2 ? a.sldx[2] : 0, m0, a.M, w, lane);
         dma_offsets<BN, NW>(oy2, a.nseg > 2 ? a.sldy[2] : 0, n0, a.N, w, lane);
     }
-#define PIPE_ISSUE(SXB, SYB, KT)                                                           \
+#define PIPE_ISSUE_P(SXB, SYB, KT, DOX, DOY)                                                        \
     do {                                                                                   \
         const int kq_ = (KT);                                                              \
         const bool z_ = kq_ < 0;                                                           \
@@ -1109,21 +1109,22 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
             y_ = s_ == 2 ? a.sY[2] : s_ == 1 ? a.sY[1] : a.sY[0];                          \
             k_ -= s_ == 2 ? a.kseg[2] : s_ == 1 ? a.kseg[1] : 0;                           \
             if (z_) {                                                                      \
-                dma_stage<BM, NW, KD>(g_dma_zero, 0, m0, a.M, 0, SXB, w, lane);            \
-                dma_stage<BN, NW, KD>(g_dma_zero, 0, n0, a.N, 0, SYB, w, lane);            \
+                if (DOX) dma_stage<BM, NW, KD>(g_dma_zero, 0, m0, a.M, 0, SXB, w, lane);            \
+                if (DOY) dma_stage<BN, NW, KD>(g_dma_zero, 0, n0, a.N, 0, SYB, w, lane);            \
             } else {                                                                       \
-                dma_stage_at<BM, NW, KD>(x_, s_ == 2 ? ox2 : s_ == 1 ? ox1 : ox0, k_, SXB, \
+                if (DOX) dma_stage_at<BM, NW, KD>(x_, s_ == 2 ? ox2 : s_ == 1 ? ox1 : ox0, k_, SXB, \
                                          w);                                               \
-                dma_stage_at<BN, NW, KD>(y_, s_ == 2 ? oy2 : s_ == 1 ? oy1 : oy0, k_, SYB, \
+                if (DOY) dma_stage_at<BN, NW, KD>(y_, s_ == 2 ? oy2 : s_ == 1 ? oy1 : oy0, k_, SYB, \
                                          w);                                               \
             }                                                                              \
         } else {                                                                           \
-            dma_stage<BM, NW, KD>(z_ ? g_dma_zero : x_, z_ ? 0 : lx_, m0, a.M, k_, SXB, w, \
+            if (DOX) dma_stage<BM, NW, KD>(z_ ? g_dma_zero : x_, z_ ? 0 : lx_, m0, a.M, k_, SXB, w, \
                                   lane);                                                   \
-            dma_stage<BN, NW, KD>(z_ ? g_dma_zero : y_, z_ ? 0 : ly_, n0, a.N, k_, SYB, w, \
+            if (DOY) dma_stage<BN, NW, KD>(z_ ? g_dma_zero : y_, z_ ? 0 : ly_, n0, a.N, k_, SYB, w, \
                                   lane);                                                   \
         }                                                                                  \
     } while (0)
+#define PIPE_ISSUE(SXB, SYB, KT) PIPE_ISSUE_P(SXB, SYB, KT, true, true)
 // (chains start every segment on a loop trip of NS stages, which the host
 // checks, so the rounding test sits between trips and the NS steps of a
 // trip stay one straight-line region)
@@ -1174,20 +1175,33 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
     // buffer for stage J + 2 (waited for: the DMA must not overwrite them),
     // after which the next stage's first fragments are read while k step 3
     // computes.  The only loads in flight at a step's wait are stage J + 1's.
-    // Waves 0..NW/2-1 issue their share of stage J + 2 right after the
-    // barrier that frees its buffer, the other half after their first k step
-    // of stage J + 1.  A wave cannot issue while its direct-to-LDS loads
+    // The waves issue their shares of a stage's X and Y rows at three
+    // points: A, right after the barrier that frees the buffer (for stage
+    // J + 2), and B / C, after the first / second k step of the next step
+    // (for its stage + 1).  A wave cannot issue while its direct-to-LDS loads
     // queue for the address unit (about 25 cycles per 1 KB instruction per
-    // CU), so when all eight waves issue at once every SIMD sits idle for the
-    // queue; staggered, each SIMD's other wave keeps the matrix core busy.
+    // CU), so when all eight waves issue at once every SIMD sits idle; with
+    // the lower and upper wave halves (one of each per SIMD) at different
+    // points, each SIMD's other wave keeps the matrix core busy.  Measured
+    // per tile width (lower X, lower Y, upper X, upper Y): 192: A A C C;
+    // 256: A B B C.
+    constexpr int PXL = 0, PYL = BN == 192 ? 0 : 1, PXH = BN == 192 ? 2 : 1, PYH = 2;
+    constexpr int PERX = DmaOffs<BM, NW, KD>::PER, PERY = DmaOffs<BN, NW, KD>::PER;
     const bool lo_ = w < NW / 2;  // (wave-uniform)
+#define PIPE_ISSUE_AT(PT, SXB, SYB, KT)                                                    \
+    do {                                                                                   \
+        if (PXL == (PT) || PYL == (PT))                                                    \
+            if (lo_) PIPE_ISSUE_P(SXB, SYB, KT, PXL == (PT), PYL == (PT));                 \
+        if (PXH == (PT) || PYH == (PT))                                                    \
+            if (!lo_) PIPE_ISSUE_P(SXB, SYB, KT, PXH == (PT), PYH == (PT));                \
+    } while (0)
     PIPE_ISSUE(sX0, sY0, 0 - pad);
-    if (lo_) {
-        PIPE_ISSUE(sX1, sY1, 1 - pad);
-        TA_WAIT_VMCNT(LPS);
-    } else {
-        TA_WAIT_VMCNT(0);
-    }
+    PIPE_ISSUE_AT(0, sX1, sY1, 1 - pad);
+    // stage 0 has landed: only point-A shares of stage 1 may be in flight
+    if (lo_)
+        TA_WAIT_VMCNT((PXL == 0 ? PERX : 0) + (PYL == 0 ? PERY : 0));
+    else
+        TA_WAIT_VMCNT((PXH == 0 ? PERX : 0) + (PYH == 0 ? PERY : 0));
     __builtin_amdgcn_s_barrier();
     pipe_frags<TM, TN, WTM, WTN, KD>(f0, sX0, sY0, wm, wn, lane, 0);
 #define PIPE_STEP(J, SXJ, SYJ, SXN, SYN)                                                   \
@@ -1195,16 +1209,17 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
         pipe_frags<TM, TN, WTM, WTN, KD>(f1, SXJ, SYJ, wm, wn, lane, 1);                   \
         pipe_mma<TM, TN>(acc, f0);                                                         \
         pipe_interleave<TM * TN, TM + TN>();                                               \
-        if (!lo_) PIPE_ISSUE(SXN, SYN, kt0 + (J) + 1);                                     \
+        PIPE_ISSUE_AT(1, SXN, SYN, kt0 + (J) + 1);                                         \
         pipe_frags<TM, TN, WTM, WTN, KD>(f0, SXJ, SYJ, wm, wn, lane, 2);                   \
         pipe_mma<TM, TN>(acc, f1);                                                         \
         pipe_interleave<TM * TN, TM + TN>();                                               \
+        PIPE_ISSUE_AT(2, SXN, SYN, kt0 + (J) + 1);                                         \
         pipe_frags<TM, TN, WTM, WTN, KD>(f1, SXJ, SYJ, wm, wn, lane, 3);                   \
         pipe_mma<TM, TN>(acc, f0);                                                         \
         pipe_interleave<TM * TN, TM + TN>();                                               \
         __builtin_amdgcn_s_waitcnt(0x0070); /* vmcnt(0) lgkmcnt(0) */                      \
         __builtin_amdgcn_s_barrier();                                                      \
-        if (lo_) PIPE_ISSUE(SXJ, SYJ, kt0 + (J) + 2);                                      \
+        PIPE_ISSUE_AT(0, SXJ, SYJ, kt0 + (J) + 2);                                         \
         pipe_frags<TM, TN, WTM, WTN, KD>(f0, SXN, SYN, wm, wn, lane, 0);                   \
         pipe_mma<TM, TN>(acc, f1);                                                         \
         pipe_interleave<TM * TN, TM + TN>();                                               \
@@ -1215,10 +1230,12 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
         PIPE_ROUND(kt0 + 1);
     }
 #undef PIPE_STEP
+#undef PIPE_ISSUE_AT
     }
     TA_WAIT_VMCNT(0);  // the surplus loads have landed before the buffers are reused
 #undef PIPE_ROUND
 #undef PIPE_ISSUE
+#undef PIPE_ISSUE_P
     __syncthreads();
     // each wave stages its 64-row halves in LDS of its own: the 4-wave
     // layouts use one X and one Y stage buffer per wave, the 8-wave layouts
