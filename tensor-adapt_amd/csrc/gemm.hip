@@ -523,6 +523,10 @@ __device__ __forceinline__ void dma_stage(const bf16* __restrict__ P, int64_t ld
     constexpr int LPR = KD / 8, RPI = 64 / LPR;  // lanes per row, rows per instruction
     constexpr int NI = ROWS / RPI;
     constexpr int PER = (NI + NW - 1) / NW;
+    // a wave-uniform base (the tile's first row at k0) plus a 32-bit byte
+    // offset per lane: the scalar-base address form (row0 < rows; the
+    // hosts check that ROWS rows of an operand span less than 4 GB)
+    const char* bs = (const char*)(P + (int64_t)row0 * ld + k0);
 #pragma unroll
     for (int h = 0; h < PER; h++) {
         int j = w + NW * h;
@@ -530,22 +534,23 @@ __device__ __forceinline__ void dma_stage(const bf16* __restrict__ P, int64_t ld
         int r = RPI * j + lane / LPR;
         int c = (lane % LPR) ^ stage_swz<KD>(r);
         int grow = min(row0 + r, rows - 1);
-        const bf16* src = P + (int64_t)grow * ld + k0 + 8 * c;
-        __builtin_amdgcn_global_load_lds((const void*)src, (lds_ptr_t)(stage + RPI * j * KD), 16, 0,
-                                         0);
+        const uint32_t off = (uint32_t)((int64_t)(grow - row0) * ld * 2) + 16u * (uint32_t)c;
+        __builtin_amdgcn_global_load_lds((const void*)(bs + off), (lds_ptr_t)(stage + RPI * j * KD),
+                                         16, 0, 0);
     }
 }
 
 // dma_stage split in two for operands whose base and row stride change
 // during the loop (the K segments of a chain): dma_offsets computes, once,
-// this lane's element offset (clamped row x ld + swizzled chunk) for each of
-// the wave's PER instructions; dma_stage_at issues them for one stage from a
-// base pointer and k0.  Same addresses as dma_stage.
+// this lane's byte offset from the tile's first row (clamped row x ld +
+// swizzled chunk) for each of the wave's PER instructions; dma_stage_at
+// issues them for one stage from the wave-uniform address of the tile's
+// first row at k0.  Same addresses as dma_stage.
 template <int ROWS, int NW, int KD = DBK>
 struct DmaOffs {
     static constexpr int LPR = KD / 8, RPI = 64 / LPR;
     static constexpr int NI = ROWS / RPI, PER = (NI + NW - 1) / NW;
-    int o[PER];
+    uint32_t o[PER];
 };
 template <int ROWS, int NW, int KD>
 __device__ __forceinline__ void dma_offsets(DmaOffs<ROWS, NW, KD>& d, int64_t ld, int row0,
@@ -557,19 +562,18 @@ __device__ __forceinline__ void dma_offsets(DmaOffs<ROWS, NW, KD>& d, int64_t ld
         j = j < D::NI ? j : j - NW;
         const int r = D::RPI * j + lane / D::LPR;
         const int c = (lane % D::LPR) ^ stage_swz<KD>(r);
-        d.o[h] = (int)((int64_t)min(row0 + r, rows - 1) * ld) + 8 * c;
+        d.o[h] = (uint32_t)((int64_t)(min(row0 + r, rows - 1) - row0) * ld * 2) + 16u * (uint32_t)c;
     }
 }
 template <int ROWS, int NW, int KD>
-__device__ __forceinline__ void dma_stage_at(const bf16* __restrict__ P,
-                                             const DmaOffs<ROWS, NW, KD>& d, int k0, bf16* stage,
-                                             int w) {
+__device__ __forceinline__ void dma_stage_at(const bf16* __restrict__ base,
+                                             const DmaOffs<ROWS, NW, KD>& d, bf16* stage, int w) {
     using D = DmaOffs<ROWS, NW, KD>;
 #pragma unroll
     for (int h = 0; h < D::PER; h++) {
         int j = w + NW * h;
         j = j < D::NI ? j : j - NW;
-        __builtin_amdgcn_global_load_lds((const void*)(P + d.o[h] + k0),
+        __builtin_amdgcn_global_load_lds((const void*)((const char*)base + d.o[h]),
                                          (lds_ptr_t)(stage + D::RPI * j * KD), 16, 0, 0);
     }
 }
@@ -1094,6 +1098,13 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
         dma_offsets<BM, NW>(ox2, a.nseg > 2 ? a.sldx[2] : 0, m0, a.M, w, lane);
         dma_offsets<BN, NW>(oy2, a.nseg > 2 ? a.sldy[2] : 0, n0, a.N, w, lane);
     }
+    // each segment's operands at the tile's first row (wave-uniform)
+    const bf16* xt0 = CHAIN ? a.sX[0] + (int64_t)m0 * a.sldx[0] : nullptr;
+    const bf16* xt1 = CHAIN ? a.sX[1] + (int64_t)m0 * a.sldx[1] : nullptr;
+    const bf16* xt2 = CHAIN && a.nseg > 2 ? a.sX[2] + (int64_t)m0 * a.sldx[2] : nullptr;
+    const bf16* yt0 = CHAIN ? a.sY[0] + (int64_t)n0 * a.sldy[0] : nullptr;
+    const bf16* yt1 = CHAIN ? a.sY[1] + (int64_t)n0 * a.sldy[1] : nullptr;
+    const bf16* yt2 = CHAIN && a.nseg > 2 ? a.sY[2] + (int64_t)n0 * a.sldy[2] : nullptr;
 #define PIPE_ISSUE_P(SXB, SYB, KT, DOX, DOY)                                                        \
     do {                                                                                   \
         const int kq_ = (KT);                                                              \
@@ -1105,16 +1116,16 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
         if constexpr (CHAIN) {                                                             \
             /* the segment's precomputed row offsets: no per-stage multiply */             \
             const int s_ = (a.nseg > 2 && k_ >= a.kseg[2]) ? 2 : k_ >= a.kseg[1] ? 1 : 0;  \
-            x_ = s_ == 2 ? a.sX[2] : s_ == 1 ? a.sX[1] : a.sX[0];                          \
-            y_ = s_ == 2 ? a.sY[2] : s_ == 1 ? a.sY[1] : a.sY[0];                          \
+            x_ = s_ == 2 ? xt2 : s_ == 1 ? xt1 : xt0;                                      \
+            y_ = s_ == 2 ? yt2 : s_ == 1 ? yt1 : yt0;                                      \
             k_ -= s_ == 2 ? a.kseg[2] : s_ == 1 ? a.kseg[1] : 0;                           \
             if (z_) {                                                                      \
                 if (DOX) dma_stage<BM, NW, KD>(g_dma_zero, 0, m0, a.M, 0, SXB, w, lane);            \
                 if (DOY) dma_stage<BN, NW, KD>(g_dma_zero, 0, n0, a.N, 0, SYB, w, lane);            \
             } else {                                                                       \
-                if (DOX) dma_stage_at<BM, NW, KD>(x_, s_ == 2 ? ox2 : s_ == 1 ? ox1 : ox0, k_, SXB, \
+                if (DOX) dma_stage_at<BM, NW, KD>(x_ + k_, s_ == 2 ? ox2 : s_ == 1 ? ox1 : ox0, SXB, \
                                          w);                                               \
-                if (DOY) dma_stage_at<BN, NW, KD>(y_, s_ == 2 ? oy2 : s_ == 1 ? oy1 : oy0, k_, SYB, \
+                if (DOY) dma_stage_at<BN, NW, KD>(y_ + k_, s_ == 2 ? oy2 : s_ == 1 ? oy1 : oy0, SYB, \
                                          w);                                               \
             }                                                                              \
         } else {                                                                           \
@@ -1412,6 +1423,9 @@ static void launch_cfg(bool xk, bool yk, const GemmArgs& a, int splits, bool vx,
 }
 
 static inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+// row stride limit of the direct-to-LDS kernels: 256 rows of an operand
+// must span less than 4 GB (32-bit byte offsets from the tile's first row)
+constexpr int64_t kMaxStageLd = int64_t(1) << 23;
 
 // Shape-driven dispatch.  out_f32: C is F32 (gemm_f32 semantics).  lora
 // (may be NULL): rank-r terms applied to C after the base epilogue, fused
@@ -1458,7 +1472,9 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
     bool vy = al16(Y) && (ldy % 8) == 0;
 
     // large K-contiguous BF16 GEMMs: k_gemm_pipe (k_gemm_dma for split-K)
-    if (xk && yk && !out_f32 && M >= 1024 && N >= 1024 && (K % BK) == 0 && vx && vy) {
+    // (the stage loads address 256 operand rows with 32-bit byte offsets)
+    if (xk && yk && !out_f32 && M >= 1024 && N >= 1024 && (K % BK) == 0 && vx && vy &&
+        ldx < kMaxStageLd && ldy < kMaxStageLd) {
         int variant = g_big_variant;
         if (variant == 0) variant = N > 3072 ? 18 : 17;
         const int BNb = big_bn(variant);
@@ -1630,8 +1646,8 @@ int gemm_chain(int M, int N, const GemmSeg* sg, int ns, bf16* C, int64_t ldc, co
         Ktot += sg[q].K;
         ok &= sg[q].K % BK == 0 && al16(sg[q].X) && al16(sg[q].Y) && sg[q].ldx % 8 == 0 &&
               sg[q].ldy % 8 == 0;
-        // the kernel keeps each segment's row offsets as 32-bit element counts
-        ok &= (int64_t)M * sg[q].ldx < INT32_MAX && (int64_t)N * sg[q].ldy < INT32_MAX;
+        // the kernel keeps each segment's row offsets as 32-bit byte counts
+        ok &= sg[q].ldx < kMaxStageLd && sg[q].ldy < kMaxStageLd;
     }
     const int tiles = ((M + 255) / 256) * ((N + BNb - 1) / BNb);
     // (as gemm_dispatch: few tiles and a long K go to split-K instead)
@@ -1752,6 +1768,7 @@ int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const Gem
     const bool vx = al16(X) && (ldx % 8) == 0;
     // (as gemm_dispatch: few tiles and a long K go to split-K instead)
     if (!(ng > 1 && is_pipe(variant) && tiles_ok && lora_ok && vx && vy && M >= 1024 &&
+          ldx < kMaxStageLd && ldy < kMaxStageLd &&
           Ntot >= 1024 && (K % BK) == 0 && (tiles >= 192 || K / BK < 32))) {
         for (int g = 0; g < ng; g++) {
             int rc = gemm_dispatch(true, true, M, gr[g].N, K, 1.f, X, ldx, gr[g].Y, ldy, 0.f,
@@ -1851,6 +1868,7 @@ int gemm_swiglu(int M, int K, const bf16* X, int64_t ldx, const bf16* Wgu, const
                     (g_big_variant == 0 || g_big_variant == 16 || g_big_variant == 18) && M >= 1024 &&
                     I % 128 == 0 && 2 * I >= 1024 && K % BK == 0 && al16(X) && ldx % 8 == 0 &&
                     al16(Wgu) && al16(gate) && al16(up) && al16(act) && I % 8 == 0 &&
+                    ldx < kMaxStageLd && K < kMaxStageLd &&
                     (tiles >= 192 || K / BK < 32);
     if (!ok) {
         const GemmGroup gr[2] = {{I, Wg, gate, I, nullptr, lg}, {I, Wu, up, I, nullptr, lu}};
