@@ -1199,12 +1199,16 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
     constexpr int PXL = 0, PYL = BN == 192 ? 0 : 1, PXH = BN == 192 ? 2 : 1, PYH = 2;
     constexpr int PERX = DmaOffs<BM, NW, KD>::PER, PERY = DmaOffs<BN, NW, KD>::PER;
     const bool lo_ = w < NW / 2;  // (wave-uniform)
+    // (stages past the last are not loaded: every step's wait is for all
+    // loads in flight, so the counts need not be static)
 #define PIPE_ISSUE_AT(PT, SXB, SYB, KT)                                                    \
     do {                                                                                   \
-        if (PXL == (PT) || PYL == (PT))                                                    \
-            if (lo_) PIPE_ISSUE_P(SXB, SYB, KT, PXL == (PT), PYL == (PT));                 \
-        if (PXH == (PT) || PYH == (PT))                                                    \
-            if (!lo_) PIPE_ISSUE_P(SXB, SYB, KT, PXH == (PT), PYH == (PT));                \
+        if ((KT) < nk) {                                                                   \
+            if (PXL == (PT) || PYL == (PT))                                                \
+                if (lo_) PIPE_ISSUE_P(SXB, SYB, KT, PXL == (PT), PYL == (PT));             \
+            if (PXH == (PT) || PYH == (PT))                                                \
+                if (!lo_) PIPE_ISSUE_P(SXB, SYB, KT, PXH == (PT), PYH == (PT));            \
+        }                                                                                  \
     } while (0)
     PIPE_ISSUE(sX0, sY0, 0 - pad);
     PIPE_ISSUE_AT(0, sX1, sY1, 1 - pad);
