@@ -67,7 +67,7 @@ struct GemmArgs {
     // tile columns [tn0[g], tn0[g + 1]) compute group g's own GEMM over the
     // same X: gN[g] output columns of gY[g], written to gC[g] (row stride
     // gldc[g]) with bias gbias[g] and, when glora[g], the LoRA pair gu/gv[g]
-    // (rank 16, lora_delta and lora_s shared).  The fields above describe
+    // (rank lora_r <= 64, lora_delta and lora_s shared).  The fields above describe
     // group 0 only as far as they are shared (M, K, X, ldy, alpha, beta).
     int ngroups;
     int tn0[3];
@@ -788,8 +788,9 @@ __device__ __forceinline__ int stg_off(int row, int col) {
 // Epilogue of one 64-row half (row fragments I0, I0 + 1) of a wave tile,
 // staged in the wave's private LDS region wb (64 x WTN BF16, stg_off
 // layout).  Same arithmetic as big_epilogue, fragment by fragment: alpha acc
-// + beta C (+ bias) rounded, then each LoRA term (rank <= 16: one MFMA k
-// step, its operand fragments loaded up front), then the BF16 values into
+// + beta C (+ bias) rounded, then each LoRA term (one MFMA k step per 16
+// of rank, up to 64; the first step's operand fragments loaded up front,
+// the others' from global memory), then the BF16 values into
 // wb, four columns per 8-byte write; the half leaves as 16-byte row vectors.
 // A lane reads and writes the same wb words for a fragment, so only the
 // final read-back needs the wave barrier.
@@ -919,6 +920,22 @@ __device__ __attribute__((always_inline)) inline void pipe_half_epilogue(
                 }
                 // transposed like the accumulators: V rows as the A operand
                 d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vb, ua, d, 0, 0, 0);
+                // ranks above 16: one more k step per 16, operand rows from
+                // global memory (rank k0 + kk .. + 7 of the lane's row/column)
+                for (int k0 = 16; k0 < a.lora_r; k0 += 16) {
+                    const int row = min(R0 + 32 * i + (lane & 31), a.M - 1);
+                    const int col = min(C0 + 32 * j + (lane & 31), a.N - 1);
+                    const bool kin2 = k0 + kk < a.lora_r;
+                    bf16x8_t u2 = *(const bf16x8_t*)(a.lora_u[p] + (int64_t)row * a.lora_ldu[p] +
+                                                     (kin2 ? k0 + kk : 0));
+                    bf16x8_t v2 = *(const bf16x8_t*)(a.lora_v[p] + (int64_t)col * a.lora_r +
+                                                     (kin2 ? k0 + kk : 0));
+                    if (!kin2) {
+#pragma unroll
+                        for (int e = 0; e < 8; e++) u2[e] = v2[e] = (__bf16)0.f;
+                    }
+                    d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v2, u2, d, 0, 0, 0);
+                }
 #pragma unroll
                 for (int r = 0; r < 16; r++)
                     v[r] = a.lora_delta ? bf2f(f2bf(v[r] + a.lora_s * bf2f(f2bf(d[r]))))
@@ -1287,6 +1304,9 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
         GemmArgs ae = a;
         ae.N = a0.gN[0];
         ae.ldc = a0.gldc[0];
+        // (ranks other than 16 read the wave's pair from global memory)
+        ae.lora_u[0] = upw ? a0.gu[1] : a0.gu[0];
+        ae.lora_v[0] = upw ? a0.gv[1] : a0.gv[0];
         bf16* Cw = (bf16*)(upw ? a0.gC[1] : a0.gC[0]);
         const int cg = 128 * tn_i + 64 * (wn & 1);
         const bf16* luw = lu ? lu + (upw ? BM * 16 : 0) : nullptr;
@@ -1509,10 +1529,10 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
             int rc = check_launch("gemm");
             return rc ? rc : lora_after();
         }
-        // LoRA terms fuse into the epilogue up to rank 16 for k_gemm_pipe (one
-        // MFMA k step) and at any rank for k_gemm_dma; otherwise they run
-        // after the GEMM
-        const bool fuse = lora && lora->n > 0 && (!is_pipe(variant) || lora->r <= 16);
+        // LoRA terms fuse into the epilogue up to rank 64 for k_gemm_pipe (one
+        // MFMA k step per 16) and at any rank for k_gemm_dma; otherwise they
+        // run after the GEMM
+        const bool fuse = lora && lora->n > 0 && (!is_pipe(variant) || lora->r <= 64);
         if (fuse) {
             a.lora_n = lora->n;
             a.lora_r = lora->r;
@@ -1666,7 +1686,7 @@ int gemm_chain(int M, int N, const GemmSeg* sg, int ns, bf16* C, int64_t ldc, co
             ok &= (kb / KD + pad) % NS == 0;
         }
     }
-    ok &= !lora || lora->n == 0 || lora->r <= 16;
+    ok &= !lora || lora->n == 0 || lora->r <= 64;
     if (!ok) {
         for (int q = 0; q < ns; q++) {
             int rc = gemm_dispatch(true, true, M, N, sg[q].K, 1.f, sg[q].X, sg[q].ldx, sg[q].Y,
@@ -1739,8 +1759,8 @@ int gemm_chain(int M, int N, const GemmSeg* sg, int ns, bf16* C, int64_t ldc, co
 }
 
 // Up to three GEMMs over the same X [M x K], C_g = bf16(X Y_g^T (+ bias_g))
-// plus the LoRA delta of group g's pair (none, or one rank-16 pair; delta
-// kind and scale shared), as ONE k_gemm_pipe launch over the N-concatenated
+// plus the LoRA delta of group g's pair (none, or one pair of rank <= 64;
+// rank, delta kind and scale shared), as ONE k_gemm_pipe launch over the N-concatenated
 // tile grid: q/k/v or gate/up projections.  Separate launches would each
 // end on a partly filled wave of tiles, and the narrow k/v projections
 // would run on the small-GEMM path; every output keeps its own epilogue, so
@@ -1759,7 +1779,8 @@ int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const Gem
         vy &= al16(gr[g].Y);
         const LoraEpi* l = gr[g].lora;
         if (l && l->n > 0) {
-            lora_ok &= l->n == 1 && l->r == 16;
+            lora_ok &= l->n == 1 && l->r <= 64 && l->ldu[0] == l->r;
+            if (l0) lora_ok &= l->r == l0->r;
             if (l0) lora_ok &= l->delta == l0->delta && l->s == l0->s;
             else l0 = l;
         }
@@ -1798,7 +1819,7 @@ int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const Gem
     a.tiles_m = (M + 255) / 256;
     a.tiles_n = Ntot / BNb;
     a.ngroups = ng;
-    a.lora_r = l0 ? 16 : 0;
+    a.lora_r = l0 ? l0->r : 0;
     a.lora_delta = l0 && l0->delta ? 1 : 0;
     a.lora_s = l0 ? l0->s : 0.f;
     int tn = 0;
@@ -1815,10 +1836,7 @@ int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const Gem
         a.glora[g] = on ? 1 : 0;
         a.gu[g] = on ? l->u[0] : nullptr;
         a.gv[g] = on ? l->v_nk[0] : nullptr;
-        if (on) {
-            TA_REQUIRE(l->ldu[0] == 16, "gemm_groups: LoRA U rows must hold rank 16");
-            a.lora_ldu[0] = 16;
-        }
+        if (on) a.lora_ldu[0] = l->r;
     }
     a.lora_n = a.glora[0];
     a.lora_u[0] = a.gu[0];
@@ -1844,8 +1862,8 @@ int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const Gem
         double mn = (double)M * Ntot, fl = 2.0 * mn * K, by = 2.0 * ((double)M * K + (double)Ntot * K + mn);
         for (int g = 0; g < ng; g++)
             if (a.glora[g]) {
-                fl += 2.0 * M * gr[g].N * 16;
-                by += 2.0 * (double)(M + gr[g].N) * 16;
+                fl += 2.0 * M * gr[g].N * a.lora_r;
+                by += 2.0 * (double)(M + gr[g].N) * a.lora_r;
             }
         kprof_end(kid, s, fl, by, big_name(variant));
     }
@@ -1857,15 +1875,15 @@ int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const Gem
 // over Wgu, the gate/up weights interleaved in blocks of 128 rows
 // ([Wg rows 0..127; Wu rows 0..127; Wg rows 128..255; ...], [2I x K]): the
 // act pass reads the BF16 gate/up tiles from LDS instead of HBM.  The
-// LoRA pairs are both on (rank 16) or both off.  Other shapes run as the
+// LoRA pairs are both on (one rank <= 64) or both off.  Other shapes run as the
 // grouped launch plus silu_mul_fwd.
 int gemm_swiglu(int M, int K, const bf16* X, int64_t ldx, const bf16* Wgu, const bf16* Wg,
                 const bf16* Wu, bf16* gate, bf16* up, bf16* act, int I, const LoraEpi* lg,
                 const LoraEpi* lu, hipStream_t s) {
     const bool on = lg && lg->n > 0;
-    const bool lora_ok = on ? (lu && lu->n == 1 && lg->n == 1 && lg->r == 16 && lu->r == 16 &&
-                               lg->delta == lu->delta && lg->s == lu->s && lg->ldu[0] == 16 &&
-                               lu->ldu[0] == 16)
+    const bool lora_ok = on ? (lu && lu->n == 1 && lg->n == 1 && lg->r <= 64 && lu->r == lg->r &&
+                               lg->delta == lu->delta && lg->s == lu->s &&
+                               lg->ldu[0] == lg->r && lu->ldu[0] == lu->r)
                             : !(lu && lu->n > 0);
     const int tiles = ((M + 255) / 256) * (2 * I / 256);
     const bool ok = Wgu && lora_ok &&
@@ -1903,10 +1921,10 @@ int gemm_swiglu(int M, int K, const bf16* X, int64_t ldx, const bf16* Wgu, const
     a.gC[2] = act;
     if (on) {
         a.lora_n = 1;
-        a.lora_r = 16;
+        a.lora_r = lg->r;
         a.lora_delta = lg->delta ? 1 : 0;
         a.lora_s = lg->s;
-        a.lora_ldu[0] = 16;
+        a.lora_ldu[0] = lg->r;
         a.gu[0] = lg->u[0];
         a.gu[1] = lu->u[0];
         a.gv[0] = lg->v_nk[0];
@@ -1921,9 +1939,9 @@ int gemm_swiglu(int M, int K, const bf16* X, int64_t ldx, const bf16* Wgu, const
     if (timed) {
         // X and both weights read once; gate, up and act written once
         const double mn = 2.0 * M * I;
-        const double fl = 2.0 * mn * K + (on ? 2.0 * mn * 16 : 0.0);
+        const double fl = 2.0 * mn * K + (on ? 2.0 * mn * a.lora_r : 0.0);
         const double by = 2.0 * ((double)M * K + 2.0 * I * (double)K + 1.5 * mn) +
-                          (on ? 2.0 * 2.0 * (M + I) * 16 : 0.0);
+                          (on ? 2.0 * 2.0 * (M + I) * a.lora_r : 0.0);
         kprof_end(KP_GEMM_SWIGLU, s, fl, by,
                   kd64 ? "void ta::k_gemm_pipe_swiglu<256, 2, 4, 64>(ta::GemmArgs)"
                        : "void ta::k_gemm_pipe_swiglu<256, 2, 4>(ta::GemmArgs)");
