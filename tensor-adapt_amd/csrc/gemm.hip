@@ -510,6 +510,30 @@ __device__ __forceinline__ int stage_swz(int R) {
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
+// One direct-to-LDS load, global_load_lds_dwordx4 in its scalar-base form
+// (wave-uniform 64-bit base, 32-bit byte offset per lane; lane i writes LDS
+// bytes lds + 16 i .. + 15), issued from inline assembly: the compiler does
+// not see it as a write to LDS, so it does not make the next LDS read wait
+// for every load in flight (it cannot tell the stage buffers apart and
+// would).  The kernels order these loads with explicit vmcnt waits and
+// barriers.
+__device__ __forceinline__ void dma16(const void* base, uint32_t off, const void* lds) {
+    const uint32_t la = (uint32_t)(uintptr_t)lds;
+    const uint64_t ba = (uint64_t)(uintptr_t)base;
+    // (readfirstlane returns int: each half goes through uint32_t so that the
+    // low word is not sign-extended into the high one)
+    const uint64_t bu =
+        (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)ba) |
+        ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(ba >> 32)) << 32);
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+                 :
+                 : "s"(__builtin_amdgcn_readfirstlane(la)), "v"(off), "s"(bu)
+                 : "memory", "m0");
+#pragma clang diagnostic pop
+}
+
 // Issue this wave's share of the loads of one stage: operand rows
 // [row0, row0 + ROWS) (clamped to rows - 1), k range [k0, k0 + 32).
 // Wave-instruction j covers stage rows 16j..16j+15.  Every one of the NW
@@ -535,8 +559,7 @@ __device__ __forceinline__ void dma_stage(const bf16* __restrict__ P, int64_t ld
         int c = (lane % LPR) ^ stage_swz<KD>(r);
         int grow = min(row0 + r, rows - 1);
         const uint32_t off = (uint32_t)((int64_t)(grow - row0) * ld * 2) + 16u * (uint32_t)c;
-        __builtin_amdgcn_global_load_lds((const void*)(bs + off), (lds_ptr_t)(stage + RPI * j * KD),
-                                         16, 0, 0);
+        dma16(bs, off, stage + RPI * j * KD);
     }
 }
 
@@ -573,8 +596,7 @@ __device__ __forceinline__ void dma_stage_at(const bf16* __restrict__ base,
     for (int h = 0; h < D::PER; h++) {
         int j = w + NW * h;
         j = j < D::NI ? j : j - NW;
-        __builtin_amdgcn_global_load_lds((const void*)((const char*)base + d.o[h]),
-                                         (lds_ptr_t)(stage + D::RPI * j * KD), 16, 0, 0);
+        dma16(base, d.o[h], stage + D::RPI * j * KD);
     }
 }
 
@@ -1203,37 +1225,17 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
     // buffer for stage J + 2 (waited for: the DMA must not overwrite them),
     // after which the next stage's first fragments are read while k step 3
     // computes.  The only loads in flight at a step's wait are stage J + 1's.
-    // The waves issue their shares of a stage's X and Y rows at three
-    // points: A, right after the barrier that frees the buffer (for stage
-    // J + 2), and B / C, after the first / second k step of the next step
-    // (for its stage + 1).  A wave cannot issue while its direct-to-LDS loads
-    // queue for the address unit (about 25 cycles per 1 KB instruction per
-    // CU), so when all eight waves issue at once every SIMD sits idle; with
-    // the lower and upper wave halves (one of each per SIMD) at different
-    // points, each SIMD's other wave keeps the matrix core busy.  Measured
-    // per tile width (lower X, lower Y, upper X, upper Y): 192: A A C C;
-    // 256: A B B C.
-    constexpr int PXL = 0, PYL = BN == 192 ? 0 : 1, PXH = BN == 192 ? 2 : 1, PYH = 2;
-    constexpr int PERX = DmaOffs<BM, NW, KD>::PER, PERY = DmaOffs<BN, NW, KD>::PER;
-    const bool lo_ = w < NW / 2;  // (wave-uniform)
-    // (stages past the last are not loaded: every step's wait is for all
-    // loads in flight, so the counts need not be static)
-#define PIPE_ISSUE_AT(PT, SXB, SYB, KT)                                                    \
-    do {                                                                                   \
-        if ((KT) < nk) {                                                                   \
-            if (PXL == (PT) || PYL == (PT))                                                \
-                if (lo_) PIPE_ISSUE_P(SXB, SYB, KT, PXL == (PT), PYL == (PT));             \
-            if (PXH == (PT) || PYH == (PT))                                                \
-                if (!lo_) PIPE_ISSUE_P(SXB, SYB, KT, PXH == (PT), PYH == (PT));            \
-        }                                                                                  \
-    } while (0)
+    // Every wave issues its share of stage J + 2 right after the barrier
+    // that frees the buffer (stages past the last are not loaded; every
+    // step's wait is for all loads in flight).  With the loads issued from
+    // inline assembly (dma16) nothing else waits for them, so the wave goes
+    // on to its MFMAs while the address unit works through the stage; with
+    // the compiler's own form every LDS read after an issue waited for all
+    // loads in flight, and staggering the issue across the wave halves was
+    // needed to keep the matrix cores busy (4% slower per c3 step than this).
     PIPE_ISSUE(sX0, sY0, 0 - pad);
-    PIPE_ISSUE_AT(0, sX1, sY1, 1 - pad);
-    // stage 0 has landed: only point-A shares of stage 1 may be in flight
-    if (lo_)
-        TA_WAIT_VMCNT((PXL == 0 ? PERX : 0) + (PYL == 0 ? PERY : 0));
-    else
-        TA_WAIT_VMCNT((PXH == 0 ? PERX : 0) + (PYH == 0 ? PERY : 0));
+    PIPE_ISSUE(sX1, sY1, 1 - pad);
+    TA_WAIT_VMCNT(LPS);
     __builtin_amdgcn_s_barrier();
     pipe_frags<TM, TN, WTM, WTN, KD>(f0, sX0, sY0, wm, wn, lane, 0);
 #define PIPE_STEP(J, SXJ, SYJ, SXN, SYN)                                                   \
@@ -1241,17 +1243,15 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
         pipe_frags<TM, TN, WTM, WTN, KD>(f1, SXJ, SYJ, wm, wn, lane, 1);                   \
         pipe_mma<TM, TN>(acc, f0);                                                         \
         pipe_interleave<TM * TN, TM + TN>();                                               \
-        PIPE_ISSUE_AT(1, SXN, SYN, kt0 + (J) + 1);                                         \
         pipe_frags<TM, TN, WTM, WTN, KD>(f0, SXJ, SYJ, wm, wn, lane, 2);                   \
         pipe_mma<TM, TN>(acc, f1);                                                         \
         pipe_interleave<TM * TN, TM + TN>();                                               \
-        PIPE_ISSUE_AT(2, SXN, SYN, kt0 + (J) + 1);                                         \
         pipe_frags<TM, TN, WTM, WTN, KD>(f1, SXJ, SYJ, wm, wn, lane, 3);                   \
         pipe_mma<TM, TN>(acc, f0);                                                         \
         pipe_interleave<TM * TN, TM + TN>();                                               \
         __builtin_amdgcn_s_waitcnt(0x0070); /* vmcnt(0) lgkmcnt(0) */                      \
         __builtin_amdgcn_s_barrier();                                                      \
-        PIPE_ISSUE_AT(0, SXJ, SYJ, kt0 + (J) + 2);                                         \
+        if (kt0 + (J) + 2 < nk) PIPE_ISSUE(SXJ, SYJ, kt0 + (J) + 2);                       \
         pipe_frags<TM, TN, WTM, WTN, KD>(f0, SXN, SYN, wm, wn, lane, 0);                   \
         pipe_mma<TM, TN>(acc, f1);                                                         \
         pipe_interleave<TM * TN, TM + TN>();                                               \
@@ -1262,7 +1262,6 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
         PIPE_ROUND(kt0 + 1);
     }
 #undef PIPE_STEP
-#undef PIPE_ISSUE_AT
     }
     TA_WAIT_VMCNT(0);  // the surplus loads have landed before the buffers are reused
 #undef PIPE_ROUND
