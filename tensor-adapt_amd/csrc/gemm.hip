@@ -35,6 +35,17 @@ namespace ta {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// 16-byte output store with the non-temporal hint (global_store ... nt).
+// A GEMM's output is written once and read by a later kernel, while its
+// operand bands are re-read by many tiles through L2; the hint keeps the
+// output lines from displacing them (c3 step 1.9% faster than plain
+// stores; the values stored are the same).
+__device__ __forceinline__ void st_out16(void* p, const bf16x8v& v) {
+    const u32x4_t x = {v.w[0], v.w[1], v.w[2], v.w[3]};
+    __builtin_nontemporal_store(x, (u32x4_t*)p);
+}
 
 constexpr int BK = 64;
 constexpr int LDS_STRIDE = BK + 8;  // bf16 elements per LDS row
@@ -478,7 +489,7 @@ __device__ __attribute__((always_inline)) inline void staged_epilogue(
         if (gm >= a.M) continue;
         bf16x8v v = *(const bf16x8v*)(wb + row * WTN + 8 * ch);
         if (vec && gn + 8 <= a.N) {
-            *(bf16x8v*)(C + (int64_t)gm * a.ldc + gn) = v;
+            st_out16(C + (int64_t)gm * a.ldc + gn, v);
         } else {
 #pragma unroll
             for (int e = 0; e < 8; e++)
@@ -980,7 +991,7 @@ __device__ __attribute__((always_inline)) inline void pipe_half_epilogue(
         if (gm >= a.M) continue;
         bf16x8v v = *(const bf16x8v*)(wb + stg_off<WTN>(row, 8 * ch));
         if (vec && gn + 8 <= a.N) {
-            *(bf16x8v*)(C + (int64_t)gm * a.ldc + gn) = v;
+            st_out16(C + (int64_t)gm * a.ldc + gn, v);
         } else {
 #pragma unroll
             for (int e = 0; e < 8; e++)
@@ -1330,7 +1341,7 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
             unpack8(*(const bf16x8v*)(ust + stg_off<WTN>(row, 8 * ch)), u);
 #pragma unroll
             for (int e = 0; e < 8; e++) o[e] = silu_mul_f(g[e], u[e]);
-            *(bf16x8v*)(actp + (int64_t)(rb + row) * I + cg + 8 * ch) = pack8(o);
+            st_out16(actp + (int64_t)(rb + row) * I + cg + 8 * ch, pack8(o));
         }
     } else {
         pipe_half_epilogue<TM, TN, WTN, 0, LP>(acc, a, (bf16*)a.C, m0 + wm * WTM, n0 + wn * WTN,

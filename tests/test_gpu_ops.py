@@ -234,6 +234,37 @@ def test_gemm_rm_kmajor_tiles(M, N, K):
     check_gemm_close(host(tc), rm_ref(1, 1, M, N, K, 1.0, X, K, Y, K, 1.0, C, N), "gemm_rm")
 
 
+@pytest.mark.parametrize("M,N,K", [(2048, 1536, 1536), (1024, 3000, 320), (1280, 1100, 192),
+                                   (1024, 1024, 64)])
+def test_gemm_stage_forms_bit_identical(M, N, K):
+    """The large-GEMM kernel forms that ta_gemm_variant selects accumulate
+    the same products in the same F32 order (64-k stages as two 32-k k
+    steps each), so 17 and 18 (the default's two tile widths) equal 15 and
+    16 (their 32-k-stage forms) bit for bit, with and without the bias
+    and beta epilogues; the default (0) agrees with the oracle GEMM."""
+    X, Y, b = rbf(M, K, scale=0.5), rbf(N, K, scale=0.02), rbf(N, scale=0.1)
+    C0 = rbf(M, N)
+    tX, tY, tb = dev(X), dev(Y), dev(b)
+
+    def run(v, bias, beta):
+        tc = dev(C0)
+        call("ta_gemm_variant", v)
+        call("ta_gemm_rm", 1, 1, M, N, K, ctypes.c_float(1.0), P(tX), K, P(tY), K,
+             ctypes.c_float(beta), P(tc), N, P(bias) if bias is not None else None, S())
+        return host(tc)
+
+    try:
+        for a, c in ((15, 17), (16, 18)):
+            for bias, beta in ((None, 0.0), (tb, 0.0), (None, 1.0)):
+                ga, gc = run(a, bias, beta), run(c, bias, beta)
+                assert np.array_equal(ga, gc), \
+                    f"variant {a} vs {c} (bias={bias is not None}, beta={beta}) differ"
+        got = run(0, None, 1.0)
+    finally:
+        call("ta_gemm_variant", 0)
+    check_gemm_close(got, rm_ref(1, 1, M, N, K, 1.0, X, K, Y, K, 1.0, C0, N), "gemm default")
+
+
 def test_gemm_rm_bias_epilogue():
     M, N, K = 256, 384, 128
     X, Y, b = rbf(M, K), rbf(N, K), rbf(N)
@@ -361,7 +392,8 @@ def test_kmeans_pp_bit_exact():
 
 
 # ── attention ─────────────────────────────────────────────────────────────
-ATTN_SHAPES = [(1, 128, 14, 2, 64), (2, 256, 12, 2, 128), (1, 100, 4, 2, 64), (1, 512, 14, 2, 64)]
+ATTN_SHAPES = [(1, 128, 14, 2, 64), (2, 256, 12, 2, 128), (1, 100, 4, 2, 64), (1, 512, 14, 2, 64),
+               (1, 1024, 12, 2, 128)]
 ROWSTAT_SHAPES = [(1, 1024, 12, 2, 128), (2, 200, 14, 2, 64), (1, 100, 4, 2, 128),
                   (1, 512, 14, 2, 64), (1, 2048, 28, 4, 128)]
 
