@@ -66,7 +66,8 @@ def build(verbose=True):
     if failed:
         raise RuntimeError("HIP compilation failed")
     tmp = OUT + ".tmp"
-    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs
+    # -z defs: a symbol left undefined fails the link instead of the first load
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-Wl,-z,defs", "-o", tmp] + objs
     subprocess.check_call(cmd)
     os.replace(tmp, OUT)
     return OUT

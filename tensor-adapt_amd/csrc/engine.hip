@@ -619,10 +619,8 @@ static int layer_fwd_body(Engine* e, Layer& ly) {
               gbytes(BT, qd + 2.0 * kvd, H, 2, 2, false),
               gemm_groups(BT, H, ly.xn, H, H, gr, 3, s));
     }
-    TIMED(TA_CAT_ELEMWISE, 0, dBT * qd * 4,
-          ta_rope_fwd(ly.Q, e->B, e->T, c.n_q, c.head_dim, c.rope_theta, s));
-    TIMED(TA_CAT_ELEMWISE, 0, dBT * kvd * 4,
-          ta_rope_fwd(ly.K, e->B, e->T, c.n_kv, c.head_dim, c.rope_theta, s));
+    TIMED(TA_CAT_ELEMWISE, 0, dBT * (qd + kvd) * 4,
+          rope_qk(ly.Q, c.n_q, ly.K, c.n_kv, e->B, e->T, c.head_dim, c.rope_theta, 1.f, s));
     // sdpa_fwd (ops.cu:578-681) without the probabilities buffer: the
     // rows' (max, 1/sum) are kept instead
     TIMED(TA_CAT_ATTN_FWD, 4.0 * tri * c.head_dim,
@@ -769,10 +767,9 @@ static int backward(Engine* e) {
                   dBT * (qd + 2.0 * kvd) * 2 + dBT * qd * 4,
               attn_bwd(e->dao, ly.Q, ly.K, ly.V, nullptr, ly.attn_st, ly.ao32, e->dQ, e->dK, e->dV,
                        e->B, e->T, c.n_q, c.n_kv, c.head_dim, e->Dbuf, e->dkv_part, s));
-        TIMED(TA_CAT_ELEMWISE, 0, dBT * qd * 4,
-              ta_rope_bwd(e->dQ, e->B, e->T, c.n_q, c.head_dim, c.rope_theta, s));
-        TIMED(TA_CAT_ELEMWISE, 0, dBT * kvd * 4,
-              ta_rope_bwd(e->dK, e->B, e->T, c.n_kv, c.head_dim, c.rope_theta, s));
+        TIMED(TA_CAT_ELEMWISE, 0, dBT * (qd + kvd) * 4,
+              rope_qk(e->dQ, c.n_q, e->dK, c.n_kv, e->B, e->T, c.head_dim, c.rope_theta, -1.f,
+                      s));
         {
             const bf16* gos[3] = {e->dQ, e->dK, e->dV};
             LoraEpi ep;

@@ -271,10 +271,10 @@ __global__ void k_rope_table(float2* __restrict__ tab, int T, int hd, float thet
     sincosf(angle, &sn, &cs);
     tab[gid] = make_float2(cs, sn);
 }
-__global__ __launch_bounds__(256) void k_rope_tab(bf16* __restrict__ x, int64_t rows, int T,
-                                                  int H, int hd, const float4* __restrict__ tab) {
+// chunk gid of x ([rows, H * hd]): 16 bytes of one head of one row
+__device__ __forceinline__ void rope_chunk(bf16* __restrict__ x, int64_t gid, int64_t rows, int T,
+                                           int H, int hd, const float4* __restrict__ tab) {
     const int qpr = hd >> 3;  // 16-byte chunks per head (4 pairs each)
-    int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
     int64_t row = gid / (H * qpr);
     int hq = (int)(gid % (H * qpr)), q = hq % qpr;
     if (row >= rows) return;
@@ -292,6 +292,20 @@ __global__ __launch_bounds__(256) void k_rope_tab(bf16* __restrict__ x, int64_t 
         o[2 * e + 1] = f[2 * e] * sn[e] + f[2 * e + 1] * cs[e];
     }
     *p = pack8(o);
+}
+__global__ __launch_bounds__(256) void k_rope_tab(bf16* __restrict__ x, int64_t rows, int T,
+                                                  int H, int hd, const float4* __restrict__ tab) {
+    rope_chunk(x, blockIdx.x * (int64_t)blockDim.x + threadIdx.x, rows, T, H, hd, tab);
+}
+// Q and K of a layer in one launch: chunks [0, n0) of the grid rotate x0
+// (H0 heads), the rest x1 (H1 heads); K alone is too small to fill the chip
+__global__ __launch_bounds__(256) void k_rope_tab2(bf16* __restrict__ x0, int H0,
+                                                   bf16* __restrict__ x1, int H1, int64_t rows,
+                                                   int T, int hd, int64_t n0,
+                                                   const float4* __restrict__ tab) {
+    const int64_t gid = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (gid < n0) rope_chunk(x0, gid, rows, T, H0, hd, tab);
+    else rope_chunk(x1, gid - n0, rows, T, H1, hd, tab);
 }
 
 // Tables live for the process, one per (device, T, hd, theta, sign), built on
@@ -444,6 +458,30 @@ static int rope(uint16_t* x, int B, int T, int H, int hd, float theta, float sig
     }
     return check_launch("rope");
 }
+
+}  // extern "C"
+
+namespace ta {
+// rope of Q (Hq heads) and K (Hk heads) of one layer, one launch when
+// both take the table path (the same bits as two rope calls)
+int rope_qk(bf16* q, int Hq, bf16* k, int Hk, int B, int T, int hd, float theta, float sign,
+            hipStream_t s) {
+    if (B <= 0 || T <= 0 || Hq <= 0 || Hk <= 0 || hd <= 0 || (hd & 7) != 0 || !al16(q) ||
+        !al16(k)) {
+        if (int rc = rope(q, B, T, Hq, hd, theta, sign, s)) return rc;
+        return rope(k, B, T, Hk, hd, theta, sign, s);
+    }
+    const int64_t rows = (int64_t)B * T;
+    const float2* tab = rope_table(T, hd, theta, sign, s);
+    TA_REQUIRE(tab, "rope: table allocation failed");
+    const int64_t n0 = rows * Hq * (hd >> 3), n = n0 + rows * Hk * (hd >> 3);
+    k_rope_tab2<<<(int)((n + 255) / 256), 256, 0, s>>>(q, Hq, k, Hk, rows, T, hd, n0,
+                                                       (const float4*)tab);
+    return check_launch("rope_qk");
+}
+}  // namespace ta
+
+extern "C" {
 
 int ta_rope_fwd(uint16_t* x, int B, int T, int H, int head_dim, float theta, void* stream) {
     return rope(x, B, T, H, head_dim, theta, 1.f, stream);

@@ -87,6 +87,10 @@ struct GemmSeg {
 // one launch over the concatenated K (rounded to BF16 between the GEMMs)
 int gemm_chain(int M, int N, const GemmSeg* sg, int ns, bf16* C, int64_t ldc, const LoraEpi* lora,
                hipStream_t s);
+// RoPE of a layer's Q ([BT, Hq * hd]) and K ([BT, Hk * hd]) in one launch
+// (sign +1 forward, -1 the inverse rotation of the backward)
+int rope_qk(bf16* q, int Hq, bf16* k, int Hk, int B, int T, int hd, float theta, float sign,
+            hipStream_t s);
 // gate/up projections (+ LoRA deltas) and act = silu(gate) up in one launch
 // over Wgu, the gate/up weights interleaved in 128-row blocks ([2I x K]);
 // falls back to gemm_groups + silu_mul_fwd for other shapes (Wgu may be NULL)
