@@ -174,10 +174,11 @@ __global__ __launch_bounds__(SK_W * 64) void k_skinny_nt(const bf16* __restrict_
 
 // ── C_p = bf16(X Y_p^T) with X and Y streamed through LDS ────────────────
 // The same product for the common case (16-byte aligned rows, K a multiple
-// of 8, n * r <= 48) with direct-to-LDS loads: K runs in stages of 256; one
+// of 8, n * r <= 64) with direct-to-LDS loads: K runs in stages of 256; one
 // global_load_lds_dwordx4 moves 2 rows x 512 contiguous bytes (whole cache
 // lines, where k_skinny_nt's fragment-shaped loads take 64 bytes of each of
-// 16 rows), NS stages in flight.  Block: 32 rows of X, 8 waves; in each
+// 16 rows), NS stage buffers (4 for one or two 16-column tiles, 3 for
+// three or four).  Block: 32 rows of X, 8 waves; in each
 // stage wave w computes k chunk w (32 wide) for both 16-row groups and
 // every 16-column tile of the concatenated Y.  16-byte unit u of row R sits
 // in slot u ^ (R % 16), so the fragment reads of 16 consecutive rows hit
@@ -233,7 +234,13 @@ __global__ __launch_bounds__(512) void k_skinny_dma(const bf16* __restrict__ X, 
     constexpr int LPS = (XI + 7) / 8 + (YI + 7) / 8;      // ... per wave
     __shared__ __attribute__((aligned(1024))) bf16 sX0[XE], sX1[XE], sX2[XE], sX3[NS == 4 ? XE : 8];
     __shared__ __attribute__((aligned(1024))) bf16 sY0[YE], sY1[YE], sY2[YE], sY3[NS == 4 ? YE : 8];
-    __shared__ floatx4 red[SK_W / 2][SK_RG][NT][64];
+    // the partial sums' exchange; with four 16-column tiles it reuses stage
+    // buffer sY0 (32 KB), which keeps the block within the LDS
+    static_assert(NT < 4 || sizeof(floatx4) * SK_W / 2 * SK_RG * NT * 64 <= sizeof(bf16) * YE,
+                  "exchange fits a Y stage buffer");
+    __shared__ floatx4 red_own[NT < 4 ? SK_W / 2 : 1][SK_RG][NT][64];
+    floatx4 (*const red)[SK_RG][NT][64] =
+        NT < 4 ? red_own : reinterpret_cast<floatx4 (*)[SK_RG][NT][64]>(sY0);
     const int lane = threadIdx.x & 63;
     int w = threadIdx.x >> 6;
     w = __builtin_amdgcn_readfirstlane(w);
@@ -279,6 +286,9 @@ __global__ __launch_bounds__(512) void k_skinny_dma(const bf16* __restrict__ X, 
         }
     }
     TA_WAIT_VMCNT(0);  // the surplus loads have landed before the block ends
+    // (exchange in sY0: every wave's loads have landed and its fragment
+    // reads are done before any wave writes there)
+    if constexpr (NT == 4) __syncthreads();
 #undef SKD_STEP
 #undef SKD_ISSUE
     // fixed-order tree over the waves: w += w + h for h = 4, 2, 1
@@ -947,12 +957,13 @@ int lora_skinny_nt(const bf16* X, int64_t ldx, int M, int K, int r, const bf16* 
     int nt = (n * r + 15) / 16;
     dim3 grid((M + 16 * SK_RG - 1) / (16 * SK_RG));
     const bool timed = kprof_begin(KP_LORA_SKINNY, s);
-    const bool dma = ((uintptr_t)X & 15) == 0 && (ldx & 7) == 0 && (K & 7) == 0 && nt <= 3;
+    const bool dma = ((uintptr_t)X & 15) == 0 && (ldx & 7) == 0 && (K & 7) == 0 && nt <= 4;
     if (dma) {
         switch (nt) {
             case 1: k_skinny_dma<1, 4><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
             case 2: k_skinny_dma<2, 4><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
-            default: k_skinny_dma<3, 3><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
+            case 3: k_skinny_dma<3, 3><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
+            default: k_skinny_dma<4, 3><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
         }
     } else switch (nt) {
         case 1: k_skinny_nt<1, 4><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
