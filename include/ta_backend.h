@@ -166,7 +166,9 @@ int ta_gemm_rm(int x_kmajor, int y_kmajor, int M, int N, int K, float alpha,
                const uint16_t* X, int ldx, const uint16_t* Y, int ldy, float beta,
                uint16_t* C, int ldc, const uint16_t* bias, void* stream);
 
-/* Kernel variant of the large K-contiguous GEMMs, for tuning sweeps:
+/* ta_gemm_rm with the kernel of the large K-contiguous GEMMs chosen for this
+ * one call (tuning sweeps and the kernel-form tests); other calls, on this
+ * thread or any other, keep the default:
  * 0 = the default (the pipelined kernel, 192- or 256-wide tiles by N),
  * 7..11 = the 8-/4-wave direct-to-LDS kernel shapes, 12/13 = the 4-wave
  * pipelined kernel with 192/256-wide tiles, 14/15 = its 8-wave 4x2 layout
@@ -174,7 +176,9 @@ int ta_gemm_rm(int x_kmajor, int y_kmajor, int M, int N, int K, float alpha,
  * the forms of 15/16 with 64-k stages (whole 128-byte operand lines per
  * direct-to-LDS row).  Other values return an error.
  * No reference counterpart. */
-int ta_gemm_variant(int variant);
+int ta_gemm_rm_variant(int variant, int x_kmajor, int y_kmajor, int M, int N, int K, float alpha,
+                       const uint16_t* X, int ldx, const uint16_t* Y, int ldy, float beta,
+                       uint16_t* C, int ldc, const uint16_t* bias, void* stream);
 
 /* ── centroid accumulator ───────────────────────────────────────────
  * replaces CentroidAccumulator::accumulate  src/centroid/centroid_accumulator.cpp:23-70
@@ -192,7 +196,9 @@ int ta_centroid_accumulate_bf16(const uint16_t* h, const uint16_t* g, int64_t BT
  * ta_centroid_accumulate_bf16; its partial rows live in a static 8 MiB device
  * array per GPU, held until the process ends, so ceil(BT/16) * (D+1) * 4
  * bytes must fit 8 MiB (BT <= 21824 at D = 1536, 9360 at D = 3584), else it
- * returns an error before launching anything.  Every call on one GPU shares
+ * returns an error before launching anything.  The GPU is the stream's
+ * (the current device for the null stream); the caller's current device is
+ * left as it was.  Every call on one GPU shares
  * that array: calls that overlap on one GPU (on different streams, or from
  * different threads) race and must be ordered by the caller. */
 int ta_centroid_accumulate_bf16_noalloc(const uint16_t* h, const uint16_t* g, int64_t BT, int D,

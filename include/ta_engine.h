@@ -45,11 +45,16 @@ typedef struct ta_adapt_config {
     float b1, b2, eps, wd;
 } ta_adapt_config;
 
-/* StepMetrics (include/tensor/trainer/adapt_trainer.hpp:18-27) plus the raw norm. */
+/* StepMetrics (include/tensor/trainer/adapt_trainer.hpp:18-27) plus the raw
+ * norm and nonfinite_logits: the number of NaN and Inf logits of the step
+ * when it was the engine's first (step count 0 before it; the reference
+ * checks the logits at step 0 only, adapt_trainer.cu:76-91,196-198), -1 on
+ * later steps, which do not count them. */
 typedef struct ta_step_metrics {
     float loss, lr, gnorm, gnorm_raw;
     int valid_tokens, step;
     double step_ms;
+    int nonfinite_logits;
 } ta_step_metrics;
 
 /* Allocates the base (W and W^T of every projection), the adapter arena and

@@ -85,9 +85,9 @@ struct GemmParams {
 // C = alpha * op(A) op(B) + beta * C with the BLAS column-major convention,
 // on the device's stream.  Throws CudaError when M, N, K or a leading
 // dimension is <= 0 (tensor.cu:134-142).  gemm_bf16: FP32 accumulation,
-// one BF16 rounding of the output.  gemm_f32: F32 in/out; the products run
-// on BF16 MFMA, exact for operands that hold BF16 values (the LoRA weight
-// gradients, the only F32 GEMMs on the training step).
+// one BF16 rounding of the output.  gemm_f32: F32 in/out at F32 accuracy:
+// each F32 operand is split into three BF16 parts (24 significand bits in
+// all) and the part products are accumulated in F32 on the BF16 MFMA.
 void gemm_bf16(const Device& dev, const GemmParams& p, const bf16_t* A, int lda,
                const bf16_t* B, int ldb, bf16_t* C, int ldc);
 void gemm_f32(const Device& dev, const GemmParams& p, const float* A, int lda, const float* B,

@@ -558,13 +558,11 @@ int centroid_acc_bf16(const bf16* h, const bf16* g, int64_t BT, int D, double* a
 }  // namespace ta
 
 // Device address of `scratch` on device dev, looked up once per device with
-// that device current (the caller's current device) and kept.
+// that device current and kept.
 static std::mutex g_na_mu;
 static float* g_na_ptr[64];
 
-static int noalloc_scratch(float** out) {
-    int dev = 0;
-    TA_HIP(hipGetDevice(&dev));
+static int noalloc_scratch(int dev, float** out) {
     TA_REQUIRE(dev >= 0 && dev < 64, "centroid_accumulate_bf16_noalloc: device %d out of range", dev);
     std::lock_guard<std::mutex> lk(g_na_mu);
     if (!g_na_ptr[dev]) {
@@ -576,6 +574,20 @@ static int noalloc_scratch(float** out) {
     *out = g_na_ptr[dev];
     return 0;
 }
+
+// Makes `dev` the current device for the lifetime of the object and restores
+// the caller's device afterwards.
+struct DeviceScope {
+    int prev = -1;
+    hipError_t err = hipSuccess;
+    explicit DeviceScope(int dev) {
+        err = hipGetDevice(&prev);
+        if (err == hipSuccess && prev != dev) err = hipSetDevice(dev);
+    }
+    ~DeviceScope() {
+        if (prev >= 0) (void)hipSetDevice(prev);
+    }
+};
 
 extern "C" {
 
@@ -597,10 +609,19 @@ int ta_centroid_accumulate_bf16_noalloc(const uint16_t* h, const uint16_t* g, in
                "D+1 floats, over the %zu-byte static scratch (at most BT=%lld at this D)",
                (long long)BT, D, (long long)nblk, kNoAllocScratchBytes,
                (long long)(max_blk * kTok));
-    float* part = nullptr;
-    const int rc = noalloc_scratch(&part);
-    if (rc != 0) return rc;
     hipStream_t s = (hipStream_t)stream;
+    // the stream's device (the current one for the null stream) holds the
+    // scratch copy and runs the kernels
+    int dev = 0;
+    if (s)
+        TA_HIP(hipStreamGetDevice(s, &dev));
+    else
+        TA_HIP(hipGetDevice(&dev));
+    DeviceScope scope(dev);
+    TA_HIP(scope.err);
+    float* part = nullptr;
+    const int rc = noalloc_scratch(dev, &part);
+    if (rc != 0) return rc;
     // the same kernels and order as ta_centroid_accumulate_bf16: every
     // partial row is written in full before the reduce reads it
     k_centroid_part<true><<<(int)nblk, 256, 0, s>>>(h, g, nullptr, BT, D, part);

@@ -62,8 +62,14 @@ struct Layer {
 struct Engine {
     ta_model_config mc;
     ta_adapt_config ac;
-    int B, T, BT, H, qd, kvd, I, V, r;
-    float scale;  // alpha / r
+    int B, T, BT, H, qd, kvd, I, V;
+    // r: the rank every buffer and kernel of the engine is laid out for, the
+    // requested rank r_real rounded up to a multiple of 16.  A holds r rows
+    // [r, in] and B r columns [out, r]; rows and columns past r_real are zero
+    // and stay zero (their h, dh, gradients and AdamW updates are exactly 0),
+    // so the step computes the rank-r_real adapter.
+    int r, r_real;
+    float scale;  // alpha / r_real
     // per-layer activation recompute: only each layer's input (res_in) is
     // kept per layer; the other cached activations live in one shared set
     // that the backward refills by rerunning the layer's forward
@@ -109,6 +115,8 @@ struct Engine {
     // set on the device when a token id of the batch lies outside [0, V):
     // the embedding then reads nothing for it, and the tail changes no state
     int32_t* bad_dev = nullptr;
+    // NaN and Inf logits of the first step (the reference's step-0 check)
+    int32_t* nonfinite_dev = nullptr;
     hipEvent_t ev[4];
     int64_t step_count = 0;
     float phase[3] = {0, 0, 0};
@@ -389,6 +397,7 @@ static int engine_alloc(Engine* e) {
     CK(alloc(e, &e->dkv_part, (int64_t)2 * e->B * c.n_q * e->T * c.head_dim, "dkv_part", 1));
     CK(alloc(e, &e->norm_dev, 64, "norm", 1));
     e->bad_dev = (int32_t*)(e->norm_dev + 1);
+    e->nonfinite_dev = (int32_t*)(e->norm_dev + 2);
     CK(alloc(e, &e->own_cacc, H + 1, "centroid"));
     e->cacc = e->own_cacc;
     CK(alloc(e, &e->tok_dev, BT, "tok"));
@@ -412,8 +421,8 @@ static int adapter_init(Engine* e) {
     for (auto& ly : e->L)
         for (auto& p : ly.pr)
             if (p.on)
-                CK(kaiming_init(e->master + p.offA, e->shadow + p.offA, (int64_t)e->r * p.in, p.in,
-                                e->s));
+                CK(kaiming_init(e->master + p.offA, e->shadow + p.offA, (int64_t)e->r_real * p.in,
+                                p.in, e->s));
     TA_HIP(hipMemsetAsync(e->cacc, 0, (e->H + 1) * sizeof(double), e->s));
     return 0;
 }
@@ -685,8 +694,11 @@ static int forward(Engine* e) {
           gemm_dispatch(true, true, BT, e->V, H, 1.f, e->xfn, H, e->lm, H, 0.f, e->logits, e->V,
                         nullptr, false, s, 0, nullptr));
     // loss (adapt_trainer.cu:201-205): dlogits overwrite the logits in place
-    TIMED(TA_CAT_CE, 0, dBT * e->V * 6,
-          ta_cross_entropy_fwd(e->logits, e->tgt_dev, e->loss_tok, e->logits, BT, e->V, s));
+    // (one read and one write of BT x V BF16); the first step also counts
+    // the NaN and Inf logits (adapt_trainer.cu:196-198)
+    TIMED(TA_CAT_CE, 0, dBT * e->V * 4,
+          cross_entropy(e->logits, e->tgt_dev, e->loss_tok, e->logits, BT, e->V,
+                        e->step_count == 0 ? e->nonfinite_dev : nullptr, s));
     return 0;
 }
 
@@ -805,7 +817,7 @@ static int engine_step_body(Engine* e, float lr_override, ta_step_metrics* m,
     const int BT = e->BT;
     // zero_grad (adapter_model.cu:222-229)
     TA_HIP(hipMemsetAsync(e->grad, 0, e->nparam * sizeof(float), e->s));
-    TA_HIP(hipMemsetAsync(e->bad_dev, 0, sizeof(int32_t), e->s));
+    TA_HIP(hipMemsetAsync(e->bad_dev, 0, 2 * sizeof(int32_t), e->s));  // and nonfinite_dev
     // B^T shadows for dh = go B (the shadows changed in the last AdamW)
     CK(transpose_batch(e->shadow, e->shadowT, e->tdesc, e->ntdesc, e->s));
     TA_HIP(hipEventRecord(e->ev[0], e->s));
@@ -824,7 +836,7 @@ static int engine_step_body(Engine* e, float lr_override, ta_step_metrics* m,
                            e->ac.b1, e->ac.b2, e->ac.eps, e->ac.wd, t, e->ac.grad_clip,
                            e->norm_dev, e->bad_dev, e->s));
     // the norm and the bad-id flag behind it
-    TA_HIP(hipMemcpyAsync(e->norm_host, e->norm_dev, 8, hipMemcpyDeviceToHost, e->s));
+    TA_HIP(hipMemcpyAsync(e->norm_host, e->norm_dev, 12, hipMemcpyDeviceToHost, e->s));
     TA_HIP(hipEventRecord(e->ev[3], e->s));
     TA_HIP(hipStreamSynchronize(e->s));
     for (int i = 0; i < 3; i++) TA_HIP(hipEventElapsedTime(&e->phase[i], e->ev[i], e->ev[i + 1]));
@@ -839,8 +851,10 @@ static int engine_step_body(Engine* e, float lr_override, ta_step_metrics* m,
         }
     if (valid > 0) mean /= (float)valid;
     float norm = e->norm_host[0];
-    int32_t bad;
+    int32_t bad, nonfinite;
     memcpy(&bad, e->norm_host + 1, sizeof bad);
+    memcpy(&nonfinite, e->norm_host + 2, sizeof nonfinite);
+    const bool first = e->step_count == 0;
     if (bad)
         return set_error(-1,
                          "engine_step: a token id of the batch lies outside [0, %d); the step was "
@@ -854,6 +868,7 @@ static int engine_step_body(Engine* e, float lr_override, ta_step_metrics* m,
         m->gnorm = std::min(norm, e->ac.grad_clip);
         m->valid_tokens = valid;
         m->step = (int)e->step_count;
+        m->nonfinite_logits = first ? nonfinite : -1;
         m->step_ms =
             std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     }
@@ -973,7 +988,8 @@ void* ta_engine_create_ex(const ta_model_config* mc, const ta_adapt_config* ac, 
     e->kvd = mc->n_kv * mc->head_dim;
     e->I = mc->inter;
     e->V = mc->vocab;
-    e->r = ac->rank;
+    e->r_real = ac->rank;
+    e->r = (ac->rank + 15) / 16 * 16;
     e->scale = ac->alpha / (float)ac->rank;  // adapter_model.cu:139
     e->recompute = (flags & TA_ENGINE_RECOMPUTE) != 0;
     if (stream) {
@@ -1092,25 +1108,46 @@ int ta_engine_step(void* ep, const int32_t* inputs, const int32_t* targets, floa
     return engine_step(e, inputs, targets, lr_override, m);
 }
 
-// Locate one adapter tensor: device pointer, element count and element size.
-static int adapter_slot(Engine* e, int layer, int target, int which, void** ptr, int64_t* cnt,
-                        size_t* es) {
+// Locate one adapter tensor: device pointer, element count and element size,
+// and its layout in the arena: `rows` rows of `width` elements `pitch` apart
+// (B [out, r_real] sits in the columns of B [out, r]; A [r_real, in] is the
+// first r_real rows of A [r, in], contiguous).
+struct Slot {
+    void* ptr;
+    int64_t cnt, rows, width, pitch;
+    size_t es;
+};
+static int adapter_slot(Engine* e, int layer, int target, int which, Slot* sl) {
     TA_REQUIRE(layer >= 0 && layer < (int)e->L.size() && target >= 0 && target < NPAIR,
                "engine adapter: bad layer/target");
     Pair& p = e->L[layer].pr[target];
     TA_REQUIRE(p.on, "engine adapter: target %d not injected", target);
     bool isA = (which == 0 || which == 2 || which == 3 || which == 6 || which == 8);
-    *cnt = isA ? (int64_t)e->r * p.in : (int64_t)p.out * e->r;
+    sl->cnt = isA ? (int64_t)e->r_real * p.in : (int64_t)p.out * e->r_real;
+    sl->rows = isA ? 1 : p.out;
+    sl->width = isA ? sl->cnt : e->r_real;
+    sl->pitch = isA ? sl->cnt : e->r;
     int64_t off = isA ? p.offA : p.offB;
-    *es = 4;
+    sl->es = 4;
     switch (which) {
-        case 0: case 1: *ptr = e->master + off; break;
-        case 2: case 4: *ptr = e->mom + off; break;
-        case 3: case 5: *ptr = e->vel + off; break;
-        case 6: case 7: *ptr = e->grad + off; break;
-        case 8: case 9: *ptr = e->shadow + off; *es = 2; break;
+        case 0: case 1: sl->ptr = e->master + off; break;
+        case 2: case 4: sl->ptr = e->mom + off; break;
+        case 3: case 5: sl->ptr = e->vel + off; break;
+        case 6: case 7: sl->ptr = e->grad + off; break;
+        case 8: case 9: sl->ptr = e->shadow + off; sl->es = 2; break;
         default: return set_error(-1, "engine adapter: bad which=%d", which);
     }
+    return 0;
+}
+
+// host <-> adapter tensor copy on the engine's stream, then wait for it
+static int adapter_copy(Engine* e, const Slot& sl, void* host, bool to_host) {
+    const size_t hp = (size_t)sl.width * sl.es, dp = (size_t)sl.pitch * sl.es;
+    if (to_host)
+        TA_HIP(hipMemcpy2DAsync(host, hp, sl.ptr, dp, hp, sl.rows, hipMemcpyDeviceToHost, e->s));
+    else
+        TA_HIP(hipMemcpy2DAsync(sl.ptr, dp, host, hp, hp, sl.rows, hipMemcpyHostToDevice, e->s));
+    TA_HIP(hipStreamSynchronize(e->s));
     return 0;
 }
 
@@ -1118,15 +1155,11 @@ int ta_engine_write_adapter(void* ep, int layer, int target, int which, const vo
                             int64_t n) {
     Engine* e = (Engine*)ep;
     TA_REQUIRE(e && host, "engine_write_adapter: null argument");
-    void* dst;
-    int64_t cnt;
-    size_t es;
-    CK(adapter_slot(e, layer, target, which, &dst, &cnt, &es));
-    TA_REQUIRE(n == cnt, "engine_write_adapter: n=%lld, tensor has %lld", (long long)n,
-               (long long)cnt);
-    TA_HIP(hipMemcpyAsync(dst, host, cnt * es, hipMemcpyHostToDevice, e->s));
-    TA_HIP(hipStreamSynchronize(e->s));
-    return 0;
+    Slot sl;
+    CK(adapter_slot(e, layer, target, which, &sl));
+    TA_REQUIRE(n == sl.cnt, "engine_write_adapter: n=%lld, tensor has %lld", (long long)n,
+               (long long)sl.cnt);
+    return adapter_copy(e, sl, const_cast<void*>(host), false);
 }
 
 int ta_engine_step_resident(void* ep, const int32_t* d_inputs, const int32_t* d_targets,
@@ -1164,15 +1197,11 @@ int ta_engine_profile_read(void* ep, double* ms, int64_t* n, double* flops, doub
 int ta_engine_read_adapter(void* ep, int layer, int target, int which, void* host, int64_t n) {
     Engine* e = (Engine*)ep;
     TA_REQUIRE(e && host, "engine_read_adapter: null argument");
-    void* src;
-    int64_t cnt;
-    size_t es;
-    CK(adapter_slot(e, layer, target, which, &src, &cnt, &es));
-    TA_REQUIRE(n == cnt, "engine_read_adapter: n=%lld, tensor has %lld", (long long)n,
-               (long long)cnt);
-    TA_HIP(hipMemcpyAsync(host, src, cnt * es, hipMemcpyDeviceToHost, e->s));
-    TA_HIP(hipStreamSynchronize(e->s));
-    return 0;
+    Slot sl;
+    CK(adapter_slot(e, layer, target, which, &sl));
+    TA_REQUIRE(n == sl.cnt, "engine_read_adapter: n=%lld, tensor has %lld", (long long)n,
+               (long long)sl.cnt);
+    return adapter_copy(e, sl, host, true);
 }
 
 int ta_engine_centroid(void* ep, double* host) {

@@ -1370,13 +1370,15 @@ __global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
     gemm_pipe_body<BN, WMW, WNW, false, true, KD>(a);
 }
 
-// Kernel variants of the large GEMMs (ta_gemm_variant): 0 picks k_gemm_pipe
+// Kernel variants of the large GEMMs (ta_gemm_rm_variant): 0 picks k_gemm_pipe
 // with 8 waves and 64-k stages (256 x 192 tiles in a 4 x 2 wave layout up
 // to N = 3072, 256 x 256 in a 2 x 4 layout above; N = 1536 then gives one
 // block per CU at M = 8192): variants 17 and 18.  7..11 are k_gemm_dma
 // shapes kept for sweeps and for the split-K partials; 12..16 force one
 // k_gemm_pipe shape with 32-k stages (15, 16: the 32-k forms of 17, 18).
-static int g_big_variant = 0;
+// The variant in force: 0 except inside a ta_gemm_rm_variant call on this
+// thread, so no caller's GEMMs change kernel because of another's sweep.
+static thread_local int g_big_variant = 0;
 static bool variant_ok(int v) { return v == 0 || (v >= 7 && v <= 18); }
 static bool is_pipe(int variant) { return variant >= 12; }
 static int big_bn(int variant) {
@@ -1543,7 +1545,8 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
         // LoRA terms fuse into the epilogue up to rank 64 for k_gemm_pipe (one
         // MFMA k step per 16) and at any rank for k_gemm_dma; otherwise they
         // run after the GEMM
-        const bool fuse = lora && lora->n > 0 && (!is_pipe(variant) || lora->r <= 64);
+        const bool fuse = lora && lora->n > 0 && (lora->r & 7) == 0 &&
+                          (!is_pipe(variant) || lora->r <= 64);
         if (fuse) {
             a.lora_n = lora->n;
             a.lora_r = lora->r;
@@ -1697,7 +1700,7 @@ int gemm_chain(int M, int N, const GemmSeg* sg, int ns, bf16* C, int64_t ldc, co
             ok &= (kb / KD + pad) % NS == 0;
         }
     }
-    ok &= !lora || lora->n == 0 || lora->r <= 64;
+    ok &= !lora || lora->n == 0 || (lora->r <= 64 && (lora->r & 7) == 0);
     if (!ok) {
         for (int q = 0; q < ns; q++) {
             int rc = gemm_dispatch(true, true, M, N, sg[q].K, 1.f, sg[q].X, sg[q].ldx, sg[q].Y,
@@ -1790,7 +1793,7 @@ int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const Gem
         vy &= al16(gr[g].Y);
         const LoraEpi* l = gr[g].lora;
         if (l && l->n > 0) {
-            lora_ok &= l->n == 1 && l->r <= 64 && l->ldu[0] == l->r;
+            lora_ok &= l->n == 1 && l->r <= 64 && (l->r & 7) == 0 && l->ldu[0] == l->r;
             if (l0) lora_ok &= l->r == l0->r;
             if (l0) lora_ok &= l->delta == l0->delta && l->s == l0->s;
             else l0 = l;
@@ -1892,7 +1895,8 @@ int gemm_swiglu(int M, int K, const bf16* X, int64_t ldx, const bf16* Wgu, const
                 const bf16* Wu, bf16* gate, bf16* up, bf16* act, int I, const LoraEpi* lg,
                 const LoraEpi* lu, hipStream_t s) {
     const bool on = lg && lg->n > 0;
-    const bool lora_ok = on ? (lu && lu->n == 1 && lg->n == 1 && lg->r <= 64 && lu->r == lg->r &&
+    const bool lora_ok = on ? (lu && lu->n == 1 && lg->n == 1 && lg->r <= 64 && (lg->r & 7) == 0 &&
+                               lu->r == lg->r &&
                                lg->delta == lu->delta && lg->s == lu->s &&
                                lg->ldu[0] == lg->r && lu->ldu[0] == lu->r)
                             : !(lu && lu->n > 0);
@@ -2002,11 +2006,6 @@ using namespace ta;
 
 extern "C" {
 
-int ta_gemm_variant(int v) {
-    TA_REQUIRE(variant_ok(v), "gemm_variant: %d is not a kernel variant (0, 7..18)", v);
-    g_big_variant = v;
-    return 0;
-}
 
 int ta_gemm_rm(int x_kmajor, int y_kmajor, int M, int N, int K, float alpha, const uint16_t* X,
                int ldx, const uint16_t* Y, int ldy, float beta, uint16_t* C, int ldc,
@@ -2015,6 +2014,20 @@ int ta_gemm_rm(int x_kmajor, int y_kmajor, int M, int N, int K, float alpha, con
                "gemm_rm: M/N/K and leading dims must be > 0");
     return gemm_dispatch(x_kmajor != 0, y_kmajor != 0, M, N, K, alpha, X, ldx, Y, ldy, beta, C,
                          ldc, bias, false, (hipStream_t)stream, 0, nullptr);
+}
+
+int ta_gemm_rm_variant(int variant, int x_kmajor, int y_kmajor, int M, int N, int K, float alpha,
+                       const uint16_t* X, int ldx, const uint16_t* Y, int ldy, float beta,
+                       uint16_t* C, int ldc, const uint16_t* bias, void* stream) {
+    TA_REQUIRE(variant_ok(variant), "gemm_rm_variant: %d is not a kernel variant (0, 7..18)",
+               variant);
+    struct Restore {
+        int v;
+        ~Restore() { g_big_variant = v; }
+    } restore{g_big_variant};
+    g_big_variant = variant;
+    return ta_gemm_rm(x_kmajor, y_kmajor, M, N, K, alpha, X, ldx, Y, ldy, beta, C, ldc, bias,
+                      stream);
 }
 
 // cuBLAS column-major C(MxN) = alpha op(A) op(B) + beta C  ==  row-major

@@ -511,7 +511,9 @@ Dataset Dataset::load(const std::string& dir) {
         size_t old = ds.tokens_.size();
         ds.tokens_.resize(old + n);
         in.read(reinterpret_cast<char*>(ds.tokens_.data() + old), (std::streamsize)(n * 4));
+        std::cerr << "[data] loaded " << f.filename() << " (" << n << " tokens)\n";
     }
+    std::cerr << "[data] total tokens: " << ds.total_tokens() << "\n";
     return ds;
 }
 

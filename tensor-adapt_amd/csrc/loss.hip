@@ -28,11 +28,22 @@ __global__ __launch_bounds__(512) void k_cross_entropy(const bf16* __restrict__ 
                                                        const int32_t* __restrict__ targets,
                                                        float* __restrict__ loss,
                                                        bf16* __restrict__ dlogits, int V,
-                                                       float inv_N) {
+                                                       float inv_N,
+                                                       int32_t* __restrict__ nonfinite) {
     int64_t n = blockIdx.x;
     const bf16* L = logits + n * (int64_t)V;
     bf16* dL = dlogits ? dlogits + n * (int64_t)V : nullptr;
     int tgt = targets[n];
+    if (nonfinite) {
+        // Inf or NaN logits of the row (the reference's step-0 check,
+        // adapt_trainer.cu:76-91), read before dlogits may overwrite them
+        int bad = 0;
+        for (int i = threadIdx.x; i < V; i += blockDim.x) bad += (L[i] & 0x7f80u) == 0x7f80u;
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) bad += __shfl_xor(bad, o, 64);
+        if ((threadIdx.x & 63) == 0 && bad) atomicAdd(nonfinite, bad);
+        __syncthreads();
+    }
     float m = -FLT_MAX, s = 0.f;
     int nv = VEC ? (V >> 3) : 0;
     if (VEC) {
@@ -116,12 +127,15 @@ __device__ __forceinline__ float block_sum16(float v, float* red) {
     return r;
 }
 
-template <int CPT>  // 16-byte chunks per lane: V <= 8 * 1024 * CPT, V % 8 == 0
+// COUNT: also add the row's NaN and Inf logits to *nonfinite (the
+// reference's step-0 check, adapt_trainer.cu:76-91)
+template <int CPT, bool COUNT>  // 16-byte chunks per lane: V <= 8 * 1024 * CPT, V % 8 == 0
 __global__ __launch_bounds__(1024) void k_cross_entropy_reg(const bf16* __restrict__ logits,
                                                             const int32_t* __restrict__ targets,
                                                             float* __restrict__ loss,
                                                             bf16* __restrict__ dlogits, int V,
-                                                            float inv_N) {
+                                                            float inv_N,
+                                                            int32_t* __restrict__ nonfinite) {
     __shared__ float red[16], tls;
     const int64_t n = blockIdx.x;
     const bf16x8v* L = (const bf16x8v*)(logits + n * (int64_t)V);
@@ -147,6 +161,21 @@ __global__ __launch_bounds__(1024) void k_cross_entropy_reg(const bf16* __restri
                 if (c * 8 + e == tgt) tls = f[e];
             }
         }
+    }
+    if (COUNT) {
+        // exponent bits all ones: Inf or NaN
+        float bad = 0.f;
+#pragma unroll
+        for (int k = 0; k < CPT; k++)
+            if (threadIdx.x + 1024 * k < nv)
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    const uint32_t w = r[k].w[e];
+                    bad += (float)((w & 0x7f80u) == 0x7f80u) +
+                           (float)((w & 0x7f800000u) == 0x7f800000u);
+                }
+        const float nb = block_sum16(bad, red);  // exact: at most V < 2^24
+        if (threadIdx.x == 0 && nb > 0.f) atomicAdd(nonfinite, (int32_t)nb);
     }
     // exp as one v_exp_f32 of x log2(e) - M log2(e) (results below the
     // normal range flush to zero, as the reference's fast-math __expf does)
@@ -189,16 +218,12 @@ __global__ __launch_bounds__(1024) void k_cross_entropy_reg(const bf16* __restri
     }
 }
 
-}  // namespace ta
-
-using namespace ta;
-
-extern "C" int ta_cross_entropy_fwd(const uint16_t* logits, const int32_t* targets,
-                                    float* loss_out, uint16_t* dlogits, int N, int V,
-                                    void* stream) {
+// cross_entropy_fwd that also adds the count of NaN and Inf logits to
+// *nonfinite when it is not null (a device int32 the caller zeroes)
+int cross_entropy(const bf16* logits, const int32_t* targets, float* loss_out, bf16* dlogits,
+                  int N, int V, int32_t* nonfinite, hipStream_t s) {
     TA_REQUIRE(N >= 0 && V > 0, "cross_entropy_fwd: bad shape N=%d V=%d", N, V);
     if (N == 0) return 0;
-    hipStream_t s = (hipStream_t)stream;
     // divisor = number of rows, masked rows included (gridDim.x in ops.cu:1005)
     float inv_N = 1.f / (float)N;
     bool vec = (V & 7) == 0 && (((uintptr_t)logits | (uintptr_t)dlogits) & 15u) == 0;
@@ -207,16 +232,33 @@ extern "C" int ta_cross_entropy_fwd(const uint16_t* logits, const int32_t* targe
     // share before the block's first barrier, and writes only its own chunks
     // (up to 20 chunks per lane fit the 128 registers of a 16-wave block)
     if (vec && cpt <= 20) {
-#define CE(C) k_cross_entropy_reg<C><<<N, 1024, 0, s>>>(logits, targets, loss_out, dlogits, V, inv_N)
-        if (cpt <= 4) CE(4);
-        else if (cpt <= 8) CE(8);
-        else if (cpt <= 16) CE(16);
-        else CE(20);
+#define CE(C, K)                                                                      \
+    k_cross_entropy_reg<C, K><<<N, 1024, 0, s>>>(logits, targets, loss_out, dlogits, V, inv_N, \
+                                                 nonfinite)
+#define CE2(C) \
+    if (nonfinite) CE(C, true); else CE(C, false)
+        if (cpt <= 4) { CE2(4); }
+        else if (cpt <= 8) { CE2(8); }
+        else if (cpt <= 16) { CE2(16); }
+        else { CE2(20); }
+#undef CE2
 #undef CE
     } else if (vec) {
-        k_cross_entropy<true><<<N, 512, 0, s>>>(logits, targets, loss_out, dlogits, V, inv_N);
+        k_cross_entropy<true><<<N, 512, 0, s>>>(logits, targets, loss_out, dlogits, V, inv_N,
+                                                nonfinite);
     } else {
-        k_cross_entropy<false><<<N, 512, 0, s>>>(logits, targets, loss_out, dlogits, V, inv_N);
+        k_cross_entropy<false><<<N, 512, 0, s>>>(logits, targets, loss_out, dlogits, V, inv_N,
+                                                 nonfinite);
     }
     return check_launch("cross_entropy_fwd");
+}
+
+}  // namespace ta
+
+using namespace ta;
+
+extern "C" int ta_cross_entropy_fwd(const uint16_t* logits, const int32_t* targets,
+                                    float* loss_out, uint16_t* dlogits, int N, int V,
+                                    void* stream) {
+    return cross_entropy(logits, targets, loss_out, dlogits, N, V, nullptr, (hipStream_t)stream);
 }

@@ -113,6 +113,11 @@ int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const 
              int Hq, int Hkv, int hd, float* Dbuf, float* part, hipStream_t s);
 int64_t attn_bwd_rowbuf_floats(int B, int T, int Hq);
 int transpose_bf16(const bf16* in, bf16* out, int64_t rows, int64_t cols, hipStream_t s);
+// cross_entropy_fwd (ops.cu:958-1020) that also adds the number of NaN and
+// Inf logits to *nonfinite when it is not null (a device int32 the caller
+// zeroes)
+int cross_entropy(const bf16* logits, const int32_t* targets, float* loss_out, bf16* dlogits,
+                  int N, int V, int32_t* nonfinite, hipStream_t s);
 int fill_normal_bf16(bf16* out, int64_t n, uint64_t seed, uint64_t sid, float std, hipStream_t s);
 int fill_bf16(bf16* out, int64_t n, float v, hipStream_t s);
 int kaiming_init(float* a32, bf16* a16, int64_t n, int in_dim, hipStream_t s);

@@ -754,6 +754,9 @@ struct AdaptTrainer::Impl {
         ta_step_metrics m{};
         check_status(ta_engine_step(eng, batch.first.data(), batch.second.data(), 0.f, &m),
                      "AdaptTrainer::step");
+        // the logits check of the first step (adapt_trainer.cu:76-91,196-198)
+        if (step_count == 0 && m.nonfinite_logits > 0)
+            std::cerr << "[trainer] WARNING: " << m.nonfinite_logits << " NaNs in logits at step 0\n";
         step_count++;
         tokens_seen += (std::size_t)B * T;
         const double ms = std::chrono::duration<double, std::milli>(Clock::now() - t0).count();

@@ -152,7 +152,8 @@ class AdaptConfig(ctypes.Structure):
 class StepMetrics(ctypes.Structure):
     _fields_ = [("loss", ctypes.c_float), ("lr", ctypes.c_float), ("gnorm", ctypes.c_float),
                 ("gnorm_raw", ctypes.c_float), ("valid_tokens", ctypes.c_int),
-                ("step", ctypes.c_int), ("step_ms", ctypes.c_double)]
+                ("step", ctypes.c_int), ("step_ms", ctypes.c_double),
+                ("nonfinite_logits", ctypes.c_int)]
 
 
 TARGETS = ("q", "k", "v", "o", "gate", "up", "down")

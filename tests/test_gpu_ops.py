@@ -237,7 +237,7 @@ def test_gemm_rm_kmajor_tiles(M, N, K):
 @pytest.mark.parametrize("M,N,K", [(2048, 1536, 1536), (1024, 3000, 320), (1280, 1100, 192),
                                    (1024, 1024, 64)])
 def test_gemm_stage_forms_bit_identical(M, N, K):
-    """The large-GEMM kernel forms that ta_gemm_variant selects accumulate
+    """The large-GEMM kernel forms that ta_gemm_rm_variant selects accumulate
     the same products in the same F32 order (64-k stages as two 32-k k
     steps each), so 17 and 18 (the default's two tile widths) equal 15 and
     16 (their 32-k-stage forms) bit for bit, with and without the bias
@@ -248,20 +248,21 @@ def test_gemm_stage_forms_bit_identical(M, N, K):
 
     def run(v, bias, beta):
         tc = dev(C0)
-        call("ta_gemm_variant", v)
-        call("ta_gemm_rm", 1, 1, M, N, K, ctypes.c_float(1.0), P(tX), K, P(tY), K,
+        call("ta_gemm_rm_variant", v, 1, 1, M, N, K, ctypes.c_float(1.0), P(tX), K, P(tY), K,
              ctypes.c_float(beta), P(tc), N, P(bias) if bias is not None else None, S())
         return host(tc)
 
-    try:
-        for a, c in ((15, 17), (16, 18)):
-            for bias, beta in ((None, 0.0), (tb, 0.0), (None, 1.0)):
-                ga, gc = run(a, bias, beta), run(c, bias, beta)
-                assert np.array_equal(ga, gc), \
-                    f"variant {a} vs {c} (bias={bias is not None}, beta={beta}) differ"
-        got = run(0, None, 1.0)
-    finally:
-        call("ta_gemm_variant", 0)
+    for a, c in ((15, 17), (16, 18)):
+        for bias, beta in ((None, 0.0), (tb, 0.0), (None, 1.0)):
+            ga, gc = run(a, bias, beta), run(c, bias, beta)
+            assert np.array_equal(ga, gc), \
+                f"variant {a} vs {c} (bias={bias is not None}, beta={beta}) differ"
+    got = run(0, None, 1.0)
+    # the variant held for that one call only: the plain entry runs the default
+    tc = dev(C0)
+    call("ta_gemm_rm", 1, 1, M, N, K, ctypes.c_float(1.0), P(tX), K, P(tY), K,
+         ctypes.c_float(1.0), P(tc), N, None, S())
+    assert np.array_equal(host(tc), got)
     check_gemm_close(got, rm_ref(1, 1, M, N, K, 1.0, X, K, Y, K, 1.0, C0, N), "gemm default")
 
 

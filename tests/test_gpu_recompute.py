@@ -97,9 +97,9 @@ def test_recompute_bit_identical_c4_layer_shapes():
 
 
 def test_c4_layer_matches_oracle():
-    """One 7B-shaped layer at T=2048 and rank 64 (generic-rank LoRA paths:
-    rank updates after the projection GEMMs, per-pair dh/gB/gA products,
-    unfused SwiGLU backward), untied LM head over the full 152064 ids, with
+    """One 7B-shaped layer at T=2048 and rank 64 (the rank-64 LoRA terms in
+    the projection GEMMs' epilogues, per-pair dh/gB/gA products for the
+    generic rank), untied LM head over the full 152064 ids, with
     recompute on.  Step 2 starts from the oracle's state after step 1, so gA
     is checked with B != 0.  Clipping is off here (the clip is checked by
     the AdamW test and the smaller step tests) so both steps compare raw
