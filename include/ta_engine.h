@@ -35,7 +35,10 @@ typedef struct ta_model_config {
     int tie; /* 1: LM head = embedding (qwen2.cu:163) */
 } ta_model_config;
 
-/* AdapterConfig fields used by the step (include/tensor/adapter/adapter_config.hpp:25-70). */
+/* AdapterConfig fields used by the step (include/tensor/adapter/adapter_config.hpp:25-70).
+ * rank: 1..64 (the reference's rank ladder tops out at 64); any rank in that
+ * range trains exactly that rank, laid out internally at the next multiple
+ * of 16 with zero extra rows of A and columns of B. */
 typedef struct ta_adapt_config {
     int rank;
     float alpha;

@@ -973,8 +973,11 @@ void* ta_engine_create_ex(const ta_model_config* mc, const ta_adapt_config* ac, 
         return nullptr;
     }
     if (mc->n_kv <= 0 || mc->n_q % mc->n_kv != 0 || mc->hidden <= 0 || mc->layers <= 0 ||
-        (mc->head_dim != 64 && mc->head_dim != 128) || ac->rank <= 0 || mc->vocab <= 0) {
-        set_error(-1, "engine_create: unsupported shape (head_dim 64/128, n_q %% n_kv == 0)");
+        (mc->head_dim != 64 && mc->head_dim != 128) || ac->rank <= 0 || ac->rank > 64 ||
+        mc->vocab <= 0) {
+        // (rank 64 is the top of the reference's rank ladder, adapter_config.cpp:53-127)
+        set_error(-1, "engine_create: unsupported shape (head_dim 64/128, n_q %% n_kv == 0, "
+                      "LoRA rank 1..64)");
         return nullptr;
     }
     Engine* e = new Engine();

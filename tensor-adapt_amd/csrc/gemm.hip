@@ -26,6 +26,7 @@
 // (gemm_f32 semantics), or F32 partials for split-K with a separate
 // fixed-order reduction (deterministic).
 #include <algorithm>
+#include <numeric>
 #include <type_traits>
 
 #include "ta_backend.h"
@@ -810,12 +811,12 @@ __device__ __attribute__((always_inline)) inline void static_for(F&& f) {
 }
 
 // Element offset of (row, col) in a wave's 64 x WTN BF16 output staging:
-// 16-byte chunks XOR-swizzled by row bits 1..3 (1..2 for WTN = 96), so the
+// 16-byte chunks XOR-swizzled by row bits 1..3 (1..2 for WTN = 96 and 32), so the
 // 8-byte writes of 32 rows at one column land in distinct banks and every
 // 16-byte chunk stays contiguous for the row read-out.
 template <int WTN>
 __device__ __forceinline__ int stg_off(int row, int col) {
-    constexpr int X = WTN == 96 ? 3 : 7;
+    constexpr int X = (WTN == 96 || WTN == 32) ? 3 : 7;
     return row * WTN + ((((col >> 3) ^ ((row >> 1) & X)) << 3) | (col & 7));
 }
 
@@ -1023,19 +1024,22 @@ __device__ __forceinline__ void round_acc(floatx16 (&acc)[TM][TN]) {
 // KD = 64: two stages of 64 k in the same LDS, rows of one whole 128-byte
 // line, so every line of an operand is fetched once; the next stage's load
 // has the same 64 k of compute to land in as with four 32-k stages.
-template <int BN, int WMW, int WNW, bool CHAIN, bool SWIGLU = false, int KD = 32>
+template <int BN, int WMW, int WNW, bool CHAIN, bool SWIGLU = false, int KD = 32, int BM = 256>
 __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmArgs& a0) {
     static_assert(KD == 32 || KD == 64, "stage depth");
-    constexpr int NS = KD == 32 ? 4 : 2, BM = 256, NW = WMW * WNW;
+    constexpr int NS = KD == 32 ? 4 : 2, NW = WMW * WNW;
     constexpr int WTM = BM / WMW, WTN = BN / WNW;
     constexpr int TM = WTM / 32, TN = WTN / 32;
     static_assert(TM * 32 == WTM && TN * 32 == WTN && TM % 2 == 0, "wave tile");
-    static_assert(KD == 32 || NW == 8, "64-k stages: 8-wave layouts");
+    // 128-row tiles: four waves of 64-row wave tiles (k_gemm_mid)
+    static_assert(BM == 256 || (BM == 128 && NW == 4 && KD == 64), "tile height");
+    static_assert(KD == 32 || NW == 8 || BM == 128, "64-k stages: 8-wave layouts");
     // DMA instructions per stage per wave
     constexpr int RPI = 64 / (KD / 8);  // stage rows per DMA instruction
     constexpr int LPS = (BM / RPI + NW - 1) / NW + (BN / RPI + NW - 1) / NW;
     constexpr int SX = BM * KD, SY = BN * KD;
-    static_assert(BN == 192 || BN == 256, "tile width");
+    static_assert(BN == 192 || BN == 256 || (BM == 128 && (BN == 64 || BN == 128)),
+                  "tile width");
     __shared__ __attribute__((aligned(1024))) bf16 sXs[NS][SX];
     __shared__ __attribute__((aligned(1024))) bf16 sYs[NS][SY];
     bf16* const sX0 = sXs[0];
@@ -1044,7 +1048,8 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
     bf16* const sY1 = sYs[1];
     // epilogue operands staged at the start: rank-16 LoRA U/V rows of the
     // first LP pairs and 512 bias entries (one DMA instruction)
-    constexpr int LP = BN == 256 ? 1 : 3;
+    // (128 x 128 tiles stage one pair, so two blocks fit a CU's LDS)
+    constexpr int LP = (BN == 256 || (BM == 128 && BN == 128)) ? 1 : 3;
     constexpr int LPU = SWIGLU ? 2 : LP;  // U rows: both pairs' h in the SwiGLU form
     static_assert(!SWIGLU || (BN == 256 && WNW == 4 && WMW == 2), "SwiGLU tile layout");
     __shared__ __attribute__((aligned(16))) bf16 sLU[LPU * BM * 16], sLV[LP * BN * 16], sB[512];
@@ -1298,7 +1303,13 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
         }
     };
     bf16 *wb0, *wb1;
-    if constexpr (NW == 4) {
+    if constexpr (BM == 128) {
+        // one 64-row half per wave (TM = 2), the four regions side by side
+        // over the two X stage buffers
+        static_assert(TM == 2 && 4 * 64 * WTN <= NS * SX, "staging fits the X stages");
+        wb0 = &sXs[0][0] + w * 64 * WTN;
+        wb1 = wb0;
+    } else if constexpr (NW == 4) {
         wb0 = sXs[w];
         wb1 = sYs[w];
         static_assert(64 * WTN <= SX && 64 * WTN <= SY, "staging fits a stage buffer");
@@ -1368,6 +1379,19 @@ template <int BN, int WMW, int WNW, int KD = 32>
 __global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
     WMW * WNW / 4, WMW * WNW / 4))) void k_gemm_pipe_swiglu(GemmArgs a) {
     gemm_pipe_body<BN, WMW, WNW, false, true, KD>(a);
+}
+// 128-row tiles (128 x BN, BN = 64 or 128; four waves of 64-row wave tiles,
+// two 64-k stages): the same pipeline and epilogue for outputs too small to
+// fill the chip with 256-row tiles (the Qwen2-0.5B shapes at B x T = 2048).
+template <int BN>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_mid(
+    GemmArgs a) {
+    gemm_pipe_body<BN, 2, 2, false, false, 64, 128>(a);
+}
+template <int BN>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gemm_mid_chain(
+    GemmArgs a) {
+    gemm_pipe_body<BN, 2, 2, true, false, 64, 128>(a);
 }
 
 // Kernel variants of the large GEMMs (ta_gemm_rm_variant): 0 picks k_gemm_pipe
@@ -1464,6 +1488,43 @@ static inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // must span less than 4 GB (32-bit byte offsets from the tile's first row)
 constexpr int64_t kMaxStageLd = int64_t(1) << 23;
 
+// Tile width of k_gemm_mid for an M x N output (0: keep the 256-row tiles).
+// The 256-row kernels stay while their tiles fill most of the chip (or split
+// K fills it); otherwise each candidate's cost is taken as (waves of 256
+// blocks) x tile area / relative efficiency (1.0 for the 256-row tiles, 0.75
+// for 128 x 128, 0.6 for 128 x 64: smaller wave tiles read more LDS per
+// MFMA) and the cheapest wins.  n_mult: every N (of every group) must be a
+// multiple of the width; big_ok: the 256-row kernel can take the shape.
+static int mid_bn(int M, int N, int BNb, int ksteps, bool big_ok, int n_mult) {
+    if (M < 128 || N < 64) return 0;
+    const int big_tiles = ((M + 255) / 256) * ((N + BNb - 1) / BNb);
+    if (big_ok && (big_tiles >= 192 || ksteps >= 32)) return 0;
+    auto cost = [](int tiles, double area, double eff) {
+        return (double)((tiles + 255) / 256) * area / eff;
+    };
+    double best = big_ok ? cost(big_tiles, 256.0 * BNb, 1.0) : 1e300;
+    int pick = 0;
+    const int bns[2] = {128, 64};
+    const double effs[2] = {0.75, 0.6};
+    for (int q = 0; q < 2; q++) {
+        if (n_mult % bns[q] != 0) continue;
+        const int t = ((M + 127) / 128) * ((N + bns[q] - 1) / bns[q]);
+        const double c = cost(t, 128.0 * bns[q], effs[q]);
+        if (c < best) {
+            best = c;
+            pick = bns[q];
+        }
+    }
+    return pick;
+}
+static const char* mid_name(int bn, bool chain) {
+    if (chain)
+        return bn == 128 ? "void ta::k_gemm_mid_chain<128>(ta::GemmArgs)"
+                         : "void ta::k_gemm_mid_chain<64>(ta::GemmArgs)";
+    return bn == 128 ? "void ta::k_gemm_mid<128>(ta::GemmArgs)"
+                     : "void ta::k_gemm_mid<64>(ta::GemmArgs)";
+}
+
 // Shape-driven dispatch.  out_f32: C is F32 (gemm_f32 semantics).  lora
 // (may be NULL): rank-r terms applied to C after the base epilogue, fused
 // into the large-GEMM kernel's epilogue when that kernel runs unsplit and
@@ -1508,10 +1569,47 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
     bool vx = al16(X) && (ldx % 8) == 0;
     bool vy = al16(Y) && (ldy % 8) == 0;
 
+    // K-contiguous BF16 GEMMs too small to fill the chip with 256-row tiles:
+    // k_gemm_mid (128-row tiles, LoRA terms in the epilogue)
+    const bool pipe_ok = xk && yk && !out_f32 && (K % BK) == 0 && vx && vy &&
+                         ldx < kMaxStageLd && ldy < kMaxStageLd;
+    if (pipe_ok && g_big_variant == 0 && force_splits <= 0) {
+        const bool big_ok = M >= 1024 && N >= 1024;
+        const int bn = mid_bn(M, N, N > 3072 ? 256 : 192, K / BK, big_ok, 128);
+        if (bn) {
+            a.tiles_m = (M + 127) / 128;
+            a.tiles_n = (N + bn - 1) / bn;
+            a.k_per_split = K;
+            if (lora && lora->n > 0) {
+                a.lora_n = lora->n;
+                a.lora_r = lora->r;
+                a.lora_delta = lora->delta ? 1 : 0;
+                a.lora_s = lora->s;
+                for (int p = 0; p < lora->n; p++) {
+                    a.lora_u[p] = lora->u[p];
+                    a.lora_ldu[p] = lora->ldu[p];
+                    a.lora_v[p] = lora->v_nk[p];
+                }
+            }
+            const bool timed = kprof_begin(KP_GEMM_BIG, s);
+            dim3 grid(a.tiles_m * a.tiles_n);
+            if (bn == 128)
+                k_gemm_mid<128><<<grid, 256, 0, s>>>(a);
+            else
+                k_gemm_mid<64><<<grid, 256, 0, s>>>(a);
+            if (timed) {
+                double mn = (double)M * N;
+                double fl = 2.0 * mn * K + 2.0 * mn * a.lora_r * a.lora_n;
+                double by = 2.0 * ((double)M * K + (double)N * K + mn * (beta != 0.f ? 2 : 1)) +
+                            2.0 * a.lora_n * (double)(M + N) * a.lora_r;
+                kprof_end(KP_GEMM_BIG, s, fl, by, mid_name(bn, false));
+            }
+            return check_launch("gemm");
+        }
+    }
     // large K-contiguous BF16 GEMMs: k_gemm_pipe (k_gemm_dma for split-K)
     // (the stage loads address 256 operand rows with 32-bit byte offsets)
-    if (xk && yk && !out_f32 && M >= 1024 && N >= 1024 && (K % BK) == 0 && vx && vy &&
-        ldx < kMaxStageLd && ldy < kMaxStageLd) {
+    if (pipe_ok && M >= 1024 && N >= 1024) {
         int variant = g_big_variant;
         if (variant == 0) variant = N > 3072 ? 18 : 17;
         const int BNb = big_bn(variant);
@@ -1701,7 +1799,22 @@ int gemm_chain(int M, int N, const GemmSeg* sg, int ns, bf16* C, int64_t ldc, co
         }
     }
     ok &= !lora || lora->n == 0 || (lora->r <= 64 && (lora->r & 7) == 0);
-    if (!ok) {
+    // 128-row tiles (k_gemm_mid_chain: two 64-k stages per trip) when the
+    // 256-row chain cannot fill the chip
+    int mid = 0;
+    if (g_big_variant == 0 && ns > 1 && M >= 128 && N >= 64) {
+        bool mok = !lora || lora->n == 0 || (lora->r <= 64 && (lora->r & 7) == 0);
+        const int nk = Ktot / 64, pad = (2 - nk % 2) % 2;
+        int kb = 0;
+        for (int q = 0; q < ns; q++) {
+            mok &= sg[q].K % BK == 0 && al16(sg[q].X) && al16(sg[q].Y) && sg[q].ldx % 8 == 0 &&
+                   sg[q].ldy % 8 == 0 && sg[q].ldx < kMaxStageLd && sg[q].ldy < kMaxStageLd;
+            kb += sg[q].K;
+            if (q + 1 < ns) mok &= (kb / 64 + pad) % 2 == 0;
+        }
+        if (mok) mid = mid_bn(M, N, BNb, Ktot / BK, ok, 128);
+    }
+    if (!ok && !mid) {
         for (int q = 0; q < ns; q++) {
             int rc = gemm_dispatch(true, true, M, N, sg[q].K, 1.f, sg[q].X, sg[q].ldx, sg[q].Y,
                                    sg[q].ldy, q ? 1.f : 0.f, C, ldc, nullptr, false, s, 0,
@@ -1723,8 +1836,8 @@ int gemm_chain(int M, int N, const GemmSeg* sg, int ns, bf16* C, int64_t ldc, co
     a.alpha = 1.f;
     a.beta = 0.f;
     a.k_per_split = Ktot;
-    a.tiles_m = (M + 255) / 256;
-    a.tiles_n = (N + BNb - 1) / BNb;
+    a.tiles_m = mid ? (M + 127) / 128 : (M + 255) / 256;
+    a.tiles_n = mid ? (N + mid - 1) / mid : (N + BNb - 1) / BNb;
     a.ngroups = 1;
     a.nseg = ns;
     int k = 0;
@@ -1749,7 +1862,11 @@ int gemm_chain(int M, int N, const GemmSeg* sg, int ns, bf16* C, int64_t ldc, co
     }
     dim3 grid(a.tiles_m * a.tiles_n);
     const bool timed = kprof_begin(KP_GEMM_CHAIN, s);
-    if (BNb == 192 && KD == 64)
+    if (mid == 128)
+        k_gemm_mid_chain<128><<<grid, 256, 0, s>>>(a);
+    else if (mid == 64)
+        k_gemm_mid_chain<64><<<grid, 256, 0, s>>>(a);
+    else if (BNb == 192 && KD == 64)
         k_gemm_pipe_chain<192, 4, 2, 64><<<grid, 512, 0, s>>>(a);
     else if (KD == 64)
         k_gemm_pipe_chain<256, 2, 4, 64><<<grid, 512, 0, s>>>(a);
@@ -1764,7 +1881,8 @@ int gemm_chain(int M, int N, const GemmSeg* sg, int ns, bf16* C, int64_t ldc, co
         double by = 2.0 * ((double)M * Ktot + (double)N * Ktot + mn) +
                     2.0 * a.lora_n * (double)(M + N) * a.lora_r;
         kprof_end(KP_GEMM_CHAIN, s, fl, by,
-                  KD == 64 ? (BNb == 192 ? "void ta::k_gemm_pipe_chain<192, 4, 2, 64>(ta::GemmArgs)"
+                  mid ? mid_name(mid, true)
+                  : KD == 64 ? (BNb == 192 ? "void ta::k_gemm_pipe_chain<192, 4, 2, 64>(ta::GemmArgs)"
                                          : "void ta::k_gemm_pipe_chain<256, 2, 4, 64>(ta::GemmArgs)")
                            : (BNb == 192 ? "void ta::k_gemm_pipe_chain<192, 4, 2>(ta::GemmArgs)"
                                          : "void ta::k_gemm_pipe_chain<256, 2, 4>(ta::GemmArgs)"));
@@ -1806,9 +1924,19 @@ int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const Gem
     const int tiles = ((M + 255) / 256) * (Ntot / BNb);
     const bool vx = al16(X) && (ldx % 8) == 0;
     // (as gemm_dispatch: few tiles and a long K go to split-K instead)
-    if (!(ng > 1 && is_pipe(variant) && tiles_ok && lora_ok && vx && vy && M >= 1024 &&
-          ldx < kMaxStageLd && ldy < kMaxStageLd &&
-          Ntot >= 1024 && (K % BK) == 0 && (tiles >= 192 || K / BK < 32))) {
+    const bool big = ng > 1 && is_pipe(variant) && tiles_ok && lora_ok && vx && vy && M >= 1024 &&
+                     ldx < kMaxStageLd && ldy < kMaxStageLd && Ntot >= 1024 && (K % BK) == 0 &&
+                     (tiles >= 192 || K / BK < 32);
+    // 128-row tiles when the 256-row grid cannot fill the chip; every
+    // group's N a multiple of the tile width
+    int nmult = 0;
+    for (int g = 0; g < ng; g++) nmult = std::gcd(nmult, gr[g].N);
+    const int mid = (g_big_variant == 0 && ng > 1 && lora_ok && vx && vy && (K % BK) == 0 &&
+                     ldx < kMaxStageLd && ldy < kMaxStageLd)
+                        ? mid_bn(M, Ntot, BNb, K / BK, big, nmult)
+                        : 0;
+    const int TBN = mid ? mid : BNb;
+    if (!big && !mid) {
         for (int g = 0; g < ng; g++) {
             int rc = gemm_dispatch(true, true, M, gr[g].N, K, 1.f, X, ldx, gr[g].Y, ldy, 0.f,
                                    gr[g].C, gr[g].ldc, gr[g].bias, false, s, 0, gr[g].lora);
@@ -1830,8 +1958,8 @@ int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const Gem
     a.beta = 0.f;
     a.bias = gr[0].bias;
     a.k_per_split = K;
-    a.tiles_m = (M + 255) / 256;
-    a.tiles_n = Ntot / BNb;
+    a.tiles_m = mid ? (M + 127) / 128 : (M + 255) / 256;
+    a.tiles_n = Ntot / TBN;
     a.ngroups = ng;
     a.lora_r = l0 ? l0->r : 0;
     a.lora_delta = l0 && l0->delta ? 1 : 0;
@@ -1841,7 +1969,7 @@ int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const Gem
         const LoraEpi* l = gr[g].lora;
         const bool on = l && l->n > 0;
         a.tn0[g] = tn;
-        tn += gr[g].N / BNb;
+        tn += gr[g].N / TBN;
         a.gN[g] = gr[g].N;
         a.gY[g] = gr[g].Y;
         a.gC[g] = gr[g].C;
@@ -1858,7 +1986,11 @@ int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const Gem
     const int kid = BNb == 256 ? KP_GEMM_BIG_WIDE : KP_GEMM_BIG;
     const bool timed = kprof_begin(kid, s);
     dim3 grid(a.tiles_m * a.tiles_n);
-    if (variant == 12)
+    if (mid == 128)
+        k_gemm_mid<128><<<grid, 256, 0, s>>>(a);
+    else if (mid == 64)
+        k_gemm_mid<64><<<grid, 256, 0, s>>>(a);
+    else if (variant == 12)
         k_gemm_pipe<192, 2, 2><<<grid, 256, 0, s>>>(a);
     else if (variant == 13)
         k_gemm_pipe<256, 2, 2><<<grid, 256, 0, s>>>(a);
@@ -1879,7 +2011,7 @@ int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const Gem
                 fl += 2.0 * M * gr[g].N * a.lora_r;
                 by += 2.0 * (double)(M + gr[g].N) * a.lora_r;
             }
-        kprof_end(kid, s, fl, by, big_name(variant));
+        kprof_end(kid, s, fl, by, mid ? mid_name(mid, false) : big_name(variant));
     }
     return check_launch("gemm_groups");
 }

@@ -1047,7 +1047,9 @@ int lora_wgrad_part(const bf16* L, int64_t ldl, int NL, const bf16* Sm, int64_t 
         case 2: WG(2); break;
         case 3: WG(3); break;
         case 4: WG(4); break;
+        case 6: WG(6); break;
         case 8: WG(8); break;
+        case 9: WG(9); break;
         case 12: WG(12); break;
         default: return set_error(-1, "lora_wgrad_part: %d small columns unsupported", NS);
     }
