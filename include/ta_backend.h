@@ -174,7 +174,9 @@ int ta_gemm_rm(int x_kmajor, int y_kmajor, int M, int N, int K, float alpha,
  * pipelined kernel with 192/256-wide tiles, 14/15 = its 8-wave 4x2 layout
  * with 256/192-wide tiles, 16 = its 8-wave 2x4 layout (256-wide), 17/18 =
  * the forms of 15/16 with 64-k stages (whole 128-byte operand lines per
- * direct-to-LDS row).  Other values return an error.
+ * direct-to-LDS row), 19/20 = the 128-row-tile kernel with 128/64-wide
+ * tiles; + 100 x s forces s K splits on the 256-row kernels (F32 partials
+ * and an ordered reduce).  Other values return an error.
  * No reference counterpart. */
 int ta_gemm_rm_variant(int variant, int x_kmajor, int y_kmajor, int M, int N, int K, float alpha,
                        const uint16_t* X, int ldx, const uint16_t* Y, int ldy, float beta,

@@ -1400,11 +1400,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 // block per CU at M = 8192): variants 17 and 18.  7..11 are k_gemm_dma
 // shapes kept for sweeps and for the split-K partials; 12..16 force one
 // k_gemm_pipe shape with 32-k stages (15, 16: the 32-k forms of 17, 18).
+// 19 and 20 force k_gemm_mid with 128- and 64-wide tiles.
 // The variant in force: 0 except inside a ta_gemm_rm_variant call on this
-// thread, so no caller's GEMMs change kernel because of another's sweep.
+// thread, so no caller's GEMMs change kernel because of another's sweep;
+// g_force_splits likewise (0: the dispatch's own split-K choice).
 static thread_local int g_big_variant = 0;
-static bool variant_ok(int v) { return v == 0 || (v >= 7 && v <= 18); }
-static bool is_pipe(int variant) { return variant >= 12; }
+static thread_local int g_force_splits = 0;
+static bool variant_ok(int v) { return v == 0 || (v >= 7 && v <= 20); }
+static bool is_pipe(int variant) { return variant >= 12 && variant <= 18; }
 static int big_bn(int variant) {
     return (variant == 8 || variant == 10 || variant == 13 || variant == 14 || variant == 16 ||
             variant == 18)
@@ -1488,34 +1491,27 @@ static inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 // must span less than 4 GB (32-bit byte offsets from the tile's first row)
 constexpr int64_t kMaxStageLd = int64_t(1) << 23;
 
-// Tile width of k_gemm_mid for an M x N output (0: keep the 256-row tiles).
-// The 256-row kernels stay while their tiles fill most of the chip (or split
-// K fills it); otherwise each candidate's cost is taken as (waves of 256
-// blocks) x tile area / relative efficiency (1.0 for the 256-row tiles, 0.75
-// for 128 x 128, 0.6 for 128 x 64: smaller wave tiles read more LDS per
-// MFMA) and the cheapest wins.  n_mult: every N (of every group) must be a
-// multiple of the width; big_ok: the 256-row kernel can take the shape.
+// Tile width of k_gemm_mid for an M x N output (0: the 256-row kernels).
+// The 256-row tiles stay while they fill most of the chip (big_ok: that
+// kernel can take the shape), and for long K (32 or more 64-k stages),
+// where they run split-K: 128-row tiles reread each operand band twice as
+// often, and at Qwen2-0.5B's K = 4864 .. 151936 the small tiles were bound
+// by those rereads (measured 1.0-2.9x slower than 256-row split-K).
+// Otherwise the 64-wide tiles while two blocks per CU hold them all (they
+// measured fastest at M = 2048, N = 896 .. 1152, K <= 1152), then the
+// 128-wide ones.  n_mult: every N (of every group) must be a multiple of
+// the width.
 static int mid_bn(int M, int N, int BNb, int ksteps, bool big_ok, int n_mult) {
     if (M < 128 || N < 64) return 0;
     const int big_tiles = ((M + 255) / 256) * ((N + BNb - 1) / BNb);
-    if (big_ok && (big_tiles >= 192 || ksteps >= 32)) return 0;
-    auto cost = [](int tiles, double area, double eff) {
-        return (double)((tiles + 255) / 256) * area / eff;
-    };
-    double best = big_ok ? cost(big_tiles, 256.0 * BNb, 1.0) : 1e300;
-    int pick = 0;
-    const int bns[2] = {128, 64};
-    const double effs[2] = {0.75, 0.6};
-    for (int q = 0; q < 2; q++) {
-        if (n_mult % bns[q] != 0) continue;
-        const int t = ((M + 127) / 128) * ((N + bns[q] - 1) / bns[q]);
-        const double c = cost(t, 128.0 * bns[q], effs[q]);
-        if (c < best) {
-            best = c;
-            pick = bns[q];
-        }
-    }
-    return pick;
+    if (big_ok && big_tiles >= 192) return 0;
+    if (ksteps >= 32 && M >= 256 && N >= 128) return 0;
+    const int t64 = ((M + 127) / 128) * ((N + 63) / 64);
+    const int t128 = ((M + 127) / 128) * ((N + 127) / 128);
+    if (n_mult % 64 == 0 && t64 <= 512) return 64;
+    if (n_mult % 128 == 0 && t128 <= 512) return 128;
+    if (big_ok) return 0;
+    return n_mult % 128 == 0 ? 128 : n_mult % 64 == 0 ? 64 : 0;
 }
 static const char* mid_name(int bn, bool chain) {
     if (chain)
@@ -1573,9 +1569,12 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
     // k_gemm_mid (128-row tiles, LoRA terms in the epilogue)
     const bool pipe_ok = xk && yk && !out_f32 && (K % BK) == 0 && vx && vy &&
                          ldx < kMaxStageLd && ldy < kMaxStageLd;
-    if (pipe_ok && g_big_variant == 0 && force_splits <= 0) {
+    if (pipe_ok && ((g_big_variant == 0 && force_splits <= 0 && g_force_splits == 0) ||
+                    g_big_variant == 19 || g_big_variant == 20)) {
         const bool big_ok = M >= 1024 && N >= 1024;
-        const int bn = mid_bn(M, N, N > 3072 ? 256 : 192, K / BK, big_ok, 128);
+        const int bn = g_big_variant == 19   ? 128
+                       : g_big_variant == 20 ? 64
+                                             : mid_bn(M, N, N > 3072 ? 256 : 192, K / BK, big_ok, 128);
         if (bn) {
             a.tiles_m = (M + 127) / 128;
             a.tiles_n = (N + bn - 1) / bn;
@@ -1609,19 +1608,35 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
     }
     // large K-contiguous BF16 GEMMs: k_gemm_pipe (k_gemm_dma for split-K)
     // (the stage loads address 256 operand rows with 32-bit byte offsets)
-    if (pipe_ok && M >= 1024 && N >= 1024) {
+    // (smaller outputs take the 256-row tiles when a variant is forced, and
+    // split-K when K is long: 32 or more 64-k stages)
+    const int ksteps = (K + BK - 1) / BK;
+    if (pipe_ok && ((M >= 1024 && N >= 1024) || (M >= 256 && N >= 128 && ksteps >= 32) ||
+                    (g_big_variant != 0 && M >= 256 && N >= 128))) {
         int variant = g_big_variant;
         if (variant == 0) variant = N > 3072 ? 18 : 17;
+        // split-K over few tiles: as many splits as keep the blocks within one
+        // per CU (at least 8 stages each), with the tile width that gives the
+        // most blocks (256-wide on a tie)
+        auto split_for = [&](int tiles) {
+            return std::max(1, std::min(256 / tiles, ksteps / 8));
+        };
+        const int t192 = ((M + 255) / 256) * ((N + 191) / 192);
+        const int t256 = ((M + 255) / 256) * ((N + 255) / 256);
+        const bool auto_split = force_splits <= 0 && g_force_splits == 0 && ksteps >= 32;
+        if (g_big_variant == 0 && auto_split && (N > 3072 ? t256 : t192) < 192)
+            variant = t192 * split_for(t192) > t256 * split_for(t256) ? 17 : 18;
         const int BNb = big_bn(variant);
         a.tiles_m = (M + 255) / 256;
         a.tiles_n = (N + BNb - 1) / BNb;
         int tiles = a.tiles_m * a.tiles_n;
-        int ksteps = (K + BK - 1) / BK;
         int splits = 1;
         if (force_splits > 0)
             splits = force_splits;
+        else if (g_force_splits > 0)
+            splits = g_force_splits;
         else if (tiles < 192 && ksteps >= 32)
-            splits = std::min((256 + tiles - 1) / tiles, ksteps / 16);
+            splits = split_for(tiles);
         if (splits < 1) splits = 1;
         int steps_per = (ksteps + splits - 1) / splits;
         a.k_per_split = steps_per * BK;
@@ -1707,7 +1722,6 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
     a.tiles_m = (M + BMv - 1) / BMv;
     a.tiles_n = (N + BNv - 1) / BNv;
     int tiles = a.tiles_m * a.tiles_n;
-    int ksteps = (K + BK - 1) / BK;
     // split K when the tile grid alone cannot fill the 256 CUs
     int splits = 1;
     if (force_splits > 0) {
@@ -1801,8 +1815,9 @@ int gemm_chain(int M, int N, const GemmSeg* sg, int ns, bf16* C, int64_t ldc, co
     ok &= !lora || lora->n == 0 || (lora->r <= 64 && (lora->r & 7) == 0);
     // 128-row tiles (k_gemm_mid_chain: two 64-k stages per trip) when the
     // 256-row chain cannot fill the chip
+    // (long chains run per segment instead, where each takes split-K)
     int mid = 0;
-    if (g_big_variant == 0 && ns > 1 && M >= 128 && N >= 64) {
+    if (g_big_variant == 0 && ns > 1 && M >= 128 && N >= 64 && Ktot / BK < 32) {
         bool mok = !lora || lora->n == 0 || (lora->r <= 64 && (lora->r & 7) == 0);
         const int nk = Ktot / 64, pad = (2 - nk % 2) % 2;
         int kb = 0;
@@ -2151,13 +2166,17 @@ int ta_gemm_rm(int x_kmajor, int y_kmajor, int M, int N, int K, float alpha, con
 int ta_gemm_rm_variant(int variant, int x_kmajor, int y_kmajor, int M, int N, int K, float alpha,
                        const uint16_t* X, int ldx, const uint16_t* Y, int ldy, float beta,
                        uint16_t* C, int ldc, const uint16_t* bias, void* stream) {
-    TA_REQUIRE(variant_ok(variant), "gemm_rm_variant: %d is not a kernel variant (0, 7..18)",
-               variant);
+    TA_REQUIRE(variant_ok(variant % 100) && variant >= 0 && variant / 100 <= 64,
+               "gemm_rm_variant: %d is not a kernel variant (0, 7..20, + 100 x splits)", variant);
     struct Restore {
-        int v;
-        ~Restore() { g_big_variant = v; }
-    } restore{g_big_variant};
-    g_big_variant = variant;
+        int v, f;
+        ~Restore() {
+            g_big_variant = v;
+            g_force_splits = f;
+        }
+    } restore{g_big_variant, g_force_splits};
+    g_big_variant = variant % 100;
+    g_force_splits = variant / 100;
     return ta_gemm_rm(x_kmajor, y_kmajor, M, N, K, alpha, X, ldx, Y, ldy, beta, C, ldc, bias,
                       stream);
 }
