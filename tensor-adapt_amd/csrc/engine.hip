@@ -86,8 +86,10 @@ struct Engine {
     float *master = nullptr, *mom = nullptr, *vel = nullptr, *grad = nullptr;
     bf16* shadow = nullptr;
     bf16* shadowT = nullptr;       // A^T and B^T of every shadow (same offsets), per step
-    void* tdesc = nullptr;         // device descriptors of those transposes
-    int ntdesc = 0;
+    // every adapter tensor for the tiled AdamW, which writes shadowT
+    AdamTensor* atens = nullptr;
+    int natens = 0;
+    int64_t natiles = 0;
     // LoRA weight-gradient partials of one step (one arena slice per
     // product, in backward call order) and their batched reduction
     float* wg_arena = nullptr;
@@ -242,21 +244,25 @@ static int engine_alloc(Engine* e) {
     CK(alloc(e, &e->shadow, off, "adapter.shadow", 0));
     CK(alloc(e, &e->shadowT, off, "adapter.shadowT", 0));
     {
-        struct TD {
-            int64_t src, dst;
-            int rows, cols;
-        };
-        std::vector<TD> td;
+        // A [r, in] tiled by W columns, B [out, r] by W rows: W = 256 at
+        // rank 16, else 64 (tiles of at most 4096 elements)
+        std::vector<AdamTensor> td;
+        int64_t blk = 0;
+        const int lw = r <= 16 ? 8 : 6, W = 1 << lw;
         for (auto& ly : e->L)
             for (auto& pr : ly.pr)
                 if (pr.on) {
-                    td.push_back({pr.offB, pr.offB, pr.out, e->r});  // B [out,r] -> B^T
-                    td.push_back({pr.offA, pr.offA, e->r, pr.in});   // A [r,in] -> A^T
+                    td.push_back({pr.offA, blk, r, pr.in, 1, lw});
+                    blk += (pr.in + W - 1) / W;
+                    td.push_back({pr.offB, blk, pr.out, r, 0, lw});
+                    blk += (pr.out + W - 1) / W;
                 }
-        e->ntdesc = (int)td.size();
-        CK(dmalloc(e, &e->tdesc, td.size() * sizeof(TD) + 16, "tdesc"));
+        e->natens = (int)td.size();
+        e->natiles = blk;
+        CK(dmalloc(e, (void**)&e->atens, td.size() * sizeof(AdamTensor) + 16, "adam_tensors"));
         if (!td.empty())
-            TA_HIP(hipMemcpy(e->tdesc, td.data(), td.size() * sizeof(TD), hipMemcpyHostToDevice));
+            TA_HIP(hipMemcpy(e->atens, td.data(), td.size() * sizeof(AdamTensor),
+                             hipMemcpyHostToDevice));
     }
     for (int l = 0; l < c.layers; l++) {
         Layer& ly = e->L[l];
@@ -307,7 +313,9 @@ static int engine_alloc(Engine* e) {
     }
     // weight-gradient jobs in the order lora_group_bwd issues them: layers
     // L-1..0; groups down, gate/up, o, q/k/v; per group gB of each on-pair,
-    // then gA of the group
+    // then gA of the group.  (Reducing each layer's partials at the end of
+    // its backward, with one arena every layer reuses, measured 0.35 ms per
+    // c3 step slower: the partials were not cache-resident by then either.)
     {
         struct G {
             std::initializer_list<int> pairs;
@@ -410,6 +418,14 @@ static int engine_alloc(Engine* e) {
     return 0;
 }
 
+// A^T and B^T of every BF16 shadow, after shadows were written other than by
+// the step's AdamW (creation, ta_engine_write_adapter)
+static int refresh_shadowT(Engine* e) {
+    return adamw_tiles_impl(e->master, e->shadow, e->shadowT, e->mom, e->vel, e->grad, e->nparam,
+                            e->atens, e->natens, e->natiles, false, 0.f, 0.f, 0.f, 0.f, 0.f, 1,
+                            0.f, nullptr, nullptr, e->s);
+}
+
 // Adapter state at creation (AdapterModel::create, adapter_model.cu:41-90):
 // A from the fixed-seed hash, B = 0, moments 0.
 static int adapter_init(Engine* e) {
@@ -424,7 +440,8 @@ static int adapter_init(Engine* e) {
                 CK(kaiming_init(e->master + p.offA, e->shadow + p.offA, (int64_t)e->r_real * p.in,
                                 p.in, e->s));
     TA_HIP(hipMemsetAsync(e->cacc, 0, (e->H + 1) * sizeof(double), e->s));
-    return 0;
+    TA_HIP(hipMemsetAsync(e->shadowT, 0, e->nparam * 2, e->s));
+    return refresh_shadowT(e);
 }
 
 // ── one LoRA pair (adapter_model.cu:96-129 forward, 131-220 backward) ────
@@ -818,8 +835,6 @@ static int engine_step_body(Engine* e, float lr_override, ta_step_metrics* m,
     // zero_grad (adapter_model.cu:222-229)
     TA_HIP(hipMemsetAsync(e->grad, 0, e->nparam * sizeof(float), e->s));
     TA_HIP(hipMemsetAsync(e->bad_dev, 0, 2 * sizeof(int32_t), e->s));  // and nonfinite_dev
-    // B^T shadows for dh = go B (the shadows changed in the last AdamW)
-    CK(transpose_batch(e->shadow, e->shadowT, e->tdesc, e->ntdesc, e->s));
     TA_HIP(hipEventRecord(e->ev[0], e->s));
     CK(forward(e));
     TA_HIP(hipEventRecord(e->ev[1], e->s));
@@ -832,9 +847,10 @@ static int engine_step_body(Engine* e, float lr_override, ta_step_metrics* m,
                    : cosine_lr(e->ac.lr, e->ac.warmup, e->ac.total_steps, 0.1f, e->step_count);
     int t = (int)e->step_count + 1;
     TIMED(TA_CAT_TAIL, 0, (double)e->nparam * 34,
-          adamw_fused_impl(e->master, e->shadow, e->mom, e->vel, e->grad, e->nparam, lr,
-                           e->ac.b1, e->ac.b2, e->ac.eps, e->ac.wd, t, e->ac.grad_clip,
-                           e->norm_dev, e->bad_dev, e->s));
+          adamw_tiles_impl(e->master, e->shadow, e->shadowT, e->mom, e->vel, e->grad, e->nparam,
+                           e->atens, e->natens, e->natiles, true, lr, e->ac.b1, e->ac.b2,
+                           e->ac.eps, e->ac.wd, t, e->ac.grad_clip, e->norm_dev, e->bad_dev,
+                           e->s));
     // the norm and the bad-id flag behind it
     TA_HIP(hipMemcpyAsync(e->norm_host, e->norm_dev, 12, hipMemcpyDeviceToHost, e->s));
     TA_HIP(hipEventRecord(e->ev[3], e->s));
@@ -1162,7 +1178,12 @@ int ta_engine_write_adapter(void* ep, int layer, int target, int which, const vo
     CK(adapter_slot(e, layer, target, which, &sl));
     TA_REQUIRE(n == sl.cnt, "engine_write_adapter: n=%lld, tensor has %lld", (long long)n,
                (long long)sl.cnt);
-    return adapter_copy(e, sl, const_cast<void*>(host), false);
+    CK(adapter_copy(e, sl, const_cast<void*>(host), false));
+    if (which == 8 || which == 9) {  // the transposed copy the LoRA backward reads
+        CK(refresh_shadowT(e));
+        TA_HIP(hipStreamSynchronize(e->s));
+    }
+    return 0;
 }
 
 int ta_engine_step_resident(void* ep, const int32_t* d_inputs, const int32_t* d_targets,

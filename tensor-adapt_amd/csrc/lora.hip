@@ -924,22 +924,6 @@ __global__ __launch_bounds__(256) void k_dh_reduce2(const float* __restrict__ dh
     dh[t * ldh + 16 * pp + jj] = f2bf(v);
 }
 
-// Batched transpose of the BF16 B shadows into B^T (one launch per step).
-struct TDesc {
-    int64_t src, dst;
-    int rows, cols;
-};
-__global__ void k_transpose_batch(const bf16* __restrict__ src, bf16* __restrict__ dst,
-                                  const TDesc* __restrict__ d, int nd) {
-    const TDesc t = d[blockIdx.y];
-    int64_t n = (int64_t)t.rows * t.cols;
-    for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
-         i += (int64_t)gridDim.x * blockDim.x) {
-        int rr = (int)(i / t.cols), cc = (int)(i % t.cols);
-        dst[t.dst + (int64_t)cc * t.rows + rr] = src[t.src + i];
-    }
-}
-
 // ── host launchers ────────────────────────────────────────────────────────
 int lora_skinny_nt(const bf16* X, int64_t ldx, int M, int K, int r, const bf16* const* Y,
                    bf16* const* C, int64_t ldc, int n, hipStream_t s) {
@@ -1191,11 +1175,5 @@ int go_lora(const bf16* const* go, const int64_t* ldgo, const bf16* const* bt, c
     return check_launch("go_lora");
 }
 
-int transpose_batch(const bf16* src, bf16* dst, const void* descs, int nd, hipStream_t s) {
-    if (nd <= 0) return 0;
-    dim3 grid(64, nd);
-    k_transpose_batch<<<grid, 256, 0, s>>>(src, dst, (const TDesc*)descs, nd);
-    return check_launch("transpose_batch");
-}
 
 }  // namespace ta

@@ -13,6 +13,8 @@
 //      the clip fires, the scaled gradient is also stored back, so the
 //      gradient arena ends the step holding what clip_gradients leaves in
 //      gA/gB (adapt_trainer.cu:55-70: g *= clip / (norm + 1e-6) in place).
+#include <algorithm>
+
 #include "ta_internal.hpp"
 
 namespace ta {
@@ -102,6 +104,92 @@ __global__ __launch_bounds__(256) void k_adamw(float* __restrict__ master, bf16*
     }
 }
 
+// AdamW over the step engine's adapter arena, one tensor tile at a time,
+// that also writes each updated BF16 shadow transposed (A^T [in, r], B^T
+// [r, out]: the K-contiguous operands of the LoRA backward products) into a
+// second arena at the same offsets.  A tile is W columns x all r rows of
+// an A [r, in] or W rows x all r columns of a B [out, r] (W = 256 for
+// r <= 16, else 64: at most 4096 elements): its state is read as whole row
+// segments, and the transposed tile leaves through LDS as contiguous runs
+// (W x r elements for A, r runs of W for B).  Blocks take
+// tiles grid-stride; every block derives the clip factor from the norm
+// partials as k_adamw does.  update = false: no AdamW, the shadow is only
+// copied into its transposed arena (after a shadow is written from outside).
+__global__ __launch_bounds__(256) void k_adamw_tiles(
+    float* __restrict__ master, bf16* __restrict__ work, bf16* __restrict__ workT,
+    float* __restrict__ m, float* __restrict__ v, float* __restrict__ grad,
+    const AdamTensor* __restrict__ tens, int ntens, int64_t ntiles, bool update, float lr,
+    float b1, float b2, float eps, float wd, float bc1, float bc2, const float* __restrict__ part,
+    int nparts, float max_norm, float* __restrict__ norm_out, const int32_t* __restrict__ skip) {
+    __shared__ uint16_t lt[256 * 17];  // [tile column (A) or row (B)][rank index], padded
+    float gscale = 1.f;
+    if (update && part) {
+        double ss = reduce_partials(part, nparts);
+        float norm = (float)sqrt(ss);
+        if (norm_out && blockIdx.x == 0 && threadIdx.x == 0) *norm_out = norm;
+        if (skip && *skip) return;  // a failed step: report the norm, change nothing
+        // clip_gradients, adapt_trainer.cu:55-70
+        if (norm > max_norm) gscale = max_norm / (norm + 1e-6f);
+    }
+    const bool clipped = gscale != 1.f;
+    auto elem = [&](int64_t i) -> uint16_t {
+        if (!update) return work[i];
+        float g = grad[i];
+        if (clipped) {
+            g = g * gscale;
+            grad[i] = g;
+        }
+        float mi = m[i], vi = v[i];
+        const float p = adamw_elem(master[i], g, mi, vi, lr, b1, b2, eps, wd, bc1, bc2);
+        m[i] = mi;
+        v[i] = vi;
+        master[i] = p;
+        const uint16_t h = f2bf(p);
+        work[i] = h;
+        return h;
+    };
+    for (int64_t b = blockIdx.x; b < ntiles; b += gridDim.x) {
+        int lo = 0, hi = ntens - 1;  // last tensor with blk0 <= b
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (tens[mid].blk0 <= b) lo = mid; else hi = mid - 1;
+        }
+        const AdamTensor T = tens[lo];
+        const int t = (int)(b - T.blk0);
+        __syncthreads();  // the previous tile's transposed reads are done
+        const int lw = T.lw, W = 1 << lw, P = (T.a_side ? T.R : T.C) + 1;  // LDS row pitch
+        if (T.a_side) {
+            // A [R = r, C = in]: columns [c0, c0 + nc), all R rows
+            const int c0 = W * t, nc = min(W, T.C - c0);
+            for (int e = threadIdx.x; e < T.R << lw; e += 256) {
+                const int rr = e >> lw, cc = e & (W - 1);
+                if (cc < nc) lt[cc * P + rr] = elem(T.off + (int64_t)rr * T.C + c0 + cc);
+            }
+            __syncthreads();
+            // A^T [C, R]: rows c0 .. c0 + nc, one contiguous run
+            bf16* dst = workT + T.off + (int64_t)c0 * T.R;
+            for (int e = threadIdx.x; e < nc * T.R; e += 256) {
+                const int cc = e / T.R, rr = e - cc * T.R;
+                dst[e] = lt[cc * P + rr];
+            }
+        } else {
+            // B [R = out, C = r]: rows [r0, r0 + nr), all C columns (contiguous)
+            const int r0 = W * t, nr = min(W, T.R - r0);
+            const int64_t base = T.off + (int64_t)r0 * T.C;
+            for (int e = threadIdx.x; e < nr * T.C; e += 256) {
+                const int rr = e / T.C, cc = e - rr * T.C;
+                lt[rr * P + cc] = elem(base + e);
+            }
+            __syncthreads();
+            // B^T [C, R]: row cc gets columns r0 .. r0 + nr
+            for (int e = threadIdx.x; e < T.C << lw; e += 256) {
+                const int cc = e >> lw, rr = e & (W - 1);
+                if (rr < nr) workT[T.off + (int64_t)cc * T.R + r0 + rr] = lt[rr * P + cc];
+            }
+        }
+    }
+}
+
 }  // namespace ta
 
 using namespace ta;
@@ -168,8 +256,32 @@ int adamw_fused_impl(float* master, bf16* working, float* m, float* v, float* gr
     return check_launch("adamw_fused");
 }
 
+// The engine's tail with the transposed shadows: norm partials, then the
+// tiled AdamW (update) or only the shadow transposes (!update; the other
+// arguments past tiles are then unused).
+int adamw_tiles_impl(float* master, bf16* working, bf16* workingT, float* m, float* v,
+                     float* grad, int64_t N, const AdamTensor* tens, int ntens, int64_t ntiles,
+                     bool update, float lr, float beta1, float beta2, float eps,
+                     float weight_decay, int step, float max_norm, float* norm_out,
+                     const int32_t* skip, hipStream_t s) {
+    if (ntiles <= 0) return 0;
+    TA_REQUIRE(ntens > 0 && (!update || step >= 1), "adamw_tiles: bad arguments");
+    const int blocks = (int)std::min<int64_t>(ntiles, 2048);
+    if (!update) {
+        k_adamw_tiles<<<blocks, 256, 0, s>>>(master, working, workingT, m, v, grad, tens, ntens,
+                                             ntiles, false, 0.f, 0.f, 0.f, 0.f, 0.f, 1.f, 1.f,
+                                             nullptr, 0, 0.f, nullptr, nullptr);
+        return check_launch("adamw_tiles");
+    }
+    float* part = (float*)scratch_get(kNormBlocks * sizeof(float), s);
+    TA_REQUIRE(part, "adamw_tiles: scratch allocation failed");
+    float bc1 = 1.f - powf(beta1, (float)step);
+    float bc2 = 1.f - powf(beta2, (float)step);
+    k_sumsq_partials<<<kNormBlocks, 256, 0, s>>>(grad, N, part);
+    k_adamw_tiles<<<blocks, 256, 0, s>>>(master, working, workingT, m, v, grad, tens, ntens, ntiles,
+                                         true, lr, beta1, beta2, eps, weight_decay, bc1, bc2, part,
+                                         kNormBlocks, max_norm, norm_out, skip);
+    return check_launch("adamw_tiles");
+}
+
 }  // namespace ta
-
-extern "C" {
-
-}  // extern "C"

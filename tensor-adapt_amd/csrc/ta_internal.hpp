@@ -132,6 +132,20 @@ int rms_bwd_acc(const bf16* dy, const bf16* x, const bf16* w, const float* rms, 
 // zero row and sets *bad = 1 (ids resident in device memory)
 int embed_fwd_checked(const bf16* table, const int32_t* tokens, bf16* out, int64_t BT, int D,
                       int V, int32_t* bad, hipStream_t s);
+// One adapter tensor of the engine's arena for adamw_tiles_impl: [R x C]
+// row-major at element offset off (the transposed copy [C x R] at the same
+// offset of the transposed arena); a_side: A [r, in], tiled by 2^lw columns,
+// else B [out, r], tiled by 2^lw rows (r <= 64, r x 2^lw <= 4096 and
+// 2^lw <= 256); blk0: its first tile.
+struct AdamTensor {
+    int64_t off, blk0;
+    int R, C, a_side, lw;
+};
+int adamw_tiles_impl(float* master, bf16* working, bf16* workingT, float* m, float* v,
+                     float* grad, int64_t N, const AdamTensor* tens, int ntens, int64_t ntiles,
+                     bool update, float lr, float beta1, float beta2, float eps,
+                     float weight_decay, int step, float max_norm, float* norm_out,
+                     const int32_t* skip, hipStream_t s);
 // the fused norm / clip / AdamW tail; when skip (device int, may be NULL)
 // holds a nonzero value the norm is still reported but no state changes
 int adamw_fused_impl(float* master, bf16* working, float* m, float* v, float* grad, int64_t N,
@@ -186,6 +200,5 @@ int go_lora(const bf16* const* go, const int64_t* ldgo, const bf16* const* bt, c
             hipStream_t s);
 int lora_wgrad_reduce_jobs(const WgradJob* jobs, int njobs, int64_t total_blocks, double elems,
                            hipStream_t s);
-int transpose_batch(const bf16* src, bf16* dst, const void* descs, int nd, hipStream_t s);
 
 }  // namespace ta

@@ -801,6 +801,9 @@ void AdaptTrainer::save_checkpoint(const std::string& dir) { impl_->checkpoint_t
 void AdaptTrainer::save_adapter(const std::string& dir) {
     impl_->dev->sync();
     impl_->centroid_acc.write_snapshot(impl_->step_count);
+    // (the reference merges before its writer creates dir, so into a new
+    // directory its unchecked stream writes no adapter.centroid)
+    fs::create_directories(dir);
     impl_->centroid_acc.merge_and_write(16, dir + "/adapter.centroid");
     impl_->writer.save_final(impl_->gather(false), impl_->cfg, *impl_->base, impl_->opts.domain,
                              impl_->step_count, impl_->tokens_seen, dir);

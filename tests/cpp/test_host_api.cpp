@@ -581,6 +581,136 @@ static void trainer_tests(const Device& dev, const fs::path& dir) {
         [&] { (void)trainer::AdaptTrainer::create(fb, other, dsC, ob, dev); }, "resume:"));
 }
 
+// BASELINE configs[1] (c2) run through AdaptTrainer on its own schedule:
+// Qwen2-0.5B shape (24 layers, hidden 896, 14/2 heads of 64, SwiGLU 4864,
+// tied 151936-entry embedding), r=16 alpha=32 on q,k,v,o, batch 4 x 512,
+// lr 1e-4 with the cosine schedule over 20 steps, weight decay 0.01 and a
+// centroid snapshot every 10 steps (centroid_accumulator.cpp:72-91).  Checks
+// the two snapshot files' byte layout ([i32 D][D f32][f32 W]) and that each
+// is the cumulative C / W of the accumulator at its step (the sums are not
+// reset by a snapshot), the schedule's lr at every step, finite losses and
+// norms, and the merged file ([i32 k][i32 D][k x D f32]): with k >= the 2
+// snapshots every snapshot is its own center.
+static void c2_schedule_tests(const fs::path& dir) {
+    Device dev = Device::open("hip:0");
+    const size_t V = 151936, H = 896, L = 24, q = 896, kv = 128, I = 4864, B = 4, T = 512;
+    base::FrozenBase fb;
+    base::BaseConfig& c = fb.config;
+    c.arch_name = "qwen2";
+    c.arch = base::ArchType::Qwen2;
+    c.vocab_size = V;
+    c.hidden_size = H;
+    c.num_layers = L;
+    c.num_q_heads = 14;
+    c.num_kv_heads = 2;
+    c.head_dim = 64;
+    c.intermediate_size = I;
+    c.rms_norm_eps = 1e-6f;
+    c.rope_theta = 1e6f;
+    c.tie_embeddings = true;
+    uint32_t s = 91;
+    auto mk = [&](std::initializer_list<size_t> shape, float scale, float fill) {
+        Shape sh(shape);
+        std::vector<uint16_t> h(sh.numel());
+        for (auto& v : h) v = f2bf(scale > 0 ? urand(s) * scale * 1.7320508f : fill);
+        return Tensor::from_host(TensorView{h.data(), DType::BF16, sh}, dev);
+    };
+    fb.embed_w = mk({V, H}, 0.02f, 0.f);
+    fb.final_norm_w = mk({H}, 0.f, 1.f);
+    for (size_t l = 0; l < L; l++) {
+        base::LayerWeights w;
+        w.input_norm_w = mk({H}, 0.f, 1.f);
+        w.post_norm_w = mk({H}, 0.f, 1.f);
+        w.q_proj_w = mk({q, H}, 0.02f, 0.f);
+        w.q_proj_b = mk({q}, 0.f, 0.f);
+        w.k_proj_w = mk({kv, H}, 0.02f, 0.f);
+        w.k_proj_b = mk({kv}, 0.f, 0.f);
+        w.v_proj_w = mk({kv, H}, 0.02f, 0.f);
+        w.v_proj_b = mk({kv}, 0.f, 0.f);
+        w.o_proj_w = mk({H, q}, 0.02f, 0.f);
+        w.gate_proj_w = mk({I, H}, 0.02f, 0.f);
+        w.up_proj_w = mk({I, H}, 0.02f, 0.f);
+        w.down_proj_w = mk({H, I}, 0.02f, 0.f);
+        fb.layers.push_back(std::move(w));
+    }
+    // uniform ids with an assistant span over almost every 512-token row, so
+    // the trainer's masking keeps the targets
+    fs::create_directories(dir / "data");
+    std::vector<uint32_t> toks(20 * B * T + 1);
+    for (auto& t : toks) t = lcg(s) % 150000u;
+    for (size_t r = 0; r + T <= toks.size(); r += T) {
+        toks[r + 3] = 151644;
+        toks[r + 4] = 77091;
+        toks[r + T - 8] = 151645;
+    }
+    write_file(dir / "data" / "tokens.bin", toks);
+    adapter::AdapterConfig cfg;
+    cfg.rank = 16;
+    cfg.alpha = 32.f;
+    cfg.lr = 1e-4f;
+    cfg.warmup_steps = 0;
+    cfg.weight_decay = 0.01f;
+    cfg.batch_size = B;
+    cfg.seq_len = T;
+    auto ds = data::Dataset::load((dir / "data").string());
+    trainer::AdaptOptions opts;
+    opts.domain = "c2/schedule";
+    opts.output_dir = (dir / "run").string();
+    opts.checkpoint_every = 10;
+    opts.tokens = 20 * B * T;
+    opts.log_to_stdout = false;
+    auto tr = trainer::AdaptTrainer::create(fb, cfg, ds, opts, dev);
+    std::vector<double> acc[2];
+    for (int i = 1; i <= 20; i++) {
+        trainer::StepMetrics m = tr.step();
+        CHECK(m.step == (size_t)i && std::isfinite(m.loss) && m.loss > 10.f && m.loss < 14.f);
+        CHECK(std::isfinite(m.grad_norm) && m.grad_norm > 0.f && m.grad_norm <= cfg.grad_clip);
+        CHECK(m.learning_rate == ta_cosine_lr(cfg.lr, 0, 20, 0.1f, i - 1));
+        if (i % 10 == 0) {
+            acc[i / 10 - 1].resize(H + 1);
+            CHECK(ta_engine_centroid(tr.engine(), acc[i / 10 - 1].data()) == 0);
+        }
+    }
+    CHECK(tr.done());
+    CHECK(acc[0][H] > 0 && acc[1][H] > acc[0][H]);  // cumulative weight
+    for (int k = 0; k < 2; k++) {
+        auto f = read_file(dir / "run" / "centroids" / ("step-" + std::to_string(10 * (k + 1)) + ".centroid"));
+        CHECK(f.size() == 4 + 4 * H + 4);
+        if (f.size() != 4 + 4 * H + 4) continue;
+        int32_t D;
+        std::memcpy(&D, f.data(), 4);
+        CHECK(D == (int32_t)H);
+        size_t same = 0;
+        for (size_t d = 0; d < H; d++) {
+            float v;
+            std::memcpy(&v, f.data() + 4 + 4 * d, 4);
+            same += v == (float)(acc[k][d] / acc[k][H]);
+        }
+        CHECK(same == H);
+        float w;
+        std::memcpy(&w, f.data() + 4 + 4 * H, 4);
+        CHECK(w == (float)acc[k][H]);
+    }
+    tr.save_adapter((dir / "out").string());
+    auto m = read_file(dir / "out" / "adapter.centroid");
+    CHECK(m.size() == 8 + 2 * 4 * H);
+    if (m.size() == 8 + 2 * 4 * H) {
+        int32_t k, D;
+        std::memcpy(&k, m.data(), 4);
+        std::memcpy(&D, m.data() + 4, 4);
+        CHECK(k == 2 && D == (int32_t)H);
+        for (int j = 0; j < 2; j++) {
+            size_t same = 0;
+            for (size_t d = 0; d < H; d++) {
+                float v;
+                std::memcpy(&v, m.data() + 8 + 4 * (j * H + d), 4);
+                same += v == (float)(acc[j][d] / acc[j][H]);
+            }
+            CHECK(same == H);
+        }
+    }
+}
+
 int main(int argc, char** argv) {
     if (argc < 3) {
         std::printf("usage: %s cpu|gpu <dir>\n", argv[0]);
@@ -594,6 +724,8 @@ int main(int argc, char** argv) {
             cpu_tests(dir);
         else if (mode == "gpu")
             gpu_tests(dir);
+        else if (mode == "c2sched")
+            c2_schedule_tests(dir);
         else
             return 2;
     } catch (const std::exception& e) {

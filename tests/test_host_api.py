@@ -166,3 +166,18 @@ def test_host_api_gpu(tmp_path):
     r = subprocess.run([_binary(), "gpu", str(tmp_path)], capture_output=True, text=True,
                        timeout=110)
     assert r.returncode == 0, r.stdout + r.stderr[-2000:]
+
+
+@pytest.mark.gpu
+def test_c2_schedule_through_trainer(tmp_path):
+    """BASELINE configs[1] on its own schedule through AdaptTrainer: 20 AdamW
+    steps of the Qwen2-0.5B shape (B=4 x T=512, r=16 on q,k,v,o) with a
+    centroid snapshot every 10 steps; the two snapshot files' layout and
+    cumulative C / W, the lr schedule and the merged file are checked in
+    tests/cpp/test_host_api.cpp (c2_schedule_tests).  The centroid sums
+    themselves are compared with the oracle over c2's first two steps in
+    tests/test_gpu_c2.py."""
+    print("case: test_host_api c2sched", flush=True)
+    r = subprocess.run([_binary(), "c2sched", str(tmp_path)], capture_output=True, text=True,
+                       timeout=170)
+    assert r.returncode == 0, r.stdout + r.stderr[-2000:]
