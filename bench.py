@@ -264,6 +264,9 @@ def main():
                     help="print the per-kernel-class time split to stderr")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run one plain device copy of MIB MiB first (counter calibration)")
+    ap.add_argument("--ce-in-dx", action="store_true",
+                    help="the measured alternative: cross-entropy gradient formed inside the LM "
+                         "head's input-gradient GEMM (TA_ENGINE_CE_IN_DX)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU (one process, one MI355X); "
@@ -276,7 +279,7 @@ def main():
     import tadapt
 
     model, adapt, B, T, recompute, workload = CONFIGS[args.config]
-    eng = tadapt.Engine(model, adapt, B, T, recompute=recompute)
+    eng = tadapt.Engine(model, adapt, B, T, recompute=recompute, ce_in_dx=args.ce_in_dx)
     eng.init_random(seed=20261201, std=0.02)
     nb = args.warmup + args.steps + len(CAT_NAMES) + len(tadapt.KPROF_KERNELS)
     batches = token_batches(nb, B, T, model["vocab"], 1)
@@ -385,7 +388,8 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (uniform random token ids; random-init N(0,0.02) BF16 base)",
-        "config": {"workload": workload,
+        "config": {"workload": workload + (" (cross-entropy gradient inside the LM head's "
+                                           "input-gradient GEMM)" if args.ce_in_dx else ""),
                    "global_batch": B, "seq_len": T, "layers": model["layers"],
                    "hidden": model["hidden"], "parallelism": "single GPU"},
         "roofline": roof,

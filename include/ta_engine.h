@@ -75,8 +75,16 @@ void* ta_engine_create(const ta_model_config* model, const ta_adapt_config* adap
  *   backward reruns a layer's forward into one shared activation set just
  *   before that layer's backward.  Results are bit-identical to the cached
  *   step; the cost is one more forward of every layer but the last.
- * Named buffers of the shared set read as "work.<name>" ("work.x_normed"). */
-enum { TA_ENGINE_RECOMPUTE = 1 };
+ * Named buffers of the shared set read as "work.<name>" ("work.x_normed").
+ *   TA_ENGINE_CE_IN_DX: the cross entropy writes no dlogits, only the loss
+ *   and each row's normaliser; the LM head's input-gradient GEMM forms
+ *   dlogits from the logits as it reads them (bit-identical results; the
+ *   "logits" buffer then keeps the logits).  Measured slower than the
+ *   default two-pass form on MI355X (the exponentials run once per output
+ *   column tile instead of once); kept as the measured alternative.  Needs
+ *   vocab % 64 == 0, vocab <= 163840, hidden >= 192 and B*T >= 256, else the
+ *   step uses the default form. */
+enum { TA_ENGINE_RECOMPUTE = 1, TA_ENGINE_CE_IN_DX = 2 };
 void* ta_engine_create_ex(const ta_model_config* model, const ta_adapt_config* adapt, int B, int T,
                           void* stream, int flags);
 int ta_engine_destroy(void* engine);

@@ -74,6 +74,10 @@ struct Engine {
     // kept per layer; the other cached activations live in one shared set
     // that the backward refills by rerunning the layer's forward
     bool recompute = false;
+    // the cross-entropy gradient formed inside the LM head's dX GEMM
+    // (TA_ENGINE_CE_IN_DX): lse2 holds each row's base-2 normaliser
+    bool ce_in_dx = false;
+    float* lse2 = nullptr;
     hipStream_t s = nullptr;
     bool own_stream = false;
     std::vector<void*> allocs;
@@ -386,6 +390,7 @@ static int engine_alloc(Engine* e) {
     CK(alloc(e, &e->xfn, (int64_t)BT * H, "xfn", 0));
     CK(alloc(e, &e->logits, (int64_t)BT * V, "logits", 0));
     CK(alloc(e, &e->loss_tok, BT, "loss_tok", 1));
+    if (e->ce_in_dx) CK(alloc(e, &e->lse2, BT, "lse2", 1));
     CK(alloc(e, &e->g_res, (int64_t)BT * H, "grad", 0));
     CK(alloc(e, &e->dres, (int64_t)BT * H, "dres", 0));
     CK(alloc(e, &e->tmpH, (int64_t)BT * H, "tmpH", 0));
@@ -713,9 +718,14 @@ static int forward(Engine* e) {
     // loss (adapt_trainer.cu:201-205): dlogits overwrite the logits in place
     // (one read and one write of BT x V BF16); the first step also counts
     // the NaN and Inf logits (adapt_trainer.cu:196-198)
-    TIMED(TA_CAT_CE, 0, dBT * e->V * 4,
-          cross_entropy(e->logits, e->tgt_dev, e->loss_tok, e->logits, BT, e->V,
-                        e->step_count == 0 ? e->nonfinite_dev : nullptr, s));
+    if (e->ce_in_dx)  // loss and row normalisers only: one read of the logits
+        TIMED(TA_CAT_CE, 0, dBT * e->V * 2,
+              cross_entropy(e->logits, e->tgt_dev, e->loss_tok, nullptr, BT, e->V,
+                            e->step_count == 0 ? e->nonfinite_dev : nullptr, s, e->lse2));
+    else
+        TIMED(TA_CAT_CE, 0, dBT * e->V * 4,
+              cross_entropy(e->logits, e->tgt_dev, e->loss_tok, e->logits, BT, e->V,
+                            e->step_count == 0 ? e->nonfinite_dev : nullptr, s));
     return 0;
 }
 
@@ -727,9 +737,14 @@ static int backward(Engine* e) {
     const double nrm_b = dBT * H * 6 + H * 2 + dBT * 4;
     e->wg_cursor = 0;
     // dres = dlogits * W_lm (qwen2.cu:205); grad = rms_norm_bwd(final)
-    TIMED(TA_CAT_LMHEAD_BWD, gflops(BT, H, e->V), gbytes(BT, H, e->V, 2, 2, false),
-          gemm_dispatch(true, true, BT, H, e->V, 1.f, e->logits, e->V, e->lmT, e->V, 0.f, e->dres,
-                        H, nullptr, false, s, 0, nullptr));
+    if (e->ce_in_dx)
+        TIMED(TA_CAT_LMHEAD_BWD, gflops(BT, H, e->V), gbytes(BT, H, e->V, 2, 2, false),
+              gemm_ce_dx(BT, H, e->V, e->logits, e->lmT, e->dres, e->lse2, e->tgt_dev,
+                         1.f / (float)BT, s));
+    else
+        TIMED(TA_CAT_LMHEAD_BWD, gflops(BT, H, e->V), gbytes(BT, H, e->V, 2, 2, false),
+              gemm_dispatch(true, true, BT, H, e->V, 1.f, e->logits, e->V, e->lmT, e->V, 0.f,
+                            e->dres, H, nullptr, false, s, 0, nullptr));
     TIMED(TA_CAT_NORM, 0, nrm_b,
           ta_rms_norm_bwd(e->dres, e->x_final, e->final_norm, e->final_rms, e->g_res, nullptr, 1,
                           BT, H, c.rms_eps, s));
@@ -984,7 +999,8 @@ void* ta_engine_create(const ta_model_config* mc, const ta_adapt_config* ac, int
 
 void* ta_engine_create_ex(const ta_model_config* mc, const ta_adapt_config* ac, int B, int T,
                           void* stream, int flags) {
-    if (!mc || !ac || B <= 0 || T <= 0 || (flags & ~TA_ENGINE_RECOMPUTE) != 0) {
+    if (!mc || !ac || B <= 0 || T <= 0 ||
+        (flags & ~(TA_ENGINE_RECOMPUTE | TA_ENGINE_CE_IN_DX)) != 0) {
         set_error(-1, "engine_create: bad arguments");
         return nullptr;
     }
@@ -1011,6 +1027,9 @@ void* ta_engine_create_ex(const ta_model_config* mc, const ta_adapt_config* ac, 
     e->r = (ac->rank + 15) / 16 * 16;
     e->scale = ac->alpha / (float)ac->rank;  // adapter_model.cu:139
     e->recompute = (flags & TA_ENGINE_RECOMPUTE) != 0;
+    // (the CE kernel's row-in-registers form and the GEMM's tile shapes)
+    e->ce_in_dx = (flags & TA_ENGINE_CE_IN_DX) != 0 && e->V % 64 == 0 && e->V <= 163840 &&
+                  e->H >= 192 && e->H % 8 == 0 && e->BT >= 256;
     if (stream) {
         e->s = (hipStream_t)stream;
     } else {

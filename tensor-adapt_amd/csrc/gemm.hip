@@ -100,6 +100,11 @@ struct GemmArgs {
     int64_t sldx[3];
     const bf16* sY[3];
     int64_t sldy[3];
+    // cross-entropy gradient formed from X = logits in the operand reads
+    // (k_gemm_pipe_ce): per-row base-2 normaliser, target id, 1 / N
+    const float* ce_lse2;
+    const int32_t* ce_tgt;
+    float ce_inv_n;
 };
 
 // Load one 16-byte chunk (8 bf16) of a K-contiguous operand row with
@@ -1013,6 +1018,34 @@ __device__ __forceinline__ void round_acc(floatx16 (&acc)[TM][TN]) {
             for (int r = 0; r < 16; r++) acc[i][j][r] = bf2f(f2bf(acc[i][j][r]));
 }
 
+// dlogits from the logits of a wave's X fragments (k_gemm_pipe_ce): lane l
+// holds 8 consecutive k (columns kb .. kb + 7) of the row whose normaliser
+// and target are ls2[i], tg[i]; the same operations as k_cross_entropy_reg,
+// so the same bits.  Stages before the first (kt < 0) hold zeros and stay.
+template <int TM>
+__device__ __forceinline__ void ce_frags(bf16x8_t (&fa)[TM], int kt, int kk, const float (&ls2)[TM],
+                                         const int (&tg)[TM], float inv_n, int lane) {
+    if (kt < 0) return;
+    const int kb = kt * 64 + 16 * kk + 8 * (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+        const u32x4_t w = __builtin_bit_cast(u32x4_t, fa[i]);
+        u32x4_t o;
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            float d[2];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const float f = h ? hi2f(w[q]) : lo2f(w[q]);
+                const float p = __builtin_amdgcn_exp2f(fmaf(f, kLog2e, -ls2[i]));
+                d[h] = (p - (float)(kb + 2 * q + h == tg[i])) * inv_n;
+            }
+            o[q] = pack2(d[0], d[1]);
+        }
+        fa[i] = __builtin_bit_cast(bf16x8_t, o);
+    }
+}
+
 // CHAIN: K segments (a.nseg > 1).  SWIGLU: Y is the gate/up weight pair
 // interleaved in blocks of 128 rows, so tile tn holds gate and up columns
 // [128 tn, 128 tn + 128); gate waves (wn < 2) write gate, up waves up, each
@@ -1024,8 +1057,11 @@ __device__ __forceinline__ void round_acc(floatx16 (&acc)[TM][TN]) {
 // KD = 64: two stages of 64 k in the same LDS, rows of one whole 128-byte
 // line, so every line of an operand is fetched once; the next stage's load
 // has the same 64 k of compute to land in as with four 32-k stages.
-template <int BN, int WMW, int WNW, bool CHAIN, bool SWIGLU = false, int KD = 32, int BM = 256>
+// CEX: X holds logits and the MFMAs take dlogits formed from them (ce_frags).
+template <int BN, int WMW, int WNW, bool CHAIN, bool SWIGLU = false, int KD = 32, int BM = 256,
+          bool CEX = false>
 __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmArgs& a0) {
+    static_assert(!CEX || (KD == 64 && !CHAIN && !SWIGLU), "CE operand form");
     static_assert(KD == 32 || KD == 64, "stage depth");
     constexpr int NS = KD == 32 ? 4 : 2, NW = WMW * WNW;
     constexpr int WTM = BM / WMW, WTN = BN / WNW;
@@ -1074,6 +1110,20 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
     int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int wm = w / WNW, wn = w % WNW;
     w = __builtin_amdgcn_readfirstlane(w);
+    float ce_l2[TM];
+    int ce_t[TM];
+    if constexpr (CEX) {
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+            const int row = min(m0 + wm * WTM + i * 32 + (lane & 31), a0.M - 1);
+            ce_l2[i] = a0.ce_lse2[row];
+            ce_t[i] = a0.ce_tgt[row];
+        }
+    }
+#define PIPE_CE(F, KT, KK)                                                       \
+    do {                                                                         \
+        if constexpr (CEX) ce_frags<TM>((F).a, (KT), (KK), ce_l2, ce_t, a0.ce_inv_n, lane); \
+    } while (0)
 
     // these loads are older than every stage load, so the prologue's wait
     // for stage 0 covers them; the main loop's barriers publish them
@@ -1255,21 +1305,26 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
     TA_WAIT_VMCNT(LPS);
     __builtin_amdgcn_s_barrier();
     pipe_frags<TM, TN, WTM, WTN, KD>(f0, sX0, sY0, wm, wn, lane, 0);
+    PIPE_CE(f0, -pad, 0);
 #define PIPE_STEP(J, SXJ, SYJ, SXN, SYN)                                                   \
     do {                                                                                   \
         pipe_frags<TM, TN, WTM, WTN, KD>(f1, SXJ, SYJ, wm, wn, lane, 1);                   \
+        PIPE_CE(f1, kt0 + (J), 1);                                                         \
         pipe_mma<TM, TN>(acc, f0);                                                         \
         pipe_interleave<TM * TN, TM + TN>();                                               \
         pipe_frags<TM, TN, WTM, WTN, KD>(f0, SXJ, SYJ, wm, wn, lane, 2);                   \
+        PIPE_CE(f0, kt0 + (J), 2);                                                         \
         pipe_mma<TM, TN>(acc, f1);                                                         \
         pipe_interleave<TM * TN, TM + TN>();                                               \
         pipe_frags<TM, TN, WTM, WTN, KD>(f1, SXJ, SYJ, wm, wn, lane, 3);                   \
+        PIPE_CE(f1, kt0 + (J), 3);                                                         \
         pipe_mma<TM, TN>(acc, f0);                                                         \
         pipe_interleave<TM * TN, TM + TN>();                                               \
         __builtin_amdgcn_s_waitcnt(0x0070); /* vmcnt(0) lgkmcnt(0) */                      \
         __builtin_amdgcn_s_barrier();                                                      \
         if (kt0 + (J) + 2 < nk) PIPE_ISSUE(SXJ, SYJ, kt0 + (J) + 2);                       \
         pipe_frags<TM, TN, WTM, WTN, KD>(f0, SXN, SYN, wm, wn, lane, 0);                   \
+        PIPE_CE(f0, kt0 + (J) + 1, 0);                                                     \
         pipe_mma<TM, TN>(acc, f1);                                                         \
         pipe_interleave<TM * TN, TM + TN>();                                               \
     } while (0)
@@ -1281,6 +1336,7 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
 #undef PIPE_STEP
     }
     TA_WAIT_VMCNT(0);  // the surplus loads have landed before the buffers are reused
+#undef PIPE_CE
 #undef PIPE_ROUND
 #undef PIPE_ISSUE
 #undef PIPE_ISSUE_P
@@ -1379,6 +1435,13 @@ template <int BN, int WMW, int WNW, int KD = 32>
 __global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
     WMW * WNW / 4, WMW * WNW / 4))) void k_gemm_pipe_swiglu(GemmArgs a) {
     gemm_pipe_body<BN, WMW, WNW, false, true, KD>(a);
+}
+// The LM head's input gradient with the cross-entropy gradient formed in the
+// operand reads (gemm_ce_dx).
+template <int BN, int WMW, int WNW>
+__global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
+    WMW * WNW / 4, WMW * WNW / 4))) void k_gemm_pipe_ce(GemmArgs a) {
+    gemm_pipe_body<BN, WMW, WNW, false, false, 64, 256, true>(a);
 }
 // 128-row tiles (128 x BN, BN = 64 or 128; four waves of 64-row wave tiles,
 // two 64-k stages): the same pipeline and epilogue for outputs too small to
@@ -2145,6 +2208,40 @@ __global__ void k_split3(const float* __restrict__ S, int64_t ld, bool kcontig, 
 #pragma unroll
         for (int q = 0; q < 6; q++) row[(int64_t)q * kp] = p[(code >> (2 * q)) & 3u];
     }
+}
+
+int gemm_ce_dx(int M, int N, int K, const bf16* logits, const bf16* Wt, bf16* C,
+               const float* lse2, const int32_t* tgt, float inv_n, hipStream_t s) {
+    TA_REQUIRE(M >= 256 && N >= 192 && K % BK == 0 && al16(logits) && al16(Wt) && al16(C) &&
+                   (N % 8) == 0 && K < kMaxStageLd && lse2 && tgt,
+               "gemm_ce_dx: unsupported shape M=%d N=%d K=%d", M, N, K);
+    GemmArgs a{};
+    a.M = M;
+    a.N = N;
+    a.K = K;
+    a.X = logits;
+    a.ldx = K;
+    a.Y = Wt;
+    a.ldy = K;
+    a.C = C;
+    a.ldc = N;
+    a.alpha = 1.f;
+    a.beta = 0.f;
+    a.k_per_split = K;
+    a.ngroups = 1;
+    a.nseg = 1;
+    a.ce_lse2 = lse2;
+    a.ce_tgt = tgt;
+    a.ce_inv_n = inv_n;
+    const int BNb = N > 3072 ? 256 : 192;
+    a.tiles_m = (M + 255) / 256;
+    a.tiles_n = (N + BNb - 1) / BNb;
+    dim3 grid(a.tiles_m * a.tiles_n);
+    if (BNb == 192)
+        k_gemm_pipe_ce<192, 4, 2><<<grid, 512, 0, s>>>(a);
+    else
+        k_gemm_pipe_ce<256, 2, 4><<<grid, 512, 0, s>>>(a);
+    return check_launch("gemm_ce_dx");
 }
 
 }  // namespace ta

@@ -135,7 +135,8 @@ __global__ __launch_bounds__(1024) void k_cross_entropy_reg(const bf16* __restri
                                                             float* __restrict__ loss,
                                                             bf16* __restrict__ dlogits, int V,
                                                             float inv_N,
-                                                            int32_t* __restrict__ nonfinite) {
+                                                            int32_t* __restrict__ nonfinite,
+                                                            float* __restrict__ lse2_out) {
     __shared__ float red[16], tls;
     const int64_t n = blockIdx.x;
     const bf16x8v* L = (const bf16x8v*)(logits + n * (int64_t)V);
@@ -193,15 +194,18 @@ __global__ __launch_bounds__(1024) void k_cross_entropy_reg(const bf16* __restri
     }
     const float S = block_sum16(sum, red);
     const float log_sum = logf(S) + M;
+    const float ls2 = log_sum * kLog2e;
     if (threadIdx.x == 0) {
         // a target outside [0, V) reads nothing (the reference would read out
         // of bounds for tgt >= V; ids come from a vocab-sized tokenizer)
         const float tl = (tgt >= 0 && tgt < V) ? tls : 0.f;
         loss[n] = -(tl - log_sum);
+        // the row's base-2 normaliser, from which dlogits can be formed
+        // elsewhere with the same bits (ce_dlogit8)
+        if (lse2_out) lse2_out[n] = ls2;
     }
     if (!dlogits) return;
     bf16x8v* dL = (bf16x8v*)(dlogits + n * (int64_t)V);
-    const float ls2 = log_sum * kLog2e;
 #pragma unroll
     for (int k = 0; k < CPT; k++) {
         const int c = threadIdx.x + 1024 * k;
@@ -219,10 +223,17 @@ __global__ __launch_bounds__(1024) void k_cross_entropy_reg(const bf16* __restri
 }
 
 // cross_entropy_fwd that also adds the count of NaN and Inf logits to
-// *nonfinite when it is not null (a device int32 the caller zeroes)
+// *nonfinite when it is not null (a device int32 the caller zeroes), and
+// writes each row's base-2 normaliser to lse2_out when it is not null (then
+// the row-in-registers kernel must take the shape: cross_entropy_lse_ok)
+bool cross_entropy_lse_ok(const bf16* logits, int V) {
+    return (V & 7) == 0 && ((uintptr_t)logits & 15u) == 0 && (V / 8 + 1023) / 1024 <= 20;
+}
 int cross_entropy(const bf16* logits, const int32_t* targets, float* loss_out, bf16* dlogits,
-                  int N, int V, int32_t* nonfinite, hipStream_t s) {
+                  int N, int V, int32_t* nonfinite, hipStream_t s, float* lse2_out) {
     TA_REQUIRE(N >= 0 && V > 0, "cross_entropy_fwd: bad shape N=%d V=%d", N, V);
+    TA_REQUIRE(!lse2_out || cross_entropy_lse_ok(logits, V),
+               "cross_entropy: row normalisers need V %% 8 == 0 and V <= 163840");
     if (N == 0) return 0;
     // divisor = number of rows, masked rows included (gridDim.x in ops.cu:1005)
     float inv_N = 1.f / (float)N;
@@ -234,7 +245,7 @@ int cross_entropy(const bf16* logits, const int32_t* targets, float* loss_out, b
     if (vec && cpt <= 20) {
 #define CE(C, K)                                                                      \
     k_cross_entropy_reg<C, K><<<N, 1024, 0, s>>>(logits, targets, loss_out, dlogits, V, inv_N, \
-                                                 nonfinite)
+                                                 nonfinite, lse2_out)
 #define CE2(C) \
     if (nonfinite) CE(C, true); else CE(C, false)
         if (cpt <= 4) { CE2(4); }
@@ -260,5 +271,6 @@ using namespace ta;
 extern "C" int ta_cross_entropy_fwd(const uint16_t* logits, const int32_t* targets,
                                     float* loss_out, uint16_t* dlogits, int N, int V,
                                     void* stream) {
-    return cross_entropy(logits, targets, loss_out, dlogits, N, V, nullptr, (hipStream_t)stream);
+    return cross_entropy(logits, targets, loss_out, dlogits, N, V, nullptr, (hipStream_t)stream,
+                         nullptr);
 }

@@ -117,7 +117,15 @@ int transpose_bf16(const bf16* in, bf16* out, int64_t rows, int64_t cols, hipStr
 // Inf logits to *nonfinite when it is not null (a device int32 the caller
 // zeroes)
 int cross_entropy(const bf16* logits, const int32_t* targets, float* loss_out, bf16* dlogits,
-                  int N, int V, int32_t* nonfinite, hipStream_t s);
+                  int N, int V, int32_t* nonfinite, hipStream_t s, float* lse2_out = nullptr);
+// whether cross_entropy can write the row normalisers for these logits
+bool cross_entropy_lse_ok(const bf16* logits, int V);
+// dX = dlogits W of the LM head with dlogits formed from the logits inside
+// the GEMM's operand reads: dlogits[t][v] = bf16((exp2(l log2(e) - lse2[t])
+// - [v == tgt[t]]) / N), the bits cross_entropy writes (X = logits [M x K],
+// Y = W^T [N x K], C = dX [M x N], all K-contiguous, beta 0).
+int gemm_ce_dx(int M, int N, int K, const bf16* logits, const bf16* Wt, bf16* C,
+               const float* lse2, const int32_t* tgt, float inv_n, hipStream_t s);
 int fill_normal_bf16(bf16* out, int64_t n, uint64_t seed, uint64_t sid, float std, hipStream_t s);
 int fill_bf16(bf16* out, int64_t n, float v, hipStream_t s);
 int kaiming_init(float* a32, bf16* a16, int64_t n, int in_dim, hipStream_t s);

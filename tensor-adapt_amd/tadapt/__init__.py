@@ -165,14 +165,17 @@ class Engine:
     """Owner of one ta_engine_* handle (the MI355X LoRA step)."""
 
     RECOMPUTE = 1  # TA_ENGINE_RECOMPUTE
+    CE_IN_DX = 2   # TA_ENGINE_CE_IN_DX
 
-    def __init__(self, model: dict, adapt: dict, B: int, T: int, recompute: bool = False):
+    def __init__(self, model: dict, adapt: dict, B: int, T: int, recompute: bool = False,
+                 ce_in_dx: bool = False):
         self.mc = ModelConfig(**model)
         self.ac = AdaptConfig(**adapt)
         self.B, self.T = B, T
         self.recompute = bool(recompute)
+        flags = (self.RECOMPUTE if recompute else 0) | (self.CE_IN_DX if ce_in_dx else 0)
         h = lib().ta_engine_create_ex(ctypes.byref(self.mc), ctypes.byref(self.ac), B, T, None,
-                                      self.RECOMPUTE if recompute else 0)
+                                      flags)
         if not h:
             raise BackendError("ta_engine_create failed: " + last_error())
         self.h = h

@@ -4,8 +4,9 @@ on q,k,v,o; B=4 x T=512) at full size against the CPU oracle, over two
 steps: loss within 1e-3 relative, grad norm within 1e-2, every gB (step 1)
 and every gA and gB (step 2, which starts from the oracle's state after
 step 1, so B != 0) within the bars below, the updated adapters within the
-same bars where the update is determined (check_band), and the update
-exactly AdamW of the engine's own gradients.
+same bars where the update is determined (check_band), the update
+exactly AdamW of the engine's own gradients, and the centroid sums (all 24
+layers, accumulated over both steps) within 2x their floor.
 
 Bars from a measured floor, not 1e-2.  tests/golden/c2_accum_floor.json
 (written by oracle/accum_floor.py, same seeds and procedure as this test)
@@ -13,7 +14,8 @@ holds, per tensor, the distance between two CPU oracles that differ only in
 accumulation: the FP64 one and one with FP32 accumulators fed by 16-wide K
 blocks, as a matrix-core GEMM accumulates; every BF16 rounding point of the
 reference is the same in both.  That distance is 0.7e-2 to 3.1e-2 (median
-2.3e-2): with about 90% of the BF16 values one ulp apart after a few layers,
+2.3e-2; 1.9e-3 and 1.7e-3 for the centroid sums after steps 1 and 2): with
+about 90% of the BF16 values one ulp apart after a few layers,
 the differences of every layer's roundings add up over the 24 layers, so no
 FP32-accumulating implementation (cuBLAS included) can meet 1e-2 here.
 Each engine gradient must lie within 2x its tensor's floor, and the median
@@ -74,4 +76,12 @@ def test_c2_full_model_matches_oracle():
         check_adamw_of_own_grads(eng, mc, ac, state, sg["lr"], step + 1, sg["gnorm_raw"])
         check_band(orc, eng, mc, ac, before={k: v for k, v in state.items() if k[2] in "AB"},
                    bar=lambda l, t, g: 2.0 * fl.get(f"l{l}.{t}.{g}", 5e-3))
+        ca, cw = eng.centroid()
+        oa, ow = orc.centroid()
+        cf = floor[step]["centroid"]
+        rc = rel(ca, oa)
+        print(f"step {step}: centroid sums {rc:.3e} (floor {cf['sums']:.3e}), weight "
+              f"{abs(cw - ow) / ow:.3e} (floor {cf['weight']:.3e})", flush=True)
+        assert rc <= 2.0 * cf["sums"], (rc, cf)
+        assert abs(cw - ow) <= 2.0 * max(cf["weight"], 1e-6) * ow, (cw, ow, cf)
     eng.close()

@@ -337,3 +337,33 @@ def test_first_step_counts_nonfinite_logits():
     assert m["nonfinite_logits"] == 2 * B * T, m
     assert eng.step(inp, tgt)["nonfinite_logits"] == -1
     eng.close()
+
+
+def test_ce_in_dx_step_bit_identical():
+    """TA_ENGINE_CE_IN_DX (the cross-entropy gradient formed inside the LM
+    head's input-gradient GEMM from the logits and each row's normaliser,
+    instead of a dlogits pass; ops.cu:958-1020, qwen2.cu:205) forms the same
+    dlogits bits as the cross-entropy kernel and runs the same GEMM tiles in
+    the same order, so at the headline shape (one c3 layer, B=8 x T=1024,
+    the full 151936 vocabulary) two steps agree bit for bit with the default
+    engine: loss, norm, the LM head's dX (dres), every gradient and every
+    updated adapter."""
+    mc = dict(vocab=151936, hidden=1536, layers=1, n_q=12, n_kv=2, head_dim=128, inter=8960,
+              rms_eps=1e-6, rope_theta=1e6, tie=1)
+    ac = dict(SMALL_ADAPT, total_steps=10)
+    B, T = 8, 1024
+    a, b = tadapt.Engine(mc, ac, B, T), tadapt.Engine(mc, ac, B, T, ce_in_dx=True)
+    a.init_random(43)
+    b.init_random(43)
+    rng = np.random.default_rng(41)
+    for step in range(2):
+        toks = chat_tokens(mc["vocab"], B, T + 1, rng)[:B * T + 1]
+        inp, tgt = toks[:-1].copy(), toks[1:].copy()
+        ma, mb = a.step(inp, tgt), b.step(inp, tgt)
+        assert ma["loss"] == mb["loss"] and ma["gnorm_raw"] == mb["gnorm_raw"], (ma, mb)
+        assert np.array_equal(a.read_buffer("dres"), b.read_buffer("dres")), step
+        for l, tg in pairs(mc, ac):
+            for w in ("gA", "gB", "A", "B", "A16", "B16"):
+                assert np.array_equal(a.adapter(l, tg, w), b.adapter(l, tg, w)), (step, l, tg, w)
+    a.close()
+    b.close()
