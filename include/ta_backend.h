@@ -8,7 +8,9 @@
  * uint16_t bit patterns.  Nothing here allocates on the caller's behalf unless
  * the comment says so; ops that need scratch memory draw it from the
  * library's pool, one set of grow-only buffers per (device, stream), so
- * calls on different streams never share scratch (freed at exit).
+ * calls on different streams never share scratch.  A stream's buffers live
+ * until ta_scratch_release(stream) or the process ends: release them before
+ * destroying a stream (a new stream may get the old handle value).
  *
  * Each declaration names the reference function it replaces (paths are in
  * carbon-os/tensor-adapt).  Layout conventions are the reference's: activations
@@ -241,6 +243,12 @@ int ta_mem_alloc(void** ptr, int64_t bytes, int device);
 int ta_mem_free(void* ptr, int device);
 int ta_mem_stats(int device, int64_t* in_use, int64_t* cached);
 int ta_mem_trim(int device);
+/* Waits for `stream` (on the current device) and frees the scratch buffers
+ * the library keeps for it; the next op on that stream allocates afresh.
+ * For hosts that create and destroy streams (one per request, say): call
+ * it before hipStreamDestroy.  No reference counterpart (the reference
+ * allocates per call). */
+int ta_scratch_release(void* stream);
 
 /* ── kernel-level timing (measurement; no reference counterpart) ─────
  * ta_kprof_select(kid) starts timing every launch of one kernel (ids: 0 the

@@ -5,7 +5,11 @@
 //                        keys in sorted order, data in tensor order
 //                        (layer by layer; q, k, v, o, then gate, up, down;
 //                        lora_A before lora_B), header padded with spaces to
-//                        a multiple of 8 bytes;
+//                        a multiple of 8 bytes; the tensor set is the
+//                        projections the AdapterConfig's inject flags name
+//                        (the reference writes q, k, v and o whatever they
+//                        say, so a configuration with MLP targets or without
+//                        one of q, k, v, o writes a different set);
 //   adapter.json         run metadata, 2-space indented, keys sorted;
 //   train_state.json     {"step", "tokens_consumed"} (checkpoints only).
 // A checkpoint here also stores optimizer.safetensors: each tensor's F32

@@ -245,6 +245,20 @@ int ta_mem_trim(int device) {
     return 0;
 }
 
+int ta_scratch_release(void* stream) {
+    hipStream_t s = (hipStream_t)stream;
+    int dev = 0;
+    TA_HIP(hipGetDevice(&dev));
+    TA_HIP(hipStreamSynchronize(s));
+    std::lock_guard<std::mutex> lk(ta::g_scratch_mu);
+    auto it = ta::g_scratch.find({dev, s});
+    if (it == ta::g_scratch.end()) return 0;
+    for (auto& sc : it->second.slot)
+        if (sc.ptr) (void)hipFree(sc.ptr);
+    ta::g_scratch.erase(it);
+    return 0;
+}
+
 const char* ta_kprof_name(int kid) {
     if (kid < 0 || kid >= ta::KP_COUNT) return "";
     const char* n = ta::g_kp.name[kid];

@@ -595,6 +595,17 @@ struct AdaptTrainer::Impl {
                            cfg.adam_beta2, cfg.adam_eps, cfg.weight_decay};
         if (hipSetDevice(dev->id()) != hipSuccess)
             throw CudaError("AdaptTrainer: hipSetDevice failed");
+        // the reference trains q, k, v and o whatever the flags say
+        // (adapter_model.cu:83-86); here every flag is honoured
+        if (cfg.inject_gate || cfg.inject_up || cfg.inject_down || !cfg.inject_q ||
+            !cfg.inject_k || !cfg.inject_v || !cfg.inject_o)
+            std::cerr << "[trainer] note: training LoRA on the projections the inject flags name ("
+                      << (cfg.inject_q ? "q " : "") << (cfg.inject_k ? "k " : "")
+                      << (cfg.inject_v ? "v " : "") << (cfg.inject_o ? "o " : "")
+                      << (cfg.inject_gate ? "gate " : "") << (cfg.inject_up ? "up " : "")
+                      << (cfg.inject_down ? "down " : "")
+                      << "); the reference trains q, k, v and o only, so adapter.safetensors "
+                         "holds a different tensor set\n";
         eng = ta_engine_create(&mc, &ac, B, T, dev->stream());
         if (!eng) throw CudaError(std::string("AdaptTrainer: ") + ta_last_error());
         try {

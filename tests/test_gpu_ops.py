@@ -192,6 +192,23 @@ def test_sum_sq_into():
     assert abs(host(acc)[0] - (2.0 + O.sum_sq(g))) <= 1e-6 * O.sum_sq(g)
 
 
+def test_scratch_release_on_a_stream_of_its_own():
+    """An op on a new stream takes scratch of its own from the pool;
+    ta_scratch_release frees it (after the stream is idle) and the next call
+    on that stream allocates afresh and gives the same result."""
+    g = RNG.standard_normal(300001).astype(np.float32)
+    tg = dev(g)
+    st = torch.cuda.Stream()
+    out = []
+    for _ in range(2):
+        acc = dev(np.zeros(1, np.float32))
+        torch.cuda.synchronize()
+        call("ta_sum_sq_into", P(tg), P(acc), g.size, ctypes.c_void_p(st.cuda_stream))
+        call("ta_scratch_release", ctypes.c_void_p(st.cuda_stream))
+        out.append(host(acc)[0])
+    assert out[0] == out[1] and abs(out[0] - O.sum_sq(g)) <= 1e-6 * O.sum_sq(g)
+
+
 # ── GEMM ──────────────────────────────────────────────────────────────────
 def check_gemm_close(got, want, what):
     r = rel_l2(f32(got), f32(want))
