@@ -40,6 +40,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "lds_tr.hpp"
 #include "ta_internal.hpp"
@@ -868,37 +869,57 @@ __global__ __launch_bounds__(256, 2) void k_attn_bwd_dq_t(const bf16* __restrict
 }
 
 // ── backward dK/dV, keys on the lanes (the engine's form: P recomputed) ───
-// Per block: 128 keys of one (b, kv head), 4 waves of 32, and a run of the
-// query heads of its GQA group [h0, h1).  The block walks (head, 64-query
-// tile) steps; each step's Q and dO tiles (xr_off layout) and the tile's
-// 1 KB of per-query values come straight into LDS by buffer-load DMA, three
-// buffer sets deep, as the K/V tiles of k_attn_fwd_t.  The wave's K and V
-// rows stay in accumulation registers as MFMA B operands: S = Q K^T and dP = dO V^T
-// (32 queries x 32 keys per MFMA tile, Q and dO rows read as A operands),
-// so lane l holds key l%32 and queries 8(r/4) + 4(l/32) + r%4 of each
-// 32-query half.  P = exp2(S scale log2(e) - lse2), exactly as the dQ pass
-// forms it, and dS = P (dP - D) (ops.cu:405-435) stay in registers
-// and, with the queries of a 16-wide k step taken in that order, are the B
-// operands (BF16 hi/lo) of dV^T += dO^T P and dK^T += Q^T dS, whose A
-// operands come from the same tiles through transposing reads.  The run's
-// heads accumulate in registers; a run covering the whole group writes dK
-// (times scale) and dV in BF16, otherwise each run writes F32 partials that
-// k_attn_dkv_sum adds in run order — the group sum of ops.cu:539-555 with
-// no atomics, so dK/dV are deterministic.
+// Per block: 128 keys of one (b, kv head) and a run of the query heads of
+// its GQA group [h0, h1).  The block walks (head, 64-query tile) steps; each
+// step's Q and dO tiles (xr_off layout) and the tile's 1 KB of per-query
+// values come straight into LDS by buffer-load DMA, three stages deep, as
+// the K/V tiles of k_attn_fwd_t.  S = Q K^T and dP = dO V^T run as 32
+// queries x 32 keys MFMA tiles with the keys' rows as B operands held in
+// accumulation registers, so lane l holds key l%32 and queries
+// 8(r/4) + 4(l/32) + r%4 of each 32-query half.  P = exp2(S scale log2(e) -
+// lse2), exactly as the dQ pass forms it, and dS = P (dP - D)
+// (ops.cu:405-435), with the queries of a 16-wide k step taken in that
+// order, are the B operands (BF16 hi/lo) of dV^T += dO^T P and
+// dK^T += Q^T dS, whose A operands come from the same tiles through
+// transposing reads.
+// The work of each 32-key group is split between two waves of different
+// roles, so that two waves share each SIMD and one's VALU work overlaps the
+// other's MFMAs.  Block: 8 waves; waves w and w + 4 own keys
+// kb*128 + 32w .. +31.
+//   V role (w < 4): S, P (masked on the diagonal), P to LDS; then dV^T.  It
+//     also issues the tile DMA.
+//   K role (w >= 4): dP; then, with P from LDS, dS and dK^T.
+// Per 32-query half each role runs 8 MFMAs before a block barrier (the V
+// role's exponentials overlap the K role's dP) and 16 after it; each
+// accumulator takes, per half, the lo then the hi product of the first
+// 16-query k step, then those of the second.  The barriers are reached by
+// every wave on every half, whether or not its keys take part in it.  P
+// travels in a buffer per half parity ([pair][4 row groups][64 lanes]
+// float4): a half's K-role reads end before the next half's barrier, which
+// the V role passes before it writes the same parity again.
+// The run's heads accumulate in registers; a run covering the whole group
+// writes dK (times scale) and dV in BF16, otherwise each run writes F32
+// partials that k_attn_dkv_sum adds in run order — the group sum of
+// ops.cu:539-555 with no atomics, so dK/dV are deterministic.
 template <int HD>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_attn_bwd_dkv_t(
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_attn_bwd_dkv_r(
     const bf16* __restrict__ dO, const bf16* __restrict__ Q, const bf16* __restrict__ K,
     const bf16* __restrict__ V, const float* __restrict__ qst, float* __restrict__ part,
     bf16* __restrict__ dK, bf16* __restrict__ dV, int T, int Hq, int Hkv, int nsplit,
     float scale) {
     constexpr int NST = HD / 16, NDB = HD / 32;
     constexpr int TB = TQ * HD * 2;
-    // DMA instructions per wave per step: Q and dO tiles, a quarter of the
-    // per-query block
+    // DMA instructions per V-role wave per step: Q and dO tiles, a quarter of
+    // the per-query block
     constexpr int LPT = 2 * (TB / 1024) / 4 + 1;
-    __shared__ __attribute__((aligned(1024))) char sQ0[TB], sQ1[TB], sQ2[TB];
-    __shared__ __attribute__((aligned(1024))) char sO0[TB], sO1[TB], sO2[TB];
-    __shared__ __attribute__((aligned(1024))) float sS0[QST], sS1[QST], sS2[QST];
+    // three stages of Q tile, dO tile and per-query block, addressed from a
+    // stage index that is not a compile-time constant, so that the compiler
+    // keeps one base per tile instead of a hoisted address per stage and
+    // fragment
+    __shared__ __attribute__((aligned(1024))) char sQ[3][TB];
+    __shared__ __attribute__((aligned(1024))) char sO[3][TB];
+    __shared__ __attribute__((aligned(1024))) float sS[3][QST];
+    __shared__ __attribute__((aligned(16))) float4 sP[2][4][4][64];
     const int nkb = (T + 127) / 128, nqt = (T + TQ - 1) / TQ, grp = Hq / Hkv;
     const int per = gridDim.x / nkb;               // B * Hkv * nsplit blocks per key block
     const int kb = (int)(blockIdx.x / per);       // low kb = most query tiles: launch first
@@ -906,27 +927,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     const int sp = rem % nsplit, bkv = rem / nsplit;
     const int B = per / (Hkv * nsplit), b = bkv / Hkv, hkv = bkv % Hkv;
     const int h0 = sp * grp / nsplit, h1 = (sp + 1) * grp / nsplit;
-    // the wave index as a scalar: conditions on it are uniform branches
-    const int lane = threadIdx.x & 63, w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // wave index and role as scalars: conditions on them are uniform branches
+    const int lane = threadIdx.x & 63, w8 = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int w = w8 & 3;
+    const bool vrole = w8 < 4;
     const int64_t qs = (int64_t)Hq * HD, ks_ = (int64_t)Hkv * HD;
     const int kw0 = kb * 128 + 32 * w, key = kw0 + (lane & 31);
-    bf16x8_t kf[NST], vf[NST];
+    // K rows (V role, the B operand of S) or V rows (K role, of dP)
+    bf16x8_t kv[NST];
     {
-        const bf16* Kh = K + (int64_t)b * T * ks_ + hkv * HD;
-        const bf16* Vh = V + (int64_t)b * T * ks_ + hkv * HD;
+        const bf16* src = (vrole ? K : V) + (int64_t)b * T * ks_ + hkv * HD;
 #pragma unroll
-        for (int st = 0; st < NST; st++) {
-            kf[st] = ld_head8(Kh, ks_, key, T, 16 * st + 8 * (lane >> 5));
-            vf[st] = ld_head8(Vh, ks_, key, T, 16 * st + 8 * (lane >> 5));
-        }
-        // K and V stay in accumulation registers for the whole kernel (the
-        // MFMAs read them there), leaving the vector registers to the
-        // pipelined Q / dO fragments
+        for (int st = 0; st < NST; st++) kv[st] = ld_head8(src, ks_, key, T, 16 * st + 8 * (lane >> 5));
 #pragma unroll
-        for (int st = 0; st < NST; st++) asm volatile("" : "+a"(kf[st]), "+a"(vf[st]));
+        for (int st = 0; st < NST; st++) asm volatile("" : "+a"(kv[st]));
     }
-    // per-lane LDS offsets within a tile: Q / dO rows for S and dP, and the
-    // two transposing reads of each 32-wide block of dO^T / Q^T
     int qoff[NST], toff[NDB][2];
 #pragma unroll
     for (int st = 0; st < NST; st++) qoff[st] = xr_off<HD / 8>(lane & 31, 16 * st + 8 * (lane >> 5));
@@ -939,40 +954,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
             toff[db][1] = xr_off<HD / 8>(r + 8, 32 * db + c);
         }
     }
-    floatx16 aK[NDB], aV[NDB];
+    // dV^T (V role) or unscaled dK^T (K role): rows are head dims
+    floatx16 acc[NDB];
 #pragma unroll
-    for (int db = 0; db < NDB; db++) {
-        aK[db] = zero16();
-        aV[db] = zero16();
-    }
+    for (int db = 0; db < NDB; db++) acc[db] = zero16();
     const int qt0 = (kb * 128) / TQ, nqh = nqt - qt0, nst = (h1 - h0) * nqh;
     AttnDma<HD, true> dma;
     dma.init(qs, w, lane);
     const bf16* Qb = Q + (int64_t)b * T * qs;
     const bf16* Ob = dO + (int64_t)b * T * qs;
     const float* Sb = qst + (int64_t)b * Hq * nqt * QST;
-    const int soff = 4 * (64 * w + 4 * lane);  // bytes: lanes 0..15 of wave w fill floats 64w..
-    // the loads of step j (Q tile, dO tile, per-query block); past the last
-    // step the last is loaded again into a buffer that is never read, so
-    // every wave issues the same number of loads per step
+    const int soff = 4 * (64 * w + 4 * lane);
     auto step_head = [&](int j, int& qt) {
         const int jj = min(j, nst - 1);
         qt = qt0 + jj % nqh;
         return hkv * grp + h0 + jj / nqh;
     };
-    auto issue_q = [&](int j, char* tQ) {
+    // the loads of step j (V-role waves only; past the last step the last is
+    // loaded again into a buffer that is never read)
+    auto issue = [&](int j, char* tQ, char* tO, float* tS) {
+        if (!vrole) return;
         int qt;
         const int hq = step_head(j, qt);
         dma.issue(rows_rsrc(Qb + hq * HD, T, qs), qs, qt * TQ, tQ, w);
-    };
-    auto issue_o = [&](int j, char* tO) {
-        int qt;
-        const int hq = step_head(j, qt);
         dma.issue(rows_rsrc(Ob + hq * HD, T, qs), qs, qt * TQ, tO, w);
-    };
-    auto issue_s = [&](int j, float* tS) {
-        int qt;
-        const int hq = step_head(j, qt);
         const uint64_t a = (uint64_t)(uintptr_t)(Sb + ((int64_t)hq * nqt + qt) * QST);
         i32x4_t rs;
         rs[0] = (int)(uint32_t)a;
@@ -992,89 +997,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma clang diagnostic pop
         }
     };
-    auto issue = [&](int j, char* tQ, char* tO, float* tS) {
-        issue_q(j, tQ);
-        issue_o(j, tO);
-        issue_s(j, tS);
-    };
     const float sl2 = scale * kLog2e;
-    // Q / dO rows of half h (queries 32h..32h+31 of the tile): the A operands
-    // of S and dP
-    auto frags = [&](const char* __restrict__ tQ, const char* __restrict__ tO, int h,
-                     bf16x8_t (&qa)[NST], bf16x8_t (&oa)[NST]) {
+    // first phase of half h: S (V role) or dP (K role) over the tile's
+    // 32 query rows, the A operands read from the Q or dO tile
+    auto mm1 = [&](const char* __restrict__ tA, int h) {
+        bf16x8_t fa[NST];
 #pragma unroll
-        for (int st = 0; st < NST; st++) {
-            qa[st] = *(const bf16x8_t*)(tQ + h * 32 * 32 * NST + qoff[st]);
-            oa[st] = *(const bf16x8_t*)(tO + h * 32 * 32 * NST + qoff[st]);
-        }
+        for (int st = 0; st < NST; st++)
+            fa[st] = *(const bf16x8_t*)(tA + h * 32 * 32 * NST + qoff[st]);
+        __builtin_amdgcn_sched_barrier(0);
+        floatx16 r = zero16();
+#pragma unroll
+        for (int st = 0; st < NST; st++) r = mfma32(fa[st], kv[st], r);
+        return r;
     };
-    auto sdp = [&](const bf16x8_t (&qa)[NST], const bf16x8_t (&oa)[NST], floatx16& S,
-                   floatx16& dP) {
-        S = zero16();
-        dP = zero16();
-#pragma unroll
-        for (int st = 0; st < NST; st++) {
-            S = mfma32(qa[st], kf[st], S);
-            dP = mfma32(oa[st], vf[st], dP);
-        }
-    };
-    // P and dS of half h (query rows 32h + 8(r/4) + 4(lane/32) + r%4, from
-    // the tile's per-query block), as BF16 hi/lo B operands of the two k
-    // steps; on a diagonal tile keys after a query are masked
-    auto pds = [&](bool diag, const float* __restrict__ tS, int q0, int h, const floatx16& S,
-                   const floatx16& dP, bf16x8_t (&pb)[2][2], bf16x8_t (&eb)[2][2]) {
-        float p[16], d[16], dq[16];
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int ql = 32 * h + 8 * c + 4 * (lane >> 5);
-            const float4 lx = *(const float4*)(tS + ql);
-            const float4 dd = *(const float4*)(tS + 64 + ql);
-            const float l4[4] = {lx.x, lx.y, lx.z, lx.w}, d4[4] = {dd.x, dd.y, dd.z, dd.w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                p[4 * c + e] = exp2_fast(S[4 * c + e] * sl2 - l4[e]);
-                dq[4 * c + e] = d4[e];
-            }
-        }
-        if (diag) {
-            // a real branch (the empty asm cannot be speculated): only the
-            // diagonal block pays for the mask
-            int kq = (lane & 31) - 4 * (lane >> 5);  // key - query offset of register 0
-            asm volatile("" : "+v"(kq));  // and the compares stay in the branch
-#pragma unroll
-            for (int r = 0; r < 16; r++) p[r] = kq <= 8 * (r >> 2) + (r & 3) ? p[r] : 0.f;
-        }
-#pragma unroll
-        for (int r = 0; r < 16; r++) d[r] = p[r] * (dP[r] - dq[r]);
+    // second phase: acc += A^T X over the half's two 16-query k steps, X the
+    // BF16 hi/lo split of P (V role) or dS (K role), A^T read transposed
+    // from the dO or Q tile; per accumulator the lo product precedes the hi
+    // one in each k step
+    auto mm2 = [&](const char* __restrict__ tA, int h, const bf16x8_t (&xb)[2][2]) {
+        bf16x8_t fa[2][NDB];
 #pragma unroll
         for (int hf = 0; hf < 2; hf++) {
-            split8(p + 8 * hf, pb[hf][0], pb[hf][1]);
-            split8(d + 8 * hf, eb[hf][0], eb[hf][1]);
-        }
-    };
-    // dV^T += dO^T P and dK^T += Q^T dS over half h's two k steps (queries
-    // 32h + 16hf .. +15, registers 8hf .. 8hf + 7), the A operands read
-    // transposed from the tiles in that query order.  All 8 NDB transposing
-    // reads of the half are issued before its MFMAs (the scheduling barrier
-    // keeps the compiler from recycling one operand's registers, which would
-    // expose the LDS latency per 32-column block), and the MFMAs alternate
-    // between accumulators so that no two consecutive ones depend.
-    auto dkv = [&](const char* __restrict__ tQ, const char* __restrict__ tO, int h,
-                   const bf16x8_t (&pb)[2][2], const bf16x8_t (&eb)[2][2]) {
-        bf16x8_t oa[2][NDB], qa[2][NDB];
-#pragma unroll
-        for (int hf = 0; hf < 2; hf++) {
-            const char* ot = tO + (32 * h + 16 * hf) * 32 * NST;
-            const char* qt_ = tQ + (32 * h + 16 * hf) * 32 * NST;
+            const char* at = tA + (32 * h + 16 * hf) * 32 * NST;
 #pragma unroll
             for (int db = 0; db < NDB; db++) {
-                i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_p)(ot + toff[db][0]));
-                i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_p)(ot + toff[db][1]));
-                oa[hf][db] = __builtin_bit_cast(
-                    bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-                lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_p)(qt_ + toff[db][0]));
-                hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_p)(qt_ + toff[db][1]));
-                qa[hf][db] = __builtin_bit_cast(
+                i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_p)(at + toff[db][0]));
+                i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_p)(at + toff[db][1]));
+                fa[hf][db] = __builtin_bit_cast(
                     bf16x8_t, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
             }
         }
@@ -1082,91 +1032,125 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 #pragma unroll
         for (int hf = 0; hf < 2; hf++) {
 #pragma unroll
-            for (int db = 0; db < NDB; db++) {
-                aV[db] = mfma32(oa[hf][db], pb[hf][1], aV[db]);
-                aK[db] = mfma32(qa[hf][db], eb[hf][1], aK[db]);
-            }
+            for (int db = 0; db < NDB; db++) acc[db] = mfma32(fa[hf][db], xb[hf][1], acc[db]);
 #pragma unroll
-            for (int db = 0; db < NDB; db++) {
-                aV[db] = mfma32(oa[hf][db], pb[hf][0], aV[db]);
-                aK[db] = mfma32(qa[hf][db], eb[hf][0], aK[db]);
-            }
+            for (int db = 0; db < NDB; db++) acc[db] = mfma32(fa[hf][db], xb[hf][0], acc[db]);
         }
     };
-    // One step: the tile half by half (the half's 2 NST fragment reads are
-    // issued together ahead of its MFMAs; the scheduling barriers keep the
-    // compiler from spreading them one per MFMA).
-    auto step = [&](const char* __restrict__ tQ, const char* __restrict__ tO,
+    // the role as a compile-time constant (RT: std::true_type for the V role),
+    // so that each role's loop is compiled and register-allocated on its own
+    auto step = [&](auto RT, const char* __restrict__ tQ, const char* __restrict__ tO,
                     const float* __restrict__ tS, int j) {
+        constexpr bool VR = decltype(RT)::value;
         const int q0 = (qt0 + j % nqh) * TQ;
-        if (kw0 > q0 + TQ - 1 || kw0 >= T) return;  // every key follows every query
-        // key and query offsets are multiples of 32: a half is wholly after
-        // the wave's keys (no mask), the diagonal block (keys after a query
-        // masked) or wholly before them (skipped)
+        // every key follows every query of the tile: no work, barriers only
+        const bool any = kw0 <= q0 + TQ - 1 && kw0 < T;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const int qh0 = q0 + 32 * h;
-            if (kw0 > qh0) continue;
-            bf16x8_t qa[NST], oa[NST];
-            floatx16 S0, D0;
-            bf16x8_t p0[2][2], e0[2][2];
-            frags(tQ, tO, h, qa, oa);
-            __builtin_amdgcn_sched_barrier(0);
-            sdp(qa, oa, S0, D0);
-            pds(kw0 == qh0, tS, q0, h, S0, D0, p0, e0);
-            dkv(tQ, tO, h, p0, e0);
+            const bool act = any && kw0 <= qh0;
+            float4* pb = &sP[h][w][0][0];
+            float p[16];
+            floatx16 dP;
+            if (act) {
+                if constexpr (VR) {
+                    const floatx16 S = mm1(tQ, h);
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        const float4 lx = *(const float4*)(tS + 32 * h + 8 * c + 4 * (lane >> 5));
+                        const float l4[4] = {lx.x, lx.y, lx.z, lx.w};
+#pragma unroll
+                        for (int e = 0; e < 4; e++) p[4 * c + e] = exp2_fast(S[4 * c + e] * sl2 - l4[e]);
+                    }
+                    if (kw0 == qh0) {
+                        int kq = (lane & 31) - 4 * (lane >> 5);
+                        asm volatile("" : "+v"(kq));
+#pragma unroll
+                        for (int r = 0; r < 16; r++) p[r] = kq <= 8 * (r >> 2) + (r & 3) ? p[r] : 0.f;
+                    }
+#pragma unroll
+                    for (int c = 0; c < 4; c++)
+                        pb[64 * c + lane] = make_float4(p[4 * c], p[4 * c + 1], p[4 * c + 2], p[4 * c + 3]);
+                } else {
+                    dP = mm1(tO, h);
+                }
+            }
+            // the V role's P stores are complete before any wave passes
+            // (the asm's memory clobber also keeps the compiler from moving
+            // LDS accesses across it)
+            asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+            if (act) {
+                bf16x8_t xb[2][2];
+                if constexpr (VR) {
+#pragma unroll
+                    for (int hf = 0; hf < 2; hf++) split8(p + 8 * hf, xb[hf][0], xb[hf][1]);
+                    mm2(tO, h, xb);
+                } else {
+                    float d[16];
+#pragma unroll
+                    for (int c = 0; c < 4; c++) {
+                        const float4 pv = pb[64 * c + lane];
+                        const float4 dd = *(const float4*)(tS + 64 + 32 * h + 8 * c + 4 * (lane >> 5));
+                        d[4 * c] = pv.x * (dP[4 * c] - dd.x);
+                        d[4 * c + 1] = pv.y * (dP[4 * c + 1] - dd.y);
+                        d[4 * c + 2] = pv.z * (dP[4 * c + 2] - dd.z);
+                        d[4 * c + 3] = pv.w * (dP[4 * c + 3] - dd.w);
+                    }
+#pragma unroll
+                    for (int hf = 0; hf < 2; hf++) split8(d + 8 * hf, xb[hf][0], xb[hf][1]);
+                    mm2(tQ, h, xb);
+                }
+            }
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    TA_WAIT_VMCNT(0);  // K and V are in; only tile loads are counted below
-    issue(0, sQ0, sO0, sS0);
-    issue(1, sQ1, sO1, sS1);
-#define ATT_STEP(J, TQ_, TO_, TS_, RQ, RO, RS) \
-    if ((J) < nst) {                           \
-        TA_WAIT_VMCNT(LPT);                    \
-        __builtin_amdgcn_s_barrier();          \
-        issue((J) + 2, RQ, RO, RS);            \
-        step(TQ_, TO_, TS_, (J));              \
-    }
-    for (int j = 0; j < nst; j += 3) {
-        ATT_STEP(j, sQ0, sO0, sS0, sQ2, sO2, sS2);
-        ATT_STEP(j + 1, sQ1, sO1, sS1, sQ0, sO0, sS0);
-        ATT_STEP(j + 2, sQ2, sO2, sS2, sQ1, sO1, sS1);
-    }
-#undef ATT_STEP
+    TA_WAIT_VMCNT(0);  // K or V rows are in; only tile loads are counted below
+    issue(0, sQ[0], sO[0], sS[0]);
+    issue(1, sQ[1], sO[1], sS[1]);
+    auto loop = [&](auto RT) {
+        constexpr bool VR = decltype(RT)::value;
+        int cur = 0, nxt = 2;  // stage of step j, stage that step j + 2 loads into
+#pragma nounroll
+        for (int j = 0; j < nst; j++) {
+            if constexpr (VR) TA_WAIT_VMCNT(LPT);
+            __builtin_amdgcn_s_barrier();
+            if constexpr (VR) issue(j + 2, sQ[nxt], sO[nxt], sS[nxt]);
+            step(RT, sQ[cur], sO[cur], sS[cur], j);
+            cur = cur == 2 ? 0 : cur + 1;
+            nxt = nxt == 2 ? 0 : nxt + 1;
+        }
+    };
+    if (vrole)
+        loop(std::true_type{});
+    else
+        loop(std::false_type{});
     TA_WAIT_VMCNT(0);  // the surplus loads have landed before the block ends
     if (key >= T) return;
     // accumulator rows are head dims 32 db + 8 j + 4 (lane / 32) + 0..3
+    const float os = vrole ? 1.f : scale;
     if (nsplit == 1) {
-        bf16* krow = dK + ((int64_t)b * T + key) * ks_ + hkv * HD;
-        bf16* vrow = dV + ((int64_t)b * T + key) * ks_ + hkv * HD;
+        bf16* row = (vrole ? dV : dK) + ((int64_t)b * T + key) * ks_ + hkv * HD;
 #pragma unroll
         for (int db = 0; db < NDB; db++)
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int d = 32 * db + 8 * j + 4 * (lane >> 5);
                 uint2 pk;
-                pk.x = pack2(scale * aK[db][4 * j], scale * aK[db][4 * j + 1]);
-                pk.y = pack2(scale * aK[db][4 * j + 2], scale * aK[db][4 * j + 3]);
-                *(uint2*)(krow + d) = pk;
-                pk.x = pack2(aV[db][4 * j], aV[db][4 * j + 1]);
-                pk.y = pack2(aV[db][4 * j + 2], aV[db][4 * j + 3]);
-                *(uint2*)(vrow + d) = pk;
+                pk.x = pack2(os * acc[db][4 * j], os * acc[db][4 * j + 1]);
+                pk.y = pack2(os * acc[db][4 * j + 2], os * acc[db][4 * j + 3]);
+                *(uint2*)(row + d) = pk;
             }
     } else {
         // partials [nsplit][2][B*T][Hkv*HD]: dK (unscaled) then dV of run sp
         const int64_t n = (int64_t)B * T * ks_;
-        float* krow = part + 2 * sp * n + ((int64_t)b * T + key) * ks_ + hkv * HD;
-        float* vrow = krow + n;
+        float* row = part + (2 * sp + (vrole ? 1 : 0)) * n + ((int64_t)b * T + key) * ks_ + hkv * HD;
 #pragma unroll
         for (int db = 0; db < NDB; db++)
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int d = 32 * db + 8 * j + 4 * (lane >> 5);
-                *(float4*)(krow + d) = make_float4(aK[db][4 * j], aK[db][4 * j + 1],
-                                                   aK[db][4 * j + 2], aK[db][4 * j + 3]);
-                *(float4*)(vrow + d) = make_float4(aV[db][4 * j], aV[db][4 * j + 1],
-                                                   aV[db][4 * j + 2], aV[db][4 * j + 3]);
+                *(float4*)(row + d) = make_float4(acc[db][4 * j], acc[db][4 * j + 1],
+                                                  acc[db][4 * j + 2], acc[db][4 * j + 3]);
             }
     }
 }
@@ -1746,10 +1730,10 @@ int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const 
     if (rc) {
         const int blocks = nkb * B * Hkv * nsplit;
         if (hd == 64)
-            k_attn_bwd_dkv_t<64><<<blocks, 256, 0, s>>>(dO, Q, K, V, Dbuf, part, dK, dV, T, Hq,
+            k_attn_bwd_dkv_r<64><<<blocks, 512, 0, s>>>(dO, Q, K, V, Dbuf, part, dK, dV, T, Hq,
                                                          Hkv, nsplit, scale);
         else
-            k_attn_bwd_dkv_t<128><<<blocks, 256, 0, s>>>(dO, Q, K, V, Dbuf, part, dK, dV, T, Hq,
+            k_attn_bwd_dkv_r<128><<<blocks, 512, 0, s>>>(dO, Q, K, V, Dbuf, part, dK, dV, T, Hq,
                                                           Hkv, nsplit, scale);
     } else if (hd == 64) {
         k_attn_bwd_dkv<64><<<(int)b1, 256, 0, s>>>(dO, Q, V, P, Dbuf, part, T, Hq, Hkv);
@@ -1760,8 +1744,8 @@ int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const 
         kprof_end(KP_ATTN_BWD_DKV, s, 6.0 * hd * tri + rf,
                   rc ? 12.0 * B * Hq * (double)T + 2.0 * bt * hd * (2.0 * Hq + 4.0 * Hkv)
                      : pb + 2.0 * bt * hd * (2.0 * Hq + Hkv) + 4.0 * bt * Hq + 8.0 * bt * Hq * hd,
-                  hd == 64 ? (rc ? "void ta::k_attn_bwd_dkv_t<64>" : "void ta::k_attn_bwd_dkv<64>")
-                           : (rc ? "void ta::k_attn_bwd_dkv_t<128>" : "void ta::k_attn_bwd_dkv<128>"));
+                  hd == 64 ? (rc ? "void ta::k_attn_bwd_dkv_r<64>" : "void ta::k_attn_bwd_dkv<64>")
+                           : (rc ? "void ta::k_attn_bwd_dkv_r<128>" : "void ta::k_attn_bwd_dkv<128>"));
     if (!rc) {
         int64_t n = (int64_t)B * T * Hkv * hd;
         int rb = (int)std::min<int64_t>((n + 255) / 256, 4096);

@@ -1710,6 +1710,37 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
         else if (tiles < 192 && ksteps >= 32)
             splits = split_for(tiles);
         if (splits < 1) splits = 1;
+        // A last wave of at most half the CUs' blocks (M 8192 x N 8960: 4.375
+        // waves of 256 x 256 tiles) runs as its own launch of 128-row tiles,
+        // two blocks per CU at a quarter of the work each: the columns past
+        // the last whole wave of 256-wide tiles go to k_gemm_mid.  Every
+        // output element keeps its k order, so the result is the same.
+        if (g_big_variant == 0 && force_splits <= 0 && g_force_splits == 0 && splits == 1 &&
+            variant == 18 && !out_f32) {
+            const int full = tiles / 256, rem = tiles % 256;
+            if (full >= 1 && rem > 0 && rem <= 128 && (full * 256) % a.tiles_m == 0) {
+                const int n_main = full * 256 / a.tiles_m * 256;
+                if (n_main > 3072 && n_main < N &&
+                    mid_bn(M, N - n_main, 256, ksteps, false, 128) != 0) {
+                    const bool fz = lora && lora->n > 0;
+                    LoraEpi lt{};
+                    if (fz) {
+                        lt = *lora;
+                        for (int p = 0; p < lora->n; p++) {
+                            lt.v_nk[p] = lora->v_nk[p] + (int64_t)n_main * lora->r;
+                            lt.v_alt[p] = nullptr;  // the mid kernel fuses every rank here
+                        }
+                    }
+                    int rc = gemm_dispatch(xk, yk, M, n_main, K, alpha, X, ldx, Y, ldy, beta, C,
+                                           ldc, bias, false, s, 0, lora);
+                    if (rc) return rc;
+                    return gemm_dispatch(xk, yk, M, N - n_main, K, alpha, X, ldx,
+                                         Y + (int64_t)n_main * ldy, ldy, beta,
+                                         (bf16*)C + n_main, ldc, bias ? bias + n_main : nullptr,
+                                         false, s, 0, fz ? &lt : nullptr);
+                }
+            }
+        }
         int steps_per = (ksteps + splits - 1) / splits;
         a.k_per_split = steps_per * BK;
         splits = (ksteps + steps_per - 1) / steps_per;

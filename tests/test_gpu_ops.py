@@ -283,6 +283,33 @@ def test_gemm_stage_forms_bit_identical(M, N, K):
     check_gemm_close(got, rm_ref(1, 1, M, N, K, 1.0, X, K, Y, K, 1.0, C0, N), "gemm default")
 
 
+@pytest.mark.parametrize("M,N,K", [(8192, 8960, 128), (2048, 8960, 192)])
+def test_gemm_last_wave_split_bit_identical(M, N, K):
+    """A last wave of at most half the CUs' 256 x 256 tiles (8192 x 8960:
+    1120 tiles, 4.375 waves; 2048 x 8960: 280 tiles) runs its columns past
+    the last whole wave (8192 ..) as 128-row tiles in a second launch.  Each
+    output element keeps its k order, so the default equals the forced
+    one-launch 256-wide form (variant 18) bit for bit, with the bias and
+    beta epilogues too, and agrees with the oracle GEMM."""
+    X, Y, b = rbf(M, K, scale=0.5), rbf(N, K, scale=0.02), rbf(N, scale=0.1)
+    C0 = rbf(M, N)
+    tX, tY, tb = dev(X), dev(Y), dev(b)
+
+    def run(v, bias, beta):
+        tc = dev(C0)
+        call("ta_gemm_rm_variant", v, 1, 1, M, N, K, ctypes.c_float(1.0), P(tX), K, P(tY), K,
+             ctypes.c_float(beta), P(tc), N, P(bias) if bias is not None else None, S())
+        return host(tc)
+
+    for bias, beta in ((None, 0.0), (tb, 0.0), (None, 1.0)):
+        g0, g18 = run(0, bias, beta), run(18, bias, beta)
+        assert np.array_equal(g0, g18), f"default vs 256-wide (bias={bias is not None}, beta={beta})"
+    got = run(0, tb, 1.0)
+    ref = O.add_bias(rm_ref(1, 1, M, N, K, 1.0, X, K, Y, K, 1.0, C0, N), b) if M <= 2048 else None
+    if ref is not None:
+        check_gemm_close(got, ref, "gemm last-wave split")
+
+
 def test_gemm_rm_bias_epilogue():
     M, N, K = 256, 384, 128
     X, Y, b = rbf(M, K), rbf(N, K), rbf(N)
