@@ -109,6 +109,14 @@ int ta_add_bias(uint16_t* out, const uint16_t* bias, int BT, int D, void* stream
 int ta_add_inplace(uint16_t* out, const uint16_t* delta, int64_t N, void* stream);
 int ta_lora_add(uint16_t* out, const uint16_t* delta, float scale, int64_t N, void* stream);
 
+/* ── LoRA A initialisation ── replaces the k_kaiming_init / k_kaiming_init_f32
+ * pair of AdapterModel::make_pair (src/adapter/adapter_model.cu:15-39,44-50):
+ * element i of A ([rank, in_dim] row-major, n = rank * in_dim) is
+ * u(i) * sqrt(1 / in_dim), u the reference's 24-bit integer hash of i (seed
+ * 0x1234) mapped to [-1, 1]; a32 gets the F32 value, a16 its BF16 rounding
+ * (either may be NULL). */
+int ta_lora_kaiming_init(float* a32, uint16_t* a16, int64_t n, int in_dim, void* stream);
+
 /* ── casts ── replace ops::cast_bf16_to_f32 / cast_f32_to_bf16  ops.hpp:135-136 */
 int ta_cast_bf16_to_f32(const uint16_t* src, float* dst, int64_t N, void* stream);
 int ta_cast_f32_to_bf16(const float* src, uint16_t* dst, int64_t N, void* stream);

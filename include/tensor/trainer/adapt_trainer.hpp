@@ -20,6 +20,7 @@
 #include <string>
 
 #include <tensor/adapter/adapter_config.hpp>
+#include <tensor/adapter/adapter_model.hpp>
 #include <tensor/backend/cuda/device.hpp>
 #include <tensor/base/frozen_base.hpp>
 #include <tensor/data/dataset.hpp>

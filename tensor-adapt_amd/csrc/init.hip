@@ -86,8 +86,8 @@ __global__ void k_kaiming(float* __restrict__ a32, bf16* __restrict__ a16, int64
         float u = (float)(r & 0xFFFFFFu) / (float)0xFFFFFF * 2.f - 1.f;
         float bound = sqrtf(1.f / (float)in_dim);
         float v = u * bound;
-        a32[i] = v;
-        a16[i] = f2bf(v);
+        if (a32) a32[i] = v;
+        if (a16) a16[i] = f2bf(v);
     }
 }
 int kaiming_init(float* a32, bf16* a16, int64_t n, int in_dim, hipStream_t s) {
@@ -176,3 +176,10 @@ int mask_targets_dev(const int32_t* in, const int32_t* tgt_in, int32_t* tgt, int
 }
 
 }  // namespace ta
+
+extern "C" int ta_lora_kaiming_init(float* a32, uint16_t* a16, int64_t n, int in_dim,
+                                    void* stream) {
+    TA_REQUIRE(n >= 0 && in_dim > 0, "lora_kaiming_init: bad arguments (n=%lld in_dim=%d)",
+               (long long)n, in_dim);
+    return ta::kaiming_init(a32, a16, n, in_dim, (hipStream_t)stream);
+}

@@ -6,9 +6,11 @@
 //                             <dir>/lr.bin for the Python side to compare
 //                             with the reference's compiled host code
 //   test_host_api gpu <dir>   device paths on hip:0
+//   test_host_api perop <dir> the per-op classes against the step engine
 // Exit status 0 when every check passed; each failure prints one line.
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -30,6 +32,9 @@
 #include <tensor/adapter/adapter_config.hpp>
 #include <tensor/base/frozen_base.hpp>
 #include <tensor/checkpoint/adapter_writer.hpp>
+#include <tensor/adapter/adapter_model.hpp>
+#include <tensor/base/arch/qwen2.hpp>
+#include <tensor/trainer/adamw.hpp>
 #include <tensor/trainer/adapt_trainer.hpp>
 #include <tensor/trainer/cosine_schedule.hpp>
 
@@ -424,14 +429,15 @@ static void gpu_tests(const fs::path& dir) {
     trainer_tests(dev, dir / "trainer");
 }
 
-// A small Qwen2 base (V=1024, H=256, 2 layers, 4 Q / 2 KV heads of 64,
-// I=512) in device tensors, N(0, 0.02) weights, unit norms, zero biases.
-static base::FrozenBase small_base(const Device& dev) {
+// A small Qwen2 base (V=1024 unless given, H=256, 2 layers, 4 Q / 2 KV
+// heads of 64, I=512) in device tensors, N(0, 0.02) weights, unit norms,
+// zero biases.
+static base::FrozenBase small_base(const Device& dev, size_t V = 1024) {
     base::FrozenBase b;
     base::BaseConfig& c = b.config;
     c.arch_name = "qwen2";
     c.arch = base::ArchType::Qwen2;
-    c.vocab_size = 1024;
+    c.vocab_size = V;
     c.hidden_size = 256;
     c.num_layers = 2;
     c.num_q_heads = 4;
@@ -449,7 +455,7 @@ static base::FrozenBase small_base(const Device& dev) {
         return Tensor::from_host(TensorView{h.data(), DType::BF16, sh}, dev);
     };
     const size_t H = 256, q = 256, kv = 128, I = 512;
-    b.embed_w = mk({1024, H}, 0.02f, 0.f);
+    b.embed_w = mk({V, H}, 0.02f, 0.f);
     b.final_norm_w = mk({H}, 0.f, 1.f);
     for (int l = 0; l < 2; l++) {
         base::LayerWeights w;
@@ -711,6 +717,205 @@ static void c2_schedule_tests(const fs::path& dir) {
     }
 }
 
+// relative L2 distance of two F32 vectors
+static double rel_l2(const std::vector<float>& a, const std::vector<float>& b) {
+    double d = 0, n = 0;
+    for (size_t i = 0; i < a.size() && i < b.size(); i++) {
+        d += ((double)a[i] - b[i]) * ((double)a[i] - b[i]);
+        n += (double)b[i] * b[i];
+    }
+    return n > 0 ? std::sqrt(d / n) : std::sqrt(d);
+}
+
+// The per-op classes (Qwen2Base, AdapterModel, AdamW) composed into the
+// reference trainer's step (adapt_trainer.cu:189-253: zero_grad, forward,
+// cross entropy over B*T rows, backward, mean of the positive per-token
+// losses, AdamW::step_all; no clip at grad_clip = 1e30), two steps, against
+// the step engine on the same base and batches.  Both start from the same
+// adapter (the reference's hashed A, B = 0); before step 2 the engine takes
+// the per-op model's state (masters, moments, BF16 weights), so each step's
+// gradients are compared from one state.  The two paths take the reference's
+// BF16 rounding points and differ in accumulation order and in the attention
+// backward's form (stored P here, recomputed P in the engine): loss within
+// 1e-3 relative, every gB (step 1; every gA is exactly 0 on both, B being 0)
+// and every gA and gB (step 2) within 1e-2 relative L2.  AdamW::step_all is
+// checked against the update written out from the model's own gradients
+// (first step: m = (1 - b1) g, v = (1 - b2) g^2, bias corrections 1 - b^1;
+// decoupled decay), and every BF16 weight against its master's rounding.
+static void perop_tests() {
+    Device dev = Device::open("hip:0");
+    const size_t V = 151936;  // the chat-template ids fit: targets survive the masking
+    base::FrozenBase fb = small_base(dev, V);
+    const base::BaseConfig& c = fb.config;
+    const int B = 2, T = 128, BT = B * T, L = (int)c.num_layers, R = 8;
+    adapter::AdapterConfig cfg;
+    cfg.rank = R;
+    cfg.alpha = 16.f;
+    cfg.weight_decay = 0.01f;
+    cfg.grad_clip = 1e30f;
+    const float lr = 1e-3f;
+
+    ta_model_config mc{(int)V, 256, L, 4, 2, 64, 512, c.rms_norm_eps, c.rope_theta, 1};
+    ta_adapt_config ac{R, cfg.alpha, 0b1111, lr, cfg.grad_clip, 0, 100, cfg.adam_beta1,
+                       cfg.adam_beta2, 1e-8f, cfg.weight_decay};
+    void* eng = ta_engine_create(&mc, &ac, B, T, dev.stream());
+    CHECK(eng != nullptr);
+    if (!eng) return;
+    auto set = [&](const std::string& name, const Tensor& t) {
+        CHECK(ta_engine_set_weight_device(eng, name.c_str(), t.bf16(), (int64_t)t.numel()) == 0);
+    };
+    set("model.embed_tokens.weight", fb.embed_w);
+    set("model.norm.weight", fb.final_norm_w);
+    for (int l = 0; l < L; l++) {
+        const base::LayerWeights& w = fb.layers[l];
+        const std::string p = "model.layers." + std::to_string(l) + ".";
+        set(p + "input_layernorm.weight", w.input_norm_w);
+        set(p + "post_attention_layernorm.weight", w.post_norm_w);
+        set(p + "self_attn.q_proj.weight", w.q_proj_w);
+        set(p + "self_attn.q_proj.bias", w.q_proj_b);
+        set(p + "self_attn.k_proj.weight", w.k_proj_w);
+        set(p + "self_attn.k_proj.bias", w.k_proj_b);
+        set(p + "self_attn.v_proj.weight", w.v_proj_w);
+        set(p + "self_attn.v_proj.bias", w.v_proj_b);
+        set(p + "self_attn.o_proj.weight", w.o_proj_w);
+        set(p + "mlp.gate_proj.weight", w.gate_proj_w);
+        set(p + "mlp.up_proj.weight", w.up_proj_w);
+        set(p + "mlp.down_proj.weight", w.down_proj_w);
+    }
+
+    adapter::AdapterModel m = adapter::AdapterModel::create(fb, cfg, dev);
+    const int64_t in[4] = {256, 256, 256, 256}, out[4] = {256, 128, 128, 256};
+    CHECK(m.layers.size() == (size_t)L &&
+          m.param_count() == (size_t)L * R * ((256 + 256) + 2 * (256 + 128) + (256 + 256)));
+    const trainer::AdamW opt(cfg);
+    CHECK(opt.beta1 == cfg.adam_beta1 && opt.weight_decay == cfg.weight_decay && opt.eps == 1e-8f);
+    auto pairs = [&](int l) {
+        return std::vector<adapter::LoraPair*>{&m.layers[l].lora_q, &m.layers[l].lora_k,
+                                               &m.layers[l].lora_v, &m.layers[l].lora_o};
+    };
+    // the engine starts from the same A (the hashed init) and B = 0
+    for (int l = 0; l < L; l++)
+        for (int p = 0; p < 4; p++) {
+            std::vector<float> e(R * in[p]);
+            CHECK(ta_engine_read_adapter(eng, l, p, 0, e.data(), R * in[p]) == 0);
+            CHECK(e == pairs(l)[p]->A_f32.to_host_f32());
+        }
+    uint32_t rs = 91;
+    for (int k = 1; k <= 2; k++) {
+        // one assistant span per row, so the masking keeps most targets
+        std::vector<int32_t> toks(BT + 1);
+        for (auto& t : toks) t = (int32_t)(lcg(rs) % 150000u);
+        for (int b = 0; b < B; b++) {
+            toks[b * T + 3] = 151644;
+            toks[b * T + 4] = 77091;
+            toks[b * T + T - 8] = 151645;
+        }
+        std::vector<int32_t> inp(toks.begin(), toks.begin() + BT), tgt(toks.begin() + 1, toks.end());
+        ta_step_metrics met{};
+        CHECK(ta_engine_step(eng, inp.data(), tgt.data(), lr, &met) == 0);
+        std::vector<int32_t> masked(BT);
+        CHECK(ta_engine_read_buffer(eng, "targets", masked.data(), BT) == 0);
+
+        Tensor tok_d = Tensor::from_host(TensorView{inp.data(), DType::I32, Shape({(size_t)BT})}, dev);
+        Tensor tgt_d = Tensor::from_host(TensorView{masked.data(), DType::I32, Shape({(size_t)BT})}, dev);
+        m.zero_grad(dev);
+        auto fwd = base::arch::Qwen2Base::forward(fb, tok_d, B, T, dev, &m);
+        CHECK(fwd.layer_cache.size() == (size_t)L && fwd.logits.numel() == (size_t)BT * V);
+        Tensor loss_tok = Tensor::empty_f32(Shape({(size_t)BT}), dev);
+        ops::cross_entropy_fwd(fwd.logits.bf16(), tgt_d.i32(), loss_tok.f32(), fwd.dlogits.bf16(),
+                               BT, (int)V, dev.stream());
+        auto grads = base::arch::Qwen2Base::backward(fb, fwd, B, T, dev, &m);
+        CHECK(grads.size() == (size_t)L && grads[0].dx_attn_in.numel() == (size_t)BT * 256);
+        double sum = 0;
+        int nv = 0;
+        for (float l : loss_tok.to_host_f32())
+            if (l > 1e-9f) {
+                sum += l;
+                nv++;
+            }
+        const double loss = nv ? sum / nv : 0.0;
+        std::printf("perop step %d: loss %.6f engine %.6f\n", k, loss, (double)met.loss);
+        CHECK(std::fabs(loss - met.loss) <= 1e-3 * std::fabs(met.loss));
+        double worst = 0;
+        for (int l = 0; l < L; l++)
+            for (int p = 0; p < 4; p++)
+                for (int which : {6, 7}) {
+                    const bool isA = which == 6;
+                    const int64_t n = isA ? R * in[p] : out[p] * R;
+                    std::vector<float> e(n);
+                    CHECK(ta_engine_read_adapter(eng, l, p, which, e.data(), n) == 0);
+                    const std::vector<float> g = (isA ? pairs(l)[p]->gA : pairs(l)[p]->gB).to_host_f32();
+                    if (k == 1 && isA) {
+                        bool zero = true;
+                        for (size_t i = 0; i < g.size(); i++) zero = zero && g[i] == 0.f && e[i] == 0.f;
+                        CHECK(zero);
+                        continue;
+                    }
+                    const double d = rel_l2(g, e);
+                    worst = std::max(worst, d);
+                    if (d > 1e-2)
+                        std::printf("FAIL layer %d pair %d %s: rel L2 %.3e\n", l, p, isA ? "gA" : "gB", d);
+                    CHECK(d <= 1e-2);
+                }
+        std::printf("perop step %d: worst gradient rel L2 %.3e\n", k, worst);
+
+        // AdamW::step_all against the update written out from the model's
+        // own gradients and state
+        std::vector<std::vector<float>> w0, m0, v0, gg;
+        for (int l = 0; l < L; l++)
+            for (adapter::LoraPair* lp : pairs(l)) {
+                w0.push_back(lp->A_f32.to_host_f32());
+                w0.push_back(lp->B_f32.to_host_f32());
+                m0.push_back(lp->mA.to_host_f32());
+                m0.push_back(lp->mB.to_host_f32());
+                v0.push_back(lp->vA.to_host_f32());
+                v0.push_back(lp->vB.to_host_f32());
+                gg.push_back(lp->gA.to_host_f32());
+                gg.push_back(lp->gB.to_host_f32());
+            }
+        opt.step_all(m, lr, k, dev);
+        const double b1 = cfg.adam_beta1, b2 = cfg.adam_beta2, wd = cfg.weight_decay;
+        const double c1 = 1.0 - std::pow(b1, k), c2 = 1.0 - std::pow(b2, k);
+        double wu = 0;
+        size_t bad_bf = 0, ti = 0;
+        for (int l = 0; l < L; l++)
+            for (adapter::LoraPair* lp : pairs(l))
+                for (int ab = 0; ab < 2; ab++, ti++) {
+                    const std::vector<float> w1 = (ab ? lp->B_f32 : lp->A_f32).to_host_f32();
+                    const std::vector<uint16_t> h1 = (ab ? lp->B_bf16 : lp->A_bf16).to_host_bf16();
+                    std::vector<float> want(w1.size());
+                    for (size_t i = 0; i < w1.size(); i++) {
+                        const double g = gg[ti][i];
+                        const double mm = b1 * m0[ti][i] + (1 - b1) * g;
+                        const double vv = b2 * v0[ti][i] + (1 - b2) * g * g;
+                        const double w = w0[ti][i];
+                        want[i] = (float)(w - lr * (mm / c1 / (std::sqrt(vv / c2) + 1e-8) + wd * w));
+                        bad_bf += h1[i] != f2bf(w1[i]);
+                    }
+                    wu = std::max(wu, rel_l2(w1, want));
+                }
+        std::printf("perop step %d: AdamW worst rel L2 %.3e, BF16 mismatches %zu\n", k, wu, bad_bf);
+        CHECK(wu <= 1e-5 && bad_bf == 0);
+
+        // the engine takes the model's state for the next step
+        if (k == 1)
+            for (int l = 0; l < L; l++)
+                for (int p = 0; p < 4; p++) {
+                    adapter::LoraPair* lp = pairs(l)[p];
+                    const Tensor* t32[6] = {&lp->A_f32, &lp->B_f32, &lp->mA, &lp->vA, &lp->mB, &lp->vB};
+                    for (int which = 0; which < 6; which++) {
+                        auto v = t32[which]->to_host_f32();
+                        CHECK(ta_engine_write_adapter(eng, l, p, which, v.data(), (int64_t)v.size()) == 0);
+                    }
+                    for (int which : {8, 9}) {
+                        auto v = (which == 8 ? lp->A_bf16 : lp->B_bf16).to_host_bf16();
+                        CHECK(ta_engine_write_adapter(eng, l, p, which, v.data(), (int64_t)v.size()) == 0);
+                    }
+                }
+    }
+    CHECK(ta_engine_destroy(eng) == 0);
+}
+
 int main(int argc, char** argv) {
     if (argc < 3) {
         std::printf("usage: %s cpu|gpu <dir>\n", argv[0]);
@@ -726,6 +931,8 @@ int main(int argc, char** argv) {
             gpu_tests(dir);
         else if (mode == "c2sched")
             c2_schedule_tests(dir);
+        else if (mode == "perop")
+            perop_tests();
         else
             return 2;
     } catch (const std::exception& e) {

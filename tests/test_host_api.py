@@ -181,3 +181,18 @@ def test_c2_schedule_through_trainer(tmp_path):
     r = subprocess.run([_binary(), "c2sched", str(tmp_path)], capture_output=True, text=True,
                        timeout=170)
     assert r.returncode == 0, r.stdout + r.stderr[-2000:]
+
+
+@pytest.mark.gpu
+def test_per_op_classes_match_engine(tmp_path):
+    """The per-op classes of include/tensor (Qwen2Base forward/backward,
+    AdapterModel, AdamW) composed into the reference trainer's step
+    (adapt_trainer.cu:189-253) agree with the step engine over two steps on
+    the same base and batches: loss, every gA/gB and the updated masters
+    (tests/cpp/test_host_api.cpp perop_tests)."""
+    print("case: test_host_api perop", flush=True)
+    r = subprocess.run([_binary(), "perop", str(tmp_path)], capture_output=True, text=True,
+                       timeout=110)
+    print(r.stdout[-3000:])
+    assert r.returncode == 0, r.stdout + r.stderr[-2000:]
+
