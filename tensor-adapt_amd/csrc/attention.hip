@@ -393,6 +393,22 @@ __global__ __launch_bounds__(256) void k_attn_fwd(const bf16* __restrict__ Q,
 // the backward recomputes P from them.
 constexpr int TQ2 = 128;  // queries per block (4 waves x 32)
 // per (b, hq) and 64-query tile, the backward's per-query values as one
+// The inverse RoPE of a backward output (ops::rope_bwd applied to the
+// written dQ / dK): four consecutive head dims d .. d + 3 (d a multiple of
+// 4) of a row at position t, from their BF16 values, with the table of
+// sign -1 ([T][hd / 2] (cos, sin)); returns the two packed words.
+__device__ __forceinline__ uint2 rope4_packed(const float2* __restrict__ rtab, int t, int hd, int d,
+                                              float a0, float a1, float a2, float a3) {
+    const float4 cs = *(const float4*)(rtab + (int64_t)t * (hd >> 1) + (d >> 1));
+    float o0, o1, o2, o3;
+    rope_rot(bf2f(f2bf(a0)), bf2f(f2bf(a1)), cs.x, cs.y, o0, o1);
+    rope_rot(bf2f(f2bf(a2)), bf2f(f2bf(a3)), cs.z, cs.w, o2, o3);
+    uint2 pk;
+    pk.x = pack2(o0, o1);
+    pk.y = pack2(o2, o3);
+    return pk;
+}
+
 // 1 KB block: [0, 64) the row's log2 normaliser lse2 = max + log2(sum) (so
 // P = exp2(S scale log2(e) - lse2)), [64, 128) the row dot D
 constexpr int QST = 256;
@@ -704,7 +720,8 @@ __global__ __launch_bounds__(256, 2) void k_attn_bwd_dq_t(const bf16* __restrict
                                                        float* __restrict__ qst,
                                                        const float* __restrict__ O32,
                                                        bf16* __restrict__ dQ, int T, int Hq,
-                                                       int Hkv, float scale) {
+                                                       int Hkv, float scale,
+                                                       const float2* __restrict__ rtab) {
     constexpr int NST = HD / 16, NDB = HD / 32;
     constexpr int TB = TK * HD * 2;
     __shared__ __attribute__((aligned(1024))) char sK0[TB], sK1[TB];
@@ -862,8 +879,14 @@ __global__ __launch_bounds__(256, 2) void k_attn_bwd_dq_t(const bf16* __restrict
         for (int j = 0; j < 4; j++) {
             const int d = 32 * db + 8 * j + 4 * (lane >> 5);
             uint2 pk;
-            pk.x = pack2(scale * acc[db][4 * j + 0], scale * acc[db][4 * j + 1]);
-            pk.y = pack2(scale * acc[db][4 * j + 2], scale * acc[db][4 * j + 3]);
+            if (rtab) {
+                pk = rope4_packed(rtab, qrow, HD, d, scale * acc[db][4 * j + 0],
+                                  scale * acc[db][4 * j + 1], scale * acc[db][4 * j + 2],
+                                  scale * acc[db][4 * j + 3]);
+            } else {
+                pk.x = pack2(scale * acc[db][4 * j + 0], scale * acc[db][4 * j + 1]);
+                pk.y = pack2(scale * acc[db][4 * j + 2], scale * acc[db][4 * j + 3]);
+            }
             *(uint2*)(drow + d) = pk;
         }
 }
@@ -906,7 +929,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     const bf16* __restrict__ dO, const bf16* __restrict__ Q, const bf16* __restrict__ K,
     const bf16* __restrict__ V, const float* __restrict__ qst, float* __restrict__ part,
     bf16* __restrict__ dK, bf16* __restrict__ dV, int T, int Hq, int Hkv, int nsplit,
-    float scale) {
+    float scale, const float2* __restrict__ rtab) {
     constexpr int NST = HD / 16, NDB = HD / 32;
     constexpr int TB = TQ * HD * 2;
     // DMA instructions per V-role wave per step: Q and dO tiles, a quarter of
@@ -1136,8 +1159,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             for (int j = 0; j < 4; j++) {
                 const int d = 32 * db + 8 * j + 4 * (lane >> 5);
                 uint2 pk;
-                pk.x = pack2(os * acc[db][4 * j], os * acc[db][4 * j + 1]);
-                pk.y = pack2(os * acc[db][4 * j + 2], os * acc[db][4 * j + 3]);
+                if (rtab && !vrole) {
+                    pk = rope4_packed(rtab, key, HD, d, os * acc[db][4 * j], os * acc[db][4 * j + 1],
+                                      os * acc[db][4 * j + 2], os * acc[db][4 * j + 3]);
+                } else {
+                    pk.x = pack2(os * acc[db][4 * j], os * acc[db][4 * j + 1]);
+                    pk.y = pack2(os * acc[db][4 * j + 2], os * acc[db][4 * j + 3]);
+                }
                 *(uint2*)(row + d) = pk;
             }
     } else {
@@ -1160,7 +1188,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 __global__ __launch_bounds__(256) void k_attn_dkv_sum(const float4* __restrict__ part,
                                                       uint2* __restrict__ dK,
                                                       uint2* __restrict__ dV, int64_t n4,
-                                                      int nsplit, float scale) {
+                                                      int nsplit, float scale,
+                                                      const float2* __restrict__ rtab, int T,
+                                                      int kvw, int hd) {
     for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n4;
          i += (int64_t)gridDim.x * blockDim.x) {
         float4 k = part[i], v = part[n4 + i];
@@ -1176,8 +1206,17 @@ __global__ __launch_bounds__(256) void k_attn_dkv_sum(const float4* __restrict__
             v.w += c.w;
         }
         uint2 pk;
-        pk.x = pack2(scale * k.x, scale * k.y);
-        pk.y = pack2(scale * k.z, scale * k.w);
+        if (rtab) {
+            // element 4i: row 4i / kvw (position row % T), head dim (4i % kvw) % hd
+            // (32-bit: the host keeps 4 n4 below 2^31)
+            const uint32_t e = 4u * (uint32_t)i, row = e / (uint32_t)kvw;
+            pk = rope4_packed(rtab, (int)(row % (uint32_t)T), hd,
+                              (int)((e - row * (uint32_t)kvw) % (uint32_t)hd), scale * k.x,
+                              scale * k.y, scale * k.z, scale * k.w);
+        } else {
+            pk.x = pack2(scale * k.x, scale * k.y);
+            pk.y = pack2(scale * k.z, scale * k.w);
+        }
         dK[i] = pk;
         pk.x = pack2(v.x, v.y);
         pk.y = pack2(v.z, v.w);
@@ -1655,8 +1694,10 @@ int64_t attn_bwd_rowbuf_floats(int B, int T, int Hq) {
 // which needs O32.
 int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const float* P,
              const float* stats, const float* O32, bf16* dQ, bf16* dK, bf16* dV, int B, int T,
-             int Hq, int Hkv, int hd, float* Dbuf, float* part, hipStream_t s) {
+             int Hq, int Hkv, int hd, float* Dbuf, float* part, hipStream_t s,
+             const float2* rtab) {
     TA_REQUIRE(P || (stats && O32), "sdpa_bwd: without P, the row statistics and O32 are needed");
+    TA_REQUIRE(!rtab || !P, "sdpa_bwd: the fused inverse RoPE is for the recompute path");
     TA_REQUIRE(B > 0 && T > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0,
                "sdpa_bwd: bad shape B=%d T=%d Hq=%d Hkv=%d", B, T, Hq, Hkv);
     TA_REQUIRE(hd == 64 || hd == 128, "sdpa_bwd: head_dim %d not supported (64 or 128)", hd);
@@ -1713,7 +1754,7 @@ int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const 
     k_attn_bwd_dq<H><<<(int)b1, 256, 0, s>>>(dO, K, V, P, Dbuf, dQ, T, Hq, Hkv, scale)
 #define DQT(H)                                                                            \
     k_attn_bwd_dq_t<H><<<(int)((int64_t)B * Hq * ((T + TQ2 - 1) / TQ2)), 256, 0, s>>>(        \
-        dO, Q, K, V, st, Dbuf, O32, dQ, T, Hq, Hkv, scale)
+        dO, Q, K, V, st, Dbuf, O32, dQ, T, Hq, Hkv, scale, rtab)
     if (hd == 64) {
         if (rc) DQT(64); else DQ(64);
     } else {
@@ -1731,10 +1772,10 @@ int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const 
         const int blocks = nkb * B * Hkv * nsplit;
         if (hd == 64)
             k_attn_bwd_dkv_r<64><<<blocks, 512, 0, s>>>(dO, Q, K, V, Dbuf, part, dK, dV, T, Hq,
-                                                         Hkv, nsplit, scale);
+                                                         Hkv, nsplit, scale, rtab);
         else
             k_attn_bwd_dkv_r<128><<<blocks, 512, 0, s>>>(dO, Q, K, V, Dbuf, part, dK, dV, T, Hq,
-                                                          Hkv, nsplit, scale);
+                                                          Hkv, nsplit, scale, rtab);
     } else if (hd == 64) {
         k_attn_bwd_dkv<64><<<(int)b1, 256, 0, s>>>(dO, Q, V, P, Dbuf, part, T, Hq, Hkv);
     } else {
@@ -1752,9 +1793,11 @@ int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const 
         k_attn_dkv_reduce<<<rb, 256, 0, s>>>(part, dK, dV, B, T, Hq, Hkv, hd, scale);
     } else if (nsplit > 1) {
         const int64_t n4 = (int64_t)B * T * Hkv * hd / 4;
+        TA_REQUIRE(!rtab || 4 * n4 < (int64_t(1) << 31), "sdpa_bwd: %lld dK elements for the fused RoPE",
+                   (long long)(4 * n4));
         const int rb = (int)std::min<int64_t>((n4 + 255) / 256, 4096);
         k_attn_dkv_sum<<<rb, 256, 0, s>>>((const float4*)part, (uint2*)dK, (uint2*)dV, n4,
-                                          nsplit, scale);
+                                          nsplit, scale, rtab, T, Hkv * hd, hd);
     }
     return check_launch("sdpa_bwd");
 }

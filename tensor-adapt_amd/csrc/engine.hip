@@ -113,6 +113,9 @@ struct Engine {
     bf16 *x_final, *xfn, *logits, *g_res, *dres, *tmpH, *dact, *dgate, *dup, *dxn2, *dao, *dQ, *dK,
         *dV, *dxn, *delta, *dh, *dh_cat;
     float *final_rms, *loss_tok, *norm_dev, *Dbuf, *dkv_part;
+    // (cos, sin) table of the inverse RoPE, taken by the attention backward
+    // as it writes dQ and dK (the forward's rotation runs in the q/k/v GEMM)
+    const float2* rope_bwd;
     double* cacc;          // the centroid sums the step adds into (own_cacc or the caller's)
     double* own_cacc = nullptr;
     int32_t *tok_dev, *tgt_dev;
@@ -408,6 +411,8 @@ static int engine_alloc(Engine* e) {
     CK(alloc(e, &e->dh_cat, (int64_t)BT * r * 3, "dh_cat", 0));
     CK(alloc(e, &e->Dbuf, attn_bwd_rowbuf_floats(e->B, e->T, c.n_q), "Dbuf", 1));
     CK(alloc(e, &e->dkv_part, (int64_t)2 * e->B * c.n_q * e->T * c.head_dim, "dkv_part", 1));
+    e->rope_bwd = rope_table(e->T, c.head_dim, c.rope_theta, -1.f, e->s);
+    if (!e->rope_bwd) return set_error(-2, "engine: RoPE table allocation failed");
     CK(alloc(e, &e->norm_dev, 64, "norm", 1));
     e->bad_dev = (int32_t*)(e->norm_dev + 1);
     e->nonfinite_dev = (int32_t*)(e->norm_dev + 2);
@@ -641,17 +646,17 @@ static int layer_fwd_body(Engine* e, Layer& ly) {
     CK(lora_group_h(e, ly, {PQ, PK, PV}, ly.xn, H));
     {
         // q, k and v projections (qwen2.cu:21-30, each with its bias and
-        // LoRA delta) in one launch over the three weight matrices
+        // LoRA delta) in one launch over the three weight matrices, with
+        // the RoPE of Q and K (qwen2.cu:109-110) on the rounded outputs
         LoraEpi eq = fwd_epi(e, ly.pr[PQ]), ek = fwd_epi(e, ly.pr[PK]), ev = fwd_epi(e, ly.pr[PV]);
-        const GemmGroup gr[3] = {{qd, ly.W[PQ], ly.Q, qd, ly.bias[0], &eq},
-                                 {kvd, ly.W[PK], ly.K, kvd, ly.bias[1], &ek},
-                                 {kvd, ly.W[PV], ly.V, kvd, ly.bias[2], &ev}};
+        const GemmGroup gr[3] = {{qd, ly.W[PQ], ly.Q, qd, ly.bias[0], &eq, true},
+                                 {kvd, ly.W[PK], ly.K, kvd, ly.bias[1], &ek, true},
+                                 {kvd, ly.W[PV], ly.V, kvd, ly.bias[2], &ev, false}};
+        const RopeSpec rope{e->B, e->T, c.head_dim, c.rope_theta};
         TIMED(TA_CAT_GEMM_FWD, gflops(BT, qd + 2.0 * kvd, H),
               gbytes(BT, qd + 2.0 * kvd, H, 2, 2, false),
-              gemm_groups(BT, H, ly.xn, H, H, gr, 3, s));
+              gemm_groups(BT, H, ly.xn, H, H, gr, 3, s, &rope));
     }
-    TIMED(TA_CAT_ELEMWISE, 0, dBT * (qd + kvd) * 4,
-          rope_qk(ly.Q, c.n_q, ly.K, c.n_kv, e->B, e->T, c.head_dim, c.rope_theta, 1.f, s));
     // sdpa_fwd (ops.cu:578-681) without the probabilities buffer: the
     // rows' (max, 1/sum) are kept instead
     TIMED(TA_CAT_ATTN_FWD, 4.0 * tri * c.head_dim,
@@ -810,10 +815,8 @@ static int backward(Engine* e) {
               16.0 * e->B * c.n_q * e->T + dBT * (2.0 * qd + 2.0 * kvd) * 2 +
                   dBT * (qd + 2.0 * kvd) * 2 + dBT * qd * 4,
               attn_bwd(e->dao, ly.Q, ly.K, ly.V, nullptr, ly.attn_st, ly.ao32, e->dQ, e->dK, e->dV,
-                       e->B, e->T, c.n_q, c.n_kv, c.head_dim, e->Dbuf, e->dkv_part, s));
-        TIMED(TA_CAT_ELEMWISE, 0, dBT * (qd + kvd) * 4,
-              rope_qk(e->dQ, c.n_q, e->dK, c.n_kv, e->B, e->T, c.head_dim, c.rope_theta, -1.f,
-                      s));
+                       e->B, e->T, c.n_q, c.n_kv, c.head_dim, e->Dbuf, e->dkv_part, s,
+                       e->rope_bwd));
         {
             const bf16* gos[3] = {e->dQ, e->dK, e->dV};
             LoraEpi ep;

@@ -105,6 +105,13 @@ struct GemmArgs {
     const float* ce_lse2;
     const int32_t* ce_tgt;
     float ce_inv_n;
+    // RoPE of the output (k_gemm_pipe / k_gemm_mid epilogue; NULL: none):
+    // rope_tab [rope_T][rope_hd / 2] (cos, sin); row m is position
+    // m % rope_T and output column c pair (c % rope_hd) / 2 of its head.
+    // Per group in grope (which the tile's group selects into rope_tab).
+    const float2* rope_tab;
+    int rope_T, rope_hd;
+    const float2* grope[3];
 };
 
 // Load one 16-byte chunk (8 bf16) of a K-contiguous operand row with
@@ -982,6 +989,22 @@ __device__ __attribute__((always_inline)) inline void pipe_half_epilogue(
                                         : bf2f(f2bf(a.lora_s * d[r] + v[r]));
             }
         }
+        if (a.rope_tab) {
+            // RoPE of the values as written (ops::rope_fwd over the output):
+            // the lane's columns d .. d + 3 of a head are pairs d/2, d/2 + 1
+            // (d a multiple of 4), position t = row % T
+            const int t = (R0 + lr) % a.rope_T;
+            const float2* tr = a.rope_tab + (int64_t)t * (a.rope_hd >> 1);
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                const int d = (C0 + 32 * j + 8 * g + c4) % a.rope_hd;
+                const float4 cs = *(const float4*)(tr + (d >> 1));
+                const float x0 = bf2f(f2bf(v[4 * g])), x1 = bf2f(f2bf(v[4 * g + 1]));
+                const float x2 = bf2f(f2bf(v[4 * g + 2])), x3 = bf2f(f2bf(v[4 * g + 3]));
+                rope_rot(x0, x1, cs.x, cs.y, v[4 * g], v[4 * g + 1]);
+                rope_rot(x2, x3, cs.z, cs.w, v[4 * g + 2], v[4 * g + 3]);
+            }
+        }
         // the packing rounds to BF16 (exact when v is a BF16 value already)
 #pragma unroll
         for (int g = 0; g < 4; g++) {
@@ -1105,6 +1128,7 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
         a.lora_n = g == 2 ? a0.glora[2] : g == 1 ? a0.glora[1] : a0.glora[0];
         a.lora_u[0] = g == 2 ? a0.gu[2] : g == 1 ? a0.gu[1] : a0.gu[0];
         a.lora_v[0] = g == 2 ? a0.gv[2] : g == 1 ? a0.gv[1] : a0.gv[0];
+        a.rope_tab = g == 2 ? a0.grope[2] : g == 1 ? a0.grope[1] : a0.grope[0];
     }
     const int m0 = tm_i * BM, n0 = tn_i * BN;
     int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -1591,7 +1615,7 @@ static const char* mid_name(int bn, bool chain) {
 int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16* X, int64_t ldx,
                   const bf16* Y, int64_t ldy, float beta, void* C, int64_t ldc, const bf16* bias,
                   bool out_f32, hipStream_t s, int force_splits, const LoraEpi* lora) {
-    GemmArgs a;
+    GemmArgs a{};
     a.M = M;
     a.N = N;
     a.K = K;
@@ -2017,8 +2041,24 @@ int gemm_chain(int M, int N, const GemmSeg* sg, int ns, bf16* C, int64_t ldc, co
 // the results are those of separate launches.  Shapes the pipe kernel does
 // not take run as separate gemm_dispatch calls.
 int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const GemmGroup* gr,
-                int ng, hipStream_t s) {
+                int ng, hipStream_t s, const RopeSpec* rope) {
     TA_REQUIRE(ng >= 1 && ng <= 3, "gemm_groups: %d groups", ng);
+    TA_REQUIRE(!rope || (rope->T > 0 && rope->hd > 0 && rope->hd % 8 == 0 && rope->B * rope->T == M),
+               "gemm_groups: bad RoPE shape (B %d, T %d, hd %d, M %d)", rope ? rope->B : 0,
+               rope ? rope->T : 0, rope ? rope->hd : 0, M);
+    // rope of the roped groups' outputs as separate passes (the other paths)
+    auto rope_after = [&]() -> int {
+        if (!rope) return 0;
+        for (int g = 0; g < ng; g++)
+            if (gr[g].rope) {
+                TA_REQUIRE(gr[g].N % rope->hd == 0 && gr[g].ldc == gr[g].N,
+                           "gemm_groups: RoPE needs whole heads in dense rows");
+                if (int rc = ta_rope_fwd(gr[g].C, rope->B, rope->T, gr[g].N / rope->hd, rope->hd,
+                                         rope->theta, s))
+                    return rc;
+            }
+        return 0;
+    };
     int Ntot = 0;
     bool all256 = true, all192 = true, lora_ok = true, vy = (ldy % 8) == 0;
     const LoraEpi* l0 = nullptr;
@@ -2060,7 +2100,7 @@ int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const Gem
                                    gr[g].C, gr[g].ldc, gr[g].bias, false, s, 0, gr[g].lora);
             if (rc) return rc;
         }
-        return 0;
+        return rope_after();
     }
     GemmArgs a{};
     a.M = M;
@@ -2101,6 +2141,20 @@ int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const Gem
     a.lora_n = a.glora[0];
     a.lora_u[0] = a.gu[0];
     a.lora_v[0] = a.gv[0];
+    if (rope) {
+        // in the epilogue: every roped group holds whole heads
+        const float2* tab = rope_table(rope->T, rope->hd, rope->theta, 1.f, s);
+        TA_REQUIRE(tab, "gemm_groups: RoPE table allocation failed");
+        a.rope_T = rope->T;
+        a.rope_hd = rope->hd;
+        for (int g = 0; g < ng; g++) {
+            TA_REQUIRE(!gr[g].rope || gr[g].N % rope->hd == 0,
+                       "gemm_groups: RoPE group of %d columns, not whole heads of %d", gr[g].N,
+                       rope->hd);
+            a.grope[g] = gr[g].rope ? tab : nullptr;
+        }
+        a.rope_tab = a.grope[0];
+    }
     const int kid = BNb == 256 ? KP_GEMM_BIG_WIDE : KP_GEMM_BIG;
     const bool timed = kprof_begin(kid, s);
     dim3 grid(a.tiles_m * a.tiles_n);

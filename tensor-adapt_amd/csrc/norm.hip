@@ -287,10 +287,7 @@ __device__ __forceinline__ void rope_chunk(bf16* __restrict__ x, int64_t gid, in
     unpack8(*p, f);
     const float cs[4] = {c01.x, c01.z, c23.x, c23.z}, sn[4] = {c01.y, c01.w, c23.y, c23.w};
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-        o[2 * e] = f[2 * e] * cs[e] - f[2 * e + 1] * sn[e];
-        o[2 * e + 1] = f[2 * e] * sn[e] + f[2 * e + 1] * cs[e];
-    }
+    for (int e = 0; e < 4; e++) rope_rot(f[2 * e], f[2 * e + 1], cs[e], sn[e], o[2 * e], o[2 * e + 1]);
     *p = pack8(o);
 }
 __global__ __launch_bounds__(256) void k_rope_tab(bf16* __restrict__ x, int64_t rows, int T,
@@ -317,7 +314,7 @@ struct RopeTab {
 };
 static std::vector<RopeTab> g_rope_tabs;
 static std::mutex g_rope_mu;
-static const float2* rope_table(int T, int hd, float theta, float sign, hipStream_t s) {
+const float2* rope_table(int T, int hd, float theta, float sign, hipStream_t s) {
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return nullptr;
     std::lock_guard<std::mutex> lk(g_rope_mu);
@@ -346,9 +343,10 @@ __global__ void k_rope_scalar(bf16* __restrict__ x, int64_t rows, int T, int H, 
     sincosf(angle, &sn, &cs);
     for (int h = 0; h < H; h++) {
         bf16* p = x + (row * H + h) * hd + 2 * i;
-        float x0 = bf2f(p[0]), x1 = bf2f(p[1]);
-        p[0] = f2bf(x0 * cs - x1 * sn);
-        p[1] = f2bf(x0 * sn + x1 * cs);
+        float o0, o1;
+        rope_rot(bf2f(p[0]), bf2f(p[1]), cs, sn, o0, o1);
+        p[0] = f2bf(o0);
+        p[1] = f2bf(o1);
     }
 }
 

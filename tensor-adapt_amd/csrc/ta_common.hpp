@@ -67,6 +67,20 @@ __device__ __forceinline__ double wave_sum_d(double v) {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// RoPE rotation of one interleaved pair (x0, x1) by (cs, sn) = (cos, sin) of
+// its angle: x0 cs - x1 sn and x0 sn + x1 cs, each product rounded on its
+// own before the sum (no fused multiply-add), as the F32 expression of
+// ops.cu:176-204 reads.  The empty asm statements keep the compiler from
+// contracting a product into the sum.  Every kernel that rotates uses this,
+// so the forward's rotation gives the same bits in whichever kernel it runs.
+__device__ __forceinline__ void rope_rot(float x0, float x1, float cs, float sn, float& o0,
+                                         float& o1) {
+    float a = x0 * cs, b = x1 * sn, c = x0 * sn, d = x1 * cs;
+    asm volatile("" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+    o0 = a - b;
+    o1 = c + d;
+}
+
 // ── SwiGLU math (ops.cu:913-940), shared by the elementwise kernels and the
 // fused SwiGLU-backward + LoRA kernel.  exp(-g) as v_exp_f32 of -g log2(e)
 // and the quotient as v_rcp_f32 (each within 1 ulp of F32; the reference is

@@ -74,6 +74,7 @@ struct GemmGroup {
     int64_t ldc;
     const bf16* bias;
     const LoraEpi* lora;
+    bool rope = false;  // rotated when gemm_groups gets a RopeSpec
 };
 // one GEMM of a gemm_chain: X [M x K] (row stride ldx) times Y [N x K]^T
 struct GemmSeg {
@@ -91,15 +92,27 @@ int gemm_chain(int M, int N, const GemmSeg* sg, int ns, bf16* C, int64_t ldc, co
 // (sign +1 forward, -1 the inverse rotation of the backward)
 int rope_qk(bf16* q, int Hq, bf16* k, int Hk, int B, int T, int hd, float theta, float sign,
             hipStream_t s);
+// (cos, sin) of sign * t * theta^(-2i/hd) for t < T, i < hd/2 ([T][hd/2]),
+// built once per (device, T, hd, theta, sign) on the caller's stream and
+// kept for the process; NULL if the allocation fails
+const float2* rope_table(int T, int hd, float theta, float sign, hipStream_t s);
+// RoPE applied by the GEMM that writes Q and K (gemm_groups): rows are
+// positions t = row % T, the output columns are heads of hd
+struct RopeSpec {
+    int B, T, hd;
+    float theta;
+};
 // gate/up projections (+ LoRA deltas) and act = silu(gate) up in one launch
 // over Wgu, the gate/up weights interleaved in 128-row blocks ([2I x K]);
 // falls back to gemm_groups + silu_mul_fwd for other shapes (Wgu may be NULL)
 int gemm_swiglu(int M, int K, const bf16* X, int64_t ldx, const bf16* Wgu, const bf16* Wg,
                 const bf16* Wu, bf16* gate, bf16* up, bf16* act, int I, const LoraEpi* lg,
                 const LoraEpi* lu, hipStream_t s);
-// the groups' GEMMs in one launch over the N-concatenated tile grid
+// the groups' GEMMs in one launch over the N-concatenated tile grid; with
+// rope, the groups whose `rope` flag is set are rotated after their final
+// rounding (ops::rope_fwd of the written output, the same bits)
 int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const GemmGroup* gr,
-                int ng, hipStream_t s);
+                int ng, hipStream_t s, const RopeSpec* rope = nullptr);
 // causal GQA attention; P [B*Hq, T, T] F32 probabilities, or (P NULL) only
 // the rows' (max, 1/sum) in stats [B*Hq*T] float pairs, from which the
 // backward recomputes P
@@ -108,9 +121,13 @@ int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* O32, f
 // Dbuf: attn_bwd_rowbuf_floats(B, T, Hq) floats of per-query values; part:
 // 2 B T Hq hd floats of dK/dV partials (each drawn from the scratch pool
 // when NULL)
+// rtab (may be NULL; the recompute path only): a rope_table(T, hd, theta,
+// -1) whose inverse rotation dQ and dK take after their BF16 rounding, as
+// ops::rope_bwd applied to the written dQ and dK would
 int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const float* P,
              const float* stats, const float* O32, bf16* dQ, bf16* dK, bf16* dV, int B, int T,
-             int Hq, int Hkv, int hd, float* Dbuf, float* part, hipStream_t s);
+             int Hq, int Hkv, int hd, float* Dbuf, float* part, hipStream_t s,
+             const float2* rtab = nullptr);
 int64_t attn_bwd_rowbuf_floats(int B, int T, int Hq);
 int transpose_bf16(const bf16* in, bf16* out, int64_t rows, int64_t cols, hipStream_t s);
 // cross_entropy_fwd (ops.cu:958-1020) that also adds the number of NaN and
