@@ -68,17 +68,17 @@ __device__ __forceinline__ double wave_sum_d(double v) {
 constexpr float kLog2e = 1.4426950408889634f;
 
 // RoPE rotation of one interleaved pair (x0, x1) by (cs, sn) = (cos, sin) of
-// its angle: x0 cs - x1 sn and x0 sn + x1 cs, each product rounded on its
-// own before the sum (no fused multiply-add), as the F32 expression of
-// ops.cu:176-204 reads.  The empty asm statements keep the compiler from
-// contracting a product into the sum.  Every kernel that rotates uses this,
-// so the forward's rotation gives the same bits in whichever kernel it runs.
+// its angle (ops.cu:176-204): x0 cs - x1 sn and x0 sn + x1 cs, written as
+// the contracted form fma(x0, cs, -(x1 sn)) and fma(x1, cs, x0 sn), the
+// products with sn rounded on their own (the empty asm statement keeps the
+// compiler from fusing them elsewhere).  Every kernel that rotates uses
+// this, so a rotation gives the same bits in whichever kernel it runs.
 __device__ __forceinline__ void rope_rot(float x0, float x1, float cs, float sn, float& o0,
                                          float& o1) {
-    float a = x0 * cs, b = x1 * sn, c = x0 * sn, d = x1 * cs;
-    asm volatile("" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
-    o0 = a - b;
-    o1 = c + d;
+    float b = x1 * sn, c = x0 * sn;
+    asm volatile("" : "+v"(b), "+v"(c));
+    o0 = __builtin_fmaf(x0, cs, -b);
+    o1 = __builtin_fmaf(x1, cs, c);
 }
 
 // ── SwiGLU math (ops.cu:913-940), shared by the elementwise kernels and the

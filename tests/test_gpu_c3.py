@@ -118,8 +118,12 @@ def _c3_depth_step(st, step):
     if step == 0:
         assert not any(np.any(eng.adapter(l, t, "gA")) for l, t in pairs(mc, ac))
     check_adamw_of_own_grads(eng, mc, ac, state, sg["lr"], step + 1, sg["gnorm_raw"])
+    # at 28 layers the gradients differ from the FP64 oracle by their
+    # FP32-accumulation floor (2-6% per tensor), so the band of
+    # undetermined updates is wider than at one or two layers: at step 2 up
+    # to 26% of an A tensor's elements fall inside it (measured, l11.o.A)
     check_band(orc, eng, mc, ac, before={k: v for k, v in state.items() if k[2] in "AB"},
-               bar=lambda l, t, g: 2.0 * fl.get(f"l{l}.{t}.{g}", 5e-3))
+               bar=lambda l, t, g: 2.0 * fl.get(f"l{l}.{t}.{g}", 5e-3), excl=0.35)
     ca, cw = eng.centroid()
     oa, ow = orc.centroid()
     cf = st["floor"][step]["centroid"]

@@ -34,7 +34,7 @@ def compare(orc, eng, mc, ac, what, bar=1e-2):
     assert not bad, "; ".join(bad)
 
 
-def check_band(orc, eng, mc, ac, before=None, bar=1e-2):
+def check_band(orc, eng, mc, ac, before=None, bar=1e-2, excl=0.25):
     """Updated adapters vs the oracle where the update is determined.
 
     An AdamW update m_hat/(sqrt(v_hat)+eps) is a sign function of the
@@ -46,9 +46,9 @@ def check_band(orc, eng, mc, ac, before=None, bar=1e-2):
     at step 1) has relative L2 <= bar (1e-2, or a per-tensor bar given as
     bar(layer, target, "gA" | "gB")) against the oracle's; as a sanity
     bound on the gradient error, fewer
-    than 25% of elements are excluded (measured on MI355X: ~1% at c1, 3-10%
-    on the 2-layer config whose gradients differ from the oracle by up to
-    1e-2: one-ulp BF16 rounding differences propagate through the
+    than `excl` (25%) of elements are excluded (measured on MI355X: ~1% at
+    c1, 3-10% on the 2-layer config whose gradients differ from the oracle
+    by up to 1e-2: one-ulp BF16 rounding differences propagate through the
     layers)."""
     for l, t in pairs(mc, ac):
         for w in ("A", "B"):
@@ -62,7 +62,7 @@ def check_band(orc, eng, mc, ac, before=None, bar=1e-2):
             uo = (orc.adapter(l, t, w).astype(np.float64) - b0)[sure]
             ug = (eng.adapter(l, t, w).astype(np.float64) - b0)[sure]
             assert rel(ug, uo) <= b, (l, t, w, rel(ug, uo), b)
-            assert (~sure).mean() < 0.25, (l, t, w, float((~sure).mean()))
+            assert (~sure).mean() < excl, (l, t, w, float((~sure).mean()))
 
 
 def check_adamw_of_own_grads(eng, mc, ac, state, lr, t, gnorm_raw):
