@@ -519,9 +519,18 @@ static int next_wgrad(Engine* e, int NL, int NS, float** part) {
 // and the gB products were made already (the fused SwiGLU backward);
 // gA_part: the gA product is left to the caller, which receives its
 // partials slice (the fused SwiGLU backward makes it for the down pair).
+// The group's gA product, when the caller launches it after the input-
+// gradient GEMM (defer): the GEMM reads dh_cat, the product reads dh_cat
+// and x, and neither writes them, so the order between the two is free.
+struct GaDeferred {
+    const bf16* x = nullptr;
+    int in = 0;
+    int64_t ldh = 0;
+    float* part = nullptr;
+};
 static int lora_group_bwd(Engine* e, Layer& ly, std::initializer_list<int> group, const bf16* x,
                           int in, const bf16* const* gos, LoraEpi* ep, bool dh_ready = false,
-                          float** gA_part = nullptr) {
+                          float** gA_part = nullptr, GaDeferred* defer = nullptr) {
     *ep = LoraEpi{};
     int on[3], n = 0, i = 0;
     const bf16* go_on[3];
@@ -585,8 +594,19 @@ static int lora_group_bwd(Engine* e, Layer& ly, std::initializer_list<int> group
         *gA_part = part;
         return 0;
     }
+    if (defer) {
+        *defer = GaDeferred{x, in, ldh, part};
+        return 0;
+    }
     TIMED(TA_CAT_LORA, gflops(ldh, in, dBT), dBT * (in + ldh) * 2,
           lora_wgrad_part(x, in, in, e->dh_cat, ldh, (int)ldh, BT, part, e->s));
+    return 0;
+}
+static int ga_launch(Engine* e, const GaDeferred& d) {
+    if (!d.part) return 0;
+    const double dBT = e->BT;
+    TIMED(TA_CAT_LORA, gflops(d.ldh, d.in, dBT), dBT * (d.in + d.ldh) * 2,
+          lora_wgrad_part(d.x, d.in, d.in, e->dh_cat, d.ldh, (int)d.ldh, e->BT, d.part, e->s));
     return 0;
 }
 
@@ -794,11 +814,13 @@ static int backward(Engine* e) {
         {
             const bf16* gos[2] = {e->dgate, e->dup};
             LoraEpi ep;
-            CK(lora_group_bwd(e, ly, {PG, PU}, ly.xn2, H, gos, &ep, fused));
+            GaDeferred ga;
+            CK(lora_group_bwd(e, ly, {PG, PU}, ly.xn2, H, gos, &ep, fused, nullptr, &ga));
             // proj_bwd_x of gate (beta 0) then up (beta 1), qwen2.cu:233-234
             const GemmSeg sg[2] = {{I, e->dgate, I, ly.Wt[PG], I}, {I, e->dup, I, ly.Wt[PU], I}};
             TIMED(TA_CAT_GEMM_DX, 2.0 * gflops(BT, H, I), 2.0 * gbytes(BT, H, I, 2, 2, false),
                   gemm_chain(BT, H, sg, 2, e->dxn2, H, ep.n ? &ep : nullptr, s));
+            CK(ga_launch(e, ga));
         }
         // grad += bf16(rms_norm_bwd(dx_normed2)), one pass
         TIMED(TA_CAT_NORM, 0, nrm_b + dBT * H * 2,
@@ -808,8 +830,10 @@ static int backward(Engine* e) {
         {
             const bf16* gos[1] = {e->g_res};
             LoraEpi ep;
-            CK(lora_group_bwd(e, ly, {PO}, ly.ao, qd, gos, &ep));
+            GaDeferred ga;
+            CK(lora_group_bwd(e, ly, {PO}, ly.ao, qd, gos, &ep, false, nullptr, &ga));
             CK(proj_bwd_x(e, ly.Wt[PO], e->g_res, e->dao, H, qd, 0.f, &ep));
+            CK(ga_launch(e, ga));
         }
         TIMED(TA_CAT_ATTN_BWD, 12.0 * tri * c.head_dim,
               16.0 * e->B * c.n_q * e->T + dBT * (2.0 * qd + 2.0 * kvd) * 2 +
@@ -820,7 +844,8 @@ static int backward(Engine* e) {
         {
             const bf16* gos[3] = {e->dQ, e->dK, e->dV};
             LoraEpi ep;
-            CK(lora_group_bwd(e, ly, {PQ, PK, PV}, ly.xn, H, gos, &ep));
+            GaDeferred ga;
+            CK(lora_group_bwd(e, ly, {PQ, PK, PV}, ly.xn, H, gos, &ep, false, nullptr, &ga));
             // proj_bwd_x of q (beta 0), k and v (beta 1), qwen2.cu:283-285
             const GemmSeg sg[3] = {{qd, e->dQ, qd, ly.Wt[PQ], qd},
                                    {kvd, e->dK, kvd, ly.Wt[PK], kvd},
@@ -828,6 +853,7 @@ static int backward(Engine* e) {
             TIMED(TA_CAT_GEMM_DX, gflops(BT, H, qd + 2.0 * kvd),
                   gbytes(BT, H, qd + 2.0 * kvd, 2, 2, false),
                   gemm_chain(BT, H, sg, 3, e->dxn, H, ep.n ? &ep : nullptr, s));
+            CK(ga_launch(e, ga));
         }
         // centroid side channel (adapt_trainer.cu:210-232): h = x_normed,
         // g = dx_attn_in of this layer
