@@ -15,8 +15,8 @@
 // workgroup runs every iteration in a single launch.  Squared distances are
 // summed sequentially over d in F32 with no contraction (__fmul_rn/__fadd_rn),
 // exactly like a scalar CPU loop, so assignments are bit-reproducible; center
-// sums run sequentially over snapshots in index order.  Every loop is bounded
-// by max_iters / iters, so the launch always drains.
+// sums run over each center's members in snapshot index order.  Every loop
+// is bounded by max_iters / iters, so the launch always drains.
 #include <float.h>
 
 #include <mutex>
@@ -224,40 +224,82 @@ __global__ __launch_bounds__(64 * kRW) void k_centroid_reduce(const float* __res
 }
 
 // ── k-means ────────────────────────────────────────────────────────────
-// Squared distance summed sequentially over i in F32 without contraction.
-// Operands are loaded 32 elements at a time (independent loads in flight)
-// before the dependent chain over them; the order of the additions is the
-// plain loop's.
-__device__ __forceinline__ float sqdist_seq(const float* __restrict__ a,
-                                           const float* __restrict__ b, int D) {
-    // hipcc would contract v * v + d into one FMA (one rounding where the
-    // sequential form rounds twice): each product passes through an empty
-    // asm statement, which no instruction combiner can look through
-    constexpr int CH = 32;
-    float d = 0.f;
+// Squared distances are sums over i = 0 .. D-1 in order, in F32, each term
+// (a_i - b_i)^2 rounded before it is added (no contraction), like the
+// reference's scalar loop.
+//
+// Snapshots staged in LDS keep row n's 16-byte chunks XOR-permuted by
+// n & sw (sw + 1: the largest power of two up to 16 dividing D / 4):
+// element (n, i) sits at n * D + snap_col(n, i, sw).  Rows read at one
+// chunk by the lanes (the distance chains, one row per lane) then fall in
+// distinct bank groups, and 64 consecutive columns of one row (the center
+// sums, one column per lane) in distinct banks; every chain still visits i
+// in order.  Snapshots read from global memory are not permuted (sw = 0).
+__device__ __forceinline__ int snap_swizzle(int D) {
+    return D % 4 == 0 ? min(16, (D >> 2) & -(D >> 2)) - 1 : 0;
+}
+__device__ __forceinline__ int snap_col(int n, int i, int sw) {
+    return ((((i >> 2) ^ (n & sw))) << 2) | (i & 3);
+}
+
+// (a - b)^2 as the reference rounds it: hipcc would contract v * v + d into
+// one FMA (one rounding where the sequential form rounds twice), so each
+// product passes through an empty asm statement, which no instruction
+// combiner can look through
+__device__ __forceinline__ float sq_term(float a, float b) {
+    const float v = __fsub_rn(a, b);
+    float q = __fmul_rn(v, v);
+    asm volatile("" : "+v"(q));
+    return q;
+}
+
+// J distance chains: row n[r] of the snapshots X (permuted by sw) against
+// the center at cb[r] (its chunks permuted by kb[r]).  With vec (D % 4 == 0,
+// rows and centers 16-byte aligned) the operands move as 16-byte chunks, CH
+// elements of every chain loaded before the dependent chains over them.
+template <int J, int CH>
+__device__ __forceinline__ void sqdist_chains(const float* __restrict__ X, int D, int sw, bool vec,
+                                              const int (&n)[J], const float* const (&cb)[J],
+                                              const int (&kb)[J], float (&out)[J]) {
+    static_assert(CH % 4 == 0, "whole chunks");
+    float d[J];
+    int ka[J];
+    const float* ar[J];
+#pragma unroll
+    for (int r = 0; r < J; r++) {
+        d[r] = 0.f;
+        ka[r] = n[r] & sw;
+        ar[r] = X + (int64_t)n[r] * D;
+    }
     int i = 0;
-    for (; i + CH <= D; i += CH) {
-        float av[CH], bv[CH];
+    if (vec) {
+        for (; i + CH <= D; i += CH) {
+            float4 av[J][CH / 4], bv[J][CH / 4];
 #pragma unroll
-        for (int j = 0; j < CH; j++) {
-            av[j] = a[i + j];
-            bv[j] = b[i + j];
-        }
+            for (int r = 0; r < J; r++)
 #pragma unroll
-        for (int j = 0; j < CH; j++) {
-            float v = __fsub_rn(av[j], bv[j]);
-            float q = __fmul_rn(v, v);
-            asm volatile("" : "+v"(q));
-            d = __fadd_rn(d, q);
+                for (int q = 0; q < CH / 4; q++) {
+                    const int ch = (i >> 2) + q;
+                    av[r][q] = *(const float4*)(ar[r] + ((ch ^ ka[r]) << 2));
+                    bv[r][q] = *(const float4*)(cb[r] + ((ch ^ kb[r]) << 2));
+                }
+#pragma unroll
+            for (int q = 0; q < CH / 4; q++)
+#pragma unroll
+                for (int r = 0; r < J; r++) {
+                    d[r] = __fadd_rn(d[r], sq_term(av[r][q].x, bv[r][q].x));
+                    d[r] = __fadd_rn(d[r], sq_term(av[r][q].y, bv[r][q].y));
+                    d[r] = __fadd_rn(d[r], sq_term(av[r][q].z, bv[r][q].z));
+                    d[r] = __fadd_rn(d[r], sq_term(av[r][q].w, bv[r][q].w));
+                }
         }
     }
-    for (; i < D; i++) {
-        float v = __fsub_rn(a[i], b[i]);
-        float q = __fmul_rn(v, v);
-        asm volatile("" : "+v"(q));
-        d = __fadd_rn(d, q);
-    }
-    return d;
+    for (; i < D; i++)
+#pragma unroll
+        for (int r = 0; r < J; r++)
+            d[r] = __fadd_rn(d[r], sq_term(ar[r][snap_col(n[r], i, sw)], cb[r][snap_col(kb[r], i, sw)]));
+#pragma unroll
+    for (int r = 0; r < J; r++) out[r] = d[r];
 }
 
 __device__ __forceinline__ uint64_t splitmix64(uint64_t& s) {
@@ -270,69 +312,29 @@ __device__ __forceinline__ double u01(uint64_t& s) {
     return (double)(splitmix64(s) >> 11) * (1.0 / 9007199254740992.0);
 }
 
-// Up to J distance chains against one center b (rows a0 + i * astride,
-// i < na), each chain in the order of sqdist_seq: every center chunk is
-// loaded once for all rows.
-template <int J>
-__device__ __forceinline__ void sqdist_seq_rows(const float* __restrict__ a0, int64_t astride,
-                                                int na, const float* __restrict__ b, int D,
-                                                float* __restrict__ out) {
-    constexpr int CH = 32;
-    float d[J];
-#pragma unroll
-    for (int r = 0; r < J; r++) d[r] = 0.f;
-    int i = 0;
-    for (; i + CH <= D; i += CH) {
-        float bv[CH];
-#pragma unroll
-        for (int j = 0; j < CH; j++) bv[j] = b[i + j];
-#pragma unroll
-        for (int r = 0; r < J; r++) {
-            if (r >= na) break;
-            const float* a = a0 + r * astride + i;
-            float av[CH];
-#pragma unroll
-            for (int j = 0; j < CH; j++) av[j] = a[j];
-#pragma unroll
-            for (int j = 0; j < CH; j++) {
-                float v = __fsub_rn(av[j], bv[j]);
-                float q = __fmul_rn(v, v);
-                asm volatile("" : "+v"(q));
-                d[r] = __fadd_rn(d[r], q);
-            }
-        }
-    }
-    for (; i < D; i++)
-#pragma unroll
-        for (int r = 0; r < J; r++) {
-            if (r >= na) break;
-            float v = __fsub_rn(a0[r * astride + i], b[i]);
-            float q = __fmul_rn(v, v);
-            asm volatile("" : "+v"(q));
-            d[r] = __fadd_rn(d[r], q);
-        }
-#pragma unroll
-    for (int r = 0; r < J; r++)
-        if (r < na) out[r] = d[r];
-}
-
-// assignment pass: dist[n*k + c] for all pairs, then argmin per n (strict <)
-__device__ __forceinline__ int kmeans_assign(const float* __restrict__ X, const float* __restrict__ C, int N,
-                             int D, int k, float* __restrict__ dist, int32_t* __restrict__ asg) {
-    const int nt = blockDim.x;
-    if (nt % k == 0 && (int64_t)N * k <= 2ll * nt) {
-        // a thread's pairs p = tid + j * nt share the center c = tid % k:
-        // rows n0 and n0 + nt / k
-        const int c = threadIdx.x % k, n0 = threadIdx.x / k, st = nt / k;
-        const int na = n0 < N ? (n0 + st < N ? 2 : 1) : 0;
-        float dd[2];
-        if (na > 0)
-            sqdist_seq_rows<2>(X + (int64_t)n0 * D, (int64_t)st * D, na, C + (int64_t)c * D, D, dd);
-        if (na > 0) dist[(int64_t)n0 * k + c] = dd[0];
-        if (na > 1) dist[(int64_t)(n0 + st) * k + c] = dd[1];
-    } else {
-        for (int p = threadIdx.x; p < N * k; p += blockDim.x)
-            dist[p] = sqdist_seq(X + (int64_t)(p / k) * D, C + (int64_t)(p % k) * D, D);
+// Assignment pass: every (center, snapshot) distance into dist [k][N], then
+// each snapshot's argmin over the centers (strict <, so the first of equal
+// distances).  A wave takes one center at a time (read at one address by all
+// its lanes) against 64 snapshots (one per lane), two such units at once.
+// C: the centers [k][D], not permuted.  Returns whether any assignment
+// changed (block-wide).
+__device__ __forceinline__ int kmeans_assign(const float* __restrict__ X, int sw, bool vec,
+                                             const float* __restrict__ C, int N, int D, int k,
+                                             float* __restrict__ dist, int32_t* __restrict__ asg) {
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), nw = blockDim.x >> 6;
+    const int nb = (N + 63) / 64, units = k * nb;
+    for (int u = w; u < units; u += 2 * nw) {
+        const int u1 = u + nw < units ? u + nw : u;
+        const int c0 = u / nb, c1 = u1 / nb;
+        const int r0 = (u % nb) * 64 + lane, r1 = (u1 % nb) * 64 + lane;
+        const int n[2] = {min(r0, N - 1), min(r1, N - 1)};
+        const float* const cb[2] = {C + (int64_t)c0 * D, C + (int64_t)c1 * D};
+        const int kb[2] = {0, 0};
+        float d[2];
+        sqdist_chains<2, 16>(X, D, sw, vec, n, cb, kb, d);
+        if (r0 < N) dist[(int64_t)c0 * N + r0] = d[0];
+        if (u1 != u && r1 < N) dist[(int64_t)c1 * N + r1] = d[1];
     }
     __syncthreads();
     int changed = 0;
@@ -340,7 +342,7 @@ __device__ __forceinline__ int kmeans_assign(const float* __restrict__ X, const 
         float best = 1e38f;
         int bk = 0;
         for (int c = 0; c < k; c++) {
-            float d = dist[(int64_t)n * k + c];
+            const float d = dist[(int64_t)c * N + n];
             if (d < best) {
                 best = d;
                 bk = c;
@@ -354,37 +356,40 @@ __device__ __forceinline__ int kmeans_assign(const float* __restrict__ X, const 
     return __syncthreads_or(changed);
 }
 
-// update pass: center c = mean of members (sequential over n); empty ->
-// zero (reference mode) or unchanged (stress mode)
-__device__ __forceinline__ void kmeans_update(const float* __restrict__ X, float* __restrict__ C, int N, int D,
-                              int k, const int32_t* __restrict__ asg, bool empty_to_zero) {
+// Update pass: center c = the mean of its members, summed in snapshot index
+// order; an empty center becomes zero (reference mode) or stays (stress
+// mode).  When every wave's 64 outputs belong to one center (D a multiple of
+// 64), a ballot over 64 assignments at a time gives its members in index
+// order and only their values are read; otherwise each output scans every
+// snapshot.  Either way the same chain of additions.
+__device__ __forceinline__ void kmeans_update(const float* __restrict__ X, int sw,
+                                              float* __restrict__ C, int N, int D, int k,
+                                              const int32_t* __restrict__ asg,
+                                              bool empty_to_zero) {
+    const bool ballot = D % 64 == 0 && blockDim.x % 64 == 0;
+    const int lane = threadIdx.x & 63;
     for (int p = threadIdx.x; p < k * D; p += blockDim.x) {
-        int c = p / D, d = p % D;
+        const int c = p / D, d = p % D;
         float s = 0.f;
         int cnt = 0;
-        // members' values loaded 16 snapshots at a time, added in index order
-        constexpr int CH = 16;
-        int n = 0;
-        for (; n + CH <= N; n += CH) {
-            float xv[CH];
-            int av[CH];
-#pragma unroll
-            for (int j = 0; j < CH; j++) {
-                xv[j] = X[(int64_t)(n + j) * D + d];
-                av[j] = asg[n + j];
+        if (ballot) {
+            for (int n0 = 0; n0 < N; n0 += 64) {
+                const int a = n0 + lane < N ? asg[n0 + lane] : -1;
+                uint64_t mem = __ballot(a == c);
+                while (mem) {
+                    const int n = n0 + __builtin_ctzll(mem);
+                    mem &= mem - 1;
+                    s = __fadd_rn(s, X[(int64_t)n * D + snap_col(n, d, sw)]);
+                    cnt++;
+                }
             }
-#pragma unroll
-            for (int j = 0; j < CH; j++)
-                if (av[j] == c) {
-                    s = __fadd_rn(s, xv[j]);
+        } else {
+            for (int n = 0; n < N; n++)
+                if (asg[n] == c) {
+                    s = __fadd_rn(s, X[(int64_t)n * D + snap_col(n, d, sw)]);
                     cnt++;
                 }
         }
-        for (; n < N; n++)
-            if (asg[n] == c) {
-                s = __fadd_rn(s, X[(int64_t)n * D + d]);
-                cnt++;
-            }
         if (cnt > 0)
             C[p] = s / (float)cnt;
         else if (empty_to_zero)
@@ -393,16 +398,23 @@ __device__ __forceinline__ void kmeans_update(const float* __restrict__ X, float
     __syncthreads();
 }
 
-// Snapshots that fit kXs floats are copied into LDS once (XL): the
-// distance chains and the center sums then read them from LDS.
+// Snapshots that fit kXs floats are copied into LDS once (XL, permuted as
+// above): the distance chains and the center sums then read them from LDS.
 constexpr int kXs = 32768;  // 128 KB
 constexpr int kDs = 4096;   // distances held in LDS by k_kmeans_pp<true>
 
 template <bool XL>
 __device__ __forceinline__ const float* stage_snapshots(const float* __restrict__ Xg, float* xs,
-                                                        int N, int D) {
-    if constexpr (!XL) return Xg;
-    for (int p = threadIdx.x; p < N * D; p += blockDim.x) xs[p] = Xg[p];
+                                                        int N, int D, int& sw) {
+    if constexpr (!XL) {
+        sw = 0;
+        return Xg;
+    }
+    sw = snap_swizzle(D);
+    for (int p = threadIdx.x; p < N * D; p += blockDim.x) {
+        const int n = p / D, d = p % D;
+        xs[(int64_t)n * D + snap_col(n, d, sw)] = Xg[p];
+    }
     __syncthreads();
     return xs;
 }
@@ -413,20 +425,21 @@ __global__ __launch_bounds__(1024) void k_kmeans_ref(const float* __restrict__ X
                                                      float* __restrict__ C,
                                                      int32_t* __restrict__ asg,
                                                      float* __restrict__ dist,
-                                                     int32_t* __restrict__ iters_out) {
-    __shared__ float xs[XL ? kXs : 1];
-    const float* __restrict__ X = stage_snapshots<XL>(Xg, xs, N, D);
+                                                     int32_t* __restrict__ iters_out, bool vec) {
+    __shared__ __attribute__((aligned(16))) float xs[XL ? kXs : 1];
+    int sw = 0;
+    const float* __restrict__ X = stage_snapshots<XL>(Xg, xs, N, D, sw);
     for (int p = threadIdx.x; p < k * D; p += blockDim.x) {
-        int c = p / D, d = p % D;
-        C[p] = X[(int64_t)(((int64_t)c * N) / k) * D + d];
+        const int c = p / D, d = p % D, n = (int)(((int64_t)c * N) / k);
+        C[p] = X[(int64_t)n * D + snap_col(n, d, sw)];
     }
     for (int n = threadIdx.x; n < N; n += blockDim.x) asg[n] = 0;
     __syncthreads();
     int it = 0;
     for (; it < max_iters; it++) {
-        int changed = kmeans_assign(X, C, N, D, k, dist, asg);
+        int changed = kmeans_assign(X, sw, vec, C, N, D, k, dist, asg);
         if (!changed) break;
-        kmeans_update(X, C, N, D, k, asg, true);
+        kmeans_update(X, sw, C, N, D, k, asg, true);
     }
     if (threadIdx.x == 0 && iters_out) *iters_out = it;
 }
@@ -437,12 +450,12 @@ __global__ __launch_bounds__(1024) void k_kmeans_pp(const float* __restrict__ Xg
                                                     int k, int iters, uint64_t seed,
                                                     float* __restrict__ Cw,  // [k*D] work
                                                     float* __restrict__ d2g,  // [N]
-                                                    float* __restrict__ distg,  // [N*k]
+                                                    float* __restrict__ distg,  // [k*N]
                                                     int32_t* __restrict__ asgg,  // [N]
                                                     float* __restrict__ C_out,
                                                     int32_t* __restrict__ asg_out,
                                                     double* __restrict__ mass_out,
-                                                    int32_t* __restrict__ seeds_out) {
+                                                    int32_t* __restrict__ seeds_out, bool vec) {
     // XL (N*D <= kXs, N <= 1024, N*k <= kDs): snapshots, assignments,
     // distances and the seeding distances in LDS; the ranking arrays reuse
     // the snapshot region once the last assignment pass has read it
@@ -454,7 +467,8 @@ __global__ __launch_bounds__(1024) void k_kmeans_pp(const float* __restrict__ Xg
     __shared__ float sd2[XL ? 1024 : 1];
     __shared__ double smass[XL ? 1 : 1024];
     __shared__ int sorder[XL ? 1 : 1024], srank[XL ? 1 : 1024];
-    const float* __restrict__ X = stage_snapshots<XL>(Xg, xs, N, D);
+    int sw = 0;
+    const float* __restrict__ X = stage_snapshots<XL>(Xg, xs, N, D, sw);
     int32_t* asg = XL ? sasg : asgg;
     float* dist = XL ? sdist : distg;
     float* d2 = XL ? sd2 : d2g;
@@ -471,10 +485,14 @@ __global__ __launch_bounds__(1024) void k_kmeans_pp(const float* __restrict__ Xg
     __syncthreads();
     // k-means++ seeding
     for (int m = 1; m < k; m++) {
-        const float* c = X + (int64_t)chosen[m - 1] * D;
+        const int cm = chosen[m - 1];
         for (int n = threadIdx.x; n < N; n += blockDim.x) {
-            float d = sqdist_seq(X + (int64_t)n * D, c, D);
-            if (d < d2[n]) d2[n] = d;
+            const int nn[1] = {n};
+            const float* const cb[1] = {X + (int64_t)cm * D};
+            const int kb[1] = {cm & sw};
+            float d[1];
+            sqdist_chains<1, 32>(X, D, sw, vec, nn, cb, kb, d);
+            if (d[0] < d2[n]) d2[n] = d[0];
         }
         __syncthreads();
         if (threadIdx.x == 0) {
@@ -493,15 +511,17 @@ __global__ __launch_bounds__(1024) void k_kmeans_pp(const float* __restrict__ Xg
         }
         __syncthreads();
     }
-    for (int p = threadIdx.x; p < k * D; p += blockDim.x)
-        Cw[p] = X[(int64_t)chosen[p / D] * D + (p % D)];
+    for (int p = threadIdx.x; p < k * D; p += blockDim.x) {
+        const int n = chosen[p / D], d = p % D;
+        Cw[p] = X[(int64_t)n * D + snap_col(n, d, sw)];
+    }
     for (int n = threadIdx.x; n < N; n += blockDim.x) asg[n] = 0;
     __syncthreads();
     for (int it = 0; it < iters; it++) {
-        kmeans_assign(X, Cw, N, D, k, dist, asg);
-        kmeans_update(X, Cw, N, D, k, asg, false);
+        kmeans_assign(X, sw, vec, Cw, N, D, k, dist, asg);
+        kmeans_update(X, sw, Cw, N, D, k, asg, false);
     }
-    kmeans_assign(X, Cw, N, D, k, dist, asg);
+    kmeans_assign(X, sw, vec, Cw, N, D, k, dist, asg);
     // rank by member weight (F64, index order), stable descending
     if (threadIdx.x == 0) {
         for (int c = 0; c < k; c++) mass[c] = 0.0;
@@ -649,12 +669,17 @@ int ta_kmeans_ref(const float* snaps, int N, int D, int k, int max_iters, float*
     hipStream_t s = (hipStream_t)stream;
     float* dist = (float*)scratch_get((size_t)N * k * sizeof(float), s);
     TA_REQUIRE(dist, "kmeans_ref: scratch allocation failed");
-    if ((int64_t)N * D <= kXs)
+    // 16-byte operand loads: whole chunks, and aligned snapshots (when read
+    // from global memory) and centers
+    const bool xl = (int64_t)N * D <= kXs;
+    const bool vec = D % 4 == 0 && ((uintptr_t)centers & 15) == 0 &&
+                     (xl || ((uintptr_t)snaps & 15) == 0);
+    if (xl)
         k_kmeans_ref<true><<<1, 1024, 0, s>>>(snaps, N, D, k, max_iters, centers, assign, dist,
-                                              iters_out);
+                                              iters_out, vec);
     else
         k_kmeans_ref<false><<<1, 1024, 0, s>>>(snaps, N, D, k, max_iters, centers, assign, dist,
-                                               iters_out);
+                                               iters_out, vec);
     return check_launch("kmeans_ref");
 }
 
@@ -672,16 +697,19 @@ int ta_kmeans_pp(const float* snaps, const float* weights, int N, int D, int k, 
     size_t total = off_asg + (size_t)N * sizeof(int32_t);
     char* base = (char*)scratch_get(total, s);
     TA_REQUIRE(base, "kmeans_pp: scratch allocation failed");
-    if ((int64_t)N * D <= kXs && N <= 1024 && (int64_t)N * k <= kDs)
+    // (the work centers sit at the scratch's 256-byte aligned start)
+    const bool xl = (int64_t)N * D <= kXs && N <= 1024 && (int64_t)N * k <= kDs;
+    const bool vec = D % 4 == 0 && (xl || ((uintptr_t)snaps & 15) == 0);
+    if (xl)
         k_kmeans_pp<true><<<1, 1024, 0, s>>>(snaps, weights, N, D, k, iters, seed, (float*)base,
                                              (float*)(base + off_d2), (float*)(base + off_dist),
                                              (int32_t*)(base + off_asg), centers, assign, mass,
-                                             seeds);
+                                             seeds, vec);
     else
         k_kmeans_pp<false><<<1, 1024, 0, s>>>(snaps, weights, N, D, k, iters, seed, (float*)base,
                                               (float*)(base + off_d2), (float*)(base + off_dist),
                                               (int32_t*)(base + off_asg), centers, assign, mass,
-                                              seeds);
+                                              seeds, vec);
     return check_launch("kmeans_pp");
 }
 

@@ -405,7 +405,12 @@ def mixture(N, D, comps, seed):
     return (means[lab] + 0.3 * r.standard_normal((N, D))).astype(np.float32)
 
 
-@pytest.mark.parametrize("N,D,k", [(64, 512, 32), (50, 64, 8), (5, 16, 8)])
+# (200, 128, 16): the center sums over four 64-snapshot ballots; (300, 256,
+# 12): snapshots past the 128 KB LDS copy (read from global memory); D = 16:
+# the per-output scan over every snapshot; D = 30: element-wise loads, no
+# column permutation
+@pytest.mark.parametrize("N,D,k", [(64, 512, 32), (50, 64, 8), (5, 16, 8), (200, 128, 16),
+                                   (300, 256, 12), (20, 30, 4)])
 def test_kmeans_ref_bit_exact(N, D, k):
     X = mixture(N, D, 16, N + D)
     kk = min(k, N)
@@ -419,8 +424,8 @@ def test_kmeans_ref_bit_exact(N, D, k):
     assert int(host(it)[0]) == ri
 
 
-def test_kmeans_pp_bit_exact():
-    N, D, k = 64, 512, 32
+@pytest.mark.parametrize("N,D,k", [(64, 512, 32), (200, 128, 16), (300, 256, 12), (40, 48, 6)])
+def test_kmeans_pp_bit_exact(N, D, k):
     X = mixture(N, D, 16, 7)
     W = np.random.default_rng(3).lognormal(0, 1, N).astype(np.float32)
     C = torch.empty(k * D, dtype=torch.float32, device=DEV)
