@@ -265,11 +265,16 @@ int ta_scratch_release(void* stream);
  * skinny products h = xA^T / dh = goB, 6 the LoRA weight gradients with
  * their reduction, 7 the chained input-gradient GEMMs, 8 the gate/up
  * projections with the SwiGLU product; -1 stops)
- * with events recorded on the launch's own stream.  ta_kprof_read waits for
+ * with start and stop events carried by the launch's own dispatch on its
+ * stream.  ta_kprof_pause(1) leaves the selection and the recorded launches
+ * as they are but times no further launch until ta_kprof_pause(0) (timing
+ * costs a few microseconds of idle GPU around each timed launch, so a
+ * measurement can time a sample of steps).  ta_kprof_read waits for
  * the recorded launches and returns their summed time, count, algorithmic
  * flops and HBM bytes, then clears them; ta_kprof_name gives the timed
  * kernel's symbol as a profiler prints it ("" before its first launch). */
 int ta_kprof_select(int kid);
+int ta_kprof_pause(int paused);
 int ta_kprof_read(double* ms, int64_t* launches, double* flops, double* bytes);
 const char* ta_kprof_name(int kid);
 

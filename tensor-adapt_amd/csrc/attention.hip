@@ -1654,9 +1654,9 @@ int attn_fwd(const bf16* Q, const bf16* K, const bf16* V, bf16* O, float* O32, f
     const bool timed = kprof_begin(KP_ATTN_FWD, s);
     float2* st = (float2*)stats;
 #define AF(H) \
-    k_attn_fwd<H, true><<<(int)blocks, 256, 0, s>>>(Q, K, V, O, O32, P, st, T, Hq, Hkv, scale, zero_fill)
+    tlaunch(k_attn_fwd<H, true>, dim3((int)blocks), dim3(256), s, Q, K, V, O, O32, P, st, T, Hq, Hkv, scale, zero_fill)
 #define AF1(H)                                                                             \
-    k_attn_fwd_t<H><<<(int)((int64_t)B * Hq * ((T + TQ2 - 1) / TQ2)), 256, 0, s>>>(         \
+    tlaunch(k_attn_fwd_t<H>, dim3((int)((int64_t)B * Hq * ((T + TQ2 - 1) / TQ2))), dim3(256), s, \
         Q, K, V, O, O32, st, T, Hq, Hkv, scale)
     // with P: two passes (P normalised when it is written); without: one
     if (hd == 64) {
@@ -1751,9 +1751,9 @@ int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const 
     // stored P: the reference's form (64-query tiles); recompute: the
     // transposed-score kernel (128-query blocks)
 #define DQ(H)                                                                             \
-    k_attn_bwd_dq<H><<<(int)b1, 256, 0, s>>>(dO, K, V, P, Dbuf, dQ, T, Hq, Hkv, scale)
+    tlaunch(k_attn_bwd_dq<H>, dim3((int)b1), dim3(256), s, dO, K, V, P, Dbuf, dQ, T, Hq, Hkv, scale)
 #define DQT(H)                                                                            \
-    k_attn_bwd_dq_t<H><<<(int)((int64_t)B * Hq * ((T + TQ2 - 1) / TQ2)), 256, 0, s>>>(        \
+    tlaunch(k_attn_bwd_dq_t<H>, dim3((int)((int64_t)B * Hq * ((T + TQ2 - 1) / TQ2))), dim3(256), s, \
         dO, Q, K, V, st, Dbuf, O32, dQ, T, Hq, Hkv, scale, rtab)
     if (hd == 64) {
         if (rc) DQT(64); else DQ(64);
@@ -1771,15 +1771,15 @@ int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const 
     if (rc) {
         const int blocks = nkb * B * Hkv * nsplit;
         if (hd == 64)
-            k_attn_bwd_dkv_r<64><<<blocks, 512, 0, s>>>(dO, Q, K, V, Dbuf, part, dK, dV, T, Hq,
+            tlaunch(k_attn_bwd_dkv_r<64>, dim3(blocks), dim3(512), s, dO, Q, K, V, Dbuf, part, dK, dV, T, Hq,
                                                          Hkv, nsplit, scale, rtab);
         else
-            k_attn_bwd_dkv_r<128><<<blocks, 512, 0, s>>>(dO, Q, K, V, Dbuf, part, dK, dV, T, Hq,
+            tlaunch(k_attn_bwd_dkv_r<128>, dim3(blocks), dim3(512), s, dO, Q, K, V, Dbuf, part, dK, dV, T, Hq,
                                                           Hkv, nsplit, scale, rtab);
     } else if (hd == 64) {
-        k_attn_bwd_dkv<64><<<(int)b1, 256, 0, s>>>(dO, Q, V, P, Dbuf, part, T, Hq, Hkv);
+        tlaunch(k_attn_bwd_dkv<64>, dim3((int)b1), dim3(256), s, dO, Q, V, P, Dbuf, part, T, Hq, Hkv);
     } else {
-        k_attn_bwd_dkv<128><<<(int)b1, 256, 0, s>>>(dO, Q, V, P, Dbuf, part, T, Hq, Hkv);
+        tlaunch(k_attn_bwd_dkv<128>, dim3((int)b1), dim3(256), s, dO, Q, V, P, Dbuf, part, T, Hq, Hkv);
     }
     if (timed)
         kprof_end(KP_ATTN_BWD_DKV, s, 6.0 * hd * tri + rf,

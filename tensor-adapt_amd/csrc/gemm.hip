@@ -1526,11 +1526,11 @@ static const char* big_name(int variant) {
 template <int EPI>
 static void launch_big(int variant, dim3 grid, const GemmArgs& a, hipStream_t s) {
     switch (variant) {
-        case 8: k_gemm_dma<256, EPI, 4, 4, 2><<<grid, 512, 0, s>>>(a); break;
-        case 9: k_gemm_dma<192, EPI, 5, 4, 2><<<grid, 512, 0, s>>>(a); break;
-        case 10: k_gemm_dma<256, EPI, 4, 2, 2><<<grid, 256, 0, s>>>(a); break;
-        case 11: k_gemm_dma<192, EPI, 4, 2, 2><<<grid, 256, 0, s>>>(a); break;
-        default: k_gemm_dma<192, EPI, 4, 4, 2><<<grid, 512, 0, s>>>(a); break;
+        case 8: tlaunch(k_gemm_dma<256, EPI, 4, 4, 2>, dim3(grid), dim3(512), s, a); break;
+        case 9: tlaunch(k_gemm_dma<192, EPI, 5, 4, 2>, dim3(grid), dim3(512), s, a); break;
+        case 10: tlaunch(k_gemm_dma<256, EPI, 4, 2, 2>, dim3(grid), dim3(256), s, a); break;
+        case 11: tlaunch(k_gemm_dma<192, EPI, 4, 2, 2>, dim3(grid), dim3(256), s, a); break;
+        default: tlaunch(k_gemm_dma<192, EPI, 4, 4, 2>, dim3(grid), dim3(512), s, a); break;
     }
 }
 
@@ -1680,9 +1680,9 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
             const bool timed = kprof_begin(KP_GEMM_BIG, s);
             dim3 grid(a.tiles_m * a.tiles_n);
             if (bn == 128)
-                k_gemm_mid<128><<<grid, 256, 0, s>>>(a);
+                tlaunch(k_gemm_mid<128>, dim3(grid), dim3(256), s, a);
             else
-                k_gemm_mid<64><<<grid, 256, 0, s>>>(a);
+                tlaunch(k_gemm_mid<64>, dim3(grid), dim3(256), s, a);
             if (timed) {
                 double mn = (double)M * N;
                 double fl = 2.0 * mn * K + 2.0 * mn * a.lora_r * a.lora_n;
@@ -1804,19 +1804,19 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
         const int kid = BNb == 256 ? KP_GEMM_BIG_WIDE : KP_GEMM_BIG;
         const bool timed = kprof_begin(kid, s);
         if (variant == 12)
-            k_gemm_pipe<192, 2, 2><<<grid, 256, 0, s>>>(a);
+            tlaunch(k_gemm_pipe<192, 2, 2>, dim3(grid), dim3(256), s, a);
         else if (variant == 13)
-            k_gemm_pipe<256, 2, 2><<<grid, 256, 0, s>>>(a);
+            tlaunch(k_gemm_pipe<256, 2, 2>, dim3(grid), dim3(256), s, a);
         else if (variant == 14)
-            k_gemm_pipe<256, 4, 2><<<grid, 512, 0, s>>>(a);
+            tlaunch(k_gemm_pipe<256, 4, 2>, dim3(grid), dim3(512), s, a);
         else if (variant == 15)
-            k_gemm_pipe<192, 4, 2><<<grid, 512, 0, s>>>(a);
+            tlaunch(k_gemm_pipe<192, 4, 2>, dim3(grid), dim3(512), s, a);
         else if (variant == 16)
-            k_gemm_pipe<256, 2, 4><<<grid, 512, 0, s>>>(a);
+            tlaunch(k_gemm_pipe<256, 2, 4>, dim3(grid), dim3(512), s, a);
         else if (variant == 17)
-            k_gemm_pipe<192, 4, 2, 64><<<grid, 512, 0, s>>>(a);
+            tlaunch(k_gemm_pipe<192, 4, 2, 64>, dim3(grid), dim3(512), s, a);
         else if (variant == 18)
-            k_gemm_pipe<256, 2, 4, 64><<<grid, 512, 0, s>>>(a);
+            tlaunch(k_gemm_pipe<256, 2, 4, 64>, dim3(grid), dim3(512), s, a);
         else
             launch_big<EPI_BF16>(variant, grid, a, s);
         if (timed) {
@@ -2005,17 +2005,17 @@ int gemm_chain(int M, int N, const GemmSeg* sg, int ns, bf16* C, int64_t ldc, co
     dim3 grid(a.tiles_m * a.tiles_n);
     const bool timed = kprof_begin(KP_GEMM_CHAIN, s);
     if (mid == 128)
-        k_gemm_mid_chain<128><<<grid, 256, 0, s>>>(a);
+        tlaunch(k_gemm_mid_chain<128>, dim3(grid), dim3(256), s, a);
     else if (mid == 64)
-        k_gemm_mid_chain<64><<<grid, 256, 0, s>>>(a);
+        tlaunch(k_gemm_mid_chain<64>, dim3(grid), dim3(256), s, a);
     else if (BNb == 192 && KD == 64)
-        k_gemm_pipe_chain<192, 4, 2, 64><<<grid, 512, 0, s>>>(a);
+        tlaunch(k_gemm_pipe_chain<192, 4, 2, 64>, dim3(grid), dim3(512), s, a);
     else if (KD == 64)
-        k_gemm_pipe_chain<256, 2, 4, 64><<<grid, 512, 0, s>>>(a);
+        tlaunch(k_gemm_pipe_chain<256, 2, 4, 64>, dim3(grid), dim3(512), s, a);
     else if (BNb == 192)
-        k_gemm_pipe_chain<192, 4, 2><<<grid, 512, 0, s>>>(a);
+        tlaunch(k_gemm_pipe_chain<192, 4, 2>, dim3(grid), dim3(512), s, a);
     else
-        k_gemm_pipe_chain<256, 2, 4><<<grid, 512, 0, s>>>(a);
+        tlaunch(k_gemm_pipe_chain<256, 2, 4>, dim3(grid), dim3(512), s, a);
     if (timed) {
         // every link's operands read once, C written once, rank-r epilogue products
         double mn = (double)M * N;
@@ -2159,23 +2159,23 @@ int gemm_groups(int M, int K, const bf16* X, int64_t ldx, int64_t ldy, const Gem
     const bool timed = kprof_begin(kid, s);
     dim3 grid(a.tiles_m * a.tiles_n);
     if (mid == 128)
-        k_gemm_mid<128><<<grid, 256, 0, s>>>(a);
+        tlaunch(k_gemm_mid<128>, dim3(grid), dim3(256), s, a);
     else if (mid == 64)
-        k_gemm_mid<64><<<grid, 256, 0, s>>>(a);
+        tlaunch(k_gemm_mid<64>, dim3(grid), dim3(256), s, a);
     else if (variant == 12)
-        k_gemm_pipe<192, 2, 2><<<grid, 256, 0, s>>>(a);
+        tlaunch(k_gemm_pipe<192, 2, 2>, dim3(grid), dim3(256), s, a);
     else if (variant == 13)
-        k_gemm_pipe<256, 2, 2><<<grid, 256, 0, s>>>(a);
+        tlaunch(k_gemm_pipe<256, 2, 2>, dim3(grid), dim3(256), s, a);
     else if (variant == 14)
-        k_gemm_pipe<256, 4, 2><<<grid, 512, 0, s>>>(a);
+        tlaunch(k_gemm_pipe<256, 4, 2>, dim3(grid), dim3(512), s, a);
     else if (variant == 15)
-        k_gemm_pipe<192, 4, 2><<<grid, 512, 0, s>>>(a);
+        tlaunch(k_gemm_pipe<192, 4, 2>, dim3(grid), dim3(512), s, a);
     else if (variant == 17)
-        k_gemm_pipe<192, 4, 2, 64><<<grid, 512, 0, s>>>(a);
+        tlaunch(k_gemm_pipe<192, 4, 2, 64>, dim3(grid), dim3(512), s, a);
     else if (variant == 18)
-        k_gemm_pipe<256, 2, 4, 64><<<grid, 512, 0, s>>>(a);
+        tlaunch(k_gemm_pipe<256, 2, 4, 64>, dim3(grid), dim3(512), s, a);
     else
-        k_gemm_pipe<256, 2, 4><<<grid, 512, 0, s>>>(a);
+        tlaunch(k_gemm_pipe<256, 2, 4>, dim3(grid), dim3(512), s, a);
     if (timed) {
         double mn = (double)M * Ntot, fl = 2.0 * mn * K, by = 2.0 * ((double)M * K + (double)Ntot * K + mn);
         for (int g = 0; g < ng; g++)
@@ -2252,9 +2252,9 @@ int gemm_swiglu(int M, int K, const bf16* X, int64_t ldx, const bf16* Wgu, const
     const bool timed = kprof_begin(KP_GEMM_SWIGLU, s);
     const bool kd64 = g_big_variant != 16;
     if (kd64)
-        k_gemm_pipe_swiglu<256, 2, 4, 64><<<tiles, 512, 0, s>>>(a);
+        tlaunch(k_gemm_pipe_swiglu<256, 2, 4, 64>, dim3(tiles), dim3(512), s, a);
     else
-        k_gemm_pipe_swiglu<256, 2, 4><<<tiles, 512, 0, s>>>(a);
+        tlaunch(k_gemm_pipe_swiglu<256, 2, 4>, dim3(tiles), dim3(512), s, a);
     if (timed) {
         // X and both weights read once; gate, up and act written once
         const double mn = 2.0 * M * I;

@@ -944,19 +944,19 @@ int lora_skinny_nt(const bf16* X, int64_t ldx, int M, int K, int r, const bf16* 
     const bool dma = ((uintptr_t)X & 15) == 0 && (ldx & 7) == 0 && (K & 7) == 0 && nt <= 4;
     if (dma) {
         switch (nt) {
-            case 1: k_skinny_dma<1, 4><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
-            case 2: k_skinny_dma<2, 4><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
-            case 3: k_skinny_dma<3, 3><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
-            default: k_skinny_dma<4, 3><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
+            case 1: tlaunch(k_skinny_dma<1, 4>, dim3(grid), dim3(SK_W * 64), s, X, ldx, M, K, r, p); break;
+            case 2: tlaunch(k_skinny_dma<2, 4>, dim3(grid), dim3(SK_W * 64), s, X, ldx, M, K, r, p); break;
+            case 3: tlaunch(k_skinny_dma<3, 3>, dim3(grid), dim3(SK_W * 64), s, X, ldx, M, K, r, p); break;
+            default: tlaunch(k_skinny_dma<4, 3>, dim3(grid), dim3(SK_W * 64), s, X, ldx, M, K, r, p); break;
         }
     } else switch (nt) {
-        case 1: k_skinny_nt<1, 4><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
-        case 2: k_skinny_nt<2, 4><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
-        case 3: k_skinny_nt<3, 3><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
-        case 4: k_skinny_nt<4, 2><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
-        case 6: k_skinny_nt<6, 2><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
-        case 8: k_skinny_nt<8, 1><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
-        case 12: k_skinny_nt<12, 1><<<grid, SK_W * 64, 0, s>>>(X, ldx, M, K, r, p); break;
+        case 1: tlaunch(k_skinny_nt<1, 4>, dim3(grid), dim3(SK_W * 64), s, X, ldx, M, K, r, p); break;
+        case 2: tlaunch(k_skinny_nt<2, 4>, dim3(grid), dim3(SK_W * 64), s, X, ldx, M, K, r, p); break;
+        case 3: tlaunch(k_skinny_nt<3, 3>, dim3(grid), dim3(SK_W * 64), s, X, ldx, M, K, r, p); break;
+        case 4: tlaunch(k_skinny_nt<4, 2>, dim3(grid), dim3(SK_W * 64), s, X, ldx, M, K, r, p); break;
+        case 6: tlaunch(k_skinny_nt<6, 2>, dim3(grid), dim3(SK_W * 64), s, X, ldx, M, K, r, p); break;
+        case 8: tlaunch(k_skinny_nt<8, 1>, dim3(grid), dim3(SK_W * 64), s, X, ldx, M, K, r, p); break;
+        case 12: tlaunch(k_skinny_nt<12, 1>, dim3(grid), dim3(SK_W * 64), s, X, ldx, M, K, r, p); break;
         default: return set_error(-1, "lora_skinny_nt: %d pairs x rank %d unsupported", n, r);
     }
     if (timed)  // X and the Y_p read once, C_p written once
@@ -1022,9 +1022,9 @@ int lora_wgrad_part(const bf16* L, int64_t ldl, int NL, const bf16* Sm, int64_t 
 #define WG(N)                                                                                  \
     do {                                                                                       \
         if (vec)                                                                               \
-            k_wgrad<N, true><<<grid, 256, 0, s>>>(L, ldl, NL, Sm, lds, NS, T, per, part);      \
+            tlaunch(k_wgrad<N, true>, dim3(grid), dim3(256), s, L, ldl, NL, Sm, lds, NS, T, per, part);      \
         else                                                                                   \
-            k_wgrad<N, false><<<grid, 256, 0, s>>>(L, ldl, NL, Sm, lds, NS, T, per, part);     \
+            tlaunch(k_wgrad<N, false>, dim3(grid), dim3(256), s, L, ldl, NL, Sm, lds, NS, T, per, part);     \
     } while (0)
     switch (nst) {
         case 1: WG(1); break;
@@ -1051,7 +1051,7 @@ int lora_wgrad_reduce_jobs(const WgradJob* jobs, int njobs, int64_t total_blocks
     TA_REQUIRE(total_blocks > 0 && total_blocks < (1ll << 31), "lora_wgrad_reduce_jobs: %lld blocks",
                (long long)total_blocks);
     const bool timed = kprof_begin(KP_LORA_WGRAD, s);
-    k_wgrad_reduce_jobs<<<(unsigned)total_blocks, 256, 0, s>>>(jobs, njobs);
+    tlaunch(k_wgrad_reduce_jobs, dim3((unsigned)total_blocks), dim3(256), s, jobs, njobs);
     if (timed)  // every gradient element read and written once (F32)
         kprof_end(KP_LORA_WGRAD, s, 0.0, 8.0 * elems,
                   "ta::k_wgrad + ta::k_wgrad_reduce_jobs (all instances)");

@@ -100,11 +100,12 @@ static size_t mem_class(size_t bytes) {
 }
 
 // Kernel-level timing (measurement only).  When kernel id `sel` is
-// selected, every launch of that kernel is bracketed with a pair of events
-// recorded on the stream it is launched on, with the algorithmic flops and
-// HBM bytes of the launch; ta_kprof_read() waits for the events and sums.
+// selected, every launch of that kernel carries a pair of events in its own
+// dispatch (tlaunch), with the algorithmic flops and HBM bytes of the launch;
+// ta_kprof_read() waits for the events and sums.
 struct KProf {
     int sel = -1;
+    bool paused = false;  // selected, but launches are not timed for now
     std::vector<hipEvent_t> ev;
     std::vector<double> flops, bytes;
     size_t used = 0;
@@ -112,9 +113,14 @@ struct KProf {
 };
 static std::mutex g_kp_mu;
 static KProf g_kp;
+static thread_local KpArm t_kp_arm;
+
+KpArm& kprof_arm() { return t_kp_arm; }
 
 bool kprof_begin(int kid, hipStream_t s) {
-    if (g_kp.sel != kid) return false;
+    (void)s;
+    t_kp_arm = KpArm{};
+    if (g_kp.sel != kid || g_kp.paused) return false;
     std::lock_guard<std::mutex> lk(g_kp_mu);
     size_t i = g_kp.used;
     while (g_kp.ev.size() < 2 * (i + 1)) {
@@ -122,15 +128,18 @@ bool kprof_begin(int kid, hipStream_t s) {
         if (hipEventCreate(&e) != hipSuccess) return false;
         g_kp.ev.push_back(e);
     }
-    return hipEventRecord(g_kp.ev[2 * i], s) == hipSuccess;
+    t_kp_arm.start = g_kp.ev[2 * i];
+    t_kp_arm.stop = g_kp.ev[2 * i + 1];
+    return true;
 }
 
 void kprof_end(int kid, hipStream_t s, double flops, double bytes, const char* name) {
-    if (g_kp.sel != kid) return;
+    (void)s;
+    const bool used = t_kp_arm.used;
+    t_kp_arm = KpArm{};
+    if (g_kp.sel != kid || !used) return;
     std::lock_guard<std::mutex> lk(g_kp_mu);
     size_t i = g_kp.used;
-    if (g_kp.ev.size() < 2 * (i + 1) || hipEventRecord(g_kp.ev[2 * i + 1], s) != hipSuccess)
-        return;
     if (g_kp.flops.size() <= i) {
         g_kp.flops.resize(i + 1);
         g_kp.bytes.resize(i + 1);
@@ -150,6 +159,13 @@ int ta_kprof_select(int kid) {
     std::lock_guard<std::mutex> lk(ta::g_kp_mu);
     ta::g_kp.sel = kid;
     ta::g_kp.used = 0;
+    ta::g_kp.paused = false;
+    return 0;
+}
+
+int ta_kprof_pause(int paused) {
+    std::lock_guard<std::mutex> lk(ta::g_kp_mu);
+    ta::g_kp.paused = paused != 0;
     return 0;
 }
 

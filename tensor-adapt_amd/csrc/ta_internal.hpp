@@ -1,6 +1,8 @@
 // ta_internal.hpp — launchers shared between the backend's translation units
 // (not part of the C-ABI).
 #pragma once
+#include <hip/hip_ext.h>
+
 #include "ta_common.hpp"
 
 // s_waitcnt vmcnt(n) with the other counters left free (gfx9 encoding)
@@ -25,9 +27,35 @@ enum KernelId {
     KP_COUNT = 9
 };
 // Bracket one launch of kernel `kid` on stream s when that kernel is being
-// timed; name is the kernel's symbol as a profiler prints it.
+// timed; name is the kernel's symbol as a profiler prints it.  The launches
+// in the bracket go through tlaunch, which hands them the bracket's events.
 bool kprof_begin(int kid, hipStream_t s);
 void kprof_end(int kid, hipStream_t s, double flops, double bytes, const char* name);
+
+// The event pair armed by kprof_begin on this thread (stop null: none).
+struct KpArm {
+    hipEvent_t start = nullptr, stop = nullptr;
+    bool used = false;
+};
+KpArm& kprof_arm();
+
+// Launch kernel<<<grid, block, 0, s>>>(args...).  Inside a kprof bracket the
+// launch records the bracket's events in its own dispatch (the first launch
+// the start, every launch the stop, so the last one's end stands): no event
+// packets go between the kernels, which would idle the GPU for a few
+// microseconds each.
+template <typename... KArgs, typename... Args>
+inline void tlaunch(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t s,
+                    Args&&... args) {
+    KpArm& k = kprof_arm();
+    if (k.stop) {
+        hipExtLaunchKernelGGL(kernel, grid, block, 0, s, k.used ? nullptr : k.start, k.stop, 0,
+                              KArgs(args)...);
+        k.used = true;
+    } else {
+        kernel<<<grid, block, 0, s>>>(KArgs(args)...);
+    }
+}
 
 // sum_{z < splits} part[z * stride + idx], added in z order (deterministic);
 // the loads of 8 splits are issued together so their latencies overlap.

@@ -122,6 +122,11 @@ def kprof_select(kid):
     call("ta_kprof_select", kid)
 
 
+def kprof_pause(paused):
+    """Keep the selection and what was recorded, but time no launch while paused."""
+    call("ta_kprof_pause", 1 if paused else 0)
+
+
 def kprof_read():
     ms, n = ctypes.c_double(), ctypes.c_int64()
     fl, by = ctypes.c_double(), ctypes.c_double()
