@@ -1729,14 +1729,14 @@ int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const 
         int64_t thr = (int64_t)B * T * Hq * (hd / 8);
         int blocks = (int)((thr + 255) / 256);
         if (hd == 64)
-            k_attn_rowdot_o<64><<<blocks, 256, 0, s>>>(dO, O32, Dbuf, B, T, Hq);
+            tlaunch(k_attn_rowdot_o<64>, dim3(blocks), dim3(256), s, dO, O32, Dbuf, B, T, Hq);
         else
-            k_attn_rowdot_o<128><<<blocks, 256, 0, s>>>(dO, O32, Dbuf, B, T, Hq);
+            tlaunch(k_attn_rowdot_o<128>, dim3(blocks), dim3(256), s, dO, O32, Dbuf, B, T, Hq);
     } else {
         if (hd == 64)
-            k_attn_rowdot_p<64><<<(int)b1, 256, 0, s>>>(dO, V, P, Dbuf, T, Hq, Hkv);
+            tlaunch(k_attn_rowdot_p<64>, dim3((int)b1), dim3(256), s, dO, V, P, Dbuf, T, Hq, Hkv);
         else
-            k_attn_rowdot_p<128><<<(int)b1, 256, 0, s>>>(dO, V, P, Dbuf, T, Hq, Hkv);
+            tlaunch(k_attn_rowdot_p<128>, dim3((int)b1), dim3(256), s, dO, V, P, Dbuf, T, Hq, Hkv);
     }
     // algorithmic work (causal half): dq pass dP = dO V^T, dQ = dS K; dkv
     // pass dP again, dV = P^T dO, dK = dS^T Q.  Bytes: BF16 operands, P and
@@ -1790,13 +1790,13 @@ int attn_bwd(const bf16* dO, const bf16* Q, const bf16* K, const bf16* V, const 
     if (!rc) {
         int64_t n = (int64_t)B * T * Hkv * hd;
         int rb = (int)std::min<int64_t>((n + 255) / 256, 4096);
-        k_attn_dkv_reduce<<<rb, 256, 0, s>>>(part, dK, dV, B, T, Hq, Hkv, hd, scale);
+        tlaunch(k_attn_dkv_reduce, dim3(rb), dim3(256), s, part, dK, dV, B, T, Hq, Hkv, hd, scale);
     } else if (nsplit > 1) {
         const int64_t n4 = (int64_t)B * T * Hkv * hd / 4;
         TA_REQUIRE(!rtab || 4 * n4 < (int64_t(1) << 31), "sdpa_bwd: %lld dK elements for the fused RoPE",
                    (long long)(4 * n4));
         const int rb = (int)std::min<int64_t>((n4 + 255) / 256, 4096);
-        k_attn_dkv_sum<<<rb, 256, 0, s>>>((const float4*)part, (uint2*)dK, (uint2*)dV, n4,
+        tlaunch(k_attn_dkv_sum, dim3(rb), dim3(256), s, (const float4*)part, (uint2*)dK, (uint2*)dV, n4,
                                           nsplit, scale, rtab, T, Hkv * hd, hd);
     }
     return check_launch("sdpa_bwd");

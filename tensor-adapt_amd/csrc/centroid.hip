@@ -563,10 +563,10 @@ static int centroid_acc(const void* h, const void* g, const float* n, int64_t BT
     float* part = (float*)scratch_get((size_t)nblk * (D + 1) * sizeof(float), s);
     TA_REQUIRE(part, "centroid_accumulate: scratch allocation failed");
     if (bf16in)
-        k_centroid_part<true><<<(int)nblk, 256, 0, s>>>(h, g, nullptr, BT, D, part);
+        tlaunch(k_centroid_part<true>, dim3((int)nblk), dim3(256), s, h, g, nullptr, BT, D, part);
     else
-        k_centroid_part<false><<<(int)nblk, 256, 0, s>>>(h, g, n, BT, D, part);
-    k_centroid_reduce<<<(D + 1 + 63) / 64, 64 * kRW, 0, s>>>(part, (int)nblk, D + 1, acc, skip);
+        tlaunch(k_centroid_part<false>, dim3((int)nblk), dim3(256), s, h, g, n, BT, D, part);
+    tlaunch(k_centroid_reduce, dim3((D + 1 + 63) / 64), dim3(64 * kRW), s, part, (int)nblk, D + 1, acc, skip);
     return check_launch("centroid_accumulate");
 }
 
@@ -644,8 +644,8 @@ int ta_centroid_accumulate_bf16_noalloc(const uint16_t* h, const uint16_t* g, in
     if (rc != 0) return rc;
     // the same kernels and order as ta_centroid_accumulate_bf16: every
     // partial row is written in full before the reduce reads it
-    k_centroid_part<true><<<(int)nblk, 256, 0, s>>>(h, g, nullptr, BT, D, part);
-    k_centroid_reduce<<<(D + 1 + 63) / 64, 64 * kRW, 0, s>>>(part, (int)nblk, D + 1, acc,
+    tlaunch(k_centroid_part<true>, dim3((int)nblk), dim3(256), s, h, g, nullptr, BT, D, part);
+    tlaunch(k_centroid_reduce, dim3((D + 1 + 63) / 64), dim3(64 * kRW), s, part, (int)nblk, D + 1, acc,
                                                              nullptr);
     return check_launch("centroid_accumulate_bf16_noalloc");
 }
@@ -675,10 +675,10 @@ int ta_kmeans_ref(const float* snaps, int N, int D, int k, int max_iters, float*
     const bool vec = D % 4 == 0 && ((uintptr_t)centers & 15) == 0 &&
                      (xl || ((uintptr_t)snaps & 15) == 0);
     if (xl)
-        k_kmeans_ref<true><<<1, 1024, 0, s>>>(snaps, N, D, k, max_iters, centers, assign, dist,
+        tlaunch(k_kmeans_ref<true>, dim3(1), dim3(1024), s, snaps, N, D, k, max_iters, centers, assign, dist,
                                               iters_out, vec);
     else
-        k_kmeans_ref<false><<<1, 1024, 0, s>>>(snaps, N, D, k, max_iters, centers, assign, dist,
+        tlaunch(k_kmeans_ref<false>, dim3(1), dim3(1024), s, snaps, N, D, k, max_iters, centers, assign, dist,
                                                iters_out, vec);
     return check_launch("kmeans_ref");
 }
@@ -701,12 +701,12 @@ int ta_kmeans_pp(const float* snaps, const float* weights, int N, int D, int k, 
     const bool xl = (int64_t)N * D <= kXs && N <= 1024 && (int64_t)N * k <= kDs;
     const bool vec = D % 4 == 0 && (xl || ((uintptr_t)snaps & 15) == 0);
     if (xl)
-        k_kmeans_pp<true><<<1, 1024, 0, s>>>(snaps, weights, N, D, k, iters, seed, (float*)base,
+        tlaunch(k_kmeans_pp<true>, dim3(1), dim3(1024), s, snaps, weights, N, D, k, iters, seed, (float*)base,
                                              (float*)(base + off_d2), (float*)(base + off_dist),
                                              (int32_t*)(base + off_asg), centers, assign, mass,
                                              seeds, vec);
     else
-        k_kmeans_pp<false><<<1, 1024, 0, s>>>(snaps, weights, N, D, k, iters, seed, (float*)base,
+        tlaunch(k_kmeans_pp<false>, dim3(1), dim3(1024), s, snaps, weights, N, D, k, iters, seed, (float*)base,
                                               (float*)(base + off_d2), (float*)(base + off_dist),
                                               (int32_t*)(base + off_asg), centers, assign, mass,
                                               seeds, vec);

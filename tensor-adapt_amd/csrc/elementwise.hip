@@ -5,7 +5,7 @@
 // sized to fill the 256 CUs a few times over; a scalar tail handles N % 8.
 // Element math follows src/backend/cuda/ops.cu line for line (cited per
 // kernel); rounding to BF16 happens exactly where the reference rounds.
-#include "ta_common.hpp"
+#include "ta_internal.hpp"
 
 namespace ta {
 
@@ -193,7 +193,7 @@ int embed_fwd_checked(const bf16* table, const int32_t* tokens, bf16* out, int64
     TA_REQUIRE(BT >= 0 && D > 0 && V > 0 && bad, "embed_fwd_checked: bad arguments");
     if (BT == 0) return 0;
     bool vec = (D & 7) == 0 && aligned16(table) && aligned16(out);
-    k_embed_fwd_checked<<<(int)((BT + 3) / 4), 256, 0, s>>>(table, tokens, out, BT, D, V, vec,
+    tlaunch(k_embed_fwd_checked, dim3((int)((BT + 3) / 4)), dim3(256), s, table, tokens, out, BT, D, V, vec,
                                                             bad);
     return check_launch("embed_fwd_checked");
 }
@@ -221,9 +221,9 @@ int ta_silu_mul_fwd(const uint16_t* gate, const uint16_t* up, uint16_t* out, int
     if (N == 0) return 0;
     hipStream_t s = (hipStream_t)stream;
     if (aligned16(gate) && aligned16(up) && aligned16(out))
-        k_silu_mul_fwd<<<stream_blocks(N >> 3, 256), 256, 0, s>>>(gate, up, out, N);
+        tlaunch(k_silu_mul_fwd, dim3(stream_blocks(N >> 3, 256)), dim3(256), s, gate, up, out, N);
     else
-        k_silu_fwd_scalar<<<stream_blocks(N, 256), 256, 0, s>>>(gate, up, out, N);
+        tlaunch(k_silu_fwd_scalar, dim3(stream_blocks(N, 256)), dim3(256), s, gate, up, out, N);
     return check_launch("silu_mul_fwd");
 }
 
@@ -233,9 +233,9 @@ int ta_silu_mul_bwd(const uint16_t* dout, const uint16_t* gate, const uint16_t* 
     if (N == 0) return 0;
     hipStream_t s = (hipStream_t)stream;
     if (aligned16(dout) && aligned16(gate) && aligned16(up) && aligned16(dgate) && aligned16(dup))
-        k_silu_mul_bwd<<<stream_blocks(N >> 3, 256), 256, 0, s>>>(dout, gate, up, dgate, dup, N);
+        tlaunch(k_silu_mul_bwd, dim3(stream_blocks(N >> 3, 256)), dim3(256), s, dout, gate, up, dgate, dup, N);
     else
-        k_silu_bwd_scalar<<<stream_blocks(N, 256), 256, 0, s>>>(dout, gate, up, dgate, dup, N);
+        tlaunch(k_silu_bwd_scalar, dim3(stream_blocks(N, 256)), dim3(256), s, dout, gate, up, dgate, dup, N);
     return check_launch("silu_mul_bwd");
 }
 
@@ -245,9 +245,9 @@ static int axpy(uint16_t* out, const uint16_t* delta, float scale, int64_t N, vo
     if (N == 0) return 0;
     hipStream_t s = (hipStream_t)stream;
     if (aligned16(out) && aligned16(delta))
-        k_axpy_bf16<<<stream_blocks(N >> 3, 256), 256, 0, s>>>(out, delta, scale, N);
+        tlaunch(k_axpy_bf16, dim3(stream_blocks(N >> 3, 256)), dim3(256), s, out, delta, scale, N);
     else
-        k_axpy_bf16_scalar<<<stream_blocks(N, 256), 256, 0, s>>>(out, delta, scale, N);
+        tlaunch(k_axpy_bf16_scalar, dim3(stream_blocks(N, 256)), dim3(256), s, out, delta, scale, N);
     return check_launch(name);
 }
 
@@ -264,23 +264,23 @@ int ta_add_bias(uint16_t* out, const uint16_t* bias, int BT, int D, void* stream
     if (BT == 0) return 0;
     hipStream_t s = (hipStream_t)stream;
     if ((D & 7) == 0 && aligned16(out) && aligned16(bias))
-        k_add_bias_v8<<<stream_blocks((int64_t)BT * (D >> 3), 256), 256, 0, s>>>(out, bias, BT, D);
+        tlaunch(k_add_bias_v8, dim3(stream_blocks((int64_t)BT * (D >> 3), 256)), dim3(256), s, out, bias, BT, D);
     else
-        k_add_bias<<<stream_blocks((int64_t)BT * D, 256), 256, 0, s>>>(out, bias, BT, D);
+        tlaunch(k_add_bias, dim3(stream_blocks((int64_t)BT * D, 256)), dim3(256), s, out, bias, BT, D);
     return check_launch("add_bias");
 }
 
 int ta_cast_bf16_to_f32(const uint16_t* src, float* dst, int64_t N, void* stream) {
     TA_REQUIRE(N >= 0, "cast_bf16_to_f32: N < 0");
     if (N == 0) return 0;
-    k_bf16_to_f32<<<stream_blocks(N, 256), 256, 0, (hipStream_t)stream>>>(src, dst, N);
+    tlaunch(k_bf16_to_f32, dim3(stream_blocks(N, 256)), dim3(256), (hipStream_t)stream, src, dst, N);
     return check_launch("cast_bf16_to_f32");
 }
 
 int ta_cast_f32_to_bf16(const float* src, uint16_t* dst, int64_t N, void* stream) {
     TA_REQUIRE(N >= 0, "cast_f32_to_bf16: N < 0");
     if (N == 0) return 0;
-    k_f32_to_bf16<<<stream_blocks(N, 256), 256, 0, (hipStream_t)stream>>>(src, dst, N);
+    tlaunch(k_f32_to_bf16, dim3(stream_blocks(N, 256)), dim3(256), (hipStream_t)stream, src, dst, N);
     return check_launch("cast_f32_to_bf16");
 }
 
@@ -290,7 +290,7 @@ int ta_embed_fwd(const uint16_t* table, const int32_t* tokens, uint16_t* out, in
     if (BT == 0) return 0;
     bool vec = (D & 7) == 0 && aligned16(table) && aligned16(out);
     int blocks = (BT + 3) / 4;
-    k_embed_fwd<<<blocks, 256, 0, (hipStream_t)stream>>>(table, tokens, out, BT, D, vec);
+    tlaunch(k_embed_fwd, dim3(blocks), dim3(256), (hipStream_t)stream, table, tokens, out, BT, D, vec);
     return check_launch("embed_fwd");
 }
 
@@ -299,7 +299,7 @@ int ta_embed_bwd(const uint16_t* dout, const int32_t* tokens, float* dtable, int
     TA_REQUIRE(BT >= 0 && D > 0, "embed_bwd: bad shape BT=%d D=%d", BT, D);
     if (BT == 0) return 0;
     int blocks = (BT + 3) / 4;
-    k_embed_bwd<<<blocks, 256, 0, (hipStream_t)stream>>>(dout, tokens, dtable, BT, D);
+    tlaunch(k_embed_bwd, dim3(blocks), dim3(256), (hipStream_t)stream, dout, tokens, dtable, BT, D);
     return check_launch("embed_bwd");
 }
 

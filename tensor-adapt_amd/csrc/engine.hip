@@ -133,42 +133,46 @@ struct Engine {
 
     // kernel-class timing (ta_engine_profile)
     int prof_cat = -1;
-    std::vector<hipEvent_t> pev;
-    std::vector<std::pair<double, double>> pwork;  // (flops, bytes) per timed launch
+    std::vector<hipEvent_t> pev;  // per-launch event pairs of the timed category
+    size_t pev_used = 0, pcall0 = 0;
+    // per timed call: (flops, bytes) and its range of event pairs
+    std::vector<std::pair<std::pair<double, double>, std::pair<size_t, size_t>>> pwork;
     double p_ms = 0, p_flops = 0, p_bytes = 0;
     int64_t p_n = 0;
 };
 
-// Bracket one launch of category `cat` with events when that category is
-// being timed.  Work figures are the algorithmic flops / HBM bytes of the
-// launch, computed from its shape.
+// Time the launches of one call of category `cat` when that category is
+// being timed: each kernel launch of the call carries a start/stop event
+// pair in its own dispatch (tlaunch), so the sum is kernel time only.  Work
+// figures are the algorithmic flops / HBM bytes of the call, computed from
+// its shape.
 static void prof_begin(Engine* e, int cat) {
     if (cat != e->prof_cat) return;
-    size_t i = e->pwork.size();
-    while (e->pev.size() < 2 * (i + 1)) {
-        hipEvent_t ev;
-        if (hipEventCreate(&ev) != hipSuccess) return;
-        e->pev.push_back(ev);
-    }
-    (void)hipEventRecord(e->pev[2 * i], e->s);
+    KpArm& k = kprof_arm();
+    k.pool = &e->pev;
+    k.npairs = &e->pev_used;
+    e->pcall0 = e->pev_used;
 }
 static void prof_end(Engine* e, int cat, double flops, double bytes) {
     if (cat != e->prof_cat) return;
-    size_t i = e->pwork.size();
-    if (e->pev.size() < 2 * (i + 1)) return;
-    (void)hipEventRecord(e->pev[2 * i + 1], e->s);
-    e->pwork.push_back({flops, bytes});
+    KpArm& k = kprof_arm();
+    k.pool = nullptr;
+    k.npairs = nullptr;
+    e->pwork.push_back({{flops, bytes}, {e->pcall0, e->pev_used}});
 }
 static int prof_collect(Engine* e) {
-    for (size_t i = 0; i < e->pwork.size(); i++) {
-        float ms = 0.f;
-        TA_HIP(hipEventElapsedTime(&ms, e->pev[2 * i], e->pev[2 * i + 1]));
-        e->p_ms += ms;
+    for (const auto& w : e->pwork) {
+        for (size_t i = w.second.first; i < w.second.second; i++) {
+            float ms = 0.f;
+            TA_HIP(hipEventElapsedTime(&ms, e->pev[2 * i], e->pev[2 * i + 1]));
+            e->p_ms += ms;
+        }
         e->p_n++;
-        e->p_flops += e->pwork[i].first;
-        e->p_bytes += e->pwork[i].second;
+        e->p_flops += w.first.first;
+        e->p_bytes += w.first.second;
     }
     e->pwork.clear();
+    e->pev_used = 0;
     return 0;
 }
 #define TIMED(cat, flops, bytes, call)             \

@@ -1564,13 +1564,13 @@ static void launch_cfg(bool xk, bool yk, const GemmArgs& a, int splits, bool vx,
                        hipStream_t s) {
     dim3 grid(a.tiles_m * a.tiles_n, 1, splits);
     if (xk && yk)
-        k_gemm<BM, BN, WM, WN, true, true, EPI><<<grid, 256, 0, s>>>(a, vx, vy);
+        tlaunch(k_gemm<BM, BN, WM, WN, true, true, EPI>, dim3(grid), dim3(256), s, a, vx, vy);
     else if (xk && !yk)
-        k_gemm<BM, BN, WM, WN, true, false, EPI><<<grid, 256, 0, s>>>(a, vx, vy);
+        tlaunch(k_gemm<BM, BN, WM, WN, true, false, EPI>, dim3(grid), dim3(256), s, a, vx, vy);
     else if (!xk && yk)
-        k_gemm<BM, BN, WM, WN, false, true, EPI><<<grid, 256, 0, s>>>(a, vx, vy);
+        tlaunch(k_gemm<BM, BN, WM, WN, false, true, EPI>, dim3(grid), dim3(256), s, a, vx, vy);
     else
-        k_gemm<BM, BN, WM, WN, false, false, EPI><<<grid, 256, 0, s>>>(a, vx, vy);
+        tlaunch(k_gemm<BM, BN, WM, WN, false, false, EPI>, dim3(grid), dim3(256), s, a, vx, vy);
 }
 
 static inline bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -1777,7 +1777,7 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
             if (!a.part) return set_error(-2, "gemm: scratch allocation of %zu bytes failed", bytes);
             launch_big<EPI_PARTIAL>(variant, grid, a, s);
             int64_t MN = (int64_t)M * N;
-            k_splitk_reduce<true><<<(int)((MN + 255) / 256), 256, 0, s>>>(a.part, splits, M, N, C,
+            tlaunch(k_splitk_reduce<true>, dim3((int)((MN + 255) / 256)), dim3(256), s, a.part, splits, M, N, C,
                                                                           ldc, alpha, beta, bias);
             int rc = check_launch("gemm");
             return rc ? rc : lora_after();
@@ -1893,10 +1893,10 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
         int64_t MN = (int64_t)M * N;
         int blocks = (int)((MN + 255) / 256);
         if (out_f32)
-            k_splitk_reduce<false><<<blocks, 256, 0, s>>>(a.part, splits, M, N, C, ldc, alpha,
+            tlaunch(k_splitk_reduce<false>, dim3(blocks), dim3(256), s, a.part, splits, M, N, C, ldc, alpha,
                                                           beta, bias);
         else
-            k_splitk_reduce<true><<<blocks, 256, 0, s>>>(a.part, splits, M, N, C, ldc, alpha,
+            tlaunch(k_splitk_reduce<true>, dim3(blocks), dim3(256), s, a.part, splits, M, N, C, ldc, alpha,
                                                          beta, bias);
     }
     int rc = check_launch("gemm");
@@ -2332,9 +2332,9 @@ int gemm_ce_dx(int M, int N, int K, const bf16* logits, const bf16* Wt, bf16* C,
     a.tiles_n = (N + BNb - 1) / BNb;
     dim3 grid(a.tiles_m * a.tiles_n);
     if (BNb == 192)
-        k_gemm_pipe_ce<192, 4, 2><<<grid, 512, 0, s>>>(a);
+        tlaunch(k_gemm_pipe_ce<192, 4, 2>, dim3(grid), dim3(512), s, a);
     else
-        k_gemm_pipe_ce<256, 2, 4><<<grid, 512, 0, s>>>(a);
+        tlaunch(k_gemm_pipe_ce<256, 2, 4>, dim3(grid), dim3(512), s, a);
     return check_launch("gemm_ce_dx");
 }
 
@@ -2410,10 +2410,8 @@ int ta_gemm_f32(int transA, int transB, int M, int N, int K, float alpha, const 
         const int kc = (int)std::min<int64_t>(kcap, K - k0);
         const int kp = (kc + 31) & ~31;
         const int64_t nx = (int64_t)N * kp, ny = (int64_t)M * kp;
-        k_split3<<<(int)std::min<int64_t>((nx + 255) / 256, 4096), 256, 0, s>>>(
-            B, ldb, transB == 0, N, k0, kc, kp, code_x, x16);
-        k_split3<<<(int)std::min<int64_t>((ny + 255) / 256, 4096), 256, 0, s>>>(
-            A, lda, transA != 0, M, k0, kc, kp, code_y, y16);
+        tlaunch(k_split3, dim3((int)std::min<int64_t>((nx + 255) / 256, 4096)), dim3(256), s, B, ldb, transB == 0, N, k0, kc, kp, code_x, x16);
+        tlaunch(k_split3, dim3((int)std::min<int64_t>((ny + 255) / 256, 4096)), dim3(256), s, A, lda, transA != 0, M, k0, kc, kp, code_y, y16);
         const int rc = gemm_dispatch(true, true, N, M, 6 * kp, alpha, x16, 6 * kp, y16, 6 * kp,
                                      k0 == 0 ? beta : 1.f, C, ldc, nullptr, true, s, 0, nullptr);
         if (rc != 0) return rc;

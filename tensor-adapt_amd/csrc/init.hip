@@ -3,7 +3,7 @@
 // the LoRA A initialisation, and the out-of-place residual add.
 #include <string.h>
 
-#include "ta_common.hpp"
+#include "ta_internal.hpp"
 
 namespace ta {
 
@@ -26,7 +26,7 @@ int transpose_bf16(const bf16* in, bf16* out, int64_t rows, int64_t cols, hipStr
     TA_REQUIRE((cols + 63) / 64 < (1ll << 31) && (rows + 63) / 64 < 65536,
                "transpose: matrix too large (%lld x %lld)", (long long)rows, (long long)cols);
     dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
-    k_transpose<<<grid, 256, 0, s>>>(in, out, rows, cols);
+    tlaunch(k_transpose, dim3(grid), dim3(256), s, in, out, rows, cols);
     return check_launch("transpose");
 }
 
@@ -54,7 +54,7 @@ __global__ void k_fill_normal(bf16* __restrict__ out, int64_t n, uint64_t seed, 
 int fill_normal_bf16(bf16* out, int64_t n, uint64_t seed, uint64_t sid, float std,
                      hipStream_t s) {
     if (n <= 0) return 0;
-    k_fill_normal<<<2048, 256, 0, s>>>(out, n, seed, sid, std);
+    tlaunch(k_fill_normal, dim3(2048), dim3(256), s, out, n, seed, sid, std);
     return check_launch("fill_normal");
 }
 
@@ -68,7 +68,7 @@ int fill_bf16(bf16* out, int64_t n, float v, hipStream_t s) {
     uint32_t u;
     memcpy(&u, &v, 4);  // host-side RNE to BF16 (finite v)
     bf16 h = (bf16)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
-    k_fill_bf16<<<1024, 256, 0, s>>>(out, n, h);
+    tlaunch(k_fill_bf16, dim3(1024), dim3(256), s, out, n, h);
     return check_launch("fill_bf16");
 }
 
@@ -92,7 +92,7 @@ __global__ void k_kaiming(float* __restrict__ a32, bf16* __restrict__ a16, int64
 }
 int kaiming_init(float* a32, bf16* a16, int64_t n, int in_dim, hipStream_t s) {
     if (n <= 0) return 0;
-    k_kaiming<<<256, 256, 0, s>>>(a32, a16, n, in_dim, 0x1234u);
+    tlaunch(k_kaiming, dim3(256), dim3(256), s, a32, a16, n, in_dim, 0x1234u);
     return check_launch("kaiming_init");
 }
 
@@ -122,7 +122,7 @@ int add2_bf16(bf16* out, const bf16* a, const bf16* b, int64_t n, hipStream_t s)
     int64_t blocks = ((n >> 3) + 255) / 256;
     if (blocks > 8192) blocks = 8192;
     if (blocks < 1) blocks = 1;
-    k_add2<<<(int)blocks, 256, 0, s>>>(out, a, b, n);
+    tlaunch(k_add2, dim3((int)blocks), dim3(256), s, out, a, b, n);
     return check_launch("add2");
 }
 
@@ -171,7 +171,7 @@ __global__ __launch_bounds__(1024) void k_mask_targets(const int32_t* __restrict
 int mask_targets_dev(const int32_t* in, const int32_t* tgt_in, int32_t* tgt, int B, int T,
                      hipStream_t s) {
     if (B <= 0 || T <= 0) return 0;
-    k_mask_targets<<<B, 1024, 0, s>>>(in, tgt_in, tgt, B, T);
+    tlaunch(k_mask_targets, dim3(B), dim3(1024), s, in, tgt_in, tgt, B, T);
     return check_launch("mask_targets");
 }
 

@@ -981,7 +981,7 @@ int lora_rank_update(bool delta, bf16* Y, int64_t ldy, int M, int N, int r, floa
     }
     dim3 grid((N + 63) / 64, (M + 63) / 64);
     int rk = (r + 31) / 32 * 32;
-#define RU(D, R) k_rank_update<D, R><<<grid, 256, 0, s>>>(Y, ldy, M, N, r, scale, p)
+#define RU(D, R) tlaunch(k_rank_update<D, R>, dim3(grid), dim3(256), s, Y, ldy, M, N, r, scale, p)
     if (delta) {
         if (rk == 32) RU(true, 32); else RU(true, 64);
     } else {
@@ -1100,12 +1100,10 @@ int silu_bwd_lora(const bf16* dact, const bf16* gate, const bf16* up, bf16* dgat
     if (int rc = silu_lora_plan(BT, I, &s_t, &s_o, &per)) return rc;
     const dim3 grid(s_o, s_t);
     if (ga_d)
-        k_silu_bwd_lora<SL_NW, true><<<grid, SL_NW * 64, 0, s>>>(
-            dact, gate, up, dgate, dup, bt_g, bt_u, h_g, h_u, dh_part, gb_g, gb_u, dh_d, ga_d, BT, I,
+        tlaunch(k_silu_bwd_lora<SL_NW, true>, dim3(grid), dim3(SL_NW * 64), s, dact, gate, up, dgate, dup, bt_g, bt_u, h_g, h_u, dh_part, gb_g, gb_u, dh_d, ga_d, BT, I,
             per);
     else
-        k_silu_bwd_lora<SL_NW, false><<<grid, SL_NW * 64, 0, s>>>(
-            dact, gate, up, dgate, dup, bt_g, bt_u, h_g, h_u, dh_part, gb_g, gb_u, dh_d, ga_d, BT, I,
+        tlaunch(k_silu_bwd_lora<SL_NW, false>, dim3(grid), dim3(SL_NW * 64), s, dact, gate, up, dgate, dup, bt_g, bt_u, h_g, h_u, dh_part, gb_g, gb_u, dh_d, ga_d, BT, I,
             per);
     return check_launch("silu_bwd_lora");
 }
@@ -1113,7 +1111,7 @@ int silu_bwd_lora(const bf16* dact, const bf16* gate, const bf16* up, bf16* dgat
 int dh_reduce2(const float* dh_part, int s_o, int BT, bf16* dh, int64_t ldh, hipStream_t s) {
     TA_REQUIRE(dh_part && dh && s_o > 0 && BT > 0 && ldh >= 32, "dh_reduce2: bad arguments");
     const int64_t n = (int64_t)BT * 32;
-    k_dh_reduce2<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(dh_part, s_o, BT, dh, ldh);
+    tlaunch(k_dh_reduce2, dim3((unsigned)((n + 255) / 256)), dim3(256), s, dh_part, s_o, BT, dh, ldh);
     return check_launch("dh_reduce2");
 }
 
@@ -1168,9 +1166,9 @@ int go_lora(const bf16* const* go, const int64_t* ldgo, const bf16* const* bt, c
     P.ntot = c;
     int s_t = 0, s_o = 0, per = 0;
     if (int rc = go_lora_plan(BT, c, &s_t, &s_o, &per)) return rc;
-    k_go_lora<GL_NW><<<dim3(s_o, s_t), GL_NW * 64, 0, s>>>(P, dh_part, BT, per);
+    tlaunch(k_go_lora<GL_NW>, dim3(dim3(s_o, s_t)), dim3(GL_NW * 64), s, P, dh_part, BT, per);
     const int64_t nel = (int64_t)BT * 16 * np;
-    k_dh_reduce_go<<<(unsigned)((nel + 255) / 256), 256, 0, s>>>(dh_part, P, GL_NW * 64, BT, dh,
+    tlaunch(k_dh_reduce_go, dim3((unsigned)((nel + 255) / 256)), dim3(256), s, dh_part, P, GL_NW * 64, BT, dh,
                                                                   ldh);
     return check_launch("go_lora");
 }

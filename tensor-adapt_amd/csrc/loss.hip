@@ -10,7 +10,7 @@
 // serves rows too long for registers and unaligned or ragged V.
 #include <float.h>
 
-#include "ta_common.hpp"
+#include "ta_internal.hpp"
 
 namespace ta {
 
@@ -244,7 +244,7 @@ int cross_entropy(const bf16* logits, const int32_t* targets, float* loss_out, b
     // (up to 20 chunks per lane fit the 128 registers of a 16-wave block)
     if (vec && cpt <= 20) {
 #define CE(C, K)                                                                      \
-    k_cross_entropy_reg<C, K><<<N, 1024, 0, s>>>(logits, targets, loss_out, dlogits, V, inv_N, \
+    tlaunch(k_cross_entropy_reg<C, K>, dim3(N), dim3(1024), s, logits, targets, loss_out, dlogits, V, inv_N, \
                                                  nonfinite, lse2_out)
 #define CE2(C) \
     if (nonfinite) CE(C, true); else CE(C, false)
@@ -255,10 +255,10 @@ int cross_entropy(const bf16* logits, const int32_t* targets, float* loss_out, b
 #undef CE2
 #undef CE
     } else if (vec) {
-        k_cross_entropy<true><<<N, 512, 0, s>>>(logits, targets, loss_out, dlogits, V, inv_N,
+        tlaunch(k_cross_entropy<true>, dim3(N), dim3(512), s, logits, targets, loss_out, dlogits, V, inv_N,
                                                 nonfinite);
     } else {
-        k_cross_entropy<false><<<N, 512, 0, s>>>(logits, targets, loss_out, dlogits, V, inv_N,
+        tlaunch(k_cross_entropy<false>, dim3(N), dim3(512), s, logits, targets, loss_out, dlogits, V, inv_N,
                                                  nonfinite);
     }
     return check_launch("cross_entropy_fwd");

@@ -324,7 +324,7 @@ const float2* rope_table(int T, int hd, float theta, float sign, hipStream_t s) 
     float2* tab = nullptr;
     int64_t n = (int64_t)T * (hd >> 1);
     if (hipMalloc((void**)&tab, n * sizeof(float2)) != hipSuccess) return nullptr;
-    k_rope_table<<<(int)((n + 255) / 256), 256, 0, s>>>(tab, T, hd, theta, sign);
+    tlaunch(k_rope_table, dim3((int)((n + 255) / 256)), dim3(256), s, tab, T, hd, theta, sign);
     g_rope_tabs.push_back({dev, T, hd, theta, sign, tab});
     return tab;
 }
@@ -366,7 +366,7 @@ int rms_fwd_res(const bf16* a, const bf16* b, bf16* xs, const bf16* w, bf16* out
         if (int rc = add2_bf16(xs, a, b, rows * D, s)) return rc;
         return ta_rms_norm_fwd(xs, w, out, rms_out, 1, (int)rows, D, eps, s);
     }
-    k_rms_fwd_v8<kMaxChunks, true><<<(int)((rows + 3) / 4), 256, 0, s>>>(a, w, out, rms_out, rows,
+    tlaunch(k_rms_fwd_v8<kMaxChunks, true>, dim3((int)((rows + 3) / 4)), dim3(256), s, a, w, out, rms_out, rows,
                                                                        D, eps, b, xs);
     return check_launch("rms_fwd_res");
 }
@@ -381,8 +381,7 @@ int rms_bwd_acc(const bf16* dy, const bf16* x, const bf16* w, const float* rms, 
             return rc;
         return ta_add_inplace(acc, tmp, rows * D, s);
     }
-    k_rms_bwd_v8<kMaxChunks, false, true><<<(int)((rows + 3) / 4), 256, 0, s>>>(
-        dy, x, w, rms, acc, nullptr, rows, D, 4);
+    tlaunch(k_rms_bwd_v8<kMaxChunks, false, true>, dim3((int)((rows + 3) / 4)), dim3(256), s, dy, x, w, rms, acc, nullptr, rows, D, 4);
     return check_launch("rms_bwd_acc");
 }
 }  // namespace ta
@@ -397,9 +396,10 @@ int ta_rms_norm_fwd(const uint16_t* x, const uint16_t* w, uint16_t* out, float* 
     hipStream_t s = (hipStream_t)stream;
     int blocks = (int)((rows + 3) / 4);
     if ((D & 7) == 0 && D <= 64 * 8 * kMaxChunks && al16(x) && al16(w) && al16(out))
-        k_rms_fwd_v8<kMaxChunks><<<blocks, 256, 0, s>>>(x, w, out, rms_out, rows, D, eps);
+        tlaunch(k_rms_fwd_v8<kMaxChunks>, dim3(blocks), dim3(256), s, x, w, out, rms_out, rows, D, eps,
+                nullptr, nullptr);
     else
-        k_rms_fwd_scalar<<<blocks, 256, 0, s>>>(x, w, out, rms_out, rows, D, eps);
+        tlaunch(k_rms_fwd_scalar, dim3(blocks), dim3(256), s, x, w, out, rms_out, rows, D, eps);
     return check_launch("rms_norm_fwd");
 }
 
@@ -417,14 +417,12 @@ int ta_rms_norm_bwd(const uint16_t* dy, const uint16_t* x, const uint16_t* w,
         int rpb = dw ? 64 : 4;  // with dw: fewer, fuller blocks keep the partials small
         int blocks = (int)((rows + rpb - 1) / rpb);
         if (!dw) {
-            k_rms_bwd_v8<kMaxChunks, false>
-                <<<blocks, 256, 0, s>>>(dy, x, w, rms_saved, dx, nullptr, rows, D, rpb);
+            tlaunch(k_rms_bwd_v8<kMaxChunks, false>, dim3(blocks), dim3(256), s, dy, x, w, rms_saved, dx, nullptr, rows, D, rpb);
         } else {
             float* part = (float*)scratch_get((size_t)blocks * D * sizeof(float), s);
             TA_REQUIRE(part, "rms_norm_bwd: scratch allocation failed");
-            k_rms_bwd_v8<kMaxChunks, true>
-                <<<blocks, 256, 0, s>>>(dy, x, w, rms_saved, dx, part, rows, D, rpb);
-            k_sum_partials<<<(D + 255) / 256, 256, 0, s>>>(part, dw, blocks, D);
+            tlaunch(k_rms_bwd_v8<kMaxChunks, true>, dim3(blocks), dim3(256), s, dy, x, w, rms_saved, dx, part, rows, D, rpb);
+            tlaunch(k_sum_partials, dim3((D + 255) / 256), dim3(256), s, part, dw, blocks, D);
         }
     } else {
         float* part = nullptr;
@@ -432,8 +430,8 @@ int ta_rms_norm_bwd(const uint16_t* dy, const uint16_t* x, const uint16_t* w,
             part = (float*)scratch_get((size_t)rows * D * sizeof(float), s);
             TA_REQUIRE(part, "rms_norm_bwd: scratch allocation failed");
         }
-        k_rms_bwd_scalar<<<(int)rows, 256, 0, s>>>(dy, x, w, rms_saved, dx, part, rows, D);
-        if (dw) k_sum_partials<<<(D + 255) / 256, 256, 0, s>>>(part, dw, (int)rows, D);
+        tlaunch(k_rms_bwd_scalar, dim3((int)rows), dim3(256), s, dy, x, w, rms_saved, dx, part, rows, D);
+        if (dw) tlaunch(k_sum_partials, dim3((D + 255) / 256), dim3(256), s, part, dw, (int)rows, D);
     }
     return check_launch("rms_norm_bwd");
 }
@@ -449,10 +447,10 @@ static int rope(uint16_t* x, int B, int T, int H, int hd, float theta, float sig
         const float2* tab = rope_table(T, hd, theta, sign, s);
         TA_REQUIRE(tab, "rope: table allocation failed");
         int64_t n = rows * H * (hd >> 3);
-        k_rope_tab<<<(int)((n + 255) / 256), 256, 0, s>>>(x, rows, T, H, hd, (const float4*)tab);
+        tlaunch(k_rope_tab, dim3((int)((n + 255) / 256)), dim3(256), s, x, rows, T, H, hd, (const float4*)tab);
     } else {
         int64_t n = rows * (hd >> 1);
-        k_rope_scalar<<<(int)((n + 255) / 256), 256, 0, s>>>(x, rows, T, H, hd, theta, sign);
+        tlaunch(k_rope_scalar, dim3((int)((n + 255) / 256)), dim3(256), s, x, rows, T, H, hd, theta, sign);
     }
     return check_launch("rope");
 }
@@ -473,7 +471,7 @@ int rope_qk(bf16* q, int Hq, bf16* k, int Hk, int B, int T, int hd, float theta,
     const float2* tab = rope_table(T, hd, theta, sign, s);
     TA_REQUIRE(tab, "rope: table allocation failed");
     const int64_t n0 = rows * Hq * (hd >> 3), n = n0 + rows * Hk * (hd >> 3);
-    k_rope_tab2<<<(int)((n + 255) / 256), 256, 0, s>>>(q, Hq, k, Hk, rows, T, hd, n0,
+    tlaunch(k_rope_tab2, dim3((int)((n + 255) / 256)), dim3(256), s, q, Hq, k, Hk, rows, T, hd, n0,
                                                        (const float4*)tab);
     return check_launch("rope_qk");
 }

@@ -209,7 +209,7 @@ int ta_adamw_step(float* master, uint16_t* working, float* m, float* v, const fl
     if (N == 0) return 0;
     float bc1 = 1.f - powf(beta1, (float)step);
     float bc2 = 1.f - powf(beta2, (float)step);
-    k_adamw<<<adam_blocks(N), 256, 0, (hipStream_t)stream>>>(master, working, m, v,
+    tlaunch(k_adamw, dim3(adam_blocks(N)), dim3(256), (hipStream_t)stream, master, working, m, v,
                                                              const_cast<float*>(grad), N, lr,
                                                              beta1, beta2, eps, weight_decay,
                                                              bc1, bc2, nullptr, 0, 0.f, nullptr,
@@ -223,8 +223,8 @@ int ta_sum_sq_into(const float* g, float* accum, int64_t N, void* stream) {
     hipStream_t s = (hipStream_t)stream;
     float* part = (float*)scratch_get(kNormBlocks * sizeof(float), s);
     TA_REQUIRE(part, "sum_sq_into: scratch allocation failed");
-    k_sumsq_partials<<<kNormBlocks, 256, 0, s>>>(g, N, part);
-    k_accum_sumsq<<<1, 256, 0, s>>>(part, kNormBlocks, accum);
+    tlaunch(k_sumsq_partials, dim3(kNormBlocks), dim3(256), s, g, N, part);
+    tlaunch(k_accum_sumsq, dim3(1), dim3(256), s, part, kNormBlocks, accum);
     return check_launch("sum_sq_into");
 }
 
@@ -249,8 +249,8 @@ int adamw_fused_impl(float* master, bf16* working, float* m, float* v, float* gr
     TA_REQUIRE(part, "adamw_fused: scratch allocation failed");
     float bc1 = 1.f - powf(beta1, (float)step);
     float bc2 = 1.f - powf(beta2, (float)step);
-    k_sumsq_partials<<<kNormBlocks, 256, 0, s>>>(grad, N, part);
-    k_adamw<<<adam_blocks(N), 256, 0, s>>>(master, working, m, v, grad, N, lr, beta1, beta2,
+    tlaunch(k_sumsq_partials, dim3(kNormBlocks), dim3(256), s, grad, N, part);
+    tlaunch(k_adamw, dim3(adam_blocks(N)), dim3(256), s, master, working, m, v, grad, N, lr, beta1, beta2,
                                            eps, weight_decay, bc1, bc2, part, kNormBlocks,
                                            max_norm, norm_out, skip);
     return check_launch("adamw_fused");
@@ -268,7 +268,7 @@ int adamw_tiles_impl(float* master, bf16* working, bf16* workingT, float* m, flo
     TA_REQUIRE(ntens > 0 && (!update || step >= 1), "adamw_tiles: bad arguments");
     const int blocks = (int)std::min<int64_t>(ntiles, 2048);
     if (!update) {
-        k_adamw_tiles<<<blocks, 256, 0, s>>>(master, working, workingT, m, v, grad, tens, ntens,
+        tlaunch(k_adamw_tiles, dim3(blocks), dim3(256), s, master, working, workingT, m, v, grad, tens, ntens,
                                              ntiles, false, 0.f, 0.f, 0.f, 0.f, 0.f, 1.f, 1.f,
                                              nullptr, 0, 0.f, nullptr, nullptr);
         return check_launch("adamw_tiles");
@@ -277,8 +277,8 @@ int adamw_tiles_impl(float* master, bf16* working, bf16* workingT, float* m, flo
     TA_REQUIRE(part, "adamw_tiles: scratch allocation failed");
     float bc1 = 1.f - powf(beta1, (float)step);
     float bc2 = 1.f - powf(beta2, (float)step);
-    k_sumsq_partials<<<kNormBlocks, 256, 0, s>>>(grad, N, part);
-    k_adamw_tiles<<<blocks, 256, 0, s>>>(master, working, workingT, m, v, grad, tens, ntens, ntiles,
+    tlaunch(k_sumsq_partials, dim3(kNormBlocks), dim3(256), s, grad, N, part);
+    tlaunch(k_adamw_tiles, dim3(blocks), dim3(256), s, master, working, workingT, m, v, grad, tens, ntens, ntiles,
                                          true, lr, beta1, beta2, eps, weight_decay, bc1, bc2, part,
                                          kNormBlocks, max_norm, norm_out, skip);
     return check_launch("adamw_tiles");

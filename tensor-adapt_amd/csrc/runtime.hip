@@ -117,9 +117,25 @@ static thread_local KpArm t_kp_arm;
 
 KpArm& kprof_arm() { return t_kp_arm; }
 
+bool kprof_pool_pair(hipEvent_t* start, hipEvent_t* stop) {
+    KpArm& k = t_kp_arm;
+    if (!k.pool || !k.npairs) return false;
+    const size_t i = *k.npairs;
+    while (k.pool->size() < 2 * (i + 1)) {
+        hipEvent_t e;
+        if (hipEventCreate(&e) != hipSuccess) return false;
+        k.pool->push_back(e);
+    }
+    *start = (*k.pool)[2 * i];
+    *stop = (*k.pool)[2 * i + 1];
+    *k.npairs = i + 1;
+    return true;
+}
+
 bool kprof_begin(int kid, hipStream_t s) {
     (void)s;
-    t_kp_arm = KpArm{};
+    t_kp_arm.start = t_kp_arm.stop = nullptr;
+    t_kp_arm.used = false;
     if (g_kp.sel != kid || g_kp.paused) return false;
     std::lock_guard<std::mutex> lk(g_kp_mu);
     size_t i = g_kp.used;
@@ -136,7 +152,8 @@ bool kprof_begin(int kid, hipStream_t s) {
 void kprof_end(int kid, hipStream_t s, double flops, double bytes, const char* name) {
     (void)s;
     const bool used = t_kp_arm.used;
-    t_kp_arm = KpArm{};
+    t_kp_arm.start = t_kp_arm.stop = nullptr;
+    t_kp_arm.used = false;
     if (g_kp.sel != kid || !used) return;
     std::lock_guard<std::mutex> lk(g_kp_mu);
     size_t i = g_kp.used;

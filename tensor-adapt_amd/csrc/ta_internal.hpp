@@ -3,6 +3,8 @@
 #pragma once
 #include <hip/hip_ext.h>
 
+#include <vector>
+
 #include "ta_common.hpp"
 
 // s_waitcnt vmcnt(n) with the other counters left free (gfx9 encoding)
@@ -32,29 +34,43 @@ enum KernelId {
 bool kprof_begin(int kid, hipStream_t s);
 void kprof_end(int kid, hipStream_t s, double flops, double bytes, const char* name);
 
-// The event pair armed by kprof_begin on this thread (stop null: none).
+// Launch timing armed on this thread.  kprof: the event pair of the
+// current kprof bracket (stop null: none).  pool: per-launch pairs for the
+// engine's class profiling (each launch takes the next pair of *pool,
+// counted in *npairs; null: off).  A launch carries at most one pair: a
+// kprof bracket wins over the pool.
 struct KpArm {
     hipEvent_t start = nullptr, stop = nullptr;
     bool used = false;
+    std::vector<hipEvent_t>* pool = nullptr;
+    size_t* npairs = nullptr;
 };
 KpArm& kprof_arm();
+// the next pair of the armed pool (created as needed); false: none
+bool kprof_pool_pair(hipEvent_t* start, hipEvent_t* stop);
 
-// Launch kernel<<<grid, block, 0, s>>>(args...).  Inside a kprof bracket the
-// launch records the bracket's events in its own dispatch (the first launch
-// the start, every launch the stop, so the last one's end stands): no event
-// packets go between the kernels, which would idle the GPU for a few
-// microseconds each.
+// Launch kernel<<<grid, block, 0, s>>>(args...).  When timing is armed the
+// launch records the events in its own dispatch: inside a kprof bracket the
+// first launch the bracket's start, every launch its stop (so the last
+// one's end stands); under the class profiling a start/stop pair of its
+// own.  No event packets go between the kernels (they would add idle GPU
+// time to what is measured).
 template <typename... KArgs, typename... Args>
 inline void tlaunch(void (*kernel)(KArgs...), dim3 grid, dim3 block, hipStream_t s,
                     Args&&... args) {
     KpArm& k = kprof_arm();
+    hipEvent_t a = nullptr, b = nullptr;
     if (k.stop) {
-        hipExtLaunchKernelGGL(kernel, grid, block, 0, s, k.used ? nullptr : k.start, k.stop, 0,
-                              KArgs(args)...);
+        a = k.used ? nullptr : k.start;
+        b = k.stop;
         k.used = true;
-    } else {
-        kernel<<<grid, block, 0, s>>>(KArgs(args)...);
+    } else if (k.pool) {
+        (void)kprof_pool_pair(&a, &b);
     }
+    if (b)
+        hipExtLaunchKernelGGL(kernel, grid, block, 0, s, a, b, 0, static_cast<KArgs>(args)...);
+    else
+        kernel<<<grid, block, 0, s>>>(static_cast<KArgs>(args)...);
 }
 
 // sum_{z < splits} part[z * stride + idx], added in z order (deterministic);
