@@ -177,8 +177,9 @@ __global__ __launch_bounds__(SK_W * 64) void k_skinny_nt(const bf16* __restrict_
 // of 8, n * r <= 64) with direct-to-LDS loads: K runs in stages of 256; one
 // global_load_lds_dwordx4 moves 2 rows x 512 contiguous bytes (whole cache
 // lines, where k_skinny_nt's fragment-shaped loads take 64 bytes of each of
-// 16 rows), NS stage buffers (4 for one or two 16-column tiles, 3 for
-// three or four).  Block: 32 rows of X, 8 waves; in each
+// 16 rows), NS stage buffers (6 for one 16-column tile, 4 for two, 3 for
+// three or four: as many as the LDS holds, since the kernel streams X with
+// little compute per byte and is bound by the bytes it has in flight).  Block: 32 rows of X, 8 waves; in each
 // stage wave w computes k chunk w (32 wide) for both 16-row groups and
 // every 16-column tile of the concatenated Y.  16-byte unit u of row R sits
 // in slot u ^ (R % 16), so the fragment reads of 16 consecutive rows hit
@@ -232,8 +233,11 @@ __global__ __launch_bounds__(512) void k_skinny_dma(const bf16* __restrict__ X, 
     constexpr int XE = 32 * SKD_K, YE = 16 * NT * SKD_K;  // elements per stage
     constexpr int XI = 16, YI = 8 * NT;                   // DMA instructions per stage
     constexpr int LPS = (XI + 7) / 8 + (YI + 7) / 8;      // ... per wave
-    __shared__ __attribute__((aligned(1024))) bf16 sX0[XE], sX1[XE], sX2[XE], sX3[NS == 4 ? XE : 8];
-    __shared__ __attribute__((aligned(1024))) bf16 sY0[YE], sY1[YE], sY2[YE], sY3[NS == 4 ? YE : 8];
+    static_assert(NS == 3 || NS == 4 || NS == 6, "3, 4 or 6 stages");
+    __shared__ __attribute__((aligned(1024))) bf16 sX0[XE], sX1[XE], sX2[XE], sX3[NS >= 4 ? XE : 8],
+        sX4[NS == 6 ? XE : 8], sX5[NS == 6 ? XE : 8];
+    __shared__ __attribute__((aligned(1024))) bf16 sY0[YE], sY1[YE], sY2[YE], sY3[NS >= 4 ? YE : 8],
+        sY4[NS == 6 ? YE : 8], sY5[NS == 6 ? YE : 8];
     // the partial sums' exchange; with four 16-column tiles it reuses stage
     // buffer sY0 (32 KB), which keeps the block within the LDS
     static_assert(NT < 4 || sizeof(floatx4) * SK_W / 2 * SK_RG * NT * 64 <= sizeof(bf16) * YE,
@@ -272,9 +276,20 @@ __global__ __launch_bounds__(512) void k_skinny_dma(const bf16* __restrict__ X, 
     } while (0)
     SKD_ISSUE(sX0, sY0, 0 - pad);
     SKD_ISSUE(sX1, sY1, 1 - pad);
-    if constexpr (NS == 4) SKD_ISSUE(sX2, sY2, 2 - pad);
+    if constexpr (NS >= 4) SKD_ISSUE(sX2, sY2, 2 - pad);
+    if constexpr (NS == 6) {
+        SKD_ISSUE(sX3, sY3, 3 - pad);
+        SKD_ISSUE(sX4, sY4, 4 - pad);
+    }
     for (int ks0 = -pad; ks0 < nst; ks0 += NS) {
-        if constexpr (NS == 4) {
+        if constexpr (NS == 6) {
+            SKD_STEP(0, sX0, sY0, sX5, sY5);
+            SKD_STEP(1, sX1, sY1, sX0, sY0);
+            SKD_STEP(2, sX2, sY2, sX1, sY1);
+            SKD_STEP(3, sX3, sY3, sX2, sY2);
+            SKD_STEP(4, sX4, sY4, sX3, sY3);
+            SKD_STEP(5, sX5, sY5, sX4, sY4);
+        } else if constexpr (NS == 4) {
             SKD_STEP(0, sX0, sY0, sX3, sY3);
             SKD_STEP(1, sX1, sY1, sX0, sY0);
             SKD_STEP(2, sX2, sY2, sX1, sY1);
@@ -944,7 +959,7 @@ int lora_skinny_nt(const bf16* X, int64_t ldx, int M, int K, int r, const bf16* 
     const bool dma = ((uintptr_t)X & 15) == 0 && (ldx & 7) == 0 && (K & 7) == 0 && nt <= 4;
     if (dma) {
         switch (nt) {
-            case 1: tlaunch(k_skinny_dma<1, 4>, dim3(grid), dim3(SK_W * 64), s, X, ldx, M, K, r, p); break;
+            case 1: tlaunch(k_skinny_dma<1, 6>, dim3(grid), dim3(SK_W * 64), s, X, ldx, M, K, r, p); break;
             case 2: tlaunch(k_skinny_dma<2, 4>, dim3(grid), dim3(SK_W * 64), s, X, ldx, M, K, r, p); break;
             case 3: tlaunch(k_skinny_dma<3, 3>, dim3(grid), dim3(SK_W * 64), s, X, ldx, M, K, r, p); break;
             default: tlaunch(k_skinny_dma<4, 3>, dim3(grid), dim3(SK_W * 64), s, X, ldx, M, K, r, p); break;
