@@ -444,7 +444,13 @@ __global__ __launch_bounds__(1024) void k_kmeans_ref(const float* __restrict__ X
     if (threadIdx.x == 0 && iters_out) *iters_out = it;
 }
 
-template <bool XL>
+// Phases of k_kmeans_pp: the whole merge in one launch, or (the Lloyd
+// iterations spread over many workgroups in launches of their own,
+// k_kmeans_dist + k_kmeans_step) the seeding up to the initial centers and
+// zero assignments, and the ranking after the last assignment.
+enum KmPhase { KM_ALL = 0, KM_SEED = 1, KM_RANK = 2 };
+
+template <bool XL, int PH = KM_ALL>
 __global__ __launch_bounds__(1024) void k_kmeans_pp(const float* __restrict__ Xg,
                                                     const float* __restrict__ W, int N, int D,
                                                     int k, int iters, uint64_t seed,
@@ -452,6 +458,7 @@ __global__ __launch_bounds__(1024) void k_kmeans_pp(const float* __restrict__ Xg
                                                     float* __restrict__ d2g,  // [N]
                                                     float* __restrict__ distg,  // [k*N]
                                                     int32_t* __restrict__ asgg,  // [N]
+                                                    int32_t* __restrict__ chosen_g,  // [k]
                                                     float* __restrict__ C_out,
                                                     int32_t* __restrict__ asg_out,
                                                     double* __restrict__ mass_out,
@@ -468,13 +475,16 @@ __global__ __launch_bounds__(1024) void k_kmeans_pp(const float* __restrict__ Xg
     __shared__ double smass[XL ? 1 : 1024];
     __shared__ int sorder[XL ? 1 : 1024], srank[XL ? 1 : 1024];
     int sw = 0;
-    const float* __restrict__ X = stage_snapshots<XL>(Xg, xs, N, D, sw);
-    int32_t* asg = XL ? sasg : asgg;
+    const float* __restrict__ X =
+        PH == KM_RANK ? Xg : stage_snapshots<XL>(Xg, xs, N, D, sw);
+    // (the split phases keep the assignments in global memory)
+    int32_t* asg = XL && PH == KM_ALL ? sasg : asgg;
     float* dist = XL ? sdist : distg;
     float* d2 = XL ? sd2 : d2g;
     double* mass = XL ? (double*)xs : smass;
     int* order = XL ? (int*)(xs + 2 * 1024) : sorder;
     int* rank_of = XL ? (int*)(xs + 3 * 1024) : srank;
+    if constexpr (PH != KM_RANK) {
     if (threadIdx.x == 0) {
         rng = seed;
         int first = (int)(u01(rng) * N);
@@ -516,12 +526,20 @@ __global__ __launch_bounds__(1024) void k_kmeans_pp(const float* __restrict__ Xg
         Cw[p] = X[(int64_t)n * D + snap_col(n, d, sw)];
     }
     for (int n = threadIdx.x; n < N; n += blockDim.x) asg[n] = 0;
+    if constexpr (PH == KM_SEED) {
+        for (int r = threadIdx.x; r < k; r += blockDim.x) chosen_g[r] = chosen[r];
+        return;
+    }
     __syncthreads();
     for (int it = 0; it < iters; it++) {
         kmeans_assign(X, sw, vec, Cw, N, D, k, dist, asg);
         kmeans_update(X, sw, Cw, N, D, k, asg, false);
     }
     kmeans_assign(X, sw, vec, Cw, N, D, k, dist, asg);
+    } else {
+        for (int r = threadIdx.x; r < k; r += blockDim.x) chosen[r] = chosen_g[r];
+        __syncthreads();
+    }
     // rank by member weight (F64, index order), stable descending
     if (threadIdx.x == 0) {
         for (int c = 0; c < k; c++) mass[c] = 0.0;
@@ -546,6 +564,44 @@ __global__ __launch_bounds__(1024) void k_kmeans_pp(const float* __restrict__ Xg
         if (mass_out) mass_out[r] = mass[order[r]];
         if (seeds_out) seeds_out[r] = chosen[r];
     }
+}
+
+// One Lloyd assignment pass spread over the GPU: block (c, j) is one wave
+// with center c against snapshots 64 j .. 64 j + 63 (one distance chain per
+// lane, the order of sqdist_chains), into dist [k][N].
+__global__ __launch_bounds__(64) void k_kmeans_dist(const float* __restrict__ X,
+                                                    const float* __restrict__ C, int N, int D,
+                                                    bool vec, float* __restrict__ dist) {
+    const int c = blockIdx.x, n = blockIdx.y * 64 + threadIdx.x;
+    const int nn[1] = {min(n, N - 1)};
+    const float* const cb[1] = {C + (int64_t)c * D};
+    const int kb[1] = {0};
+    float d[1];
+    sqdist_chains<1, 32>(X, D, 0, vec, nn, cb, kb, d);
+    if (n < N) dist[(int64_t)c * N + n] = d[0];
+}
+
+// Then each snapshot's argmin over dist (strict <, as kmeans_assign) and,
+// with update, the centers' member means (kmeans_update, stress mode).
+__global__ __launch_bounds__(1024) void k_kmeans_step(const float* __restrict__ X,
+                                                      float* __restrict__ C, int N, int D, int k,
+                                                      const float* __restrict__ dist,
+                                                      int32_t* __restrict__ asg, bool update) {
+    for (int n = threadIdx.x; n < N; n += blockDim.x) {
+        float best = 1e38f;
+        int bk = 0;
+        for (int c = 0; c < k; c++) {
+            const float d = dist[(int64_t)c * N + n];
+            if (d < best) {
+                best = d;
+                bk = c;
+            }
+        }
+        asg[n] = bk;
+    }
+    if (!update) return;
+    __syncthreads();
+    kmeans_update(X, 0, C, N, D, k, asg, false);
 }
 
 }  // namespace ta
@@ -694,22 +750,49 @@ int ta_kmeans_pp(const float* snaps, const float* weights, int N, int D, int k, 
     off_d2 = (off_d2 + 255) & ~(size_t)255;
     size_t off_dist = off_d2 + (((size_t)N * sizeof(float) + 255) & ~(size_t)255);
     size_t off_asg = off_dist + (((size_t)N * k * sizeof(float) + 255) & ~(size_t)255);
-    size_t total = off_asg + (size_t)N * sizeof(int32_t);
+    size_t off_ch = off_asg + (((size_t)N * sizeof(int32_t) + 255) & ~(size_t)255);
+    size_t total = off_ch + (size_t)k * sizeof(int32_t);
     char* base = (char*)scratch_get(total, s);
     TA_REQUIRE(base, "kmeans_pp: scratch allocation failed");
     // (the work centers sit at the scratch's 256-byte aligned start)
     const bool xl = (int64_t)N * D <= kXs && N <= 1024 && (int64_t)N * k <= kDs;
     const bool vec = D % 4 == 0 && (xl || ((uintptr_t)snaps & 15) == 0);
+    float* Cw = (float*)base;
+    float* d2 = (float*)(base + off_d2);
+    float* dist = (float*)(base + off_dist);
+    int32_t* asg = (int32_t*)(base + off_asg);
+    int32_t* ch = (int32_t*)(base + off_ch);
+    // Lloyd iterations on one workgroup while their distance work is small
+    // (each assignment pass: k N D chain steps on one CU); above that, each
+    // pass in launches of its own: the distances over k x ceil(N / 64)
+    // waves, then the argmin and the center sums on one workgroup (the same
+    // arithmetic in the same order, so the same bits)
+    const bool spread = (int64_t)k * N * D >= (int64_t(1) << 19) && iters > 0;
+    if (!spread) {
+        if (xl)
+            tlaunch(k_kmeans_pp<true>, dim3(1), dim3(1024), s, snaps, weights, N, D, k, iters,
+                    seed, Cw, d2, dist, asg, ch, centers, assign, mass, seeds, vec);
+        else
+            tlaunch(k_kmeans_pp<false>, dim3(1), dim3(1024), s, snaps, weights, N, D, k, iters,
+                    seed, Cw, d2, dist, asg, ch, centers, assign, mass, seeds, vec);
+        return check_launch("kmeans_pp");
+    }
     if (xl)
-        tlaunch(k_kmeans_pp<true>, dim3(1), dim3(1024), s, snaps, weights, N, D, k, iters, seed, (float*)base,
-                                             (float*)(base + off_d2), (float*)(base + off_dist),
-                                             (int32_t*)(base + off_asg), centers, assign, mass,
-                                             seeds, vec);
+        tlaunch(k_kmeans_pp<true, KM_SEED>, dim3(1), dim3(1024), s, snaps, weights, N, D, k, iters,
+                seed, Cw, d2, dist, asg, ch, centers, assign, mass, seeds, vec);
     else
-        tlaunch(k_kmeans_pp<false>, dim3(1), dim3(1024), s, snaps, weights, N, D, k, iters, seed, (float*)base,
-                                              (float*)(base + off_d2), (float*)(base + off_dist),
-                                              (int32_t*)(base + off_asg), centers, assign, mass,
-                                              seeds, vec);
+        tlaunch(k_kmeans_pp<false, KM_SEED>, dim3(1), dim3(1024), s, snaps, weights, N, D, k,
+                iters, seed, Cw, d2, dist, asg, ch, centers, assign, mass, seeds, vec);
+    // the passes read the snapshots from global memory: 16-byte loads need
+    // them aligned
+    const bool gvec = D % 4 == 0 && ((uintptr_t)snaps & 15) == 0;
+    const dim3 dgrid(k, (N + 63) / 64);
+    for (int it = 0; it <= iters; it++) {
+        tlaunch(k_kmeans_dist, dgrid, dim3(64), s, snaps, Cw, N, D, gvec, dist);
+        tlaunch(k_kmeans_step, dim3(1), dim3(1024), s, snaps, Cw, N, D, k, dist, asg, it < iters);
+    }
+    tlaunch(k_kmeans_pp<false, KM_RANK>, dim3(1), dim3(1024), s, snaps, weights, N, D, k, iters,
+            seed, Cw, d2, dist, asg, ch, centers, assign, mass, seeds, vec);
     return check_launch("kmeans_pp");
 }
 
