@@ -368,19 +368,35 @@ __device__ __forceinline__ void kmeans_update(const float* __restrict__ X, int s
                                               bool empty_to_zero) {
     const bool ballot = D % 64 == 0 && blockDim.x % 64 == 0;
     const int lane = threadIdx.x & 63;
+    // the first 256 assignments stay in registers for every output
+    int a4[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) a4[q] = ballot && 64 * q + lane < N ? asg[64 * q + lane] : -1;
     for (int p = threadIdx.x; p < k * D; p += blockDim.x) {
         const int c = p / D, d = p % D;
         float s = 0.f;
         int cnt = 0;
         if (ballot) {
             for (int n0 = 0; n0 < N; n0 += 64) {
-                const int a = n0 + lane < N ? asg[n0 + lane] : -1;
+                const int a = n0 < 256 ? a4[n0 >> 6] : n0 + lane < N ? asg[n0 + lane] : -1;
                 uint64_t mem = __ballot(a == c);
+                // up to four members' values loaded together, then added in
+                // index order
                 while (mem) {
-                    const int n = n0 + __builtin_ctzll(mem);
-                    mem &= mem - 1;
-                    s = __fadd_rn(s, X[(int64_t)n * D + snap_col(n, d, sw)]);
-                    cnt++;
+                    float xv[4];
+                    int nm = 0;
+#pragma unroll
+                    for (int u = 0; u < 4; u++) {
+                        if (!mem) break;
+                        const int n = n0 + __builtin_ctzll(mem);
+                        mem &= mem - 1;
+                        xv[u] = X[(int64_t)n * D + snap_col(n, d, sw)];
+                        nm++;
+                    }
+#pragma unroll
+                    for (int u = 0; u < 4; u++)
+                        if (u < nm) s = __fadd_rn(s, xv[u]);
+                    cnt += nm;
                 }
             }
         } else {
@@ -577,7 +593,7 @@ __global__ __launch_bounds__(64) void k_kmeans_dist(const float* __restrict__ X,
     const float* const cb[1] = {C + (int64_t)c * D};
     const int kb[1] = {0};
     float d[1];
-    sqdist_chains<1, 32>(X, D, 0, vec, nn, cb, kb, d);
+    sqdist_chains<1, 64>(X, D, 0, vec, nn, cb, kb, d);
     if (n < N) dist[(int64_t)c * N + n] = d[0];
 }
 
@@ -588,14 +604,19 @@ __global__ __launch_bounds__(1024) void k_kmeans_step(const float* __restrict__ 
                                                       const float* __restrict__ dist,
                                                       int32_t* __restrict__ asg, bool update) {
     for (int n = threadIdx.x; n < N; n += blockDim.x) {
+        // (the distances come from global memory: 16 loads in flight)
         float best = 1e38f;
         int bk = 0;
-        for (int c = 0; c < k; c++) {
-            const float d = dist[(int64_t)c * N + n];
-            if (d < best) {
-                best = d;
-                bk = c;
-            }
+        for (int c0 = 0; c0 < k; c0 += 16) {
+            float v[16];
+#pragma unroll
+            for (int u = 0; u < 16; u++) v[u] = c0 + u < k ? dist[(int64_t)(c0 + u) * N + n] : 0.f;
+#pragma unroll
+            for (int u = 0; u < 16; u++)
+                if (c0 + u < k && v[u] < best) {
+                    best = v[u];
+                    bk = c0 + u;
+                }
         }
         asg[n] = bk;
     }
