@@ -577,14 +577,20 @@ __global__ __launch_bounds__(256, 2) void k_attn_fwd_t(const bf16* __restrict__ 
     AttnDma<HD, true> dma;
     dma.init(ks_, w, lane);
     const i32x4_t rK = rows_rsrc(Kh, T, ks_), rV = rows_rsrc(Vh, T, ks_);
+    auto issueK = [&](int kt, char* dK) { dma.issue(rK, ks_, min(kt, nkt - 1) * TK, dK, w); };
+    auto issueV = [&](int kt, char* dV) { dma.issue(rV, ks_, min(kt, nkt - 1) * TK, dV, w); };
     auto issue = [&](int kt, char* dK, char* dV) {
-        const int kq = min(kt, nkt - 1);
-        dma.issue(rK, ks_, kq * TK, dK, w);
-        dma.issue(rV, ks_, kq * TK, dV, w);
+        issueK(kt, dK);
+        issueV(kt, dV);
     };
-    auto tile = [&](const char* __restrict__ sK, const char* __restrict__ sV, int kt) {
+    // tile kt; the next tile's V loads go out after this tile's first MFMAs
+    auto tile = [&](const char* __restrict__ sK, const char* __restrict__ sV, int kt,
+                    char* nV) {
         const int k0 = kt * TK;
-        if (k0 > qw0 + 31 || qw0 >= T) return;  // every key follows every query of this wave
+        if (k0 > qw0 + 31 || qw0 >= T) {  // every key follows every query of this wave
+            issueV(kt + 1, nV);
+            return;
+        }
         floatx16 s[2];
 #pragma unroll
         for (int h = 0; h < 2; h++) {
@@ -593,6 +599,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_fwd_t(const bf16* __restrict__ 
             for (int st = 0; st < NST; st++)
                 s[h] = mfma32(*(const bf16x8_t*)(sK + h * 32 * 32 * NST + koff[st]), qf[st], s[h]);
         }
+        issueV(kt + 1, nV);
         // scores in base-2 units; on a tile reaching past this wave's first
         // query, keys after the query are masked (which covers keys past T
         // for every row below T; rows past T are never stored).  The mask
@@ -661,14 +668,15 @@ __global__ __launch_bounds__(256, 2) void k_attn_fwd_t(const bf16* __restrict__ 
     issue(0, sK0, sV0);
     // one step: wait for this wave's loads of the tile, barrier (after it
     // every wave's loads have landed and every wave is done reading the
-    // previous tile's buffers), refill those buffers with the next tile,
-    // compute
+    // previous tile's buffers), refill the K buffer with the next tile,
+    // compute (the next tile's V loads go out after the first MFMAs, so a
+    // wave starts its MFMAs before it has issued every load of the step)
 #define ATT_STEP(KT, SK, SV, RK, RV)          \
     if ((KT) < nkt) {                         \
         TA_WAIT_VMCNT(0);                     \
         __builtin_amdgcn_s_barrier();         \
-        issue((KT) + 1, RK, RV);              \
-        tile(SK, SV, (KT));                   \
+        issueK((KT) + 1, RK);                 \
+        tile(SK, SV, (KT), RV);               \
     }
     for (int kt = 0; kt < nkt; kt += 2) {
         ATT_STEP(kt, sK0, sV0, sK1, sV1);
@@ -792,14 +800,20 @@ __global__ __launch_bounds__(256, 2) void k_attn_bwd_dq_t(const bf16* __restrict
     AttnDma<HD, true> dma;
     dma.init(ks_, w, lane);
     const i32x4_t rK = rows_rsrc(Kh, T, ks_), rV = rows_rsrc(Vh, T, ks_);
+    auto issueK = [&](int kt, char* dK) { dma.issue(rK, ks_, min(kt, nkt - 1) * TK, dK, w); };
+    auto issueV = [&](int kt, char* dV) { dma.issue(rV, ks_, min(kt, nkt - 1) * TK, dV, w); };
     auto issue = [&](int kt, char* dK, char* dV) {
-        const int kq = min(kt, nkt - 1);
-        dma.issue(rK, ks_, kq * TK, dK, w);
-        dma.issue(rV, ks_, kq * TK, dV, w);
+        issueK(kt, dK);
+        issueV(kt, dV);
     };
-    auto tile = [&](const char* __restrict__ sK, const char* __restrict__ sV, int kt) {
+    // tile kt; the next tile's V loads go out after this tile's first MFMAs
+    auto tile = [&](const char* __restrict__ sK, const char* __restrict__ sV, int kt,
+                    char* nV) {
         const int k0 = kt * TK;
-        if (k0 > qw0 + 31 || qw0 >= T) return;  // every key follows every query of this wave
+        if (k0 > qw0 + 31 || qw0 >= T) {  // every key follows every query of this wave
+            issueV(kt + 1, nV);
+            return;
+        }
         floatx16 sT[2], dp[2];
 #pragma unroll
         for (int h = 0; h < 2; h++) {
@@ -812,6 +826,7 @@ __global__ __launch_bounds__(256, 2) void k_attn_bwd_dq_t(const bf16* __restrict
             for (int st = 0; st < NST; st++)
                 dp[h] = mfma32(*(const bf16x8_t*)(sV + h * 32 * 32 * NST + koff[st]), of[st], dp[h]);
         }
+        issueV(kt + 1, nV);
         // P exactly as the forward's statistics define it (keys after the
         // query masked on a tile reaching past the wave's first query, a
         // real branch as in the forward); dS = P (dP - D)
@@ -858,12 +873,14 @@ __global__ __launch_bounds__(256, 2) void k_attn_bwd_dq_t(const bf16* __restrict
     };
     TA_WAIT_VMCNT(0);  // Q, dO, O and the statistics are in; only tile loads are counted below
     issue(0, sK0, sV0);
+    // one step as in the forward kernel: K of the next tile at the barrier,
+    // its V after this tile's score and dP MFMAs
 #define ATT_STEP(KT, SK, SV, RK, RV)          \
     if ((KT) < nkt) {                         \
         TA_WAIT_VMCNT(0);                     \
         __builtin_amdgcn_s_barrier();         \
-        issue((KT) + 1, RK, RV);              \
-        tile(SK, SV, (KT));                   \
+        issueK((KT) + 1, RK);                 \
+        tile(SK, SV, (KT), RV);               \
     }
     for (int kt = 0; kt < nkt; kt += 2) {
         ATT_STEP(kt, sK0, sV0, sK1, sV1);
