@@ -913,7 +913,9 @@ __global__ __launch_bounds__(256, 2) void k_attn_bwd_dq_t(const bf16* __restrict
 // its GQA group [h0, h1).  The block walks (head, 64-query tile) steps; each
 // step's Q and dO tiles (xr_off layout) and the tile's 1 KB of per-query
 // values come straight into LDS by buffer-load DMA, three stages deep, as
-// the K/V tiles of k_attn_fwd_t.  S = Q K^T and dP = dO V^T run as 32
+// the K/V tiles of k_attn_fwd_t (the Q tile and the per-query block of step
+// j + 2 go out at step j's barrier, its dO tile after the V role's first
+// score MFMAs of step j).  S = Q K^T and dP = dO V^T run as 32
 // queries x 32 keys MFMA tiles with the keys' rows as B operands held in
 // accumulation registers, so lane l holds key l%32 and queries
 // 8(r/4) + 4(l/32) + r%4 of each 32-query half.  P = exp2(S scale log2(e) -
@@ -1012,12 +1014,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     };
     // the loads of step j (V-role waves only; past the last step the last is
     // loaded again into a buffer that is never read)
-    auto issue = [&](int j, char* tQ, char* tO, float* tS) {
+    auto issueO = [&](int j, char* tO) {
+        if (!vrole) return;
+        int qt;
+        const int hq = step_head(j, qt);
+        dma.issue(rows_rsrc(Ob + hq * HD, T, qs), qs, qt * TQ, tO, w);
+    };
+    auto issueQ = [&](int j, char* tQ, float* tS) {
         if (!vrole) return;
         int qt;
         const int hq = step_head(j, qt);
         dma.issue(rows_rsrc(Qb + hq * HD, T, qs), qs, qt * TQ, tQ, w);
-        dma.issue(rows_rsrc(Ob + hq * HD, T, qs), qs, qt * TQ, tO, w);
         const uint64_t a = (uint64_t)(uintptr_t)(Sb + ((int64_t)hq * nqt + qt) * QST);
         i32x4_t rs;
         rs[0] = (int)(uint32_t)a;
@@ -1036,6 +1043,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
                          : "memory", "m0");
 #pragma clang diagnostic pop
         }
+    };
+    auto issue = [&](int j, char* tQ, char* tO, float* tS) {
+        issueQ(j, tQ, tS);
+        issueO(j, tO);
     };
     const float sl2 = scale * kLog2e;
     // first phase of half h: S (V role) or dP (K role) over the tile's
@@ -1080,7 +1091,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
     // the role as a compile-time constant (RT: std::true_type for the V role),
     // so that each role's loop is compiled and register-allocated on its own
     auto step = [&](auto RT, const char* __restrict__ tQ, const char* __restrict__ tO,
-                    const float* __restrict__ tS, int j) {
+                    const float* __restrict__ tS, int j, int jn, char* nO) {
         constexpr bool VR = decltype(RT)::value;
         const int q0 = (qt0 + j % nqh) * TQ;
         // every key follows every query of the tile: no work, barriers only
@@ -1092,9 +1103,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
             float4* pb = &sP[h][w][0][0];
             float p[16];
             floatx16 dP;
+            if constexpr (VR) {
+                if (h == 0 && !act) issueO(jn, nO);
+            }
             if (act) {
                 if constexpr (VR) {
                     const floatx16 S = mm1(tQ, h);
+                    if (h == 0) issueO(jn, nO);
 #pragma unroll
                     for (int c = 0; c < 4; c++) {
                         const float4 lx = *(const float4*)(tS + 32 * h + 8 * c + 4 * (lane >> 5));
@@ -1154,8 +1169,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         for (int j = 0; j < nst; j++) {
             if constexpr (VR) TA_WAIT_VMCNT(LPT);
             __builtin_amdgcn_s_barrier();
-            if constexpr (VR) issue(j + 2, sQ[nxt], sO[nxt], sS[nxt]);
-            step(RT, sQ[cur], sO[cur], sS[cur], j);
+            if constexpr (VR) issueQ(j + 2, sQ[nxt], sS[nxt]);
+            step(RT, sQ[cur], sO[cur], sS[cur], j, j + 2, sO[nxt]);
             cur = cur == 2 ? 0 : cur + 1;
             nxt = nxt == 2 ? 0 : nxt + 1;
         }
