@@ -1081,10 +1081,13 @@ __device__ __forceinline__ void ce_frags(bf16x8_t (&fa)[TM], int kt, int kk, con
 // line, so every line of an operand is fetched once; the next stage's load
 // has the same 64 k of compute to land in as with four 32-k stages.
 // CEX: X holds logits and the MFMAs take dlogits formed from them (ce_frags).
+// PART: split-K, split blockIdx.z over k [z k_per_split, +k_per_split): F32
+// partials of the split into part[z][M][N], no epilogue arithmetic.
 template <int BN, int WMW, int WNW, bool CHAIN, bool SWIGLU = false, int KD = 32, int BM = 256,
-          bool CEX = false>
+          bool CEX = false, bool PART = false>
 __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmArgs& a0) {
     static_assert(!CEX || (KD == 64 && !CHAIN && !SWIGLU), "CE operand form");
+    static_assert(!PART || (KD == 64 && !CHAIN && !SWIGLU && !CEX), "split-K partials form");
     static_assert(KD == 32 || KD == 64, "stage depth");
     constexpr int NS = KD == 32 ? 4 : 2, NW = WMW * WNW;
     constexpr int WTM = BM / WMW, WTN = BN / WNW;
@@ -1129,6 +1132,16 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
         a.lora_u[0] = g == 2 ? a0.gu[2] : g == 1 ? a0.gu[1] : a0.gu[0];
         a.lora_v[0] = g == 2 ? a0.gv[2] : g == 1 ? a0.gv[1] : a0.gv[0];
         a.rope_tab = g == 2 ? a0.grope[2] : g == 1 ? a0.grope[1] : a0.grope[0];
+    }
+    if constexpr (PART) {
+        // the split's K range is the whole K of operands that start at its
+        // first k (both are K-contiguous, k_per_split a multiple of 64)
+        const int k0 = blockIdx.z * a0.k_per_split;
+        a.X += k0;
+        a.Y += k0;
+        a.K = min(a0.K - k0, a0.k_per_split);
+        a.lora_n = 0;
+        a.bias = nullptr;
     }
     const int m0 = tm_i * BM, n0 = tn_i * BN;
     int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -1364,6 +1377,53 @@ __device__ __attribute__((always_inline)) inline void gemm_pipe_body(const GemmA
 #undef PIPE_STEP
     }
     TA_WAIT_VMCNT(0);  // the surplus loads have landed before the buffers are reused
+    if constexpr (PART) {
+        // F32 partials through LDS, 32 rows of the wave tile at a time: lane
+        // l of acc[i][j] holds row 32i + l%32, columns 32j + 8g + 4(l/32) + e
+        // (register 4g + e); written as [32][WTN + 4] F32 into a wave-private
+        // region of the stage buffers (free after the main loop), read back
+        // as 16-byte row runs, so each global store covers whole row segments
+        constexpr int LDW = WTN + 4, RB = 32 * LDW * 4;  // region bytes per wave
+        constexpr int NXR = (int)sizeof(sXs) / RB;        // regions in the X buffers
+        static_assert(NXR + (int)sizeof(sYs) / RB >= NW, "partial staging fits the stage buffers");
+        __syncthreads();  // every wave is done with the stage buffers
+        float* const st = (float*)(w < NXR ? (char*)&sXs[0][0] + w * RB
+                                           : (char*)&sYs[0][0] + (w - NXR) * RB);
+        float* const P = a0.part + (int64_t)blockIdx.z * a0.M * a0.N;
+        const bool v4 = (a0.N & 3) == 0;
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+#pragma unroll
+            for (int j = 0; j < TN; j++)
+#pragma unroll
+                for (int g = 0; g < 4; g++)
+                    *(float4*)(st + (lane & 31) * LDW + 32 * j + 8 * g + 4 * (lane >> 5)) =
+                        make_float4(acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2],
+                                    acc[i][j][4 * g + 3]);
+            // one wave's LDS accesses execute in order
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            __builtin_amdgcn_wave_barrier();
+            const int r0 = m0 + wm * WTM + 32 * i, c0 = n0 + wn * WTN;
+            for (int q = lane; q < 32 * (WTN / 4); q += 64) {
+                const int rr = q / (WTN / 4), cc = 4 * (q % (WTN / 4));
+                const int row = r0 + rr, col = c0 + cc;
+                if (row >= a0.M) continue;
+                const float4 v = *(const float4*)(st + rr * LDW + cc);
+                float* d = P + (int64_t)row * a0.N + col;
+                if (v4 && col + 3 < a0.N) {
+                    *(float4*)d = v;
+                } else {
+                    const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (col + e < a0.N) d[e] = vv[e];
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // the reads are done before the next chunk's writes
+            __builtin_amdgcn_wave_barrier();
+        }
+        return;
+    }
 #undef PIPE_CE
 #undef PIPE_ROUND
 #undef PIPE_ISSUE
@@ -1463,6 +1523,12 @@ template <int BN, int WMW, int WNW, int KD = 32>
 __global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
     WMW * WNW / 4, WMW * WNW / 4))) void k_gemm_pipe_swiglu(GemmArgs a) {
     gemm_pipe_body<BN, WMW, WNW, false, true, KD>(a);
+}
+// split-K F32 partials (grid z = splits), reduced by k_splitk_reduce
+template <int BN, int WMW, int WNW>
+__global__ __launch_bounds__(WMW * WNW * 64) __attribute__((amdgpu_waves_per_eu(
+    WMW * WNW / 4, WMW * WNW / 4))) void k_gemm_pipe_part(GemmArgs a) {
+    gemm_pipe_body<BN, WMW, WNW, false, false, 64, 256, false, true>(a);
 }
 // The LM head's input gradient with the cross-entropy gradient formed in the
 // operand reads (gemm_ce_dx).
@@ -1774,12 +1840,22 @@ int gemm_dispatch(bool xk, bool yk, int M, int N, int K, float alpha, const bf16
         splits = (ksteps + steps_per - 1) / steps_per;
         dim3 grid(tiles, 1, splits);
         if (splits > 1) {
-            // F32 partials from the 8-wave direct-to-LDS kernel of the same tile width
-            if (is_pipe(variant)) variant = BNb == 256 ? 8 : 7;
             size_t bytes = (size_t)splits * M * N * sizeof(float);
             a.part = (float*)scratch_get(bytes, s);
             if (!a.part) return set_error(-2, "gemm: scratch allocation of %zu bytes failed", bytes);
-            launch_big<EPI_PARTIAL>(variant, grid, a, s);
+            // F32 partials from the 64-k pipeline kernel of the tile width
+            // when each split runs 32 or more stages (the LM head's input
+            // gradient at B x T = 2048: 10% faster), else from the 8-wave
+            // direct-to-LDS kernel, whose shorter prologue wins on splits of
+            // about 10 stages (same bits either way)
+            const bool long_split = steps_per >= 32;
+            if (variant == 17 && long_split)
+                tlaunch(k_gemm_pipe_part<192, 4, 2>, dim3(grid), dim3(512), s, a);
+            else if (variant == 18 && long_split)
+                tlaunch(k_gemm_pipe_part<256, 2, 4>, dim3(grid), dim3(512), s, a);
+            else
+                launch_big<EPI_PARTIAL>(is_pipe(variant) ? (BNb == 256 ? 8 : 7) : variant, grid,
+                                        a, s);
             int64_t MN = (int64_t)M * N;
             tlaunch(k_splitk_reduce<true>, dim3((int)((MN + 255) / 256)), dim3(256), s, a.part, splits, M, N, C,
                                                                           ldc, alpha, beta, bias);
