@@ -148,6 +148,35 @@ __global__ __launch_bounds__(256) void k_adamw_tiles(
         work[i] = h;
         return h;
     };
+    // elements i .. i + 3 (i a multiple of 4: every tensor starts on a
+    // 64-element boundary), each with elem's arithmetic, moved as 16-byte
+    // F32 and 8-byte BF16 vectors
+    auto elem4 = [&](int64_t i, uint16_t (&h)[4]) {
+        if (!update) {
+            const uint2 w = *(const uint2*)(work + i);
+            h[0] = (uint16_t)w.x, h[1] = (uint16_t)(w.x >> 16);
+            h[2] = (uint16_t)w.y, h[3] = (uint16_t)(w.y >> 16);
+            return;
+        }
+        float4 g = *(const float4*)(grad + i);
+        if (clipped) {
+            g.x *= gscale, g.y *= gscale, g.z *= gscale, g.w *= gscale;
+            *(float4*)(grad + i) = g;
+        }
+        float4 mi = *(const float4*)(m + i), vi = *(const float4*)(v + i);
+        float4 pm = *(const float4*)(master + i);
+        pm.x = adamw_elem(pm.x, g.x, mi.x, vi.x, lr, b1, b2, eps, wd, bc1, bc2);
+        pm.y = adamw_elem(pm.y, g.y, mi.y, vi.y, lr, b1, b2, eps, wd, bc1, bc2);
+        pm.z = adamw_elem(pm.z, g.z, mi.z, vi.z, lr, b1, b2, eps, wd, bc1, bc2);
+        pm.w = adamw_elem(pm.w, g.w, mi.w, vi.w, lr, b1, b2, eps, wd, bc1, bc2);
+        *(float4*)(m + i) = mi;
+        *(float4*)(v + i) = vi;
+        *(float4*)(master + i) = pm;
+        const uint2 w = make_uint2(pack2(pm.x, pm.y), pack2(pm.z, pm.w));
+        *(uint2*)(work + i) = w;
+        h[0] = (uint16_t)w.x, h[1] = (uint16_t)(w.x >> 16);
+        h[2] = (uint16_t)w.y, h[3] = (uint16_t)(w.y >> 16);
+    };
     for (int64_t b = blockIdx.x; b < ntiles; b += gridDim.x) {
         int lo = 0, hi = ntens - 1;  // last tensor with blk0 <= b
         while (lo < hi) {
@@ -158,7 +187,48 @@ __global__ __launch_bounds__(256) void k_adamw_tiles(
         const int t = (int)(b - T.blk0);
         __syncthreads();  // the previous tile's transposed reads are done
         const int lw = T.lw, W = 1 << lw, P = (T.a_side ? T.R : T.C) + 1;  // LDS row pitch
-        if (T.a_side) {
+        if ((T.R & 3) == 0 && (T.C & 3) == 0) {
+            // four consecutive elements per thread, in memory and in the
+            // transposed copy (both dimensions multiples of 4)
+            if (T.a_side) {
+                const int c0 = W * t, nc = min(W, T.C - c0);  // nc: a multiple of 4
+                for (int e = threadIdx.x; e < T.R << (lw - 2); e += 256) {
+                    const int rr = e >> (lw - 2), cc = (e & ((W >> 2) - 1)) << 2;
+                    if (cc < nc) {
+                        uint16_t h[4];
+                        elem4(T.off + (int64_t)rr * T.C + c0 + cc, h);
+#pragma unroll
+                        for (int k = 0; k < 4; k++) lt[(cc + k) * P + rr] = h[k];
+                    }
+                }
+                __syncthreads();
+                bf16* dst = workT + T.off + (int64_t)c0 * T.R;
+                for (int e = 4 * threadIdx.x; e < nc * T.R; e += 1024) {
+                    const int cc = e / T.R, rr = e - cc * T.R;  // rr .. rr + 3 in one row
+                    const int q = cc * P + rr;
+                    *(uint2*)(dst + e) = make_uint2((uint32_t)lt[q] | ((uint32_t)lt[q + 1] << 16),
+                                                    (uint32_t)lt[q + 2] | ((uint32_t)lt[q + 3] << 16));
+                }
+            } else {
+                const int r0 = W * t, nr = min(W, T.R - r0);  // nr: a multiple of 4
+                const int64_t base = T.off + (int64_t)r0 * T.C;
+                for (int e = 4 * threadIdx.x; e < nr * T.C; e += 1024) {
+                    const int rr = e / T.C, cc = e - rr * T.C;
+                    uint16_t h[4];
+                    elem4(base + e, h);
+#pragma unroll
+                    for (int k = 0; k < 4; k++) lt[rr * P + cc + k] = h[k];
+                }
+                __syncthreads();
+                for (int e = threadIdx.x; e < T.C << (lw - 2); e += 256) {
+                    const int cc = e >> (lw - 2), rr = (e & ((W >> 2) - 1)) << 2;
+                    if (rr < nr)
+                        *(uint2*)(workT + T.off + (int64_t)cc * T.R + r0 + rr) = make_uint2(
+                            (uint32_t)lt[rr * P + cc] | ((uint32_t)lt[(rr + 1) * P + cc] << 16),
+                            (uint32_t)lt[(rr + 2) * P + cc] | ((uint32_t)lt[(rr + 3) * P + cc] << 16));
+                }
+            }
+        } else if (T.a_side) {
             // A [R = r, C = in]: columns [c0, c0 + nc), all R rows
             const int c0 = W * t, nc = min(W, T.C - c0);
             for (int e = threadIdx.x; e < T.R << lw; e += 256) {
