@@ -11,6 +11,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <string>
@@ -104,11 +105,12 @@ static size_t mem_class(size_t bytes) {
 // dispatch (tlaunch), with the algorithmic flops and HBM bytes of the launch;
 // ta_kprof_read() waits for the events and sums.
 struct KProf {
-    int sel = -1;
-    bool paused = false;  // selected, but launches are not timed for now
+    std::atomic<int> sel{-1};
+    std::atomic<bool> paused{false};  // selected, but launches are not timed for now
     std::vector<hipEvent_t> ev;
     std::vector<double> flops, bytes;
-    size_t used = 0;
+    std::vector<char> valid;  // the slot's launch carried its events
+    size_t used = 0;          // slots reserved since the last read
     const char* name[KP_COUNT] = {};
 };
 static std::mutex g_kp_mu;
@@ -132,39 +134,47 @@ bool kprof_pool_pair(hipEvent_t* start, hipEvent_t* stop) {
     return true;
 }
 
+// Each timed call reserves its own slot (event pair) here, so calls on
+// several threads never share one; kprof_end marks whether the launch
+// carried the events.
 bool kprof_begin(int kid, hipStream_t s) {
     (void)s;
     t_kp_arm.start = t_kp_arm.stop = nullptr;
     t_kp_arm.used = false;
-    if (g_kp.sel != kid || g_kp.paused) return false;
+    if (g_kp.sel.load() != kid || g_kp.paused.load()) return false;
     std::lock_guard<std::mutex> lk(g_kp_mu);
-    size_t i = g_kp.used;
+    const size_t i = g_kp.used;
     while (g_kp.ev.size() < 2 * (i + 1)) {
         hipEvent_t e;
         if (hipEventCreate(&e) != hipSuccess) return false;
         g_kp.ev.push_back(e);
     }
+    if (g_kp.flops.size() <= i) {
+        g_kp.flops.resize(i + 1);
+        g_kp.bytes.resize(i + 1);
+        g_kp.valid.resize(i + 1);
+    }
+    g_kp.valid[i] = 0;
+    g_kp.used = i + 1;
     t_kp_arm.start = g_kp.ev[2 * i];
     t_kp_arm.stop = g_kp.ev[2 * i + 1];
+    t_kp_arm.slot = i;
     return true;
 }
 
 void kprof_end(int kid, hipStream_t s, double flops, double bytes, const char* name) {
     (void)s;
-    const bool used = t_kp_arm.used;
+    const bool armed = t_kp_arm.stop != nullptr, used = t_kp_arm.used;
+    const size_t i = t_kp_arm.slot;
     t_kp_arm.start = t_kp_arm.stop = nullptr;
     t_kp_arm.used = false;
-    if (g_kp.sel != kid || !used) return;
+    if (!armed) return;
     std::lock_guard<std::mutex> lk(g_kp_mu);
-    size_t i = g_kp.used;
-    if (g_kp.flops.size() <= i) {
-        g_kp.flops.resize(i + 1);
-        g_kp.bytes.resize(i + 1);
-    }
+    if (i >= g_kp.used) return;  // a selection since kprof_begin dropped the slot
     g_kp.flops[i] = flops;
     g_kp.bytes[i] = bytes;
-    g_kp.name[kid] = name;
-    g_kp.used = i + 1;
+    g_kp.valid[i] = used ? 1 : 0;
+    if (used) g_kp.name[kid] = name;
 }
 
 }  // namespace ta
@@ -189,7 +199,10 @@ int ta_kprof_pause(int paused) {
 int ta_kprof_read(double* ms, int64_t* launches, double* flops, double* bytes) {
     std::lock_guard<std::mutex> lk(ta::g_kp_mu);
     double tms = 0, tf = 0, tb = 0;
+    int64_t n = 0;
     for (size_t i = 0; i < ta::g_kp.used; i++) {
+        if (!ta::g_kp.valid[i]) continue;
+        n++;
         TA_HIP(hipEventSynchronize(ta::g_kp.ev[2 * i + 1]));
         float x = 0.f;
         TA_HIP(hipEventElapsedTime(&x, ta::g_kp.ev[2 * i], ta::g_kp.ev[2 * i + 1]));
@@ -198,7 +211,7 @@ int ta_kprof_read(double* ms, int64_t* launches, double* flops, double* bytes) {
         tb += ta::g_kp.bytes[i];
     }
     if (ms) *ms = tms;
-    if (launches) *launches = (int64_t)ta::g_kp.used;
+    if (launches) *launches = n;
     if (flops) *flops = tf;
     if (bytes) *bytes = tb;
     ta::g_kp.used = 0;

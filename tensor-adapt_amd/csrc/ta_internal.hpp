@@ -42,6 +42,7 @@ void kprof_end(int kid, hipStream_t s, double flops, double bytes, const char* n
 struct KpArm {
     hipEvent_t start = nullptr, stop = nullptr;
     bool used = false;
+    size_t slot = 0;  // the kernel-timing slot kprof_begin reserved
     std::vector<hipEvent_t>* pool = nullptr;
     size_t* npairs = nullptr;
 };
