@@ -310,15 +310,16 @@ def test_gemm_last_wave_split_bit_identical(M, N, K):
         check_gemm_close(got, ref, "gemm last-wave split")
 
 
-@pytest.mark.parametrize("M,N,K", [(2048, 896, 4864), (2048, 900, 16384), (1024, 1536, 16384)])
+@pytest.mark.parametrize("M,N,K", [(2048, 896, 4864), (2048, 900, 16384), (1024, 1536, 16384),
+                                   (1000, 900, 32768)])
 def test_gemm_split_k_partials(M, N, K):
     """Long-K GEMMs on too few tiles to fill the chip (the Qwen2-0.5B shapes
     at B x T = 2048) run split-K, each split's F32 partials then the ordered
     reduce with alpha, beta and the bias.  Splits of about 10 stages (the
     first shape, 8 splits) take the direct-to-LDS kernel; splits of 32 or
-    more the 64-k pipeline kernel, 256-wide (N = 900: the element stores)
-    and 192-wide.  Checked against the oracle GEMM, with the bias and
-    beta = 1."""
+    more the 64-k pipeline kernel, 256-wide (N = 900: the element stores;
+    M = 1000: rows past M skipped) and 192-wide.  Checked against the
+    oracle GEMM, with the bias and beta = 1."""
     X, Y, b = rbf(M, K, scale=0.5), rbf(N, K, scale=0.02), rbf(N, scale=0.1)
     C0 = rbf(M, N)
     tc = dev(C0)
